@@ -1,0 +1,191 @@
+/*
+ * qr_hip.h -- C ABI of libqr_hip.so: quantr-in-c's quantized GEMV and MoE hot
+ * path on one MI355X (gfx950), with device-resident weights and activations.
+ *
+ * Plain C, plain pointers and sizes.  Every function returns a qr_status
+ * (0 on success, a negative code on failure; qr_last_error() then holds a
+ * message for the calling thread).  Unless a function says otherwise, pointer
+ * arguments are DEVICE pointers, work is enqueued on the context's stream and
+ * the call returns without waiting (qr_sync() waits).
+ *
+ * Block formats are the reference's own (include/quant.h:28-50 and the raw
+ * 210-byte Q6_K of src/quant.c:220-226); type ids are GGML's (0 F32, 8 Q8_0,
+ * 12 Q4_K, 13 Q5_K, 14 Q6_K).  Results equal the reference's C99 build bit for
+ * bit: int32 unit sums, fp32 GEMV outputs (fp32 terms added in the
+ * reference's sequential order), router indices and weights, and the MoE
+ * layer output.  The reference's Q4_K dot is defective (it reads fp16 bit
+ * patterns as floats, src/quant.c:302-309); Q4_K here is the corrected form,
+ * which equals the reference's Q5_K dot on the same block with a zero fifth
+ * bit plane.
+ *
+ * The host-pointer drop-ins with the reference's own signatures are in
+ * qr_dropin.h.
+ */
+#ifndef QR_HIP_H
+#define QR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    QR_OK = 0,
+    QR_ERR_INVALID = -1,     /* bad argument (null, size, alignment, type) */
+    QR_ERR_HIP = -2,         /* HIP runtime error */
+    QR_ERR_NOMEM = -3,       /* device or host allocation failed */
+    QR_ERR_UNSUPPORTED = -4, /* valid but not implemented (e.g. a token count) */
+    QR_ERR_NODEV = -5        /* no usable GPU */
+} qr_status;
+
+#define QR_TYPE_F32 0
+#define QR_TYPE_Q8_0 8
+#define QR_TYPE_Q4_K 12
+#define QR_TYPE_Q5_K 13
+#define QR_TYPE_Q6_K 14
+
+/* fp32 accumulation order of the router / F32 GEMV, one per reference build:
+ * SEQ    matmul_ref and the -std=c99 build's matmul_omp (src/kernels.c:18-28)
+ * AVX2   matmul_omp built -mavx2 -mfma (src/kernels.c:50-65)
+ * AVX512 matmul_omp built -mavx512f    (src/kernels.c:38-49)              */
+#define QR_ORDER_SEQ 0
+#define QR_ORDER_AVX2 1
+#define QR_ORDER_AVX512 2
+
+typedef struct qr_ctx qr_ctx;
+
+/* ---- context, memory, timing ------------------------------------------ */
+const char* qr_last_error(void);
+const char* qr_version(void);
+int qr_device_count(int* count);
+int qr_ctx_create(int device, qr_ctx** out);
+int qr_ctx_destroy(qr_ctx* ctx);
+/* Use an existing hipStream_t (NULL restores the context's own stream). */
+int qr_ctx_set_stream(qr_ctx* ctx, void* hip_stream);
+void* qr_ctx_get_stream(qr_ctx* ctx);
+int qr_sync(qr_ctx* ctx);
+int qr_malloc(qr_ctx* ctx, size_t bytes, void** dptr);
+int qr_free(qr_ctx* ctx, void* dptr);
+/* Copies are ordered on the context stream and complete before returning. */
+int qr_memcpy_h2d(qr_ctx* ctx, void* dst, const void* src, size_t bytes);
+int qr_memcpy_d2h(qr_ctx* ctx, void* dst, const void* src, size_t bytes);
+int qr_memcpy_d2d(qr_ctx* ctx, void* dst, const void* src, size_t bytes);
+int qr_memset(qr_ctx* ctx, void* dst, int value, size_t bytes);
+/* HIP events on the context stream: start, then stop -> elapsed ms. */
+int qr_timer_start(qr_ctx* ctx);
+int qr_timer_stop(qr_ctx* ctx, float* ms);
+/* HIP graph capture of the context stream: calls between begin and end are
+ * recorded, not run; the instantiated graph replays them back to back.  Only
+ * calls that allocate nothing and set no memory may be captured (qr_gemv,
+ * qr_matmul_f32, qr_softmax, and qr_moe_forward once it has run for the same
+ * or a larger T outside capture). */
+int qr_capture_begin(qr_ctx* ctx);
+int qr_capture_end(qr_ctx* ctx, void** graph);
+int qr_graph_launch(qr_ctx* ctx, void* graph);
+int qr_graph_destroy(void* graph);
+/* A plain streaming copy kernel (dst = src, 16-byte chunks): the reference
+ * point for hardware byte counters. */
+int qr_copy_kernel(qr_ctx* ctx, void* dst, const void* src, size_t bytes);
+
+/* ---- quantized GEMV ------------------------------------------------------ */
+
+/* quantize_row_q8_0 (src/quant.c:143-158) of n floats into n/32 block_q8_0
+ * (34-byte) blocks; a tail shorter than 32 is not written. */
+int qr_quantize_q8_0(qr_ctx* ctx, const float* x, void* y, long n);
+
+/* y[t*ystride + r] = W[r] . x[t*xstride ...] for r < n, t < nt, with W an
+ * [n][row_bytes(type, d)] weight matrix (16-byte aligned) and x fp32,
+ * quantized to Q8_0 inside the call as matmul_q_fused does
+ * (src/quant.c:441-523).  type F32 runs the fp32 GEMV in SEQ order.
+ * nt in {1, 2, 3, 4, 8}.  acc (optional, [nt][n][units]) receives the int32
+ * sum of every 32-element unit, accb (optional, [nt][units]) the activation
+ * block sums -- a parity mode for bit-exact integer checks. */
+int qr_gemv_ex(qr_ctx* ctx, uint32_t type, const void* w, const float* x, int xstride,
+               float* y, int ystride, int n, int d, int nt, int32_t* acc, int32_t* accb);
+int qr_gemv(qr_ctx* ctx, uint32_t type, const void* w, const float* x, float* y, int n, int d,
+            int nt);
+
+/* fp32 GEMV in a reference accumulation order (router logits):
+ * y[t][r] = sum_j w[r][j] * x[t][j]. */
+int qr_matmul_f32(qr_ctx* ctx, int order, const float* w, const float* x, float* y, int n, int d,
+                  int nt);
+
+/* softmax_ref (src/kernels.c:191-207) of each of `rows` rows of n floats,
+ * in place; expf is bit-exact with glibc's. */
+int qr_softmax(qr_ctx* ctx, float* x, int rows, int n);
+
+/* Bytes per weight row (whole blocks only, src/quant.c:477-484). */
+size_t qr_row_bytes(uint32_t type, int d);
+
+/* ---- MoE layer --------------------------------------------------------- */
+
+/* One MoE layer's device weights.  Expert tensors are [E][rows][cols] in
+ * GGUF order, expert e's matrix at base + e * rows * row_bytes(type, cols)
+ * (src/model.c:412-419).  up is ffn_up_exps (the SiLU slot, expert_w1), gate
+ * is ffn_gate_exps (the linear slot, expert_w3), down is ffn_down_exps
+ * (expert_w2); hb = silu(up . xb) * (gate . xb) (src/runtime.c:252-256).
+ * sh_* describe an optional shared expert with a sigmoid gate (no reference
+ * counterpart; sh_hidden 0 disables it). */
+typedef struct {
+    int dim;
+    int hidden;
+    int n_experts;
+    int n_used;
+    const float* router;          /* ffn_gate_inp [E][dim] fp32 */
+    const void* up;
+    const void* gate;
+    const void* down;
+    uint32_t up_type, gate_type, down_type;
+    int sh_hidden;
+    const float* sh_gate_inp;     /* [dim] fp32 */
+    const void* sh_up;
+    const void* sh_gate;
+    const void* sh_down;
+    uint32_t sh_up_type, sh_gate_type, sh_down_type;
+} qr_moe_layer;
+
+/* Router for T tokens (src/runtime.c:205-230): logits in `order`, softmax,
+ * K argmax passes (strict '>', lowest index on ties), weights renormalised by
+ * their sequential sum.  idx/wts are [T][K]; probs (optional) [T][E]. */
+int qr_moe_route(qr_ctx* ctx, const qr_moe_layer* L, const float* xb, int T, int order,
+                 float* probs, int32_t* idx, float* wts);
+
+/* Token-to-expert dispatch of T*K (token, slot) pairs p = t*K + k:
+ * counts[E], offsets[E+1] (exclusive scan), perm[T*K] = pairs grouped by
+ * expert and ascending p inside each group, inv[p] = position of p in perm.
+ * Deterministic (no dependence on atomic ordering). */
+int qr_moe_dispatch(qr_ctx* ctx, const int32_t* idx, int T, int K, int E, int32_t* counts,
+                    int32_t* offsets, int32_t* perm, int32_t* inv);
+
+/* The whole layer for T tokens: x[t] += sum_k w[t][k] * expert(xb[t]) in slot
+ * order (src/runtime.c:242-269), plus the shared expert when present.
+ * idx_out / w_out (optional, [T][K]) receive the routing. */
+int qr_moe_forward(qr_ctx* ctx, const qr_moe_layer* L, float* x, const float* xb, int T,
+                   int order, int32_t* idx_out, float* w_out);
+
+/* ---- weight registry (host pointer -> device copy) ---------------------- */
+
+/* Upload `bytes` from host memory once and return the device copy; later
+ * calls with the same host pointer return the same copy (the registry keys
+ * on the host address and size).  Copies live until released. */
+int qr_weights_upload(qr_ctx* ctx, const void* host, size_t bytes, const void** dev);
+/* Upload nparts host blocks of part_bytes each into one contiguous device
+ * tensor (part i at offset i * part_bytes), registered under `key`: the
+ * per-expert weight tensors of src/model.c:421-433 that are not one 3-D
+ * slab. */
+int qr_weights_upload_parts(qr_ctx* ctx, const void* key, const void* const* parts,
+                            size_t part_bytes, int nparts, const void** dev);
+int qr_weights_lookup(qr_ctx* ctx, const void* host, const void** dev);
+int qr_weights_release(qr_ctx* ctx, const void* host);
+int qr_weights_release_all(qr_ctx* ctx);
+
+/* ---- test hooks ---------------------------------------------------------- */
+/* y[i] = expf(x[i]) with the device restatement of glibc's expf. */
+int qr_test_expf(qr_ctx* ctx, const float* x, float* y, long n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QR_HIP_H */

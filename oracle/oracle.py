@@ -1,0 +1,307 @@
+"""ctypes binding of the parity checker (test infrastructure only).
+
+``Oracle`` wraps liboracle.so, the C99 restatement of quantr-in-c's quantized
+GEMV and MoE path (oracle/qr_oracle.c).  ``RefLib`` wraps oracle/_ref/libqref_*.so,
+the reference's own sources compiled where they lie plus ref_driver.c; those
+files exist only where the reference checkout was present at build time.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
+module.  The product never does.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 0, 8, 12, 13, 14
+ORDER_SEQ, ORDER_AVX2, ORDER_AVX512 = 0, 1, 2
+# KernelBackend values (include/types.h:99-108)
+BACKEND_REF, BACKEND_AVX2, BACKEND_AVX512 = 0, 1, 2
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def row_bytes(qtype, d):
+    """Bytes per weight row (src/quant.c:477-484)."""
+    if qtype == TYPE_Q8_0:
+        return (d // 32) * 34
+    if qtype == TYPE_Q4_K:
+        return (d // 256) * 144
+    if qtype == TYPE_Q5_K:
+        return (d // 256) * 176
+    if qtype == TYPE_Q6_K:
+        return (d // 256) * 210
+    return d * 4
+
+
+class MoeLayer(C.Structure):
+    _fields_ = [
+        ("dim", C.c_int), ("hidden", C.c_int), ("n_experts", C.c_int), ("n_used", C.c_int),
+        ("router", C.c_void_p), ("up", C.c_void_p), ("gate", C.c_void_p), ("down", C.c_void_p),
+        ("up_type", C.c_uint32), ("gate_type", C.c_uint32), ("down_type", C.c_uint32),
+        ("sh_hidden", C.c_int), ("sh_gate_inp", C.c_void_p), ("sh_up", C.c_void_p),
+        ("sh_gate", C.c_void_p), ("sh_down", C.c_void_p),
+        ("sh_up_type", C.c_uint32), ("sh_gate_type", C.c_uint32), ("sh_down_type", C.c_uint32),
+    ]
+
+
+def build_oracle():
+    """Compile liboracle.so (and oracle/_ref when the reference checkout exists)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    if os.path.isdir("/root/reference/src"):
+        subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
+
+
+class Oracle:
+    def __init__(self, path=None):
+        path = path or os.path.join(HERE, "liboracle.so")
+        if not os.path.exists(path):
+            build_oracle()
+        L = self.lib = C.CDLL(path)
+        L.qro_h2f.restype = C.c_float
+        L.qro_h2f.argtypes = [C.c_uint16]
+        L.qro_h2f_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_long]
+        L.qro_f2h.restype = C.c_uint16
+        L.qro_f2h.argtypes = [C.c_float]
+        L.qro_row_bytes.restype = C.c_size_t
+        L.qro_row_bytes.argtypes = [C.c_uint32, C.c_int]
+        L.qro_units_per_row.restype = C.c_int
+        L.qro_units_per_row.argtypes = [C.c_uint32, C.c_int]
+        L.qro_quantize_row_q8_0.argtypes = [_f32p, C.c_void_p, C.c_int]
+        L.qro_dequantize_row.argtypes = [_f32p, C.c_void_p, C.c_uint32, C.c_int]
+        L.qro_vec_dot.restype = C.c_float
+        L.qro_vec_dot.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
+        L.qro_row_accum.restype = C.c_int
+        L.qro_row_accum.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int, _i32p, C.c_void_p]
+        L.qro_matmul_q_fused_batch.argtypes = [_f32p, _f32p, C.c_void_p, C.c_uint32, C.c_int,
+                                               C.c_int, C.c_int, C.c_int, C.c_int]
+        L.qro_matmul_f32.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
+        L.qro_softmax.argtypes = [_f32p, C.c_int]
+        L.qro_silu.restype = C.c_float
+        L.qro_silu.argtypes = [C.c_float]
+        L.qro_expf_batch.argtypes = [_f32p, _f32p, C.c_size_t]
+        L.qro_route.restype = C.c_int
+        L.qro_route.argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                C.c_void_p, C.c_void_p, _i32p, _f32p]
+        L.qro_moe_forward.argtypes = [_f32p, _f32p, C.c_int, C.POINTER(MoeLayer), C.c_int,
+                                      C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+        L.qro_shared_expert.argtypes = [_f32p, _f32p, C.POINTER(MoeLayer), C.c_int]
+        L.qro_moe_dispatch.restype = C.c_int
+        L.qro_moe_dispatch.argtypes = [_i32p, C.c_int, C.c_int, C.c_int, _i32p, _i32p, _i32p, _i32p]
+
+    # --- fp16 helpers, include/quant.h:53-77
+    def h2f(self, h):
+        return self.lib.qro_h2f(int(h))
+
+    def h2f_bits(self, codes):
+        """uint16 codes -> uint32 float bits (NaN payloads preserved)."""
+        codes = np.ascontiguousarray(codes, np.uint16)
+        out = np.empty(codes.size, np.float32)
+        self.lib.qro_h2f_batch(_ptr(codes), _ptr(out), codes.size)
+        return out.view(np.uint32)
+
+    def f2h(self, f):
+        return self.lib.qro_f2h(float(f))
+
+    # --- src/quant.c:143-158
+    def quantize_q8_0(self, x):
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        out = np.zeros((x.size // 32) * 34, np.uint8)
+        self.lib.qro_quantize_row_q8_0(x, _ptr(out), x.size)
+        return out
+
+    def dequantize(self, blob, qtype, n):
+        out = np.zeros(n, np.float32)
+        blob = np.ascontiguousarray(blob, np.uint8)
+        self.lib.qro_dequantize_row(out, _ptr(blob), qtype, n)
+        return out
+
+    def vec_dot(self, qtype, row, xq8, d, order=ORDER_SEQ):
+        row = np.ascontiguousarray(row, np.uint8)
+        xq8 = np.ascontiguousarray(xq8, np.uint8)
+        return self.lib.qro_vec_dot(qtype, _ptr(row), _ptr(xq8), d, order)
+
+    def row_accum(self, qtype, row, xq8, d):
+        units = self.lib.qro_units_per_row(qtype, d)
+        isum = np.zeros(max(units, 1), np.int32)
+        bsum = np.zeros(max(units, 1), np.int32)
+        row = np.ascontiguousarray(row, np.uint8)
+        xq8 = np.ascontiguousarray(xq8, np.uint8)
+        self.lib.qro_row_accum(qtype, _ptr(row), _ptr(xq8), d, isum, _ptr(bsum))
+        return isum[:units], bsum[:units]
+
+    def matmul_q_fused(self, x, w, qtype, n, d, threads=1, order=ORDER_SEQ):
+        """x: [nt, d] or [d]; returns [nt, n] or [n] (src/quant.c:441-523)."""
+        x = np.ascontiguousarray(x, np.float32)
+        nt = 1 if x.ndim == 1 else x.shape[0]
+        out = np.zeros((nt, n), np.float32)
+        wptr = None if w is None else _ptr(np.ascontiguousarray(w))
+        self.lib.qro_matmul_q_fused_batch(out, x.reshape(nt, d), wptr, qtype, n, d, nt,
+                                          threads, order)
+        return out[0] if x.ndim == 1 else out
+
+    def matmul_f32(self, x, w, n, d, order=ORDER_SEQ):
+        out = np.zeros(n, np.float32)
+        self.lib.qro_matmul_f32(out, np.ascontiguousarray(x, np.float32),
+                                np.ascontiguousarray(w, np.float32), n, d, order)
+        return out
+
+    def softmax(self, x):
+        x = np.array(x, np.float32)
+        self.lib.qro_softmax(x, x.size)
+        return x
+
+    def expf(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        self.lib.qro_expf_batch(x.ravel(), out.ravel(), x.size)
+        return out
+
+    def route(self, xb, router_w, E, K, order=ORDER_SEQ):
+        dim = xb.size
+        logits = np.zeros(E, np.float32)
+        probs = np.zeros(E, np.float32)
+        idx = np.zeros(K, np.int32)
+        wts = np.zeros(K, np.float32)
+        self.lib.qro_route(np.ascontiguousarray(xb, np.float32),
+                           np.ascontiguousarray(router_w, np.float32), dim, E, K, order,
+                           _ptr(logits), _ptr(probs), idx, wts)
+        return logits, probs, idx, wts
+
+    @staticmethod
+    def make_layer(keep, dim, hidden, E, K, router, up, up_type, gate, gate_type, down, down_type,
+                   shared=None):
+        """Build a MoeLayer; `keep` is a list that holds the numpy buffers alive."""
+        bufs = [np.ascontiguousarray(router, np.float32), np.ascontiguousarray(up),
+                np.ascontiguousarray(gate), np.ascontiguousarray(down)]
+        keep.extend(bufs)
+        L = MoeLayer(dim, hidden, E, K, _ptr(bufs[0]), _ptr(bufs[1]), _ptr(bufs[2]),
+                     _ptr(bufs[3]), up_type, gate_type, down_type)
+        if shared is not None:
+            sb = [np.ascontiguousarray(shared["gate_inp"], np.float32),
+                  np.ascontiguousarray(shared["up"]), np.ascontiguousarray(shared["gate"]),
+                  np.ascontiguousarray(shared["down"])]
+            keep.extend(sb)
+            L.sh_hidden = shared["hidden"]
+            L.sh_gate_inp, L.sh_up, L.sh_gate, L.sh_down = [_ptr(b) for b in sb]
+            L.sh_up_type = shared["up_type"]
+            L.sh_gate_type = shared["gate_type"]
+            L.sh_down_type = shared["down_type"]
+        return L
+
+    def moe_forward(self, x, xb, layer, order=ORDER_SEQ, dot_order=ORDER_SEQ, threads=1):
+        """Returns (x_out [T,dim], idx [T,K], wts [T,K]) (src/runtime.c:202-269 per token).
+        order: router (KernelOps.matmul) order; dot_order: Q8_0 fused-dot order."""
+        x = np.array(x, np.float32, copy=True)
+        T, K = x.shape[0], layer.n_used
+        idx = np.zeros((T, K), np.int32)
+        wts = np.zeros((T, K), np.float32)
+        self.lib.qro_moe_forward(x, np.ascontiguousarray(xb, np.float32), T, C.byref(layer),
+                                 order, dot_order, threads, _ptr(idx), _ptr(wts))
+        return x, idx, wts
+
+    def shared_expert(self, xb, layer, threads=1):
+        y = np.zeros(layer.dim, np.float32)
+        self.lib.qro_shared_expert(y, np.ascontiguousarray(xb, np.float32), C.byref(layer), threads)
+        return y
+
+    def dispatch(self, idx, E):
+        idx = np.ascontiguousarray(idx, np.int32)
+        T, K = idx.shape
+        counts = np.zeros(E, np.int32)
+        offsets = np.zeros(E + 1, np.int32)
+        perm = np.zeros(T * K, np.int32)
+        inv = np.zeros(T * K, np.int32)
+        rc = self.lib.qro_moe_dispatch(idx.ravel(), T, K, E, counts, offsets, perm, inv)
+        if rc != 0:
+            raise ValueError("dispatch: expert index out of range")
+        return counts, offsets, perm, inv
+
+
+class RefLib:
+    """The reference's own code (oracle/_ref/libqref_<flavour>.so)."""
+
+    def __init__(self, flavour="c99"):
+        path = os.path.join(HERE, "_ref", "libqref_%s.so" % flavour)
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.path = path
+        L = self.lib = C.CDLL(path)
+        L.refdrv_h2f.restype = C.c_float
+        L.refdrv_h2f.argtypes = [C.c_uint16]
+        L.refdrv_f2h.restype = C.c_uint16
+        L.refdrv_f2h.argtypes = [C.c_float]
+        L.quantize_row_q8_0.argtypes = [_f32p, C.c_void_p, C.c_int]
+        L.dequantize_row.argtypes = [_f32p, C.c_void_p, C.c_uint32, C.c_int]
+        for name in ("vec_dot_q8_0_q8_0", "vec_dot_q4K_q8_0", "vec_dot_q5K_q8_0",
+                     "vec_dot_q6K_q8_0"):
+            f = getattr(L, name)
+            f.restype = C.c_float
+            f.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+        L.matmul_q_fused.argtypes = [_f32p, _f32p, C.c_void_p, C.c_uint32, C.c_int, C.c_int, C.c_int]
+        L.refdrv_matmul.argtypes = [C.c_int, _f32p, _f32p, _f32p, C.c_int, C.c_int]
+        L.refdrv_softmax.argtypes = [C.c_int, _f32p, C.c_int]
+        L.refdrv_moe_layer.restype = C.c_int
+        L.refdrv_moe_layer.argtypes = [_f32p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                       C.c_int, C.c_int, _f32p, C.c_void_p, C.c_uint32,
+                                       C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32,
+                                       C.c_int, C.c_int]
+
+    def quantize_q8_0(self, x):
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        out = np.zeros((x.size // 32) * 34, np.uint8)
+        self.lib.quantize_row_q8_0(x, _ptr(out), x.size)
+        return out
+
+    def dequantize(self, blob, qtype, n):
+        out = np.zeros(n, np.float32)
+        self.lib.dequantize_row(out, _ptr(np.ascontiguousarray(blob, np.uint8)), qtype, n)
+        return out
+
+    def vec_dot(self, qtype, row, xq8, d):
+        name = {TYPE_Q8_0: "vec_dot_q8_0_q8_0", TYPE_Q4_K: "vec_dot_q4K_q8_0",
+                TYPE_Q5_K: "vec_dot_q5K_q8_0", TYPE_Q6_K: "vec_dot_q6K_q8_0"}[qtype]
+        return getattr(self.lib, name)(_ptr(np.ascontiguousarray(row, np.uint8)),
+                                       _ptr(np.ascontiguousarray(xq8, np.uint8)), d)
+
+    def matmul_q_fused(self, x, w, qtype, n, d, threads=1):
+        out = np.zeros(n, np.float32)
+        self.lib.matmul_q_fused(out, np.ascontiguousarray(x, np.float32),
+                                _ptr(np.ascontiguousarray(w)), qtype, n, d, threads)
+        return out
+
+    def matmul(self, backend, x, w, n, d):
+        out = np.zeros(n, np.float32)
+        self.lib.refdrv_matmul(backend, out, np.ascontiguousarray(x, np.float32),
+                               np.ascontiguousarray(w, np.float32), n, d)
+        return out
+
+    def softmax(self, backend, x):
+        x = np.array(x, np.float32)
+        self.lib.refdrv_softmax(backend, x, x.size)
+        return x
+
+    def moe_layer(self, x_in, dim, hidden, E, K, router, up, up_type, gate, gate_type, down,
+                  down_type, backend=BACKEND_REF, threads=1):
+        x_in = np.ascontiguousarray(x_in, np.float32)
+        T = x_in.shape[0]
+        xb = np.zeros_like(x_in)
+        xo = np.zeros_like(x_in)
+        rc = self.lib.refdrv_moe_layer(x_in, _ptr(xb), _ptr(xo), T, dim, hidden, E, K,
+                                       np.ascontiguousarray(router, np.float32),
+                                       _ptr(np.ascontiguousarray(up)), up_type,
+                                       _ptr(np.ascontiguousarray(gate)), gate_type,
+                                       _ptr(np.ascontiguousarray(down)), down_type,
+                                       backend, threads)
+        if rc != 0:
+            raise RuntimeError("refdrv_moe_layer failed: %d" % rc)
+        return xb, xo

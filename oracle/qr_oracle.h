@@ -1,0 +1,126 @@
+/*
+ * qr_oracle.h -- CPU restatement of quantr-in-c's quantized GEMV and MoE path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker: it is loaded
+ * by tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline leg, and
+ * by nothing else.  The product (libqr_hip.so) never links, loads or calls it.
+ *
+ * Each function restates the reference's arithmetic in plain C99, in the
+ * reference's evaluation order, compiled with -ffp-contract=off so that no
+ * multiply-add is fused unless the reference fuses it explicitly.
+ *
+ * Pinning (what checks each function against something other than itself):
+ *   qro_h2f / qro_f2h           golden vectors from the compiled reference (all
+ *                               65536 codes / special floats), round-trip laws
+ *   qro_quantize_row_q8_0       golden vectors from the compiled reference
+ *   qro_dequantize_row          golden vectors (types 8, 12, 13, 14)
+ *   qro_vec_dot Q8_0 SEQ/AVX2   golden vectors from the -std=c99 and the
+ *                               -mavx2 -mfma builds of the reference
+ *   qro_vec_dot Q5_K, Q6_K      golden vectors
+ *   qro_vec_dot Q4_K            the reference's Q4_K dot is defective; the
+ *                               corrected form equals the reference's Q5_K dot
+ *                               on the same block with a zero high-bit plane,
+ *                               checked bit-exactly against golden Q5_K vectors,
+ *                               and against an fp64 dequantize-then-dot
+ *   qro_row_accum               brute-force integer sums on tiny rows
+ *   qro_matmul_f32 SEQ/AVX2     golden vectors (matmul_ref, matmul_omp AVX2)
+ *   qro_softmax                 golden vectors (softmax_ref)
+ *   qro_moe_token               golden vectors of the reference's
+ *                               forward_runtime MoE block
+ *   qro_moe_dispatch            invariants (bijection, counts, stable order)
+ *                               and brute force; no reference counterpart
+ *   qro_shared_expert           closed form; no reference counterpart
+ *                               (parity unpinned by the reference)
+ */
+#ifndef QR_ORACLE_H
+#define QR_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML type ids used by the reference (src/quant.c:478-483, src/model.c:20-30). */
+#define QRO_TYPE_F32 0
+#define QRO_TYPE_Q8_0 8
+#define QRO_TYPE_Q4_K 12
+#define QRO_TYPE_Q5_K 13
+#define QRO_TYPE_Q6_K 14
+
+/* fp32 accumulation orders of the reference builds.
+ * SEQ:    the portable C99 loops (Makefile CFLAGS -O3 -std=c99, no FMA):
+ *         matmul_ref (src/kernels.c:18-28), the scalar vec_dot_q8_0_q8_0
+ *         (src/quant.c:279-285) and every K-quant dot.
+ * AVX2:   the -mavx2 -mfma build (.github/workflows/ci.yml:21): matmul_omp's
+ *         8-lane FMA chains (src/kernels.c:50-65) and vec_dot_q8_0_q8_0's
+ *         8-lane accumulators (src/quant.c:245-277).
+ * AVX512: matmul_omp's 16-lane FMA chains + _mm512_reduce_add_ps tree
+ *         (src/kernels.c:38-49), for an -mavx512f build. */
+#define QRO_ORDER_SEQ 0
+#define QRO_ORDER_AVX2 1
+#define QRO_ORDER_AVX512 2
+
+float qro_h2f(uint16_t h);
+uint16_t qro_f2h(float f);
+void qro_h2f_batch(const uint16_t* h, float* out, long n);
+
+size_t qro_row_bytes(uint32_t type, int d);
+int qro_units_per_row(uint32_t type, int d);
+
+void qro_quantize_row_q8_0(const float* x, void* y, int k);
+void qro_dequantize_row(float* out, const void* src, uint32_t type, int n);
+
+float qro_vec_dot(uint32_t type, const void* row, const void* xq8, int d, int order);
+int qro_row_accum(uint32_t type, const void* row, const void* xq8, int d,
+                  int32_t* isum, int32_t* bsum);
+
+void qro_matmul_q_fused(float* out, const float* x, const void* w, uint32_t type,
+                        int n, int d, int threads, int order);
+void qro_matmul_q_fused_batch(float* out, const float* x, const void* w, uint32_t type,
+                              int n, int d, int nt, int threads, int order);
+void qro_matmul_f32(float* out, const float* x, const float* w, int n, int d, int order);
+
+void qro_softmax(float* x, int n);
+float qro_silu(float x);
+void qro_expf_batch(const float* in, float* out, size_t n);
+
+int qro_route(const float* xb, const float* router_w, int dim, int E, int K, int order,
+              float* logits, float* probs, int32_t* idx, float* wts);
+
+typedef struct {
+    int dim;          /* model width (Config.dim) */
+    int hidden;       /* expert ffn width (Config.hidden_dim) */
+    int n_experts;    /* Config.expert_count */
+    int n_used;       /* Config.expert_used_count */
+    const float* router;      /* ffn_gate_inp [E][dim] fp32 */
+    const void* up;           /* ffn_up_exps   [E][hidden][dim], the SiLU slot (expert_w1) */
+    const void* gate;         /* ffn_gate_exps [E][hidden][dim], the linear slot (expert_w3) */
+    const void* down;         /* ffn_down_exps [E][dim][hidden] (expert_w2) */
+    uint32_t up_type, gate_type, down_type;
+    /* Optional shared expert with a sigmoid gate (no reference counterpart). */
+    int sh_hidden;            /* 0 = none */
+    const float* sh_gate_inp; /* [dim] fp32 */
+    const void* sh_up;
+    const void* sh_gate;
+    const void* sh_down;
+    uint32_t sh_up_type, sh_gate_type, sh_down_type;
+} qro_moe_layer;
+
+size_t qro_expert_slice_bytes(uint32_t type, int ne0, int ne1);
+
+/* router_order: the router's KernelOps.matmul order (and F32 experts');
+ * dot_order: the Q8_0 fused-dot order of the build (K-quant dots have one). */
+void qro_moe_token(float* x, const float* xb, const qro_moe_layer* L, int router_order,
+                   int dot_order, int threads, int32_t* idx_out, float* w_out);
+void qro_moe_forward(float* x, const float* xb, int T, const qro_moe_layer* L, int router_order,
+                     int dot_order, int threads, int32_t* idx_out, float* w_out);
+void qro_shared_expert(float* y, const float* xb, const qro_moe_layer* L, int threads);
+int qro_moe_dispatch(const int32_t* idx, int T, int K, int E, int32_t* counts,
+                     int32_t* offsets, int32_t* perm, int32_t* inv);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,166 @@
+/*
+ * ref_driver.c -- test-only harness compiled together with the reference's own
+ * sources (src/quant.c, src/kernels.c, src/runtime.c, src/model.c, src/gguf.c,
+ * src/threadpool.c, built where they lie) into oracle/_ref/libqref_*.so.
+ *
+ * TEST INFRASTRUCTURE ONLY.  It exposes the reference's static-inline fp16
+ * helpers and KernelOps function pointers as plain exported symbols, and runs
+ * the reference's MoE block (which only exists inline in forward_runtime,
+ * src/runtime.c:202-269) on caller-supplied tensors through a one-layer
+ * in-memory Transformer.  Nothing here computes; every number comes from the
+ * reference's own code.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "kernels.h"
+#include "model.h"
+#include "quant.h"
+#include "runtime.h"
+#include "types.h"
+
+float refdrv_h2f(uint16_t h) { return fp16_to_fp32(h); }
+/* Batch form: writes through memory so NaN payloads keep their bits. */
+void refdrv_h2f_batch(const uint16_t* h, float* out, long n) {
+    long i;
+    for (i = 0; i < n; i++) out[i] = fp16_to_fp32(h[i]);
+}
+uint16_t refdrv_f2h(float f) { return fp32_to_fp16(f); }
+
+int refdrv_has_avx2_paths(void) {
+#if defined(__AVX2__)
+    return 1;
+#else
+    return 0;
+#endif
+}
+
+int refdrv_has_avx512_paths(void) {
+#if defined(__AVX512F__)
+    return 1;
+#else
+    return 0;
+#endif
+}
+
+/* KernelOps.matmul / softmax / rmsnorm of a backend (src/kernels.c:209-214). */
+void refdrv_matmul(int backend, float* out, const float* x, const float* w, int n, int d) {
+    kernels_for_backend((KernelBackend)backend)->matmul(out, x, w, n, d, 1);
+}
+void refdrv_softmax(int backend, float* x, int n) {
+    kernels_for_backend((KernelBackend)backend)->softmax(x, n);
+}
+void refdrv_rmsnorm(int backend, float* o, const float* x, const float* w, int n) {
+    kernels_for_backend((KernelBackend)backend)->rmsnorm(o, x, w, n);
+}
+
+/*
+ * Run the reference's forward_runtime on a one-layer MoE model for T tokens.
+ * Token t's embedding row is x_in[t] (an F32 table); attention weights are
+ * NULL so the attention block adds exactly zero; the MoE input is therefore
+ * xb = rmsnorm(x_in[t]) with unit weights, returned in xb_out[t], and the
+ * residual after the MoE block is returned in x_out[t].  The backend picks the
+ * router's KernelOps.matmul order; threads is the OpenMP width of
+ * matmul_q_fused.  Experts are [E][rows][cols] tensors sliced as
+ * src/model.c:412-419 does.
+ */
+int refdrv_moe_layer(const float* x_in, float* xb_out, float* x_out, int T, int dim, int hidden,
+                     int E, int K, const float* router, const void* up, uint32_t up_type,
+                     const void* gate, uint32_t gate_type, const void* down, uint32_t down_type,
+                     int backend, int threads) {
+    Transformer t;
+    RuntimeContext rt;
+    RuntimeOptions opt;
+    float* ones;
+    float* rms_att[1];
+    float* rms_ffn[1];
+    float* null_l[1] = {NULL};
+    float* router_l[1];
+    float** ew1[1];
+    float** ew2[1];
+    float** ew3[1];
+    uint32_t t_up[1], t_down[1], t_gate[1];
+    size_t s_up, s_down, s_gate;
+    int e, tok;
+
+    if (E > 256 || K > 16 || K > E) return -1;
+    memset(&t, 0, sizeof(t));
+    t.config.dim = dim;
+    t.config.hidden_dim = hidden;
+    t.config.n_layers = 1;
+    t.config.n_heads = 1;
+    t.config.n_kv_heads = 1;
+    t.config.vocab_size = 1;
+    t.config.seq_len = 1;
+    t.config.rope_freq_base = 10000.0f;
+    t.config.expert_count = E;
+    t.config.expert_used_count = K;
+
+    ones = (float*)malloc((size_t)dim * sizeof(float));
+    ew1[0] = (float**)malloc((size_t)E * sizeof(float*));
+    ew2[0] = (float**)malloc((size_t)E * sizeof(float*));
+    ew3[0] = (float**)malloc((size_t)E * sizeof(float*));
+    if (!ones || !ew1[0] || !ew2[0] || !ew3[0]) return -2;
+    for (e = 0; e < dim; e++) ones[e] = 1.0f;
+
+    s_up = (up_type == 8 ? (size_t)(dim / 32) * 34 : up_type == 12 ? (size_t)(dim / 256) * 144
+            : up_type == 13 ? (size_t)(dim / 256) * 176 : up_type == 14 ? (size_t)(dim / 256) * 210
+            : (size_t)dim * 4) * (size_t)hidden;
+    s_gate = (gate_type == 8 ? (size_t)(dim / 32) * 34 : gate_type == 12 ? (size_t)(dim / 256) * 144
+              : gate_type == 13 ? (size_t)(dim / 256) * 176 : gate_type == 14 ? (size_t)(dim / 256) * 210
+              : (size_t)dim * 4) * (size_t)hidden;
+    s_down = (down_type == 8 ? (size_t)(hidden / 32) * 34 : down_type == 12 ? (size_t)(hidden / 256) * 144
+              : down_type == 13 ? (size_t)(hidden / 256) * 176 : down_type == 14 ? (size_t)(hidden / 256) * 210
+              : (size_t)hidden * 4) * (size_t)dim;
+    for (e = 0; e < E; e++) {
+        ew1[0][e] = (float*)((const char*)up + (size_t)e * s_up);
+        ew3[0][e] = (float*)((const char*)gate + (size_t)e * s_gate);
+        ew2[0][e] = (float*)((const char*)down + (size_t)e * s_down);
+    }
+    rms_att[0] = ones;
+    rms_ffn[0] = ones;
+    router_l[0] = (float*)router;
+    t_up[0] = up_type;
+    t_down[0] = down_type;
+    t_gate[0] = gate_type;
+
+    t.weights.token_embedding_table = (float*)x_in;
+    t.weights.token_embd_type = 0;
+    t.weights.token_embd_row_bytes = (size_t)dim * sizeof(float);
+    t.weights.rms_att_weight = rms_att;
+    t.weights.rms_ffn_weight = rms_ffn;
+    t.weights.wq = null_l;
+    t.weights.wk = null_l;
+    t.weights.wv = null_l;
+    t.weights.wo = null_l;
+    t.weights.rms_final_weight = ones;
+    t.weights.wcls = NULL;
+    t.weights.ffn_gate_inp = router_l;
+    t.weights.expert_w1 = ew1;
+    t.weights.expert_w2 = ew2;
+    t.weights.expert_w3 = ew3;
+    t.weights.exp_w1_type = t_up;
+    t.weights.exp_w2_type = t_down;
+    t.weights.exp_w3_type = t_gate;
+    malloc_run_state(&t.state, &t.config);
+
+    memset(&opt, 0, sizeof(opt));
+    opt.backend = (KernelBackend)backend;
+    opt.num_threads = threads;
+    runtime_init(&rt, opt);
+
+    for (tok = 0; tok < T; tok++) {
+        if (xb_out) {
+            rt.kernels->rmsnorm(xb_out + (size_t)tok * dim, x_in + (size_t)tok * dim, ones, dim);
+        }
+        forward_runtime(&rt, &t, tok, 0);
+        if (x_out) memcpy(x_out + (size_t)tok * dim, t.state.x, (size_t)dim * sizeof(float));
+    }
+
+    free_run_state(&t.state);
+    free(ones);
+    free(ew1[0]);
+    free(ew2[0]);
+    free(ew3[0]);
+    return 0;
+}

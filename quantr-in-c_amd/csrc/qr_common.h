@@ -1,0 +1,119 @@
+// qr_common.h -- block formats and exact scalar numerics shared by the gfx950
+// kernels of libqr_hip.so.
+//
+// Everything here is bit-exact with quantr-in-c's C99 code when compiled with
+// -ffp-contract=off (the library's build flag): every float operation rounds
+// once, in the written order, as the reference's -std=c99 build does.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+// GGML type ids (src/quant.c:478-483).
+#define QR_T_F32 0
+#define QR_T_Q8_0 8
+#define QR_T_Q4_K 12
+#define QR_T_Q5_K 13
+#define QR_T_Q6_K 14
+
+#define QR_Q8_BYTES 34   // block_q8_0, include/quant.h:28-33
+#define QR_Q4K_BYTES 144 // block_q4_K, include/quant.h:35-42
+#define QR_Q5K_BYTES 176 // block_q5_K, include/quant.h:44-50
+#define QR_Q6K_BYTES 210 // raw Q6_K block, src/quant.c:220-226
+
+// fp16 bits -> fp32 by exponent rebias (include/quant.h:53-66).  Half
+// subnormals keep exponent 0 and decode to mant * 2^-136, as in the reference.
+__host__ __device__ inline float qr_h2f(uint32_t h) {
+  uint32_t w = (h & 0x7FFFu) << 13;
+  const uint32_t sign = (h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1Fu;
+  if (e == 0x1Fu) {
+    w |= 0x7F800000u;
+  } else if (e != 0) {
+    w += 0x38000000u;
+  }
+  w |= sign;
+  return __builtin_bit_cast(float, w);
+}
+
+// Truncating fp32 -> fp16 bits (include/quant.h:68-77): exponents at or below
+// zero flush to signed zero, at or above 31 saturate to infinity, the mantissa
+// is cut, never rounded.
+__host__ __device__ inline uint32_t qr_f2h(float f) {
+  const uint32_t x = __builtin_bit_cast(uint32_t, f);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const int e = (int)((x >> 23) & 0xFFu) - 127 + 15;
+  if (e <= 0) return sign;
+  if (e >= 31) return sign | 0x7C00u;
+  return sign | ((uint32_t)e << 10) | ((x >> 13) & 0x3FFu);
+}
+
+// expf, bit-exact with glibc's (the reference calls glibc expf in
+// softmax_ref, src/kernels.c:200, and silu, src/runtime.c:16).  glibc >= 2.27
+// uses the published ARM optimized-routines algorithm (Szabolcs Nagy): with
+// N = 32, z = x*N/ln2 is split into an integer k and r = z - k, 2^(k/N) comes
+// from a table of the correctly rounded 2^(i/N) with the exponent bits of
+// i/N removed, and 2^(r/N) from a cubic, all in double, rounded once to float.
+// glibc's x86-64 FMA build fuses the reduction r = x*N/ln2 - k and the cubic's
+// multiply-adds; so does this, and with that every float input gives glibc's
+// bits (an exhaustive CPU test compares all 2^32 inputs with the host libm).
+__host__ __device__ inline float qr_expf(float x) {
+  constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
+  constexpr double kShift = 0x1.8p+52;
+  constexpr double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+  constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+  constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+  constexpr uint64_t kTab[32] = {
+      0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+      0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+      0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+      0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+      0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+      0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+      0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+      0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+  };
+  const uint32_t ux = __builtin_bit_cast(uint32_t, x);
+  const uint32_t abstop = (ux >> 20) & 0x7FFu;
+  if (abstop >= 0x42Bu) {  // |x| >= 88, inf or nan
+    if (ux == 0xFF800000u) return 0.0f;         // -inf
+    if (abstop >= 0x7F8u) return x + x;          // +inf, nan
+    if (x > 0x1.62e42ep6f) return __builtin_bit_cast(float, 0x7F800000u);  // overflow
+    if (x < -0x1.9fe368p6f) return 0.0f;         // underflow
+  }
+  const double xd = (double)x;
+  const double z = kInvLn2N * xd;
+  double kd = z + kShift;
+  const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+  kd -= kShift;
+  // glibc's FMA build contracts z - kd into one fused operation
+  const double r = __builtin_fma(kInvLn2N, xd, -kd);
+  const uint64_t t = kTab[ki % 32] + (ki << 47);
+  const double s = __builtin_bit_cast(double, t);
+  const double p = __builtin_fma(kC0, r, kC1);
+  const double r2 = r * r;
+  double y = __builtin_fma(kC2, r, 1.0);
+  y = __builtin_fma(p, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+// silu(x) = x / (1 + expf(-x)) (src/runtime.c:15-17).
+__host__ __device__ inline float qr_silu(float x) { return x / (1.0f + qr_expf(-x)); }
+
+__host__ __device__ inline int qr_block_elems(int type) { return type == QR_T_Q8_0 ? 32 : 256; }
+__host__ __device__ inline int qr_block_bytes(int type) {
+  return type == QR_T_Q8_0 ? QR_Q8_BYTES
+       : type == QR_T_Q4_K ? QR_Q4K_BYTES
+       : type == QR_T_Q5_K ? QR_Q5K_BYTES
+       : type == QR_T_Q6_K ? QR_Q6K_BYTES : 4;
+}
+// Bytes per weight row, whole blocks only (src/quant.c:477-484).
+__host__ __device__ inline size_t qr_wrow_bytes(int type, int d) {
+  if (type == QR_T_F32) return (size_t)d * 4u;
+  return (size_t)(d / qr_block_elems(type)) * (size_t)qr_block_bytes(type);
+}
+// 32-element integer units (= fp32 terms) per row.
+__host__ __device__ inline int qr_units(int type, int d) {
+  return type == QR_T_Q8_0 ? d / 32 : (d / 256) * 8;
+}

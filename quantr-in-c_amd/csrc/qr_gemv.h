@@ -1,0 +1,356 @@
+// qr_gemv.h -- device building blocks of the quantized GEMV: the in-LDS Q8_0
+// activation quantizer, per-format 32-element unit dots, and the sequential
+// per-row fp32 reduction.  Shared by the plain GEMV kernels (qr_gemv.hip) and
+// the grouped MoE expert kernels (qr_moe.hip).
+#pragma once
+
+#include "qr_common.h"
+
+namespace qr {
+
+// ---------------------------------------------------------------------------
+// Activation in LDS.  One token's Q8_0 activation is d int8 values plus, per
+// 32-element block, the decoded fp16 scale (float) and the integer sum of the
+// block's values.  K-quant nibble layouts pair element 2i with 2i+1 in one
+// byte; for Q4_K the int8 values are stored per 8-element group as
+// [x0 x2 x4 x6 | x1 x3 x5 x7] so that the low and high nibbles of one weight
+// dword multiply one activation dword each.  Other formats use natural order.
+// ---------------------------------------------------------------------------
+struct ActLds {
+  int8_t* q;     // [nt][(d/32)*32]
+  float* bd;     // [nt][d/32]  h2f(f2h(d)) of each block
+  int32_t* bs;   // [nt][d/32]  sum of the block's int8 values
+};
+
+__device__ inline uint32_t pack4(int a, int b, int c, int e) {
+  return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) | ((uint32_t)(uint8_t)c << 16) |
+         ((uint32_t)(uint8_t)e << 24);
+}
+
+// quantize_row_q8_0 (src/quant.c:143-158) of nt rows x[t*xstride .. +d) into
+// LDS, by the whole workgroup.  Each thread owns 8-element groups; the four
+// threads of one 32-block are adjacent lanes, so amax and the block sum reduce
+// with two xor-shuffles.  amax is a max (order-free); d = amax/127 and 1/d
+// are correctly rounded IEEE divisions; rintf rounds ties to even like
+// lrintf; the stored scale goes through the truncating fp16 routine.
+//
+// Rows t < nlive come from x + rows[t] * xstride (rows may be null: row t);
+// rows nlive <= t < nt are filled with zeros so that every LDS slot a kernel
+// may read is defined.
+template <bool PERM>
+__device__ inline void quantize_act_lds(const float* __restrict__ x, size_t xstride,
+                                        const int* rows, int nlive, int nt, int d, ActLds a) {
+  const int nxb = d >> 5;                 // whole 32-blocks; a shorter tail is ignored
+  const int ngroups = nxb * 4;            // 8-element groups per row
+  const int qstride = nxb * 32;           // LDS row stride of the int8 values
+  const int total = nt * ngroups;
+  const int nthr = blockDim.x;            // a multiple of 64
+  for (int base = 0; base < ((total + nthr - 1) / nthr) * nthr; base += nthr) {
+    const int gi = base + (int)threadIdx.x;
+    const bool live = gi < total;
+    const int t = live ? gi / ngroups : 0;
+    const int g = live ? gi - t * ngroups : 0;
+    float v[8];
+    if (live && t < nlive) {
+      const size_t row = rows ? (size_t)rows[t] : (size_t)t;
+      const float4* p = reinterpret_cast<const float4*>(x + row * xstride + (size_t)g * 8);
+      const float4 u0 = p[0], u1 = p[1];
+      v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w;
+      v[4] = u1.x; v[5] = u1.y; v[6] = u1.z; v[7] = u1.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float av = __builtin_fabsf(v[i]);
+      amax = av > amax ? av : amax;
+    }
+    // groups g..g+3 of one block sit in lanes 4k..4k+3 when nthr % 4 == 0
+    float o1 = __shfl_xor(amax, 1);
+    amax = o1 > amax ? o1 : amax;
+    o1 = __shfl_xor(amax, 2);
+    amax = o1 > amax ? o1 : amax;
+    const float dd = amax / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    int q[8];
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      q[i] = (int)(int8_t)(int)__builtin_rintf(v[i] * id);
+      s += q[i];
+    }
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    if (live) {
+      uint32_t w0, w1;
+      if (PERM) {
+        w0 = pack4(q[0], q[2], q[4], q[6]);
+        w1 = pack4(q[1], q[3], q[5], q[7]);
+      } else {
+        w0 = pack4(q[0], q[1], q[2], q[3]);
+        w1 = pack4(q[4], q[5], q[6], q[7]);
+      }
+      uint2* dst = reinterpret_cast<uint2*>(a.q + (size_t)t * qstride + (size_t)g * 8);
+      *dst = make_uint2(w0, w1);
+      if ((g & 3) == 0) {
+        const int b = t * nxb + (g >> 2);
+        a.bd[b] = qr_h2f(qr_f2h(dd));
+        a.bs[b] = s;
+      }
+    }
+  }
+}
+
+__device__ inline int sdot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Spread 4 bits to bit 0 of 4 bytes (no carries: the shifted copies of the 4
+// bits land on distinct positions).
+__device__ inline uint32_t spread4(uint32_t x) { return ((x & 0xFu) * 0x00204081u) & 0x01010101u; }
+// Spread the four 2-bit fields of a byte to bits 0-1 of 4 bytes.
+__device__ inline uint32_t spread2x4(uint32_t b) {
+  uint32_t t = (b | (b << 12)) & 0x000F000Fu;
+  return (t | (t << 6)) & 0x03030303u;
+}
+// Interleave the low / high nibble bytes of a packed dword back into element
+// order: lo holds elements 0,2,4,6 and hi 1,3,5,7 (one per byte).
+__device__ inline uint32_t nib_lo_pair(uint32_t lo, uint32_t hi) {
+  return __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // [lo0 hi0 lo1 hi1]
+}
+__device__ inline uint32_t nib_hi_pair(uint32_t lo, uint32_t hi) {
+  return __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // [lo2 hi2 lo3 hi3]
+}
+
+// Unaligned dword from LDS (byte offset o), from two aligned dwords.
+__device__ inline uint32_t lds_u32(const uint32_t* lds, int o) {
+  const uint32_t lo = lds[o >> 2];
+  const uint32_t hi = lds[(o >> 2) + 1];
+  return __builtin_amdgcn_alignbyte(hi, lo, (uint32_t)(o & 3));
+}
+
+// ---------------------------------------------------------------------------
+// Per-unit integer dots.  A unit is 32 weights against one Q8_0 activation
+// block; `xa` points at its 32 int8 values in LDS (4-byte aligned).
+// ---------------------------------------------------------------------------
+
+// Q4_K sub-block: 16 bytes of nibbles against a PERM-layout activation.
+__device__ inline int dot_q4_unit(uint4 qs, const int8_t* xa) {
+  const uint4 x0 = *reinterpret_cast<const uint4*>(xa);
+  const uint4 x1 = *reinterpret_cast<const uint4*>(xa + 16);
+  int acc = 0;
+  acc = sdot4(qs.x & 0x0F0F0F0Fu, x0.x, acc);
+  acc = sdot4((qs.x >> 4) & 0x0F0F0F0Fu, x0.y, acc);
+  acc = sdot4(qs.y & 0x0F0F0F0Fu, x0.z, acc);
+  acc = sdot4((qs.y >> 4) & 0x0F0F0F0Fu, x0.w, acc);
+  acc = sdot4(qs.z & 0x0F0F0F0Fu, x1.x, acc);
+  acc = sdot4((qs.z >> 4) & 0x0F0F0F0Fu, x1.y, acc);
+  acc = sdot4(qs.w & 0x0F0F0F0Fu, x1.z, acc);
+  acc = sdot4((qs.w >> 4) & 0x0F0F0F0Fu, x1.w, acc);
+  return acc;
+}
+
+// 4-bit nibbles (+ optional high bits already spread per natural dword)
+// against a natural-order activation.  w holds 4 packed dwords (32 nibbles).
+__device__ inline int dot_nib_natural(uint4 qs, const uint32_t hb[8], const int8_t* xa) {
+  const uint4 x0 = *reinterpret_cast<const uint4*>(xa);
+  const uint4 x1 = *reinterpret_cast<const uint4*>(xa + 16);
+  const uint32_t wq[4] = {qs.x, qs.y, qs.z, qs.w};
+  const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  int acc = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const uint32_t lo = wq[k] & 0x0F0F0F0Fu;
+    const uint32_t hi = (wq[k] >> 4) & 0x0F0F0F0Fu;
+    acc = sdot4(nib_lo_pair(lo, hi) | hb[2 * k], xv[2 * k], acc);
+    acc = sdot4(nib_hi_pair(lo, hi) | hb[2 * k + 1], xv[2 * k + 1], acc);
+  }
+  return acc;
+}
+
+// Q5_K sub-block: nibbles plus the fifth-bit dword (bit l = element l).
+__device__ inline int dot_q5_unit(uint4 qs, uint32_t qh, const int8_t* xa) {
+  uint32_t hb[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) hb[i] = spread4(qh >> (4 * i)) << 4;
+  return dot_nib_natural(qs, hb, xa);
+}
+
+// Q6_K sub-block: 16 bytes of low nibbles plus 8 bytes of 2-bit high pairs
+// (byte i holds elements 4i..4i+3).  Returns sum(q * x) with q in 0..63; the
+// caller subtracts 32 * bsum to get the reference's sum((q - 32) * x).
+__device__ inline int dot_q6_unit_raw(uint4 ql, uint2 qh, const int8_t* xa) {
+  uint32_t hb[8];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    hb[i] = spread2x4((qh.x >> (8 * i)) & 0xFFu) << 4;
+    hb[4 + i] = spread2x4((qh.y >> (8 * i)) & 0xFFu) << 4;
+  }
+  return dot_nib_natural(ql, hb, xa);
+}
+
+// Q8_0 block: 8 dwords of int8 weights against a natural-order activation.
+__device__ inline int dot_q8_unit(const uint32_t w[8], const int8_t* xa) {
+  const uint4 x0 = *reinterpret_cast<const uint4*>(xa);
+  const uint4 x1 = *reinterpret_cast<const uint4*>(xa + 16);
+  int acc = 0;
+  acc = sdot4(w[0], x0.x, acc);
+  acc = sdot4(w[1], x0.y, acc);
+  acc = sdot4(w[2], x0.z, acc);
+  acc = sdot4(w[3], x0.w, acc);
+  acc = sdot4(w[4], x1.x, acc);
+  acc = sdot4(w[5], x1.y, acc);
+  acc = sdot4(w[6], x1.z, acc);
+  acc = sdot4(w[7], x1.w, acc);
+  return acc;
+}
+
+// fp32 terms, in the reference's operation order (contraction is off).
+// Q4_K/Q5_K: (sc*isum - m*bsum) * bd   (src/quant.c:399)
+__device__ inline float term_q45(uint32_t hdr0, uint32_t sbyte, int isum, int bsum, float bd) {
+  const float d = qr_h2f(hdr0 & 0xFFFFu);
+  const float dmin = qr_h2f(hdr0 >> 16);
+  const float sc = (float)(sbyte & 63u) * d;
+  const float m = (float)(sbyte >> 6) * dmin;
+  return (sc * (float)isum - m * (float)bsum) * bd;
+}
+// Q6_K: sc * isum * bd, left to right (src/quant.c:433)
+__device__ inline float term_q6(int scale_i8, uint32_t dh, int isum, float bd) {
+  const float sc = (float)scale_i8 * qr_h2f(dh);
+  return sc * (float)isum * bd;
+}
+// Q8_0: isum * da * db, left to right (src/quant.c:284)
+__device__ inline float term_q8(uint32_t dh, int isum, float bd) {
+  return (float)isum * qr_h2f(dh) * bd;
+}
+
+
+// ---------------------------------------------------------------------------
+// Weight tiles.  A tile is R consecutive rows of one [rows][row_bytes]
+// matrix: one contiguous byte range.
+// ---------------------------------------------------------------------------
+template <int TYPE>
+struct Fmt {
+  // 144- and 176-byte blocks keep every sub-block 16-byte aligned: lanes load
+  // their own bytes with 128-bit global loads.  34- and 210-byte blocks do
+  // not: the tile is first copied to LDS with 128-bit loads.
+  static constexpr bool kDirect = (TYPE == QR_T_Q4_K || TYPE == QR_T_Q5_K);
+  static constexpr bool kPerm = (TYPE == QR_T_Q4_K);
+};
+
+__host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
+
+// LDS bytes of a staged tile of `bytes` bytes starting anywhere: up to 15
+// bytes of head, the tail rounded to 16, and one slack dword for lds_u32.
+__host__ __device__ inline size_t stage_bytes(size_t bytes) { return align16(bytes + 15 + 4 + 15); }
+
+// Copy matrix bytes [gstart, gend) into LDS; LDS byte 0 is matrix byte
+// (gstart & ~15).  `total` is the matrix size: whole 16-byte chunks use
+// 128-bit loads, a chunk reaching past `total` is read a dword or half-word
+// at a time, so no load leaves the matrix (row sizes are even).
+__device__ inline void stage_tile(const uint8_t* __restrict__ W, size_t total, size_t gstart,
+                                  size_t gend, uint32_t* lds) {
+  const size_t a0 = gstart & ~(size_t)15;
+  const int nch = (int)((gend - a0 + 15) >> 4);
+  for (int c = threadIdx.x; c < nch; c += blockDim.x) {
+    const size_t off = a0 + (size_t)c * 16;
+    uint4 v;
+    if (off + 16 <= total) {
+      v = *reinterpret_cast<const uint4*>(W + off);
+    } else {
+      uint32_t w[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const size_t o = off + 4 * k;
+        if (o + 4 <= total) w[k] = *reinterpret_cast<const uint32_t*>(W + o);
+        else if (o + 2 <= total) w[k] = *reinterpret_cast<const uint16_t*>(W + o);
+        else w[k] = 0;
+      }
+      v = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    reinterpret_cast<uint4*>(lds)[c] = v;
+  }
+}
+
+struct UnitSrc {
+  const uint32_t* tile;  // staged tile (Q8_0 / Q6_K)
+  ActLds act;            // quantized activation rows
+  int nxb;               // activation blocks per row (d / 32)
+};
+
+// Terms (and int32 sums) of unit u of one row for NT activation rows
+// tok0 .. tok0+NT-1.  `wrow` is the row in global memory (direct formats),
+// `row_lds` its byte offset in the staged tile (staged formats).
+template <int TYPE, int NT>
+__device__ inline void unit_terms(const uint8_t* __restrict__ wrow, int row_lds, int u,
+                                  const UnitSrc& S, int tok0, float* terms_out,
+                                  int32_t* isum_out) {
+  const int nxb = S.nxb;
+  if constexpr (TYPE == QR_T_Q4_K || TYPE == QR_T_Q5_K) {
+    const int b = u >> 3, s = u & 7;
+    const uint8_t* blk = wrow + (size_t)b * (TYPE == QR_T_Q4_K ? QR_Q4K_BYTES : QR_Q5K_BYTES);
+    const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
+    const uint32_t sbyte = ((s < 4 ? hdr.y : hdr.z) >> (8 * (s & 3))) & 0xFFu;
+    uint4 qs;
+    uint32_t qh = 0;
+    if constexpr (TYPE == QR_T_Q4_K) {
+      qs = *reinterpret_cast<const uint4*>(blk + 16 + 16 * s);
+    } else {
+      qs = *reinterpret_cast<const uint4*>(blk + 48 + 16 * s);
+      qh = *reinterpret_cast<const uint32_t*>(blk + 16 + 4 * s);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const int a = (tok0 + t) * nxb + u;
+      const int8_t* xa = S.act.q + (size_t)a * 32;
+      int isum;
+      if constexpr (TYPE == QR_T_Q4_K) isum = dot_q4_unit(qs, xa);
+      else isum = dot_q5_unit(qs, qh, xa);
+      terms_out[t] = term_q45(hdr.x, sbyte, isum, S.act.bs[a], S.act.bd[a]);
+      isum_out[t] = isum;
+    }
+  } else if constexpr (TYPE == QR_T_Q6_K) {
+    const int b = u >> 3, s = u & 7;
+    const int o = row_lds + b * QR_Q6K_BYTES;
+    const uint32_t* T = S.tile;
+    const uint4 ql = make_uint4(lds_u32(T, o + 16 * s), lds_u32(T, o + 16 * s + 4),
+                                lds_u32(T, o + 16 * s + 8), lds_u32(T, o + 16 * s + 12));
+    const uint2 qh = make_uint2(lds_u32(T, o + 128 + 8 * s), lds_u32(T, o + 128 + 8 * s + 4));
+    const int scale = (int)(int8_t)(lds_u32(T, o + 192 + s) & 0xFFu);
+    const uint32_t dh = lds_u32(T, o + 208) & 0xFFFFu;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const int a = (tok0 + t) * nxb + u;
+      const int8_t* xa = S.act.q + (size_t)a * 32;
+      const int isum = dot_q6_unit_raw(ql, qh, xa) - 32 * S.act.bs[a];
+      terms_out[t] = term_q6(scale, dh, isum, S.act.bd[a]);
+      isum_out[t] = isum;
+    }
+  } else {  // Q8_0
+    const int o = row_lds + u * QR_Q8_BYTES;
+    const uint32_t* T = S.tile;
+    const uint32_t dh = lds_u32(T, o) & 0xFFFFu;
+    uint32_t w[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) w[k] = lds_u32(T, o + 2 + 4 * k);
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const int a = (tok0 + t) * nxb + u;
+      const int isum = dot_q8_unit(w, S.act.q + (size_t)a * 32);
+      terms_out[t] = term_q8(dh, isum, S.act.bd[a]);
+      isum_out[t] = isum;
+    }
+  }
+}
+
+// Sequential sum of one row's terms from 0.0f, unit 0 first (the fp32
+// accumulation of every reference dot, src/quant.c:279-285, 384-400, 422-434).
+__device__ inline float row_sum(const float* tp, int U) {
+  float s = 0.0f;
+  for (int u = 0; u < U; u++) s += tp[u];
+  return s;
+}
+
+}  // namespace qr

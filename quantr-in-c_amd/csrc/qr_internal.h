@@ -1,0 +1,51 @@
+// qr_internal.h -- declarations shared between the .hip translation units of
+// libqr_hip.so (not part of the C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/qr_hip.h"
+
+namespace qr {
+
+// qr_gemv.hip
+size_t gemv_lds_bytes(int type, int d, int nt, int R);
+int gemv_rows_per_wg(int type, int n, int d, int nt);
+hipError_t gemv_launch(int type, const void* W, const float* X, float* Y, int n, int d, int nt,
+                       int xstride, int ystride, int32_t* acc, int32_t* accb, hipStream_t st);
+hipError_t gemv_f32_launch(int order, const float* W, const float* X, float* Y, int n, int d,
+                           int nt, int xstride, int ystride, hipStream_t st);
+hipError_t quantize_q8_0_launch(const float* x, void* y, long nblocks, hipStream_t st);
+
+// qr_moe.hip
+struct MoeScratch {
+  // Device buffers sized for T tokens (grown on demand by the runtime).
+  float* logits;      // [T][E]
+  int32_t* idx;       // [T][K]
+  float* wts;         // [T][K]
+  int32_t* counts;    // [E]
+  int32_t* offsets;   // [E+1]
+  int32_t* tiles;     // [E+1] exclusive scan of ceil(counts[e] / token tile)
+  int32_t* perm;      // [T*K]
+  int32_t* inv;       // [T*K]
+  float* hb;          // [T*K][hidden]
+  float* y;           // [T*K][dim]
+  float* hbs;         // [T][sh_hidden]  shared expert
+  float* ysh;         // [T][dim]        shared expert output
+  float* sgl;         // [T]             shared expert gate logit
+};
+size_t moe_scratch_bytes(const qr_moe_layer* L, int T);
+void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s);
+hipError_t moe_route_launch(const qr_moe_layer* L, const float* xb, int T, int order,
+                            float* logits, float* probs, int32_t* idx, float* wts,
+                            hipStream_t st);
+hipError_t moe_dispatch_launch(const int32_t* idx, int T, int K, int E, int tile, int32_t* counts,
+                               int32_t* offsets, int32_t* tiles, int32_t* perm, int32_t* inv,
+                               hipStream_t st);
+hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, int T, int order,
+                              const MoeScratch& s, hipStream_t st);
+hipError_t softmax_launch(float* x, int rows, int n, hipStream_t st);
+
+}  // namespace qr

@@ -1,0 +1,798 @@
+// qr_moe.hip -- the MoE layer of quantr-in-c (src/runtime.c:202-269) for T
+// tokens on gfx950, bit-exact with the reference's per-token block:
+//
+//   logits  = W_r . xb          (KernelOps.matmul order: SEQ / AVX2 / AVX512)
+//   probs   = softmax_ref(logits)                       src/kernels.c:191-207
+//   idx,w   = K argmax passes, strict '>', mask -1e9f   src/runtime.c:208-222
+//   w      /= sequential sum of w                       src/runtime.c:224-230
+//   per slot k:  hb = silu(up_e . xb) * (gate_e . xb)   src/runtime.c:252-256
+//                y  = down_e . hb   (hb re-quantised)   src/runtime.c:259-260
+//                xb2 += y * w_k     (slot order)        src/runtime.c:262-264
+//   x += xb2                                            src/runtime.c:267-269
+//
+// Kernels:
+//   k_route_topk     one wave per token: softmax (glibc-exact expf), top-K,
+//                    renormalisation.
+//   k_dispatch       T > 1: histogram, exclusive scan and a stable permute of
+//                    the T*K (token, slot) pairs by expert; ranks come from
+//                    wave ballots and per-wave counts, never from the order in
+//                    which atomics land.
+//   k_expert         grouped GEMV over (row tile, work item); a work item is
+//                    up to NT pairs of one expert, so each weight tile is
+//                    read once for NT tokens.  Gate/up mode runs both
+//                    matrices and writes silu(up) * gate.
+//   k_down_combine1  T == 1: all K down projections of the token plus the
+//                    slot-order combine (and the shared expert) in one pass.
+//   k_combine        T > 1: slot-order gather-combine.
+#include "qr_gemv.h"
+#include "qr_internal.h"
+
+namespace qr {
+
+constexpr float kMask = -1e9f;  // src/runtime.c:211, 221
+
+// ---------------------------------------------------------------------------
+// Scratch.
+// ---------------------------------------------------------------------------
+static size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+size_t moe_scratch_bytes(const qr_moe_layer* L, int T) {
+  const size_t E = L->n_experts, K = L->n_used, P = (size_t)T * K;
+  size_t b = 0;
+  b += a256(T * E * 4);            // logits
+  b += a256(P * 4) * 2;            // idx, wts
+  b += a256(E * 4);                // counts
+  b += a256((E + 1) * 4) * 2;      // offsets, tiles
+  b += a256(P * 4) * 2;            // perm, inv
+  b += a256(P * (size_t)L->hidden * 4);
+  b += a256(P * (size_t)L->dim * 4);
+  const size_t sh = L->sh_hidden > 0 ? (size_t)L->sh_hidden : 0;
+  b += a256((size_t)T * (sh ? sh : 1) * 4);
+  b += a256((size_t)T * L->dim * 4);
+  b += a256((size_t)T * 4);
+  return b;
+}
+
+void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s) {
+  const size_t E = L->n_experts, K = L->n_used, P = (size_t)T * K;
+  uint8_t* p = static_cast<uint8_t*>(base);
+  auto take = [&](size_t bytes) {
+    uint8_t* r = p;
+    p += a256(bytes);
+    return r;
+  };
+  s->logits = reinterpret_cast<float*>(take(T * E * 4));
+  s->idx = reinterpret_cast<int32_t*>(take(P * 4));
+  s->wts = reinterpret_cast<float*>(take(P * 4));
+  s->counts = reinterpret_cast<int32_t*>(take(E * 4));
+  s->offsets = reinterpret_cast<int32_t*>(take((E + 1) * 4));
+  s->tiles = reinterpret_cast<int32_t*>(take((E + 1) * 4));
+  s->perm = reinterpret_cast<int32_t*>(take(P * 4));
+  s->inv = reinterpret_cast<int32_t*>(take(P * 4));
+  s->hb = reinterpret_cast<float*>(take(P * (size_t)L->hidden * 4));
+  s->y = reinterpret_cast<float*>(take(P * (size_t)L->dim * 4));
+  const size_t sh = L->sh_hidden > 0 ? (size_t)L->sh_hidden : 0;
+  s->hbs = reinterpret_cast<float*>(take((size_t)T * (sh ? sh : 1) * 4));
+  s->ysh = reinterpret_cast<float*>(take((size_t)T * L->dim * 4));
+  s->sgl = reinterpret_cast<float*>(take((size_t)T * 4));
+}
+
+// ---------------------------------------------------------------------------
+// Router: softmax + top-K + renormalisation, one wave per token.
+// ---------------------------------------------------------------------------
+constexpr int kRouteWaves = 4;
+
+__global__ __launch_bounds__(64 * kRouteWaves) void k_route_topk(const float* __restrict__ logits,
+                                                                  int T, int E, int K,
+                                                                  float* __restrict__ probs,
+                                                                  int32_t* __restrict__ idx,
+                                                                  float* __restrict__ wts) {
+  __shared__ float P[kRouteWaves][256];
+  __shared__ float Wk[kRouteWaves][16];
+  __shared__ float Inv[kRouteWaves];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * kRouteWaves + wave;
+  const bool live = t < T;  // uniform per wave; every thread reaches every barrier
+  const float* lg = logits + (size_t)(live ? t : 0) * E;
+  float* pw = P[wave];
+
+  // max: seeded with x[0], strictly greater wins (src/kernels.c:192-197)
+  float mx = live ? lg[0] : 0.0f;
+  for (int e = lane; e < E; e += 64) {
+    const float v = live ? lg[e] : 0.0f;
+    if (v > mx) mx = v;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v = __shfl_xor(mx, o);
+    if (v > mx) mx = v;
+  }
+  for (int e = lane; e < E; e += 64) pw[e] = live ? qr_expf(lg[e] - mx) : 0.0f;
+  __syncthreads();
+  if (lane == 0) {
+    float sum = 0.0f;  // sequential, e ascending (src/kernels.c:198-202)
+    for (int e = 0; e < E; e++) sum += pw[e];
+    Inv[wave] = 1.0f / sum;
+  }
+  __syncthreads();
+  const float inv = Inv[wave];
+  for (int e = lane; e < E; e += 64) {
+    const float v = pw[e] * inv;
+    pw[e] = v;
+    if (live && probs) probs[(size_t)t * E + e] = v;
+  }
+  __syncthreads();
+
+  // K argmax passes (src/runtime.c:210-222): the winner is the lowest index
+  // holding the maximum value; values must beat -1e9f.
+  for (int k = 0; k < K; k++) {
+    float bv = kMask;
+    int bi = -1;
+    for (int e = lane; e < E; e += 64) {
+      const float v = pw[e];
+      if (v > bv) {
+        bv = v;
+        bi = e;
+      }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (ov > bv || (ov == bv && oi >= 0 && (bi < 0 || oi < bi))) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane == 0) {
+      Wk[wave][k] = bv;
+      if (live) idx[(size_t)t * K + k] = bi;
+    }
+    if (bi >= 0 && (bi & 63) == lane) pw[bi] = kMask;
+    __syncthreads();
+  }
+  if (lane == 0 && live) {
+    float wsum = 0.0f;  // src/runtime.c:224-230
+    for (int k = 0; k < K; k++) wsum += Wk[wave][k];
+    for (int k = 0; k < K; k++) wts[(size_t)t * K + k] = Wk[wave][k] / wsum;
+  }
+}
+
+hipError_t moe_route_launch(const qr_moe_layer* L, const float* xb, int T, int order,
+                            float* logits, float* probs, int32_t* idx, float* wts,
+                            hipStream_t st) {
+  const int E = L->n_experts;
+  hipError_t e = gemv_f32_launch(order, L->router, xb, logits, E, L->dim, T, L->dim, E, st);
+  if (e != hipSuccess) return e;
+  const int grid = (T + kRouteWaves - 1) / kRouteWaves;
+  hipLaunchKernelGGL(k_route_topk, dim3(grid), dim3(64 * kRouteWaves), 0, st, logits, T, E,
+                     L->n_used, probs, idx, wts);
+  return hipGetLastError();
+}
+
+// softmax_ref rows (the KernelOps.softmax drop-in): one wave per row.
+__global__ __launch_bounds__(256) void k_softmax(float* __restrict__ x, int rows, int n) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + wave;
+  if (r >= rows) return;  // no barriers below
+  float* p = x + (size_t)r * n;
+  float mx = p[0];
+  for (int e = lane; e < n; e += 64)
+    if (p[e] > mx) mx = p[e];
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v = __shfl_xor(mx, o);
+    if (v > mx) mx = v;
+  }
+  for (int e = lane; e < n; e += 64) p[e] = qr_expf(p[e] - mx);
+  // the sequential sum runs in lane 0 over values written by this wave; make
+  // them visible to it first
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  float inv = 0.0f;
+  if (lane == 0) {
+    float sum = 0.0f;
+    for (int e = 0; e < n; e++) sum += p[e];
+    inv = 1.0f / sum;
+  }
+  inv = __shfl(inv, 0);
+  for (int e = lane; e < n; e += 64) p[e] *= inv;
+}
+
+hipError_t softmax_launch(float* x, int rows, int n, hipStream_t st) {
+  hipLaunchKernelGGL(k_softmax, dim3((rows + 3) / 4), dim3(256), 0, st, x, rows, n);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Dispatch: one workgroup of 1024 threads, E <= 256.
+// ---------------------------------------------------------------------------
+constexpr int kDispThreads = 1024;
+constexpr int kDispWaves = kDispThreads / 64;
+
+__global__ __launch_bounds__(kDispThreads) void k_dispatch(const int32_t* __restrict__ idx, int P,
+                                                           int E, int tile,
+                                                           int32_t* __restrict__ counts,
+                                                           int32_t* __restrict__ offsets,
+                                                           int32_t* __restrict__ tiles,
+                                                           int32_t* __restrict__ perm,
+                                                           int32_t* __restrict__ inv) {
+  __shared__ int cnt[256];
+  __shared__ int off[257];
+  __shared__ int run[256];
+  __shared__ int wtab[kDispWaves][256];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  for (int e = tid; e < E; e += kDispThreads) {
+    cnt[e] = 0;
+    run[e] = 0;
+  }
+  __syncthreads();
+  for (int p = tid; p < P; p += kDispThreads) {
+    const int e = idx[p];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);  // a count: order-free
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0, tacc = 0;
+    for (int e = 0; e < E; e++) {
+      off[e] = acc;
+      counts[e] = cnt[e];
+      offsets[e] = acc;
+      if (tiles) tiles[e] = tacc;
+      acc += cnt[e];
+      tacc += (cnt[e] + tile - 1) / tile;
+    }
+    off[E] = acc;
+    offsets[E] = acc;
+    if (tiles) tiles[E] = tacc;
+  }
+  __syncthreads();
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int c0 = 0; c0 < P; c0 += kDispThreads) {
+    for (int i = tid; i < kDispWaves * 256; i += kDispThreads) (&wtab[0][0])[i] = 0;
+    __syncthreads();
+    const int p = c0 + tid;
+    int e = p < P ? idx[p] : -1;
+    if (e >= E) e = -1;
+    const bool valid = e >= 0;
+    // lanes of this wave holding the same expert: match the 8 expert bits
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+      const bool bit = valid && ((e >> b) & 1);
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const int rank = __popcll(peers & lt);
+    if (valid && rank == 0) wtab[wave][e] = __popcll(peers);
+    __syncthreads();
+    if (valid) {
+      int base = off[e] + run[e] + rank;
+      for (int w = 0; w < wave; w++) base += wtab[w][e];
+      perm[base] = p;
+      inv[p] = base;
+    } else if (p < P) {
+      inv[p] = -1;
+    }
+    __syncthreads();
+    for (int ee = tid; ee < E; ee += kDispThreads) {
+      int s = 0;
+      for (int w = 0; w < kDispWaves; w++) s += wtab[w][ee];
+      run[ee] += s;
+    }
+    __syncthreads();
+  }
+}
+
+hipError_t moe_dispatch_launch(const int32_t* idx, int T, int K, int E, int tile, int32_t* counts,
+                               int32_t* offsets, int32_t* tiles, int32_t* perm, int32_t* inv,
+                               hipStream_t st) {
+  if (E > 256) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(kDispThreads), 0, st, idx, T * K, E, tile, counts,
+                     offsets, tiles, perm, inv);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Grouped expert GEMV.
+// ---------------------------------------------------------------------------
+enum { kModeSingle = 0, kModeDispatched = 1, kModeDense = 2 };
+
+struct ExpertArgs {
+  const uint8_t* W1;   // [E][rows][rb]  (up in gate/up mode)
+  const uint8_t* W2;   // [E][rows][rb]  (gate in gate/up mode)
+  size_t slice;        // bytes per expert (0: one dense expert)
+  int rows, cols, rows_per_wg;
+  const float* X;      // activation rows
+  int xstride;
+  float* Y;            // output rows, one per pair position
+  int ystride;
+  int mode;
+  int x_by_token;      // dispatched mode: activation row = perm[p] / K (else p)
+  const int32_t* idx;
+  const int32_t* offsets;
+  const int32_t* perm;
+  const int32_t* tiles;
+  int E, K, P;
+};
+
+__host__ __device__ inline size_t expert_lds_layout(int type, int cols, int nt, int R, int nmat,
+                                                    size_t* o_bd, size_t* o_bs, size_t* o_terms,
+                                                    size_t* o_tile, size_t* o_rows,
+                                                    size_t* tile_stride) {
+  const int nxb = cols / 32;
+  const int U = qr_units(type, cols);
+  size_t off = align16((size_t)nt * nxb * 32);
+  *o_bd = off;
+  off = align16(off + (size_t)nt * nxb * 4);
+  *o_bs = off;
+  off = align16(off + (size_t)nt * nxb * 4);
+  *o_rows = off;
+  off = align16(off + (size_t)nt * 4);
+  *o_terms = off;
+  off = align16(off + (size_t)nmat * nt * R * (U + 1) * 4);
+  *o_tile = off;
+  *tile_stride = 0;
+  if (type == QR_T_Q8_0 || type == QR_T_Q6_K) {
+    *tile_stride = stage_bytes((size_t)R * qr_wrow_bytes(type, cols));
+    off += (size_t)nmat * *tile_stride;
+  }
+  return off;
+}
+
+// Resolve a work item to (expert, first pair, pair count).  Returns false if
+// the item is past the end of the work.
+__device__ inline bool expert_item(const ExpertArgs& a, int item, int NT, int* e, int* p0,
+                                   int* np) {
+  if (a.mode == kModeSingle) {
+    if (item >= a.K) return false;
+    *e = a.idx[item];
+    *p0 = item;
+    *np = 1;
+  } else if (a.mode == kModeDense) {
+    *p0 = item * NT;
+    if (*p0 >= a.P) return false;
+    *e = 0;
+    *np = min(NT, a.P - *p0);
+  } else {
+    const int ntiles = a.tiles[a.E];
+    if (item >= ntiles) return false;
+    int lo = 0, hi = a.E;  // largest e with tiles[e] <= item
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (a.tiles[mid] <= item) lo = mid;
+      else hi = mid;
+    }
+    *e = lo;
+    *p0 = a.offsets[lo] + (item - a.tiles[lo]) * NT;
+    *np = min(NT, a.offsets[lo + 1] - *p0);
+  }
+  return *e >= 0 && *e < a.E && *np > 0;
+}
+
+template <int TYPE, int NT, bool GATEUP>
+__global__ __launch_bounds__(256) void k_expert(ExpertArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  int e, p0, np;
+  if (!expert_item(a, blockIdx.y, NT, &e, &p0, &np)) return;  // uniform per workgroup
+  const int R0 = a.rows_per_wg;
+  const int r0 = blockIdx.x * R0;
+  const int R = min(R0, a.rows - r0);
+  if (R <= 0) return;
+  constexpr int NMAT = GATEUP ? 2 : 1;
+  const int cols = a.cols;
+  const int U = qr_units(TYPE, cols);
+  const size_t rb = qr_wrow_bytes(TYPE, cols);
+  size_t o_bd, o_bs, o_terms, o_tile, o_rows, tstr;
+  expert_lds_layout(TYPE, cols, NT, R0, NMAT, &o_bd, &o_bs, &o_terms, &o_tile, &o_rows, &tstr);
+  UnitSrc S;
+  S.act.q = reinterpret_cast<int8_t*>(smem);
+  S.act.bd = reinterpret_cast<float*>(smem + o_bd);
+  S.act.bs = reinterpret_cast<int32_t*>(smem + o_bs);
+  S.nxb = cols >> 5;
+  int* rowmap = reinterpret_cast<int*>(smem + o_rows);
+  float* terms = reinterpret_cast<float*>(smem + o_terms);
+  const int tstride = U + 1;
+
+  const uint8_t* Wm[2] = {a.W1 + (size_t)e * a.slice, GATEUP ? a.W2 + (size_t)e * a.slice : nullptr};
+  const size_t gstart = (size_t)r0 * rb;
+  const size_t mtotal = (size_t)a.rows * rb;
+  if constexpr (!Fmt<TYPE>::kDirect) {
+    for (int m = 0; m < NMAT; m++)
+      stage_tile(Wm[m], mtotal, gstart, gstart + (size_t)R * rb,
+                 reinterpret_cast<uint32_t*>(smem + o_tile + m * tstr));
+  }
+  if (threadIdx.x < NT) {
+    const int t = threadIdx.x;
+    int row = 0;
+    if (t < np) {
+      const int p = p0 + t;
+      row = (a.mode == kModeDispatched && a.x_by_token) ? a.perm[p] / a.K
+            : (a.mode == kModeSingle ? 0 : p);
+    }
+    rowmap[t] = row;
+  }
+  __syncthreads();
+  quantize_act_lds<Fmt<TYPE>::kPerm>(a.X, (size_t)a.xstride, rowmap, np, NT, cols, S.act);
+  __syncthreads();
+
+  const int lds_base = (int)(gstart & 15);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nwaves = blockDim.x >> 6;
+  const int per_mat = R * U;
+  for (int fu = wave * 64 + lane; fu < NMAT * per_mat; fu += nwaves * 64) {
+    const int m = fu / per_mat;
+    const int rem = fu - m * per_mat;
+    const int row = rem / U;
+    const int u = rem - row * U;
+    UnitSrc Sm = S;
+    Sm.tile = reinterpret_cast<const uint32_t*>(smem + o_tile + m * tstr);
+    float tv[NT];
+    int32_t is[NT];
+    unit_terms<TYPE, NT>(Wm[m] + gstart + (size_t)row * rb, lds_base + row * (int)rb, u, Sm, 0,
+                         tv, is);
+#pragma unroll
+    for (int t = 0; t < NT; t++) terms[(((size_t)m * NT + t) * R0 + row) * tstride + u] = tv[t];
+  }
+  __syncthreads();
+
+  for (int i = threadIdx.x; i < np * R; i += blockDim.x) {
+    const int t = i / R, row = i - t * R;
+    const float v1 = row_sum(terms + ((size_t)t * R0 + row) * tstride, U);
+    float out = v1;
+    if constexpr (GATEUP) {
+      const float v2 = row_sum(terms + (((size_t)NT + t) * R0 + row) * tstride, U);
+      out = qr_silu(v1) * v2;
+    }
+    a.Y[(size_t)(p0 + t) * a.ystride + r0 + row] = out;
+  }
+}
+
+static int expert_rows_per_wg(int type, int rows, int cols, int nt, int nmat) {
+  const int U = qr_units(type, cols);
+  int R = 64;
+  size_t a, b, c, d, e, f;
+  while (R > 1 && ((size_t)nmat * R * U > 16 * 256 ||
+                   expert_lds_layout(type, cols, nt, R, nmat, &a, &b, &c, &d, &e, &f) > 48 * 1024 ||
+                   (rows + R - 1) / R < 64))
+    R >>= 1;
+  return R;
+}
+
+template <int TYPE, int NT, bool GATEUP>
+static hipError_t expert_launch_t(ExpertArgs a, int items, hipStream_t st) {
+  constexpr int NMAT = GATEUP ? 2 : 1;
+  a.rows_per_wg = expert_rows_per_wg(TYPE, a.rows, a.cols, NT, NMAT);
+  size_t o1, o2, o3, o4, o5, o6;
+  const size_t lds =
+      expert_lds_layout(TYPE, a.cols, NT, a.rows_per_wg, NMAT, &o1, &o2, &o3, &o4, &o5, &o6);
+  const int U = qr_units(TYPE, a.cols);
+  int threads = ((NMAT * a.rows_per_wg * U + 63) / 64) * 64;
+  threads = threads < 64 ? 64 : (threads > 256 ? 256 : threads);
+  dim3 grid((a.rows + a.rows_per_wg - 1) / a.rows_per_wg, items);
+  if (grid.x == 0 || grid.y == 0) return hipSuccess;
+  if (lds > 64 * 1024) return hipErrorInvalidValue;  // dynamic LDS without an opt-in
+  hipLaunchKernelGGL((k_expert<TYPE, NT, GATEUP>), grid, dim3(threads), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int TYPE, bool GATEUP>
+static hipError_t expert_launch_nt(const ExpertArgs& a, int nt, int items, hipStream_t st) {
+  switch (nt) {
+    case 1: return expert_launch_t<TYPE, 1, GATEUP>(a, items, st);
+    case 2: return expert_launch_t<TYPE, 2, GATEUP>(a, items, st);
+    case 4: return expert_launch_t<TYPE, 4, GATEUP>(a, items, st);
+    case 8: return expert_launch_t<TYPE, 8, GATEUP>(a, items, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+static hipError_t expert_launch(int type, bool gateup, const ExpertArgs& a, int nt, int items,
+                                hipStream_t st) {
+  switch (type) {
+    case QR_T_Q4_K:
+      return gateup ? expert_launch_nt<QR_T_Q4_K, true>(a, nt, items, st)
+                    : expert_launch_nt<QR_T_Q4_K, false>(a, nt, items, st);
+    case QR_T_Q5_K:
+      return gateup ? expert_launch_nt<QR_T_Q5_K, true>(a, nt, items, st)
+                    : expert_launch_nt<QR_T_Q5_K, false>(a, nt, items, st);
+    case QR_T_Q6_K:
+      return gateup ? expert_launch_nt<QR_T_Q6_K, true>(a, nt, items, st)
+                    : expert_launch_nt<QR_T_Q6_K, false>(a, nt, items, st);
+    case QR_T_Q8_0:
+      return gateup ? expert_launch_nt<QR_T_Q8_0, true>(a, nt, items, st)
+                    : expert_launch_nt<QR_T_Q8_0, false>(a, nt, items, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// T == 1: the K down projections of one token plus the slot-order combine.
+// A workgroup owns R rows of every selected expert's down matrix.
+// ---------------------------------------------------------------------------
+struct DownArgs {
+  const uint8_t* W;    // [E][dim][rb]
+  size_t slice;
+  int dim, hidden, rows_per_wg, K, E;
+  const float* hb;     // [K][hidden]
+  const int32_t* idx;  // [K]
+  const float* wts;    // [K]
+  float* x;            // [dim], updated in place
+  const float* ysh;    // optional shared-expert output [dim]
+  const float* sgl;    // its gate logit (scalar)
+};
+
+__host__ __device__ inline size_t down1_lds_layout(int type, int hidden, int K, int R, size_t* o_bd,
+                                                   size_t* o_bs, size_t* o_terms, size_t* o_tile,
+                                                   size_t* tile_stride) {
+  const int nxb = hidden / 32;
+  const int U = qr_units(type, hidden);
+  size_t off = align16((size_t)K * nxb * 32);
+  *o_bd = off;
+  off = align16(off + (size_t)K * nxb * 4);
+  *o_bs = off;
+  off = align16(off + (size_t)K * nxb * 4);
+  *o_terms = off;
+  off = align16(off + (size_t)K * R * (U + 1) * 4);
+  *o_tile = off;
+  *tile_stride = 0;
+  if (type == QR_T_Q8_0 || type == QR_T_Q6_K) {
+    *tile_stride = stage_bytes((size_t)R * qr_wrow_bytes(type, hidden));
+    off += (size_t)K * *tile_stride;
+  }
+  return off;
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_down_combine1(DownArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int R0 = a.rows_per_wg;
+  const int r0 = blockIdx.x * R0;
+  const int R = min(R0, a.dim - r0);
+  if (R <= 0) return;
+  const int K = a.K;
+  const int U = qr_units(TYPE, a.hidden);
+  const size_t rb = qr_wrow_bytes(TYPE, a.hidden);
+  size_t o_bd, o_bs, o_terms, o_tile, tstr;
+  down1_lds_layout(TYPE, a.hidden, K, R0, &o_bd, &o_bs, &o_terms, &o_tile, &tstr);
+  UnitSrc S;
+  S.act.q = reinterpret_cast<int8_t*>(smem);
+  S.act.bd = reinterpret_cast<float*>(smem + o_bd);
+  S.act.bs = reinterpret_cast<int32_t*>(smem + o_bs);
+  S.nxb = a.hidden >> 5;
+  float* terms = reinterpret_cast<float*>(smem + o_terms);
+  const int tstride = U + 1;
+  const size_t gstart = (size_t)r0 * rb;
+  const size_t mtotal = (size_t)a.dim * rb;
+  // A slot whose index is out of range (only NaN router inputs produce one)
+  // contributes nothing and its weights are never touched.
+  auto valid = [&](int k) { return a.idx[k] >= 0 && a.idx[k] < a.E; };
+  if constexpr (!Fmt<TYPE>::kDirect) {
+    for (int k = 0; k < K; k++) {
+      if (!valid(k)) continue;
+      const uint8_t* Wk = a.W + (size_t)a.idx[k] * a.slice;
+      stage_tile(Wk, mtotal, gstart, gstart + (size_t)R * rb,
+                 reinterpret_cast<uint32_t*>(smem + o_tile + k * tstr));
+    }
+  }
+  quantize_act_lds<Fmt<TYPE>::kPerm>(a.hb, (size_t)a.hidden, nullptr, K, K, a.hidden, S.act);
+  __syncthreads();
+
+  const int lds_base = (int)(gstart & 15);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nwaves = blockDim.x >> 6;
+  const int per_k = R * U;
+  for (int fu = wave * 64 + lane; fu < K * per_k; fu += nwaves * 64) {
+    const int k = fu / per_k;
+    const int rem = fu - k * per_k;
+    const int row = rem / U;
+    const int u = rem - row * U;
+    float tv[1] = {0.0f};
+    int32_t is[1];
+    if (valid(k)) {
+      UnitSrc Sk = S;
+      Sk.tile = reinterpret_cast<const uint32_t*>(smem + o_tile + k * tstr);
+      const uint8_t* Wk = a.W + (size_t)a.idx[k] * a.slice;
+      unit_terms<TYPE, 1>(Wk + gstart + (size_t)row * rb, lds_base + row * (int)rb, u, Sk, k, tv,
+                          is);
+    }
+    terms[((size_t)k * R0 + row) * tstride + u] = tv[0];
+  }
+  __syncthreads();
+
+  for (int row = threadIdx.x; row < R; row += blockDim.x) {
+    float acc = 0.0f;  // xb2 = 0 (src/runtime.c:242)
+    for (int k = 0; k < K; k++) {
+      if (!valid(k)) continue;
+      const float y = row_sum(terms + ((size_t)k * R0 + row) * tstride, U);
+      acc += y * a.wts[k];
+    }
+    if (a.ysh) {
+      const float sg = 1.0f / (1.0f + qr_expf(-a.sgl[0]));
+      acc += sg * a.ysh[r0 + row];
+    }
+    a.x[r0 + row] += acc;
+  }
+}
+
+static int down1_rows_per_wg(int type, int dim, int hidden, int K) {
+  const int U = qr_units(type, hidden);
+  int R = 64;
+  size_t a, b, c, d, e;
+  while (R > 1 && ((size_t)K * R * U > 16 * 256 ||
+                   down1_lds_layout(type, hidden, K, R, &a, &b, &c, &d, &e) > 48 * 1024 ||
+                   (dim + R - 1) / R < 256))
+    R >>= 1;
+  return R;
+}
+
+template <int TYPE>
+static hipError_t down1_launch_t(DownArgs a, hipStream_t st) {
+  a.rows_per_wg = down1_rows_per_wg(TYPE, a.dim, a.hidden, a.K);
+  size_t o1, o2, o3, o4, o5;
+  const size_t lds = down1_lds_layout(TYPE, a.hidden, a.K, a.rows_per_wg, &o1, &o2, &o3, &o4, &o5);
+  const int U = qr_units(TYPE, a.hidden);
+  int threads = ((a.K * a.rows_per_wg * U + 63) / 64) * 64;
+  threads = threads < 64 ? 64 : (threads > 256 ? 256 : threads);
+  const int grid = (a.dim + a.rows_per_wg - 1) / a.rows_per_wg;
+  if (lds > 64 * 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_down_combine1<TYPE>, dim3(grid), dim3(threads), lds, st, a);
+  return hipGetLastError();
+}
+
+static hipError_t down1_launch(int type, const DownArgs& a, hipStream_t st) {
+  switch (type) {
+    case QR_T_Q4_K: return down1_launch_t<QR_T_Q4_K>(a, st);
+    case QR_T_Q5_K: return down1_launch_t<QR_T_Q5_K>(a, st);
+    case QR_T_Q6_K: return down1_launch_t<QR_T_Q6_K>(a, st);
+    case QR_T_Q8_0: return down1_launch_t<QR_T_Q8_0>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// T > 1 combine: x[t][i] += ((0 + y_0 w_0) + y_1 w_1 + ...) (+ shared), the
+// expert outputs gathered from their dispatch positions in slot order.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_combine(float* __restrict__ x, const float* __restrict__ y,
+                                                 const int32_t* __restrict__ inv,
+                                                 const float* __restrict__ wts, int T, int K,
+                                                 int dim, const float* __restrict__ ysh,
+                                                 const float* __restrict__ sgl) {
+  const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (long)T * dim) return;
+  const int t = (int)(gid / dim), i = (int)(gid - (long)t * dim);
+  float acc = 0.0f;
+  for (int k = 0; k < K; k++) {
+    const int pos = inv[t * K + k];
+    if (pos >= 0) acc += y[(size_t)pos * dim + i] * wts[t * K + k];
+  }
+  if (ysh) {
+    const float sg = 1.0f / (1.0f + qr_expf(-sgl[t]));
+    acc += sg * ysh[(size_t)t * dim + i];
+  }
+  x[(size_t)t * dim + i] += acc;
+}
+
+// ---------------------------------------------------------------------------
+// The layer.
+// ---------------------------------------------------------------------------
+static int pick_tile(int P, int E) {
+  const double avg = (double)P / E;
+  return avg >= 6 ? 8 : avg >= 3 ? 4 : avg >= 1.5 ? 2 : 1;
+}
+
+static hipError_t shared_expert(const qr_moe_layer* L, const float* xb, int T, const MoeScratch& s,
+                                hipStream_t st) {
+  const int nt = T >= 8 ? 8 : T >= 4 ? 4 : T >= 2 ? 2 : 1;
+  ExpertArgs g{};
+  g.W1 = static_cast<const uint8_t*>(L->sh_up);
+  g.W2 = static_cast<const uint8_t*>(L->sh_gate);
+  g.slice = 0;
+  g.rows = L->sh_hidden;
+  g.cols = L->dim;
+  g.X = xb;
+  g.xstride = L->dim;
+  g.Y = s.hbs;
+  g.ystride = L->sh_hidden;
+  g.mode = kModeDense;
+  g.E = 1;
+  g.K = 1;
+  g.P = T;
+  hipError_t e = expert_launch((int)L->sh_up_type, true, g, nt, (T + nt - 1) / nt, st);
+  if (e != hipSuccess) return e;
+  ExpertArgs dn = g;
+  dn.W1 = static_cast<const uint8_t*>(L->sh_down);
+  dn.W2 = nullptr;
+  dn.rows = L->dim;
+  dn.cols = L->sh_hidden;
+  dn.X = s.hbs;
+  dn.xstride = L->sh_hidden;
+  dn.Y = s.ysh;
+  dn.ystride = L->dim;
+  e = expert_launch((int)L->sh_down_type, false, dn, nt, (T + nt - 1) / nt, st);
+  if (e != hipSuccess) return e;
+  // gate logit: sequential dot (one row) for every token
+  return gemv_f32_launch(QR_ORDER_SEQ, L->sh_gate_inp, xb, s.sgl, 1, L->dim, T, L->dim, 1, st);
+}
+
+hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, int T, int order,
+                              const MoeScratch& s, hipStream_t st) {
+  const int E = L->n_experts, K = L->n_used, P = T * K;
+  hipError_t e = moe_route_launch(L, xb, T, order, s.logits, nullptr, s.idx, s.wts, st);
+  if (e != hipSuccess) return e;
+  const bool sh = L->sh_hidden > 0;
+  const size_t su = qr_wrow_bytes((int)L->up_type, L->dim) * (size_t)L->hidden;
+  const size_t sd = qr_wrow_bytes((int)L->down_type, L->hidden) * (size_t)L->dim;
+
+  ExpertArgs g{};
+  g.W1 = static_cast<const uint8_t*>(L->up);
+  g.W2 = static_cast<const uint8_t*>(L->gate);
+  g.slice = su;
+  g.rows = L->hidden;
+  g.cols = L->dim;
+  g.X = xb;
+  g.xstride = L->dim;
+  g.Y = s.hb;
+  g.ystride = L->hidden;
+  g.idx = s.idx;
+  g.offsets = s.offsets;
+  g.perm = s.perm;
+  g.tiles = s.tiles;
+  g.E = E;
+  g.K = K;
+  g.P = P;
+
+  if (T == 1) {
+    g.mode = kModeSingle;
+    e = expert_launch((int)L->up_type, true, g, 1, K, st);
+    if (e != hipSuccess) return e;
+    if (sh) {
+      e = shared_expert(L, xb, T, s, st);
+      if (e != hipSuccess) return e;
+    }
+    DownArgs dn{};
+    dn.W = static_cast<const uint8_t*>(L->down);
+    dn.slice = sd;
+    dn.dim = L->dim;
+    dn.hidden = L->hidden;
+    dn.K = K;
+    dn.E = E;
+    dn.hb = s.hb;
+    dn.idx = s.idx;
+    dn.wts = s.wts;
+    dn.x = x;
+    dn.ysh = sh ? s.ysh : nullptr;
+    dn.sgl = s.sgl;
+    return down1_launch((int)L->down_type, dn, st);
+  }
+
+  const int nt = pick_tile(P, E);
+  e = moe_dispatch_launch(s.idx, T, K, E, nt, s.counts, s.offsets, s.tiles, s.perm, s.inv, st);
+  if (e != hipSuccess) return e;
+  const int items = (P + nt - 1) / nt + E;  // >= sum_e ceil(count_e / nt)
+  g.mode = kModeDispatched;
+  g.x_by_token = 1;
+  e = expert_launch((int)L->up_type, true, g, nt, items, st);
+  if (e != hipSuccess) return e;
+  ExpertArgs dn = g;
+  dn.W1 = static_cast<const uint8_t*>(L->down);
+  dn.W2 = nullptr;
+  dn.slice = sd;
+  dn.rows = L->dim;
+  dn.cols = L->hidden;
+  dn.X = s.hb;
+  dn.xstride = L->hidden;
+  dn.Y = s.y;
+  dn.ystride = L->dim;
+  dn.x_by_token = 0;
+  e = expert_launch((int)L->down_type, false, dn, nt, items, st);
+  if (e != hipSuccess) return e;
+  if (sh) {
+    e = shared_expert(L, xb, T, s, st);
+    if (e != hipSuccess) return e;
+  }
+  const long n = (long)T * L->dim;
+  hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, s.y, s.inv,
+                     s.wts, T, K, L->dim, sh ? s.ysh : nullptr, s.sgl);
+  return hipGetLastError();
+}
+
+}  // namespace qr

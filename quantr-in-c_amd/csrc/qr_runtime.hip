@@ -1,0 +1,543 @@
+// qr_runtime.hip -- context, memory, weight registry, timing and the C-ABI
+// entry points of libqr_hip.so.  Argument checking happens here, on the host,
+// before any kernel is launched: every launch below has had its sizes,
+// alignments and types validated against what the kernel assumes.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
+
+#include "qr_common.h"
+#include "qr_internal.h"
+
+struct RegEntry {
+  void* dev;
+  size_t bytes;
+};
+
+struct qr_ctx {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  std::mutex mu;
+  std::unordered_map<const void*, RegEntry> registry;
+  void* moe_scratch = nullptr;
+  size_t moe_scratch_bytes = 0;
+};
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(QR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define QR_HIP(call, what)                     \
+  do {                                         \
+    hipError_t e_ = (call);                    \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+bool known_type(uint32_t t) {
+  return t == QR_T_F32 || t == QR_T_Q8_0 || t == QR_T_Q4_K || t == QR_T_Q5_K || t == QR_T_Q6_K;
+}
+
+int set_device(qr_ctx* c) {
+  QR_HIP(hipSetDevice(c->device), "hipSetDevice");
+  return QR_OK;
+}
+
+// ---- small kernels ---------------------------------------------------------
+__global__ void k_copy16(uint4* __restrict__ dst, const uint4* __restrict__ src, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
+       i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
+__global__ void k_test_expf(const float* __restrict__ x, float* __restrict__ y, long n) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = qr_expf(x[i]);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qr_last_error(void) { return g_err; }
+
+const char* qr_version(void) { return "qr_hip 0.1 gfx950"; }
+
+int qr_device_count(int* count) {
+  if (!count) return fail(QR_ERR_INVALID, "qr_device_count: null count");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) {
+    *count = 0;
+    return hip_fail(e, "hipGetDeviceCount");
+  }
+  *count = n;
+  return QR_OK;
+}
+
+int qr_ctx_create(int device, qr_ctx** out) {
+  if (!out) return fail(QR_ERR_INVALID, "qr_ctx_create: null out");
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+    return fail(QR_ERR_NODEV, "qr_ctx_create: no HIP device");
+  if (device < 0 || device >= n)
+    return fail(QR_ERR_INVALID, "qr_ctx_create: device %d of %d", device, n);
+  hipDeviceProp_t prop;
+  QR_HIP(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(QR_ERR_NODEV, "qr_ctx_create: device %d is %s, this library is built for gfx950",
+                device, prop.gcnArchName);
+  qr_ctx* c = new qr_ctx();
+  c->device = device;
+  if (set_device(c) != QR_OK) {
+    delete c;
+    return QR_ERR_HIP;
+  }
+  hipError_t e = hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreate(&c->ev0);
+  if (e == hipSuccess) e = hipEventCreate(&c->ev1);
+  if (e != hipSuccess) {
+    delete c;
+    return hip_fail(e, "qr_ctx_create");
+  }
+  c->stream = c->own;
+  *out = c;
+  return QR_OK;
+}
+
+int qr_ctx_destroy(qr_ctx* c) {
+  if (!c) return QR_OK;
+  set_device(c);
+  (void)hipStreamSynchronize(c->stream);
+  for (auto& kv : c->registry) (void)hipFree(kv.second.dev);
+  if (c->moe_scratch) (void)hipFree(c->moe_scratch);
+  if (c->ev0) (void)hipEventDestroy(c->ev0);
+  if (c->ev1) (void)hipEventDestroy(c->ev1);
+  if (c->own) (void)hipStreamDestroy(c->own);
+  delete c;
+  return QR_OK;
+}
+
+int qr_ctx_set_stream(qr_ctx* c, void* s) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_ctx_set_stream: null ctx");
+  c->stream = s ? static_cast<hipStream_t>(s) : c->own;
+  return QR_OK;
+}
+
+void* qr_ctx_get_stream(qr_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+int qr_sync(qr_ctx* c) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_sync: null ctx");
+  QR_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return QR_OK;
+}
+
+int qr_malloc(qr_ctx* c, size_t bytes, void** p) {
+  if (!c || !p) return fail(QR_ERR_INVALID, "qr_malloc: null argument");
+  *p = nullptr;
+  if (set_device(c) != QR_OK) return QR_ERR_HIP;
+  hipError_t e = hipMalloc(p, bytes ? bytes : 16);
+  if (e != hipSuccess) return fail(QR_ERR_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  return QR_OK;
+}
+
+int qr_free(qr_ctx* c, void* p) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_free: null ctx");
+  if (!p) return QR_OK;
+  QR_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  QR_HIP(hipFree(p), "hipFree");
+  return QR_OK;
+}
+
+int qr_memcpy_h2d(qr_ctx* c, void* dst, const void* src, size_t n) {
+  if (!c || (n && (!dst || !src))) return fail(QR_ERR_INVALID, "qr_memcpy_h2d: null argument");
+  if (!n) return QR_OK;
+  QR_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D");
+  QR_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return QR_OK;
+}
+
+int qr_memcpy_d2h(qr_ctx* c, void* dst, const void* src, size_t n) {
+  if (!c || (n && (!dst || !src))) return fail(QR_ERR_INVALID, "qr_memcpy_d2h: null argument");
+  if (!n) return QR_OK;
+  QR_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H");
+  QR_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return QR_OK;
+}
+
+int qr_memcpy_d2d(qr_ctx* c, void* dst, const void* src, size_t n) {
+  if (!c || (n && (!dst || !src))) return fail(QR_ERR_INVALID, "qr_memcpy_d2d: null argument");
+  if (!n) return QR_OK;
+  QR_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, c->stream), "hipMemcpyAsync D2D");
+  return QR_OK;
+}
+
+int qr_memset(qr_ctx* c, void* dst, int v, size_t n) {
+  if (!c || (n && !dst)) return fail(QR_ERR_INVALID, "qr_memset: null argument");
+  if (!n) return QR_OK;
+  QR_HIP(hipMemsetAsync(dst, v, n, c->stream), "hipMemsetAsync");
+  return QR_OK;
+}
+
+int qr_timer_start(qr_ctx* c) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_timer_start: null ctx");
+  QR_HIP(hipEventRecord(c->ev0, c->stream), "hipEventRecord");
+  return QR_OK;
+}
+
+int qr_timer_stop(qr_ctx* c, float* ms) {
+  if (!c || !ms) return fail(QR_ERR_INVALID, "qr_timer_stop: null argument");
+  QR_HIP(hipEventRecord(c->ev1, c->stream), "hipEventRecord");
+  QR_HIP(hipEventSynchronize(c->ev1), "hipEventSynchronize");
+  QR_HIP(hipEventElapsedTime(ms, c->ev0, c->ev1), "hipEventElapsedTime");
+  return QR_OK;
+}
+
+int qr_capture_begin(qr_ctx* c) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_capture_begin: null ctx");
+  QR_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  return QR_OK;
+}
+
+int qr_capture_end(qr_ctx* c, void** graph) {
+  if (!c || !graph) return fail(QR_ERR_INVALID, "qr_capture_end: null argument");
+  *graph = nullptr;
+  hipGraph_t g = nullptr;
+  QR_HIP(hipStreamEndCapture(c->stream, &g), "hipStreamEndCapture");
+  hipGraphExec_t ex = nullptr;
+  hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+  *graph = ex;
+  return QR_OK;
+}
+
+int qr_graph_launch(qr_ctx* c, void* graph) {
+  if (!c || !graph) return fail(QR_ERR_INVALID, "qr_graph_launch: null argument");
+  QR_HIP(hipGraphLaunch(static_cast<hipGraphExec_t>(graph), c->stream), "hipGraphLaunch");
+  return QR_OK;
+}
+
+int qr_graph_destroy(void* graph) {
+  if (!graph) return QR_OK;
+  QR_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph)), "hipGraphExecDestroy");
+  return QR_OK;
+}
+
+int qr_copy_kernel(qr_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c || !dst || !src) return fail(QR_ERR_INVALID, "qr_copy_kernel: null argument");
+  if (!aligned(dst, 16) || !aligned(src, 16) || (bytes & 15))
+    return fail(QR_ERR_INVALID, "qr_copy_kernel: needs 16-byte aligned pointers and size");
+  const size_t n16 = bytes / 16;
+  if (!n16) return QR_OK;
+  size_t grid = (n16 + 255) / 256;
+  if (grid > 8192) grid = 8192;
+  hipLaunchKernelGGL(k_copy16, dim3((unsigned)grid), dim3(256), 0, c->stream,
+                     static_cast<uint4*>(dst), static_cast<const uint4*>(src), n16);
+  QR_HIP(hipGetLastError(), "k_copy16");
+  return QR_OK;
+}
+
+size_t qr_row_bytes(uint32_t type, int d) {
+  if (d < 0 || !known_type(type)) return 0;
+  return qr_wrow_bytes((int)type, d);
+}
+
+int qr_quantize_q8_0(qr_ctx* c, const float* x, void* y, long n) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_quantize_q8_0: null ctx");
+  if (n < 0) return fail(QR_ERR_INVALID, "qr_quantize_q8_0: negative size");
+  const long nb = n / 32;
+  if (nb == 0) return QR_OK;
+  if (!x || !y) return fail(QR_ERR_INVALID, "qr_quantize_q8_0: null pointer");
+  QR_HIP(qr::quantize_q8_0_launch(x, y, nb, c->stream), "k_quantize_q8_0");
+  return QR_OK;
+}
+
+int qr_gemv_ex(qr_ctx* c, uint32_t type, const void* w, const float* x, int xstride, float* y,
+               int ystride, int n, int d, int nt, int32_t* acc, int32_t* accb) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_gemv: null ctx");
+  if (!known_type(type)) return fail(QR_ERR_INVALID, "qr_gemv: unknown type %u", type);
+  if (n < 0 || d < 0) return fail(QR_ERR_INVALID, "qr_gemv: negative size");
+  if (!(nt == 1 || nt == 2 || nt == 3 || nt == 4 || nt == 8))
+    return fail(QR_ERR_UNSUPPORTED, "qr_gemv: nt=%d (supported 1,2,3,4,8)", nt);
+  if (n == 0) return QR_OK;
+  if (!x || !y) return fail(QR_ERR_INVALID, "qr_gemv: null x or y");
+  if (xstride < d || ystride < n) return fail(QR_ERR_INVALID, "qr_gemv: stride below size");
+  if (!w) {  // src/quant.c:443-446: no weights -> zero output
+    for (int t = 0; t < nt; t++)
+      QR_HIP(hipMemsetAsync(y + (size_t)t * ystride, 0, (size_t)n * 4, c->stream), "hipMemsetAsync");
+    return QR_OK;
+  }
+  if (type == QR_T_F32) {
+    if (acc || accb) return fail(QR_ERR_INVALID, "qr_gemv: F32 has no integer sums");
+    QR_HIP(qr::gemv_f32_launch(QR_ORDER_SEQ, static_cast<const float*>(w), x, y, n, d, nt,
+                               xstride, ystride, c->stream), "k_gemv_f32");
+    return QR_OK;
+  }
+  if (!aligned(w, 16)) return fail(QR_ERR_INVALID, "qr_gemv: weights must be 16-byte aligned");
+  if (!aligned(x, 16) || (nt > 1 && (xstride & 3)))
+    return fail(QR_ERR_INVALID, "qr_gemv: x must be 16-byte aligned (and xstride a multiple of 4)");
+  const int R = qr::gemv_rows_per_wg((int)type, n, d, nt);
+  if (qr::gemv_lds_bytes((int)type, d, nt, R) > 64 * 1024)
+    return fail(QR_ERR_UNSUPPORTED, "qr_gemv: d=%d nt=%d exceeds the LDS budget", d, nt);
+  QR_HIP(qr::gemv_launch((int)type, w, x, y, n, d, nt, xstride, ystride, acc, accb, c->stream),
+         "k_gemv");
+  return QR_OK;
+}
+
+int qr_gemv(qr_ctx* c, uint32_t type, const void* w, const float* x, float* y, int n, int d,
+            int nt) {
+  return qr_gemv_ex(c, type, w, x, d, y, n, n, d, nt, nullptr, nullptr);
+}
+
+int qr_matmul_f32(qr_ctx* c, int order, const float* w, const float* x, float* y, int n, int d,
+                  int nt) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_matmul_f32: null ctx");
+  if (order < QR_ORDER_SEQ || order > QR_ORDER_AVX512)
+    return fail(QR_ERR_INVALID, "qr_matmul_f32: order %d", order);
+  if (n < 0 || d < 0 || nt < 1) return fail(QR_ERR_INVALID, "qr_matmul_f32: bad size");
+  if (n == 0) return QR_OK;
+  if (!w || !x || !y) return fail(QR_ERR_INVALID, "qr_matmul_f32: null pointer");
+  QR_HIP(qr::gemv_f32_launch(order, w, x, y, n, d, nt, d, n, c->stream), "k_gemv_f32");
+  return QR_OK;
+}
+
+int qr_softmax(qr_ctx* c, float* x, int rows, int n) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_softmax: null ctx");
+  if (rows < 0 || n < 0) return fail(QR_ERR_INVALID, "qr_softmax: bad size");
+  if (rows == 0 || n == 0) return QR_OK;
+  if (!x) return fail(QR_ERR_INVALID, "qr_softmax: null pointer");
+  QR_HIP(qr::softmax_launch(x, rows, n, c->stream), "k_softmax");
+  return QR_OK;
+}
+
+int qr_test_expf(qr_ctx* c, const float* x, float* y, long n) {
+  if (!c || (n > 0 && (!x || !y))) return fail(QR_ERR_INVALID, "qr_test_expf: null argument");
+  if (n <= 0) return QR_OK;
+  const long grid = (n + 255) / 256;
+  hipLaunchKernelGGL(k_test_expf, dim3((unsigned)grid), dim3(256), 0, c->stream, x, y, n);
+  QR_HIP(hipGetLastError(), "k_test_expf");
+  return QR_OK;
+}
+
+// ---- MoE --------------------------------------------------------------------
+static int check_layer(const qr_moe_layer* L, const char* who) {
+  if (!L) return fail(QR_ERR_INVALID, "%s: null layer", who);
+  if (L->dim <= 0 || L->n_experts <= 0 || L->n_used <= 0 || L->hidden <= 0)
+    return fail(QR_ERR_INVALID, "%s: bad layer sizes", who);
+  // src/runtime.c:204 and 208 hold the logits and the choice on the stack.
+  if (L->n_experts > 256 || L->n_used > 16 || L->n_used > L->n_experts)
+    return fail(QR_ERR_INVALID, "%s: E=%d K=%d (E <= 256, K <= 16, K <= E)", who, L->n_experts,
+                L->n_used);
+  if (!L->router) return fail(QR_ERR_INVALID, "%s: null router", who);
+  if (L->dim % 32) return fail(QR_ERR_INVALID, "%s: dim must be a multiple of 32", who);
+  return QR_OK;
+}
+
+static int check_experts(const qr_moe_layer* L, const char* who) {
+  const uint32_t ts[3] = {L->up_type, L->gate_type, L->down_type};
+  const void* ps[3] = {L->up, L->gate, L->down};
+  for (int i = 0; i < 3; i++) {
+    if (ts[i] == QR_T_F32 || !known_type(ts[i]))
+      return fail(QR_ERR_UNSUPPORTED, "%s: expert type %u (quantized types only)", who, ts[i]);
+    if (!ps[i]) return fail(QR_ERR_INVALID, "%s: null expert tensor", who);
+    if (!aligned(ps[i], 16)) return fail(QR_ERR_INVALID, "%s: expert tensors must be 16-byte aligned", who);
+  }
+  if (L->up_type != L->gate_type)
+    return fail(QR_ERR_UNSUPPORTED, "%s: up and gate must share a type", who);
+  if (L->hidden % 32) return fail(QR_ERR_INVALID, "%s: hidden must be a multiple of 32", who);
+  // expert slices must stay 16-byte aligned
+  const size_t su = qr_row_bytes(L->up_type, L->dim) * (size_t)L->hidden;
+  const size_t sd = qr_row_bytes(L->down_type, L->hidden) * (size_t)L->dim;
+  if ((su & 15) || (sd & 15)) return fail(QR_ERR_UNSUPPORTED, "%s: expert slice not 16-byte aligned", who);
+  if (L->sh_hidden > 0) {
+    if (!L->sh_gate_inp || !L->sh_up || !L->sh_gate || !L->sh_down)
+      return fail(QR_ERR_INVALID, "%s: null shared-expert tensor", who);
+    if (L->sh_up_type != L->sh_gate_type || L->sh_up_type == QR_T_F32 ||
+        L->sh_down_type == QR_T_F32 || !known_type(L->sh_up_type) || !known_type(L->sh_down_type))
+      return fail(QR_ERR_UNSUPPORTED, "%s: shared expert types", who);
+    if (L->sh_hidden % 32) return fail(QR_ERR_INVALID, "%s: sh_hidden must be a multiple of 32", who);
+    if (!aligned(L->sh_up, 16) || !aligned(L->sh_gate, 16) || !aligned(L->sh_down, 16))
+      return fail(QR_ERR_INVALID, "%s: shared tensors must be 16-byte aligned", who);
+  }
+  return QR_OK;
+}
+
+int qr_moe_route(qr_ctx* c, const qr_moe_layer* L, const float* xb, int T, int order,
+                 float* probs, int32_t* idx, float* wts) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_moe_route: null ctx");
+  int rc = check_layer(L, "qr_moe_route");
+  if (rc) return rc;
+  if (order < QR_ORDER_SEQ || order > QR_ORDER_AVX512)
+    return fail(QR_ERR_INVALID, "qr_moe_route: order %d", order);
+  if (T < 0) return fail(QR_ERR_INVALID, "qr_moe_route: T < 0");
+  if (T == 0) return QR_OK;
+  if (!xb || !idx || !wts) return fail(QR_ERR_INVALID, "qr_moe_route: null pointer");
+  float* logits = nullptr;
+  QR_HIP(hipMallocAsync((void**)&logits, (size_t)T * L->n_experts * 4, c->stream), "hipMallocAsync");
+  hipError_t e = qr::moe_route_launch(L, xb, T, order, logits, probs, idx, wts, c->stream);
+  (void)hipFreeAsync(logits, c->stream);
+  QR_HIP(e, "moe_route");
+  return QR_OK;
+}
+
+int qr_moe_dispatch(qr_ctx* c, const int32_t* idx, int T, int K, int E, int32_t* counts,
+                    int32_t* offsets, int32_t* perm, int32_t* inv) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_moe_dispatch: null ctx");
+  if (T < 0 || K <= 0 || E <= 0 || E > 256 || K > 16)
+    return fail(QR_ERR_INVALID, "qr_moe_dispatch: T=%d K=%d E=%d (E <= 256, K <= 16)", T, K, E);
+  if (!counts || !offsets || (T > 0 && (!idx || !perm || !inv)))
+    return fail(QR_ERR_INVALID, "qr_moe_dispatch: null pointer");
+  QR_HIP(qr::moe_dispatch_launch(idx, T, K, E, 1, counts, offsets, nullptr, perm, inv, c->stream),
+         "moe_dispatch");
+  return QR_OK;
+}
+
+int qr_moe_forward(qr_ctx* c, const qr_moe_layer* L, float* x, const float* xb, int T, int order,
+                   int32_t* idx_out, float* w_out) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_moe_forward: null ctx");
+  int rc = check_layer(L, "qr_moe_forward");
+  if (rc) return rc;
+  rc = check_experts(L, "qr_moe_forward");
+  if (rc) return rc;
+  if (order < QR_ORDER_SEQ || order > QR_ORDER_AVX512)
+    return fail(QR_ERR_INVALID, "qr_moe_forward: order %d", order);
+  if (T < 0) return fail(QR_ERR_INVALID, "qr_moe_forward: T < 0");
+  if (T == 0) return QR_OK;
+  if (!x || !xb) return fail(QR_ERR_INVALID, "qr_moe_forward: null x / xb");
+  if (!aligned(xb, 16) || !aligned(x, 16)) return fail(QR_ERR_INVALID, "qr_moe_forward: x/xb alignment");
+  const size_t need = qr::moe_scratch_bytes(L, T);
+  if (need > c->moe_scratch_bytes) {
+    if (set_device(c) != QR_OK) return QR_ERR_HIP;
+    QR_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (c->moe_scratch) (void)hipFree(c->moe_scratch);
+    c->moe_scratch = nullptr;
+    c->moe_scratch_bytes = 0;
+    hipError_t e = hipMalloc(&c->moe_scratch, need);
+    if (e != hipSuccess) return fail(QR_ERR_NOMEM, "qr_moe_forward: scratch %zu bytes", need);
+    c->moe_scratch_bytes = need;
+  }
+  qr::MoeScratch s;
+  qr::moe_scratch_carve(c->moe_scratch, L, T, &s);
+  QR_HIP(qr::moe_forward_launch(L, x, xb, T, order, s, c->stream), "moe_forward");
+  const size_t kb = (size_t)T * L->n_used;
+  if (idx_out) QR_HIP(hipMemcpyAsync(idx_out, s.idx, kb * 4, hipMemcpyDeviceToDevice, c->stream), "copy idx");
+  if (w_out) QR_HIP(hipMemcpyAsync(w_out, s.wts, kb * 4, hipMemcpyDeviceToDevice, c->stream), "copy wts");
+  return QR_OK;
+}
+
+// ---- registry -----------------------------------------------------------------
+int qr_weights_upload(qr_ctx* c, const void* host, size_t bytes, const void** dev) {
+  if (!c || !host || !dev) return fail(QR_ERR_INVALID, "qr_weights_upload: null argument");
+  std::lock_guard<std::mutex> lk(c->mu);
+  auto it = c->registry.find(host);
+  if (it != c->registry.end()) {
+    if (it->second.bytes >= bytes) {
+      *dev = it->second.dev;
+      return QR_OK;
+    }
+    (void)hipFree(it->second.dev);
+    c->registry.erase(it);
+  }
+  if (set_device(c) != QR_OK) return QR_ERR_HIP;
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
+  if (e != hipSuccess) return fail(QR_ERR_NOMEM, "qr_weights_upload: hipMalloc(%zu)", bytes);
+  e = hipMemcpyAsync(p, host, bytes, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return hip_fail(e, "qr_weights_upload: copy");
+  }
+  c->registry[host] = RegEntry{p, bytes};
+  *dev = p;
+  return QR_OK;
+}
+
+int qr_weights_upload_parts(qr_ctx* c, const void* key, const void* const* parts,
+                            size_t part_bytes, int nparts, const void** dev) {
+  if (!c || !key || !parts || !dev || nparts <= 0)
+    return fail(QR_ERR_INVALID, "qr_weights_upload_parts: bad argument");
+  for (int i = 0; i < nparts; i++)
+    if (!parts[i]) return fail(QR_ERR_INVALID, "qr_weights_upload_parts: null part %d", i);
+  const size_t bytes = part_bytes * (size_t)nparts;
+  std::lock_guard<std::mutex> lk(c->mu);
+  auto it = c->registry.find(key);
+  if (it != c->registry.end()) {
+    if (it->second.bytes >= bytes) {
+      *dev = it->second.dev;
+      return QR_OK;
+    }
+    (void)hipFree(it->second.dev);
+    c->registry.erase(it);
+  }
+  if (set_device(c) != QR_OK) return QR_ERR_HIP;
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
+  if (e != hipSuccess) return fail(QR_ERR_NOMEM, "qr_weights_upload_parts: hipMalloc(%zu)", bytes);
+  for (int i = 0; i < nparts && e == hipSuccess; i++)
+    e = hipMemcpyAsync(static_cast<uint8_t*>(p) + (size_t)i * part_bytes, parts[i], part_bytes,
+                       hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return hip_fail(e, "qr_weights_upload_parts: copy");
+  }
+  c->registry[key] = RegEntry{p, bytes};
+  *dev = p;
+  return QR_OK;
+}
+
+int qr_weights_lookup(qr_ctx* c, const void* host, const void** dev) {
+  if (!c || !host || !dev) return fail(QR_ERR_INVALID, "qr_weights_lookup: null argument");
+  std::lock_guard<std::mutex> lk(c->mu);
+  auto it = c->registry.find(host);
+  if (it == c->registry.end()) {
+    *dev = nullptr;
+    return fail(QR_ERR_INVALID, "qr_weights_lookup: %p not registered", host);
+  }
+  *dev = it->second.dev;
+  return QR_OK;
+}
+
+int qr_weights_release(qr_ctx* c, const void* host) {
+  if (!c || !host) return fail(QR_ERR_INVALID, "qr_weights_release: null argument");
+  std::lock_guard<std::mutex> lk(c->mu);
+  auto it = c->registry.find(host);
+  if (it == c->registry.end()) return QR_OK;
+  (void)hipStreamSynchronize(c->stream);
+  (void)hipFree(it->second.dev);
+  c->registry.erase(it);
+  return QR_OK;
+}
+
+int qr_weights_release_all(qr_ctx* c) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_weights_release_all: null ctx");
+  std::lock_guard<std::mutex> lk(c->mu);
+  (void)hipStreamSynchronize(c->stream);
+  for (auto& kv : c->registry) (void)hipFree(kv.second.dev);
+  c->registry.clear();
+  return QR_OK;
+}
+
+}  // extern "C"

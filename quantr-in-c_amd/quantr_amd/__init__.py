@@ -1,0 +1,265 @@
+"""ctypes binding of libqr_hip.so, the MI355X (gfx950) quantized GEMV + MoE
+library whose C ABI is declared in include/qr_hip.h and include/qr_dropin.h.
+
+This module only moves bytes and calls the C ABI; all arithmetic happens in the
+HIP kernels.  If the library has not been built, importing works but
+``load()`` raises: there is no CPU fallback.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+REPO_DIR = os.path.dirname(PKG_DIR)
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libqr_hip.so")
+HEADERS = [os.path.join(REPO_DIR, "include", "qr_hip.h"),
+           os.path.join(REPO_DIR, "include", "qr_dropin.h")]
+
+TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 0, 8, 12, 13, 14
+ORDER_SEQ, ORDER_AVX2, ORDER_AVX512 = 0, 1, 2
+
+_vp = C.c_void_p
+
+
+class QrError(RuntimeError):
+    pass
+
+
+class MoeLayer(C.Structure):
+    """qr_moe_layer (include/qr_hip.h); pointers are device addresses."""
+    _fields_ = [
+        ("dim", C.c_int), ("hidden", C.c_int), ("n_experts", C.c_int), ("n_used", C.c_int),
+        ("router", _vp), ("up", _vp), ("gate", _vp), ("down", _vp),
+        ("up_type", C.c_uint32), ("gate_type", C.c_uint32), ("down_type", C.c_uint32),
+        ("sh_hidden", C.c_int), ("sh_gate_inp", _vp), ("sh_up", _vp), ("sh_gate", _vp),
+        ("sh_down", _vp),
+        ("sh_up_type", C.c_uint32), ("sh_gate_type", C.c_uint32), ("sh_down_type", C.c_uint32),
+    ]
+
+
+_SIGS = {
+    "qr_last_error": (C.c_char_p, []),
+    "qr_version": (C.c_char_p, []),
+    "qr_device_count": (C.c_int, [C.POINTER(C.c_int)]),
+    "qr_ctx_create": (C.c_int, [C.c_int, C.POINTER(_vp)]),
+    "qr_ctx_destroy": (C.c_int, [_vp]),
+    "qr_ctx_set_stream": (C.c_int, [_vp, _vp]),
+    "qr_ctx_get_stream": (_vp, [_vp]),
+    "qr_sync": (C.c_int, [_vp]),
+    "qr_malloc": (C.c_int, [_vp, C.c_size_t, C.POINTER(_vp)]),
+    "qr_free": (C.c_int, [_vp, _vp]),
+    "qr_memcpy_h2d": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
+    "qr_memcpy_d2h": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
+    "qr_memcpy_d2d": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
+    "qr_memset": (C.c_int, [_vp, _vp, C.c_int, C.c_size_t]),
+    "qr_timer_start": (C.c_int, [_vp]),
+    "qr_timer_stop": (C.c_int, [_vp, C.POINTER(C.c_float)]),
+    "qr_copy_kernel": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
+    "qr_capture_begin": (C.c_int, [_vp]),
+    "qr_capture_end": (C.c_int, [_vp, C.POINTER(_vp)]),
+    "qr_graph_launch": (C.c_int, [_vp, _vp]),
+    "qr_graph_destroy": (C.c_int, [_vp]),
+    "qr_quantize_q8_0": (C.c_int, [_vp, _vp, _vp, C.c_long]),
+    "qr_gemv_ex": (C.c_int, [_vp, C.c_uint32, _vp, _vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int,
+                             C.c_int, _vp, _vp]),
+    "qr_gemv": (C.c_int, [_vp, C.c_uint32, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
+    "qr_matmul_f32": (C.c_int, [_vp, C.c_int, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
+    "qr_softmax": (C.c_int, [_vp, _vp, C.c_int, C.c_int]),
+    "qr_row_bytes": (C.c_size_t, [C.c_uint32, C.c_int]),
+    "qr_moe_route": (C.c_int, [_vp, C.POINTER(MoeLayer), _vp, C.c_int, C.c_int, _vp, _vp, _vp]),
+    "qr_moe_dispatch": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp]),
+    "qr_moe_forward": (C.c_int, [_vp, C.POINTER(MoeLayer), _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
+    "qr_weights_upload": (C.c_int, [_vp, _vp, C.c_size_t, C.POINTER(_vp)]),
+    "qr_weights_upload_parts": (C.c_int, [_vp, _vp, _vp, C.c_size_t, C.c_int, C.POINTER(_vp)]),
+    "qr_weights_lookup": (C.c_int, [_vp, _vp, C.POINTER(_vp)]),
+    "qr_weights_release": (C.c_int, [_vp, _vp]),
+    "qr_weights_release_all": (C.c_int, [_vp]),
+    "qr_test_expf": (C.c_int, [_vp, _vp, _vp, C.c_long]),
+    # drop-ins (include/qr_dropin.h)
+    "qr_dropin_init": (C.c_int, [C.c_int, C.c_int]),
+    "qr_dropin_shutdown": (None, []),
+    "qr_gpu_available": (C.c_int, []),
+    "qr_matmul_q_fused": (None, [_vp, _vp, _vp, C.c_uint32, C.c_int, C.c_int, C.c_int]),
+    "qr_quantize_row_q8_0": (None, [_vp, _vp, C.c_int]),
+    "qr_ops_matmul": (None, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
+    "qr_ops_softmax": (None, [_vp, C.c_int]),
+    "qr_moe_block": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32,
+                               C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "qr_dropin_register_weights": (C.c_int, [_vp, C.c_size_t]),
+    "qr_dropin_release_weights": (None, []),
+}
+
+_lib = None
+
+
+def load(path=None):
+    """Load libqr_hip.so (built by __graft_entry__.build() or `make`)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    path = path or LIB_PATH
+    if not os.path.exists(path):
+        raise QrError("libqr_hip.so is not built (%s); run __graft_entry__.build()" % path)
+    lib = C.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    if path == LIB_PATH:
+        _lib = lib
+    return lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(_vp)
+
+
+class DevBuf:
+    """A device allocation owned by a Device."""
+
+    def __init__(self, dev, nbytes):
+        self.dev = dev
+        self.nbytes = int(nbytes)
+        p = _vp()
+        dev._check(dev.lib.qr_malloc(dev.ctx, max(self.nbytes, 16), C.byref(p)), "qr_malloc")
+        self.ptr = p.value
+
+    def offset(self, nbytes):
+        return self.ptr + int(nbytes)
+
+    def free(self):
+        if self.ptr is not None and self.dev.ctx is not None:
+            self.dev.lib.qr_free(self.dev.ctx, _vp(self.ptr))
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Device:
+    """One qr_ctx on one GPU."""
+
+    def __init__(self, device=0, lib=None):
+        self.lib = lib or load()
+        ctx = _vp()
+        self._check(self.lib.qr_ctx_create(device, C.byref(ctx)), "qr_ctx_create")
+        self.ctx = ctx.value
+
+    def _check(self, rc, what):
+        if rc != 0:
+            msg = self.lib.qr_last_error().decode(errors="replace")
+            raise QrError("%s failed (%d): %s" % (what, rc, msg))
+
+    def close(self):
+        if self.ctx is not None:
+            self.lib.qr_ctx_destroy(_vp(self.ctx))
+            self.ctx = None
+
+    # ---- memory
+    def alloc(self, nbytes):
+        return DevBuf(self, nbytes)
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        b = DevBuf(self, arr.nbytes)
+        self._check(self.lib.qr_memcpy_h2d(self.ctx, _vp(b.ptr), _ptr(arr), arr.nbytes), "h2d")
+        return b
+
+    def download(self, buf, shape, dtype, offset=0):
+        out = np.empty(shape, dtype)
+        ptr = buf.ptr if isinstance(buf, DevBuf) else buf
+        self._check(self.lib.qr_memcpy_d2h(self.ctx, _ptr(out), _vp(ptr + offset), out.nbytes),
+                    "d2h")
+        return out
+
+    def write(self, buf, arr, offset=0):
+        arr = np.ascontiguousarray(arr)
+        ptr = buf.ptr if isinstance(buf, DevBuf) else buf
+        self._check(self.lib.qr_memcpy_h2d(self.ctx, _vp(ptr + offset), _ptr(arr), arr.nbytes),
+                    "h2d")
+
+    def copy(self, dst, src, nbytes):
+        self._check(self.lib.qr_memcpy_d2d(self.ctx, _vp(dst), _vp(src), nbytes), "d2d")
+
+    def sync(self):
+        self._check(self.lib.qr_sync(self.ctx), "qr_sync")
+
+    # ---- timing on the context stream
+    def timer_start(self):
+        self._check(self.lib.qr_timer_start(self.ctx), "qr_timer_start")
+
+    def timer_stop(self):
+        ms = C.c_float()
+        self._check(self.lib.qr_timer_stop(self.ctx, C.byref(ms)), "qr_timer_stop")
+        return ms.value
+
+    # ---- HIP graphs
+    def capture(self, fn):
+        """Record fn()'s enqueued work into a graph; returns the graph handle."""
+        self._check(self.lib.qr_capture_begin(self.ctx), "qr_capture_begin")
+        try:
+            fn()
+        finally:
+            g = _vp()
+            rc = self.lib.qr_capture_end(self.ctx, C.byref(g))
+        self._check(rc, "qr_capture_end")
+        return g.value
+
+    def graph_launch(self, g):
+        self._check(self.lib.qr_graph_launch(self.ctx, _vp(g)), "qr_graph_launch")
+
+    def graph_destroy(self, g):
+        self._check(self.lib.qr_graph_destroy(_vp(g)), "qr_graph_destroy")
+
+    # ---- ops (device pointers)
+    def quantize_q8_0(self, x_ptr, y_ptr, n):
+        self._check(self.lib.qr_quantize_q8_0(self.ctx, _vp(x_ptr), _vp(y_ptr), n), "qr_quantize_q8_0")
+
+    def gemv(self, qtype, w_ptr, x_ptr, y_ptr, n, d, nt=1, xstride=None, ystride=None,
+             acc_ptr=None, accb_ptr=None):
+        self._check(self.lib.qr_gemv_ex(self.ctx, qtype, _vp(w_ptr), _vp(x_ptr),
+                                         xstride or d, _vp(y_ptr), ystride or n, n, d, nt,
+                                         _vp(acc_ptr), _vp(accb_ptr)), "qr_gemv_ex")
+
+    def matmul_f32(self, order, w_ptr, x_ptr, y_ptr, n, d, nt=1):
+        self._check(self.lib.qr_matmul_f32(self.ctx, order, _vp(w_ptr), _vp(x_ptr), _vp(y_ptr),
+                                           n, d, nt), "qr_matmul_f32")
+
+    def softmax(self, x_ptr, rows, n):
+        self._check(self.lib.qr_softmax(self.ctx, _vp(x_ptr), rows, n), "qr_softmax")
+
+    def moe_route(self, layer, xb_ptr, T, order, probs_ptr, idx_ptr, wts_ptr):
+        self._check(self.lib.qr_moe_route(self.ctx, C.byref(layer), _vp(xb_ptr), T, order,
+                                          _vp(probs_ptr), _vp(idx_ptr), _vp(wts_ptr)),
+                    "qr_moe_route")
+
+    def moe_dispatch(self, idx_ptr, T, K, E, counts, offsets, perm, inv):
+        self._check(self.lib.qr_moe_dispatch(self.ctx, _vp(idx_ptr), T, K, E, _vp(counts),
+                                             _vp(offsets), _vp(perm), _vp(inv)), "qr_moe_dispatch")
+
+    def moe_forward(self, layer, x_ptr, xb_ptr, T, order, idx_ptr=None, w_ptr=None):
+        self._check(self.lib.qr_moe_forward(self.ctx, C.byref(layer), _vp(x_ptr), _vp(xb_ptr), T,
+                                            order, _vp(idx_ptr), _vp(w_ptr)), "qr_moe_forward")
+
+    def copy_kernel(self, dst, src, nbytes):
+        self._check(self.lib.qr_copy_kernel(self.ctx, _vp(dst), _vp(src), nbytes), "qr_copy_kernel")
+
+    def test_expf(self, x_ptr, y_ptr, n):
+        self._check(self.lib.qr_test_expf(self.ctx, _vp(x_ptr), _vp(y_ptr), n), "qr_test_expf")
+
+
+def declared_symbols():
+    """Function names declared in include/qr_hip.h and include/qr_dropin.h."""
+    import re
+    names = []
+    for h in HEADERS:
+        src = open(h).read()
+        src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        for m in re.finditer(r"\b(qr_[a-z0-9_]+)\s*\(", src):
+            if m.group(1) not in names:
+                names.append(m.group(1))
+    return names

@@ -1,0 +1,139 @@
+"""Deterministic inputs for the golden fixtures (numpy PCG64 streams).
+
+The fixtures in this directory store the reference's outputs together with a
+SHA-256 of the inputs they were computed from; the tests rebuild the inputs
+with these functions and check the digest before comparing, so a change here
+shows up as a digest mismatch rather than as a silent parity failure.
+
+Weight blocks are random bytes with their fp16 scale fields overwritten by
+moderate normal halves: every byte pattern is a valid block under the
+reference's decoding (src/quant.c:160-240), so random bytes exercise all
+nibble, fifth-bit and sub-scale combinations.
+"""
+import hashlib
+
+import numpy as np
+
+TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 8, 12, 13, 14
+BLOCK = {TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144), TYPE_Q5_K: (256, 176), TYPE_Q6_K: (256, 210)}
+
+
+def digest(*arrays):
+    h = hashlib.sha256()
+    for a in arrays:
+        a = np.ascontiguousarray(a)
+        h.update(str(a.dtype).encode())
+        h.update(str(a.shape).encode())
+        h.update(a.tobytes())
+    return h.hexdigest()
+
+
+def _halves(rng, n, lo, hi):
+    return rng.uniform(lo, hi, size=n).astype(np.float16).view(np.uint16)
+
+
+def blocks(seed, qtype, nblocks, scale_lo=2e-4, scale_hi=1e-3):
+    """nblocks random blocks of qtype (uint8 [nblocks * block_bytes])."""
+    rng = np.random.default_rng(seed)
+    bb = BLOCK[qtype][1]
+    b = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
+    if qtype == TYPE_Q8_0:
+        b[:, 0:2] = _halves(rng, nblocks, 5e-4, 2e-3).view(np.uint8).reshape(nblocks, 2)
+    elif qtype in (TYPE_Q4_K, TYPE_Q5_K):
+        b[:, 0:2] = _halves(rng, nblocks, scale_lo, scale_hi).view(np.uint8).reshape(nblocks, 2)
+        b[:, 2:4] = _halves(rng, nblocks, scale_lo, scale_hi).view(np.uint8).reshape(nblocks, 2)
+    else:
+        b[:, 208:210] = _halves(rng, nblocks, scale_lo, scale_hi).view(np.uint8).reshape(nblocks, 2)
+    return b.reshape(-1)
+
+
+def special_blocks(qtype):
+    """Blocks with edge-case scales: zero, half subnormals (decoded by the
+    reference as mant * 2^-136), the largest half, and saturated fields."""
+    bb = BLOCK[qtype][1]
+    codes = [0x0000, 0x0001, 0x03FF, 0x0400, 0x3C00, 0x7BFF, 0x8400, 0xBC00]
+    out = []
+    rng = np.random.default_rng(1234 + qtype)
+    for c in codes:
+        b = rng.integers(0, 256, size=bb, dtype=np.uint8)
+        if qtype == TYPE_Q8_0:
+            b[0:2] = np.array([c], np.uint16).view(np.uint8)
+        elif qtype in (TYPE_Q4_K, TYPE_Q5_K):
+            b[0:2] = np.array([c], np.uint16).view(np.uint8)
+            b[2:4] = np.array([c ^ 0x8000], np.uint16).view(np.uint8)
+        else:
+            b[208:210] = np.array([c], np.uint16).view(np.uint8)
+        out.append(b)
+    b = np.full(bb, 0xFF, np.uint8)  # every nibble 15, every scale 63 / min 3
+    if qtype == TYPE_Q8_0:
+        b[0:2] = np.array([0x3C00], np.uint16).view(np.uint8)
+    elif qtype in (TYPE_Q4_K, TYPE_Q5_K):
+        b[0:4] = np.array([0x3C00, 0x3800], np.uint16).view(np.uint8)
+    else:
+        b[208:210] = np.array([0x3C00], np.uint16).view(np.uint8)
+    out.append(b)
+    return np.concatenate(out)
+
+
+def q4k_to_q5k(blob):
+    """Q4_K bytes -> Q5_K bytes with a zero fifth-bit plane (same decoded values)."""
+    src = np.ascontiguousarray(blob, np.uint8).reshape(-1, 144)
+    out = np.zeros((src.shape[0], 176), np.uint8)
+    out[:, 0:16] = src[:, 0:16]
+    out[:, 48:176] = src[:, 16:144]
+    return out.reshape(-1)
+
+
+def activations(seed, rows, d, std=1.0):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((rows, d)) * std).astype(np.float32)
+
+
+def dot_set(seed, qtype, nrows, d):
+    """nrows random rows of d elements plus one row made of special_blocks."""
+    elems, bb = BLOCK[qtype]
+    nb = d // elems
+    main = blocks(seed, qtype, nrows * nb).reshape(nrows, nb * bb)
+    spec = np.resize(special_blocks(qtype), nb * bb).reshape(1, nb * bb)
+    return np.concatenate([main, spec]).astype(np.uint8)
+
+
+# MoE golden cases: dim, hidden, E, K, T, up/gate type, down type.  Case "a"
+# stores Q4_K experts; the reference is run on their zero-fifth-bit Q5_K form.
+MOE_CASES = {
+    "a": (512, 256, 16, 4, 6, TYPE_Q4_K, TYPE_Q6_K),
+    "b": (512, 256, 8, 2, 4, TYPE_Q8_0, TYPE_Q8_0),
+    "c": (256, 256, 64, 8, 8, TYPE_Q5_K, TYPE_Q6_K),
+}
+
+
+def moe_inputs(name):
+    dim, hidden, E, K, T, ut, dt = MOE_CASES[name]
+    seed = 500 + 10 * (ord(name) - ord("a"))
+    ue = BLOCK[ut][0]
+    de = BLOCK[dt][0]
+    return dict(dim=dim, hidden=hidden, E=E, K=K, T=T, up_type=ut, down_type=dt,
+                up=blocks(seed, ut, E * hidden * (dim // ue)),
+                gate=blocks(seed + 1, ut, E * hidden * (dim // ue)),
+                down=blocks(seed + 2, dt, E * dim * (hidden // de)),
+                router=activations(seed + 3, E, dim, std=0.05),
+                x=activations(seed + 4, T, dim))
+
+
+def q8_edge_rows():
+    """Rows of 64 floats (two Q8_0 blocks each) hitting quantize_row_q8_0's
+    edge cases."""
+    rows = []
+    rows.append(np.zeros(64, np.float32))                               # amax 0 -> d 0, id 0
+    rows.append(np.full(64, 0.75, np.float32))                          # all equal
+    rows.append(np.linspace(-1e-30, 1e-30, 64).astype(np.float32))      # d flushes to 0 in fp16
+    rows.append(np.linspace(-1e30, 1e30, 64).astype(np.float32))        # d saturates to inf
+    r = np.arange(64, dtype=np.float32) - 31.5                          # ties at .5 after scaling
+    r[0] = 127.0
+    r[32] = -127.0
+    rows.append(r.astype(np.float32))
+    rows.append(((np.arange(64) - 16) * 0.125).astype(np.float32))      # tests/tests.c:59-61 ramp
+    rows.append(np.float32(2.0) ** np.arange(-60, 4).astype(np.float32))
+    rng = np.random.default_rng(77)
+    rows.append((rng.standard_normal(64) * 1e-5).astype(np.float32))    # amax near fp16 min normal * 127
+    return np.stack(rows).astype(np.float32)

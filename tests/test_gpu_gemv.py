@@ -1,0 +1,205 @@
+"""GPU parity of the quantized GEMV path against the oracle, through the C ABI.
+
+Every comparison is bit-exact: int32 unit sums, activation block sums, fp32
+outputs (the reference's sequential term order), the device Q8_0 quantizer,
+expf, softmax and the fp32 router GEMV in each reference order.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import inputs as I
+import quantr_amd as Q
+from conftest import assert_bits_equal, bits
+from oracle import ORDER_AVX2, ORDER_AVX512, ORDER_SEQ
+from quantr_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+TYPES = (Q.TYPE_Q8_0, Q.TYPE_Q4_K, Q.TYPE_Q5_K, Q.TYPE_Q6_K)
+
+
+def _run_gemv(dev, qtype, W, X, n, d, nt, with_acc=True):
+    """Upload W [n][rb] and X [nt][d]; return (y [nt][n], acc [nt][n][units], accb)."""
+    units = (d // 32) if qtype == Q.TYPE_Q8_0 else (d // 256) * 8
+    wb = dev.upload(W)
+    xb = dev.upload(np.ascontiguousarray(X, np.float32))
+    yb = dev.alloc(nt * n * 4)
+    acc = dev.alloc(max(nt * n * units, 1) * 4) if with_acc else None
+    accb = dev.alloc(max(nt * units, 1) * 4) if with_acc else None
+    dev.gemv(qtype, wb.ptr, xb.ptr, yb.ptr, n, d, nt, acc_ptr=acc.ptr if acc else None,
+             accb_ptr=accb.ptr if accb else None)
+    y = dev.download(yb, (nt, n), np.float32)
+    if not with_acc:
+        return y, None, None
+    return (y, dev.download(acc, (nt, n, units), np.int32),
+            dev.download(accb, (nt, units), np.int32))
+
+
+def _check_gemv(dev, oracle, qtype, W, X, n, d, nt, check_acc=True):
+    y, acc, accb = _run_gemv(dev, qtype, W, X, n, d, nt, with_acc=check_acc)
+    want = oracle.matmul_q_fused(X, W, qtype, n, d, threads=16)
+    assert_bits_equal(y, want.reshape(nt, n), "gemv type %d %dx%d nt=%d" % (qtype, n, d, nt))
+    if check_acc:
+        for t in range(nt):
+            xq = oracle.quantize_q8_0(X[t])
+            for r in range(n):
+                isum, bsum = oracle.row_accum(qtype, W[r], xq, d)
+                assert (acc[t, r] == isum).all(), "int sums row %d tok %d" % (r, t)
+            assert (accb[t] == bsum).all(), "activation block sums tok %d" % t
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("n,d", [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632)])
+def test_gemv_tinyllama_shapes_nt1(dev, oracle, qtype, n, d):
+    """TinyLlama-1.1B layer shapes, weights N(0, 0.02) quantized, x N(0, 1)."""
+    W = synth.weights(1000 + n + d + qtype, n, d, qtype)
+    X = synth.normal(7, (1, d))
+    _check_gemv(dev, oracle, qtype, W, X, n, d, 1, check_acc=(n * d <= 2048 * 2048))
+
+
+@pytest.mark.parametrize("qtype", (Q.TYPE_Q4_K, Q.TYPE_Q5_K, Q.TYPE_Q6_K))
+def test_gemv_lm_head_32000(dev, oracle, qtype):
+    """The 32000 x 2048 lm_head of the K-quant sweep, batch 1 and 4."""
+    W = synth.weights(77 + qtype, 32000, 2048, qtype)
+    for nt in (1, 4):
+        X = synth.normal(8 + nt, (nt, 2048))
+        _check_gemv(dev, oracle, qtype, W, X, 32000, 2048, nt, check_acc=False)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("nt", [1, 2, 3, 4, 8])
+def test_gemv_batch_widths(dev, oracle, qtype, nt):
+    """Token counts 1..8 (speculative-verify width 4): int sums per token."""
+    W = synth.weights(31 + qtype, 384, 2048, qtype)
+    X = synth.normal(32 + nt, (nt, 2048))
+    _check_gemv(dev, oracle, qtype, W, X, 384, 2048, nt)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("d", [2048, 768])
+def test_gemv_random_blocks(dev, oracle, qtype, d):
+    """Random block bytes (every nibble / fifth-bit / scale pattern) plus a row
+    of edge-case blocks: zero, subnormal, largest and negative half scales."""
+    W = I.dot_set(900 + qtype + d, qtype, 63, d)
+    X = I.activations(901, 4, d)
+    _check_gemv(dev, oracle, qtype, W, X, W.shape[0], d, 4)
+
+
+@pytest.mark.parametrize("qtype,d", [(Q.TYPE_Q4_K, 1408), (Q.TYPE_Q6_K, 1408), (Q.TYPE_Q5_K, 300),
+                                     (Q.TYPE_Q8_0, 1408), (Q.TYPE_Q8_0, 48), (Q.TYPE_Q4_K, 128),
+                                     (Q.TYPE_Q8_0, 16)])
+def test_gemv_ragged_widths(dev, oracle, qtype, d):
+    """Widths that are not whole blocks: the reference keeps only whole blocks
+    (src/quant.c:292, 467, 477-484) and a row shorter than one block is 0."""
+    elems, bb = I.BLOCK[qtype]
+    nb = d // elems
+    n = 37
+    W = I.blocks(5 + d, qtype, max(n * nb, 1))[: n * nb * bb].reshape(n, nb * bb)
+    X = I.activations(6, 1, d)
+    y, _, _ = _run_gemv(dev, qtype, W, X, n, d, 1, with_acc=False)
+    want = oracle.matmul_q_fused(X, W, qtype, n, d)
+    assert_bits_equal(y, want, "ragged d=%d" % d)
+
+
+def test_gemv_f32_rows(dev, oracle):
+    """matmul_q_fused's F32 rows (src/quant.c:448-464): sequential order."""
+    W = I.activations(3, 129, 2048, std=0.02)
+    X = I.activations(4, 2, 2048)
+    wb, xb, yb = dev.upload(W), dev.upload(X), dev.alloc(2 * 129 * 4)
+    dev.gemv(Q.TYPE_F32, wb.ptr, xb.ptr, yb.ptr, 129, 2048, 2)
+    got = dev.download(yb, (2, 129), np.float32)
+    want = np.stack([oracle.matmul_f32(x, W, 129, 2048, ORDER_SEQ) for x in X])
+    assert_bits_equal(got, want, "F32 rows")
+
+
+def test_gemv_null_weights_zero(dev):
+    """NULL weights give zeros (src/quant.c:443-446)."""
+    xb, yb = dev.upload(np.ones((1, 256), np.float32)), dev.upload(np.full(64, 7.0, np.float32))
+    dev.gemv(Q.TYPE_Q4_K, None, xb.ptr, yb.ptr, 64, 256, 1)
+    assert (dev.download(yb, 64, np.float32) == 0).all()
+
+
+def test_quantize_q8_0_device(dev, oracle):
+    """quantize_row_q8_0 (src/quant.c:143-158) on the device, edge rows and
+    N(0, 1) rows."""
+    rows = np.concatenate([I.q8_edge_rows().reshape(-1), I.activations(12, 8, 4096).reshape(-1)])
+    xb = dev.upload(rows)
+    yb = dev.alloc(rows.size // 32 * 34)
+    dev.quantize_q8_0(xb.ptr, yb.ptr, rows.size)
+    got = dev.download(yb, rows.size // 32 * 34, np.uint8)
+    assert (got == oracle.quantize_q8_0(rows)).all()
+
+
+@pytest.mark.parametrize("E,d", [(128, 2048), (60, 2048), (16, 2051)])
+@pytest.mark.parametrize("order", [ORDER_SEQ, ORDER_AVX2, ORDER_AVX512])
+def test_router_matmul(dev, oracle, E, d, order):
+    """Router logits in each reference order (src/kernels.c:18-73)."""
+    W = I.activations(40 + E, E, d, std=0.02)
+    X = I.activations(41 + E, 16, d)
+    wb, xb, yb = dev.upload(W), dev.upload(X), dev.alloc(16 * E * 4)
+    dev.matmul_f32(order, wb.ptr, xb.ptr, yb.ptr, E, d, 16)
+    got = dev.download(yb, (16, E), np.float32)
+    want = np.stack([oracle.matmul_f32(x, W, E, d, order) for x in X])
+    assert_bits_equal(got, want, "router order %d" % order)
+
+
+def test_softmax_device(dev, oracle):
+    """softmax_ref rows with glibc-exact expf, including ties and -inf gaps."""
+    rows = [I.activations(50, 1, 128)[0] * 4, np.zeros(60, np.float32),
+            np.array([1.0, 2.0, 3.0, 4.0], np.float32), I.activations(51, 1, 2048)[0] * 30]
+    for r in rows:
+        xb = dev.upload(r)
+        dev.softmax(xb.ptr, 1, r.size)
+        assert_bits_equal(dev.download(xb, r.size, np.float32), oracle.softmax(r), "softmax")
+
+
+def test_expf_device_vs_libm(dev, oracle):
+    """The device expf restatement against the host C library, on a stride
+    through all float bit patterns plus the special values."""
+    pats = np.arange(0, 2 ** 32, 251, dtype=np.uint64).astype(np.uint32)
+    x = pats.view(np.float32)
+    x = np.concatenate([x[~np.isnan(x)], np.array([0.0, -0.0, np.inf, -np.inf, 88.72, -103.97,
+                                                   -87.3, 1e-30, -1e-30], np.float32)])
+    xb, yb = dev.upload(x), dev.alloc(x.size * 4)
+    dev.test_expf(xb.ptr, yb.ptr, x.size)
+    assert_bits_equal(dev.download(yb, x.size, np.float32), oracle.expf(x), "expf")
+
+
+# ---- drop-in host-pointer entry points (include/qr_dropin.h) ----------------
+def _fp(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+@pytest.mark.parametrize("qtype", TYPES + (Q.TYPE_F32,))
+def test_dropin_matmul_q_fused(oracle, qtype):
+    lib = Q.load()
+    assert lib.qr_gpu_available() != 0
+    n, d = 500, 2048
+    W = (I.activations(60, n, d, std=0.02) if qtype == Q.TYPE_F32
+         else synth.weights(61 + qtype, n, d, qtype))
+    x = I.activations(62, 1, d)[0]
+    out = np.zeros(n, np.float32)
+    for _ in range(2):  # second call reuses the registered device copy
+        lib.qr_matmul_q_fused(_fp(out), _fp(x), _fp(W), qtype, n, d, 8)
+        assert_bits_equal(out, oracle.matmul_q_fused(x, W, qtype, n, d), "drop-in")
+    lib.qr_matmul_q_fused(_fp(out), _fp(x), None, qtype, n, d, 8)
+    assert (out == 0).all()
+
+
+def test_dropin_quantize_and_ops(oracle):
+    lib = Q.load()
+    x = I.activations(70, 1, 4096)[0]
+    y = np.zeros(4096 // 32 * 34, np.uint8)
+    lib.qr_quantize_row_q8_0(_fp(x), _fp(y), 4096)
+    assert (y == oracle.quantize_q8_0(x)).all()
+    W = I.activations(71, 128, 2048, std=0.02)
+    xb = I.activations(72, 1, 2048)[0]
+    out = np.zeros(128, np.float32)
+    assert lib.qr_dropin_init(0, ORDER_AVX2) == 0
+    lib.qr_ops_matmul(_fp(out), _fp(xb), _fp(W), 128, 2048, 1)
+    assert_bits_equal(out, oracle.matmul_f32(xb, W, 128, 2048, ORDER_AVX2), "ops matmul")
+    p = out.copy()
+    lib.qr_ops_softmax(_fp(p), 128)
+    assert_bits_equal(p, oracle.softmax(out), "ops softmax")

@@ -1,0 +1,231 @@
+"""GPU parity of the MoE layer against the oracle, through the C ABI.
+
+Bit-exact: router top-k indices and weights, dispatch permutation, and the
+layer output (the oracle's per-token block, src/runtime.c:202-269, which the
+CPU suite pins to the reference's own forward_runtime).  Quantized dots run in
+the sequential order on the GPU, so the oracle is asked for that dot order;
+the router runs in the order under test.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import inputs as I
+import quantr_amd as Q
+from conftest import assert_bits_equal
+from oracle import ORDER_AVX2, ORDER_SEQ, Oracle
+from quantr_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+class DevLayer:
+    """A MoE layer uploaded to the device, plus the host copies for the oracle."""
+
+    def __init__(self, dev, dim, hidden, E, K, router, up, gate, down, ut, dt, shared=None):
+        self.h = dict(dim=dim, hidden=hidden, E=E, K=K, router=router, up=up, gate=gate,
+                      down=down, ut=ut, dt=dt, shared=shared)
+        self.bufs = [dev.upload(router), dev.upload(up), dev.upload(gate), dev.upload(down)]
+        L = Q.MoeLayer(dim, hidden, E, K, *[b.ptr for b in self.bufs], ut, ut, dt)
+        if shared is not None:
+            sb = [dev.upload(shared["gate_inp"]), dev.upload(shared["up"]),
+                  dev.upload(shared["gate"]), dev.upload(shared["down"])]
+            self.bufs += sb
+            L.sh_hidden = shared["hidden"]
+            L.sh_gate_inp, L.sh_up, L.sh_gate, L.sh_down = [b.ptr for b in sb]
+            L.sh_up_type = L.sh_gate_type = shared["up_type"]
+            L.sh_down_type = shared["down_type"]
+        self.L = L
+
+    def oracle_layer(self, keep):
+        h = self.h
+        return Oracle.make_layer(keep, h["dim"], h["hidden"], h["E"], h["K"], h["router"], h["up"],
+                                 h["ut"], h["gate"], h["ut"], h["down"], h["dt"],
+                                 shared=h["shared"])
+
+
+def run_moe(dev, layer, x, xb, order):
+    T, dim = x.shape
+    K = layer.L.n_used
+    xd, xbd = dev.upload(x), dev.upload(xb)
+    idx, w = dev.alloc(T * K * 4), dev.alloc(T * K * 4)
+    dev.moe_forward(layer.L, xd.ptr, xbd.ptr, T, order, idx.ptr, w.ptr)
+    return (dev.download(xd, (T, dim), np.float32), dev.download(idx, (T, K), np.int32),
+            dev.download(w, (T, K), np.float32))
+
+
+def check_moe(dev, oracle, layer, x, xb, order, what):
+    got, gi, gw = run_moe(dev, layer, x, xb, order)
+    keep = []
+    want, wi, ww = oracle.moe_forward(x, xb, layer.oracle_layer(keep), order=order,
+                                      dot_order=ORDER_SEQ, threads=16)
+    assert (gi == wi).all(), "%s: routing indices differ" % what
+    assert_bits_equal(gw, ww, what + " routing weights")
+    assert_bits_equal(got, want, what + " layer output")
+
+
+def random_layer(dev, name):
+    m = I.moe_inputs(name)
+    return DevLayer(dev, m["dim"], m["hidden"], m["E"], m["K"], m["router"], m["up"], m["gate"],
+                    m["down"], m["up_type"], m["down_type"]), m
+
+
+@pytest.mark.parametrize("name", sorted(I.MOE_CASES))
+@pytest.mark.parametrize("order", [ORDER_SEQ, ORDER_AVX2])
+@pytest.mark.parametrize("T", [1, 3, 16])
+def test_moe_golden_shapes(dev, oracle, name, order, T):
+    """The golden MoE cases (random block bytes) at several token counts."""
+    layer, m = random_layer(dev, name)
+    x = I.activations(800 + T, T, m["dim"])
+    xb = I.activations(801 + T, T, m["dim"])
+    check_moe(dev, oracle, layer, x, xb, order, "case %s T=%d" % (name, T))
+
+
+def test_moe_matches_reference_fixture(dev, golden):
+    """End to end against the reference's forward_runtime output (fixture),
+    for the Q4_K / Q6_K and Q5_K / Q6_K cases (no Q8_0 experts: the reference's
+    AVX2 build uses a lane order for Q8_0 dots that the GPU does not run)."""
+    g = golden("moe.npz")
+    for name in ("a", "c"):
+        layer, m = random_layer(dev, name)
+        for build, order in (("c99", ORDER_SEQ), ("avx2", ORDER_AVX2)):
+            xb = g["xb_%s_%s" % (name, build)]
+            got, _, _ = run_moe(dev, layer, m["x"], xb, order)
+            assert_bits_equal(got, g["xo_%s_%s" % (name, build)], "reference %s/%s" % (name, build))
+
+
+_QWEN3 = {}
+
+
+def qwen3_layer(dev):
+    """Qwen3-30B-A3B-shaped layer: 2048 wide, 128 experts top-8, ffn 768,
+    gate/up Q4_K, down Q6_K, N(0, 0.02) weights, Zipf(1.1) router skew."""
+    if "layer" not in _QWEN3:
+        dim, hidden, E, K = 2048, 768, 128, 8
+        router, u, _ = synth.zipf_router(3000, E, dim)
+        up = synth.weights(3001, E * hidden, dim, Q.TYPE_Q4_K)
+        gate = synth.weights(3002, E * hidden, dim, Q.TYPE_Q4_K)
+        down = synth.weights(3003, E * dim, hidden, Q.TYPE_Q6_K)
+        _QWEN3["layer"] = DevLayer(dev, dim, hidden, E, K, router, up, gate, down, Q.TYPE_Q4_K,
+                                   Q.TYPE_Q6_K)
+        _QWEN3["u"] = u
+    return _QWEN3["layer"], _QWEN3["u"]
+
+
+@pytest.mark.parametrize("T", [1, 16, 64])
+@pytest.mark.parametrize("order", [ORDER_SEQ, ORDER_AVX2])
+def test_moe_qwen3_shape(dev, oracle, T, order):
+    layer, u = qwen3_layer(dev)
+    xb = synth.zipf_tokens(3100 + T, T, 2048, u)
+    x = synth.normal(3200 + T, (T, 2048))
+    check_moe(dev, oracle, layer, x, xb, order, "qwen3 T=%d" % T)
+
+
+def test_moe_qwen3_t512_routing_and_output(dev, oracle):
+    """T = 512: routing and dispatch bit-exact; output bit-exact on every token."""
+    layer, u = qwen3_layer(dev)
+    T = 512
+    xb = synth.zipf_tokens(3512, T, 2048, u)
+    x = synth.normal(3513, (T, 2048))
+    check_moe(dev, oracle, layer, x, xb, ORDER_AVX2, "qwen3 T=512")
+
+
+def test_moe_qwen15_shared_expert(dev, oracle):
+    """Qwen1.5-MoE-A2.7B shape: 60 experts top-4, ffn 1408 (gate/up Q4_K; the
+    1408-wide down projection stored Q8_0, since 1408 is not a whole number of
+    256-blocks), shared expert ffn 5632 Q4_K with a sigmoid gate."""
+    dim, hidden, E, K, SH = 2048, 1408, 60, 4, 5632
+    router = synth.normal(4000, (E, dim), 0.02)
+    up = synth.weights(4001, E * hidden, dim, Q.TYPE_Q4_K)
+    gate = synth.weights(4002, E * hidden, dim, Q.TYPE_Q4_K)
+    down = synth.weights(4003, E * dim, hidden, Q.TYPE_Q8_0)
+    shared = dict(hidden=SH, gate_inp=synth.normal(4004, (dim,), 0.02),
+                  up=synth.weights(4005, SH, dim, Q.TYPE_Q4_K),
+                  gate=synth.weights(4006, SH, dim, Q.TYPE_Q4_K),
+                  down=synth.weights(4007, dim, SH, Q.TYPE_Q4_K),
+                  up_type=Q.TYPE_Q4_K, down_type=Q.TYPE_Q4_K)
+    layer = DevLayer(dev, dim, hidden, E, K, router, up, gate, down, Q.TYPE_Q4_K, Q.TYPE_Q8_0,
+                     shared=shared)
+    for T in (1, 8, 64):
+        xb = synth.normal(4100 + T, (T, dim))
+        x = synth.normal(4200 + T, (T, dim))
+        check_moe(dev, oracle, layer, x, xb, ORDER_SEQ, "qwen1.5 T=%d" % T)
+
+
+@pytest.mark.parametrize("order", [ORDER_SEQ, ORDER_AVX2])
+def test_route_topk_probs(dev, oracle, order):
+    """Router logits, softmax probabilities, top-8 indices and renormalised
+    weights for 64 tokens, with exact ties planted in the router rows."""
+    E, K, dim, T = 128, 8, 2048, 64
+    W = I.activations(5000, E, dim, std=0.02)
+    W[7] = W[3]  # identical experts tie on every token: lowest index must win
+    W[100] = W[3]
+    X = I.activations(5001, T, dim)
+    wb, xb = dev.upload(W), dev.upload(X)
+    L = Q.MoeLayer(dim, 768, E, K, wb.ptr, None, None, None, 0, 0, 0)
+    pb, ib, wtb = dev.alloc(T * E * 4), dev.alloc(T * K * 4), dev.alloc(T * K * 4)
+    dev.moe_route(L, xb.ptr, T, order, pb.ptr, ib.ptr, wtb.ptr)
+    probs = dev.download(pb, (T, E), np.float32)
+    idx = dev.download(ib, (T, K), np.int32)
+    wts = dev.download(wtb, (T, K), np.float32)
+    for t in range(T):
+        _, p, i, w = oracle.route(X[t], W, E, K, order)
+        assert_bits_equal(probs[t], p, "probs t=%d" % t)
+        assert (idx[t] == i).all(), "indices t=%d" % t
+        assert_bits_equal(wts[t], w, "weights t=%d" % t)
+
+
+@pytest.mark.parametrize("T,K,E", [(512, 8, 128), (64, 4, 60), (1, 8, 128), (7, 3, 5),
+                                   (300, 16, 256)])
+def test_dispatch(dev, oracle, T, K, E):
+    """Histogram, exclusive scan and stable permute against the oracle's
+    counting sort; plus the invariants (bijection, grouping, order)."""
+    rng = np.random.default_rng(T * 1000 + E)
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    idx = np.stack([rng.choice(E, size=K, replace=False, p=p / p.sum()) for _ in range(T)])
+    idx = idx.astype(np.int32)
+    ib = dev.upload(idx)
+    cb, ob, pb, vb = dev.alloc(E * 4), dev.alloc((E + 1) * 4), dev.alloc(T * K * 4), dev.alloc(T * K * 4)
+    dev.moe_dispatch(ib.ptr, T, K, E, cb.ptr, ob.ptr, pb.ptr, vb.ptr)
+    counts = dev.download(cb, E, np.int32)
+    offsets = dev.download(ob, E + 1, np.int32)
+    perm = dev.download(pb, T * K, np.int32)
+    inv = dev.download(vb, T * K, np.int32)
+    c, o, pm, iv = oracle.dispatch(idx, E)
+    assert (counts == c).all() and (offsets == o).all() and (perm == pm).all() and (inv == iv).all()
+    assert counts.sum() == T * K and sorted(perm.tolist()) == list(range(T * K))
+    assert (perm[inv] == np.arange(T * K)).all()
+    flat = idx.ravel()
+    for e in range(E):
+        seg = perm[offsets[e]:offsets[e + 1]]
+        assert (flat[seg] == e).all() and (np.diff(seg) > 0).all()
+
+
+def test_dropin_moe_block(dev, oracle):
+    """qr_moe_block: the MoE block with the reference's host pointers (per
+    expert pointer arrays as TransformerWeights holds them)."""
+    lib = Q.load()
+    m = I.moe_inputs("a")
+    dim, hidden, E, K = m["dim"], m["hidden"], m["E"], m["K"]
+    su = m["up"].size // E
+    sd = m["down"].size // E
+    base_u, base_g, base_d = (a.ctypes.data for a in (m["up"], m["gate"], m["down"]))
+    up_p = (C.c_void_p * E)(*[base_u + e * su for e in range(E)])
+    gate_p = (C.c_void_p * E)(*[base_g + e * su for e in range(E)])
+    # a non-contiguous copy of the down experts: exercises the gather upload
+    down_parts = [np.array(m["down"][e * sd:(e + 1) * sd]) for e in range(E)]
+    down_p = (C.c_void_p * E)(*[a.ctypes.data for a in down_parts[::-1]][::-1])
+    assert lib.qr_dropin_init(0, ORDER_SEQ) == 0
+    x0 = I.activations(990, 1, dim)[0]
+    xb = I.activations(991, 1, dim)[0]
+    x = x0.copy()
+    rc = lib.qr_moe_block(x.ctypes.data_as(C.c_void_p), xb.ctypes.data_as(C.c_void_p),
+                          m["router"].ctypes.data_as(C.c_void_p), up_p, gate_p, down_p,
+                          m["up_type"], m["up_type"], m["down_type"], dim, hidden, E, K, 8)
+    assert rc == 0
+    keep = []
+    L = Oracle.make_layer(keep, dim, hidden, E, K, m["router"], m["up"], m["up_type"], m["gate"],
+                          m["up_type"], m["down"], m["down_type"])
+    want, _, _ = oracle.moe_forward(x0[None, :], xb[None, :], L, order=ORDER_SEQ)
+    assert_bits_equal(x, want[0], "drop-in MoE block")
