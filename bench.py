@@ -102,10 +102,14 @@ def copy_calibration(dev, nbytes=512 << 20):
     """One pass of the plain copy kernel over a known size: the reference
     point for FETCH_SIZE / WRITE_SIZE counter runs of this same command."""
     a, b = dev.alloc(nbytes), dev.alloc(nbytes)
+    for _ in range(3):  # first touch of both buffers and clocks up
+        dev.copy_kernel(b.ptr, a.ptr, nbytes)
     dev.sync()
+    reps = 10
     dev.timer_start()
-    dev.copy_kernel(b.ptr, a.ptr, nbytes)
-    ms = dev.timer_stop()
+    for _ in range(reps):
+        dev.copy_kernel(b.ptr, a.ptr, nbytes)
+    ms = dev.timer_stop() / reps
     a.free()
     b.free()
     return dict(bytes=nbytes, ms=ms, gbps=2 * nbytes / (ms / 1e3) / 1e9)

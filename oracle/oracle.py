@@ -194,7 +194,7 @@ class Oracle:
             L.sh_hidden = shared["hidden"]
             L.sh_gate_inp, L.sh_up, L.sh_gate, L.sh_down = [_ptr(b) for b in sb]
             L.sh_up_type = shared["up_type"]
-            L.sh_gate_type = shared["gate_type"]
+            L.sh_gate_type = shared.get("gate_type", shared["up_type"])
             L.sh_down_type = shared["down_type"]
         return L
 

@@ -88,8 +88,12 @@ int refdrv_moe_layer(const float* x_in, float* xb_out, float* x_out, int T, int 
     t.config.dim = dim;
     t.config.hidden_dim = hidden;
     t.config.n_layers = 1;
+    /* forward_runtime's attention holds one head's key row in a 512-float
+     * stack buffer (src/runtime.c:145): keep head_dim = dim / n_heads <= 512.
+     * With NULL attention weights the heads add exactly zero either way. */
     t.config.n_heads = 1;
-    t.config.n_kv_heads = 1;
+    while (dim / t.config.n_heads > 512 || dim % t.config.n_heads) t.config.n_heads++;
+    t.config.n_kv_heads = t.config.n_heads;
     t.config.vocab_size = 1;
     t.config.seq_len = 1;
     t.config.rope_freq_base = 10000.0f;

@@ -181,15 +181,23 @@ def test_dropin_matmul_q_fused(oracle, qtype):
          else synth.weights(61 + qtype, n, d, qtype))
     x = I.activations(62, 1, d)[0]
     out = np.zeros(n, np.float32)
-    for _ in range(2):  # second call reuses the registered device copy
-        lib.qr_matmul_q_fused(_fp(out), _fp(x), _fp(W), qtype, n, d, 8)
-        assert_bits_equal(out, oracle.matmul_q_fused(x, W, qtype, n, d), "drop-in")
-    lib.qr_matmul_q_fused(_fp(out), _fp(x), None, qtype, n, d, 8)
-    assert (out == 0).all()
+    # The registry keys on the host address, valid while the weights live (the
+    # reference's mmap lives until free_transformer): drop the copies of
+    # earlier tests, whose freed arrays may share W's address.
+    lib.qr_dropin_release_weights()
+    try:
+        for _ in range(2):  # second call reuses the registered device copy
+            lib.qr_matmul_q_fused(_fp(out), _fp(x), _fp(W), qtype, n, d, 8)
+            assert_bits_equal(out, oracle.matmul_q_fused(x, W, qtype, n, d), "drop-in")
+        lib.qr_matmul_q_fused(_fp(out), _fp(x), None, qtype, n, d, 8)
+        assert (out == 0).all()
+    finally:
+        lib.qr_dropin_release_weights()
 
 
 def test_dropin_quantize_and_ops(oracle):
     lib = Q.load()
+    lib.qr_dropin_release_weights()
     x = I.activations(70, 1, 4096)[0]
     y = np.zeros(4096 // 32 * 34, np.uint8)
     lib.qr_quantize_row_q8_0(_fp(x), _fp(y), 4096)

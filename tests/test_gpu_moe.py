@@ -217,6 +217,7 @@ def test_dropin_moe_block(dev, oracle):
     down_parts = [np.array(m["down"][e * sd:(e + 1) * sd]) for e in range(E)]
     down_p = (C.c_void_p * E)(*[a.ctypes.data for a in down_parts[::-1]][::-1])
     assert lib.qr_dropin_init(0, ORDER_SEQ) == 0
+    lib.qr_dropin_release_weights()  # host addresses of earlier tests may be reused
     x0 = I.activations(990, 1, dim)[0]
     xb = I.activations(991, 1, dim)[0]
     x = x0.copy()
@@ -229,3 +230,4 @@ def test_dropin_moe_block(dev, oracle):
                           m["up_type"], m["down"], m["down_type"])
     want, _, _ = oracle.moe_forward(x0[None, :], xb[None, :], L, order=ORDER_SEQ)
     assert_bits_equal(x, want[0], "drop-in MoE block")
+    lib.qr_dropin_release_weights()
