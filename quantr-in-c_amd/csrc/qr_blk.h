@@ -1,0 +1,230 @@
+// qr_blk.h -- the block-per-lane GEMV engine for the 16-byte aligned K-quant
+// formats (Q4_K 144-byte and Q5_K 176-byte super-blocks).
+//
+// A wave tile is RB = 64 / nb whole rows of nb super-blocks each; lane
+// l = r * nb + b holds super-block b of tile row r: its header and sub-blocks
+// arrive as 16-byte loads of one contiguous 144 / 176-byte range (neighbouring
+// lanes read neighbouring blocks, so a wave streams RB * row_bytes contiguous
+// bytes).  The lane decodes the block header once for its 8 units, takes the
+// int32 sum of each unit against the Q8_0 activation block in LDS with
+// v_dot4_i32_i8, and forms the unit's fp32 term in the reference's operation
+// order.  The row's terms must be added one after another from 0.0f, block 0
+// first: the lanes of a row do that as a chain of nb stages, stage k adding
+// block k's 8 terms onto the partial sum that lane k-1 handed over with a DPP
+// wave shift -- no LDS round trip.
+#pragma once
+
+#include "qr_gemv.h"
+
+namespace qr {
+
+constexpr int kBlkWaves = 4;  // waves per workgroup
+
+// Activation in LDS, per token: activation block u at byte
+// (u / 8) * kActRow + (u % 8) * kActBlk, holding [32 int8 | bd f32 | (float)bs
+// | bs i32 | pad].  kActRow = 8 blocks + 16 bytes, so the 8 blocks that the
+// lanes of one row read at the same time fall on different LDS banks.
+constexpr int kActBlk = 48;
+constexpr int kActRow = 8 * kActBlk + 16;
+
+__host__ __device__ inline size_t act_tok_bytes(int d) {
+  return (size_t)((d / 32 + 7) / 8) * kActRow;
+}
+__device__ inline int act_off(int u) { return (u >> 3) * kActRow + (u & 7) * kActBlk; }
+
+// DPP quad permutations (lane ^ 1, lane ^ 2) and the whole-wave shift by one
+// lane (lane l receives lane l-1; lane 0 receives `fill`).
+__device__ inline int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+__device__ inline int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
+__device__ inline float dpp_xor1f(float v) {
+  return __builtin_bit_cast(float, dpp_xor1(__builtin_bit_cast(int, v)));
+}
+__device__ inline float dpp_xor2f(float v) {
+  return __builtin_bit_cast(float, dpp_xor2(__builtin_bit_cast(int, v)));
+}
+__device__ inline float wave_shr1f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x138, 0xF, 0xF, false));
+}
+
+// quantize_row_q8_0 (src/quant.c:143-158) of nt rows x[t * xstride ..+ d)
+// into the LDS layout above, by the whole workgroup: four adjacent lanes per
+// 32-element block, 8 elements each; amax and the integer sum reduce across
+// the quad with DPP.  amax is a max (order-free); d = amax / 127 and 1 / d are
+// correctly rounded divisions; rintf rounds ties to even like lrintf; the
+// stored scale goes through the truncating fp16 routine.  PERM stores each
+// 8-element group as [x0 x2 x4 x6 | x1 x3 x5 x7] (the Q4_K nibble order).
+//
+// act_prefetch loads a thread's first 8 elements: issued before a kernel's
+// weight loads, the (small) activation read is not queued behind them.
+struct ActPre {
+  float v[8];
+};
+__device__ inline void act_load8(const float* __restrict__ x, size_t xstride, int nt, int d, int gi,
+                                 float (&v)[8]) {
+  const int per_tok = (d >> 5) * 4;
+  if (gi < nt * per_tok) {
+    const int t = gi / per_tok, g = gi - t * per_tok;
+    const float4* p = reinterpret_cast<const float4*>(x + (size_t)t * xstride + (size_t)g * 8);
+    const float4 u0 = p[0], u1 = p[1];
+    v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w;
+    v[4] = u1.x; v[5] = u1.y; v[6] = u1.z; v[7] = u1.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = 0.0f;
+  }
+}
+__device__ inline void act_prefetch(const float* __restrict__ x, size_t xstride, int nt, int d,
+                                    ActPre& pre) {
+  act_load8(x, xstride, nt, d, (int)threadIdx.x, pre.v);
+}
+
+template <bool PERM>
+__device__ inline void quantize_act_blk(const float* __restrict__ x, size_t xstride, int nt,
+                                        int d, uint8_t* lds, const ActPre& pre) {
+  const int nxb = d >> 5;
+  const int per_tok = nxb * 4;
+  const int total = nt * per_tok;
+  const size_t tokb = act_tok_bytes(d);
+  const int nthr = blockDim.x;  // a multiple of 64: quads never straddle waves
+  for (int base = 0; base < total; base += nthr) {
+    const int gi = base + (int)threadIdx.x;
+    const bool live = gi < total;
+    const int t = live ? gi / per_tok : 0;
+    const int g = live ? gi - t * per_tok : 0;
+    float v[8];
+    if (base == 0) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = pre.v[i];
+    } else {
+      act_load8(x, xstride, nt, d, gi, v);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float av = __builtin_fabsf(v[i]);
+      amax = av > amax ? av : amax;
+    }
+    float o = dpp_xor1f(amax);
+    amax = o > amax ? o : amax;
+    o = dpp_xor2f(amax);
+    amax = o > amax ? o : amax;
+    const float dd = amax / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    int q[8];
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      q[i] = (int)(int8_t)(int)__builtin_rintf(v[i] * id);
+      s += q[i];
+    }
+    s += dpp_xor1(s);
+    s += dpp_xor2(s);
+    if (live) {
+      uint32_t w0, w1;
+      if (PERM) {
+        w0 = pack4(q[0], q[2], q[4], q[6]);
+        w1 = pack4(q[1], q[3], q[5], q[7]);
+      } else {
+        w0 = pack4(q[0], q[1], q[2], q[3]);
+        w1 = pack4(q[4], q[5], q[6], q[7]);
+      }
+      const int blk = g >> 2, part = g & 3;
+      uint8_t* ab = lds + (size_t)t * tokb + act_off(blk);
+      *reinterpret_cast<uint2*>(ab + part * 8) = make_uint2(w0, w1);
+      if (part == 0) {
+        float* f = reinterpret_cast<float*>(ab + 32);
+        f[0] = qr_h2f(qr_f2h(dd));
+        f[1] = (float)s;
+        reinterpret_cast<int*>(ab + 40)[0] = s;
+      }
+    }
+  }
+}
+
+// One activation block read back from LDS.
+struct ActView {
+  uint32_t q[8];
+  float bd, bsf;
+  int bs;
+};
+__device__ inline ActView act_read(const uint8_t* ab) {
+  const uint4 a = *reinterpret_cast<const uint4*>(ab);
+  const uint4 b = *reinterpret_cast<const uint4*>(ab + 16);
+  const uint4 c = *reinterpret_cast<const uint4*>(ab + 32);
+  ActView v;
+  v.q[0] = a.x; v.q[1] = a.y; v.q[2] = a.z; v.q[3] = a.w;
+  v.q[4] = b.x; v.q[5] = b.y; v.q[6] = b.z; v.q[7] = b.w;
+  v.bd = __builtin_bit_cast(float, c.x);
+  v.bsf = __builtin_bit_cast(float, c.y);
+  v.bs = (int)c.z;
+  return v;
+}
+
+template <int TYPE>
+struct BlkFmt {
+  static constexpr int kBytes = TYPE == QR_T_Q4_K ? QR_Q4K_BYTES : QR_Q5K_BYTES;
+  static constexpr int kChunks = kBytes / 16;           // 9 or 11
+  static constexpr int kQs = TYPE == QR_T_Q4_K ? 1 : 3;  // first chunk of the nibbles
+};
+
+// The 8 unit terms (and int32 sums) of one super-block held in chunks c[]
+// against NT activation rows; `act` is the LDS activation, `b` the block's
+// index in its row (units 8b .. 8b+7).
+template <int TYPE, int NT>
+__device__ inline void blk_terms(const uint4* c, int b, const uint8_t* act, size_t tokb,
+                                 float (&terms)[NT][8], int32_t (&isums)[NT][8]) {
+  const uint4 hdr = c[0];
+  const float dd = qr_h2f(hdr.x & 0xFFFFu);
+  const float dm = qr_h2f(hdr.x >> 16);
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    const uint32_t sbyte = ((s < 4 ? hdr.y : hdr.z) >> (8 * (s & 3))) & 0xFFu;
+    const float sc = (float)(sbyte & 63u) * dd;
+    const float m = (float)(sbyte >> 6) * dm;
+    const uint4 qs = c[BlkFmt<TYPE>::kQs + s];
+    uint32_t qh = 0;
+    if constexpr (TYPE == QR_T_Q5_K) {
+      const uint4 h = c[1 + (s >> 2)];
+      qh = (s & 3) == 0 ? h.x : (s & 3) == 1 ? h.y : (s & 3) == 2 ? h.z : h.w;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const ActView a = act_read(act + (size_t)t * tokb + act_off(8 * b + s));
+      int isum;
+      if constexpr (TYPE == QR_T_Q4_K) isum = dot_q4_regs(qs, a.q);
+      else isum = dot_q5_regs(qs, qh, a.q);
+      terms[t][s] = (sc * (float)isum - m * a.bsf) * a.bd;
+      isums[t][s] = isum;
+    }
+  }
+}
+
+// Sequential row sums: lanes b = 0 .. nb-1 of each row hold the row's terms
+// block by block; returns, in the lane holding block nb-1, the sum from 0.0f
+// over block 0's 8 terms, then block 1's, ... (other lanes: unspecified).
+// Every lane of the wave must be active.
+template <int NT>
+__device__ inline void blk_chain(const float (&terms)[NT][8], int b, int nb, float (&out)[NT]) {
+  float p[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) p[t] = 0.0f;
+  for (int k = 0; k < nb; k++) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      float v = p[t];
+#pragma unroll
+      for (int s = 0; s < 8; s++) v += terms[t][s];
+      out[t] = v;
+    }
+    if (k + 1 < nb) {
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const float sh = wave_shr1f(out[t]);
+        p[t] = b == k + 1 ? sh : p[t];
+      }
+    }
+  }
+}
+
+}  // namespace qr

@@ -23,17 +23,14 @@
 
 // fp16 bits -> fp32 by exponent rebias (include/quant.h:53-66).  Half
 // subnormals keep exponent 0 and decode to mant * 2^-136, as in the reference.
+// Branch-free: exponent 31 ORs in 0x7F800000, which (the shifted exponent's
+// top three bits being clear) is the same as adding 0x70000000; exponents
+// 1..30 add the 0x38000000 rebias; exponent 0 adds nothing.
 __host__ __device__ inline float qr_h2f(uint32_t h) {
-  uint32_t w = (h & 0x7FFFu) << 13;
-  const uint32_t sign = (h & 0x8000u) << 16;
-  const uint32_t e = (h >> 10) & 0x1Fu;
-  if (e == 0x1Fu) {
-    w |= 0x7F800000u;
-  } else if (e != 0) {
-    w += 0x38000000u;
-  }
-  w |= sign;
-  return __builtin_bit_cast(float, w);
+  const uint32_t w = (h & 0x7FFFu) << 13;
+  const uint32_t e = h & 0x7C00u;
+  const uint32_t adj = e == 0x7C00u ? 0x70000000u : (e != 0 ? 0x38000000u : 0u);
+  return __builtin_bit_cast(float, (w + adj) | ((h & 0x8000u) << 16));
 }
 
 // Truncating fp32 -> fp16 bits (include/quant.h:68-77): exponents at or below

@@ -133,32 +133,38 @@ __device__ inline uint32_t lds_u32(const uint32_t* lds, int o) {
 
 // ---------------------------------------------------------------------------
 // Per-unit integer dots.  A unit is 32 weights against one Q8_0 activation
-// block; `xa` points at its 32 int8 values in LDS (4-byte aligned).
+// block: xv holds its 32 int8 values as 8 dwords (PERM order for Q4_K,
+// natural order otherwise).  The *_unit forms read them from LDS (`xa`,
+// 16-byte aligned).
 // ---------------------------------------------------------------------------
-
-// Q4_K sub-block: 16 bytes of nibbles against a PERM-layout activation.
-__device__ inline int dot_q4_unit(uint4 qs, const int8_t* xa) {
+__device__ inline void act8_from_lds(const int8_t* xa, uint32_t xv[8]) {
   const uint4 x0 = *reinterpret_cast<const uint4*>(xa);
   const uint4 x1 = *reinterpret_cast<const uint4*>(xa + 16);
-  int acc = 0;
-  acc = sdot4(qs.x & 0x0F0F0F0Fu, x0.x, acc);
-  acc = sdot4((qs.x >> 4) & 0x0F0F0F0Fu, x0.y, acc);
-  acc = sdot4(qs.y & 0x0F0F0F0Fu, x0.z, acc);
-  acc = sdot4((qs.y >> 4) & 0x0F0F0F0Fu, x0.w, acc);
-  acc = sdot4(qs.z & 0x0F0F0F0Fu, x1.x, acc);
-  acc = sdot4((qs.z >> 4) & 0x0F0F0F0Fu, x1.y, acc);
-  acc = sdot4(qs.w & 0x0F0F0F0Fu, x1.z, acc);
-  acc = sdot4((qs.w >> 4) & 0x0F0F0F0Fu, x1.w, acc);
-  return acc;
+  xv[0] = x0.x; xv[1] = x0.y; xv[2] = x0.z; xv[3] = x0.w;
+  xv[4] = x1.x; xv[5] = x1.y; xv[6] = x1.z; xv[7] = x1.w;
 }
 
-// 4-bit nibbles (+ optional high bits already spread per natural dword)
-// against a natural-order activation.  w holds 4 packed dwords (32 nibbles).
-__device__ inline int dot_nib_natural(uint4 qs, const uint32_t hb[8], const int8_t* xa) {
-  const uint4 x0 = *reinterpret_cast<const uint4*>(xa);
-  const uint4 x1 = *reinterpret_cast<const uint4*>(xa + 16);
+// Q4_K sub-block: 16 bytes of nibbles against a PERM-layout activation.
+__device__ inline int dot_q4_regs(uint4 qs, const uint32_t xv[8]) {
   const uint32_t wq[4] = {qs.x, qs.y, qs.z, qs.w};
-  const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  int acc = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    acc = sdot4(wq[k] & 0x0F0F0F0Fu, xv[2 * k], acc);
+    acc = sdot4((wq[k] >> 4) & 0x0F0F0F0Fu, xv[2 * k + 1], acc);
+  }
+  return acc;
+}
+__device__ inline int dot_q4_unit(uint4 qs, const int8_t* xa) {
+  uint32_t xv[8];
+  act8_from_lds(xa, xv);
+  return dot_q4_regs(qs, xv);
+}
+
+// 4-bit nibbles (+ high bits already spread per natural dword) against a
+// natural-order activation.  qs holds 4 packed dwords (32 nibbles).
+__device__ inline int dot_nib_regs(uint4 qs, const uint32_t hb[8], const uint32_t xv[8]) {
+  const uint32_t wq[4] = {qs.x, qs.y, qs.z, qs.w};
   int acc = 0;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
@@ -171,40 +177,47 @@ __device__ inline int dot_nib_natural(uint4 qs, const uint32_t hb[8], const int8
 }
 
 // Q5_K sub-block: nibbles plus the fifth-bit dword (bit l = element l).
-__device__ inline int dot_q5_unit(uint4 qs, uint32_t qh, const int8_t* xa) {
+__device__ inline int dot_q5_regs(uint4 qs, uint32_t qh, const uint32_t xv[8]) {
   uint32_t hb[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) hb[i] = spread4(qh >> (4 * i)) << 4;
-  return dot_nib_natural(qs, hb, xa);
+  return dot_nib_regs(qs, hb, xv);
+}
+__device__ inline int dot_q5_unit(uint4 qs, uint32_t qh, const int8_t* xa) {
+  uint32_t xv[8];
+  act8_from_lds(xa, xv);
+  return dot_q5_regs(qs, qh, xv);
 }
 
 // Q6_K sub-block: 16 bytes of low nibbles plus 8 bytes of 2-bit high pairs
 // (byte i holds elements 4i..4i+3).  Returns sum(q * x) with q in 0..63; the
 // caller subtracts 32 * bsum to get the reference's sum((q - 32) * x).
-__device__ inline int dot_q6_unit_raw(uint4 ql, uint2 qh, const int8_t* xa) {
+__device__ inline int dot_q6_regs_raw(uint4 ql, uint2 qh, const uint32_t xv[8]) {
   uint32_t hb[8];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     hb[i] = spread2x4((qh.x >> (8 * i)) & 0xFFu) << 4;
     hb[4 + i] = spread2x4((qh.y >> (8 * i)) & 0xFFu) << 4;
   }
-  return dot_nib_natural(ql, hb, xa);
+  return dot_nib_regs(ql, hb, xv);
+}
+__device__ inline int dot_q6_unit_raw(uint4 ql, uint2 qh, const int8_t* xa) {
+  uint32_t xv[8];
+  act8_from_lds(xa, xv);
+  return dot_q6_regs_raw(ql, qh, xv);
 }
 
 // Q8_0 block: 8 dwords of int8 weights against a natural-order activation.
-__device__ inline int dot_q8_unit(const uint32_t w[8], const int8_t* xa) {
-  const uint4 x0 = *reinterpret_cast<const uint4*>(xa);
-  const uint4 x1 = *reinterpret_cast<const uint4*>(xa + 16);
+__device__ inline int dot_q8_regs(const uint32_t w[8], const uint32_t xv[8]) {
   int acc = 0;
-  acc = sdot4(w[0], x0.x, acc);
-  acc = sdot4(w[1], x0.y, acc);
-  acc = sdot4(w[2], x0.z, acc);
-  acc = sdot4(w[3], x0.w, acc);
-  acc = sdot4(w[4], x1.x, acc);
-  acc = sdot4(w[5], x1.y, acc);
-  acc = sdot4(w[6], x1.z, acc);
-  acc = sdot4(w[7], x1.w, acc);
+#pragma unroll
+  for (int k = 0; k < 8; k++) acc = sdot4(w[k], xv[k], acc);
   return acc;
+}
+__device__ inline int dot_q8_unit(const uint32_t w[8], const int8_t* xa) {
+  uint32_t xv[8];
+  act8_from_lds(xa, xv);
+  return dot_q8_regs(w, xv);
 }
 
 // fp32 terms, in the reference's operation order (contraction is off).
@@ -283,6 +296,27 @@ struct UnitSrc {
 // Terms (and int32 sums) of unit u of one row for NT activation rows
 // tok0 .. tok0+NT-1.  `wrow` is the row in global memory (direct formats),
 // `row_lds` its byte offset in the staged tile (staged formats).
+// Q4_K / Q5_K unit u (super-block u/8, sub-block u%8) from registers: the
+// block's 16-byte header, the sub-block's 16 bytes of nibbles and, for Q5_K,
+// its fifth-bit dword.  Terms and int32 sums for activation rows
+// tok0 .. tok0+NT-1.
+template <int TYPE, int NT>
+__device__ inline void direct_unit_terms(uint4 hdr, uint4 qs, uint32_t qh, int u, const ActLds& act,
+                                         int nxb, int tok0, float* terms_out, int32_t* isum_out) {
+  const int s = u & 7;
+  const uint32_t sbyte = ((s < 4 ? hdr.y : hdr.z) >> (8 * (s & 3))) & 0xFFu;
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int a = (tok0 + t) * nxb + u;
+    const int8_t* xa = act.q + (size_t)a * 32;
+    int isum;
+    if constexpr (TYPE == QR_T_Q4_K) isum = dot_q4_unit(qs, xa);
+    else isum = dot_q5_unit(qs, qh, xa);
+    terms_out[t] = term_q45(hdr.x, sbyte, isum, act.bs[a], act.bd[a]);
+    isum_out[t] = isum;
+  }
+}
+
 template <int TYPE, int NT>
 __device__ inline void unit_terms(const uint8_t* __restrict__ wrow, int row_lds, int u,
                                   const UnitSrc& S, int tok0, float* terms_out,
@@ -292,7 +326,6 @@ __device__ inline void unit_terms(const uint8_t* __restrict__ wrow, int row_lds,
     const int b = u >> 3, s = u & 7;
     const uint8_t* blk = wrow + (size_t)b * (TYPE == QR_T_Q4_K ? QR_Q4K_BYTES : QR_Q5K_BYTES);
     const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
-    const uint32_t sbyte = ((s < 4 ? hdr.y : hdr.z) >> (8 * (s & 3))) & 0xFFu;
     uint4 qs;
     uint32_t qh = 0;
     if constexpr (TYPE == QR_T_Q4_K) {
@@ -301,16 +334,7 @@ __device__ inline void unit_terms(const uint8_t* __restrict__ wrow, int row_lds,
       qs = *reinterpret_cast<const uint4*>(blk + 48 + 16 * s);
       qh = *reinterpret_cast<const uint32_t*>(blk + 16 + 4 * s);
     }
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-      const int a = (tok0 + t) * nxb + u;
-      const int8_t* xa = S.act.q + (size_t)a * 32;
-      int isum;
-      if constexpr (TYPE == QR_T_Q4_K) isum = dot_q4_unit(qs, xa);
-      else isum = dot_q5_unit(qs, qh, xa);
-      terms_out[t] = term_q45(hdr.x, sbyte, isum, S.act.bs[a], S.act.bd[a]);
-      isum_out[t] = isum;
-    }
+    direct_unit_terms<TYPE, NT>(hdr, qs, qh, u, S.act, nxb, tok0, terms_out, isum_out);
   } else if constexpr (TYPE == QR_T_Q6_K) {
     const int b = u >> 3, s = u & 7;
     const int o = row_lds + b * QR_Q6K_BYTES;

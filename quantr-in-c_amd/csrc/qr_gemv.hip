@@ -12,8 +12,12 @@
 // of W).  Its waves sweep the rows' units 64 at a time (lane = unit), compute
 // each unit's int32 sum with v_dot4_i32_i8 and its fp32 term, and park the
 // term in LDS; then R*NT threads add their row's terms in unit order.
+#include <cstdlib>
+
 #include "qr_gemv.h"
 #include "qr_internal.h"
+#include "qr_stream.h"
+#include "qr_blk.h"
 
 namespace qr {
 
@@ -109,11 +113,209 @@ __global__ __launch_bounds__(kWg) void k_gemv(GemvArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// Streaming GEMV (the wave-tile engine of qr_stream.h): persistent
+// workgroups of independent waves, each walking tiles of RW rows with its
+// activation blocks in registers and the next tile's loads in flight while it
+// sums.  NS = 1 when every slot of a lane has the same unit (U divides 64).
+// ---------------------------------------------------------------------------
+template <int TYPE, int NT, int NS>
+__global__ __launch_bounds__(64 * kStreamWaves) void k_gemv_stream(GemvArgs g) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const TileShape sh = tile_shape(TYPE, g.d);
+  const StreamLds L = stream_lds(TYPE, NT, sh);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  uint8_t* slice = smem + (size_t)wave * L.slice;
+  float* terms = reinterpret_cast<float*>(slice);
+  uint32_t* stage = reinterpret_cast<uint32_t*>(slice + wave_terms_bytes(NT, sh));
+
+  const int ntiles = (g.n + sh.RW - 1) / sh.RW;
+  const int tstep = gridDim.x * kStreamWaves;
+  int tile = blockIdx.x * kStreamWaves + wave;
+  if (tile >= ntiles) return;  // no workgroup barriers below
+  const size_t total = (size_t)g.n * sh.rb;
+  const Slots sl = make_slots(sh.U, lane);
+  TileRegs<TYPE> R;
+  load_tile<TYPE>(g.W, total, tile * sh.RW, min(sh.RW, g.n - tile * sh.RW), sh, sl, lane, R);
+  LaneAct<NT, NS> A;
+  quantize_lane_act<TYPE, NT, NS>(g.X, (size_t)g.xstride, sl, sh.RW, A);
+  if (g.accb && tile == 0) {
+#pragma unroll
+    for (int i = 0; i < NS; i++)
+      if (sl.row[i] == 0)
+#pragma unroll
+        for (int t = 0; t < NT; t++) g.accb[t * sh.U + sl.u[i]] = A.a[t][i].bs;
+  }
+
+  for (;;) {
+    const int r0 = tile * sh.RW;
+    const int RWt = min(sh.RW, g.n - r0);
+    if constexpr (!IsDirect<TYPE>::value) {
+      stage_regs<TYPE>(R, stage, lane);
+      wave_lds_sync();
+    }
+    tile_terms<TYPE, NT, NS>(R, sl, RWt, r0, sh, A, stage, terms, g.acc, g.n);
+    wave_lds_sync();
+    const int next = tile + tstep;
+    if (next < ntiles)
+      load_tile<TYPE>(g.W, total, next * sh.RW, min(sh.RW, g.n - next * sh.RW), sh, sl, lane, R);
+    for (int i = lane; i < RWt * NT; i += 64) {
+      const int t = i / RWt, row = i - t * RWt;
+      g.Y[(size_t)t * g.ystride + r0 + row] = row_sum_seq(terms + (t * sh.RW + row) * sh.TS, sh.U);
+    }
+    if (next >= ntiles) break;
+    wave_lds_sync();
+    tile = next;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Block-per-lane GEMV for Q4_K / Q5_K (qr_blk.h): persistent workgroups that
+// quantize the activation into LDS once; each wave walks tiles of RB = 64/nb
+// rows with lane = super-block, the next tile's loads issued before the row
+// chain of the current one.
+// ---------------------------------------------------------------------------
+template <int TYPE, int NT>
+__global__ __launch_bounds__(64 * kBlkWaves) void k_gemv_blk(GemvArgs g) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int BB = BlkFmt<TYPE>::kBytes;
+  constexpr int NCH = BlkFmt<TYPE>::kChunks;
+  const int nb = g.d >> 8;
+  const int U = nb * 8;
+  const int RB = 64 / nb;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int rl = lane / nb, b = lane - rl * nb;
+  const bool lane_on = rl < RB;
+  const size_t rb = (size_t)nb * BB;
+  const size_t tokb = act_tok_bytes(g.d);
+  const int ntiles = (g.n + RB - 1) / RB;
+  const int tstep = gridDim.x * kBlkWaves;
+  int tile = blockIdx.x * kBlkWaves + wave;
+
+  // lane's block in tile t: W + t * tile_bytes + lane_off (rows of one tile
+  // are contiguous); the tile step is a constant byte stride
+  const size_t tile_bytes = (size_t)RB * rb;
+  const size_t lane_off = (size_t)rl * rb + (size_t)b * BB;
+  const size_t step_bytes = (size_t)tstep * tile_bytes;
+  const uint8_t* wp = g.W + (size_t)tile * tile_bytes + lane_off;
+  uint4 c[NCH];
+  auto load = [&](int t, const uint8_t* p) {
+    if (lane_on && t * RB + rl < g.n) {
+      const uint4* q = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+      for (int k = 0; k < NCH; k++) c[k] = q[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < NCH; k++) c[k] = make_uint4(0, 0, 0, 0);
+    }
+  };
+  // The activation is read and quantized before the first weight loads are
+  // issued: behind a whole grid's weight requests its read would wait in the
+  // same memory queues, and no wave can start before it is in LDS.
+  ActPre pre;
+  act_prefetch(g.X, (size_t)g.xstride, NT, g.d, pre);
+  quantize_act_blk<TYPE == QR_T_Q4_K>(g.X, (size_t)g.xstride, NT, g.d, smem, pre);
+  asm volatile("" ::: "memory");
+  if (tile < ntiles) load(tile, wp);
+  __syncthreads();
+  if (g.accb && blockIdx.x == 0) {
+    for (int i = threadIdx.x; i < NT * U; i += blockDim.x) {
+      const int t = i / U, u = i - t * U;
+      g.accb[i] = reinterpret_cast<const int*>(smem + (size_t)t * tokb + act_off(u) + 40)[0];
+    }
+  }
+  if (tile >= ntiles) return;  // no barriers below
+
+  for (;;) {
+    const int row = tile * RB + rl;
+    const bool live = lane_on && row < g.n;
+    float terms[NT][8];
+    int32_t isums[NT][8];
+    blk_terms<TYPE, NT>(c, b, smem, tokb, terms, isums);
+    if (g.acc && live) {
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int s = 0; s < 8; s++) g.acc[((size_t)t * g.n + row) * U + 8 * b + s] = isums[t][s];
+    }
+    const int next = tile + tstep;
+    wp += step_bytes;
+    if (next < ntiles) load(next, wp);
+    float y[NT];
+    blk_chain<NT>(terms, b, nb, y);
+    if (live && b == nb - 1) {
+#pragma unroll
+      for (int t = 0; t < NT; t++) g.Y[(size_t)t * g.ystride + row] = y[t];
+    }
+    if (next >= ntiles) break;
+    tile = next;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
 size_t gemv_lds_bytes(int type, int d, int nt, int R) {
   size_t a, b, c, e;
   return gemv_lds_layout(type, d, nt, R, &a, &b, &c, &e);
+}
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cu = 0;
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cu <= 0)
+      cu = 256;
+    cached[dev] = cu;
+  }
+  return cached[dev];
+}
+
+// Workgroups per CU of the streaming kernels (QR_STREAM_WG_PER_CU overrides,
+// 1..16, for tuning sweeps).
+static int stream_wg_per_cu() {
+  static int v = 0;
+  if (!v) {
+    const char* e = getenv("QR_STREAM_WG_PER_CU");
+    int x = e ? atoi(e) : 0;
+    v = (x >= 1 && x <= 16) ? x : 2;
+  }
+  return v;
+}
+
+bool gemv_stream_ok(int type, int d, int nt) {
+  if (type == QR_T_F32) return false;
+  const TileShape sh = tile_shape(type, d);
+  if (sh.RW < 1 || (d & 3)) return false;
+  // activation registers: nt blocks per distinct slot unit (1 when U divides
+  // 64, else kUPL); more than 4 blocks per lane spill
+  const int ns = (64 % sh.U == 0) ? 1 : kUPL;
+  if (nt * ns > 4) return false;
+  return stream_lds(type, nt, sh).total <= 64 * 1024;
+}
+
+template <int TYPE, int NT>
+static hipError_t launch_stream_t(const GemvArgs& a, hipStream_t st) {
+  const TileShape sh = tile_shape(TYPE, a.d);
+  const size_t lds = stream_lds(TYPE, NT, sh).total;
+  const int ntiles = (a.n + sh.RW - 1) / sh.RW;
+  const int want = (ntiles + kStreamWaves - 1) / kStreamWaves;
+  const int cap = device_cus() * stream_wg_per_cu();
+  const int grid = want < cap ? want : cap;
+  if (grid <= 0) return hipSuccess;
+  if (64 % sh.U == 0) {
+    hipLaunchKernelGGL((k_gemv_stream<TYPE, NT, 1>), dim3(grid), dim3(64 * kStreamWaves), lds, st, a);
+  } else {
+    if constexpr (NT == 1)
+      hipLaunchKernelGGL((k_gemv_stream<TYPE, 1, kUPL>), dim3(grid), dim3(64 * kStreamWaves), lds,
+                         st, a);
+    else
+      return hipErrorInvalidValue;  // excluded by gemv_stream_ok
+  }
+  return hipGetLastError();
 }
 
 // Rows per workgroup: enough workgroups to cover the 256 CUs several times,
@@ -139,14 +341,46 @@ static hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+bool gemv_blk_ok(int type, int d, int nt) {
+  if (type != QR_T_Q4_K && type != QR_T_Q5_K) return false;
+  const int nb = d >> 8;
+  if (nb < 1 || nb > 64 || (d & 3) || nt > 2) return false;  // more tokens: register spills
+  return (size_t)nt * act_tok_bytes(d) <= 64 * 1024;
+}
+
+template <int TYPE, int NT>
+static hipError_t launch_blk_t(const GemvArgs& a, hipStream_t st) {
+  const int nb = a.d >> 8;
+  const int RB = 64 / nb;
+  const size_t lds = (size_t)NT * act_tok_bytes(a.d);
+  const int ntiles = (a.n + RB - 1) / RB;
+  const int want = (ntiles + kBlkWaves - 1) / kBlkWaves;
+  const int cap = device_cus() * stream_wg_per_cu();
+  const int grid = want < cap ? want : cap;
+  if (grid <= 0) return hipSuccess;
+  hipLaunchKernelGGL((k_gemv_blk<TYPE, NT>), dim3(grid), dim3(64 * kBlkWaves), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int TYPE, int NT>
+static hipError_t launch_any_t(const GemvArgs& a, hipStream_t st) {
+  if constexpr ((TYPE == QR_T_Q4_K || TYPE == QR_T_Q5_K) && NT <= 2) {
+    if (gemv_blk_ok(TYPE, a.d, NT)) return launch_blk_t<TYPE, NT>(a, st);
+  }
+  if constexpr (NT <= 4) {
+    if (gemv_stream_ok(TYPE, a.d, NT)) return launch_stream_t<TYPE, NT>(a, st);
+  }
+  return launch_t<TYPE, NT>(a, st);
+}
+
 template <int TYPE>
 static hipError_t launch_nt(const GemvArgs& a, int nt, hipStream_t st) {
   switch (nt) {
-    case 1: return launch_t<TYPE, 1>(a, st);
-    case 2: return launch_t<TYPE, 2>(a, st);
-    case 3: return launch_t<TYPE, 3>(a, st);
-    case 4: return launch_t<TYPE, 4>(a, st);
-    case 8: return launch_t<TYPE, 8>(a, st);
+    case 1: return launch_any_t<TYPE, 1>(a, st);
+    case 2: return launch_any_t<TYPE, 2>(a, st);
+    case 3: return launch_any_t<TYPE, 3>(a, st);
+    case 4: return launch_any_t<TYPE, 4>(a, st);
+    case 8: return launch_any_t<TYPE, 8>(a, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -12,6 +12,9 @@ namespace qr {
 
 // qr_gemv.hip
 size_t gemv_lds_bytes(int type, int d, int nt, int R);
+bool gemv_stream_ok(int type, int d, int nt);
+bool gemv_blk_ok(int type, int d, int nt);
+int device_cus();
 int gemv_rows_per_wg(int type, int n, int d, int nt);
 hipError_t gemv_launch(int type, const void* W, const float* X, float* Y, int n, int d, int nt,
                        int xstride, int ystride, int32_t* acc, int32_t* accb, hipStream_t st);

@@ -298,7 +298,8 @@ int qr_gemv_ex(qr_ctx* c, uint32_t type, const void* w, const float* x, int xstr
   if (!aligned(x, 16) || (nt > 1 && (xstride & 3)))
     return fail(QR_ERR_INVALID, "qr_gemv: x must be 16-byte aligned (and xstride a multiple of 4)");
   const int R = qr::gemv_rows_per_wg((int)type, n, d, nt);
-  if (qr::gemv_lds_bytes((int)type, d, nt, R) > 64 * 1024)
+  if (!qr::gemv_blk_ok((int)type, d, nt) && !qr::gemv_stream_ok((int)type, d, nt) &&
+      qr::gemv_lds_bytes((int)type, d, nt, R) > 64 * 1024)
     return fail(QR_ERR_UNSUPPORTED, "qr_gemv: d=%d nt=%d exceeds the LDS budget", d, nt);
   QR_HIP(qr::gemv_launch((int)type, w, x, y, n, d, nt, xstride, ystride, acc, accb, c->stream),
          "k_gemv");
