@@ -467,9 +467,119 @@ __global__ __launch_bounds__(256) void k_gemv_f32(const float* __restrict__ W,
   }
 }
 
+// LDS-staged variant: a workgroup copies RPW weight rows into LDS with one
+// round trip of 128-bit loads, then LANES x RPW x TPW threads run the chains
+// out of LDS (row stride RS floats, RS = 8 mod 32, so the RPW rows' chains
+// read distinct banks), the activation read through the cache with the next
+// 8 loads in flight.
+template <int LANES>
+__global__ __launch_bounds__(256) void k_gemv_f32_lds(const float* __restrict__ W,
+                                                      const float* __restrict__ X,
+                                                      float* __restrict__ Y, int n, int d, int nt,
+                                                      int xstride, int ystride, int RPW, int RS) {
+  extern __shared__ __align__(16) float sw[];
+  const int TPW = 256 / (LANES * RPW);
+  const int r0 = blockIdx.x * RPW;
+  const int t0 = blockIdx.y * TPW;
+  const int nr = min(RPW, n - r0);
+  // stage rows r0 .. r0+nr-1
+  if ((d & 3) == 0 && ((reinterpret_cast<uintptr_t>(W) & 15) == 0)) {
+    const int d4 = d >> 2;
+    for (int i = threadIdx.x; i < nr * d4; i += blockDim.x) {
+      const int rr = i / d4, j4 = i - rr * d4;
+      const float4 v = reinterpret_cast<const float4*>(W + (size_t)(r0 + rr) * d)[j4];
+      *reinterpret_cast<float4*>(sw + rr * RS + 4 * j4) = v;
+    }
+  } else {
+    for (int i = threadIdx.x; i < nr * d; i += blockDim.x) {
+      const int rr = i / d, j = i - rr * d;
+      sw[rr * RS + j] = W[(size_t)(r0 + rr) * d + j];
+    }
+  }
+  __syncthreads();
+  const int k = threadIdx.x % LANES;
+  const int rr = (threadIdx.x / LANES) % RPW;
+  const int tt = threadIdx.x / (LANES * RPW);
+  const bool live = rr < nr && t0 + tt < nt;
+  const float* w = sw + rr * RS;
+  const float* x = X + (size_t)(live ? t0 + tt : 0) * xstride;
+  if constexpr (LANES == 1) {
+    if (!live) return;  // no barriers below
+    float s = 0.0f;
+    int j = 0;
+    for (; j + 8 <= d; j += 8) {
+      float xv[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) xv[q] = x[j + q];
+#pragma unroll
+      for (int q = 0; q < 8; q++) s += w[j + q] * xv[q];
+    }
+    for (; j < d; j++) s += w[j] * x[j];
+    Y[(size_t)(t0 + tt) * ystride + r0 + rr] = s;
+  } else {
+    const int dm = d - d % LANES;
+    float acc = 0.0f;
+    if (live) {
+      int j = k;
+      for (; j + 7 * LANES < dm; j += 8 * LANES) {
+        float xv[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) xv[q] = x[j + q * LANES];
+#pragma unroll
+        for (int q = 0; q < 8; q++) acc = __builtin_fmaf(w[j + q * LANES], xv[q], acc);
+      }
+      for (; j < dm; j += LANES) acc = __builtin_fmaf(w[j], x[j], acc);
+    }
+    float v[LANES];
+    const int base = (int)(threadIdx.x & 63) - k;
+#pragma unroll
+    for (int i = 0; i < LANES; i++) v[i] = __shfl(acc, base + i);
+    if (!live || k != 0) return;
+    float s = 0.0f;
+    if constexpr (LANES == 8) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) s += v[i];
+    } else {
+      float t8[8], t4[4];
+#pragma unroll
+      for (int i = 0; i < 8; i++) t8[i] = v[8 + i] + v[i];
+#pragma unroll
+      for (int i = 0; i < 4; i++) t4[i] = t8[4 + i] + t8[i];
+      const float a02 = t4[0] + t4[2];
+      const float a13 = t4[1] + t4[3];
+      s += a02 + a13;
+    }
+    for (int j = dm; j < d; j++) s += w[j] * x[j];
+    Y[(size_t)(t0 + tt) * ystride + r0 + rr] = s;
+  }
+}
+
+template <int LANES>
+static hipError_t launch_f32_lds(const float* W, const float* X, float* Y, int n, int d, int nt,
+                                 int xstride, int ystride, hipStream_t st) {
+  const int RS = ((d + 31) & ~31) + 8;
+  int RPW = 4;
+  while (RPW > 1 && (size_t)RPW * RS * 4 > 64 * 1024) RPW >>= 1;
+  if ((size_t)RPW * RS * 4 > 64 * 1024) return hipErrorInvalidValue;
+  const int TPW = 256 / (LANES * RPW);
+  dim3 grid((n + RPW - 1) / RPW, (nt + TPW - 1) / TPW);
+  hipLaunchKernelGGL(k_gemv_f32_lds<LANES>, grid, dim3(256), (size_t)RPW * RS * 4, st, W, X, Y, n,
+                     d, nt, xstride, ystride, RPW, RS);
+  return hipGetLastError();
+}
+
 hipError_t gemv_f32_launch(int order, const float* W, const float* X, float* Y, int n, int d,
                            int nt, int xstride, int ystride, hipStream_t st) {
   const int lanes = order == QR_ORDER_SEQ ? 1 : order == QR_ORDER_AVX2 ? 8 : 16;
+  if (n <= 0 || nt <= 0) return hipSuccess;
+  // rows that fit LDS go through the staged kernel
+  if ((size_t)(((d + 31) & ~31) + 8) * 4 <= 64 * 1024) {
+    switch (lanes) {
+      case 1: return launch_f32_lds<1>(W, X, Y, n, d, nt, xstride, ystride, st);
+      case 8: return launch_f32_lds<8>(W, X, Y, n, d, nt, xstride, ystride, st);
+      default: return launch_f32_lds<16>(W, X, Y, n, d, nt, xstride, ystride, st);
+    }
+  }
   const long total = (long)n * nt * lanes;
   const int threads = 256;
   const long grid = (total + threads - 1) / threads;

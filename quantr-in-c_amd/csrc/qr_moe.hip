@@ -78,81 +78,153 @@ void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s) 
 }
 
 // ---------------------------------------------------------------------------
-// Router: softmax + top-K + renormalisation, one wave per token.
+// Router: softmax + top-K + renormalisation, one wave per token, no
+// workgroup barriers (each wave owns its LDS row).
 // ---------------------------------------------------------------------------
 constexpr int kRouteWaves = 4;
+
+// (value, index) candidate order of the reference's argmax scan: a larger
+// value wins; equal values go to the lower index; index -1 (nothing yet)
+// loses to any real candidate.
+__device__ inline bool cand_better(float ov, int oi, float v, int i) {
+  return ov > v || (ov == v && oi >= 0 && (i < 0 || oi < i));
+}
+template <int CTRL>
+__device__ inline void cand_step(float& v, int& i) {
+  const float ov = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                 0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+  const int oi = __builtin_amdgcn_update_dpp(-1, i, CTRL, 0xF, 0xF, false);
+  if (cand_better(ov, oi, v, i)) {
+    v = ov;
+    i = oi;
+  }
+}
+// Best candidate of the wave, returned in every lane: butterflies inside each
+// 16-lane row (DPP quad xor 1, xor 2, half-row mirror, row mirror), then the
+// four row winners read with readlane and combined in row order.
+__device__ inline void wave_best(float& v, int& i) {
+  cand_step<0xB1>(v, i);
+  cand_step<0x4E>(v, i);
+  cand_step<0x141>(v, i);
+  cand_step<0x140>(v, i);
+  float bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  int bi = __builtin_amdgcn_readlane(i, 0);
+#pragma unroll
+  for (int r = 1; r < 4; r++) {
+    const float ov =
+        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * r));
+    const int oi = __builtin_amdgcn_readlane(i, 16 * r);
+    if (cand_better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  v = bv;
+  i = bi;
+}
+__device__ inline float wave_max(float v) {
+  auto step = [&](float o) { v = o > v ? o : v; };
+  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+  float m = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+#pragma unroll
+  for (int r = 1; r < 4; r++) {
+    const float o = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * r));
+    m = o > m ? o : m;
+  }
+  return m;
+}
+
+__device__ inline void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 __global__ __launch_bounds__(64 * kRouteWaves) void k_route_topk(const float* __restrict__ logits,
                                                                   int T, int E, int K,
                                                                   float* __restrict__ probs,
                                                                   int32_t* __restrict__ idx,
                                                                   float* __restrict__ wts) {
-  __shared__ float P[kRouteWaves][256];
-  __shared__ float Wk[kRouteWaves][16];
-  __shared__ float Inv[kRouteWaves];
+  __shared__ __align__(16) float P[kRouteWaves][256];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x * kRouteWaves + wave;
-  const bool live = t < T;  // uniform per wave; every thread reaches every barrier
-  const float* lg = logits + (size_t)(live ? t : 0) * E;
+  if (t >= T) return;  // whole wave; no workgroup barriers below
+  const float* lg = logits + (size_t)t * E;
   float* pw = P[wave];
 
-  // max: seeded with x[0], strictly greater wins (src/kernels.c:192-197)
-  float mx = live ? lg[0] : 0.0f;
+  // max: seeded with x[0], strictly greater wins (src/kernels.c:192-197);
+  // a max, so the lane split does not change it
+  float mx = lg[0];
   for (int e = lane; e < E; e += 64) {
-    const float v = live ? lg[e] : 0.0f;
+    const float v = lg[e];
     if (v > mx) mx = v;
   }
-  for (int o = 32; o > 0; o >>= 1) {
-    const float v = __shfl_xor(mx, o);
-    if (v > mx) mx = v;
-  }
-  for (int e = lane; e < E; e += 64) pw[e] = live ? qr_expf(lg[e] - mx) : 0.0f;
-  __syncthreads();
+  mx = wave_max(mx);
+  for (int e = lane; e < E; e += 64) pw[e] = qr_expf(lg[e] - mx);
+  wave_lds_fence();
+  // sequential sum, e ascending (src/kernels.c:198-202), in lane 0
+  float inv = 0.0f;
   if (lane == 0) {
-    float sum = 0.0f;  // sequential, e ascending (src/kernels.c:198-202)
-    for (int e = 0; e < E; e++) sum += pw[e];
-    Inv[wave] = 1.0f / sum;
+    float sum = 0.0f;
+    int e = 0;
+    for (; e + 16 <= E; e += 16) {
+      float4 q[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) q[k] = *reinterpret_cast<const float4*>(pw + e + 4 * k);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        sum += q[k].x;
+        sum += q[k].y;
+        sum += q[k].z;
+        sum += q[k].w;
+      }
+    }
+    for (; e < E; e++) sum += pw[e];
+    inv = 1.0f / sum;
   }
-  __syncthreads();
-  const float inv = Inv[wave];
-  for (int e = lane; e < E; e += 64) {
-    const float v = pw[e] * inv;
-    pw[e] = v;
-    if (live && probs) probs[(size_t)t * E + e] = v;
+  inv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv), 0));
+  // each lane keeps its own probabilities (e = lane, lane + 64, ...) in
+  // registers for the top-K passes
+  float pv[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int e = lane + 64 * q;
+    pv[q] = -1e9f;
+    if (e < E) {
+      const float v = pw[e] * inv;
+      pv[q] = v;
+      if (probs) probs[(size_t)t * E + e] = v;
+    }
   }
-  __syncthreads();
 
   // K argmax passes (src/runtime.c:210-222): the winner is the lowest index
   // holding the maximum value; values must beat -1e9f.
+  float wsel[16];
+  int isel[16];
   for (int k = 0; k < K; k++) {
     float bv = kMask;
     int bi = -1;
-    for (int e = lane; e < E; e += 64) {
-      const float v = pw[e];
-      if (v > bv) {
-        bv = v;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int e = lane + 64 * q;
+      if (e < E && pv[q] > bv) {
+        bv = pv[q];
         bi = e;
       }
     }
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
-      if (ov > bv || (ov == bv && oi >= 0 && (bi < 0 || oi < bi))) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if (lane == 0) {
-      Wk[wave][k] = bv;
-      if (live) idx[(size_t)t * K + k] = bi;
-    }
-    if (bi >= 0 && (bi & 63) == lane) pw[bi] = kMask;
-    __syncthreads();
+    wave_best(bv, bi);
+    wsel[k] = bv;
+    isel[k] = bi;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      if (bi == lane + 64 * q) pv[q] = kMask;
   }
-  if (lane == 0 && live) {
+  if (lane == 0) {
     float wsum = 0.0f;  // src/runtime.c:224-230
-    for (int k = 0; k < K; k++) wsum += Wk[wave][k];
-    for (int k = 0; k < K; k++) wts[(size_t)t * K + k] = Wk[wave][k] / wsum;
+    for (int k = 0; k < K; k++) wsum += wsel[k];
+    for (int k = 0; k < K; k++) {
+      idx[(size_t)t * K + k] = isel[k];
+      wts[(size_t)t * K + k] = wsel[k] / wsum;
+    }
   }
 }
 
