@@ -38,6 +38,8 @@ struct MoeScratch {
   float* hbs;         // [T][sh_hidden]  shared expert
   float* ysh;         // [T][dim]        shared expert output
   float* sgl;         // [T]             shared expert gate logit
+  uint8_t* xq;        // [T][dim/32] quantized activation records (MFMA path)
+  uint8_t* hq;        // [T*K][hidden/32] quantized hb records (MFMA path)
 };
 size_t moe_scratch_bytes(const qr_moe_layer* L, int T);
 void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s);
@@ -50,5 +52,15 @@ hipError_t moe_dispatch_launch(const int32_t* idx, int T, int K, int E, int tile
 hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, int T, int order,
                               const MoeScratch& s, hipStream_t st);
 hipError_t softmax_launch(float* x, int rows, int n, hipStream_t st);
+
+// qr_moe_mfma.hip
+bool mfma_type_ok(int type);
+hipError_t quant_rows_launch(const float* x, int xstride, int nrows, int cols, bool perm,
+                             uint8_t* out, hipStream_t st);
+hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const uint8_t* W2,
+                              size_t slice, int E, int K, int rows, int cols, const uint8_t* XQ,
+                              int x_by_token, const int32_t* offsets, const int32_t* perm,
+                              const int32_t* tiles, float* Y, int ystride, int items,
+                              hipStream_t st);
 
 }  // namespace qr

@@ -24,6 +24,8 @@
 //   k_down_combine1  T == 1: all K down projections of the token plus the
 //                    slot-order combine (and the shared expert) in one pass.
 //   k_combine        T > 1: slot-order gather-combine.
+#include <cstdlib>
+
 #include "qr_gemv.h"
 #include "qr_internal.h"
 
@@ -50,6 +52,8 @@ size_t moe_scratch_bytes(const qr_moe_layer* L, int T) {
   b += a256((size_t)T * (sh ? sh : 1) * 4);
   b += a256((size_t)T * L->dim * 4);
   b += a256((size_t)T * 4);
+  b += a256((size_t)T * (L->dim / 32) * 48);
+  b += a256(P * (size_t)(L->hidden / 32) * 48);
   return b;
 }
 
@@ -75,6 +79,8 @@ void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s) 
   s->hbs = reinterpret_cast<float*>(take((size_t)T * (sh ? sh : 1) * 4));
   s->ysh = reinterpret_cast<float*>(take((size_t)T * L->dim * 4));
   s->sgl = reinterpret_cast<float*>(take((size_t)T * 4));
+  s->xq = take((size_t)T * (L->dim / 32) * 48);
+  s->hq = take(P * (size_t)(L->hidden / 32) * 48);
 }
 
 // ---------------------------------------------------------------------------
@@ -746,6 +752,19 @@ __global__ __launch_bounds__(256) void k_combine(float* __restrict__ x, const fl
 // ---------------------------------------------------------------------------
 // The layer.
 // ---------------------------------------------------------------------------
+// Average pairs per expert from which the grouped products use MFMA
+// (QR_MFMA_MIN_PAIRS overrides, for tuning sweeps).
+static int mfma_min_pairs() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("QR_MFMA_MIN_PAIRS");
+    const int x = e ? atoi(e) : 0;
+    v = x > 0 ? x : 4;
+  }
+  return v;
+}
+#define kMfmaPairsPerExpert mfma_min_pairs()
+
 static int pick_tile(int P, int E) {
   const double avg = (double)P / E;
   return avg >= 6 ? 8 : avg >= 3 ? 4 : avg >= 1.5 ? 2 : 1;
@@ -836,6 +855,26 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
     return down1_launch((int)L->down_type, dn, st);
   }
 
+  // Many pairs per expert: grouped products on int8 MFMA (qr_moe_mfma.hip).
+  if (P >= kMfmaPairsPerExpert * E && mfma_type_ok((int)L->up_type) &&
+      mfma_type_ok((int)L->down_type)) {
+    constexpr int kTile = 32;  // pairs per MFMA work item
+    e = moe_dispatch_launch(s.idx, T, K, E, kTile, s.counts, s.offsets, s.tiles, s.perm, s.inv, st);
+    if (e != hipSuccess) return e;
+    const int items = (P + kTile - 1) / kTile + E;  // >= sum_e ceil(count_e / kTile)
+    e = quant_rows_launch(xb, L->dim, T, L->dim, L->up_type != QR_T_Q8_0, s.xq, st);
+    if (e != hipSuccess) return e;
+    e = expert_mfma_launch((int)L->up_type, true, static_cast<const uint8_t*>(L->up),
+                           static_cast<const uint8_t*>(L->gate), su, E, K, L->hidden, L->dim, s.xq,
+                           1, s.offsets, s.perm, s.tiles, s.hb, L->hidden, items, st);
+    if (e != hipSuccess) return e;
+    e = quant_rows_launch(s.hb, L->hidden, P, L->hidden, L->down_type != QR_T_Q8_0, s.hq, st);
+    if (e != hipSuccess) return e;
+    e = expert_mfma_launch((int)L->down_type, false, static_cast<const uint8_t*>(L->down), nullptr,
+                           sd, E, K, L->dim, L->hidden, s.hq, 0, s.offsets, s.perm, s.tiles, s.y,
+                           L->dim, items, st);
+    if (e != hipSuccess) return e;
+  } else {
   const int nt = pick_tile(P, E);
   e = moe_dispatch_launch(s.idx, T, K, E, nt, s.counts, s.offsets, s.tiles, s.perm, s.inv, st);
   if (e != hipSuccess) return e;
@@ -857,6 +896,7 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
   dn.x_by_token = 0;
   e = expert_launch((int)L->down_type, false, dn, nt, items, st);
   if (e != hipSuccess) return e;
+  }
   if (sh) {
     e = shared_expert(L, xb, T, s, st);
     if (e != hipSuccess) return e;
