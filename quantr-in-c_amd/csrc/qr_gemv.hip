@@ -484,11 +484,27 @@ __global__ __launch_bounds__(256) void k_gemv_f32_lds(const float* __restrict__ 
   const int nr = min(RPW, n - r0);
   // stage rows r0 .. r0+nr-1
   if ((d & 3) == 0 && ((reinterpret_cast<uintptr_t>(W) & 15) == 0)) {
+    // each thread's 8 loads of a batch are in flight before its LDS stores
     const int d4 = d >> 2;
-    for (int i = threadIdx.x; i < nr * d4; i += blockDim.x) {
-      const int rr = i / d4, j4 = i - rr * d4;
-      const float4 v = reinterpret_cast<const float4*>(W + (size_t)(r0 + rr) * d)[j4];
-      *reinterpret_cast<float4*>(sw + rr * RS + 4 * j4) = v;
+    const int total = nr * d4;
+    for (int base = 0; base < total; base += 8 * (int)blockDim.x) {
+      float4 v0, v1, v2, v3, v4, v5, v6, v7;
+      float4* v[8] = {&v0, &v1, &v2, &v3, &v4, &v5, &v6, &v7};
+#pragma unroll
+      for (int b = 0; b < 8; b++) {
+        const int i = base + b * (int)blockDim.x + (int)threadIdx.x;
+        const int ic = i < total ? i : 0;
+        const int rr = ic / d4, j4 = ic - rr * d4;
+        *v[b] = reinterpret_cast<const float4*>(W + (size_t)(r0 + rr) * d)[j4];
+      }
+#pragma unroll
+      for (int b = 0; b < 8; b++) {
+        const int i = base + b * (int)blockDim.x + (int)threadIdx.x;
+        if (i < total) {
+          const int rr = i / d4, j4 = i - rr * d4;
+          *reinterpret_cast<float4*>(sw + rr * RS + 4 * j4) = *v[b];
+        }
+      }
     }
   } else {
     for (int i = threadIdx.x; i < nr * d; i += blockDim.x) {

@@ -40,18 +40,30 @@ struct MoeScratch {
   float* sgl;         // [T]             shared expert gate logit
   uint8_t* xq;        // [T][dim/32] quantized activation records (MFMA path)
   uint8_t* hq;        // [T*K][hidden/32] quantized hb records (MFMA path)
+  unsigned* counters_route;  // [T] zeroed once; the fused router leaves them zero
 };
+size_t moe_counter_bytes(int T);
 size_t moe_scratch_bytes(const qr_moe_layer* L, int T);
 void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s);
 hipError_t moe_route_launch(const qr_moe_layer* L, const float* xb, int T, int order,
                             float* logits, float* probs, int32_t* idx, float* wts,
-                            hipStream_t st);
+                            hipStream_t st, unsigned* counters = nullptr);
 hipError_t moe_dispatch_launch(const int32_t* idx, int T, int K, int E, int tile, int32_t* counts,
                                int32_t* offsets, int32_t* tiles, int32_t* perm, int32_t* inv,
                                hipStream_t st);
 hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, int T, int order,
                               const MoeScratch& s, hipStream_t st);
 hipError_t softmax_launch(float* x, int rows, int n, hipStream_t st);
+
+// qr_moe_t1.hip
+bool gateup1_ok(int type, int dim);
+hipError_t gateup1_launch(int type, const void* up, const void* gate, size_t slice, int dim,
+                          int hidden, int E, int K, const float* xb, const int32_t* idx, float* hb,
+                          hipStream_t st);
+bool down1v2_ok(int type, int K, int hidden);
+hipError_t down1v2_launch(int type, const void* down, size_t slice, int dim, int hidden, int E,
+                          int K, const float* hb, const int32_t* idx, const float* wts, float* x,
+                          const float* ysh, const float* sgl, hipStream_t st);
 
 // qr_moe_mfma.hip
 bool mfma_type_ok(int type);

@@ -57,6 +57,9 @@ size_t moe_scratch_bytes(const qr_moe_layer* L, int T) {
   return b;
 }
 
+size_t moe_counter_bytes(int T) { return a256((size_t)(T + 1) * 4);
+}
+
 void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s) {
   const size_t E = L->n_experts, K = L->n_used, P = (size_t)T * K;
   uint8_t* p = static_cast<uint8_t*>(base);
@@ -145,18 +148,12 @@ __device__ inline float wave_max(float v) {
 
 __device__ inline void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-__global__ __launch_bounds__(64 * kRouteWaves) void k_route_topk(const float* __restrict__ logits,
-                                                                  int T, int E, int K,
-                                                                  float* __restrict__ probs,
-                                                                  int32_t* __restrict__ idx,
-                                                                  float* __restrict__ wts) {
-  __shared__ __align__(16) float P[kRouteWaves][256];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int t = blockIdx.x * kRouteWaves + wave;
-  if (t >= T) return;  // whole wave; no workgroup barriers below
-  const float* lg = logits + (size_t)t * E;
-  float* pw = P[wave];
-
+// softmax_ref + K argmax passes + renormalisation of one token's E logits
+// (src/kernels.c:191-207, src/runtime.c:208-230) by one wave; `pw` is a
+// wave-private LDS row of >= E floats.
+__device__ inline void route_one(const float* __restrict__ lg, int E, int K, float* pw, int lane,
+                                 float* __restrict__ probs, int32_t* __restrict__ idx,
+                                 float* __restrict__ wts) {
   // max: seeded with x[0], strictly greater wins (src/kernels.c:192-197);
   // a max, so the lane split does not change it
   float mx = lg[0];
@@ -198,15 +195,16 @@ __global__ __launch_bounds__(64 * kRouteWaves) void k_route_topk(const float* __
     if (e < E) {
       const float v = pw[e] * inv;
       pv[q] = v;
-      if (probs) probs[(size_t)t * E + e] = v;
+      if (probs) probs[e] = v;
     }
   }
-
   // K argmax passes (src/runtime.c:210-222): the winner is the lowest index
   // holding the maximum value; values must beat -1e9f.
   float wsel[16];
   int isel[16];
-  for (int k = 0; k < K; k++) {
+#pragma unroll
+  for (int k = 0; k < 16; k++) {  // K <= 16 (checked on the host); static indices
+    if (k >= K) break;
     float bv = kMask;
     int bi = -1;
 #pragma unroll
@@ -226,19 +224,255 @@ __global__ __launch_bounds__(64 * kRouteWaves) void k_route_topk(const float* __
   }
   if (lane == 0) {
     float wsum = 0.0f;  // src/runtime.c:224-230
-    for (int k = 0; k < K; k++) wsum += wsel[k];
-    for (int k = 0; k < K; k++) {
-      idx[(size_t)t * K + k] = isel[k];
-      wts[(size_t)t * K + k] = wsel[k] / wsum;
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+      if (k < K) wsum += wsel[k];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k < K) {
+        idx[k] = isel[k];
+        wts[k] = wsel[k] / wsum;
+      }
     }
   }
 }
 
+__global__ __launch_bounds__(64 * kRouteWaves) void k_route_topk(const float* __restrict__ logits,
+                                                                  int T, int E, int K,
+                                                                  float* __restrict__ probs,
+                                                                  int32_t* __restrict__ idx,
+                                                                  float* __restrict__ wts) {
+  __shared__ __align__(16) float P[kRouteWaves][256];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * kRouteWaves + wave;
+  if (t >= T) return;  // whole wave; no workgroup barriers below
+  route_one(logits + (size_t)t * E, E, K, P[wave], lane, probs ? probs + (size_t)t * E : nullptr,
+            idx + (size_t)t * K, wts + (size_t)t * K);
+}
+
+// Copy nr router rows (W + (r0 + q) d, to slot q) and ntk token rows
+// (X + (t0 + q) d, to slot RPW + q) of d floats into LDS slots of stride RS
+// floats, the whole workgroup; every thread's 128-bit loads of a batch are in
+// flight before its LDS stores.
+__device__ inline void stage_router_rows(float* sm, int RS, int RPW, const float* W, int r0,
+                                         int nr, const float* X, int t0, int ntk, int d) {
+  constexpr int kBatch = 8;
+  const int d4 = d >> 2;
+  const int total = (nr + ntk) * d4;
+  for (int base = 0; base < total; base += kBatch * (int)blockDim.x) {
+    float4 v0, v1, v2, v3, v4, v5, v6, v7;
+    float4* v[kBatch] = {&v0, &v1, &v2, &v3, &v4, &v5, &v6, &v7};
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+      const int i = base + b * (int)blockDim.x + (int)threadIdx.x;
+      const int ic = i < total ? i : 0;
+      const int q = ic / d4, j4 = ic - q * d4;
+      const float* src = q < nr ? W + (size_t)(r0 + q) * d : X + (size_t)(t0 + q - nr) * d;
+      *v[b] = reinterpret_cast<const float4*>(src)[j4];
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+      const int i = base + b * (int)blockDim.x + (int)threadIdx.x;
+      if (i < total) {
+        const int q = i / d4, j4 = i - q * d4;
+        const int slot = q < nr ? q : RPW + q - nr;
+        *reinterpret_cast<float4*>(sm + slot * RS + 4 * j4) = *v[b];
+      }
+    }
+  }
+}
+
+// FMA chain over j = k, k + LANES, ... < dm out of LDS, 16 steps' operands
+// read before their FMAs.
+template <int LANES>
+__device__ inline float lds_chain(const float* w, const float* x, int k, int dm) {
+  float acc = 0.0f;
+  int j = k;
+  for (; j + 15 * LANES < dm; j += 16 * LANES) {
+    float wv[16], xv[16];
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+      wv[q] = w[j + q * LANES];
+      xv[q] = x[j + q * LANES];
+    }
+#pragma unroll
+    for (int q = 0; q < 16; q++) acc = __builtin_fmaf(wv[q], xv[q], acc);
+  }
+  for (; j < dm; j += LANES) acc = __builtin_fmaf(w[j], x[j], acc);
+  return acc;
+}
+
+// Sequential mul-then-add over j < d out of LDS (matmul_ref order), 16 steps'
+// operands read before their adds.
+__device__ inline float lds_seq(const float* w, const float* x, int d) {
+  float s = 0.0f;
+  int j = 0;
+  for (; j + 16 <= d; j += 16) {
+    float wv[16], xv[16];
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+      wv[q] = w[j + q];
+      xv[q] = x[j + q];
+    }
+#pragma unroll
+    for (int q = 0; q < 16; q++) s += wv[q] * xv[q];
+  }
+  for (; j < d; j++) s += w[j] * x[j];
+  return s;
+}
+
+// Fused router for small T: a workgroup stages RPW router rows and TPW
+// tokens in LDS (row stride RS floats, RS = 8 mod 32), runs one thread per
+// (token, row, chain) in the reference build's accumulation order and writes
+// the logits; the last workgroup of each token block to finish (a device-
+// scope counter, reset by that workgroup) then routes the block's tokens,
+// one wave per token.
+template <int LANES>
+__global__ __launch_bounds__(256) void k_router_fused(const float* __restrict__ W,
+                                                      const float* __restrict__ X, int E, int d,
+                                                      int T, int K, int RPW, int TPW, int RS,
+                                                      float* __restrict__ logits,
+                                                      float* __restrict__ probs,
+                                                      int32_t* __restrict__ idx,
+                                                      float* __restrict__ wts,
+                                                      unsigned* __restrict__ counters) {
+  extern __shared__ __align__(16) float sm[];
+  __shared__ int is_last;
+  float* sw = sm;
+  float* sx = sm + RPW * RS;
+  const int r0 = blockIdx.x * RPW;
+  const int t0 = blockIdx.y * TPW;
+  const int nr = min(RPW, E - r0);
+  const int ntk = min(TPW, T - t0);
+  const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(W) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+  // staged row q < nr is router row r0 + q at slot q; q >= nr is token
+  // t0 + q - nr at slot RPW + q - nr (the token rows start at sx even when the
+  // last row block is short)
+  if (vec) {
+    stage_router_rows(sm, RS, RPW, W, r0, nr, X, t0, ntk, d);
+  } else {
+    for (int i = threadIdx.x; i < (nr + ntk) * d; i += blockDim.x) {
+      const int q = i / d, j = i - q * d;
+      const int slot = q < nr ? q : RPW + q - nr;
+      sm[slot * RS + j] = q < nr ? W[(size_t)(r0 + q) * d + j] : X[(size_t)(t0 + q - nr) * d + j];
+    }
+  }
+  __syncthreads();
+  {
+    const int k = threadIdx.x % LANES;
+    const int rr = (threadIdx.x / LANES) % RPW;
+    const int tt = threadIdx.x / (LANES * RPW);
+    const bool live = rr < nr && tt < ntk;
+    const float* w = sw + rr * RS;
+    const float* x = sx + (live ? tt : 0) * RS;
+    if constexpr (LANES == 1) {
+      if (live) {
+        const float s = lds_seq(w, x, d);
+        __hip_atomic_store(logits + (size_t)(t0 + tt) * E + r0 + rr, s, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    } else {
+      const int dm = d - d % LANES;
+      const float acc = live ? lds_chain<LANES>(w, x, k, dm) : 0.0f;
+      float v[LANES];
+      const int base = (int)(threadIdx.x & 63) - k;
+#pragma unroll
+      for (int i = 0; i < LANES; i++) v[i] = __shfl(acc, base + i);
+      if (live && k == 0) {
+        float s = 0.0f;
+        if constexpr (LANES == 8) {
+#pragma unroll
+          for (int i = 0; i < 8; i++) s += v[i];
+        } else {
+          float t8[8], t4[4];
+#pragma unroll
+          for (int i = 0; i < 8; i++) t8[i] = v[8 + i] + v[i];
+#pragma unroll
+          for (int i = 0; i < 4; i++) t4[i] = t8[4 + i] + t8[i];
+          const float a02 = t4[0] + t4[2];
+          const float a13 = t4[1] + t4[3];
+          s += a02 + a13;
+        }
+        for (int j = dm; j < d; j++) s += w[j] * x[j];
+        __hip_atomic_store(logits + (size_t)(t0 + tt) * E + r0 + rr, s, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (!counters) return;  // logits only
+  // last workgroup of this token block?
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) is_last = atomicAdd(&counters[blockIdx.y], 1u) == gridDim.x - 1;
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  if (threadIdx.x == 0) counters[blockIdx.y] = 0u;  // every workgroup of the block has counted
+  // The logits come from other workgroups, possibly on other XCDs (each with
+  // its own L2): they were written and are read back with agent-scope
+  // atomics, into a wave-private LDS row.
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float* lgl = sm + 4 * 256 + wave * 256;
+  for (int tt = wave; tt < ntk; tt += (int)(blockDim.x >> 6)) {
+    const int t = t0 + tt;
+    for (int e = lane; e < E; e += 64)
+      lgl[e] = __hip_atomic_load(logits + (size_t)t * E + e, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+    wave_lds_fence();
+    route_one(lgl, E, K, sm + wave * 256, lane, probs ? probs + (size_t)t * E : nullptr,
+              idx + (size_t)t * K, wts + (size_t)t * K);
+    wave_lds_fence();
+  }
+}
+
+// Fused router for T <= kFusedRouteT: (RPW, TPW) keep LANES * RPW * TPW <= 256
+// chains and RPW + TPW staged rows within 64 KB of LDS.
+constexpr int kFusedRouteT = 16;
+
+template <int LANES>
+static hipError_t router_fused_t(const qr_moe_layer* L, const float* xb, int T, float* logits,
+                                 float* probs, int32_t* idx, float* wts, unsigned* counters,
+                                 hipStream_t st) {
+  const int d = L->dim, E = L->n_experts;
+  const int RS = ((d + 31) & ~31) + 8;
+  int TPW = T < 4 ? T : 4;
+  int RPW = 256 / (LANES * TPW);
+  if (RPW > 8) RPW = 8;
+  while ((RPW + TPW) * (size_t)RS * 4 > 64 * 1024 && RPW > 1) RPW--;
+  while ((RPW + TPW) * (size_t)RS * 4 > 64 * 1024 && TPW > 1) TPW--;
+  if ((RPW + TPW) * (size_t)RS * 4 > 64 * 1024) return hipErrorInvalidValue;
+  dim3 grid((E + RPW - 1) / RPW, (T + TPW - 1) / TPW);
+  hipLaunchKernelGGL(k_router_fused<LANES>, grid, dim3(256), (size_t)(RPW + TPW) * RS * 4, st,
+                     L->router, xb, E, d, T, L->n_used, RPW, TPW, RS, logits, probs, idx, wts,
+                     counters);
+  return hipGetLastError();
+}
+
+bool router_fused_ok(const qr_moe_layer* L, int T) {
+  (void)T;
+  const int RS = ((L->dim + 31) & ~31) + 8;
+  return (size_t)2 * RS * 4 <= 64 * 1024;
+}
+
 hipError_t moe_route_launch(const qr_moe_layer* L, const float* xb, int T, int order,
                             float* logits, float* probs, int32_t* idx, float* wts,
-                            hipStream_t st) {
+                            hipStream_t st, unsigned* counters) {
   const int E = L->n_experts;
-  hipError_t e = gemv_f32_launch(order, L->router, xb, logits, E, L->dim, T, L->dim, E, st);
+  hipError_t e;
+  if (T <= kFusedRouteT && router_fused_ok(L, T)) {
+    // small T: logits and routing in one launch; larger T: logits here,
+    // routing by k_route_topk below
+    unsigned* cnt = T <= kFusedRouteT ? counters : nullptr;
+    switch (order) {
+      case QR_ORDER_SEQ: e = router_fused_t<1>(L, xb, T, logits, probs, idx, wts, cnt, st); break;
+      case QR_ORDER_AVX2: e = router_fused_t<8>(L, xb, T, logits, probs, idx, wts, cnt, st); break;
+      default: e = router_fused_t<16>(L, xb, T, logits, probs, idx, wts, cnt, st); break;
+    }
+    if (e != hipSuccess || cnt) return e;
+  } else {
+    e = gemv_f32_launch(order, L->router, xb, logits, E, L->dim, T, L->dim, E, st);
+  }
   if (e != hipSuccess) return e;
   const int grid = (T + kRouteWaves - 1) / kRouteWaves;
   hipLaunchKernelGGL(k_route_topk, dim3(grid), dim3(64 * kRouteWaves), 0, st, logits, T, E,
@@ -759,7 +993,7 @@ static int mfma_min_pairs() {
   if (v < 0) {
     const char* e = getenv("QR_MFMA_MIN_PAIRS");
     const int x = e ? atoi(e) : 0;
-    v = x > 0 ? x : 4;
+    v = x > 0 ? x : 1;
   }
   return v;
 }
@@ -807,7 +1041,7 @@ static hipError_t shared_expert(const qr_moe_layer* L, const float* xb, int T, c
 hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, int T, int order,
                               const MoeScratch& s, hipStream_t st) {
   const int E = L->n_experts, K = L->n_used, P = T * K;
-  hipError_t e = moe_route_launch(L, xb, T, order, s.logits, nullptr, s.idx, s.wts, st);
+  hipError_t e = moe_route_launch(L, xb, T, order, s.logits, nullptr, s.idx, s.wts, st, s.counters_route);
   if (e != hipSuccess) return e;
   const bool sh = L->sh_hidden > 0;
   const size_t su = qr_wrow_bytes((int)L->up_type, L->dim) * (size_t)L->hidden;
@@ -832,13 +1066,21 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
   g.P = P;
 
   if (T == 1) {
-    g.mode = kModeSingle;
-    e = expert_launch((int)L->up_type, true, g, 1, K, st);
+    if (gateup1_ok((int)L->up_type, L->dim)) {
+      e = gateup1_launch((int)L->up_type, L->up, L->gate, su, L->dim, L->hidden, E, K, xb, s.idx,
+                         s.hb, st);
+    } else {
+      g.mode = kModeSingle;
+      e = expert_launch((int)L->up_type, true, g, 1, K, st);
+    }
     if (e != hipSuccess) return e;
     if (sh) {
       e = shared_expert(L, xb, T, s, st);
       if (e != hipSuccess) return e;
     }
+    if (down1v2_ok((int)L->down_type, K, L->hidden))
+      return down1v2_launch((int)L->down_type, L->down, sd, L->dim, L->hidden, E, K, s.hb, s.idx,
+                            s.wts, x, sh ? s.ysh : nullptr, s.sgl, st);
     DownArgs dn{};
     dn.W = static_cast<const uint8_t*>(L->down);
     dn.slice = sd;

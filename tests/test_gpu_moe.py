@@ -231,3 +231,24 @@ def test_dropin_moe_block(dev, oracle):
     want, _, _ = oracle.moe_forward(x0[None, :], xb[None, :], L, order=ORDER_SEQ)
     assert_bits_equal(x, want[0], "drop-in MoE block")
     lib.qr_dropin_release_weights()
+
+
+@pytest.mark.parametrize("ut,dt", [(Q.TYPE_Q4_K, Q.TYPE_Q4_K), (Q.TYPE_Q5_K, Q.TYPE_Q5_K),
+                                   (Q.TYPE_Q4_K, Q.TYPE_Q8_0), (Q.TYPE_Q8_0, Q.TYPE_Q6_K)])
+@pytest.mark.parametrize("T", [1, 5, 48])
+def test_moe_type_pairs(dev, oracle, ut, dt, T):
+    """Every expert weight-type pair through the one-token, grouped-GEMV and
+    grouped-MFMA paths (T = 1, 5, 48 with 20 experts top-6: 0.3, 1.5 and 14
+    pairs per expert), random block bytes; E = 20 is not a multiple of the
+    router rows a workgroup stages."""
+    dim, hidden, E, K = 512, 256, 20, 6
+    ue, de = I.BLOCK[ut][0], I.BLOCK[dt][0]
+    seed = 7000 + 100 * ut + dt
+    up = I.blocks(seed, ut, E * hidden * (dim // ue))
+    gate = I.blocks(seed + 1, ut, E * hidden * (dim // ue))
+    down = I.blocks(seed + 2, dt, E * dim * (hidden // de))
+    router = I.activations(seed + 3, E, dim, std=0.05)
+    layer = DevLayer(dev, dim, hidden, E, K, router, up, gate, down, ut, dt)
+    x = I.activations(seed + 4 + T, T, dim)
+    xb = I.activations(seed + 5 + T, T, dim)
+    check_moe(dev, oracle, layer, x, xb, ORDER_AVX2, "types %d/%d T=%d" % (ut, dt, T))
