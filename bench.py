@@ -86,16 +86,26 @@ def bench_gemv(dev, qtype, n, d, nt, steps, warmup, copies=16, seed=1):
     g = dev.capture(record)
     dev.graph_launch(g)  # one untimed replay
     dev.sync()
-    dev.timer_start()
-    dev.graph_launch(g)
-    ms = dev.timer_stop()
-    dev.sync()
+    ms = timed_replays(dev, g)
     dev.graph_destroy(g)
     wbuf.free()
     s = ms / 1e3 / steps
     return dict(ms_per_step=ms / steps, weight_gbps=wbytes / s / 1e9,
                 alg_bytes=gemv_alg_bytes(qtype, n, d, nt),
                 achieved_gbps=gemv_alg_bytes(qtype, n, d, nt) / s / 1e9)
+
+
+def timed_replays(dev, g, reps=5):
+    """Median over `reps` timed replays of graph g (HIP events on the launch
+    stream, synchronized before and after each replay)."""
+    t = []
+    for _ in range(reps):
+        dev.sync()
+        dev.timer_start()
+        dev.graph_launch(g)
+        t.append(dev.timer_stop())
+    dev.sync()
+    return float(np.median(t))
 
 
 def copy_calibration(dev, nbytes=512 << 20):
@@ -180,9 +190,7 @@ def bench_moe(dev, M, T, steps, warmup, nbatches=8, order=Q.ORDER_AVX2):
     g = dev.capture(lambda: [one(i) for i in range(steps)])
     dev.graph_launch(g)
     dev.sync()
-    dev.timer_start()
-    dev.graph_launch(g)
-    ms = dev.timer_stop()
+    ms = timed_replays(dev, g)
     dev.graph_destroy(g)
     s = ms / 1e3 / steps
     return dict(T=T, ms_per_step=ms / steps, tokens_per_s=T / s,

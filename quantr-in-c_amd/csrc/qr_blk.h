@@ -21,9 +21,18 @@ namespace qr {
 constexpr int kBlkWaves = 4;  // waves per workgroup
 
 // Activation in LDS, per token: activation block u at byte
-// (u / 8) * kActRow + (u % 8) * kActBlk, holding [32 int8 | bd f32 | (float)bs
-// | bs i32 | pad].  kActRow = 8 blocks + 16 bytes, so the 8 blocks that the
-// lanes of one row read at the same time fall on different LDS banks.
+// (u / 8) * kActRow + (u % 8) * kActBlk, 48 bytes:
+//   NIB layout (Q4_K):  [xh 16 B | xl 16 B | bd f32 | bsf f32 | c i32 | bs i32]
+//   NAT layout (Q5_K):  [32 int8 in element order | bd f32 | bsf f32 | - | bs i32]
+// bd = h2f(f2h(d)) of the block, bs its integer sum, bsf = (float)bs.  In the
+// NIB layout each int8 value x is split as x + 128 = 16 * xh + xl with xh, xl
+// in 0..15: xl is kept as an unsigned nibble, xh - 8 as a signed nibble (8 per
+// dword, element order, nibble k = bits 4k..4k+3), and c = 128 * sum(xh - 8).
+// Then for 4-bit weights q:  sum(q * x) = 16 * sum((q - 8) * (xh - 8))
+// + sum(q * xl) + c, two 8-nibble dot products per weight dword and no
+// unpacking of the weight nibbles (q - 8 is q ^ 8 as a signed nibble).
+// kActRow = 8 blocks + 16 bytes, so the 8 blocks that the lanes of one row
+// read at the same time fall on different LDS banks.
 constexpr int kActBlk = 48;
 constexpr int kActRow = 8 * kActBlk + 16;
 
@@ -79,9 +88,12 @@ __device__ inline void act_prefetch(const float* __restrict__ x, size_t xstride,
   act_load8(x, xstride, nt, d, (int)threadIdx.x, pre.v);
 }
 
-template <bool PERM>
+// xs (optional): the activation already staged in LDS, group gi's 8 floats
+// at xs + 8 gi (see stage_act_dma); then every pass reads from there.
+template <bool NIB>
 __device__ inline void quantize_act_blk(const float* __restrict__ x, size_t xstride, int nt,
-                                        int d, uint8_t* lds, const ActPre& pre) {
+                                        int d, uint8_t* lds, const ActPre& pre,
+                                        const float* xs = nullptr) {
   const int nxb = d >> 5;
   const int per_tok = nxb * 4;
   const int total = nt * per_tok;
@@ -93,7 +105,12 @@ __device__ inline void quantize_act_blk(const float* __restrict__ x, size_t xstr
     const int t = live ? gi / per_tok : 0;
     const int g = live ? gi - t * per_tok : 0;
     float v[8];
-    if (base == 0) {
+    if (xs) {
+      const float4* p = reinterpret_cast<const float4*>(xs + (size_t)(live ? gi : 0) * 8);
+      const float4 u0 = p[0], u1 = p[1];
+      v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w;
+      v[4] = u1.x; v[5] = u1.y; v[6] = u1.z; v[7] = u1.w;
+    } else if (base == 0) {
 #pragma unroll
       for (int i = 0; i < 8; i++) v[i] = pre.v[i];
     } else {
@@ -120,33 +137,122 @@ __device__ inline void quantize_act_blk(const float* __restrict__ x, size_t xstr
     }
     s += dpp_xor1(s);
     s += dpp_xor2(s);
-    if (live) {
-      uint32_t w0, w1;
-      if (PERM) {
-        w0 = pack4(q[0], q[2], q[4], q[6]);
-        w1 = pack4(q[1], q[3], q[5], q[7]);
-      } else {
-        w0 = pack4(q[0], q[1], q[2], q[3]);
-        w1 = pack4(q[4], q[5], q[6], q[7]);
+    const int blk = g >> 2, part = g & 3;
+    uint8_t* ab = lds + (size_t)t * tokb + act_off(blk);
+    if constexpr (NIB) {
+      uint32_t wh = 0, wl = 0;
+      int hs = 0;  // sum of (xh - 8) over the 8 elements
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t xb = (uint32_t)(q[i] + 128);  // 1..255
+        wh |= ((xb >> 4) ^ 8u) << (4 * i);
+        wl |= (xb & 15u) << (4 * i);
+        hs += (int)(xb >> 4) - 8;
       }
-      const int blk = g >> 2, part = g & 3;
-      uint8_t* ab = lds + (size_t)t * tokb + act_off(blk);
-      *reinterpret_cast<uint2*>(ab + part * 8) = make_uint2(w0, w1);
+      hs += dpp_xor1(hs);
+      hs += dpp_xor2(hs);
+      if (live) {
+        reinterpret_cast<uint32_t*>(ab)[part] = wh;
+        reinterpret_cast<uint32_t*>(ab + 16)[part] = wl;
+        if (part == 0) {
+          float* f = reinterpret_cast<float*>(ab + 32);
+          f[0] = qr_h2f(qr_f2h(dd));
+          f[1] = (float)s;
+          reinterpret_cast<int*>(ab + 40)[0] = 128 * hs;
+          reinterpret_cast<int*>(ab + 44)[0] = s;
+        }
+      }
+    } else if (live) {
+      *reinterpret_cast<uint2*>(ab + part * 8) =
+          make_uint2(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]));
       if (part == 0) {
         float* f = reinterpret_cast<float*>(ab + 32);
         f[0] = qr_h2f(qr_f2h(dd));
         f[1] = (float)s;
-        reinterpret_cast<int*>(ab + 40)[0] = s;
+        reinterpret_cast<int*>(ab + 44)[0] = s;
       }
     }
   }
 }
 
+// ---------------------------------------------------------------------------
+// Weight tiles through LDS.  A wave moves a tile's bytes from HBM into its LDS
+// slot with global_load_lds_dwordx4 (one instruction = 64 lanes x 16 bytes =
+// 1 KiB contiguous: fully coalesced, and no VGPRs held while in flight); each
+// lane then reads its own super-block back from the slot (a 144 / 176-byte
+// lane stride touches distinct banks within every 16 lanes).
+//
+// The DMA is issued from inline asm and waited for explicitly with the wave's
+// vmcnt: the compiler, which cannot tell the slots from the activation in
+// LDS, would otherwise wait for every DMA in flight before any LDS access.
+// Vector-memory loads complete in issue order, so "at most N operations in
+// flight" after a tile's DMA plus N later DMA operations means the tile has
+// landed; later stores only make such a wait stricter.  Every DMA instruction
+// is issued with all lanes active (lanes past the valid bytes reload the
+// tile's first 16 bytes into slot bytes nobody reads), so the count of DMA
+// operations per tile is exactly NCH.
+// ---------------------------------------------------------------------------
+template <int NCH>
+__device__ inline void tile_dma(const uint8_t* g, uint8_t* s, int valid, int lane) {
+  const uint32_t sbase =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)s);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot's earlier reads are done
+#pragma unroll
+  for (int k = 0; k < NCH; k++) {
+    const int off = k * 1024 + lane * 16;
+    const uint8_t* src = g + (off < valid ? off : 0);
+    asm volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %0, off"
+        :
+        : "v"(src), "s"(sbase + (uint32_t)(k * 1024))
+        : "memory", "m0");
+  }
+}
+
+// Stage the fp32 activation of nt tokens into LDS xs by DMA, laid out for
+// quantize_act_blk: 8-element group gi = t * (d / 8) + g at xs + 32 gi bytes.
+// A workgroup of 256 threads quantizes group gi = pass * 256 + thread, so wave
+// w stages the 2 KiB of groups its own threads read in each pass (2 DMA
+// instructions per pass; lanes past the last group reload group 0).  Returns
+// the number of DMA instructions issued (2 per pass).  Call with all 64 lanes.
+__device__ inline int stage_act_dma(const float* __restrict__ x, size_t xstride, int nt, int d,
+                                    uint8_t* xs, int wave, int lane) {
+  const int per_tok = d >> 3;
+  const int total = nt * per_tok;
+  const int passes = (total + 255) >> 8;
+  const uint32_t xbase =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)xs);
+  for (int p = 0; p < passes; p++) {
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int first = p * 256 + wave * 64 + k * 32;  // first group of this instruction
+      int gi = first + (lane >> 1);
+      gi = gi < total ? gi : 0;
+      const int t = gi / per_tok, g = gi - t * per_tok;
+      const float* src = x + (size_t)t * xstride + (size_t)g * 8 + 4 * (lane & 1);
+      asm volatile(
+          "s_mov_b32 m0, %1\n\t"
+          "global_load_lds_dwordx4 %0, off"
+          :
+          : "v"(src), "s"(xbase + (uint32_t)(first * 32))
+          : "memory", "m0");
+    }
+  }
+  return 2 * passes;
+}
+
+// Wait until at most N of the wave's vector memory operations are in flight.
+template <int N>
+__device__ inline void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // One activation block read back from LDS.
 struct ActView {
-  uint32_t q[8];
+  uint32_t q[8];  // NAT: 32 int8;  NIB: xh[0..3] = q[0..3], xl[0..3] = q[4..7]
   float bd, bsf;
-  int bs;
+  int c, bs;
 };
 __device__ inline ActView act_read(const uint8_t* ab) {
   const uint4 a = *reinterpret_cast<const uint4*>(ab);
@@ -157,8 +263,23 @@ __device__ inline ActView act_read(const uint8_t* ab) {
   v.q[4] = b.x; v.q[5] = b.y; v.q[6] = b.z; v.q[7] = b.w;
   v.bd = __builtin_bit_cast(float, c.x);
   v.bsf = __builtin_bit_cast(float, c.y);
-  v.bs = (int)c.z;
+  v.c = (int)c.z;
+  v.bs = (int)c.w;
   return v;
+}
+
+// sum(q * x) of one 32-element unit of 4-bit weights (4 dwords of 8 nibbles,
+// element order) against a NIB-layout activation block.
+__device__ inline int dot_q4_nib(uint4 qs, const ActView& a) {
+  int hi = __builtin_amdgcn_sdot8((int)(qs.x ^ 0x88888888u), (int)a.q[0], 0, false);
+  hi = __builtin_amdgcn_sdot8((int)(qs.y ^ 0x88888888u), (int)a.q[1], hi, false);
+  hi = __builtin_amdgcn_sdot8((int)(qs.z ^ 0x88888888u), (int)a.q[2], hi, false);
+  hi = __builtin_amdgcn_sdot8((int)(qs.w ^ 0x88888888u), (int)a.q[3], hi, false);
+  uint32_t lo = __builtin_amdgcn_udot8(qs.x, a.q[4], (uint32_t)a.c, false);
+  lo = __builtin_amdgcn_udot8(qs.y, a.q[5], lo, false);
+  lo = __builtin_amdgcn_udot8(qs.z, a.q[6], lo, false);
+  lo = __builtin_amdgcn_udot8(qs.w, a.q[7], lo, false);
+  return (int)((uint32_t)hi << 4) + (int)lo;
 }
 
 template <int TYPE>
@@ -166,22 +287,26 @@ struct BlkFmt {
   static constexpr int kBytes = TYPE == QR_T_Q4_K ? QR_Q4K_BYTES : QR_Q5K_BYTES;
   static constexpr int kChunks = kBytes / 16;           // 9 or 11
   static constexpr int kQs = TYPE == QR_T_Q4_K ? 1 : 3;  // first chunk of the nibbles
+  static constexpr bool kNib = TYPE == QR_T_Q4_K;        // activation layout
 };
 
 // The 8 unit terms (and int32 sums) of one super-block held in chunks c[]
 // against NT activation rows; `act` is the LDS activation, `b` the block's
-// index in its row (units 8b .. 8b+7).
+// index in its row (units 8b .. 8b+7).  Term of unit s, as src/quant.c:384-400:
+// (sc * (float)isum - m * (float)bsum) * bd with sc = (scale & 63) * d and
+// m = (scale >> 6) * dmin, every operation rounded once.
 template <int TYPE, int NT>
 __device__ inline void blk_terms(const uint4* c, int b, const uint8_t* act, size_t tokb,
                                  float (&terms)[NT][8], int32_t (&isums)[NT][8]) {
   const uint4 hdr = c[0];
   const float dd = qr_h2f(hdr.x & 0xFFFFu);
   const float dm = qr_h2f(hdr.x >> 16);
+  const uint32_t s6[2] = {hdr.y & 0x3F3F3F3Fu, hdr.z & 0x3F3F3F3Fu};
+  const uint32_t m2[2] = {(hdr.y >> 6) & 0x03030303u, (hdr.z >> 6) & 0x03030303u};
 #pragma unroll
   for (int s = 0; s < 8; s++) {
-    const uint32_t sbyte = ((s < 4 ? hdr.y : hdr.z) >> (8 * (s & 3))) & 0xFFu;
-    const float sc = (float)(sbyte & 63u) * dd;
-    const float m = (float)(sbyte >> 6) * dm;
+    const float sc = (float)((s6[s >> 2] >> (8 * (s & 3))) & 0xFFu) * dd;
+    const float m = (float)((m2[s >> 2] >> (8 * (s & 3))) & 0xFFu) * dm;
     const uint4 qs = c[BlkFmt<TYPE>::kQs + s];
     uint32_t qh = 0;
     if constexpr (TYPE == QR_T_Q5_K) {
@@ -192,7 +317,7 @@ __device__ inline void blk_terms(const uint4* c, int b, const uint8_t* act, size
     for (int t = 0; t < NT; t++) {
       const ActView a = act_read(act + (size_t)t * tokb + act_off(8 * b + s));
       int isum;
-      if constexpr (TYPE == QR_T_Q4_K) isum = dot_q4_regs(qs, a.q);
+      if constexpr (TYPE == QR_T_Q4_K) isum = dot_q4_nib(qs, a);
       else isum = dot_q5_regs(qs, qh, a.q);
       terms[t][s] = (sc * (float)isum - m * a.bsf) * a.bd;
       isums[t][s] = isum;
@@ -203,26 +328,27 @@ __device__ inline void blk_terms(const uint4* c, int b, const uint8_t* act, size
 // Sequential row sums: lanes b = 0 .. nb-1 of each row hold the row's terms
 // block by block; returns, in the lane holding block nb-1, the sum from 0.0f
 // over block 0's 8 terms, then block 1's, ... (other lanes: unspecified).
+// Stage k adds every lane's 8 terms onto the stage k-1 value of the lane
+// before it (a DPP wave shift); by induction lane k holds the exact prefix at
+// stage k, so no lane needs a select and the critical path is the nb*8 adds.
 // Every lane of the wave must be active.
 template <int NT>
 __device__ inline void blk_chain(const float (&terms)[NT][8], int b, int nb, float (&out)[NT]) {
-  float p[NT];
+  (void)b;
 #pragma unroll
-  for (int t = 0; t < NT; t++) p[t] = 0.0f;
-  for (int k = 0; k < nb; k++) {
+  for (int t = 0; t < NT; t++) {
+    float v = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; s++) v += terms[t][s];
+    out[t] = v;
+  }
+  for (int k = 1; k < nb; k++) {
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-      float v = p[t];
+      float v = wave_shr1f(out[t]);
 #pragma unroll
       for (int s = 0; s < 8; s++) v += terms[t][s];
       out[t] = v;
-    }
-    if (k + 1 < nb) {
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const float sh = wave_shr1f(out[t]);
-        p[t] = b == k + 1 ? sh : p[t];
-      }
     }
   }
 }

@@ -169,20 +169,40 @@ __global__ __launch_bounds__(64 * kStreamWaves) void k_gemv_stream(GemvArgs g) {
 }
 
 // ---------------------------------------------------------------------------
-// Block-per-lane GEMV for Q4_K / Q5_K (qr_blk.h): persistent workgroups that
-// quantize the activation into LDS once; each wave walks tiles of RB = 64/nb
-// rows with lane = super-block, the next tile's loads issued before the row
-// chain of the current one.
+// Block-per-lane GEMV for Q4_K / Q5_K (qr_blk.h): each wave walks tiles of
+// RB = 64/nb rows with lane = super-block.  A tile's bytes come into the
+// wave's LDS slot by DMA (coalesced 1 KiB instructions), D tiles in flight per
+// wave; the lane reads its block from the slot, and the slot is refilled with
+// the tile D steps ahead before the lane's terms are formed.
+//
+// Start-up: the activation's DMA into an LDS staging area goes first (XS),
+// then the first D tiles' DMA; each wave then waits only for its own part of
+// the activation (loads complete in issue order: at most NCH x tiles-issued
+// operations still in flight) and the workgroup quantizes it from LDS, while
+// the weight stream is already on its way.  Without staging (large
+// activations) the activation is loaded into registers before the tile DMA.
 // ---------------------------------------------------------------------------
-template <int TYPE, int NT>
+template <int TYPE>
+__host__ __device__ constexpr size_t blk_slot_bytes() {
+  return (size_t)64 * BlkFmt<TYPE>::kBytes;
+}
+// LDS staging of the activation: whole passes of 256 groups of 8 floats.
+__host__ __device__ inline size_t blk_xs_bytes(int d, int nt) {
+  return (size_t)((nt * (d >> 3) + 255) >> 8) * 8192;
+}
+constexpr size_t kXsMax = 16 * 1024;
+
+template <int TYPE, int NT, int D, bool XS>
 __global__ __launch_bounds__(64 * kBlkWaves) void k_gemv_blk(GemvArgs g) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int BB = BlkFmt<TYPE>::kBytes;
   constexpr int NCH = BlkFmt<TYPE>::kChunks;
+  constexpr size_t SB = blk_slot_bytes<TYPE>();
   const int nb = g.d >> 8;
   const int U = nb * 8;
   const int RB = 64 / nb;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // wave-uniform (scalar) tile indices
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int rl = lane / nb, b = lane - rl * nb;
   const bool lane_on = rl < RB;
   const size_t rb = (size_t)nb * BB;
@@ -190,64 +210,88 @@ __global__ __launch_bounds__(64 * kBlkWaves) void k_gemv_blk(GemvArgs g) {
   const int ntiles = (g.n + RB - 1) / RB;
   const int tstep = gridDim.x * kBlkWaves;
   int tile = blockIdx.x * kBlkWaves + wave;
-
-  // lane's block in tile t: W + t * tile_bytes + lane_off (rows of one tile
-  // are contiguous); the tile step is a constant byte stride
   const size_t tile_bytes = (size_t)RB * rb;
-  const size_t lane_off = (size_t)rl * rb + (size_t)b * BB;
-  const size_t step_bytes = (size_t)tstep * tile_bytes;
-  const uint8_t* wp = g.W + (size_t)tile * tile_bytes + lane_off;
-  uint4 c[NCH];
-  auto load = [&](int t, const uint8_t* p) {
-    if (lane_on && t * RB + rl < g.n) {
-      const uint4* q = reinterpret_cast<const uint4*>(p);
-#pragma unroll
-      for (int k = 0; k < NCH; k++) c[k] = q[k];
-    } else {
-#pragma unroll
-      for (int k = 0; k < NCH; k++) c[k] = make_uint4(0, 0, 0, 0);
+  const size_t xsb = XS ? blk_xs_bytes(g.d, NT) : 0;
+  float* xs = reinterpret_cast<float*>(smem);
+  uint8_t* act = smem + xsb;
+  uint8_t* slots = act + align16((size_t)NT * tokb) + (size_t)wave * D * SB;
+
+  auto dma = [&](int s, int t) {
+    if (t < ntiles) {
+      const int rows = min(RB, g.n - t * RB);
+      tile_dma<NCH>(g.W + (size_t)t * tile_bytes, slots + s * SB, rows * (int)rb, lane);
     }
   };
-  // The activation is read and quantized before the first weight loads are
-  // issued: behind a whole grid's weight requests its read would wait in the
-  // same memory queues, and no wave can start before it is in LDS.
   ActPre pre;
-  act_prefetch(g.X, (size_t)g.xstride, NT, g.d, pre);
-  quantize_act_blk<TYPE == QR_T_Q4_K>(g.X, (size_t)g.xstride, NT, g.d, smem, pre);
-  asm volatile("" ::: "memory");
-  if (tile < ntiles) load(tile, wp);
-  __syncthreads();
+  if constexpr (XS) {
+    stage_act_dma(g.X, (size_t)g.xstride, NT, g.d, smem, wave, lane);
+    int issued = 0;
+#pragma unroll
+    for (int s = 0; s < D; s++) {
+      issued += tile + s * tstep < ntiles;
+      dma(s, tile + s * tstep);
+    }
+    if (issued == 0) wait_vmcnt<0>();
+    else if (issued == 1) wait_vmcnt<NCH>();
+    else wait_vmcnt<2 * NCH>();
+    quantize_act_blk<BlkFmt<TYPE>::kNib>(g.X, (size_t)g.xstride, NT, g.d, act, pre, xs);
+  } else {
+    // the compiler's wait for these loads also covers the first tile's DMA
+    act_prefetch(g.X, (size_t)g.xstride, NT, g.d, pre);
+    dma(0, tile);
+    quantize_act_blk<BlkFmt<TYPE>::kNib>(g.X, (size_t)g.xstride, NT, g.d, act, pre);
+#pragma unroll
+    for (int s = 1; s < D; s++) dma(s, tile + s * tstep);
+  }
+  // LDS-only barrier: the tile DMA stays in flight across it
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
   if (g.accb && blockIdx.x == 0) {
     for (int i = threadIdx.x; i < NT * U; i += blockDim.x) {
       const int t = i / U, u = i - t * U;
-      g.accb[i] = reinterpret_cast<const int*>(smem + (size_t)t * tokb + act_off(u) + 40)[0];
+      g.accb[i] = reinterpret_cast<const int*>(act + (size_t)t * tokb + act_off(u) + 44)[0];
     }
   }
   if (tile >= ntiles) return;  // no barriers below
 
   for (;;) {
-    const int row = tile * RB + rl;
-    const bool live = lane_on && row < g.n;
-    float terms[NT][8];
-    int32_t isums[NT][8];
-    blk_terms<TYPE, NT>(c, b, smem, tokb, terms, isums);
-    if (g.acc && live) {
 #pragma unroll
-      for (int t = 0; t < NT; t++)
+    for (int s = 0; s < D; s++) {
+      const int cur = tile + s * tstep;
+      if (cur < ntiles) {
+        // the slot's tile is complete once no more than the later tiles'
+        // DMA (issued after it) is in flight
+        if (D == 2 && cur + tstep < ntiles) wait_vmcnt<NCH>();
+        else wait_vmcnt<0>();
+        uint4 c[NCH];
+        {
+          const uint4* q = reinterpret_cast<const uint4*>(slots + s * SB + (size_t)lane * BB);
 #pragma unroll
-        for (int s = 0; s < 8; s++) g.acc[((size_t)t * g.n + row) * U + 8 * b + s] = isums[t][s];
+          for (int k = 0; k < NCH; k++) c[k] = q[k];
+        }
+        dma(s, cur + D * tstep);
+        const int row = cur * RB + rl;
+        const bool live = lane_on && row < g.n;
+        float terms[NT][8];
+        int32_t isums[NT][8];
+        blk_terms<TYPE, NT>(c, b, act, tokb, terms, isums);
+        if (g.acc && live) {
+#pragma unroll
+          for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+              g.acc[((size_t)t * g.n + row) * U + 8 * b + q] = isums[t][q];
+        }
+        float y[NT];
+        blk_chain<NT>(terms, b, nb, y);
+        if (live && b == nb - 1) {
+#pragma unroll
+          for (int t = 0; t < NT; t++) g.Y[(size_t)t * g.ystride + row] = y[t];
+        }
+      }
     }
-    const int next = tile + tstep;
-    wp += step_bytes;
-    if (next < ntiles) load(next, wp);
-    float y[NT];
-    blk_chain<NT>(terms, b, nb, y);
-    if (live && b == nb - 1) {
-#pragma unroll
-      for (int t = 0; t < NT; t++) g.Y[(size_t)t * g.ystride + row] = y[t];
-    }
-    if (next >= ntiles) break;
-    tile = next;
+    tile += D * tstep;
+    if (tile >= ntiles) break;
   }
 }
 
@@ -341,25 +385,93 @@ static hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int TYPE>
+static size_t blk_lds_bytes(int d, int nt, int D, bool xs) {
+  return (xs ? blk_xs_bytes(d, nt) : 0) + align16((size_t)nt * act_tok_bytes(d)) +
+         (size_t)kBlkWaves * D * blk_slot_bytes<TYPE>();
+}
+static size_t blk_lds_bytes_t(int type, int d, int nt, int D, bool xs) {
+  return type == QR_T_Q4_K ? blk_lds_bytes<QR_T_Q4_K>(d, nt, D, xs)
+                           : blk_lds_bytes<QR_T_Q5_K>(d, nt, D, xs);
+}
+constexpr size_t kLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
+
 bool gemv_blk_ok(int type, int d, int nt) {
   if (type != QR_T_Q4_K && type != QR_T_Q5_K) return false;
   const int nb = d >> 8;
   if (nb < 1 || nb > 64 || (d & 3) || nt > 2) return false;  // more tokens: register spills
-  return (size_t)nt * act_tok_bytes(d) <= 64 * 1024;
+  return blk_lds_bytes_t(type, d, nt, 1, false) <= kLdsMax;
+}
+
+// Tuning knobs of the block-per-lane kernel for sweeps: QR_BLK_DEPTH (1 or 2
+// tiles in flight per wave) and QR_BLK_WG_PER_CU (1..16 workgroups per CU;
+// default: as many as fit in LDS, at most 4).
+static int env_knob(const char* name, int lo, int hi, int dflt) {
+  const char* e = getenv(name);
+  const int x = e ? atoi(e) : 0;
+  return (x >= lo && x <= hi) ? x : dflt;
+}
+static int blk_depth() {
+  static int v = 0;
+  if (!v) v = env_knob("QR_BLK_DEPTH", 1, 2, 1);
+  return v;
+}
+static int blk_wg_per_cu() {
+  static int v = -1;
+  if (v < 0) v = env_knob("QR_BLK_WG_PER_CU", 1, 16, 0);
+  return v;
+}
+
+// Opt a kernel into LDS beyond 64 KiB, once per device.
+static hipError_t lds_opt_in(const void* fn, bool* done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  if (!done[dev]) {
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
+    if (e != hipSuccess) return e;
+    done[dev] = true;
+  }
+  return hipSuccess;
+}
+
+template <int TYPE, int NT, int D, bool XS>
+static hipError_t launch_blk_d(const GemvArgs& a, int grid, size_t lds, hipStream_t st) {
+  static bool opted[64] = {false};
+  if (lds > 64 * 1024) {
+    hipError_t e = lds_opt_in((const void*)k_gemv_blk<TYPE, NT, D, XS>, opted);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((k_gemv_blk<TYPE, NT, D, XS>), dim3(grid), dim3(64 * kBlkWaves), lds, st, a);
+  return hipGetLastError();
 }
 
 template <int TYPE, int NT>
 static hipError_t launch_blk_t(const GemvArgs& a, hipStream_t st) {
   const int nb = a.d >> 8;
   const int RB = 64 / nb;
-  const size_t lds = (size_t)NT * act_tok_bytes(a.d);
+  int D = blk_depth();
+  const bool xs = blk_xs_bytes(a.d, NT) <= kXsMax;
+  if (blk_lds_bytes<TYPE>(a.d, NT, D, xs) > kLdsMax) D = 1;
+  const size_t lds = blk_lds_bytes<TYPE>(a.d, NT, D, xs);
+  if (lds > kLdsMax) return hipErrorInvalidValue;  // excluded by gemv_blk_ok
   const int ntiles = (a.n + RB - 1) / RB;
   const int want = (ntiles + kBlkWaves - 1) / kBlkWaves;
-  const int cap = device_cus() * stream_wg_per_cu();
+  int per_cu = blk_wg_per_cu();
+  if (per_cu == 0) {
+    per_cu = (int)(kLdsMax / lds);
+    per_cu = per_cu < 1 ? 1 : (per_cu > 4 ? 4 : per_cu);
+  }
+  const int cap = device_cus() * per_cu;
   const int grid = want < cap ? want : cap;
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((k_gemv_blk<TYPE, NT>), dim3(grid), dim3(64 * kBlkWaves), lds, st, a);
-  return hipGetLastError();
+  if (xs) {
+    if (D == 2) return launch_blk_d<TYPE, NT, 2, true>(a, grid, lds, st);
+    return launch_blk_d<TYPE, NT, 1, true>(a, grid, lds, st);
+  }
+  if (D == 2) return launch_blk_d<TYPE, NT, 2, false>(a, grid, lds, st);
+  return launch_blk_d<TYPE, NT, 1, false>(a, grid, lds, st);
 }
 
 template <int TYPE, int NT>

@@ -50,7 +50,7 @@ __global__ __launch_bounds__(64 * kBlkWaves) void k_gateup1(GateUp1Args a) {
   // activation first (see k_gemv_blk), then the weight stream
   ActPre pre;
   act_prefetch(a.xb, (size_t)a.dim, 1, a.dim, pre);
-  quantize_act_blk<TYPE == QR_T_Q4_K>(a.xb, (size_t)a.dim, 1, a.dim, smem, pre);
+  quantize_act_blk<BlkFmt<TYPE>::kNib>(a.xb, (size_t)a.dim, 1, a.dim, smem, pre);
   asm volatile("" ::: "memory");
   uint4 c[NCH];
   const int row = r0 + rl;
