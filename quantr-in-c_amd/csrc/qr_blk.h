@@ -192,23 +192,44 @@ __device__ inline void quantize_act_blk(const float* __restrict__ x, size_t xstr
 // tile's first 16 bytes into slot bytes nobody reads), so the count of DMA
 // operations per tile is exactly NCH.
 // ---------------------------------------------------------------------------
+
+// One global_load_lds_dwordx4: each lane's 16 bytes at src land at LDS byte
+// lds + 16 * lane (lds wave-uniform).  M0 carries the LDS address; the
+// compiler does not track M0 across inline asm, so the asm saves and restores
+// it around the instruction.
+__device__ inline void lds_dma16(const void* src, uint32_t lds) {
+  int save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(src), "s"(lds)
+      : "memory");
+}
+// The LDS byte address of a pointer into LDS, wave-uniform.
+__device__ inline uint32_t lds_u32addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)p);
+}
+
 template <int NCH>
 __device__ inline void tile_dma(const uint8_t* g, uint8_t* s, int valid, int lane) {
-  const uint32_t sbase =
-      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)s);
+  const uint32_t sbase = lds_u32addr(s);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot's earlier reads are done
 #pragma unroll
   for (int k = 0; k < NCH; k++) {
     const int off = k * 1024 + lane * 16;
-    const uint8_t* src = g + (off < valid ? off : 0);
-    asm volatile(
-        "s_mov_b32 m0, %1\n\t"
-        "global_load_lds_dwordx4 %0, off"
-        :
-        : "v"(src), "s"(sbase + (uint32_t)(k * 1024))
-        : "memory", "m0");
+    lds_dma16(g + (off < valid ? off : 0), sbase + (uint32_t)(k * 1024));
   }
 }
+
+// LDS staging of the activation: whole passes of 256 groups of 8 floats.
+__host__ __device__ inline size_t blk_xs_bytes(int d, int nt) {
+  return (size_t)((nt * (d >> 3) + 255) >> 8) * 8192;
+}
+constexpr size_t kXsMax = 16 * 1024;
 
 // Stage the fp32 activation of nt tokens into LDS xs by DMA, laid out for
 // quantize_act_blk: 8-element group gi = t * (d / 8) + g at xs + 32 gi bytes.
@@ -221,8 +242,7 @@ __device__ inline int stage_act_dma(const float* __restrict__ x, size_t xstride,
   const int per_tok = d >> 3;
   const int total = nt * per_tok;
   const int passes = (total + 255) >> 8;
-  const uint32_t xbase =
-      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)xs);
+  const uint32_t xbase = lds_u32addr(xs);
   for (int p = 0; p < passes; p++) {
 #pragma unroll
     for (int k = 0; k < 2; k++) {
@@ -230,13 +250,8 @@ __device__ inline int stage_act_dma(const float* __restrict__ x, size_t xstride,
       int gi = first + (lane >> 1);
       gi = gi < total ? gi : 0;
       const int t = gi / per_tok, g = gi - t * per_tok;
-      const float* src = x + (size_t)t * xstride + (size_t)g * 8 + 4 * (lane & 1);
-      asm volatile(
-          "s_mov_b32 m0, %1\n\t"
-          "global_load_lds_dwordx4 %0, off"
-          :
-          : "v"(src), "s"(xbase + (uint32_t)(first * 32))
-          : "memory", "m0");
+      lds_dma16(x + (size_t)t * xstride + (size_t)g * 8 + 4 * (lane & 1),
+                xbase + (uint32_t)(first * 32));
     }
   }
   return 2 * passes;

@@ -54,22 +54,25 @@ __host__ __device__ inline uint32_t qr_f2h(float f) {
 // glibc's x86-64 FMA build fuses the reduction r = x*N/ln2 - k and the cubic's
 // multiply-adds; so does this, and with that every float input gives glibc's
 // bits (an exhaustive CPU test compares all 2^32 inputs with the host libm).
+// 2^(i/32) for i < 32, correctly rounded, with the exponent bits of i/32
+// removed (the table of the published algorithm).
+constexpr uint64_t kExpTab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
 __host__ __device__ inline float qr_expf(float x) {
   constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
   constexpr double kShift = 0x1.8p+52;
   constexpr double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
   constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
   constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
-  constexpr uint64_t kTab[32] = {
-      0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
-      0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
-      0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
-      0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
-      0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
-      0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
-      0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-      0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
-  };
   const uint32_t ux = __builtin_bit_cast(uint32_t, x);
   const uint32_t abstop = (ux >> 20) & 0x7FFu;
   if (abstop >= 0x42Bu) {  // |x| >= 88, inf or nan
@@ -85,7 +88,7 @@ __host__ __device__ inline float qr_expf(float x) {
   kd -= kShift;
   // glibc's FMA build contracts z - kd into one fused operation
   const double r = __builtin_fma(kInvLn2N, xd, -kd);
-  const uint64_t t = kTab[ki % 32] + (ki << 47);
+  const uint64_t t = kExpTab[ki % 32] + (ki << 47);
   const double s = __builtin_bit_cast(double, t);
   const double p = __builtin_fma(kC0, r, kC1);
   const double r2 = r * r;
@@ -97,6 +100,62 @@ __host__ __device__ inline float qr_expf(float x) {
 
 // silu(x) = x / (1 + expf(-x)) (src/runtime.c:15-17).
 __host__ __device__ inline float qr_silu(float x) { return x / (1.0f + qr_expf(-x)); }
+
+// The same expf with its table in registers: lane i < 32 of a VGPR pair holds
+// kExpTab[i] and a lookup is a ds_bpermute.  A kernel loads the table once, at
+// its start next to its other first loads, instead of paying a dependent
+// memory round trip in every latency-critical expf.  qr_expf_w must be called
+// with every lane of the wave active (a permute reads nothing from inactive
+// lanes); its special cases are selects.
+struct ExpTab {
+  int lo, hi;
+};
+static __device__ const uint64_t kExpTabDev[32] = {
+    kExpTab[0],  kExpTab[1],  kExpTab[2],  kExpTab[3],  kExpTab[4],  kExpTab[5],  kExpTab[6],
+    kExpTab[7],  kExpTab[8],  kExpTab[9],  kExpTab[10], kExpTab[11], kExpTab[12], kExpTab[13],
+    kExpTab[14], kExpTab[15], kExpTab[16], kExpTab[17], kExpTab[18], kExpTab[19], kExpTab[20],
+    kExpTab[21], kExpTab[22], kExpTab[23], kExpTab[24], kExpTab[25], kExpTab[26], kExpTab[27],
+    kExpTab[28], kExpTab[29], kExpTab[30], kExpTab[31]};
+__device__ inline ExpTab qr_expf_tab() {
+  const uint64_t v = kExpTabDev[threadIdx.x & 31];
+  return ExpTab{(int)(uint32_t)v, (int)(uint32_t)(v >> 32)};
+}
+__device__ inline float qr_expf_w(float x, const ExpTab& T) {
+  constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
+  constexpr double kShift = 0x1.8p+52;
+  constexpr double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+  constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+  constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+  const uint32_t ux = __builtin_bit_cast(uint32_t, x);
+  const uint32_t abstop = (ux >> 20) & 0x7FFu;
+  const double xd = (double)x;
+  const double z = kInvLn2N * xd;
+  double kd = z + kShift;
+  const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+  kd -= kShift;
+  const double r = __builtin_fma(kInvLn2N, xd, -kd);
+  const int ti = (int)(ki & 31u) << 2;
+  const uint32_t tlo = (uint32_t)__builtin_amdgcn_ds_bpermute(ti, T.lo);
+  const uint32_t thi = (uint32_t)__builtin_amdgcn_ds_bpermute(ti, T.hi);
+  const uint64_t t = (((uint64_t)thi << 32) | tlo) + (ki << 47);
+  const double s = __builtin_bit_cast(double, t);
+  const double p = __builtin_fma(kC0, r, kC1);
+  const double r2 = r * r;
+  double y = __builtin_fma(kC2, r, 1.0);
+  y = __builtin_fma(p, r2, y);
+  y = y * s;
+  float res = (float)y;
+  if (abstop >= 0x42Bu) {  // |x| >= 88, inf or nan
+    if (ux == 0xFF800000u) res = 0.0f;                                        // -inf
+    else if (abstop >= 0x7F8u) res = x + x;                                   // +inf, nan
+    else if (x > 0x1.62e42ep6f) res = __builtin_bit_cast(float, 0x7F800000u);  // overflow
+    else if (x < -0x1.9fe368p6f) res = 0.0f;                                  // underflow
+  }
+  return res;
+}
+__device__ inline float qr_silu_w(float x, const ExpTab& T) {
+  return x / (1.0f + qr_expf_w(-x, T));
+}
 
 __host__ __device__ inline int qr_block_elems(int type) { return type == QR_T_Q8_0 ? 32 : 256; }
 __host__ __device__ inline int qr_block_bytes(int type) {

@@ -186,11 +186,6 @@ template <int TYPE>
 __host__ __device__ constexpr size_t blk_slot_bytes() {
   return (size_t)64 * BlkFmt<TYPE>::kBytes;
 }
-// LDS staging of the activation: whole passes of 256 groups of 8 floats.
-__host__ __device__ inline size_t blk_xs_bytes(int d, int nt) {
-  return (size_t)((nt * (d >> 3) + 255) >> 8) * 8192;
-}
-constexpr size_t kXsMax = 16 * 1024;
 
 template <int TYPE, int NT, int D, bool XS>
 __global__ __launch_bounds__(64 * kBlkWaves) void k_gemv_blk(GemvArgs g) {

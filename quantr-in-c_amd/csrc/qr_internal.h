@@ -56,11 +56,14 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
 hipError_t softmax_launch(float* x, int rows, int n, hipStream_t st);
 
 // qr_moe_t1.hip
-bool gateup1_ok(int type, int dim);
-hipError_t gateup1_launch(int type, const void* up, const void* gate, size_t slice, int dim,
-                          int hidden, int E, int K, const float* xb, const int32_t* idx, float* hb,
+bool router1_ok(int dim);
+hipError_t router1_launch(int order, const float* W, const float* xb, int E, int d, float* logits,
                           hipStream_t st);
-bool down1v2_ok(int type, int K, int hidden);
+bool gateup1_ok(int type, int dim, int E, int K);
+hipError_t gateup1_launch(int type, const void* up, const void* gate, size_t slice, int dim,
+                          int hidden, int E, int K, const float* xb, const float* logits,
+                          int32_t* idx, float* wts, float* hb, hipStream_t st);
+bool down1v2_ok(int type, int K, int dim, int hidden);
 hipError_t down1v2_launch(int type, const void* down, size_t slice, int dim, int hidden, int E,
                           int K, const float* hb, const int32_t* idx, const float* wts, float* x,
                           const float* ysh, const float* sgl, hipStream_t st);

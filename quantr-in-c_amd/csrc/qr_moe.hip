@@ -28,10 +28,9 @@
 
 #include "qr_gemv.h"
 #include "qr_internal.h"
+#include "qr_route.h"
 
 namespace qr {
-
-constexpr float kMask = -1e9f;  // src/runtime.c:211, 221
 
 // ---------------------------------------------------------------------------
 // Scratch.
@@ -92,157 +91,12 @@ void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s) 
 // ---------------------------------------------------------------------------
 constexpr int kRouteWaves = 4;
 
-// (value, index) candidate order of the reference's argmax scan: a larger
-// value wins; equal values go to the lower index; index -1 (nothing yet)
-// loses to any real candidate.
-__device__ inline bool cand_better(float ov, int oi, float v, int i) {
-  return ov > v || (ov == v && oi >= 0 && (i < 0 || oi < i));
-}
-template <int CTRL>
-__device__ inline void cand_step(float& v, int& i) {
-  const float ov = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                                 0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-  const int oi = __builtin_amdgcn_update_dpp(-1, i, CTRL, 0xF, 0xF, false);
-  if (cand_better(ov, oi, v, i)) {
-    v = ov;
-    i = oi;
-  }
-}
-// Best candidate of the wave, returned in every lane: butterflies inside each
-// 16-lane row (DPP quad xor 1, xor 2, half-row mirror, row mirror), then the
-// four row winners read with readlane and combined in row order.
-__device__ inline void wave_best(float& v, int& i) {
-  cand_step<0xB1>(v, i);
-  cand_step<0x4E>(v, i);
-  cand_step<0x141>(v, i);
-  cand_step<0x140>(v, i);
-  float bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-  int bi = __builtin_amdgcn_readlane(i, 0);
-#pragma unroll
-  for (int r = 1; r < 4; r++) {
-    const float ov =
-        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * r));
-    const int oi = __builtin_amdgcn_readlane(i, 16 * r);
-    if (cand_better(ov, oi, bv, bi)) {
-      bv = ov;
-      bi = oi;
-    }
-  }
-  v = bv;
-  i = bi;
-}
-__device__ inline float wave_max(float v) {
-  auto step = [&](float o) { v = o > v ? o : v; };
-  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
-  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
-  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
-  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
-  float m = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-#pragma unroll
-  for (int r = 1; r < 4; r++) {
-    const float o = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * r));
-    m = o > m ? o : m;
-  }
-  return m;
-}
-
-__device__ inline void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
-// softmax_ref + K argmax passes + renormalisation of one token's E logits
-// (src/kernels.c:191-207, src/runtime.c:208-230) by one wave; `pw` is a
-// wave-private LDS row of >= E floats.
-__device__ inline void route_one(const float* __restrict__ lg, int E, int K, float* pw, int lane,
-                                 float* __restrict__ probs, int32_t* __restrict__ idx,
-                                 float* __restrict__ wts) {
-  // max: seeded with x[0], strictly greater wins (src/kernels.c:192-197);
-  // a max, so the lane split does not change it
-  float mx = lg[0];
-  for (int e = lane; e < E; e += 64) {
-    const float v = lg[e];
-    if (v > mx) mx = v;
-  }
-  mx = wave_max(mx);
-  for (int e = lane; e < E; e += 64) pw[e] = qr_expf(lg[e] - mx);
-  wave_lds_fence();
-  // sequential sum, e ascending (src/kernels.c:198-202), in lane 0
-  float inv = 0.0f;
-  if (lane == 0) {
-    float sum = 0.0f;
-    int e = 0;
-    for (; e + 16 <= E; e += 16) {
-      float4 q[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) q[k] = *reinterpret_cast<const float4*>(pw + e + 4 * k);
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        sum += q[k].x;
-        sum += q[k].y;
-        sum += q[k].z;
-        sum += q[k].w;
-      }
-    }
-    for (; e < E; e++) sum += pw[e];
-    inv = 1.0f / sum;
-  }
-  inv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv), 0));
-  // each lane keeps its own probabilities (e = lane, lane + 64, ...) in
-  // registers for the top-K passes
-  float pv[4];
-#pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const int e = lane + 64 * q;
-    pv[q] = -1e9f;
-    if (e < E) {
-      const float v = pw[e] * inv;
-      pv[q] = v;
-      if (probs) probs[e] = v;
-    }
-  }
-  // K argmax passes (src/runtime.c:210-222): the winner is the lowest index
-  // holding the maximum value; values must beat -1e9f.
-  float wsel[16];
-  int isel[16];
-#pragma unroll
-  for (int k = 0; k < 16; k++) {  // K <= 16 (checked on the host); static indices
-    if (k >= K) break;
-    float bv = kMask;
-    int bi = -1;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const int e = lane + 64 * q;
-      if (e < E && pv[q] > bv) {
-        bv = pv[q];
-        bi = e;
-      }
-    }
-    wave_best(bv, bi);
-    wsel[k] = bv;
-    isel[k] = bi;
-#pragma unroll
-    for (int q = 0; q < 4; q++)
-      if (bi == lane + 64 * q) pv[q] = kMask;
-  }
-  if (lane == 0) {
-    float wsum = 0.0f;  // src/runtime.c:224-230
-#pragma unroll
-    for (int k = 0; k < 16; k++)
-      if (k < K) wsum += wsel[k];
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-      if (k < K) {
-        idx[k] = isel[k];
-        wts[k] = wsel[k] / wsum;
-      }
-    }
-  }
-}
-
 __global__ __launch_bounds__(64 * kRouteWaves) void k_route_topk(const float* __restrict__ logits,
                                                                   int T, int E, int K,
                                                                   float* __restrict__ probs,
                                                                   int32_t* __restrict__ idx,
                                                                   float* __restrict__ wts) {
-  __shared__ __align__(16) float P[kRouteWaves][256];
+  __shared__ __align__(16) float P[kRouteWaves][kRouteRow];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x * kRouteWaves + wave;
   if (t >= T) return;  // whole wave; no workgroup barriers below
@@ -280,45 +134,6 @@ __device__ inline void stage_router_rows(float* sm, int RS, int RPW, const float
       }
     }
   }
-}
-
-// FMA chain over j = k, k + LANES, ... < dm out of LDS, 16 steps' operands
-// read before their FMAs.
-template <int LANES>
-__device__ inline float lds_chain(const float* w, const float* x, int k, int dm) {
-  float acc = 0.0f;
-  int j = k;
-  for (; j + 15 * LANES < dm; j += 16 * LANES) {
-    float wv[16], xv[16];
-#pragma unroll
-    for (int q = 0; q < 16; q++) {
-      wv[q] = w[j + q * LANES];
-      xv[q] = x[j + q * LANES];
-    }
-#pragma unroll
-    for (int q = 0; q < 16; q++) acc = __builtin_fmaf(wv[q], xv[q], acc);
-  }
-  for (; j < dm; j += LANES) acc = __builtin_fmaf(w[j], x[j], acc);
-  return acc;
-}
-
-// Sequential mul-then-add over j < d out of LDS (matmul_ref order), 16 steps'
-// operands read before their adds.
-__device__ inline float lds_seq(const float* w, const float* x, int d) {
-  float s = 0.0f;
-  int j = 0;
-  for (; j + 16 <= d; j += 16) {
-    float wv[16], xv[16];
-#pragma unroll
-    for (int q = 0; q < 16; q++) {
-      wv[q] = w[j + q];
-      xv[q] = x[j + q];
-    }
-#pragma unroll
-    for (int q = 0; q < 16; q++) s += wv[q] * xv[q];
-  }
-  for (; j < d; j++) s += w[j] * x[j];
-  return s;
 }
 
 // Fused router for small T: a workgroup stages RPW router rows and TPW
@@ -413,14 +228,14 @@ __global__ __launch_bounds__(256) void k_router_fused(const float* __restrict__ 
   // its own L2): they were written and are read back with agent-scope
   // atomics, into a wave-private LDS row.
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float* lgl = sm + 4 * 256 + wave * 256;
+  float* lgl = sm + 4 * kRouteRow + wave * 256;
   for (int tt = wave; tt < ntk; tt += (int)(blockDim.x >> 6)) {
     const int t = t0 + tt;
     for (int e = lane; e < E; e += 64)
       lgl[e] = __hip_atomic_load(logits + (size_t)t * E + e, __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
     wave_lds_fence();
-    route_one(lgl, E, K, sm + wave * 256, lane, probs ? probs + (size_t)t * E : nullptr,
+    route_one(lgl, E, K, sm + wave * kRouteRow, lane, probs ? probs + (size_t)t * E : nullptr,
               idx + (size_t)t * K, wts + (size_t)t * K);
     wave_lds_fence();
   }
@@ -443,7 +258,12 @@ static hipError_t router_fused_t(const qr_moe_layer* L, const float* xb, int T, 
   while ((RPW + TPW) * (size_t)RS * 4 > 64 * 1024 && TPW > 1) TPW--;
   if ((RPW + TPW) * (size_t)RS * 4 > 64 * 1024) return hipErrorInvalidValue;
   dim3 grid((E + RPW - 1) / RPW, (T + TPW - 1) / TPW);
-  hipLaunchKernelGGL(k_router_fused<LANES>, grid, dim3(256), (size_t)(RPW + TPW) * RS * 4, st,
+  // LDS: the staged rows, and at least the routing tail's four routing rows
+  // and four logit rows (the staged rows are dead by then)
+  size_t lds = (size_t)(RPW + TPW) * RS * 4;
+  const size_t tail = (size_t)(4 * kRouteRow + 4 * 256) * 4;
+  if (lds < tail) lds = tail;
+  hipLaunchKernelGGL(k_router_fused<LANES>, grid, dim3(256), lds, st,
                      L->router, xb, E, d, T, L->n_used, RPW, TPW, RS, logits, probs, idx, wts,
                      counters);
   return hipGetLastError();
@@ -1041,11 +861,32 @@ static hipError_t shared_expert(const qr_moe_layer* L, const float* xb, int T, c
 hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, int T, int order,
                               const MoeScratch& s, hipStream_t st) {
   const int E = L->n_experts, K = L->n_used, P = T * K;
-  hipError_t e = moe_route_launch(L, xb, T, order, s.logits, nullptr, s.idx, s.wts, st, s.counters_route);
-  if (e != hipSuccess) return e;
   const bool sh = L->sh_hidden > 0;
   const size_t su = qr_wrow_bytes((int)L->up_type, L->dim) * (size_t)L->hidden;
   const size_t sd = qr_wrow_bytes((int)L->down_type, L->hidden) * (size_t)L->dim;
+  hipError_t e;
+
+  // One token: logits, then gate/up with the routing done in every wave, then
+  // down + combine (qr_moe_t1.hip): three launches, no routing kernel.
+  if (T == 1 && router1_ok(L->dim) && gateup1_ok((int)L->up_type, L->dim, E, K) &&
+      L->up_type == L->gate_type && down1v2_ok((int)L->down_type, K, L->dim, L->hidden) &&
+      (reinterpret_cast<uintptr_t>(L->router) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(xb) & 15) == 0) {
+    e = router1_launch(order, L->router, xb, E, L->dim, s.logits, st);
+    if (e != hipSuccess) return e;
+    e = gateup1_launch((int)L->up_type, L->up, L->gate, su, L->dim, L->hidden, E, K, xb, s.logits,
+                       s.idx, s.wts, s.hb, st);
+    if (e != hipSuccess) return e;
+    if (sh) {
+      e = shared_expert(L, xb, T, s, st);
+      if (e != hipSuccess) return e;
+    }
+    return down1v2_launch((int)L->down_type, L->down, sd, L->dim, L->hidden, E, K, s.hb, s.idx,
+                          s.wts, x, sh ? s.ysh : nullptr, s.sgl, st);
+  }
+
+  e = moe_route_launch(L, xb, T, order, s.logits, nullptr, s.idx, s.wts, st, s.counters_route);
+  if (e != hipSuccess) return e;
 
   ExpertArgs g{};
   g.W1 = static_cast<const uint8_t*>(L->up);
@@ -1066,21 +907,13 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
   g.P = P;
 
   if (T == 1) {
-    if (gateup1_ok((int)L->up_type, L->dim)) {
-      e = gateup1_launch((int)L->up_type, L->up, L->gate, su, L->dim, L->hidden, E, K, xb, s.idx,
-                         s.hb, st);
-    } else {
-      g.mode = kModeSingle;
-      e = expert_launch((int)L->up_type, true, g, 1, K, st);
-    }
+    g.mode = kModeSingle;
+    e = expert_launch((int)L->up_type, true, g, 1, K, st);
     if (e != hipSuccess) return e;
     if (sh) {
       e = shared_expert(L, xb, T, s, st);
       if (e != hipSuccess) return e;
     }
-    if (down1v2_ok((int)L->down_type, K, L->hidden))
-      return down1v2_launch((int)L->down_type, L->down, sd, L->dim, L->hidden, E, K, s.hb, s.idx,
-                            s.wts, x, sh ? s.ysh : nullptr, s.sgl, st);
     DownArgs dn{};
     dn.W = static_cast<const uint8_t*>(L->down);
     dn.slice = sd;

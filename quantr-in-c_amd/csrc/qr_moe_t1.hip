@@ -1,19 +1,107 @@
-// qr_moe_t1.hip -- the MoE layer's expert products for one token (decode),
-// src/runtime.c:242-269 with K selected experts:
+// qr_moe_t1.hip -- the MoE layer for one token (decode), src/runtime.c:202-269:
+// three launches, each one memory round trip deep plus its weight stream.
 //
-//   k_gateup1  hb[k] = silu(up_e . xb) * (gate_e . xb) for every slot k, on
-//              the block-per-lane engine (qr_blk.h): a wave holds RB rows of
-//              up in lanes 0-31 and the same rows of gate in lanes 32-63, so
-//              SwiGLU pairs the two row chains with one lane shuffle.
-//   k_down1    y_k = down_e . hb[k] for the K slots of a tile of rows, one wave
-//              per slot on the wave-tile engine (qr_stream.h), then
-//              x += ((0 + y_0 w_0) + y_1 w_1 + ...) in slot order (+ the shared
-//              expert) for the tile's rows.
+//   k_router1   logits[e] = W_r[e] . xb in the reference build's order
+//               (KernelOps.matmul: SEQ / AVX2 / AVX512), one 64-thread
+//               workgroup per expert row; the row and xb arrive in LDS by DMA.
+//   k_gateup1   wave 0 of every workgroup routes the token from the E logits
+//               (softmax_ref, K argmax passes -- the same code in every
+//               workgroup, so all get the same bit-exact experts), then waves
+//               stream
+//               RB rows of its slot's up matrix (lanes 0-31) and the same rows
+//               of gate (lanes 32-63) through LDS on the block-per-lane engine
+//               (qr_blk.h):  hb[k] = silu(up_e . xb) * (gate_e . xb).  The
+//               activation is staged by DMA ahead of the weights; workgroup 0
+//               publishes the indices and renormalised weights.
+//   k_down1     per tile of RW output rows, one wave per slot k: the expert
+//               index comes in by scalar load while hb[k] is staged by DMA,
+//               then the tile of down_e rows is staged by DMA;
+//               y_k = down_e . hb[k] (hb re-quantised), and
+//               x += ((0 + y_0 w_0) + y_1 w_1 + ...) in slot order (+ the
+//               shared expert) for the tile's rows.
 #include "qr_blk.h"
 #include "qr_internal.h"
+#include "qr_route.h"
 #include "qr_stream.h"
 
 namespace qr {
+
+// DMA `nbytes` from g into LDS s in whole 1 KiB instructions; lanes past the
+// end reload g's first 16 bytes into bytes nobody reads (s must hold the
+// rounded-up size).  Returns the number of instructions issued.
+__device__ inline int dma_bytes(const uint8_t* g, uint8_t* s, int nbytes, int lane) {
+  const uint32_t sbase = lds_u32addr(s);
+  const int n = (nbytes + 1023) >> 10;
+  for (int k = 0; k < n; k++) {
+    const int off = k * 1024 + lane * 16;
+    lds_dma16(g + (off < nbytes ? off : 0), sbase + (uint32_t)(k * 1024));
+  }
+  return n;
+}
+
+__host__ __device__ inline size_t kib_round(size_t b) { return (b + 1023) & ~(size_t)1023; }
+
+// ---------------------------------------------------------------------------
+// Router logits.
+// ---------------------------------------------------------------------------
+template <int LANES>
+__global__ __launch_bounds__(64) void k_router1(const float* __restrict__ W,
+                                                const float* __restrict__ xb, int d,
+                                                float* __restrict__ logits) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int e = blockIdx.x, lane = threadIdx.x;
+  const size_t rbytes = kib_round((size_t)d * 4);
+  float* sw = reinterpret_cast<float*>(smem);
+  float* sx = reinterpret_cast<float*>(smem + rbytes);
+  dma_bytes(reinterpret_cast<const uint8_t*>(W + (size_t)e * d), smem, d * 4, lane);
+  dma_bytes(reinterpret_cast<const uint8_t*>(xb), smem + rbytes, d * 4, lane);
+  wait_vmcnt<0>();
+  if constexpr (LANES == 1) {
+    if (lane == 0) logits[e] = lds_seq(sw, sx, d);  // matmul_ref, src/kernels.c:18-28
+  } else {
+    // matmul_omp, src/kernels.c:38-65: LANES FMA chains, lanes combined in the
+    // build's order, then the multiply-add tail
+    const int k = lane;
+    const int dm = d - d % LANES;
+    const float acc = k < LANES ? lds_chain<LANES>(sw, sx, k, dm) : 0.0f;
+    float v[LANES];
+#pragma unroll
+    for (int i = 0; i < LANES; i++) v[i] = __shfl(acc, i);
+    if (lane == 0) {
+      float s = 0.0f;
+      if constexpr (LANES == 8) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) s += v[i];
+      } else {
+        float t8[8], t4[4];
+#pragma unroll
+        for (int i = 0; i < 8; i++) t8[i] = v[8 + i] + v[i];
+#pragma unroll
+        for (int i = 0; i < 4; i++) t4[i] = t8[4 + i] + t8[i];
+        const float a02 = t4[0] + t4[2];
+        const float a13 = t4[1] + t4[3];
+        s += a02 + a13;
+      }
+      for (int j = dm; j < d; j++) s += sw[j] * sx[j];
+      logits[e] = s;
+    }
+  }
+}
+
+bool router1_ok(int dim) { return dim > 0 && (dim & 3) == 0 && 2 * kib_round((size_t)dim * 4) <= 64 * 1024; }
+
+hipError_t router1_launch(int order, const float* W, const float* xb, int E, int d, float* logits,
+                          hipStream_t st) {
+  if ((reinterpret_cast<uintptr_t>(W) & 15) || (reinterpret_cast<uintptr_t>(xb) & 15))
+    return hipErrorInvalidValue;
+  const size_t lds = 2 * kib_round((size_t)d * 4);
+  switch (order) {
+    case QR_ORDER_SEQ: hipLaunchKernelGGL(k_router1<1>, dim3(E), dim3(64), lds, st, W, xb, d, logits); break;
+    case QR_ORDER_AVX2: hipLaunchKernelGGL(k_router1<8>, dim3(E), dim3(64), lds, st, W, xb, d, logits); break;
+    default: hipLaunchKernelGGL(k_router1<16>, dim3(E), dim3(64), lds, st, W, xb, d, logits); break;
+  }
+  return hipGetLastError();
+}
 
 // ---------------------------------------------------------------------------
 // Gate/up.
@@ -24,18 +112,32 @@ struct GateUp1Args {
   size_t slice;         // bytes per expert
   int dim, hidden, E, K;
   const float* xb;      // [dim]
-  const int32_t* idx;   // [K]
+  const float* logits;  // [E]
+  int32_t* idx;         // [K] out (workgroup 0)
+  float* wts;           // [K] out (workgroup 0)
   float* hb;            // [K][hidden]
 };
+
+// LDS: activation staging | activation (NIB/NAT) | routing row | slots
+__host__ __device__ inline size_t gateup1_lds(int type, int dim, size_t* o_act, size_t* o_pw,
+                                              size_t* o_slots) {
+  const size_t xs = blk_xs_bytes(dim, 1);
+  *o_act = xs;
+  *o_pw = *o_act + align16(act_tok_bytes(dim));
+  *o_slots = *o_pw + (size_t)kRouteRow * 4;
+  const size_t sb = (size_t)64 * (type == QR_T_Q4_K ? QR_Q4K_BYTES : QR_Q5K_BYTES);
+  return *o_slots + (size_t)kBlkWaves * sb;
+}
 
 template <int TYPE>
 __global__ __launch_bounds__(64 * kBlkWaves) void k_gateup1(GateUp1Args a) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int BB = BlkFmt<TYPE>::kBytes;
   constexpr int NCH = BlkFmt<TYPE>::kChunks;
+  constexpr int SB = 64 * BB;
   const int nb = a.dim >> 8;
   const int RB = 32 / nb;  // rows per wave tile, per matrix
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int half = lane >> 5, l = lane & 31;
   const int rl = l / nb, b = l - rl * nb;
   const size_t rb = (size_t)nb * BB;
@@ -44,38 +146,109 @@ __global__ __launch_bounds__(64 * kBlkWaves) void k_gateup1(GateUp1Args a) {
   const bool wave_on = tile < a.K * tiles_per_slot;
   const int k = wave_on ? tile / tiles_per_slot : 0;
   const int r0 = (tile - k * tiles_per_slot) * RB;
-  const int e = wave_on ? a.idx[k] : -1;
-  const bool ok = wave_on && e >= 0 && e < a.E;  // uniform per wave
+  size_t o_act, o_pw, o_slots;
+  gateup1_lds(TYPE, a.dim, &o_act, &o_pw, &o_slots);
+  uint8_t* act = smem + o_act;
+  float* pw = reinterpret_cast<float*>(smem + o_pw);
+  uint8_t* slot = smem + o_slots + (size_t)wave * SB;
 
-  // activation first (see k_gemv_blk), then the weight stream
-  ActPre pre;
-  act_prefetch(a.xb, (size_t)a.dim, 1, a.dim, pre);
-  quantize_act_blk<BlkFmt<TYPE>::kNib>(a.xb, (size_t)a.dim, 1, a.dim, smem, pre);
-  asm volatile("" ::: "memory");
-  uint4 c[NCH];
-  const int row = r0 + rl;
-  const bool lane_on = ok && rl < RB && row < a.hidden;
-  if (lane_on) {
-    const uint8_t* W = half ? a.gate : a.up;
-    const uint4* p = reinterpret_cast<const uint4*>(W + (size_t)e * a.slice + (size_t)row * rb +
-                                                    (size_t)b * BB);
-#pragma unroll
-    for (int q = 0; q < NCH; q++) c[q] = p[q];
-  } else {
-#pragma unroll
-    for (int q = 0; q < NCH; q++) c[q] = make_uint4(0, 0, 0, 0);
+  // 1. the activation's DMA first, then the expf table's load
+  stage_act_dma(a.xb, (size_t)a.dim, 1, a.dim, smem, wave, lane);
+  const ExpTab tab = qr_expf_tab();
+  // 2. routing: wave 0 computes the softmax and the rank keys while the other
+  //    waves quantize the activation; after the barrier every thread ranks
+  //    the E candidates (route_rank_wg); workgroup 0 publishes the routing
+  const int* sidx = route_idx(pw);
+  if (wave == 0) {
+    float pv[4];
+    route_softmax(a.logits, a.E, pw, lane, nullptr, tab, pv);
+    route_rank_keys(pv, a.E, a.K, pw, lane);
   }
-  __syncthreads();
+  // 3. quantize the staged activation (every wave's own part has landed once
+  //    its DMA is done)
+  wait_vmcnt<0>();
+  ActPre pre;
+  quantize_act_blk<BlkFmt<TYPE>::kNib>(a.xb, (size_t)a.dim, 1, a.dim, act, pre,
+                                       reinterpret_cast<const float*>(smem));
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  route_rank_wg(a.E, a.K, pw, (int)threadIdx.x, (int)blockDim.x);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  if (blockIdx.x == 0 && wave == 0) route_write(pw, a.K, lane, a.idx, a.wts);
+  const int e = wave_on ? __builtin_amdgcn_readfirstlane(sidx[k]) : -1;
+  const bool ok = wave_on && e >= 0 && e < a.E;  // uniform per wave
   if (!ok) return;  // no barriers below
+  // 4. the weight tile: up rows r0.. at slot bytes [0, RB rb), the same gate
+  //    rows at [32 BB, 32 BB + RB rb): lane l reads its block at l * BB
+  {
+    const int rows = min(RB, a.hidden - r0);
+    const int valid = rows * (int)rb;
+    const uint8_t* ub = a.up + (size_t)e * a.slice + (size_t)r0 * rb;
+    const uint8_t* gb = a.gate + (size_t)e * a.slice + (size_t)r0 * rb;
+    const uint32_t sbase = lds_u32addr(slot);
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+      const int o = c * 1024 + lane * 16;
+      const uint8_t* src = o < 32 * BB ? (o < valid ? ub + o : ub)
+                                       : (o - 32 * BB < valid ? gb + (o - 32 * BB) : ub);
+      lds_dma16(src, sbase + (uint32_t)(c * 1024));
+    }
+  }
 
+  wait_vmcnt<0>();
+  uint4 c[NCH];
+  {
+    const uint4* q = reinterpret_cast<const uint4*>(slot + (size_t)lane * BB);
+#pragma unroll
+    for (int j = 0; j < NCH; j++) c[j] = q[j];
+  }
   float terms[1][8];
   int32_t isums[1][8];
-  blk_terms<TYPE, 1>(c, b, smem, act_tok_bytes(a.dim), terms, isums);
+  blk_terms<TYPE, 1>(c, b, act, act_tok_bytes(a.dim), terms, isums);
   float y[1];
   blk_chain<1>(terms, b, nb, y);
   const float g = __shfl(y[0], lane + 32);  // gate row chain of the same row
+  const float sv = qr_silu_w(y[0], tab);  // every lane
+  const int row = r0 + rl;
   if (half == 0 && rl < RB && row < a.hidden && b == nb - 1)
-    a.hb[(size_t)k * a.hidden + row] = qr_silu(y[0]) * g;
+    a.hb[(size_t)k * a.hidden + row] = sv * g;
+}
+
+bool gateup1_ok(int type, int dim, int E, int K) {
+  if (type != QR_T_Q4_K && type != QR_T_Q5_K) return false;
+  const int nb = dim >> 8;
+  if (nb < 1 || nb > 32 || (dim & 3) || E > 256 || K > 16) return false;
+  size_t a, b, c;
+  return blk_xs_bytes(dim, 1) <= 16 * 1024 && gateup1_lds(type, dim, &a, &b, &c) <= 64 * 1024;
+}
+
+hipError_t gateup1_launch(int type, const void* up, const void* gate, size_t slice, int dim,
+                          int hidden, int E, int K, const float* xb, const float* logits,
+                          int32_t* idx, float* wts, float* hb, hipStream_t st) {
+  GateUp1Args a;
+  a.up = static_cast<const uint8_t*>(up);
+  a.gate = static_cast<const uint8_t*>(gate);
+  a.slice = slice;
+  a.dim = dim;
+  a.hidden = hidden;
+  a.E = E;
+  a.K = K;
+  a.xb = xb;
+  a.logits = logits;
+  a.idx = idx;
+  a.wts = wts;
+  a.hb = hb;
+  const int RB = 32 / (dim >> 8);
+  const int tiles = K * ((hidden + RB - 1) / RB);
+  const int grid = (tiles + kBlkWaves - 1) / kBlkWaves;
+  size_t o1, o2, o3;
+  const size_t lds = gateup1_lds(type, dim, &o1, &o2, &o3);
+  if (type == QR_T_Q4_K)
+    hipLaunchKernelGGL(k_gateup1<QR_T_Q4_K>, dim3(grid), dim3(64 * kBlkWaves), lds, st, a);
+  else
+    hipLaunchKernelGGL(k_gateup1<QR_T_Q5_K>, dim3(grid), dim3(64 * kBlkWaves), lds, st, a);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -92,51 +265,66 @@ struct Down1Args {
   const float* ysh;     // optional shared-expert output [dim]
   const float* sgl;     // its gate logit
   int RW;               // rows per tile
-  size_t slice_bytes;   // LDS per wave: terms, then the staged tile
-  size_t terms_bytes;
+  int o_wave;           // LDS offset of wave 0's slice
+  int slice_bytes;      // LDS per wave: terms | hb staging | weight tile staging
+  int o_hs, o_stage;    // offsets inside a slice
 };
 
 template <int TYPE>
 __global__ __launch_bounds__(1024) void k_down1(Down1Args a) {
   extern __shared__ __align__(16) uint8_t smem[];
-  const TileShape sh0 = tile_shape(TYPE, a.hidden);
-  TileShape sh = sh0;
+  TileShape sh = tile_shape(TYPE, a.hidden);
   sh.RW = a.RW;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int k = wave;  // slot
   const int r0 = blockIdx.x * a.RW;
   const int RWt = min(a.RW, a.dim - r0);
   float* ys = reinterpret_cast<float*>(smem);  // [K][RW]
-  uint8_t* slice = smem + align16((size_t)a.K * a.RW * 4) + (size_t)wave * a.slice_bytes;
+  uint8_t* slice = smem + a.o_wave + (size_t)wave * a.slice_bytes;
   float* terms = reinterpret_cast<float*>(slice);
-  uint32_t* stage = reinterpret_cast<uint32_t*>(slice + a.terms_bytes);
-  const int e = a.idx[k];
-  const bool ok = e >= 0 && e < a.E;  // uniform per wave
+  float* hs = reinterpret_cast<float*>(slice + a.o_hs);
+  uint8_t* stage = slice + a.o_stage;
 
+  // the expert index by scalar load (its own counter), hb[k] by DMA meanwhile
+  const int e = __builtin_amdgcn_readfirstlane(a.idx[k]);
+  const int nh = dma_bytes(reinterpret_cast<const uint8_t*>(a.hb + (size_t)k * a.hidden),
+                           reinterpret_cast<uint8_t*>(hs), a.hidden * 4, lane);
+  (void)nh;
+  const bool ok = e >= 0 && e < a.E;  // uniform per wave
   if (ok) {
+    // the tile's byte range [r0 rb, (r0 + RWt) rb) from its 16-byte aligned start
+    const size_t gs = (size_t)r0 * sh.rb;
+    const size_t a0 = gs & ~(size_t)15;
+    const uint8_t* W = a.down + (size_t)e * a.slice;
+    const int nbytes = (int)(gs + (size_t)RWt * sh.rb - a0);
+    const int nt = dma_bytes(W + a0, stage, nbytes, lane);
+    // hb staged (loads complete in order: only the tile's DMA may be in flight)
+    switch (nt) {
+      case 1: wait_vmcnt<1>(); break;
+      case 2: wait_vmcnt<2>(); break;
+      case 3: wait_vmcnt<3>(); break;
+      case 4: wait_vmcnt<4>(); break;
+      case 5: wait_vmcnt<5>(); break;
+      case 6: wait_vmcnt<6>(); break;
+      case 7: wait_vmcnt<7>(); break;
+      case 8: wait_vmcnt<8>(); break;
+      default: wait_vmcnt<0>(); break;
+    }
     const Slots sl = make_slots(sh.U, lane);
     LaneAct<1, kUPL> A;
-    quantize_lane_act<TYPE, 1, kUPL>(a.hb + (size_t)k * a.hidden, (size_t)a.hidden, sl, sh.RW, A);
-    asm volatile("" ::: "memory");
+    quantize_lane_act<TYPE, 1, kUPL>(hs, (size_t)a.hidden, sl, sh.RW, A);
+    wait_vmcnt<0>();
     TileRegs<TYPE> R;
-    const uint8_t* W = a.down + (size_t)e * a.slice;
-    load_tile<TYPE>(W, a.slice, r0, RWt, sh, sl, lane, R);
-    if constexpr (!IsDirect<TYPE>::value) {
-      // the wave's stage area holds the tile's chunks only (not the engine's
-      // full kCPL chunks): copy those that fit
-      const int nch = (int)((a.slice_bytes - a.terms_bytes) / 16);
-#pragma unroll
-      for (int j = 0; j < kCPL; j++) {
-        const int ci = j * 64 + lane;
-        if (ci < nch) reinterpret_cast<uint4*>(stage)[ci] = R.c[j];
-      }
-      wave_lds_sync();
-    }
-    tile_terms<TYPE, 1, kUPL>(R, sl, RWt, r0, sh, A, stage, terms, nullptr, a.dim);
+    if constexpr (IsDirect<TYPE>::value) load_tile_lds<TYPE>(stage, r0, RWt, sh, sl, R);
+    tile_terms<TYPE, 1, kUPL>(R, sl, RWt, r0, sh, A, reinterpret_cast<const uint32_t*>(stage),
+                              terms, nullptr, a.dim);
     wave_lds_sync();
     for (int i = lane; i < RWt; i += 64) ys[k * a.RW + i] = row_sum_seq(terms + i * sh.TS, sh.U);
+  } else {
+    wait_vmcnt<0>();  // no DMA in flight when the wave moves on
   }
-  __syncthreads();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
   for (int i = threadIdx.x; i < RWt; i += blockDim.x) {
     float acc = 0.0f;  // xb2 = 0 (src/runtime.c:242)
     for (int kk = 0; kk < a.K; kk++) {
@@ -152,65 +340,61 @@ __global__ __launch_bounds__(1024) void k_down1(Down1Args a) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// Host side.
-// ---------------------------------------------------------------------------
-bool gateup1_ok(int type, int dim) {
-  if (type != QR_T_Q4_K && type != QR_T_Q5_K) return false;
-  const int nb = dim >> 8;
-  return nb >= 1 && nb <= 32 && (dim & 3) == 0 && act_tok_bytes(dim) <= 64 * 1024;
+// LDS of a k_down1 workgroup with RW rows per tile: ys, then K wave slices of
+// [terms | hb staging | weight staging], the staging areas whole KiB (DMA).
+static size_t down1_lds(int type, int K, int RW, int hidden, const TileShape& sh, Down1Args* a) {
+  const size_t terms = align16((size_t)RW * sh.TS * 4);
+  const size_t hsb = kib_round((size_t)hidden * 4);
+  const size_t stb = kib_round((size_t)RW * sh.rb + 15);
+  a->o_wave = (int)align16((size_t)K * RW * 4);
+  a->o_hs = (int)terms;
+  a->o_stage = (int)(terms + hsb);
+  a->slice_bytes = (int)(terms + hsb + stb);
+  (void)type;
+  return (size_t)a->o_wave + (size_t)K * a->slice_bytes;
 }
 
-hipError_t gateup1_launch(int type, const void* up, const void* gate, size_t slice, int dim,
-                          int hidden, int E, int K, const float* xb, const int32_t* idx, float* hb,
-                          hipStream_t st) {
-  GateUp1Args a;
-  a.up = static_cast<const uint8_t*>(up);
-  a.gate = static_cast<const uint8_t*>(gate);
-  a.slice = slice;
-  a.dim = dim;
-  a.hidden = hidden;
-  a.E = E;
-  a.K = K;
-  a.xb = xb;
-  a.idx = idx;
-  a.hb = hb;
-  const int RB = 32 / (dim >> 8);
-  const int tiles = K * ((hidden + RB - 1) / RB);
-  const int grid = (tiles + kBlkWaves - 1) / kBlkWaves;
-  const size_t lds = act_tok_bytes(dim);
-  if (type == QR_T_Q4_K)
-    hipLaunchKernelGGL(k_gateup1<QR_T_Q4_K>, dim3(grid), dim3(64 * kBlkWaves), lds, st, a);
-  else
-    hipLaunchKernelGGL(k_gateup1<QR_T_Q5_K>, dim3(grid), dim3(64 * kBlkWaves), lds, st, a);
-  return hipGetLastError();
-}
-
-// LDS of a k_down1 workgroup with RW rows per tile.
-static size_t down1_lds(int type, int K, int RW, const TileShape& sh, size_t* slice,
-                        size_t* terms) {
-  *terms = align16((size_t)RW * sh.TS * 4);
-  const bool direct = type == QR_T_Q4_K || type == QR_T_Q5_K;
-  *slice = *terms + (direct ? 0 : align16((size_t)RW * sh.rb + 15 + 4 + 15));
-  return align16((size_t)K * RW * 4) + (size_t)K * *slice;
-}
-
-// Rows per tile: the engine's shape, reduced until K wave slices fit 64 KB.
-static int down1_rows(int type, int K, int hidden) {
+// Rows per tile: enough tiles to cover the CUs, within the engine's shape, a
+// DMA of at most 8 KiB and K slices within 160 KiB of LDS.
+static int down1_rows(int type, int K, int dim, int hidden) {
   const TileShape sh = tile_shape(type, hidden);
-  int RW = sh.RW;
-  size_t s, t;
-  while (RW > 1 && down1_lds(type, K, RW, sh, &s, &t) > 64 * 1024) RW--;
+  const int cus = device_cus();
+  int RW = (dim + cus - 1) / cus;
+  if (RW > sh.RW) RW = sh.RW;
+  Down1Args t;
+  while (RW > 1 && ((size_t)RW * sh.rb + 15 > 8 * 1024 ||
+                    down1_lds(type, K, RW, hidden, sh, &t) > 160 * 1024))
+    RW--;
   return RW;
 }
 
-bool down1v2_ok(int type, int K, int hidden) {
-  if (type == QR_T_F32 || K > 16 || (hidden & 3)) return false;
+bool down1v2_ok(int type, int K, int dim, int hidden) {
+  if (type == QR_T_F32 || K > 16 || K < 1 || (hidden & 3)) return false;
   const TileShape sh = tile_shape(type, hidden);
-  if (sh.RW < 1) return false;
-  const int RW = down1_rows(type, K, hidden);
-  size_t s, t;
-  return RW >= 1 && down1_lds(type, K, RW, sh, &s, &t) <= 64 * 1024;
+  if (sh.RW < 1 || kib_round((size_t)hidden * 4) > 16 * 1024) return false;
+  const int RW = down1_rows(type, K, dim, hidden);
+  Down1Args t;
+  return RW >= 1 && (size_t)RW * sh.rb + 15 <= 8 * 1024 &&
+         down1_lds(type, K, RW, hidden, sh, &t) <= 160 * 1024;
+}
+
+template <int TYPE>
+static hipError_t down1_launch_t(const Down1Args& a, int grid, size_t lds, hipStream_t st) {
+  static bool opted[64] = {false};
+  if (lds > 64 * 1024) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!opted[dev]) {
+      e = hipFuncSetAttribute((const void*)k_down1<TYPE>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      if (e != hipSuccess) return e;
+      opted[dev] = true;
+    }
+  }
+  hipLaunchKernelGGL(k_down1<TYPE>, dim3(grid), dim3(64 * a.K), lds, st, a);
+  return hipGetLastError();
 }
 
 hipError_t down1v2_launch(int type, const void* down, size_t slice, int dim, int hidden, int E,
@@ -230,25 +414,16 @@ hipError_t down1v2_launch(int type, const void* down, size_t slice, int dim, int
   a.ysh = ysh;
   a.sgl = sgl;
   const TileShape sh = tile_shape(type, hidden);
-  a.RW = down1_rows(type, K, hidden);
-  const size_t lds = down1_lds(type, K, a.RW, sh, &a.slice_bytes, &a.terms_bytes);
+  a.RW = down1_rows(type, K, dim, hidden);
+  const size_t lds = down1_lds(type, K, a.RW, hidden, sh, &a);
   const int grid = (dim + a.RW - 1) / a.RW;
   switch (type) {
-    case QR_T_Q4_K:
-      hipLaunchKernelGGL(k_down1<QR_T_Q4_K>, dim3(grid), dim3(64 * K), lds, st, a);
-      break;
-    case QR_T_Q5_K:
-      hipLaunchKernelGGL(k_down1<QR_T_Q5_K>, dim3(grid), dim3(64 * K), lds, st, a);
-      break;
-    case QR_T_Q6_K:
-      hipLaunchKernelGGL(k_down1<QR_T_Q6_K>, dim3(grid), dim3(64 * K), lds, st, a);
-      break;
-    case QR_T_Q8_0:
-      hipLaunchKernelGGL(k_down1<QR_T_Q8_0>, dim3(grid), dim3(64 * K), lds, st, a);
-      break;
+    case QR_T_Q4_K: return down1_launch_t<QR_T_Q4_K>(a, grid, lds, st);
+    case QR_T_Q5_K: return down1_launch_t<QR_T_Q5_K>(a, grid, lds, st);
+    case QR_T_Q6_K: return down1_launch_t<QR_T_Q6_K>(a, grid, lds, st);
+    case QR_T_Q8_0: return down1_launch_t<QR_T_Q8_0>(a, grid, lds, st);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace qr

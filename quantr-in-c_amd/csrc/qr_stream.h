@@ -170,6 +170,36 @@ __device__ inline void load_tile(const uint8_t* __restrict__ W, size_t total, in
   }
 }
 
+// Direct formats from a tile staged in LDS (byte 0 = matrix byte r0 * rb, which
+// is 16-byte aligned for these formats): the same registers as load_tile.
+template <int TYPE>
+__device__ inline void load_tile_lds(const uint8_t* stage, int r0, int RWt, const TileShape& sh,
+                                     const Slots& sl, TileRegs<TYPE>& R) {
+  (void)r0;
+  if constexpr (IsDirect<TYPE>::value) {
+    constexpr int BB = TYPE == QR_T_Q4_K ? QR_Q4K_BYTES : QR_Q5K_BYTES;
+#pragma unroll
+    for (int i = 0; i < kUPL; i++) {
+      if (sl.row[i] < RWt) {
+        const uint8_t* blk = stage + (size_t)sl.row[i] * sh.rb + (size_t)(sl.u[i] >> 3) * BB;
+        const int s = sl.u[i] & 7;
+        R.hdr[i] = *reinterpret_cast<const uint4*>(blk);
+        if constexpr (TYPE == QR_T_Q4_K) {
+          R.qs[i] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * s);
+          R.qh[i] = 0;
+        } else {
+          R.qs[i] = *reinterpret_cast<const uint4*>(blk + 48 + 16 * s);
+          R.qh[i] = *reinterpret_cast<const uint32_t*>(blk + 16 + 4 * s);
+        }
+      } else {
+        R.hdr[i] = make_uint4(0, 0, 0, 0);
+        R.qs[i] = make_uint4(0, 0, 0, 0);
+        R.qh[i] = 0;
+      }
+    }
+  }
+}
+
 // Staged formats: copy the tile's chunks into the wave's stage area.
 template <int TYPE>
 __device__ inline void stage_regs(const TileRegs<TYPE>& R, uint32_t* stage, int lane) {
