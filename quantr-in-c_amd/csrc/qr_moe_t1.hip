@@ -268,6 +268,7 @@ struct Down1Args {
   int o_wave;           // LDS offset of wave 0's slice
   int slice_bytes;      // LDS per wave: terms | hb staging | weight tile staging
   int o_hs, o_stage;    // offsets inside a slice
+  int o_ab;             // the wave's quantized hb blocks (48 bytes each)
 };
 
 template <int TYPE>
@@ -285,8 +286,24 @@ __global__ __launch_bounds__(1024) void k_down1(Down1Args a) {
   float* hs = reinterpret_cast<float*>(slice + a.o_hs);
   uint8_t* stage = slice + a.o_stage;
 
-  // the expert index by scalar load (its own counter), hb[k] by DMA meanwhile
-  const int e = __builtin_amdgcn_readfirstlane(a.idx[k]);
+  // the expert indices and weights by scalar loads (their own counter), hb[k]
+  // by DMA meanwhile
+  // (16 entries each, 64 bytes: the scratch regions of idx and wts are 256
+  // bytes, and entries past K are never used)
+  int eks[16];
+  float wks[16];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int4 iv = reinterpret_cast<const int4*>(a.idx)[j];
+    const float4 wv = reinterpret_cast<const float4*>(a.wts)[j];
+    eks[4 * j] = iv.x; eks[4 * j + 1] = iv.y; eks[4 * j + 2] = iv.z; eks[4 * j + 3] = iv.w;
+    wks[4 * j] = wv.x; wks[4 * j + 1] = wv.y; wks[4 * j + 2] = wv.z; wks[4 * j + 3] = wv.w;
+  }
+  int e = -1;
+#pragma unroll
+  for (int kk = 0; kk < 16; kk++)
+    if (kk == k) e = eks[kk];
+  e = __builtin_amdgcn_readfirstlane(e);
   const int nh = dma_bytes(reinterpret_cast<const uint8_t*>(a.hb + (size_t)k * a.hidden),
                            reinterpret_cast<uint8_t*>(hs), a.hidden * 4, lane);
   (void)nh;
@@ -312,7 +329,7 @@ __global__ __launch_bounds__(1024) void k_down1(Down1Args a) {
     }
     const Slots sl = make_slots(sh.U, lane);
     LaneAct<1, kUPL> A;
-    quantize_lane_act<TYPE, 1, kUPL>(hs, (size_t)a.hidden, sl, sh.RW, A);
+    quantize_lane_act_wave<TYPE, kUPL>(hs, sl, sh.RW, sh.U, slice + a.o_ab, lane, A);
     wait_vmcnt<0>();
     TileRegs<TYPE> R;
     if constexpr (IsDirect<TYPE>::value) load_tile_lds<TYPE>(stage, r0, RWt, sh, sl, R);
@@ -327,10 +344,12 @@ __global__ __launch_bounds__(1024) void k_down1(Down1Args a) {
   __builtin_amdgcn_s_barrier();
   for (int i = threadIdx.x; i < RWt; i += blockDim.x) {
     float acc = 0.0f;  // xb2 = 0 (src/runtime.c:242)
-    for (int kk = 0; kk < a.K; kk++) {
-      const int ek = a.idx[kk];
+#pragma unroll
+    for (int kk = 0; kk < 16; kk++) {
+      if (kk >= a.K) break;
+      const int ek = eks[kk];
       if (ek < 0 || ek >= a.E) continue;
-      acc += ys[kk * a.RW + i] * a.wts[kk];
+      acc += ys[kk * a.RW + i] * wks[kk];
     }
     if (a.ysh) {
       const float sg = 1.0f / (1.0f + qr_expf(-a.sgl[0]));
@@ -341,15 +360,18 @@ __global__ __launch_bounds__(1024) void k_down1(Down1Args a) {
 }
 
 // LDS of a k_down1 workgroup with RW rows per tile: ys, then K wave slices of
-// [terms | hb staging | weight staging], the staging areas whole KiB (DMA).
+// [terms | hb staging | weight staging | quantized hb], the staging areas
+// whole KiB (DMA).
 static size_t down1_lds(int type, int K, int RW, int hidden, const TileShape& sh, Down1Args* a) {
   const size_t terms = align16((size_t)RW * sh.TS * 4);
   const size_t hsb = kib_round((size_t)hidden * 4);
   const size_t stb = kib_round((size_t)RW * sh.rb + 15);
+  const size_t abb = (size_t)(hidden / 32) * 48;
   a->o_wave = (int)align16((size_t)K * RW * 4);
   a->o_hs = (int)terms;
   a->o_stage = (int)(terms + hsb);
-  a->slice_bytes = (int)(terms + hsb + stb);
+  a->o_ab = (int)(terms + hsb + stb);
+  a->slice_bytes = (int)align16(terms + hsb + stb + abb);
   (void)type;
   return (size_t)a->o_wave + (size_t)K * a->slice_bytes;
 }

@@ -283,6 +283,77 @@ __device__ inline void quantize_lane_act(const float* __restrict__ X, size_t xst
   }
 }
 
+// The same activation blocks, each quantized once per wave: lane u < U
+// quantizes block u of x (global or LDS) into the wave's LDS area ab
+// (48 bytes per block: 32 int8, bd, bs), then every lane gathers the blocks
+// of its slots.  U blocks instead of 64 x kUPL.
+//
+// Four adjacent lanes share a block, 8 elements each (amax and the integer sum
+// reduce across the quad with DPP; the operations are quantize_block's).
+template <int TYPE, int NS>
+__device__ inline void quantize_lane_act_wave(const float* __restrict__ X, const Slots& sl, int RW,
+                                              int U, uint8_t* ab, int lane, LaneAct<1, NS>& A) {
+  constexpr bool PERM = TYPE == QR_T_Q4_K;
+  for (int base = 0; base < 4 * U; base += 64) {
+    const int gi = base + lane;
+    const bool live = gi < 4 * U;
+    const int u = gi >> 2, part = gi & 3;
+    float v[8];
+    if (live) {
+      const float4* p = reinterpret_cast<const float4*>(X + (size_t)u * 32 + part * 8);
+      const float4 f0 = p[0], f1 = p[1];
+      v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
+      v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float av = __builtin_fabsf(v[i]);
+      amax = av > amax ? av : amax;
+    }
+    float o = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, amax), 0xB1, 0xF, 0xF, false));
+    amax = o > amax ? o : amax;
+    o = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, amax), 0x4E, 0xF, 0xF, false));
+    amax = o > amax ? o : amax;
+    const float dd = amax / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    int q[8];
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      q[i] = (int)(int8_t)(int)__builtin_rintf(v[i] * id);
+      s += q[i];
+    }
+    s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, false);
+    s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, false);
+    if (live) {
+      uint8_t* ob = ab + (size_t)u * 48;
+      *reinterpret_cast<uint2*>(ob + part * 8) =
+          PERM ? make_uint2(pack4(q[0], q[2], q[4], q[6]), pack4(q[1], q[3], q[5], q[7]))
+               : make_uint2(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]));
+      if (part == 0)
+        *reinterpret_cast<uint2*>(ob + 32) =
+            make_uint2(__builtin_bit_cast(uint32_t, qr_h2f(qr_f2h(dd))), (uint32_t)s);
+    }
+  }
+  wave_lds_sync();
+#pragma unroll
+  for (int i = 0; i < NS; i++) {
+    if (sl.row[i] < RW) {
+      const uint4* o = reinterpret_cast<const uint4*>(ab + (size_t)sl.u[i] * 48);
+      const uint4 q0 = o[0], q1 = o[1], c = o[2];
+      ActBlock& a = A.a[0][i];
+      a.q[0] = q0.x; a.q[1] = q0.y; a.q[2] = q0.z; a.q[3] = q0.w;
+      a.q[4] = q1.x; a.q[5] = q1.y; a.q[6] = q1.z; a.q[7] = q1.w;
+      a.bd = __builtin_bit_cast(float, c.x);
+      a.bs = (int)c.y;
+    }
+  }
+}
+
 // Terms of every valid slot into terms[t][row][u] (t < NT).  `stage` is the
 // staged tile whose byte 0 is matrix byte (r0 * rb) & ~15.  Optional acc
 // receives the int32 unit sums ([NT][n][U]).
