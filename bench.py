@@ -265,7 +265,7 @@ def cpu_baseline_moe(M, tokens, cores):
 
 # ---------------------------------------------------------------------------
 def load_traffic():
-    p = os.path.join(REPO, "profiles", "q4k_gemv_32000x2048_traffic.json")
+    p = os.path.join(REPO, "profiles", "k_gemv_blk_q4k_32000x2048_traffic.json")
     if not os.path.exists(p):
         return None
     try:
