@@ -418,7 +418,7 @@ static int blk_wg_per_cu() {
 }
 
 // Opt a kernel into LDS beyond 64 KiB, once per device.
-static hipError_t lds_opt_in(const void* fn, bool* done) {
+hipError_t lds_opt_in(const void* fn, bool* done) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;

@@ -15,6 +15,9 @@ size_t gemv_lds_bytes(int type, int d, int nt, int R);
 bool gemv_stream_ok(int type, int d, int nt);
 bool gemv_blk_ok(int type, int d, int nt);
 int device_cus();
+// Let kernel fn use up to 160 KiB of dynamic LDS on the current device (once
+// per device; done[] is the caller's per-device flag array of 64 entries).
+hipError_t lds_opt_in(const void* fn, bool* done);
 int gemv_rows_per_wg(int type, int n, int d, int nt);
 hipError_t gemv_launch(int type, const void* W, const float* X, float* Y, int n, int d, int nt,
                        int xstride, int ystride, int32_t* acc, int32_t* accb, hipStream_t st);
@@ -72,10 +75,13 @@ hipError_t down1v2_launch(int type, const void* down, size_t slice, int dim, int
 bool mfma_type_ok(int type);
 hipError_t quant_rows_launch(const float* x, int xstride, int nrows, int cols, bool perm,
                              uint8_t* out, hipStream_t st);
+// Pairs per work item of the grouped MFMA products for T tokens (the
+// dispatch's tile size).
+int mfma_tile(int T, int K, int E);
 hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const uint8_t* W2,
                               size_t slice, int E, int K, int rows, int cols, const uint8_t* XQ,
                               int x_by_token, const int32_t* offsets, const int32_t* perm,
-                              const int32_t* tiles, float* Y, int ystride, int items,
+                              const int32_t* tiles, float* Y, int ystride, int items, int tile,
                               hipStream_t st);
 
 }  // namespace qr

@@ -361,19 +361,45 @@ __global__ __launch_bounds__(kDispThreads) void k_dispatch(const int32_t* __rest
     if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);  // a count: order-free
   }
   __syncthreads();
-  if (tid == 0) {
-    int acc = 0, tacc = 0;
-    for (int e = 0; e < E; e++) {
-      off[e] = acc;
-      counts[e] = cnt[e];
-      offsets[e] = acc;
-      if (tiles) tiles[e] = tacc;
-      acc += cnt[e];
-      tacc += (cnt[e] + tile - 1) / tile;
+  if (wave == 0) {
+    // exclusive scans of the counts and of the tiles per expert: lane l owns
+    // experts 4l .. 4l+3, then an inclusive scan across the wave
+    int c[4], tl[4], cs = 0, ts = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int e = 4 * lane + i;
+      c[i] = e < E ? cnt[e] : 0;
+      tl[i] = (c[i] + tile - 1) / tile;
+      cs += c[i];
+      ts += tl[i];
     }
-    off[E] = acc;
-    offsets[E] = acc;
-    if (tiles) tiles[E] = tacc;
+    int ci = cs, ti = ts;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(ci, o), w = __shfl_up(ti, o);
+      if (lane >= o) {
+        ci += v;
+        ti += w;
+      }
+    }
+    int acc = ci - cs, tacc = ti - ts;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int e = 4 * lane + i;
+      if (e < E) {
+        off[e] = acc;
+        counts[e] = c[i];
+        offsets[e] = acc;
+        if (tiles) tiles[e] = tacc;
+      }
+      acc += c[i];
+      tacc += tl[i];
+    }
+    if (lane == 63) {
+      off[E] = ci;
+      offsets[E] = ci;
+      if (tiles) tiles[E] = ti;
+    }
   }
   __syncthreads();
   const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -933,7 +959,7 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
   // Many pairs per expert: grouped products on int8 MFMA (qr_moe_mfma.hip).
   if (P >= kMfmaPairsPerExpert * E && mfma_type_ok((int)L->up_type) &&
       mfma_type_ok((int)L->down_type)) {
-    constexpr int kTile = 32;  // pairs per MFMA work item
+    const int kTile = mfma_tile(T, K, E);  // pairs per MFMA work item
     e = moe_dispatch_launch(s.idx, T, K, E, kTile, s.counts, s.offsets, s.tiles, s.perm, s.inv, st);
     if (e != hipSuccess) return e;
     const int items = (P + kTile - 1) / kTile + E;  // >= sum_e ceil(count_e / kTile)
@@ -941,13 +967,13 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
     if (e != hipSuccess) return e;
     e = expert_mfma_launch((int)L->up_type, true, static_cast<const uint8_t*>(L->up),
                            static_cast<const uint8_t*>(L->gate), su, E, K, L->hidden, L->dim, s.xq,
-                           1, s.offsets, s.perm, s.tiles, s.hb, L->hidden, items, st);
+                           1, s.offsets, s.perm, s.tiles, s.hb, L->hidden, items, kTile, st);
     if (e != hipSuccess) return e;
     e = quant_rows_launch(s.hb, L->hidden, P, L->hidden, L->down_type != QR_T_Q8_0, s.hq, st);
     if (e != hipSuccess) return e;
     e = expert_mfma_launch((int)L->down_type, false, static_cast<const uint8_t*>(L->down), nullptr,
                            sd, E, K, L->dim, L->hidden, s.hq, 0, s.offsets, s.perm, s.tiles, s.y,
-                           L->dim, items, st);
+                           L->dim, items, kTile, st);
     if (e != hipSuccess) return e;
   } else {
   const int nt = pick_tile(P, E);

@@ -20,7 +20,9 @@
 // The 8 elements of a lane's A and B may be in any order as long as both use
 // it: K-quant nibbles pair with activations stored [x0 x2 x4 x6 | x1 x3 x5 x7]
 // (the order a nibble dword unpacks to), Q8_0 with natural order.
-#include "qr_gemv.h"
+#include <stdio.h>
+
+#include "qr_blk.h"
 #include "qr_internal.h"
 
 namespace qr {
@@ -170,35 +172,77 @@ __device__ inline void unit_scale(const uint32_t* wl, int o, int s, float* sc, f
 
 // ---------------------------------------------------------------------------
 // The grouped MFMA kernel.
+//
+// A workgroup of 4 waves takes one work item: 64 weight rows of expert e (16
+// per wave; in gate/up mode the same 16 rows of both matrices) against one
+// tile of up to NTOK = 16 NJ dispatched pairs of e.  The K loop walks the rows
+// one stage at a time (one super-block, or 8 Q8_0 blocks: 8 units) through
+// rings of D LDS slots filled by global_load_lds_dwordx4: the stage's
+// activation records, shared by the 4 waves (each wave moves a quarter), and
+// each wave's own 16 x NMAT row stages.  One barrier per stage: past it every
+// wave's share of stage st has landed and every wave is done with stage
+// st - 1, whose slots then take stage st + D - 1.  DMA waits are counted by
+// hand (loads complete in issue order), so the compiler never holds a
+// register or a wait for the stream.
 // ---------------------------------------------------------------------------
 struct MfmaArgs {
   const uint8_t* W1;      // [E][rows][rb] (up in gate/up mode)
   const uint8_t* W2;      // [E][rows][rb] (gate in gate/up mode)
   size_t slice;           // bytes per expert
-  size_t wtotal;          // bytes of each weight tensor
   int rows, cols, E, K;
   const uint8_t* XQ;      // activation records [xrows][cols/32][kXQ]
   int x_by_token;         // activation row of dispatch position p: perm[p] / K, else p
-  const int32_t* offsets; // dispatch (tile = kMT)
+  const int32_t* offsets; // dispatch (tile = NTOK)
   const int32_t* perm;
   const int32_t* tiles;
   float* Y;               // [P][ystride], row = dispatch position
   int ystride;
 };
 
-template <int TYPE, bool GATEUP>
-__global__ __launch_bounds__(256) void k_expert_mfma(MfmaArgs a) {
-  constexpr int NMAT = GATEUP ? 2 : 1;
-  constexpr int SLOT = MF<TYPE>::kSlot;
-  constexpr int NCH = MF<TYPE>::kChunks;
-  constexpr int NLOAD = (NMAT * kMR * NCH + 255) / 256;
-  constexpr int ACT_TOK = 8 * kXQ + 16;  // LDS stride of one pair's 8 records
-  __shared__ __align__(16) uint32_t wl[NMAT * kMR * SLOT / 4];
-  __shared__ __align__(16) float scl[NMAT][8][kMR];
-  __shared__ __align__(16) float mnl[NMAT][8][kMR];
-  __shared__ __align__(16) uint8_t act[kMT * ACT_TOK];
-  __shared__ int xrow[kMT];
-  __shared__ int whead[NMAT * kMR];  // misaligned head bytes of each row's stage
+template <int TYPE, bool GATEUP, int NJ, int RA, int D, int NW>
+struct MfmaGeo {
+  static constexpr int NMAT = GATEUP ? 2 : 1;
+  static constexpr int NTOK = 16 * NJ;
+  static constexpr int WR = 16 * RA;                       // rows per wave
+  static constexpr int MR = NW * WR;                       // rows per workgroup
+  // 16-byte chunks per row stage: Q4_K / Q5_K stages start 16-byte aligned,
+  // the others anywhere (up to 15 bytes of head)
+  static constexpr int NCH = (TYPE == QR_T_Q4_K || TYPE == QR_T_Q5_K) ? MF<TYPE>::kStage / 16
+                                                                      : MF<TYPE>::kChunks;
+  static constexpr int SLOT = NCH * 16;                    // LDS bytes per row stage
+  static constexpr int WCH = NMAT * WR * NCH;              // a wave's chunks per stage
+  static constexpr int WI = (WCH + 63) / 64;               // its DMA instructions
+  static constexpr int WST = WI * 1024;                    // its LDS slot (whole instructions)
+  // a pair's 8 records take 24 chunks plus one pad chunk: a 400-byte LDS
+  // stride puts the 16 pairs of an MFMA B tile on different banks
+  static constexpr int APC = 8 * kXQ / 16 + 1;             // chunks per pair (with pad)
+  static constexpr int ACH = NTOK * APC;                   // activation chunks per stage
+  static constexpr int AI = (ACH + 64 * NW - 1) / (64 * NW);  // per wave
+  static constexpr int AST = NW * AI * 1024;               // LDS of one activation stage
+  static constexpr int NI = WI + AI;                       // DMA instructions per wave and stage
+  static constexpr int NSC = NMAT * 8 * WR;                // a wave's (matrix, unit, row)s
+  static constexpr int SCL = NSC * 4;                      // their scales (or mins), bytes
+  static constexpr int O_W = D * AST;                      // weight rings, wave-major
+  static constexpr int O_S = O_W + NW * D * WST;           // scales, per wave
+  static constexpr int O_M = O_S + NW * SCL;               // mins, per wave
+  static constexpr int LDS = O_M + NW * SCL;
+  // activation row of each pair, read once before the first stage: it shares
+  // the scale area, first written after the first stage's barrier
+  static constexpr int O_X = O_S;
+  static_assert(NTOK * 4 <= NW * SCL, "xrow");
+  static_assert(D == 2 || D == 3, "ring depth");
+  static_assert(NI <= 63, "vmcnt range");
+  static_assert(NSC % 64 == 0, "scale passes");
+};
+
+template <int TYPE, bool GATEUP, int NJ, int RA, int D, int NW>
+__global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
+  using G = MfmaGeo<TYPE, GATEUP, NJ, RA, D, NW>;
+  constexpr int NMAT = G::NMAT;
+  constexpr int NCH = G::NCH;
+  constexpr int WR = G::WR;
+  constexpr int KST = MF<TYPE>::kStage;
+  extern __shared__ __align__(16) uint8_t smem[];
 
   // work item -> (expert e, first dispatch position p0, pair count np)
   const int item = blockIdx.y;
@@ -211,179 +255,208 @@ __global__ __launch_bounds__(256) void k_expert_mfma(MfmaArgs a) {
     else hi = mid;
   }
   const int e = lo;
-  const int p0 = a.offsets[e] + (item - a.tiles[e]) * kMT;
-  const int np = min(kMT, a.offsets[e + 1] - p0);
+  const int p0 = a.offsets[e] + (item - a.tiles[e]) * G::NTOK;
+  const int np = min(G::NTOK, a.offsets[e + 1] - p0);
   if (np <= 0) return;  // uniform
-  const int r0 = blockIdx.x * kMR;
-  const int nr = min(kMR, a.rows - r0);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   const int kg = lane >> 4, ln = lane & 15;
+  const int rw0 = blockIdx.x * G::MR + wave * WR;  // the wave's first row
   const int U = TYPE == QR_T_Q8_0 ? a.cols / 32 : (a.cols / 256) * 8;
   const size_t rb = qr_wrow_bytes(TYPE, a.cols);
   const int nstage = (U + 7) / 8;
-  if (tid < kMT) {
+  int* xrow = reinterpret_cast<int*>(smem + G::O_X);
+  if (threadIdx.x < G::NTOK) {
     int xr = 0;
-    if (tid < np) xr = a.x_by_token ? a.perm[p0 + tid] / a.K : p0 + tid;
-    xrow[tid] = xr;
+    const int tt = threadIdx.x;
+    if (tt < np) xr = a.x_by_token ? a.perm[p0 + tt] / a.K : p0 + tt;
+    xrow[tt] = xr;
   }
-
-  float acc[NMAT][2][4];
-#pragma unroll
-  for (int m = 0; m < NMAT; m++)
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) acc[m][j][i] = 0.0f;
-
-  uint4 wreg[NLOAD];
-  uint4 areg[3];
   __syncthreads();  // xrow
-  // global loads of stage st into registers
-  auto load_stage = [&](int st) {
+
+  // Per-lane DMA sources, stage-invariant parts.  Weight chunk c = k*64+lane
+  // of this wave: matrix c / (WR NCH), row rw0 + (c / NCH) % WR, chunk c % NCH
+  // of the row's stage; chunks past the row's stage bytes, rows past the
+  // matrix and lanes past the wave's chunks reload the workgroup's first row's
+  // stage start.
+  const size_t ebase = (size_t)e * a.slice;
+  size_t wrow[G::WI];     // row start (within the tensor), or ~0 if no row
+  int wch[G::WI];
+  const uint8_t* wmat[G::WI];
 #pragma unroll
-    for (int q = 0; q < NLOAD; q++) {
-      const int c = tid + 256 * q;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (c < NMAT * kMR * NCH) {
-        const int m = c / (kMR * NCH);
-        const int rem = c - m * kMR * NCH;
-        const int rr = rem / NCH, ch = rem - rr * NCH;
-        if (rr < nr) {
-          const size_t base = (size_t)e * a.slice + (size_t)(r0 + rr) * rb;
-          const size_t start = base + (size_t)st * MF<TYPE>::kStage;
-          const size_t end = base + min((size_t)(st + 1) * MF<TYPE>::kStage, rb);
-          const size_t off = (start & ~(size_t)15) + (size_t)ch * 16;
-          const uint8_t* W = m == 0 ? a.W1 : a.W2;
-          if (off < end) {
-            if (off + 16 <= a.wtotal) {
-              v = *reinterpret_cast<const uint4*>(W + off);
-            } else {  // the tensor ends inside this chunk: no load leaves it
-              uint32_t w[4];
+  for (int k = 0; k < G::WI; k++) {
+    const int c = k * 64 + lane;
+    const int m = c / (WR * NCH);
+    const int rem = c - m * WR * NCH;
+    const int rr = rem / NCH;
+    wch[k] = rem - rr * NCH;
+    const int row = rw0 + rr;
+    wrow[k] = (c < G::WCH && row < a.rows) ? ebase + (size_t)row * rb : ~(size_t)0;
+    wmat[k] = (GATEUP && m == 1) ? a.W2 : a.W1;
+  }
+  const size_t row0 = ebase + (size_t)(blockIdx.x * G::MR) * rb;
+  // Activation chunk c = (wave AI + k) 64 + lane: pair c / APC, chunk c % APC
+  // of its 8 records (unit (c % APC) / 3; chunk 24 is the pad).  asrc: the
+  // chunk's offset in XQ at stage 0, or ~0 (reload pair 0's first chunk).
+  const size_t xq_row = (size_t)U * kXQ;
+  size_t asrc[G::AI];
+  int aunit[G::AI];
 #pragma unroll
-              for (int k = 0; k < 4; k++) {
-                const size_t o = off + 4 * k;
-                if (o + 4 <= a.wtotal) w[k] = *reinterpret_cast<const uint32_t*>(W + o);
-                else if (o + 2 <= a.wtotal) w[k] = *reinterpret_cast<const uint16_t*>(W + o);
-                else w[k] = 0;
-              }
-              v = make_uint4(w[0], w[1], w[2], w[3]);
-            }
-          }
+  for (int k = 0; k < G::AI; k++) {
+    const int c = (wave * G::AI + k) * 64 + lane;
+    const int tt = c / G::APC;
+    const int ch = c - tt * G::APC;
+    const bool ok = c < G::ACH && tt < np && ch < G::APC - 1;
+    asrc[k] = ok ? (size_t)xrow[tt] * xq_row + 16 * (size_t)ch : ~(size_t)0;
+    aunit[k] = ch / 3;
+  }
+  const size_t asrc0 = (size_t)xrow[0] * xq_row;
+
+  auto issue = [&](int st) {
+    const int slot = st % D;
+    const uint32_t abase = lds_u32addr(smem + slot * G::AST) + (uint32_t)(wave * G::AI * 1024);
+#pragma unroll
+    for (int k = 0; k < G::AI; k++) {
+      const bool ok = asrc[k] != ~(size_t)0 && 8 * st + aunit[k] < U;
+      const size_t src = (ok ? asrc[k] : asrc0) + (size_t)(8 * st) * kXQ;
+      lds_dma16(a.XQ + src, abase + (uint32_t)(k * 1024));
+    }
+    const uint32_t wbase = lds_u32addr(smem + G::O_W + (wave * D + slot) * G::WST);
+    const size_t s0 = (size_t)st * KST;
+    const size_t clampsrc = (row0 + s0) & ~(size_t)15;
+#pragma unroll
+    for (int k = 0; k < G::WI; k++) {
+      size_t src = clampsrc;
+      const uint8_t* W = a.W1;
+      if (wrow[k] != ~(size_t)0) {
+        const size_t start = wrow[k] + s0;
+        const size_t end = wrow[k] + (s0 + KST < rb ? s0 + KST : rb);
+        const size_t off = (start & ~(size_t)15) + 16 * (size_t)wch[k];
+        if (off < end) {
+          src = off;
+          W = wmat[k];
         }
       }
-      wreg[q] = v;
-    }
-    // activation records of the stage's units: 24 16-byte chunks per pair
-#pragma unroll
-    for (int q = 0; q < 3; q++) {
-      const int c = tid + 256 * q;  // < 768 = kMT * 24
-      const int tt = c / 24, ch = c - tt * 24;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      const int u0 = st * 8 + (ch * 16) / kXQ;
-      if (tt < np && u0 < U) {
-        const uint8_t* rec = a.XQ + ((size_t)xrow[tt] * (a.cols / 32) + (size_t)st * 8) * kXQ;
-        v = reinterpret_cast<const uint4*>(rec)[ch];
-      }
-      areg[q] = v;
+      lds_dma16(W + src, wbase + (uint32_t)(k * 1024));
     }
   };
 
-  load_stage(0);
-  for (int st = 0; st < nstage; st++) {
-    __syncthreads();  // previous stage's LDS reads are done
+  float acc[NMAT][RA][NJ][4];
 #pragma unroll
-    for (int q = 0; q < NLOAD; q++) {
-      const int c = tid + 256 * q;
-      if (c < NMAT * kMR * NCH) {
-        const int m = c / (kMR * NCH);
-        const int rem = c - m * kMR * NCH;
-        const int rr = rem / NCH, ch = rem - rr * NCH;
-        reinterpret_cast<uint4*>(wl)[((m * kMR + rr) * SLOT) / 16 + ch] = wreg[q];
-        if (ch == 0) {
-          const size_t start = (size_t)e * a.slice + (size_t)(r0 + rr) * rb +
-                               (size_t)st * MF<TYPE>::kStage;
-          whead[m * kMR + rr] = (int)(start & 15);
-        }
-      }
-    }
+  for (int m = 0; m < NMAT; m++)
 #pragma unroll
-    for (int q = 0; q < 3; q++) {
-      const int c = tid + 256 * q;
-      const int tt = c / 24, ch = c - tt * 24;
-      *reinterpret_cast<uint4*>(act + tt * ACT_TOK + ch * 16) = areg[q];
-    }
-    __syncthreads();
-    if (st + 1 < nstage) load_stage(st + 1);
-    // scales and mins of the stage's (row, unit)s
-    const int su = min(8, U - st * 8);
-    for (int i = tid; i < NMAT * kMR * 8; i += 256) {
-      const int m = i / (kMR * 8);
-      const int rem = i - m * kMR * 8;
-      const int s = rem / kMR, rr = rem - s * kMR;
-      float sc = 0.0f, mn = 0.0f;
-      if (s < su && rr < nr) {
-        const int o = (m * kMR + rr) * SLOT + whead[m * kMR + rr];
-        unit_scale<TYPE>(wl, o, s, &sc, &mn);
-      }
-      scl[m][s][rr] = sc;
-      mnl[m][s][rr] = mn;
-    }
-    __syncthreads();
+    for (int r = 0; r < RA; r++)
+#pragma unroll
+      for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[m][r][j][i] = 0.0f;
 
-    const int rw = wave * 16 + ln;  // this lane's A row (within the 64)
-    for (int s = 0; s < su; s++) {
-      long A[NMAT];
+  float* scl = reinterpret_cast<float*>(smem + G::O_S + wave * G::SCL);
+  float* mnl = reinterpret_cast<float*>(smem + G::O_M + wave * G::SCL);
+
 #pragma unroll
-      for (int m = 0; m < NMAT; m++) {
-        const int o = (m * kMR + rw) * SLOT + whead[m * kMR + rw];
-        A[m] = unit_a<TYPE>(wl, o, s, kg);
+  for (int s = 0; s < D - 1; s++)
+    if (s < nstage) issue(s);
+  for (int st = 0; st < nstage; st++) {
+    // stage st has landed once no more than the later stages' DMA is in flight
+    if (D == 3 && st + 1 < nstage) wait_vmcnt<G::NI>();
+    else wait_vmcnt<0>();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (st + D - 1 < nstage) issue(st + D - 1);
+    const int slot = st % D;
+    const uint32_t* wl = reinterpret_cast<const uint32_t*>(smem + G::O_W + (wave * D + slot) * G::WST);
+    const uint8_t* as = smem + slot * G::AST;
+    const int su = min(8, U - st * 8);
+    const size_t s0 = (size_t)st * KST;
+    // scales and mins of the wave's (matrix, unit, row)s: entry
+    // (m * 8 + s) * WR + rr
+#pragma unroll
+    for (int q = 0; q < G::NSC / 64; q++) {
+      const int i = q * 64 + lane;
+      const int m = i / (8 * WR), s = (i / WR) & 7, rr = i % WR;
+      float sc = 0.0f, mn = 0.0f;
+      const int row = rw0 + rr;
+      if (s < su && row < a.rows) {
+        const int hd = (int)((ebase + (size_t)row * rb + s0) & 15);
+        unit_scale<TYPE>(wl, (m * WR + rr) * G::SLOT + hd, s, &sc, &mn);
       }
+      scl[i] = sc;
+      mnl[i] = mn;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // head bytes of this lane's A rows (both matrices share them: same slice
+    // and row sizes, 16-byte aligned bases)
+    int hA[RA];
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const uint8_t* rec = act + (16 * j + ln) * ACT_TOK + s * kXQ;
+    for (int r = 0; r < RA; r++)
+      hA[r] = (int)((ebase + (size_t)(rw0 + 16 * r + ln) * rb + s0) & 15);
+    auto unit_step = [&](int s) {
+      long A[NMAT][RA];
+#pragma unroll
+      for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int r = 0; r < RA; r++)
+          A[m][r] = unit_a<TYPE>(wl, (m * WR + 16 * r + ln) * G::SLOT + hA[r], s, kg);
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const uint8_t* rec = as + (16 * j + ln) * (16 * G::APC) + s * kXQ;
         const uint2 bq = *reinterpret_cast<const uint2*>(rec + 8 * kg);
         const long B = (long)((uint64_t)bq.x | ((uint64_t)bq.y << 32));
         const float bd = *reinterpret_cast<const float*>(rec + 32);
         const float bsf = *reinterpret_cast<const float*>(rec + 36);
         const int bs = *reinterpret_cast<const int*>(rec + 40);
 #pragma unroll
-        for (int m = 0; m < NMAT; m++) {
-          const v4i zero = {0, 0, 0, 0};
-          const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[m], B, zero, 0, 0, 0);
-          const float4 sc4 = *reinterpret_cast<const float4*>(&scl[m][s][wave * 16 + 4 * kg]);
-          const float4 mn4 = *reinterpret_cast<const float4*>(&mnl[m][s][wave * 16 + 4 * kg]);
-          const float scv[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
-          const float mnv[4] = {mn4.x, mn4.y, mn4.z, mn4.w};
+        for (int m = 0; m < NMAT; m++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            float term;
-            if constexpr (MF<TYPE>::kMin) {
-              term = (scv[i] * (float)D[i] - mnv[i] * bsf) * bd;
-            } else if constexpr (TYPE == QR_T_Q6_K) {
-              term = scv[i] * (float)(D[i] - 32 * bs) * bd;
-            } else {
-              term = (float)D[i] * scv[i] * bd;
+          for (int r = 0; r < RA; r++) {
+            const v4i zero = {0, 0, 0, 0};
+            const v4i Dv = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[m][r], B, zero, 0, 0, 0);
+            const int si = (m * 8 + s) * WR + 16 * r + 4 * kg;
+            const float4 sc4 = *reinterpret_cast<const float4*>(scl + si);
+            const float4 mn4 = *reinterpret_cast<const float4*>(mnl + si);
+            const float scv[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
+            const float mnv[4] = {mn4.x, mn4.y, mn4.z, mn4.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              float term;
+              if constexpr (MF<TYPE>::kMin) {
+                term = (scv[i] * (float)Dv[i] - mnv[i] * bsf) * bd;
+              } else if constexpr (TYPE == QR_T_Q6_K) {
+                term = scv[i] * (float)(Dv[i] - 32 * bs) * bd;
+              } else {
+                term = (float)Dv[i] * scv[i] * bd;
+              }
+              acc[m][r][j][i] += term;
             }
-            acc[m][j][i] += term;
           }
-        }
       }
+    };
+    if (su == 8) {
+      // every stage of a K-quant, and whole Q8_0 stages: unrolled, so the
+      // units' LDS reads and MFMAs interleave
+#pragma unroll
+      for (int s = 0; s < 8; s++) unit_step(s);
+    } else {
+      for (int s = 0; s < su; s++) unit_step(s);
     }
   }
 
-  // outputs: rows r0 + 16 wave + 4 kg + i, pairs 16 j + ln
+  // outputs: rows rw0 + 16 r + 4 kg + i, pairs 16 j + ln
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
+  for (int j = 0; j < NJ; j++) {
     const int tt = 16 * j + ln;
     if (tt >= np) continue;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int rr = wave * 16 + 4 * kg + i;
-      if (rr >= nr) continue;
-      float out = acc[0][j][i];
-      if constexpr (GATEUP) out = qr_silu(acc[0][j][i]) * acc[1][j][i];
-      a.Y[(size_t)(p0 + tt) * a.ystride + r0 + rr] = out;
-    }
+    for (int r = 0; r < RA; r++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int row = rw0 + 16 * r + 4 * kg + i;
+        if (row >= a.rows) continue;
+        float out = acc[0][r][j][i];
+        if constexpr (GATEUP) out = qr_silu(acc[0][r][j][i]) * acc[NMAT - 1][r][j][i];
+        a.Y[(size_t)(p0 + tt) * a.ystride + row] = out;
+      }
   }
 }
 
@@ -404,24 +477,87 @@ hipError_t quant_rows_launch(const float* x, int xstride, int nrows, int cols, b
   return hipGetLastError();
 }
 
-template <int TYPE, bool GATEUP>
+// Pairs per work item: 16 while experts see few pairs each (less padding of
+// the 16-pair MFMA tile), 32 beyond (half the weight re-reads).
+int mfma_tile(int T, int K, int E) {
+  static int forced = -1;
+  if (forced < 0) {
+    const char* s = getenv("QR_MFMA_TILE");
+    const int v = s ? atoi(s) : 0;
+    forced = (v == 16 || v == 32) ? v : 0;
+  }
+  if (forced) return forced;
+  return (long)T * K >= 16L * E ? 32 : 16;
+}
+
+template <int TYPE, bool GATEUP, int NJ, int D, int NW>
 static hipError_t mfma_launch_t(const MfmaArgs& a, int items, hipStream_t st) {
-  dim3 grid((a.rows + kMR - 1) / kMR, items);
-  if (grid.x == 0 || grid.y == 0) return hipSuccess;
-  hipLaunchKernelGGL((k_expert_mfma<TYPE, GATEUP>), grid, dim3(256), 0, st, a);
-  return hipGetLastError();
+  using G = MfmaGeo<TYPE, GATEUP, NJ, 1, D, NW>;
+  if constexpr (G::LDS > 160 * 1024) {
+    return mfma_launch_t<TYPE, GATEUP, NJ, 2, 4>(a, items, st);  // the shape that always fits
+  } else {
+    static bool opted[64] = {false};
+    dim3 grid((a.rows + G::MR - 1) / G::MR, items);
+    if (grid.x == 0 || grid.y == 0) return hipSuccess;
+    if (G::LDS > 64 * 1024) {
+      const hipError_t e = lds_opt_in((const void*)k_expert_mfma<TYPE, GATEUP, NJ, 1, D, NW>, opted);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((k_expert_mfma<TYPE, GATEUP, NJ, 1, D, NW>), grid, dim3(64 * NW), G::LDS,
+                       st, a);
+    return hipGetLastError();
+  }
+}
+
+// Kernel shape (waves per workgroup NW, each on 16 rows; ring depth D) per
+// product; the QR_MFMA_GU / QR_MFMA_DN overrides ("NW,D") are for tuning
+// sweeps.
+static void mfma_shape(bool gateup, int* nw, int* d) {
+  static int cfg[2][2] = {{-1, -1}, {-1, -1}};
+  int* c = cfg[gateup ? 1 : 0];
+  if (c[0] < 0) {
+    c[0] = 4;
+    c[1] = 2;
+    const char* s = getenv(gateup ? "QR_MFMA_GU" : "QR_MFMA_DN");
+    int x = 0, y = 0;
+    if (s && sscanf(s, "%d,%d", &x, &y) == 2 && (x == 4 || x == 8) && (y == 2 || y == 3)) {
+      c[0] = x;
+      c[1] = y;
+    }
+  }
+  *nw = c[0];
+  *d = c[1];
+}
+
+template <int TYPE, bool GATEUP, int NJ>
+static hipError_t mfma_launch_shape(const MfmaArgs& a, int items, hipStream_t st) {
+  int nw, d;
+  mfma_shape(GATEUP, &nw, &d);
+  if (nw == 8) return d == 3 ? mfma_launch_t<TYPE, GATEUP, NJ, 3, 8>(a, items, st)
+                             : mfma_launch_t<TYPE, GATEUP, NJ, 2, 8>(a, items, st);
+  return d == 3 ? mfma_launch_t<TYPE, GATEUP, NJ, 3, 4>(a, items, st)
+                : mfma_launch_t<TYPE, GATEUP, NJ, 2, 4>(a, items, st);
+}
+
+template <int TYPE, bool GATEUP>
+static hipError_t mfma_launch_nj(const MfmaArgs& a, int items, int tile, hipStream_t st) {
+  if (tile == 32) return mfma_launch_shape<TYPE, GATEUP, 2>(a, items, st);
+  return mfma_launch_shape<TYPE, GATEUP, 1>(a, items, st);
 }
 
 hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const uint8_t* W2,
                               size_t slice, int E, int K, int rows, int cols, const uint8_t* XQ,
                               int x_by_token, const int32_t* offsets, const int32_t* perm,
-                              const int32_t* tiles, float* Y, int ystride, int items,
+                              const int32_t* tiles, float* Y, int ystride, int items, int tile,
                               hipStream_t st) {
+  if (tile != 16 && tile != 32) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(W1) & 15) || (gateup && (reinterpret_cast<uintptr_t>(W2) & 15)) ||
+      (reinterpret_cast<uintptr_t>(XQ) & 15))
+    return hipErrorInvalidValue;
   MfmaArgs a;
   a.W1 = W1;
   a.W2 = W2;
   a.slice = slice;
-  a.wtotal = slice * (size_t)E;
   a.rows = rows;
   a.cols = cols;
   a.E = E;
@@ -434,14 +570,14 @@ hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const ui
   a.Y = Y;
   a.ystride = ystride;
   switch (type) {
-    case QR_T_Q4_K: return gateup ? mfma_launch_t<QR_T_Q4_K, true>(a, items, st)
-                                  : mfma_launch_t<QR_T_Q4_K, false>(a, items, st);
-    case QR_T_Q5_K: return gateup ? mfma_launch_t<QR_T_Q5_K, true>(a, items, st)
-                                  : mfma_launch_t<QR_T_Q5_K, false>(a, items, st);
-    case QR_T_Q6_K: return gateup ? mfma_launch_t<QR_T_Q6_K, true>(a, items, st)
-                                  : mfma_launch_t<QR_T_Q6_K, false>(a, items, st);
-    case QR_T_Q8_0: return gateup ? mfma_launch_t<QR_T_Q8_0, true>(a, items, st)
-                                  : mfma_launch_t<QR_T_Q8_0, false>(a, items, st);
+    case QR_T_Q4_K: return gateup ? mfma_launch_nj<QR_T_Q4_K, true>(a, items, tile, st)
+                                  : mfma_launch_nj<QR_T_Q4_K, false>(a, items, tile, st);
+    case QR_T_Q5_K: return gateup ? mfma_launch_nj<QR_T_Q5_K, true>(a, items, tile, st)
+                                  : mfma_launch_nj<QR_T_Q5_K, false>(a, items, tile, st);
+    case QR_T_Q6_K: return gateup ? mfma_launch_nj<QR_T_Q6_K, true>(a, items, tile, st)
+                                  : mfma_launch_nj<QR_T_Q6_K, false>(a, items, tile, st);
+    case QR_T_Q8_0: return gateup ? mfma_launch_nj<QR_T_Q8_0, true>(a, items, tile, st)
+                                  : mfma_launch_nj<QR_T_Q8_0, false>(a, items, tile, st);
     default: return hipErrorInvalidValue;
   }
 }
