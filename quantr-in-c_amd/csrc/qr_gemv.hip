@@ -424,7 +424,13 @@ hipError_t lds_opt_in(const void* fn, bool* done) {
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
   if (!done[dev]) {
-    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
+    // the dynamic allowance is what the kernel's static LDS leaves of the CU's
+    hipFuncAttributes fa;
+    e = hipFuncGetAttributes(&fa, fn);
+    if (e != hipSuccess) return e;
+    const size_t stat = fa.sharedSizeBytes;
+    if (stat >= kLdsMax) return hipErrorInvalidValue;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kLdsMax - stat));
     if (e != hipSuccess) return e;
     done[dev] = true;
   }

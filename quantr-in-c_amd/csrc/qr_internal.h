@@ -43,14 +43,12 @@ struct MoeScratch {
   float* sgl;         // [T]             shared expert gate logit
   uint8_t* xq;        // [T][dim/32] quantized activation records (MFMA path)
   uint8_t* hq;        // [T*K][hidden/32] quantized hb records (MFMA path)
-  unsigned* counters_route;  // [T] zeroed once; the fused router leaves them zero
 };
-size_t moe_counter_bytes(int T);
 size_t moe_scratch_bytes(const qr_moe_layer* L, int T);
 void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s);
 hipError_t moe_route_launch(const qr_moe_layer* L, const float* xb, int T, int order,
                             float* logits, float* probs, int32_t* idx, float* wts,
-                            hipStream_t st, unsigned* counters = nullptr);
+                            hipStream_t st);
 hipError_t moe_dispatch_launch(const int32_t* idx, int T, int K, int E, int tile, int32_t* counts,
                                int32_t* offsets, int32_t* tiles, int32_t* perm, int32_t* inv,
                                hipStream_t st);
@@ -71,6 +69,14 @@ hipError_t down1v2_launch(int type, const void* down, size_t slice, int dim, int
                           int K, const float* hb, const int32_t* idx, const float* wts, float* x,
                           const float* ysh, const float* sgl, hipStream_t st);
 
+// qr_moe_tn.hip
+bool rlogits_ok(int d);
+hipError_t rlogits_launch(int order, const float* W, const float* X, int T, int E, int d,
+                          float* logits, hipStream_t st);
+hipError_t route_rank_launch(const float* logits, int T, int E, int K, float* probs, int32_t* idx,
+                             float* wts, const float* X, int d, bool perm, uint8_t* XQ,
+                             hipStream_t st);
+
 // qr_moe_mfma.hip
 bool mfma_type_ok(int type);
 hipError_t quant_rows_launch(const float* x, int xstride, int nrows, int cols, bool perm,
@@ -82,6 +88,6 @@ hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const ui
                               size_t slice, int E, int K, int rows, int cols, const uint8_t* XQ,
                               int x_by_token, const int32_t* offsets, const int32_t* perm,
                               const int32_t* tiles, float* Y, int ystride, int items, int tile,
-                              hipStream_t st);
+                              uint8_t* QO, bool qperm, hipStream_t st);
 
 }  // namespace qr

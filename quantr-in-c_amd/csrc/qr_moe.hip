@@ -29,6 +29,7 @@
 #include "qr_gemv.h"
 #include "qr_internal.h"
 #include "qr_route.h"
+#include "qr_tokens.h"
 
 namespace qr {
 
@@ -54,9 +55,6 @@ size_t moe_scratch_bytes(const qr_moe_layer* L, int T) {
   b += a256((size_t)T * (L->dim / 32) * 48);
   b += a256(P * (size_t)(L->hidden / 32) * 48);
   return b;
-}
-
-size_t moe_counter_bytes(int T) { return a256((size_t)(T + 1) * 4);
 }
 
 void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s) {
@@ -104,195 +102,22 @@ __global__ __launch_bounds__(64 * kRouteWaves) void k_route_topk(const float* __
             idx + (size_t)t * K, wts + (size_t)t * K);
 }
 
-// Copy nr router rows (W + (r0 + q) d, to slot q) and ntk token rows
-// (X + (t0 + q) d, to slot RPW + q) of d floats into LDS slots of stride RS
-// floats, the whole workgroup; every thread's 128-bit loads of a batch are in
-// flight before its LDS stores.
-__device__ inline void stage_router_rows(float* sm, int RS, int RPW, const float* W, int r0,
-                                         int nr, const float* X, int t0, int ntk, int d) {
-  constexpr int kBatch = 8;
-  const int d4 = d >> 2;
-  const int total = (nr + ntk) * d4;
-  for (int base = 0; base < total; base += kBatch * (int)blockDim.x) {
-    float4 v0, v1, v2, v3, v4, v5, v6, v7;
-    float4* v[kBatch] = {&v0, &v1, &v2, &v3, &v4, &v5, &v6, &v7};
-#pragma unroll
-    for (int b = 0; b < kBatch; b++) {
-      const int i = base + b * (int)blockDim.x + (int)threadIdx.x;
-      const int ic = i < total ? i : 0;
-      const int q = ic / d4, j4 = ic - q * d4;
-      const float* src = q < nr ? W + (size_t)(r0 + q) * d : X + (size_t)(t0 + q - nr) * d;
-      *v[b] = reinterpret_cast<const float4*>(src)[j4];
-    }
-#pragma unroll
-    for (int b = 0; b < kBatch; b++) {
-      const int i = base + b * (int)blockDim.x + (int)threadIdx.x;
-      if (i < total) {
-        const int q = i / d4, j4 = i - q * d4;
-        const int slot = q < nr ? q : RPW + q - nr;
-        *reinterpret_cast<float4*>(sm + slot * RS + 4 * j4) = *v[b];
-      }
-    }
-  }
-}
-
-// Fused router for small T: a workgroup stages RPW router rows and TPW
-// tokens in LDS (row stride RS floats, RS = 8 mod 32), runs one thread per
-// (token, row, chain) in the reference build's accumulation order and writes
-// the logits; the last workgroup of each token block to finish (a device-
-// scope counter, reset by that workgroup) then routes the block's tokens,
-// one wave per token.
-template <int LANES>
-__global__ __launch_bounds__(256) void k_router_fused(const float* __restrict__ W,
-                                                      const float* __restrict__ X, int E, int d,
-                                                      int T, int K, int RPW, int TPW, int RS,
-                                                      float* __restrict__ logits,
-                                                      float* __restrict__ probs,
-                                                      int32_t* __restrict__ idx,
-                                                      float* __restrict__ wts,
-                                                      unsigned* __restrict__ counters) {
-  extern __shared__ __align__(16) float sm[];
-  __shared__ int is_last;
-  float* sw = sm;
-  float* sx = sm + RPW * RS;
-  const int r0 = blockIdx.x * RPW;
-  const int t0 = blockIdx.y * TPW;
-  const int nr = min(RPW, E - r0);
-  const int ntk = min(TPW, T - t0);
-  const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(W) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(X) & 15) == 0;
-  // staged row q < nr is router row r0 + q at slot q; q >= nr is token
-  // t0 + q - nr at slot RPW + q - nr (the token rows start at sx even when the
-  // last row block is short)
-  if (vec) {
-    stage_router_rows(sm, RS, RPW, W, r0, nr, X, t0, ntk, d);
-  } else {
-    for (int i = threadIdx.x; i < (nr + ntk) * d; i += blockDim.x) {
-      const int q = i / d, j = i - q * d;
-      const int slot = q < nr ? q : RPW + q - nr;
-      sm[slot * RS + j] = q < nr ? W[(size_t)(r0 + q) * d + j] : X[(size_t)(t0 + q - nr) * d + j];
-    }
-  }
-  __syncthreads();
-  {
-    const int k = threadIdx.x % LANES;
-    const int rr = (threadIdx.x / LANES) % RPW;
-    const int tt = threadIdx.x / (LANES * RPW);
-    const bool live = rr < nr && tt < ntk;
-    const float* w = sw + rr * RS;
-    const float* x = sx + (live ? tt : 0) * RS;
-    if constexpr (LANES == 1) {
-      if (live) {
-        const float s = lds_seq(w, x, d);
-        __hip_atomic_store(logits + (size_t)(t0 + tt) * E + r0 + rr, s, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      }
-    } else {
-      const int dm = d - d % LANES;
-      const float acc = live ? lds_chain<LANES>(w, x, k, dm) : 0.0f;
-      float v[LANES];
-      const int base = (int)(threadIdx.x & 63) - k;
-#pragma unroll
-      for (int i = 0; i < LANES; i++) v[i] = __shfl(acc, base + i);
-      if (live && k == 0) {
-        float s = 0.0f;
-        if constexpr (LANES == 8) {
-#pragma unroll
-          for (int i = 0; i < 8; i++) s += v[i];
-        } else {
-          float t8[8], t4[4];
-#pragma unroll
-          for (int i = 0; i < 8; i++) t8[i] = v[8 + i] + v[i];
-#pragma unroll
-          for (int i = 0; i < 4; i++) t4[i] = t8[4 + i] + t8[i];
-          const float a02 = t4[0] + t4[2];
-          const float a13 = t4[1] + t4[3];
-          s += a02 + a13;
-        }
-        for (int j = dm; j < d; j++) s += w[j] * x[j];
-        __hip_atomic_store(logits + (size_t)(t0 + tt) * E + r0 + rr, s, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
-  if (!counters) return;  // logits only
-  // last workgroup of this token block?
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) is_last = atomicAdd(&counters[blockIdx.y], 1u) == gridDim.x - 1;
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  if (threadIdx.x == 0) counters[blockIdx.y] = 0u;  // every workgroup of the block has counted
-  // The logits come from other workgroups, possibly on other XCDs (each with
-  // its own L2): they were written and are read back with agent-scope
-  // atomics, into a wave-private LDS row.
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float* lgl = sm + 4 * kRouteRow + wave * 256;
-  for (int tt = wave; tt < ntk; tt += (int)(blockDim.x >> 6)) {
-    const int t = t0 + tt;
-    for (int e = lane; e < E; e += 64)
-      lgl[e] = __hip_atomic_load(logits + (size_t)t * E + e, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-    wave_lds_fence();
-    route_one(lgl, E, K, sm + wave * kRouteRow, lane, probs ? probs + (size_t)t * E : nullptr,
-              idx + (size_t)t * K, wts + (size_t)t * K);
-    wave_lds_fence();
-  }
-}
-
-// Fused router for T <= kFusedRouteT: (RPW, TPW) keep LANES * RPW * TPW <= 256
-// chains and RPW + TPW staged rows within 64 KB of LDS.
-constexpr int kFusedRouteT = 16;
-
-template <int LANES>
-static hipError_t router_fused_t(const qr_moe_layer* L, const float* xb, int T, float* logits,
-                                 float* probs, int32_t* idx, float* wts, unsigned* counters,
-                                 hipStream_t st) {
-  const int d = L->dim, E = L->n_experts;
-  const int RS = ((d + 31) & ~31) + 8;
-  int TPW = T < 4 ? T : 4;
-  int RPW = 256 / (LANES * TPW);
-  if (RPW > 8) RPW = 8;
-  while ((RPW + TPW) * (size_t)RS * 4 > 64 * 1024 && RPW > 1) RPW--;
-  while ((RPW + TPW) * (size_t)RS * 4 > 64 * 1024 && TPW > 1) TPW--;
-  if ((RPW + TPW) * (size_t)RS * 4 > 64 * 1024) return hipErrorInvalidValue;
-  dim3 grid((E + RPW - 1) / RPW, (T + TPW - 1) / TPW);
-  // LDS: the staged rows, and at least the routing tail's four routing rows
-  // and four logit rows (the staged rows are dead by then)
-  size_t lds = (size_t)(RPW + TPW) * RS * 4;
-  const size_t tail = (size_t)(4 * kRouteRow + 4 * 256) * 4;
-  if (lds < tail) lds = tail;
-  hipLaunchKernelGGL(k_router_fused<LANES>, grid, dim3(256), lds, st,
-                     L->router, xb, E, d, T, L->n_used, RPW, TPW, RS, logits, probs, idx, wts,
-                     counters);
-  return hipGetLastError();
-}
-
-bool router_fused_ok(const qr_moe_layer* L, int T) {
-  (void)T;
-  const int RS = ((L->dim + 31) & ~31) + 8;
-  return (size_t)2 * RS * 4 <= 64 * 1024;
-}
-
 hipError_t moe_route_launch(const qr_moe_layer* L, const float* xb, int T, int order,
                             float* logits, float* probs, int32_t* idx, float* wts,
-                            hipStream_t st, unsigned* counters) {
+                            hipStream_t st) {
   const int E = L->n_experts;
   hipError_t e;
-  if (T <= kFusedRouteT && router_fused_ok(L, T)) {
-    // small T: logits and routing in one launch; larger T: logits here,
-    // routing by k_route_topk below
-    unsigned* cnt = T <= kFusedRouteT ? counters : nullptr;
-    switch (order) {
-      case QR_ORDER_SEQ: e = router_fused_t<1>(L, xb, T, logits, probs, idx, wts, cnt, st); break;
-      case QR_ORDER_AVX2: e = router_fused_t<8>(L, xb, T, logits, probs, idx, wts, cnt, st); break;
-      default: e = router_fused_t<16>(L, xb, T, logits, probs, idx, wts, cnt, st); break;
-    }
-    if (e != hipSuccess || cnt) return e;
-  } else {
-    e = gemv_f32_launch(order, L->router, xb, logits, E, L->dim, T, L->dim, E, st);
+  if (T <= 0) return hipSuccess;
+  if (rlogits_ok(L->dim) && E <= 256 && L->n_used <= 16 &&
+      (reinterpret_cast<uintptr_t>(L->router) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(xb) & 15) == 0) {
+    // tiled logits (qr_moe_tn.hip), then one workgroup per token ranks the top K
+    e = rlogits_launch(order, L->router, xb, T, E, L->dim, logits, st);
+    if (e != hipSuccess) return e;
+    return route_rank_launch(logits, T, E, L->n_used, probs, idx, wts, xb, L->dim, false,
+                             nullptr, st);
   }
+  e = gemv_f32_launch(order, L->router, xb, logits, E, L->dim, T, L->dim, E, st);
   if (e != hipSuccess) return e;
   const int grid = (T + kRouteWaves - 1) / kRouteWaves;
   hipLaunchKernelGGL(k_route_topk, dim3(grid), dim3(64 * kRouteWaves), 0, st, logits, T, E,
@@ -334,11 +159,8 @@ hipError_t softmax_launch(float* x, int rows, int n, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------
-// Dispatch: one workgroup of 1024 threads, E <= 256.
+// Dispatch: one workgroup of kDispThreads threads (qr_tokens.h).
 // ---------------------------------------------------------------------------
-constexpr int kDispThreads = 1024;
-constexpr int kDispWaves = kDispThreads / 64;
-
 __global__ __launch_bounds__(kDispThreads) void k_dispatch(const int32_t* __restrict__ idx, int P,
                                                            int E, int tile,
                                                            int32_t* __restrict__ counts,
@@ -346,97 +168,7 @@ __global__ __launch_bounds__(kDispThreads) void k_dispatch(const int32_t* __rest
                                                            int32_t* __restrict__ tiles,
                                                            int32_t* __restrict__ perm,
                                                            int32_t* __restrict__ inv) {
-  __shared__ int cnt[256];
-  __shared__ int off[257];
-  __shared__ int run[256];
-  __shared__ int wtab[kDispWaves][256];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  for (int e = tid; e < E; e += kDispThreads) {
-    cnt[e] = 0;
-    run[e] = 0;
-  }
-  __syncthreads();
-  for (int p = tid; p < P; p += kDispThreads) {
-    const int e = idx[p];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);  // a count: order-free
-  }
-  __syncthreads();
-  if (wave == 0) {
-    // exclusive scans of the counts and of the tiles per expert: lane l owns
-    // experts 4l .. 4l+3, then an inclusive scan across the wave
-    int c[4], tl[4], cs = 0, ts = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int e = 4 * lane + i;
-      c[i] = e < E ? cnt[e] : 0;
-      tl[i] = (c[i] + tile - 1) / tile;
-      cs += c[i];
-      ts += tl[i];
-    }
-    int ci = cs, ti = ts;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(ci, o), w = __shfl_up(ti, o);
-      if (lane >= o) {
-        ci += v;
-        ti += w;
-      }
-    }
-    int acc = ci - cs, tacc = ti - ts;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int e = 4 * lane + i;
-      if (e < E) {
-        off[e] = acc;
-        counts[e] = c[i];
-        offsets[e] = acc;
-        if (tiles) tiles[e] = tacc;
-      }
-      acc += c[i];
-      tacc += tl[i];
-    }
-    if (lane == 63) {
-      off[E] = ci;
-      offsets[E] = ci;
-      if (tiles) tiles[E] = ti;
-    }
-  }
-  __syncthreads();
-  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int c0 = 0; c0 < P; c0 += kDispThreads) {
-    for (int i = tid; i < kDispWaves * 256; i += kDispThreads) (&wtab[0][0])[i] = 0;
-    __syncthreads();
-    const int p = c0 + tid;
-    int e = p < P ? idx[p] : -1;
-    if (e >= E) e = -1;
-    const bool valid = e >= 0;
-    // lanes of this wave holding the same expert: match the 8 expert bits
-    uint64_t peers = __ballot(valid);
-#pragma unroll
-    for (int b = 0; b < 8; b++) {
-      const bool bit = valid && ((e >> b) & 1);
-      const uint64_t m = __ballot(bit);
-      peers &= bit ? m : ~m;
-    }
-    const int rank = __popcll(peers & lt);
-    if (valid && rank == 0) wtab[wave][e] = __popcll(peers);
-    __syncthreads();
-    if (valid) {
-      int base = off[e] + run[e] + rank;
-      for (int w = 0; w < wave; w++) base += wtab[w][e];
-      perm[base] = p;
-      inv[p] = base;
-    } else if (p < P) {
-      inv[p] = -1;
-    }
-    __syncthreads();
-    for (int ee = tid; ee < E; ee += kDispThreads) {
-      int s = 0;
-      for (int w = 0; w < kDispWaves; w++) s += wtab[w][ee];
-      run[ee] += s;
-    }
-    __syncthreads();
-  }
+  dispatch_wg(idx, P, E, tile, counts, offsets, tiles, perm, inv);
 }
 
 hipError_t moe_dispatch_launch(const int32_t* idx, int T, int K, int E, int tile, int32_t* counts,
@@ -911,7 +643,41 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
                           s.wts, x, sh ? s.ysh : nullptr, s.sgl, st);
   }
 
-  e = moe_route_launch(L, xb, T, order, s.logits, nullptr, s.idx, s.wts, st, s.counters_route);
+  // Many tokens on int8 MFMA: tiled logits; routing + xb records; dispatch;
+  // gate/up writing hb records; down; combine.
+  if (T > 1 && P >= kMfmaPairsPerExpert * E && mfma_type_ok((int)L->up_type) &&
+      mfma_type_ok((int)L->down_type) && rlogits_ok(L->dim) && E <= 256 && K <= 16 &&
+      (reinterpret_cast<uintptr_t>(L->router) & 15) == 0) {
+    const int kTile = mfma_tile(T, K, E);  // pairs per MFMA work item
+    const bool perm_x = L->up_type != QR_T_Q8_0;
+    e = rlogits_launch(order, L->router, xb, T, E, L->dim, s.logits, st);
+    if (e != hipSuccess) return e;
+    e = route_rank_launch(s.logits, T, E, K, nullptr, s.idx, s.wts, xb, L->dim, perm_x, s.xq, st);
+    if (e != hipSuccess) return e;
+    e = moe_dispatch_launch(s.idx, T, K, E, kTile, s.counts, s.offsets, s.tiles, s.perm, s.inv,
+                            st);
+    if (e != hipSuccess) return e;
+    const int items = (P + kTile - 1) / kTile + E;  // >= sum_e ceil(count_e / kTile)
+    e = expert_mfma_launch((int)L->up_type, true, static_cast<const uint8_t*>(L->up),
+                           static_cast<const uint8_t*>(L->gate), su, E, K, L->hidden, L->dim, s.xq,
+                           1, s.offsets, s.perm, s.tiles, s.hb, L->hidden, items, kTile, s.hq,
+                           L->down_type != QR_T_Q8_0, st);
+    if (e != hipSuccess) return e;
+    e = expert_mfma_launch((int)L->down_type, false, static_cast<const uint8_t*>(L->down), nullptr,
+                           sd, E, K, L->dim, L->hidden, s.hq, 0, s.offsets, s.perm, s.tiles, s.y,
+                           L->dim, items, kTile, nullptr, false, st);
+    if (e != hipSuccess) return e;
+    if (sh) {
+      e = shared_expert(L, xb, T, s, st);
+      if (e != hipSuccess) return e;
+    }
+    const long n = (long)T * L->dim;
+    hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, s.y,
+                       s.inv, s.wts, T, K, L->dim, sh ? s.ysh : nullptr, s.sgl);
+    return hipGetLastError();
+  }
+
+  e = moe_route_launch(L, xb, T, order, s.logits, nullptr, s.idx, s.wts, st);
   if (e != hipSuccess) return e;
 
   ExpertArgs g{};
@@ -967,13 +733,14 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
     if (e != hipSuccess) return e;
     e = expert_mfma_launch((int)L->up_type, true, static_cast<const uint8_t*>(L->up),
                            static_cast<const uint8_t*>(L->gate), su, E, K, L->hidden, L->dim, s.xq,
-                           1, s.offsets, s.perm, s.tiles, s.hb, L->hidden, items, kTile, st);
+                           1, s.offsets, s.perm, s.tiles, s.hb, L->hidden, items, kTile, nullptr,
+                           false, st);
     if (e != hipSuccess) return e;
     e = quant_rows_launch(s.hb, L->hidden, P, L->hidden, L->down_type != QR_T_Q8_0, s.hq, st);
     if (e != hipSuccess) return e;
     e = expert_mfma_launch((int)L->down_type, false, static_cast<const uint8_t*>(L->down), nullptr,
                            sd, E, K, L->dim, L->hidden, s.hq, 0, s.offsets, s.perm, s.tiles, s.y,
-                           L->dim, items, kTile, st);
+                           L->dim, items, kTile, nullptr, false, st);
     if (e != hipSuccess) return e;
   } else {
   const int nt = pick_tile(P, E);

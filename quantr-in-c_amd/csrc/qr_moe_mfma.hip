@@ -23,15 +23,13 @@
 #include <stdio.h>
 
 #include "qr_blk.h"
+#include "qr_tokens.h"
 #include "qr_internal.h"
 
 namespace qr {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kXQ = 48;   // activation record: [32 int8 | bd f32 | (float)bs f32 | bs i32 | pad]
-constexpr int kMR = 64;   // weight rows per workgroup (16 per wave)
-constexpr int kMT = 32;   // pairs per workgroup (two MFMA column tiles)
 
 // ---------------------------------------------------------------------------
 // Activation rows -> quantized records in HBM (quantize_row_q8_0,
@@ -40,64 +38,7 @@ constexpr int kMT = 32;   // pairs per workgroup (two MFMA column tiles)
 template <bool PERM>
 __global__ __launch_bounds__(256) void k_quant_rows(const float* __restrict__ x, int xstride,
                                                    int nrows, int cols, uint8_t* __restrict__ out) {
-  const int U = cols >> 5;
-  const long total = (long)nrows * U * 4;
-  const long gi = (long)blockIdx.x * 256 + threadIdx.x;
-  const bool live = gi < total;
-  const long blk = live ? gi >> 2 : 0;
-  const int part = (int)(gi & 3);
-  const long r = blk / U;
-  const int u = (int)(blk - r * U);
-  float v[8];
-  if (live) {
-    const float4* p = reinterpret_cast<const float4*>(x + r * xstride + u * 32 + part * 8);
-    const float4 a = p[0], b = p[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = 0.0f;
-  }
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const float av = __builtin_fabsf(v[i]);
-    amax = av > amax ? av : amax;
-  }
-  auto xor1 = [](int q) { return __builtin_amdgcn_update_dpp(0, q, 0xB1, 0xF, 0xF, false); };
-  auto xor2 = [](int q) { return __builtin_amdgcn_update_dpp(0, q, 0x4E, 0xF, 0xF, false); };
-  float o = __builtin_bit_cast(float, xor1(__builtin_bit_cast(int, amax)));
-  amax = o > amax ? o : amax;
-  o = __builtin_bit_cast(float, xor2(__builtin_bit_cast(int, amax)));
-  amax = o > amax ? o : amax;
-  const float dd = amax / 127.0f;
-  const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
-  int q[8];
-  int s = 0;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    q[i] = (int)(int8_t)(int)__builtin_rintf(v[i] * id);
-    s += q[i];
-  }
-  s += xor1(s);
-  s += xor2(s);
-  if (!live) return;
-  uint8_t* rec = out + blk * kXQ;
-  uint32_t w0, w1;
-  if (PERM) {
-    w0 = pack4(q[0], q[2], q[4], q[6]);
-    w1 = pack4(q[1], q[3], q[5], q[7]);
-  } else {
-    w0 = pack4(q[0], q[1], q[2], q[3]);
-    w1 = pack4(q[4], q[5], q[6], q[7]);
-  }
-  *reinterpret_cast<uint2*>(rec + part * 8) = make_uint2(w0, w1);
-  if (part == 0) {
-    float* f = reinterpret_cast<float*>(rec + 32);
-    f[0] = qr_h2f(qr_f2h(dd));
-    f[1] = (float)s;
-    reinterpret_cast<int*>(rec + 40)[0] = s;
-  }
+  quant_rows_group<PERM>(x, xstride, nrows, cols, out, (long)blockIdx.x * 256 + threadIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -197,6 +138,10 @@ struct MfmaArgs {
   const int32_t* tiles;
   float* Y;               // [P][ystride], row = dispatch position
   int ystride;
+  // gate/up mode, optional: instead of Y, the activation records of the down
+  // product ([P][rows/32], PERM order if qperm), quantized from the tile
+  uint8_t* QO;
+  int qperm;
 };
 
 template <int TYPE, bool GATEUP, int NJ, int RA, int D, int NW>
@@ -442,6 +387,47 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
     }
   }
 
+  if constexpr (GATEUP) {
+    if (a.QO) {
+      // hb = silu(up) * gate of the tile's rows and pairs -> LDS [NTOK][MR]
+      // (the activation ring is free now) -> whole 32-row blocks per pair
+      // quantized (quantize_row_q8_0, as the down product's matmul_q_fused
+      // does) into the down product's activation records
+      float* ob = reinterpret_cast<float*>(smem);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();  // every wave is done with the last stage
+#pragma unroll
+      for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int r = 0; r < RA; r++)
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            ob[(16 * j + ln) * G::MR + wave * WR + 16 * r + 4 * kg + i] =
+                qr_silu(acc[0][r][j][i]) * acc[NMAT - 1][r][j][i];
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      constexpr int NB = G::MR / 32;  // blocks per pair in the tile
+      const int nrec = a.rows >> 5;
+      for (int g = threadIdx.x; g < G::NTOK * NB * 4; g += 64 * NW) {  // whole quads
+        const int tt = g / (NB * 4), rem = g - tt * (NB * 4);
+        const int blk = rem >> 2, part = rem & 3;
+        const float* src = ob + tt * G::MR + blk * 32 + part * 8;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = src[i];
+        uint2 q8;
+        float bd;
+        int bs;
+        if (a.qperm) quant8_core<true>(v, &q8, &bd, &bs);
+        else quant8_core<false>(v, &q8, &bd, &bs);
+        const int row0 = blockIdx.x * G::MR + blk * 32;
+        if (tt < np && row0 < a.rows)
+          record_store(a.QO + ((size_t)(p0 + tt) * nrec + (row0 >> 5)) * kXQ, part, q8, bd, bs);
+      }
+      return;
+    }
+  }
+
   // outputs: rows rw0 + 16 r + 4 kg + i, pairs 16 j + ln
 #pragma unroll
   for (int j = 0; j < NJ; j++) {
@@ -549,8 +535,10 @@ hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const ui
                               size_t slice, int E, int K, int rows, int cols, const uint8_t* XQ,
                               int x_by_token, const int32_t* offsets, const int32_t* perm,
                               const int32_t* tiles, float* Y, int ystride, int items, int tile,
-                              hipStream_t st) {
+                              uint8_t* QO, bool qperm, hipStream_t st) {
   if (tile != 16 && tile != 32) return hipErrorInvalidValue;
+  if (QO && (!gateup || (rows & 31) || (reinterpret_cast<uintptr_t>(QO) & 15)))
+    return hipErrorInvalidValue;
   if ((reinterpret_cast<uintptr_t>(W1) & 15) || (gateup && (reinterpret_cast<uintptr_t>(W2) & 15)) ||
       (reinterpret_cast<uintptr_t>(XQ) & 15))
     return hipErrorInvalidValue;
@@ -569,6 +557,8 @@ hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const ui
   a.tiles = tiles;
   a.Y = Y;
   a.ystride = ystride;
+  a.QO = QO;
+  a.qperm = qperm ? 1 : 0;
   switch (type) {
     case QR_T_Q4_K: return gateup ? mfma_launch_nj<QR_T_Q4_K, true>(a, items, tile, st)
                                   : mfma_launch_nj<QR_T_Q4_K, false>(a, items, tile, st);

@@ -1,0 +1,230 @@
+// qr_moe_tn.hip -- the router side of the MoE layer for T > 1 tokens
+// (src/runtime.c:202-230 applied to every token):
+//
+//   k_rlogits        logits[t][e] = W_r[e] . xb[t] in the reference build's
+//                    accumulation order (KernelOps.matmul: SEQ / AVX2 / AVX512),
+//                    a tile of tokens x router rows per workgroup from K-chunks
+//                    of both double-buffered into LDS by DMA.
+//   k_route_rank     one workgroup per token: softmax_ref, top-K as an exact
+//                    rank over the workgroup, renormalisation; the other waves
+//                    quantize the token's xb into the activation records of
+//                    the grouped products meanwhile.
+#include <cstdlib>
+
+#include "qr_blk.h"
+#include "qr_internal.h"
+#include "qr_route.h"
+#include "qr_tokens.h"
+
+namespace qr {
+
+// ---------------------------------------------------------------------------
+// Router logits for many tokens.  Thread (k, tb, rb) of the 256 runs chain k
+// of the TT x RT outputs (token tb TT + i, row rb RT + q) of the workgroup's
+// tile: LANES = 1 is matmul_ref's sequential mul-then-add (src/kernels.c:18-28),
+// LANES = 8 / 16 matmul_omp's FMA chains over j = k mod LANES, combined in the
+// build's lane order, then the multiply-add tail (src/kernels.c:38-65).  A
+// chain walks the K-chunks in order, so chunking keeps every chain's order.
+// ---------------------------------------------------------------------------
+constexpr int kRlCk = 256;          // elements per chunk: one 1 KiB DMA per row
+constexpr int kRlRs = kRlCk + 8;    // LDS row stride (floats): 8-bank skew per row
+
+template <int TW, int RW>
+__host__ __device__ constexpr size_t rlogits_lds() {
+  return (size_t)2 * (TW + RW) * kRlRs * 4;
+}
+
+template <int LANES, int NTB, int TT, int NRB, int RT>
+__global__ __launch_bounds__(256) void k_rlogits(const float* __restrict__ W,
+                                                 const float* __restrict__ X, int T, int E, int d,
+                                                 float* __restrict__ logits) {
+  static_assert(LANES * NTB * NRB == 256, "thread layout");
+  constexpr int TW = NTB * TT, RW = NRB * RT;
+  static_assert((TW + RW) % 4 == 0, "rows per wave");
+  constexpr int NIW = (TW + RW) / 4;  // DMA instructions per wave and chunk
+  constexpr int BUF = (TW + RW) * kRlRs;
+  extern __shared__ __align__(16) float sm[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int k = tid % LANES, tb = (tid / LANES) % NTB, rb = tid / (LANES * NTB);
+  const int r0 = blockIdx.x * RW, t0 = blockIdx.y * TW;
+  const int nch = (d + kRlCk - 1) / kRlCk;
+  const int dm = d - d % LANES;
+
+  // chunk c of LDS row i (rows 0..RW-1: router rows r0 + i, then tokens
+  // t0 + i - RW; past-the-end rows and tokens reload the last one) into
+  // buffer b; wave w moves rows w, w + 4, ...
+  auto issue = [&](int c, int b) {
+    const int nb = min(kRlCk, d - c * kRlCk) * 4;
+    const int o = lane * 16;
+#pragma unroll
+    for (int n = 0; n < NIW; n++) {
+      const int i = wave + 4 * n;
+      const float* src = i < RW ? W + (size_t)min(r0 + i, E - 1) * d
+                                : X + (size_t)min(t0 + i - RW, T - 1) * d;
+      lds_dma16(reinterpret_cast<const uint8_t*>(src + c * kRlCk) + (o < nb ? o : 0),
+                lds_u32addr(sm + b * BUF + i * kRlRs));
+    }
+  };
+
+  float acc[TT][RT];
+#pragma unroll
+  for (int i = 0; i < TT; i++)
+#pragma unroll
+    for (int q = 0; q < RT; q++) acc[i][q] = 0.0f;
+
+  issue(0, 0);
+  for (int c = 0; c < nch; c++) {
+    if (c + 1 < nch) {
+      issue(c + 1, (c + 1) & 1);
+      wait_vmcnt<NIW>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    const float* sw = sm + (c & 1) * BUF + (rb * RT) * kRlRs;
+    const float* sx = sm + (c & 1) * BUF + (RW + tb * TT) * kRlRs;
+    const int jend = min(dm, (c + 1) * kRlCk) - c * kRlCk;
+#pragma unroll 4
+    for (int j = k; j < jend; j += LANES) {
+      float wv[RT], xv[TT];
+#pragma unroll
+      for (int q = 0; q < RT; q++) wv[q] = sw[q * kRlRs + j];
+#pragma unroll
+      for (int i = 0; i < TT; i++) xv[i] = sx[i * kRlRs + j];
+#pragma unroll
+      for (int i = 0; i < TT; i++)
+#pragma unroll
+        for (int q = 0; q < RT; q++) {
+          if constexpr (LANES == 1) acc[i][q] += wv[q] * xv[i];
+          else acc[i][q] = __builtin_fmaf(wv[q], xv[i], acc[i][q]);
+        }
+    }
+    if (c + 1 < nch) {
+      // every thread is done with this buffer before chunk c + 2 lands in it
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+    }
+  }
+
+  // combine the LANES chains of each output (adjacent lanes) and add the tail
+  const int base = lane - k;
+  const int last0 = (nch - 1) * kRlCk;  // the tail lies in the last chunk
+  const float* lw = sm + ((nch - 1) & 1) * BUF + (rb * RT) * kRlRs;
+  const float* lx = sm + ((nch - 1) & 1) * BUF + (RW + tb * TT) * kRlRs;
+#pragma unroll
+  for (int i = 0; i < TT; i++)
+#pragma unroll
+    for (int q = 0; q < RT; q++) {
+      const int t = t0 + tb * TT + i, e = r0 + rb * RT + q;
+      float s;
+      if constexpr (LANES == 1) {
+        s = acc[i][q];
+      } else {
+        float v[LANES];
+#pragma unroll
+        for (int l = 0; l < LANES; l++) v[l] = __shfl(acc[i][q], base + l);
+        s = 0.0f;
+        if constexpr (LANES == 8) {
+#pragma unroll
+          for (int l = 0; l < 8; l++) s += v[l];
+        } else {
+          float t8[8], t4[4];
+#pragma unroll
+          for (int l = 0; l < 8; l++) t8[l] = v[8 + l] + v[l];
+#pragma unroll
+          for (int l = 0; l < 4; l++) t4[l] = t8[4 + l] + t8[l];
+          const float a02 = t4[0] + t4[2];
+          const float a13 = t4[1] + t4[3];
+          s += a02 + a13;
+        }
+        for (int j = dm; j < d; j++) s += lw[q * kRlRs + j - last0] * lx[i * kRlRs + j - last0];
+      }
+      if (k == 0 && t < T && e < E) logits[(size_t)t * E + e] = s;
+    }
+}
+
+bool rlogits_ok(int d) { return d > 0 && (d & 3) == 0; }
+
+template <int LANES, int NTB, int TT, int NRB, int RT>
+static hipError_t rlogits_launch_t(const float* W, const float* X, int T, int E, int d,
+                                   float* logits, hipStream_t st) {
+  constexpr int TW = NTB * TT, RW = NRB * RT;
+  constexpr size_t lds = rlogits_lds<TW, RW>();
+  static bool opted[64] = {false};
+  if (lds > 64 * 1024) {
+    const hipError_t e = lds_opt_in((const void*)k_rlogits<LANES, NTB, TT, NRB, RT>, opted);
+    if (e != hipSuccess) return e;
+  }
+  const dim3 grid((E + RW - 1) / RW, (T + TW - 1) / TW);
+  hipLaunchKernelGGL((k_rlogits<LANES, NTB, TT, NRB, RT>), grid, dim3(256), lds, st, W, X, T, E,
+                     d, logits);
+  return hipGetLastError();
+}
+
+// Tiles of 16 tokens x 16 router rows, or x 4 rows for few tokens (more
+// workgroups for the same work).
+hipError_t rlogits_launch(int order, const float* W, const float* X, int T, int E, int d,
+                          float* logits, hipStream_t st) {
+  if (!rlogits_ok(d) || (reinterpret_cast<uintptr_t>(W) & 15) ||
+      (reinterpret_cast<uintptr_t>(X) & 15))
+    return hipErrorInvalidValue;
+  if (T <= 0 || E <= 0) return hipSuccess;
+  const bool small = T <= 64;
+  switch (order) {
+    case QR_ORDER_SEQ: return rlogits_launch_t<1, 16, 1, 16, 1>(W, X, T, E, d, logits, st);
+    case QR_ORDER_AVX2:
+      return small ? rlogits_launch_t<8, 8, 2, 4, 1>(W, X, T, E, d, logits, st)
+                   : rlogits_launch_t<8, 4, 4, 8, 2>(W, X, T, E, d, logits, st);
+    default:
+      return small ? rlogits_launch_t<16, 4, 4, 4, 1>(W, X, T, E, d, logits, st)
+                   : rlogits_launch_t<16, 4, 4, 4, 4>(W, X, T, E, d, logits, st);
+  }
+}
+
+// One workgroup of 4 waves per token: wave 0 computes the softmax and the
+// rank keys while the others quantize the token's xb into its activation
+// records; every thread then ranks the E candidates (route_rank_wg) and wave
+// 0 writes the renormalised routing.
+__global__ __launch_bounds__(256) void k_route_rank(
+    const float* __restrict__ logits, int T, int E, int K, float* __restrict__ probs,
+    int32_t* __restrict__ idx, float* __restrict__ wts, const float* __restrict__ X, int d,
+    int perm, uint8_t* __restrict__ XQ) {
+  __shared__ __align__(16) float pw[kRouteRow];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x;
+  if (wave == 0) {
+    const ExpTab tab = qr_expf_tab();
+    float pv[4];
+    route_softmax(logits + (size_t)t * E, E, pw, lane, probs ? probs + (size_t)t * E : nullptr,
+                  tab, pv);
+    route_rank_keys(pv, E, K, pw, lane);
+  } else if (XQ) {
+    // waves 1..3: the token's activation records, 48 blocks per pass
+    const int groups = (d >> 5) * 4;
+    uint8_t* out = XQ + (size_t)t * (d >> 5) * kXQ;
+    const float* x = X + (size_t)t * d;
+    for (int g0 = 0; g0 < groups; g0 += 192) {
+      if (perm) quant_rows_group<true>(x, d, 1, d, out, g0 + (int)threadIdx.x - 64);
+      else quant_rows_group<false>(x, d, 1, d, out, g0 + (int)threadIdx.x - 64);
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  route_rank_wg(E, K, pw, (int)threadIdx.x, (int)blockDim.x);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  if (wave == 0) route_write(pw, K, lane, idx + (size_t)t * K, wts + (size_t)t * K);
+}
+
+hipError_t route_rank_launch(const float* logits, int T, int E, int K, float* probs, int32_t* idx,
+                             float* wts, const float* X, int d, bool perm, uint8_t* XQ,
+                             hipStream_t st) {
+  if (E > 256 || K > 16 || T <= 0) return T <= 0 ? hipSuccess : hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_route_rank, dim3(T), dim3(256), 0, st, logits, T, E, K, probs, idx, wts, X,
+                     d, perm ? 1 : 0, XQ);
+  return hipGetLastError();
+}
+
+}  // namespace qr

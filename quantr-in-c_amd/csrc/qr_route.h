@@ -288,6 +288,32 @@ __device__ inline void route_rank_wg(int E, int K, float* pw, int t, int nthr) {
   }
 }
 
+// One wave's top-K from the keys route_rank_keys wrote (and a wave fence):
+// lane l ranks candidates l, l + 64, ... against all E keys; a candidate of
+// rank r < K writes itself to slot r (keys are distinct, masked ones are 0).
+__device__ inline void route_rank_wave(int E, int K, float* pw, int lane) {
+  const uint64_t* keys = route_keys(pw);
+  for (int q = 0; q < E; q += 64) {  // wave-uniform
+    const int e = lane + q;
+    const uint64_t mine = e < E ? keys[e] : ~0ull;
+    int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
+    int j = 0;
+    for (; j + 4 <= E; j += 4) {
+      c0 += keys[j] > mine;
+      c1 += keys[j + 1] > mine;
+      c2 += keys[j + 2] > mine;
+      c3 += keys[j + 3] > mine;
+    }
+    for (; j < E; j++) c0 += keys[j] > mine;
+    const int r = (c0 + c1) + (c2 + c3);
+    if (e < E && mine != 0ull && r < K) {
+      route_idx(pw)[r] = e;
+      route_wts(pw)[r] = route_probs(pw)[e];
+    }
+  }
+  wave_lds_fence();
+}
+
 // Renormalised routing weights w_k / sum(w), the sum sequential in slot order
 // (src/runtime.c:224-230), written with the indices by lane 0 (from the
 // routing row filled by route_select with K passes).

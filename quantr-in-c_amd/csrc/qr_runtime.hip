@@ -27,10 +27,6 @@ struct qr_ctx {
   std::unordered_map<const void*, RegEntry> registry;
   void* moe_scratch = nullptr;
   size_t moe_scratch_bytes = 0;
-  // Fused-router completion counters: zeroed when allocated, returned to zero
-  // by every kernel that uses them.
-  unsigned* moe_counters = nullptr;
-  size_t moe_counters_bytes = 0;
 };
 
 namespace {
@@ -143,7 +139,6 @@ int qr_ctx_destroy(qr_ctx* c) {
   (void)hipStreamSynchronize(c->stream);
   for (auto& kv : c->registry) (void)hipFree(kv.second.dev);
   if (c->moe_scratch) (void)hipFree(c->moe_scratch);
-  if (c->moe_counters) (void)hipFree(c->moe_counters);
   if (c->ev0) (void)hipEventDestroy(c->ev0);
   if (c->ev1) (void)hipEventDestroy(c->ev1);
   if (c->own) (void)hipStreamDestroy(c->own);
@@ -451,28 +446,8 @@ int qr_moe_forward(qr_ctx* c, const qr_moe_layer* L, float* x, const float* xb, 
     if (e != hipSuccess) return fail(QR_ERR_NOMEM, "qr_moe_forward: scratch %zu bytes", need);
     c->moe_scratch_bytes = need;
   }
-  const size_t cneed = qr::moe_counter_bytes(T);
-  if (cneed > c->moe_counters_bytes) {
-    if (set_device(c) != QR_OK) return QR_ERR_HIP;
-    QR_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    if (c->moe_counters) (void)hipFree(c->moe_counters);
-    c->moe_counters = nullptr;
-    c->moe_counters_bytes = 0;
-    void* p = nullptr;
-    hipError_t e = hipMalloc(&p, cneed);
-    if (e != hipSuccess) return fail(QR_ERR_NOMEM, "qr_moe_forward: counters %zu bytes", cneed);
-    e = hipMemsetAsync(p, 0, cneed, c->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    if (e != hipSuccess) {
-      (void)hipFree(p);
-      return hip_fail(e, "qr_moe_forward: counters");
-    }
-    c->moe_counters = static_cast<unsigned*>(p);
-    c->moe_counters_bytes = cneed;
-  }
   qr::MoeScratch s;
   qr::moe_scratch_carve(c->moe_scratch, L, T, &s);
-  s.counters_route = c->moe_counters;
   QR_HIP(qr::moe_forward_launch(L, x, xb, T, order, s, c->stream), "moe_forward");
   const size_t kb = (size_t)T * L->n_used;
   if (idx_out) QR_HIP(hipMemcpyAsync(idx_out, s.idx, kb * 4, hipMemcpyDeviceToDevice, c->stream), "copy idx");
