@@ -416,6 +416,13 @@ static int blk_wg_per_cu() {
   if (v < 0) v = env_knob("QR_BLK_WG_PER_CU", 1, 16, 0);
   return v;
 }
+// QR_BLK_XS: 1 stages the activation through LDS by DMA, 2 loads it into
+// registers (less LDS per workgroup); default 1.
+static int blk_xs_mode() {
+  static int v = 0;
+  if (!v) v = env_knob("QR_BLK_XS", 1, 2, 1);
+  return v;
+}
 
 // Opt a kernel into LDS beyond 64 KiB, once per device.
 hipError_t lds_opt_in(const void* fn, bool* done) {
@@ -453,7 +460,7 @@ static hipError_t launch_blk_t(const GemvArgs& a, hipStream_t st) {
   const int nb = a.d >> 8;
   const int RB = 64 / nb;
   int D = blk_depth();
-  const bool xs = blk_xs_bytes(a.d, NT) <= kXsMax;
+  const bool xs = blk_xs_mode() == 1 && blk_xs_bytes(a.d, NT) <= kXsMax;
   if (blk_lds_bytes<TYPE>(a.d, NT, D, xs) > kLdsMax) D = 1;
   const size_t lds = blk_lds_bytes<TYPE>(a.d, NT, D, xs);
   if (lds > kLdsMax) return hipErrorInvalidValue;  // excluded by gemv_blk_ok

@@ -22,6 +22,8 @@
 // (the order a nibble dword unpacks to), Q8_0 with natural order.
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "qr_blk.h"
 #include "qr_tokens.h"
 #include "qr_internal.h"
@@ -93,21 +95,35 @@ __device__ inline long unit_a(const uint32_t* wl, int o, int s, int kg) {
   return (long)((uint64_t)lo | ((uint64_t)hi << 32));
 }
 
-// fp32 scale (and min) of unit s of a staged row.
+// fp32 scales (and mins) of the four units s0 .. s0 + 3 of a staged row (0
+// past unit su), the row's header decoded once.
 template <int TYPE>
-__device__ inline void unit_scale(const uint32_t* wl, int o, int s, float* sc, float* mn) {
+__device__ inline void unit_scales4(const uint32_t* wl, int o, int s0, int su, float (&sc)[4],
+                                    float (&mn)[4]) {
   if constexpr (TYPE == QR_T_Q4_K || TYPE == QR_T_Q5_K) {
     const uint32_t h0 = wl[o >> 2];
-    const uint32_t sbyte = (wl[(o + 4 + s) >> 2] >> (8 * ((4 + s) & 3))) & 0xFFu;
-    *sc = (float)(sbyte & 63u) * qr_h2f(h0 & 0xFFFFu);
-    *mn = (float)(sbyte >> 6) * qr_h2f(h0 >> 16);
+    const float d = qr_h2f(h0 & 0xFFFFu), dm = qr_h2f(h0 >> 16);
+    const uint32_t w = wl[(o + 4 + s0) >> 2];  // 16-byte aligned stage: o % 4 == 0
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t b = (w >> (8 * i)) & 0xFFu;
+      sc[i] = (float)(b & 63u) * d;
+      mn[i] = (float)(b >> 6) * dm;
+    }
   } else if constexpr (TYPE == QR_T_Q6_K) {
-    const int scale = (int)(int8_t)(lds_u32(wl, o + 192 + s) & 0xFFu);
-    *sc = (float)scale * qr_h2f(lds_u32(wl, o + 208) & 0xFFFFu);
-    *mn = 0.0f;
+    const float d = qr_h2f(lds_u32(wl, o + 208) & 0xFFFFu);
+    const uint32_t w = lds_u32(wl, o + 192 + s0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      sc[i] = (float)(int)(int8_t)((w >> (8 * i)) & 0xFFu) * d;
+      mn[i] = 0.0f;
+    }
   } else {
-    *sc = qr_h2f(lds_u32(wl, o + QR_Q8_BYTES * s) & 0xFFFFu);
-    *mn = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      sc[i] = s0 + i < su ? qr_h2f(lds_u32(wl, o + QR_Q8_BYTES * (s0 + i)) & 0xFFFFu) : 0.0f;
+      mn[i] = 0.0f;
+    }
   }
 }
 
@@ -142,6 +158,7 @@ struct MfmaArgs {
   // product ([P][rows/32], PERM order if qperm), quantized from the tile
   uint8_t* QO;
   int qperm;
+  int skinny;             // work items of at most 4 pairs take the skinny form
 };
 
 template <int TYPE, bool GATEUP, int NJ, int RA, int D, int NW>
@@ -225,9 +242,10 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
   // matrix and lanes past the wave's chunks reload the workgroup's first row's
   // stage start.
   const size_t ebase = (size_t)e * a.slice;
-  size_t wrow[G::WI];     // row start (within the tensor), or ~0 if no row
+  const uint32_t row0 = (uint32_t)(blockIdx.x * G::MR) * (uint32_t)rb;  // within the slice
+  const uint8_t* wbase[G::WI];  // the chunk's matrix, at the expert's slice
+  uint32_t wroff[G::WI];        // its row's offset in the slice, or ~0 (no row)
   int wch[G::WI];
-  const uint8_t* wmat[G::WI];
 #pragma unroll
   for (int k = 0; k < G::WI; k++) {
     const int c = k * 64 + lane;
@@ -236,10 +254,9 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
     const int rr = rem / NCH;
     wch[k] = rem - rr * NCH;
     const int row = rw0 + rr;
-    wrow[k] = (c < G::WCH && row < a.rows) ? ebase + (size_t)row * rb : ~(size_t)0;
-    wmat[k] = (GATEUP && m == 1) ? a.W2 : a.W1;
+    wroff[k] = (c < G::WCH && row < a.rows) ? (uint32_t)row * (uint32_t)rb : ~0u;
+    wbase[k] = ((GATEUP && m == 1) ? a.W2 : a.W1) + ebase;
   }
-  const size_t row0 = ebase + (size_t)(blockIdx.x * G::MR) * rb;
   // Activation chunk c = (wave AI + k) 64 + lane: pair c / APC, chunk c % APC
   // of its 8 records (unit (c % APC) / 3; chunk 24 is the pad).  asrc: the
   // chunk's offset in XQ at stage 0, or ~0 (reload pair 0's first chunk).
@@ -266,184 +283,234 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
       const size_t src = (ok ? asrc[k] : asrc0) + (size_t)(8 * st) * kXQ;
       lds_dma16(a.XQ + src, abase + (uint32_t)(k * 1024));
     }
-    const uint32_t wbase = lds_u32addr(smem + G::O_W + (wave * D + slot) * G::WST);
-    const size_t s0 = (size_t)st * KST;
-    const size_t clampsrc = (row0 + s0) & ~(size_t)15;
+    const uint32_t wlds = lds_u32addr(smem + G::O_W + (wave * D + slot) * G::WST);
+    // offsets within the expert's slice: its base is 16-byte aligned, so
+    // alignment within the slice is alignment in memory
+    const uint32_t s0 = (uint32_t)st * KST;
+    const uint32_t se = s0 + KST < (uint32_t)rb ? s0 + KST : (uint32_t)rb;
+    const uint32_t clampoff = (row0 + s0) & ~15u;
 #pragma unroll
     for (int k = 0; k < G::WI; k++) {
-      size_t src = clampsrc;
-      const uint8_t* W = a.W1;
-      if (wrow[k] != ~(size_t)0) {
-        const size_t start = wrow[k] + s0;
-        const size_t end = wrow[k] + (s0 + KST < rb ? s0 + KST : rb);
-        const size_t off = (start & ~(size_t)15) + 16 * (size_t)wch[k];
-        if (off < end) {
-          src = off;
-          W = wmat[k];
+      uint32_t off = clampoff;
+      const uint8_t* W = a.W1 + ebase;
+      if (wroff[k] != ~0u) {
+        const uint32_t o = ((wroff[k] + s0) & ~15u) + 16u * (uint32_t)wch[k];
+        if (o < wroff[k] + se) {
+          off = o;
+          W = wbase[k];
         }
       }
-      lds_dma16(W + src, wbase + (uint32_t)(k * 1024));
+      lds_dma16(W + off, wlds + (uint32_t)(k * 1024));
     }
   };
-
-  float acc[NMAT][RA][NJ][4];
-#pragma unroll
-  for (int m = 0; m < NMAT; m++)
-#pragma unroll
-    for (int r = 0; r < RA; r++)
-#pragma unroll
-      for (int j = 0; j < NJ; j++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[m][r][j][i] = 0.0f;
 
   float* scl = reinterpret_cast<float*>(smem + G::O_S + wave * G::SCL);
   float* mnl = reinterpret_cast<float*>(smem + G::O_M + wave * G::SCL);
 
+  // The stage loop and the outputs, in two forms.  Full: an MFMA per (unit,
+  // matrix, 16-row tile, 16-pair column tile), A = weights, B = pairs; lane
+  // (ln, kg) accumulates rows 4 kg + i of pair 16 j + ln.  Skinny (a work
+  // item of at most 4 pairs): A = the pairs with each pair's 32 elements split
+  // into 4 k-quarters on 4 A rows (row 4 t + q holds pair t's quarter q, zeros
+  // elsewhere), B = weights; lane (ln, kg) receives the 4 quarter sums of pair
+  // kg and row ln, adds them (exact integers) and forms one term -- a quarter
+  // of the full form's epilogue work for the same 16 rows.
+  auto run = [&](auto skinny_tag) {
+    constexpr bool SK = decltype(skinny_tag)::value;
+    float acc[NMAT][RA][NJ][4];
 #pragma unroll
-  for (int s = 0; s < D - 1; s++)
-    if (s < nstage) issue(s);
-  for (int st = 0; st < nstage; st++) {
-    // stage st has landed once no more than the later stages' DMA is in flight
-    if (D == 3 && st + 1 < nstage) wait_vmcnt<G::NI>();
-    else wait_vmcnt<0>();
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    if (st + D - 1 < nstage) issue(st + D - 1);
-    const int slot = st % D;
-    const uint32_t* wl = reinterpret_cast<const uint32_t*>(smem + G::O_W + (wave * D + slot) * G::WST);
-    const uint8_t* as = smem + slot * G::AST;
-    const int su = min(8, U - st * 8);
-    const size_t s0 = (size_t)st * KST;
-    // scales and mins of the wave's (matrix, unit, row)s: entry
-    // (m * 8 + s) * WR + rr
+    for (int m = 0; m < NMAT; m++)
 #pragma unroll
-    for (int q = 0; q < G::NSC / 64; q++) {
-      const int i = q * 64 + lane;
-      const int m = i / (8 * WR), s = (i / WR) & 7, rr = i % WR;
-      float sc = 0.0f, mn = 0.0f;
-      const int row = rw0 + rr;
-      if (s < su && row < a.rows) {
-        const int hd = (int)((ebase + (size_t)row * rb + s0) & 15);
-        unit_scale<TYPE>(wl, (m * WR + rr) * G::SLOT + hd, s, &sc, &mn);
+      for (int r = 0; r < RA; r++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[m][r][j][i] = 0.0f;
+
+#pragma unroll
+    for (int s = 0; s < D - 1; s++)
+      if (s < nstage) issue(s);
+    for (int st = 0; st < nstage; st++) {
+      // stage st has landed once no more than the later stages' DMA is in flight
+      if (D == 3 && st + 1 < nstage) wait_vmcnt<G::NI>();
+      else wait_vmcnt<0>();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      if (st + D - 1 < nstage) issue(st + D - 1);
+      const int slot = st % D;
+      const uint32_t* wl =
+          reinterpret_cast<const uint32_t*>(smem + G::O_W + (wave * D + slot) * G::WST);
+      const uint8_t* as = smem + slot * G::AST;
+      const int su = min(8, U - st * 8);
+      const uint32_t s0 = (uint32_t)st * KST;
+      // scales and mins of the wave's (matrix, unit, row)s, entry
+      // (m * 8 + s) * WR + rr: lane (m, rr, half) decodes row rr's header once
+      // for units 4 half .. 4 half + 3
+      for (int i = lane; i < NMAT * WR * 2; i += 64) {
+        const int m = i / (2 * WR), rem = i - m * 2 * WR;
+        const int rr = rem >> 1, half = rem & 1;
+        float sc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mn[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const int row = rw0 + rr;
+        if (4 * half < su && row < a.rows) {
+          const int hd = (int)(((uint32_t)row * (uint32_t)rb + s0) & 15u);
+          unit_scales4<TYPE>(wl, (m * WR + rr) * G::SLOT + hd, 4 * half, su, sc, mn);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          scl[(m * 8 + 4 * half + q) * WR + rr] = sc[q];
+          mnl[(m * 8 + 4 * half + q) * WR + rr] = mn[q];
+        }
       }
-      scl[i] = sc;
-      mnl[i] = mn;
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    // head bytes of this lane's A rows (both matrices share them: same slice
-    // and row sizes, 16-byte aligned bases)
-    int hA[RA];
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      // head bytes of this lane's weight rows (both matrices share them: same
+      // slice and row sizes, 16-byte aligned bases)
+      int hA[RA];
 #pragma unroll
-    for (int r = 0; r < RA; r++)
-      hA[r] = (int)((ebase + (size_t)(rw0 + 16 * r + ln) * rb + s0) & 15);
-    auto unit_step = [&](int s) {
-      long A[NMAT][RA];
-#pragma unroll
-      for (int m = 0; m < NMAT; m++)
-#pragma unroll
-        for (int r = 0; r < RA; r++)
-          A[m][r] = unit_a<TYPE>(wl, (m * WR + 16 * r + ln) * G::SLOT + hA[r], s, kg);
-#pragma unroll
-      for (int j = 0; j < NJ; j++) {
-        const uint8_t* rec = as + (16 * j + ln) * (16 * G::APC) + s * kXQ;
-        const uint2 bq = *reinterpret_cast<const uint2*>(rec + 8 * kg);
-        const long B = (long)((uint64_t)bq.x | ((uint64_t)bq.y << 32));
-        const float bd = *reinterpret_cast<const float*>(rec + 32);
-        const float bsf = *reinterpret_cast<const float*>(rec + 36);
-        const int bs = *reinterpret_cast<const int*>(rec + 40);
+      for (int r = 0; r < RA; r++)
+        hA[r] = (int)(((uint32_t)(rw0 + 16 * r + ln) * (uint32_t)rb + s0) & 15u);
+      auto term_of = [&](float sc, float mn, int isum, float bd, float bsf, int bs) {
+        if constexpr (MF<TYPE>::kMin) return (sc * (float)isum - mn * bsf) * bd;
+        else if constexpr (TYPE == QR_T_Q6_K) return sc * (float)(isum - 32 * bs) * bd;
+        else return (float)isum * sc * bd;
+      };
+      auto unit_step = [&](int s) {
+        long Wq[NMAT][RA];
 #pragma unroll
         for (int m = 0; m < NMAT; m++)
 #pragma unroll
-          for (int r = 0; r < RA; r++) {
-            const v4i zero = {0, 0, 0, 0};
-            const v4i Dv = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[m][r], B, zero, 0, 0, 0);
-            const int si = (m * 8 + s) * WR + 16 * r + 4 * kg;
-            const float4 sc4 = *reinterpret_cast<const float4*>(scl + si);
-            const float4 mn4 = *reinterpret_cast<const float4*>(mnl + si);
-            const float scv[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
-            const float mnv[4] = {mn4.x, mn4.y, mn4.z, mn4.w};
+          for (int r = 0; r < RA; r++)
+            Wq[m][r] = unit_a<TYPE>(wl, (m * WR + 16 * r + ln) * G::SLOT + hA[r], s, kg);
+        if constexpr (SK) {
+          // A: pair ln / 4's quarter ln % 4 on A row ln (zeros in the other
+          // k-groups); the term's pair is kg
+          const uint8_t* ra = as + (ln >> 2) * (16 * G::APC) + s * kXQ;
+          const uint2 xq = *reinterpret_cast<const uint2*>(ra + 8 * kg);
+          const bool mine = kg == (ln & 3);
+          const long Aq = mine ? (long)((uint64_t)xq.x | ((uint64_t)xq.y << 32)) : 0l;
+          const uint8_t* rt = as + kg * (16 * G::APC) + s * kXQ;
+          const float bd = *reinterpret_cast<const float*>(rt + 32);
+          const float bsf = *reinterpret_cast<const float*>(rt + 36);
+          const int bs = *reinterpret_cast<const int*>(rt + 40);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-              float term;
-              if constexpr (MF<TYPE>::kMin) {
-                term = (scv[i] * (float)Dv[i] - mnv[i] * bsf) * bd;
-              } else if constexpr (TYPE == QR_T_Q6_K) {
-                term = scv[i] * (float)(Dv[i] - 32 * bs) * bd;
-              } else {
-                term = (float)Dv[i] * scv[i] * bd;
-              }
-              acc[m][r][j][i] += term;
+          for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int r = 0; r < RA; r++) {
+              const v4i zero = {0, 0, 0, 0};
+              const v4i Dv = __builtin_amdgcn_mfma_i32_16x16x32_i8(Aq, Wq[m][r], zero, 0, 0, 0);
+              const int isum = (Dv[0] + Dv[1]) + (Dv[2] + Dv[3]);
+              const int si = (m * 8 + s) * WR + 16 * r + ln;
+              acc[m][r][0][0] += term_of(scl[si], mnl[si], isum, bd, bsf, bs);
             }
+        } else {
+#pragma unroll
+          for (int j = 0; j < NJ; j++) {
+            const uint8_t* rec = as + (16 * j + ln) * (16 * G::APC) + s * kXQ;
+            const uint2 bq = *reinterpret_cast<const uint2*>(rec + 8 * kg);
+            const long B = (long)((uint64_t)bq.x | ((uint64_t)bq.y << 32));
+            const float bd = *reinterpret_cast<const float*>(rec + 32);
+            const float bsf = *reinterpret_cast<const float*>(rec + 36);
+            const int bs = *reinterpret_cast<const int*>(rec + 40);
+#pragma unroll
+            for (int m = 0; m < NMAT; m++)
+#pragma unroll
+              for (int r = 0; r < RA; r++) {
+                const v4i zero = {0, 0, 0, 0};
+                const v4i Dv = __builtin_amdgcn_mfma_i32_16x16x32_i8(Wq[m][r], B, zero, 0, 0, 0);
+                const int si = (m * 8 + s) * WR + 16 * r + 4 * kg;
+                const float4 sc4 = *reinterpret_cast<const float4*>(scl + si);
+                const float4 mn4 = *reinterpret_cast<const float4*>(mnl + si);
+                const float scv[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
+                const float mnv[4] = {mn4.x, mn4.y, mn4.z, mn4.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                  acc[m][r][j][i] += term_of(scv[i], mnv[i], Dv[i], bd, bsf, bs);
+              }
           }
+        }
+      };
+      if (su == 8) {
+        // every stage of a K-quant, and whole Q8_0 stages: unrolled, so the
+        // units' LDS reads and MFMAs interleave
+#pragma unroll
+        for (int s = 0; s < 8; s++) unit_step(s);
+      } else {
+        for (int s = 0; s < su; s++) unit_step(s);
+      }
+    }
+
+    // output element (j, i) of row tile r: pair tt, row
+    auto out_pos = [&](int r, int j, int i, int* tt, int* row) {
+      if constexpr (SK) {
+        *tt = kg;
+        *row = rw0 + 16 * r + ln;
+      } else {
+        *tt = 16 * j + ln;
+        *row = rw0 + 16 * r + 4 * kg + i;
       }
     };
-    if (su == 8) {
-      // every stage of a K-quant, and whole Q8_0 stages: unrolled, so the
-      // units' LDS reads and MFMAs interleave
-#pragma unroll
-      for (int s = 0; s < 8; s++) unit_step(s);
-    } else {
-      for (int s = 0; s < su; s++) unit_step(s);
-    }
-  }
+    constexpr int OJ = SK ? 1 : NJ, OI = SK ? 1 : 4;
 
-  if constexpr (GATEUP) {
-    if (a.QO) {
-      // hb = silu(up) * gate of the tile's rows and pairs -> LDS [NTOK][MR]
-      // (the activation ring is free now) -> whole 32-row blocks per pair
-      // quantized (quantize_row_q8_0, as the down product's matmul_q_fused
-      // does) into the down product's activation records
-      float* ob = reinterpret_cast<float*>(smem);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      __builtin_amdgcn_s_barrier();  // every wave is done with the last stage
+    if constexpr (GATEUP) {
+      if (a.QO) {
+        // hb = silu(up) * gate of the tile's rows and pairs -> LDS [NTOK][MR]
+        // (the activation ring is free now) -> whole 32-row blocks per pair
+        // quantized (quantize_row_q8_0, as the down product's matmul_q_fused
+        // does) into the down product's activation records
+        float* ob = reinterpret_cast<float*>(smem);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // every wave is done with the last stage
 #pragma unroll
-      for (int j = 0; j < NJ; j++)
+        for (int j = 0; j < OJ; j++)
 #pragma unroll
-        for (int r = 0; r < RA; r++)
+          for (int r = 0; r < RA; r++)
 #pragma unroll
-          for (int i = 0; i < 4; i++)
-            ob[(16 * j + ln) * G::MR + wave * WR + 16 * r + 4 * kg + i] =
-                qr_silu(acc[0][r][j][i]) * acc[NMAT - 1][r][j][i];
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      constexpr int NB = G::MR / 32;  // blocks per pair in the tile
-      const int nrec = a.rows >> 5;
-      for (int g = threadIdx.x; g < G::NTOK * NB * 4; g += 64 * NW) {  // whole quads
-        const int tt = g / (NB * 4), rem = g - tt * (NB * 4);
-        const int blk = rem >> 2, part = rem & 3;
-        const float* src = ob + tt * G::MR + blk * 32 + part * 8;
-        float v[8];
+            for (int i = 0; i < OI; i++) {
+              int tt, row;
+              out_pos(r, j, i, &tt, &row);
+              ob[tt * G::MR + (row - blockIdx.x * G::MR)] =
+                  qr_silu(acc[0][r][j][i]) * acc[NMAT - 1][r][j][i];
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        constexpr int NB = G::MR / 32;  // blocks per pair in the tile
+        constexpr int NT = SK ? 4 : G::NTOK;
+        const int nrec = a.rows >> 5;
+        for (int g = threadIdx.x; g < NT * NB * 4; g += 64 * NW) {  // whole quads
+          const int tt = g / (NB * 4), rem = g - tt * (NB * 4);
+          const int blk = rem >> 2, part = rem & 3;
+          const float* src = ob + tt * G::MR + blk * 32 + part * 8;
+          float v[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = src[i];
-        uint2 q8;
-        float bd;
-        int bs;
-        if (a.qperm) quant8_core<true>(v, &q8, &bd, &bs);
-        else quant8_core<false>(v, &q8, &bd, &bs);
-        const int row0 = blockIdx.x * G::MR + blk * 32;
-        if (tt < np && row0 < a.rows)
-          record_store(a.QO + ((size_t)(p0 + tt) * nrec + (row0 >> 5)) * kXQ, part, q8, bd, bs);
+          for (int i = 0; i < 8; i++) v[i] = src[i];
+          uint2 q8;
+          float bd;
+          int bs;
+          if (a.qperm) quant8_core<true>(v, &q8, &bd, &bs);
+          else quant8_core<false>(v, &q8, &bd, &bs);
+          const int row0 = blockIdx.x * G::MR + blk * 32;
+          if (tt < np && row0 < a.rows)
+            record_store(a.QO + ((size_t)(p0 + tt) * nrec + (row0 >> 5)) * kXQ, part, q8, bd, bs);
+        }
+        return;
       }
-      return;
     }
-  }
 
-  // outputs: rows rw0 + 16 r + 4 kg + i, pairs 16 j + ln
 #pragma unroll
-  for (int j = 0; j < NJ; j++) {
-    const int tt = 16 * j + ln;
-    if (tt >= np) continue;
+    for (int j = 0; j < OJ; j++)
 #pragma unroll
-    for (int r = 0; r < RA; r++)
+      for (int r = 0; r < RA; r++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int row = rw0 + 16 * r + 4 * kg + i;
-        if (row >= a.rows) continue;
-        float out = acc[0][r][j][i];
-        if constexpr (GATEUP) out = qr_silu(acc[0][r][j][i]) * acc[NMAT - 1][r][j][i];
-        a.Y[(size_t)(p0 + tt) * a.ystride + row] = out;
-      }
-  }
+        for (int i = 0; i < OI; i++) {
+          int tt, row;
+          out_pos(r, j, i, &tt, &row);
+          if (tt >= np || row >= a.rows) continue;
+          float out = acc[0][r][j][i];
+          if constexpr (GATEUP) out = qr_silu(acc[0][r][j][i]) * acc[NMAT - 1][r][j][i];
+          a.Y[(size_t)(p0 + tt) * a.ystride + row] = out;
+        }
+  };
+  if (np <= 4 && a.skinny) run(std::true_type{});
+  else run(std::false_type{});
 }
 
 // ---------------------------------------------------------------------------
@@ -537,6 +604,7 @@ hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const ui
                               const int32_t* tiles, float* Y, int ystride, int items, int tile,
                               uint8_t* QO, bool qperm, hipStream_t st) {
   if (tile != 16 && tile != 32) return hipErrorInvalidValue;
+  if (slice >= ((size_t)1 << 32)) return hipErrorInvalidValue;  // 32-bit offsets in a slice
   if (QO && (!gateup || (rows & 31) || (reinterpret_cast<uintptr_t>(QO) & 15)))
     return hipErrorInvalidValue;
   if ((reinterpret_cast<uintptr_t>(W1) & 15) || (gateup && (reinterpret_cast<uintptr_t>(W2) & 15)) ||
@@ -559,6 +627,14 @@ hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const ui
   a.ystride = ystride;
   a.QO = QO;
   a.qperm = qperm ? 1 : 0;
+  {
+    static int knob = -1;  // QR_MFMA_SKINNY=0 turns the skinny form off (tuning sweeps)
+    if (knob < 0) {
+      const char* e = getenv("QR_MFMA_SKINNY");
+      knob = (e && e[0] == '0') ? 0 : 1;
+    }
+    a.skinny = knob;
+  }
   switch (type) {
     case QR_T_Q4_K: return gateup ? mfma_launch_nj<QR_T_Q4_K, true>(a, items, tile, st)
                                   : mfma_launch_nj<QR_T_Q4_K, false>(a, items, tile, st);
