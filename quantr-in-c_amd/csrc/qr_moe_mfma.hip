@@ -315,8 +315,12 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
   // elsewhere), B = weights; lane (ln, kg) receives the 4 quarter sums of pair
   // kg and row ln, adds them (exact integers) and forms one term -- a quarter
   // of the full form's epilogue work for the same 16 rows.
-  auto run = [&](auto skinny_tag) {
-    constexpr bool SK = decltype(skinny_tag)::value;
+  auto run = [&](auto form_tag) {
+    // form: 0 skinny, else the number of 16-pair column tiles computed (the
+    // work item's pairs need no more)
+    constexpr int FORM = decltype(form_tag)::value;
+    constexpr bool SK = FORM == 0;
+    constexpr int NJA = SK ? 1 : FORM;
     float acc[NMAT][RA][NJ][4];
 #pragma unroll
     for (int m = 0; m < NMAT; m++)
@@ -403,7 +407,7 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
             }
         } else {
 #pragma unroll
-          for (int j = 0; j < NJ; j++) {
+          for (int j = 0; j < NJA; j++) {
             const uint8_t* rec = as + (16 * j + ln) * (16 * G::APC) + s * kXQ;
             const uint2 bq = *reinterpret_cast<const uint2*>(rec + 8 * kg);
             const long B = (long)((uint64_t)bq.x | ((uint64_t)bq.y << 32));
@@ -448,7 +452,7 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
         *row = rw0 + 16 * r + 4 * kg + i;
       }
     };
-    constexpr int OJ = SK ? 1 : NJ, OI = SK ? 1 : 4;
+    constexpr int OJ = NJA, OI = SK ? 1 : 4;
 
     if constexpr (GATEUP) {
       if (a.QO) {
@@ -473,7 +477,7 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         constexpr int NB = G::MR / 32;  // blocks per pair in the tile
-        constexpr int NT = SK ? 4 : G::NTOK;
+        constexpr int NT = SK ? 4 : 16 * NJA;
         const int nrec = a.rows >> 5;
         for (int g = threadIdx.x; g < NT * NB * 4; g += 64 * NW) {  // whole quads
           const int tt = g / (NB * 4), rem = g - tt * (NB * 4);
@@ -509,8 +513,9 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
           a.Y[(size_t)(p0 + tt) * a.ystride + row] = out;
         }
   };
-  if (np <= 4 && a.skinny) run(std::true_type{});
-  else run(std::false_type{});
+  if (np <= 4 && a.skinny) run(std::integral_constant<int, 0>{});
+  else if (NJ == 1 || np <= 16) run(std::integral_constant<int, 1>{});
+  else run(std::integral_constant<int, NJ>{});
 }
 
 // ---------------------------------------------------------------------------

@@ -29,12 +29,13 @@ namespace qr {
 constexpr int kRlCk = 256;          // elements per chunk: one 1 KiB DMA per row
 constexpr int kRlRs = kRlCk + 8;    // LDS row stride (floats): 8-bank skew per row
 
-template <int TW, int RW>
+template <int TW, int RW, int NBUF>
 __host__ __device__ constexpr size_t rlogits_lds() {
-  return (size_t)2 * (TW + RW) * kRlRs * 4;
+  return (size_t)NBUF * (TW + RW) * kRlRs * 4;
 }
 
-template <int LANES, int NTB, int TT, int NRB, int RT>
+// NBUF chunk buffers: NBUF - 1 chunks in flight while one is consumed.
+template <int LANES, int NTB, int TT, int NRB, int RT, int NBUF>
 __global__ __launch_bounds__(256) void k_rlogits(const float* __restrict__ W,
                                                  const float* __restrict__ X, int T, int E, int d,
                                                  float* __restrict__ logits) {
@@ -42,6 +43,7 @@ __global__ __launch_bounds__(256) void k_rlogits(const float* __restrict__ W,
   constexpr int TW = NTB * TT, RW = NRB * RT;
   static_assert((TW + RW) % 4 == 0, "rows per wave");
   constexpr int NIW = (TW + RW) / 4;  // DMA instructions per wave and chunk
+  static_assert(NIW * (NBUF - 1) <= 63, "vmcnt range");
   constexpr int BUF = (TW + RW) * kRlRs;
   extern __shared__ __align__(16) float sm[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -73,18 +75,25 @@ __global__ __launch_bounds__(256) void k_rlogits(const float* __restrict__ W,
 #pragma unroll
     for (int q = 0; q < RT; q++) acc[i][q] = 0.0f;
 
-  issue(0, 0);
+#pragma unroll
+  for (int c = 0; c < NBUF - 1; c++)
+    if (c < nch) issue(c, c);
   for (int c = 0; c < nch; c++) {
-    if (c + 1 < nch) {
-      issue(c + 1, (c + 1) & 1);
-      wait_vmcnt<NIW>();
-    } else {
-      wait_vmcnt<0>();
+    if (c + NBUF - 1 < nch) issue(c + NBUF - 1, (c + NBUF - 1) % NBUF);
+    // chunk c has landed once only the later chunks' DMA is in flight
+    const int later = min(NBUF - 1, nch - 1 - c);
+    switch (later) {
+      case 0: wait_vmcnt<0>(); break;
+      case 1: wait_vmcnt<NIW>(); break;
+      case 2: wait_vmcnt<(NBUF > 2 ? 2 : 0) * NIW>(); break;
+      case 3: wait_vmcnt<(NBUF > 3 ? 3 : 0) * NIW>(); break;
+      case 4: wait_vmcnt<(NBUF > 4 ? 4 : 0) * NIW>(); break;
+      default: wait_vmcnt<(NBUF > 5 ? 5 : 0) * NIW>(); break;
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
-    const float* sw = sm + (c & 1) * BUF + (rb * RT) * kRlRs;
-    const float* sx = sm + (c & 1) * BUF + (RW + tb * TT) * kRlRs;
+    const float* sw = sm + (c % NBUF) * BUF + (rb * RT) * kRlRs;
+    const float* sx = sm + (c % NBUF) * BUF + (RW + tb * TT) * kRlRs;
     const int jend = min(dm, (c + 1) * kRlCk) - c * kRlCk;
 #pragma unroll 4
     for (int j = k; j < jend; j += LANES) {
@@ -101,8 +110,8 @@ __global__ __launch_bounds__(256) void k_rlogits(const float* __restrict__ W,
           else acc[i][q] = __builtin_fmaf(wv[q], xv[i], acc[i][q]);
         }
     }
-    if (c + 1 < nch) {
-      // every thread is done with this buffer before chunk c + 2 lands in it
+    if (c + NBUF < nch) {
+      // every thread is done with this buffer before chunk c + NBUF lands in it
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
     }
@@ -111,8 +120,8 @@ __global__ __launch_bounds__(256) void k_rlogits(const float* __restrict__ W,
   // combine the LANES chains of each output (adjacent lanes) and add the tail
   const int base = lane - k;
   const int last0 = (nch - 1) * kRlCk;  // the tail lies in the last chunk
-  const float* lw = sm + ((nch - 1) & 1) * BUF + (rb * RT) * kRlRs;
-  const float* lx = sm + ((nch - 1) & 1) * BUF + (RW + tb * TT) * kRlRs;
+  const float* lw = sm + ((nch - 1) % NBUF) * BUF + (rb * RT) * kRlRs;
+  const float* lx = sm + ((nch - 1) % NBUF) * BUF + (RW + tb * TT) * kRlRs;
 #pragma unroll
   for (int i = 0; i < TT; i++)
 #pragma unroll
@@ -147,24 +156,27 @@ __global__ __launch_bounds__(256) void k_rlogits(const float* __restrict__ W,
 
 bool rlogits_ok(int d) { return d > 0 && (d & 3) == 0; }
 
-template <int LANES, int NTB, int TT, int NRB, int RT>
+template <int LANES, int NTB, int TT, int NRB, int RT, int NBUF>
 static hipError_t rlogits_launch_t(const float* W, const float* X, int T, int E, int d,
                                    float* logits, hipStream_t st) {
   constexpr int TW = NTB * TT, RW = NRB * RT;
-  constexpr size_t lds = rlogits_lds<TW, RW>();
+  constexpr size_t lds = rlogits_lds<TW, RW, NBUF>();
+  static_assert(lds <= 160 * 1024, "LDS");
   static bool opted[64] = {false};
   if (lds > 64 * 1024) {
-    const hipError_t e = lds_opt_in((const void*)k_rlogits<LANES, NTB, TT, NRB, RT>, opted);
+    const hipError_t e =
+        lds_opt_in((const void*)k_rlogits<LANES, NTB, TT, NRB, RT, NBUF>, opted);
     if (e != hipSuccess) return e;
   }
   const dim3 grid((E + RW - 1) / RW, (T + TW - 1) / TW);
-  hipLaunchKernelGGL((k_rlogits<LANES, NTB, TT, NRB, RT>), grid, dim3(256), lds, st, W, X, T, E,
-                     d, logits);
+  hipLaunchKernelGGL((k_rlogits<LANES, NTB, TT, NRB, RT, NBUF>), grid, dim3(256), lds, st, W, X,
+                     T, E, d, logits);
   return hipGetLastError();
 }
 
 // Tiles of 16 tokens x 16 router rows, or x 4 rows for few tokens (more
-// workgroups for the same work).
+// workgroups for the same work); two chunk buffers (deeper rings measured no
+// faster).
 hipError_t rlogits_launch(int order, const float* W, const float* X, int T, int E, int d,
                           float* logits, hipStream_t st) {
   if (!rlogits_ok(d) || (reinterpret_cast<uintptr_t>(W) & 15) ||
@@ -173,13 +185,13 @@ hipError_t rlogits_launch(int order, const float* W, const float* X, int T, int 
   if (T <= 0 || E <= 0) return hipSuccess;
   const bool small = T <= 64;
   switch (order) {
-    case QR_ORDER_SEQ: return rlogits_launch_t<1, 16, 1, 16, 1>(W, X, T, E, d, logits, st);
+    case QR_ORDER_SEQ: return rlogits_launch_t<1, 16, 1, 16, 1, 2>(W, X, T, E, d, logits, st);
     case QR_ORDER_AVX2:
-      return small ? rlogits_launch_t<8, 8, 2, 4, 1>(W, X, T, E, d, logits, st)
-                   : rlogits_launch_t<8, 4, 4, 8, 2>(W, X, T, E, d, logits, st);
+      return small ? rlogits_launch_t<8, 8, 2, 4, 1, 2>(W, X, T, E, d, logits, st)
+                   : rlogits_launch_t<8, 4, 4, 8, 2, 2>(W, X, T, E, d, logits, st);
     default:
-      return small ? rlogits_launch_t<16, 4, 4, 4, 1>(W, X, T, E, d, logits, st)
-                   : rlogits_launch_t<16, 4, 4, 4, 4>(W, X, T, E, d, logits, st);
+      return small ? rlogits_launch_t<16, 4, 4, 4, 1, 2>(W, X, T, E, d, logits, st)
+                   : rlogits_launch_t<16, 4, 4, 4, 4, 2>(W, X, T, E, d, logits, st);
   }
 }
 
