@@ -283,6 +283,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--moe-layers", type=int, default=48)
+    ap.add_argument("--moe-t", default="1,16,512",
+                    help="token counts of the MoE leg (comma-separated), e.g. 16 for a profile")
+    ap.add_argument("--moe-steps", type=int, default=0,
+                    help="layers timed per token count (0: the defaults, 100 / 100 / 20)")
+    ap.add_argument("--no-gemv", action="store_true",
+                    help="skip the GEMV headline (profiling runs of the MoE leg; value is null)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the sharding "
@@ -292,15 +298,19 @@ def main():
     dev = Q.Device(0)
     cal = copy_calibration(dev)
     log("bench: copy kernel %.0f GB/s (read+write) over %d MB" % (cal["gbps"], cal["bytes"] >> 20))
-    g = bench_gemv(dev, Q.TYPE_Q4_K, 32000, 2048, 1, args.steps, args.warmup)
-    log("bench: Q4_K 32000x2048 T=1: %.3f us/launch, %.0f GB/s weights, %.0f GB/s algorithmic"
-        % (g["ms_per_step"] * 1e3, g["weight_gbps"], g["achieved_gbps"]))
+    g = None
+    if not args.no_gemv:
+        g = bench_gemv(dev, Q.TYPE_Q4_K, 32000, 2048, 1, args.steps, args.warmup)
+        log("bench: Q4_K 32000x2048 T=1: %.3f us/launch, %.0f GB/s weights, %.0f GB/s algorithmic"
+            % (g["ms_per_step"] * 1e3, g["weight_gbps"], g["achieved_gbps"]))
 
     moe = None
     if not args.no_moe:
         M = build_qwen3(dev, args.moe_layers)
         moe = {}
-        for T, steps in ((1, max(args.steps, 100)), (16, 100), (512, 20)):
+        default_steps = {1: max(args.steps, 100), 16: 100, 512: 20}
+        for T in [int(t) for t in args.moe_t.split(",") if t.strip()]:
+            steps = args.moe_steps or default_steps.get(T, 20)
             r = bench_moe(dev, M, T, steps, 3)
             moe["T%d" % T] = r
             log("bench: MoE Qwen3 T=%d: %.1f us/layer, %.0f tokens/s, %.1f experts touched, "
@@ -320,12 +330,12 @@ def main():
 
     out = {
         "metric": METRIC,
-        "value": round(g["weight_gbps"], 2),
+        "value": round(g["weight_gbps"], 2) if g else None,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(g["ms_per_step"], 6),
+        "ms_per_step": round(g["ms_per_step"], 6) if g else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -337,7 +347,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(g["achieved_gbps"], 2),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(g["achieved_gbps"] / HBM_PEAK_GBPS, 4),
-                     "traffic": load_traffic()},
+                     "traffic": load_traffic()} if g else None,
         "cpu_baseline": cpu,
         "moe_qwen3": moe,
         "copy_kernel_gbps": round(cal["gbps"], 1),

@@ -1,14 +1,14 @@
-// qr_moe_mfma.hip -- grouped expert products on int8 MFMA for experts that
-// receive many tokens (the MoE layer at large T).
+// qr_moe_mfma.hip -- grouped expert products on int8 MFMA (the MoE layer for
+// T > 1 tokens).
 //
-// A work item is (64 weight rows of one expert) x (up to 32 dispatched
-// (token, slot) pairs of that expert).  The K loop walks the row one "stage"
-// at a time -- one K-quant super-block, or 8 Q8_0 blocks -- staging the 64
-// rows' bytes (both matrices in gate/up mode), the pairs' quantized
-// activation blocks, and each (row, unit)'s fp32 scale and min into LDS.
-// Each 32-element unit is one v_mfma_i32_16x16x32_i8: a 16 x 16 tile of exact
-// int32 unit sums (16 rows x 16 pairs per wave, two such column tiles).  The
-// epilogue forms the reference's fp32 term of every (row, pair, unit) --
+// A work item is (64 weight rows of one expert) x (up to 16 or 32 dispatched
+// (token, slot) pairs of that expert).  The K loop walks the rows one "stage"
+// at a time -- one K-quant super-block, or 8 Q8_0 blocks -- with the rows'
+// bytes (both matrices in gate/up mode) and the pairs' quantized activation
+// records moved into LDS rings by DMA, and each (row, unit)'s fp32 scale and
+// min decoded into LDS.  Each 32-element unit is one v_mfma_i32_16x16x32_i8
+// per 16 x 16 tile of exact int32 unit sums.  The epilogue forms the
+// reference's fp32 term of every (row, pair, unit) --
 // (sc*isum - m*bsum)*bd for Q4_K/Q5_K (src/quant.c:384-400),
 // sc*isum*bd for Q6_K (src/quant.c:422-434), isum*d*bd for Q8_0
 // (src/quant.c:279-285) -- and adds it to the (row, pair) accumulator in
