@@ -14,7 +14,7 @@ import pytest
 import inputs as I
 import quantr_amd as Q
 from conftest import assert_bits_equal
-from oracle import ORDER_AVX2, ORDER_SEQ, Oracle
+from oracle import ORDER_AVX2, ORDER_AVX512, ORDER_SEQ, Oracle
 from quantr_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -176,6 +176,37 @@ def test_route_topk_probs(dev, oracle, order):
         assert_bits_equal(wts[t], w, "weights t=%d" % t)
 
 
+@pytest.mark.parametrize("dim,E,K,T,order", [
+    (1056, 60, 4, 37, ORDER_AVX512),   # a 32-element last K chunk (1056 = 4 x 256 + 32)
+    (1056, 60, 4, 37, ORDER_AVX2),
+    (288, 256, 16, 20, ORDER_SEQ),     # largest E and K
+    (544, 5, 3, 3, ORDER_AVX2),        # E below one wave, few tokens
+    (2048, 128, 8, 100, ORDER_AVX512), # the 16-token x 16-row tiles, ragged token tile
+    (1056, 128, 8, 70, ORDER_SEQ),     # sequential order, ragged tiles
+])
+def test_route_shapes(dev, oracle, dim, E, K, T, order):
+    """Tiled router logits + workgroup rank routing at widths with a partial
+    last K chunk, ragged token and expert counts, in every accumulation
+    order, against the oracle's per-token router (probabilities, indices,
+    weights bit-exact).  (The C ABI takes widths in multiples of 32, so the
+    reference's per-lane tails of matmul_omp do not arise here.)"""
+    W = I.activations(5100 + dim + E, E, dim, std=0.02)
+    W[E // 2] = W[0]  # a planted tie
+    X = I.activations(5200 + T, T, dim)
+    wb, xb = dev.upload(W), dev.upload(X)
+    L = Q.MoeLayer(dim, 768, E, K, wb.ptr, None, None, None, 0, 0, 0)
+    pb, ib, wtb = dev.alloc(T * E * 4), dev.alloc(T * K * 4), dev.alloc(T * K * 4)
+    dev.moe_route(L, xb.ptr, T, order, pb.ptr, ib.ptr, wtb.ptr)
+    probs = dev.download(pb, (T, E), np.float32)
+    idx = dev.download(ib, (T, K), np.int32)
+    wts = dev.download(wtb, (T, K), np.float32)
+    for t in range(T):
+        _, p, i, w = oracle.route(X[t], W, E, K, order)
+        assert_bits_equal(probs[t], p, "probs t=%d" % t)
+        assert (idx[t] == i).all(), "indices t=%d" % t
+        assert_bits_equal(wts[t], w, "weights t=%d" % t)
+
+
 @pytest.mark.parametrize("T,K,E", [(512, 8, 128), (64, 4, 60), (1, 8, 128), (7, 3, 5),
                                    (300, 16, 256)])
 def test_dispatch(dev, oracle, T, K, E):
@@ -252,3 +283,23 @@ def test_moe_type_pairs(dev, oracle, ut, dt, T):
     x = I.activations(seed + 4 + T, T, dim)
     xb = I.activations(seed + 5 + T, T, dim)
     check_moe(dev, oracle, layer, x, xb, ORDER_AVX2, "types %d/%d T=%d" % (ut, dt, T))
+
+
+@pytest.mark.parametrize("T", [24, 70])
+def test_moe_ragged_hidden(dev, oracle, T):
+    """The many-token MFMA path with an expert width that leaves the last
+    64-row gate/up tile half full (hidden = 288 = 9 blocks of 32) and a Q8_0
+    down product whose last K stage holds one block; T = 24 uses 16-pair work
+    items, T = 70 32-pair ones (all three item forms)."""
+    dim, hidden, E, K = 512, 288, 16, 4
+    ut, dt = Q.TYPE_Q4_K, Q.TYPE_Q8_0
+    ue, de = I.BLOCK[ut][0], I.BLOCK[dt][0]
+    seed = 7900 + T
+    up = I.blocks(seed, ut, E * hidden * (dim // ue))
+    gate = I.blocks(seed + 1, ut, E * hidden * (dim // ue))
+    down = I.blocks(seed + 2, dt, E * dim * (hidden // de))
+    router = I.activations(seed + 3, E, dim, std=0.05)
+    layer = DevLayer(dev, dim, hidden, E, K, router, up, gate, down, ut, dt)
+    x = I.activations(seed + 4, T, dim)
+    xb = I.activations(seed + 5, T, dim)
+    check_moe(dev, oracle, layer, x, xb, ORDER_AVX2, "hidden 288 T=%d" % T)
