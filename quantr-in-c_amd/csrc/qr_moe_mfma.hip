@@ -192,7 +192,7 @@ struct MfmaGeo {
   // the scale area, first written after the first stage's barrier
   static constexpr int O_X = O_S;
   static_assert(NTOK * 4 <= NW * SCL, "xrow");
-  static_assert(D == 2 || D == 3, "ring depth");
+  static_assert(D >= 1 && D <= 3, "ring depth");
   static_assert(NI <= 63, "vmcnt range");
   static_assert(NSC % 64 == 0, "scale passes");
 };
@@ -335,12 +335,21 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
     for (int s = 0; s < D - 1; s++)
       if (s < nstage) issue(s);
     for (int st = 0; st < nstage; st++) {
+      if constexpr (D == 1) {
+        // one slot: every wave is done with stage st - 1 before stage st
+        // lands in it
+        if (st > 0) {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          __builtin_amdgcn_s_barrier();
+        }
+        issue(st);
+      }
       // stage st has landed once no more than the later stages' DMA is in flight
       if (D == 3 && st + 1 < nstage) wait_vmcnt<G::NI>();
       else wait_vmcnt<0>();
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
-      if (st + D - 1 < nstage) issue(st + D - 1);
+      if (D > 1 && st + D - 1 < nstage) issue(st + D - 1);
       const int slot = st % D;
       const uint32_t* wl =
           reinterpret_cast<const uint32_t*>(smem + G::O_W + (wave * D + slot) * G::WST);
@@ -568,31 +577,39 @@ static hipError_t mfma_launch_t(const MfmaArgs& a, int items, hipStream_t st) {
 }
 
 // Kernel shape (waves per workgroup NW, each on 16 rows; ring depth D) per
-// product; the QR_MFMA_GU / QR_MFMA_DN overrides ("NW,D") are for tuning
-// sweeps.
-static void mfma_shape(bool gateup, int* nw, int* d) {
+// product.  Measured on the Qwen3-30B-A3B layer: one slot (the least LDS, the
+// most workgroups per CU) wins where the epilogue's VALU work dominates --
+// both products with 32-pair items, the 24-unit down product always -- and
+// two slots for gate/up with 16-pair items, whose eight stages are latency
+// bound.  QR_MFMA_GU / QR_MFMA_DN ("NW,D") override, for tuning sweeps.
+static void mfma_shape(bool gateup, int tile, int* nw, int* d) {
   static int cfg[2][2] = {{-1, -1}, {-1, -1}};
   int* c = cfg[gateup ? 1 : 0];
   if (c[0] < 0) {
-    c[0] = 4;
-    c[1] = 2;
+    c[0] = 0;
     const char* s = getenv(gateup ? "QR_MFMA_GU" : "QR_MFMA_DN");
     int x = 0, y = 0;
-    if (s && sscanf(s, "%d,%d", &x, &y) == 2 && (x == 4 || x == 8) && (y == 2 || y == 3)) {
+    if (s && sscanf(s, "%d,%d", &x, &y) == 2 && (x == 4 || x == 8) && (y >= 1 && y <= 3)) {
       c[0] = x;
       c[1] = y;
     }
   }
-  *nw = c[0];
-  *d = c[1];
+  if (c[0] > 0) {
+    *nw = c[0];
+    *d = c[1];
+  } else {
+    *nw = 4;
+    *d = (gateup && tile == 16) ? 2 : 1;
+  }
 }
 
 template <int TYPE, bool GATEUP, int NJ>
 static hipError_t mfma_launch_shape(const MfmaArgs& a, int items, hipStream_t st) {
   int nw, d;
-  mfma_shape(GATEUP, &nw, &d);
+  mfma_shape(GATEUP, 16 * NJ, &nw, &d);
   if (nw == 8) return d == 3 ? mfma_launch_t<TYPE, GATEUP, NJ, 3, 8>(a, items, st)
                              : mfma_launch_t<TYPE, GATEUP, NJ, 2, 8>(a, items, st);
+  if (d == 1) return mfma_launch_t<TYPE, GATEUP, NJ, 1, 4>(a, items, st);
   return d == 3 ? mfma_launch_t<TYPE, GATEUP, NJ, 3, 4>(a, items, st)
                 : mfma_launch_t<TYPE, GATEUP, NJ, 2, 4>(a, items, st);
 }
