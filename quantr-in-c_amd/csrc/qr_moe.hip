@@ -539,26 +539,67 @@ static hipError_t down1_launch(int type, const DownArgs& a, hipStream_t st) {
 
 // ---------------------------------------------------------------------------
 // T > 1 combine: x[t][i] += ((0 + y_0 w_0) + y_1 w_1 + ...) (+ shared), the
-// expert outputs gathered from their dispatch positions in slot order.
+// expert outputs gathered from their dispatch positions in slot order
+// (src/runtime.c:262-269).  Four outputs per thread: the token's K positions
+// and weights first, then all K rows' float4s, then the adds in slot order.
 // ---------------------------------------------------------------------------
+constexpr int kCombineMaxK = 16;
+
 __global__ __launch_bounds__(256) void k_combine(float* __restrict__ x, const float* __restrict__ y,
                                                  const int32_t* __restrict__ inv,
                                                  const float* __restrict__ wts, int T, int K,
                                                  int dim, const float* __restrict__ ysh,
                                                  const float* __restrict__ sgl) {
+  const int d4 = dim >> 2;
   const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (long)T * dim) return;
-  const int t = (int)(gid / dim), i = (int)(gid - (long)t * dim);
-  float acc = 0.0f;
-  for (int k = 0; k < K; k++) {
-    const int pos = inv[t * K + k];
-    if (pos >= 0) acc += y[(size_t)pos * dim + i] * wts[t * K + k];
+  if (gid >= (long)T * d4) return;
+  const int t = (int)(gid / d4), i4 = (int)(gid - (long)t * d4);
+  int pos[kCombineMaxK];
+  float w[kCombineMaxK];
+#pragma unroll
+  for (int k = 0; k < kCombineMaxK; k++) {
+    pos[k] = k < K ? inv[t * K + k] : -1;
+    w[k] = k < K ? wts[t * K + k] : 0.0f;
+  }
+  float4 v[kCombineMaxK];
+#pragma unroll
+  for (int k = 0; k < kCombineMaxK; k++)
+    if (pos[k] >= 0) v[k] = reinterpret_cast<const float4*>(y + (size_t)pos[k] * dim)[i4];
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int k = 0; k < kCombineMaxK; k++) {
+    if (pos[k] >= 0) {
+      acc.x += v[k].x * w[k];
+      acc.y += v[k].y * w[k];
+      acc.z += v[k].z * w[k];
+      acc.w += v[k].w * w[k];
+    }
   }
   if (ysh) {
     const float sg = 1.0f / (1.0f + qr_expf(-sgl[t]));
-    acc += sg * ysh[(size_t)t * dim + i];
+    const float4 s4 = reinterpret_cast<const float4*>(ysh + (size_t)t * dim)[i4];
+    acc.x += sg * s4.x;
+    acc.y += sg * s4.y;
+    acc.z += sg * s4.z;
+    acc.w += sg * s4.w;
   }
-  x[(size_t)t * dim + i] += acc;
+  float4* xp = reinterpret_cast<float4*>(x + (size_t)t * dim) + i4;
+  float4 xv = *xp;
+  xv.x += acc.x;
+  xv.y += acc.y;
+  xv.z += acc.z;
+  xv.w += acc.w;
+  *xp = xv;
+}
+
+static hipError_t combine_launch(float* x, const float* y, const int32_t* inv, const float* wts,
+                                 int T, int K, int dim, const float* ysh, const float* sgl,
+                                 hipStream_t st) {
+  if (K > kCombineMaxK || (dim & 3)) return hipErrorInvalidValue;
+  const long n4 = (long)T * (dim >> 2);
+  hipLaunchKernelGGL(k_combine, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, x, y, inv,
+                     wts, T, K, dim, ysh, sgl);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -671,10 +712,7 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
       e = shared_expert(L, xb, T, s, st);
       if (e != hipSuccess) return e;
     }
-    const long n = (long)T * L->dim;
-    hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, s.y,
-                       s.inv, s.wts, T, K, L->dim, sh ? s.ysh : nullptr, s.sgl);
-    return hipGetLastError();
+    return combine_launch(x, s.y, s.inv, s.wts, T, K, L->dim, sh ? s.ysh : nullptr, s.sgl, st);
   }
 
   e = moe_route_launch(L, xb, T, order, s.logits, nullptr, s.idx, s.wts, st);
@@ -769,10 +807,7 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
     e = shared_expert(L, xb, T, s, st);
     if (e != hipSuccess) return e;
   }
-  const long n = (long)T * L->dim;
-  hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, s.y, s.inv,
-                     s.wts, T, K, L->dim, sh ? s.ysh : nullptr, s.sgl);
-  return hipGetLastError();
+  return combine_launch(x, s.y, s.inv, s.wts, T, K, L->dim, sh ? s.ysh : nullptr, s.sgl, st);
 }
 
 }  // namespace qr

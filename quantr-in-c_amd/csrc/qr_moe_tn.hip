@@ -154,7 +154,144 @@ __global__ __launch_bounds__(256) void k_rlogits(const float* __restrict__ W,
     }
 }
 
+// The FMA-chain orders with four adjacent chains per thread: thread (cg, tb,
+// rb) runs chains 4 cg .. 4 cg + 3 of its TT x RT outputs, so each step reads
+// one float4 per token and per row (chain k's element j = s LANES + k sits
+// next to chain k + 1's); the LANES chains of an output live in LANES / 4
+// adjacent lanes and are combined as above.
+template <int LANES, int NTB, int TT, int NRB, int RT, int NBUF>
+__global__ __launch_bounds__(256) void k_rlogits4(const float* __restrict__ W,
+                                                  const float* __restrict__ X, int T, int E, int d,
+                                                  float* __restrict__ logits) {
+  constexpr int G = LANES / 4;  // threads per output
+  static_assert(LANES == 8 || LANES == 16, "FMA-chain orders");
+  static_assert(G * NTB * NRB == 256, "thread layout");
+  constexpr int TW = NTB * TT, RW = NRB * RT;
+  static_assert((TW + RW) % 4 == 0, "rows per wave");
+  constexpr int NIW = (TW + RW) / 4;
+  static_assert(NIW * (NBUF - 1) <= 63, "vmcnt range");
+  constexpr int BUF = (TW + RW) * kRlRs;
+  extern __shared__ __align__(16) float sm[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cg = tid % G, tb = (tid / G) % NTB, rb = tid / (G * NTB);
+  const int r0 = blockIdx.x * RW, t0 = blockIdx.y * TW;
+  const int nch = (d + kRlCk - 1) / kRlCk;
+  const int dm = d - d % LANES;
+
+  auto issue = [&](int c, int b) {
+    const int nb = min(kRlCk, d - c * kRlCk) * 4;
+    const int o = lane * 16;
+#pragma unroll
+    for (int n = 0; n < NIW; n++) {
+      const int i = wave + 4 * n;
+      const float* src = i < RW ? W + (size_t)min(r0 + i, E - 1) * d
+                                : X + (size_t)min(t0 + i - RW, T - 1) * d;
+      lds_dma16(reinterpret_cast<const uint8_t*>(src + c * kRlCk) + (o < nb ? o : 0),
+                lds_u32addr(sm + b * BUF + i * kRlRs));
+    }
+  };
+
+  float acc[TT][RT][4];
+#pragma unroll
+  for (int i = 0; i < TT; i++)
+#pragma unroll
+    for (int q = 0; q < RT; q++)
+#pragma unroll
+      for (int c = 0; c < 4; c++) acc[i][q][c] = 0.0f;
+
+#pragma unroll
+  for (int c = 0; c < NBUF - 1; c++)
+    if (c < nch) issue(c, c);
+  for (int c = 0; c < nch; c++) {
+    if (c + NBUF - 1 < nch) issue(c + NBUF - 1, (c + NBUF - 1) % NBUF);
+    const int later = min(NBUF - 1, nch - 1 - c);
+    switch (later) {
+      case 0: wait_vmcnt<0>(); break;
+      case 1: wait_vmcnt<NIW>(); break;
+      case 2: wait_vmcnt<(NBUF > 2 ? 2 : 0) * NIW>(); break;
+      default: wait_vmcnt<(NBUF > 3 ? 3 : 0) * NIW>(); break;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    const float* sw = sm + (c % NBUF) * BUF + (rb * RT) * kRlRs;
+    const float* sx = sm + (c % NBUF) * BUF + (RW + tb * TT) * kRlRs;
+    const int jend = min(dm, (c + 1) * kRlCk) - c * kRlCk;
+#pragma unroll 4
+    for (int j = 4 * cg; j < jend; j += LANES) {
+      float4 wv[RT], xv[TT];
+#pragma unroll
+      for (int q = 0; q < RT; q++) wv[q] = *reinterpret_cast<const float4*>(sw + q * kRlRs + j);
+#pragma unroll
+      for (int i = 0; i < TT; i++) xv[i] = *reinterpret_cast<const float4*>(sx + i * kRlRs + j);
+#pragma unroll
+      for (int i = 0; i < TT; i++)
+#pragma unroll
+        for (int q = 0; q < RT; q++) {
+          acc[i][q][0] = __builtin_fmaf(wv[q].x, xv[i].x, acc[i][q][0]);
+          acc[i][q][1] = __builtin_fmaf(wv[q].y, xv[i].y, acc[i][q][1]);
+          acc[i][q][2] = __builtin_fmaf(wv[q].z, xv[i].z, acc[i][q][2]);
+          acc[i][q][3] = __builtin_fmaf(wv[q].w, xv[i].w, acc[i][q][3]);
+        }
+    }
+    if (c + NBUF < nch) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+    }
+  }
+
+  const int base = lane - cg;
+  const int last0 = (nch - 1) * kRlCk;
+  const float* lw = sm + ((nch - 1) % NBUF) * BUF + (rb * RT) * kRlRs;
+  const float* lx = sm + ((nch - 1) % NBUF) * BUF + (RW + tb * TT) * kRlRs;
+#pragma unroll
+  for (int i = 0; i < TT; i++)
+#pragma unroll
+    for (int q = 0; q < RT; q++) {
+      const int t = t0 + tb * TT + i, e = r0 + rb * RT + q;
+      float v[LANES];
+#pragma unroll
+      for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[4 * g + c] = __shfl(acc[i][q][c], base + g);
+      float s = 0.0f;
+      if constexpr (LANES == 8) {
+#pragma unroll
+        for (int l = 0; l < 8; l++) s += v[l];
+      } else {
+        float t8[8], t4[4];
+#pragma unroll
+        for (int l = 0; l < 8; l++) t8[l] = v[8 + l] + v[l];
+#pragma unroll
+        for (int l = 0; l < 4; l++) t4[l] = t8[4 + l] + t8[l];
+        const float a02 = t4[0] + t4[2];
+        const float a13 = t4[1] + t4[3];
+        s += a02 + a13;
+      }
+      for (int j = dm; j < d; j++) s += lw[q * kRlRs + j - last0] * lx[i * kRlRs + j - last0];
+      if (cg == 0 && t < T && e < E) logits[(size_t)t * E + e] = s;
+    }
+}
+
 bool rlogits_ok(int d) { return d > 0 && (d & 3) == 0; }
+
+template <int LANES, int NTB, int TT, int NRB, int RT, int NBUF>
+static hipError_t rlogits4_launch_t(const float* W, const float* X, int T, int E, int d,
+                                    float* logits, hipStream_t st) {
+  constexpr int TW = NTB * TT, RW = NRB * RT;
+  constexpr size_t lds = rlogits_lds<TW, RW, NBUF>();
+  static_assert(lds <= 160 * 1024, "LDS");
+  static bool opted[64] = {false};
+  if (lds > 64 * 1024) {
+    const hipError_t e =
+        lds_opt_in((const void*)k_rlogits4<LANES, NTB, TT, NRB, RT, NBUF>, opted);
+    if (e != hipSuccess) return e;
+  }
+  const dim3 grid((E + RW - 1) / RW, (T + TW - 1) / TW);
+  hipLaunchKernelGGL((k_rlogits4<LANES, NTB, TT, NRB, RT, NBUF>), grid, dim3(256), lds, st, W, X,
+                     T, E, d, logits);
+  return hipGetLastError();
+}
 
 template <int LANES, int NTB, int TT, int NRB, int RT, int NBUF>
 static hipError_t rlogits_launch_t(const float* W, const float* X, int T, int E, int d,
@@ -174,9 +311,20 @@ static hipError_t rlogits_launch_t(const float* W, const float* X, int T, int E,
   return hipGetLastError();
 }
 
-// Tiles of 16 tokens x 16 router rows, or x 4 rows for few tokens (more
-// workgroups for the same work); two chunk buffers (deeper rings measured no
-// faster).
+// QR_RLOGITS_VEC4=0 selects the one-chain-per-thread kernels (tuning sweeps).
+static bool rlogits_vec4() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("QR_RLOGITS_VEC4");
+    v = (e && e[0] == '0') ? 0 : 1;
+  }
+  return v == 1;
+}
+
+// Tiles of 16 tokens x 4 router rows for few tokens (more workgroups for the
+// same work; one chain per thread); 16 x 16 tiles with four chains per thread
+// beyond (a quarter of the LDS read instructions); two chunk buffers (deeper
+// rings measured no faster).
 hipError_t rlogits_launch(int order, const float* W, const float* X, int T, int E, int d,
                           float* logits, hipStream_t st) {
   if (!rlogits_ok(d) || (reinterpret_cast<uintptr_t>(W) & 15) ||
@@ -187,11 +335,13 @@ hipError_t rlogits_launch(int order, const float* W, const float* X, int T, int 
   switch (order) {
     case QR_ORDER_SEQ: return rlogits_launch_t<1, 16, 1, 16, 1, 2>(W, X, T, E, d, logits, st);
     case QR_ORDER_AVX2:
-      return small ? rlogits_launch_t<8, 8, 2, 4, 1, 2>(W, X, T, E, d, logits, st)
-                   : rlogits_launch_t<8, 4, 4, 8, 2, 2>(W, X, T, E, d, logits, st);
+      if (small) return rlogits_launch_t<8, 8, 2, 4, 1, 2>(W, X, T, E, d, logits, st);
+      return rlogits_vec4() ? rlogits4_launch_t<8, 8, 2, 16, 1, 2>(W, X, T, E, d, logits, st)
+                            : rlogits_launch_t<8, 4, 4, 8, 2, 2>(W, X, T, E, d, logits, st);
     default:
-      return small ? rlogits_launch_t<16, 4, 4, 4, 1, 2>(W, X, T, E, d, logits, st)
-                   : rlogits_launch_t<16, 4, 4, 4, 4, 2>(W, X, T, E, d, logits, st);
+      if (small) return rlogits_launch_t<16, 4, 4, 4, 1, 2>(W, X, T, E, d, logits, st);
+      return rlogits_vec4() ? rlogits4_launch_t<16, 4, 4, 16, 1, 2>(W, X, T, E, d, logits, st)
+                            : rlogits_launch_t<16, 4, 4, 4, 4, 2>(W, X, T, E, d, logits, st);
   }
 }
 
