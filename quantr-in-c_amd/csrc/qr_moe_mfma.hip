@@ -130,17 +130,18 @@ __device__ inline void unit_scales4(const uint32_t* wl, int o, int s0, int su, f
 // ---------------------------------------------------------------------------
 // The grouped MFMA kernel.
 //
-// A workgroup of 4 waves takes one work item: 64 weight rows of expert e (16
-// per wave; in gate/up mode the same 16 rows of both matrices) against one
-// tile of up to NTOK = 16 NJ dispatched pairs of e.  The K loop walks the rows
-// one stage at a time (one super-block, or 8 Q8_0 blocks: 8 units) through
-// rings of D LDS slots filled by global_load_lds_dwordx4: the stage's
-// activation records, shared by the 4 waves (each wave moves a quarter), and
-// each wave's own 16 x NMAT row stages.  One barrier per stage: past it every
-// wave's share of stage st has landed and every wave is done with stage
-// st - 1, whose slots then take stage st + D - 1.  DMA waits are counted by
-// hand (loads complete in issue order), so the compiler never holds a
-// register or a wait for the stream.
+// A workgroup of NW waves takes one work item: 16 NW weight rows of expert e
+// (16 per wave; in gate/up mode the same 16 rows of both matrices) against
+// one tile of up to NTOK = 16 NJ dispatched pairs of e.  The K loop walks the
+// rows one stage at a time (one super-block, or 8 Q8_0 blocks: 8 units)
+// through rings of D LDS slots filled by global_load_lds_dwordx4: the stage's
+// activation records, shared by the waves (each moves its share), and each
+// wave's own 16 x NMAT row stages.  With D >= 2, one barrier per stage: past
+// it every wave's share of stage st has landed and every wave is done with
+// stage st - 1, whose slots then take stage st + D - 1.  With one slot, a
+// second barrier before each stage's DMA.  DMA waits are counted by hand
+// (loads complete in issue order), so the compiler never holds a register or
+// a wait for the stream.
 // ---------------------------------------------------------------------------
 struct MfmaArgs {
   const uint8_t* W1;      // [E][rows][rb] (up in gate/up mode)
@@ -194,7 +195,6 @@ struct MfmaGeo {
   static_assert(NTOK * 4 <= NW * SCL, "xrow");
   static_assert(D >= 1 && D <= 3, "ring depth");
   static_assert(NI <= 63, "vmcnt range");
-  static_assert(NSC % 64 == 0, "scale passes");
 };
 
 template <int TYPE, bool GATEUP, int NJ, int RA, int D, int NW>
