@@ -299,14 +299,13 @@ __global__ __launch_bounds__(1024) void k_down1(Down1Args a) {
     eks[4 * j] = iv.x; eks[4 * j + 1] = iv.y; eks[4 * j + 2] = iv.z; eks[4 * j + 3] = iv.w;
     wks[4 * j] = wv.x; wks[4 * j + 1] = wv.y; wks[4 * j + 2] = wv.z; wks[4 * j + 3] = wv.w;
   }
+  dma_bytes(reinterpret_cast<const uint8_t*>(a.hb + (size_t)k * a.hidden),
+            reinterpret_cast<uint8_t*>(hs), a.hidden * 4, lane);
   int e = -1;
 #pragma unroll
   for (int kk = 0; kk < 16; kk++)
     if (kk == k) e = eks[kk];
   e = __builtin_amdgcn_readfirstlane(e);
-  const int nh = dma_bytes(reinterpret_cast<const uint8_t*>(a.hb + (size_t)k * a.hidden),
-                           reinterpret_cast<uint8_t*>(hs), a.hidden * 4, lane);
-  (void)nh;
   const bool ok = e >= 0 && e < a.E;  // uniform per wave
   if (ok) {
     // the tile's byte range [r0 rb, (r0 + RWt) rb) from its 16-byte aligned start

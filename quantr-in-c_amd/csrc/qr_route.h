@@ -122,31 +122,42 @@ __device__ inline void route_softmax(const float* __restrict__ lg, int E, float*
   for (int q = 0; q < 4; q++)
     if (lane + 64 * q < E && lv[q] > mx) mx = lv[q];
   mx = wave_max(mx);
+  float ev[4];
 #pragma unroll
   for (int q = 0; q < 4; q++) {
+    ev[q] = 0.0f;
     if (64 * q >= E) break;  // uniform
-    const float ev = qr_expf_w(lv[q] - mx, tab);  // every lane
-    if (lane + 64 * q < E) pw[lane + 64 * q] = ev;
+    ev[q] = qr_expf_w(lv[q] - mx, tab);  // every lane
+    if (lane + 64 * q < E) pw[lane + 64 * q] = ev[q];
   }
   wave_lds_fence();
-  // sequential sum, e ascending (src/kernels.c:198-202), in lane 0
+  // sequential sum, e ascending (src/kernels.c:198-202), in lane 0: 32
+  // exponentials per step, the next step's loads issued before this step's adds
   float inv = 0.0f;
   if (lane == 0) {
     float sum = 0.0f;
-    int e = 0;
-    for (; e + 16 <= E; e += 16) {
-      float4 q[4];
+    const int e32 = E & ~31;
+    float4 cur[8], nxt[8];
+    if (e32 > 0) {
 #pragma unroll
-      for (int k = 0; k < 4; k++) q[k] = *reinterpret_cast<const float4*>(pw + e + 4 * k);
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        sum += q[k].x;
-        sum += q[k].y;
-        sum += q[k].z;
-        sum += q[k].w;
-      }
+      for (int k = 0; k < 8; k++) cur[k] = *reinterpret_cast<const float4*>(pw + 4 * k);
     }
-    for (; e < E; e++) sum += pw[e];
+    for (int e = 0; e < e32; e += 32) {
+      if (e + 32 < e32) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) nxt[k] = *reinterpret_cast<const float4*>(pw + e + 32 + 4 * k);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        sum += cur[k].x;
+        sum += cur[k].y;
+        sum += cur[k].z;
+        sum += cur[k].w;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; k++) cur[k] = nxt[k];
+    }
+    for (int e = e32; e < E; e++) sum += pw[e];
     inv = 1.0f / sum;
   }
   inv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv), 0));
@@ -155,7 +166,7 @@ __device__ inline void route_softmax(const float* __restrict__ lg, int E, float*
     const int e = lane + 64 * q;
     pv[q] = kMask;
     if (e < E) {
-      const float v = pw[e] * inv;
+      const float v = ev[q] * inv;
       pv[q] = v;
       if (probs) probs[e] = v;
     }
@@ -256,20 +267,24 @@ __device__ inline void route_rank_wg_g(int E, int K, float* pw, int t, int nthr)
   const bool live = e < E;
   const uint64_t* keys = route_keys(pw);
   const uint64_t mine = live ? keys[e] : ~0ull;
-  const int per = (E + G - 1) / G;
-  const int j0 = g * per, j1 = min(E, j0 + per);
+  // this thread counts the keys j = g, g + G, g + 2G, ...: the G threads of a
+  // candidate read adjacent keys, so one read instruction touches G adjacent
+  // 8-byte words (distinct LDS banks) and broadcasts each
   int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
-  int j = j0;
-  for (; j + 8 <= j1; j += 8) {
-    uint64_t k8[8];
+  int j = g;
+  for (; j + 15 * G < E; j += 16 * G) {
+    uint64_t k16[16];
 #pragma unroll
-    for (int u = 0; u < 8; u++) k8[u] = keys[j + u];
-    c0 += (k8[0] > mine) + (k8[4] > mine);
-    c1 += (k8[1] > mine) + (k8[5] > mine);
-    c2 += (k8[2] > mine) + (k8[6] > mine);
-    c3 += (k8[3] > mine) + (k8[7] > mine);
+    for (int u = 0; u < 16; u++) k16[u] = keys[j + u * G];
+#pragma unroll
+    for (int u = 0; u < 16; u += 4) {
+      c0 += k16[u] > mine;
+      c1 += k16[u + 1] > mine;
+      c2 += k16[u + 2] > mine;
+      c3 += k16[u + 3] > mine;
+    }
   }
-  for (; j < j1; j++) c0 += keys[j] > mine;
+  for (; j < E; j += G) c0 += keys[j] > mine;
   int r = (c0 + c1) + (c2 + c3);
   if (G >= 2) r += __builtin_amdgcn_update_dpp(0, r, 0xB1, 0xF, 0xF, false);  // lane ^ 1
   if (G >= 4) r += __builtin_amdgcn_update_dpp(0, r, 0x4E, 0xF, 0xF, false);  // lane ^ 2
@@ -286,32 +301,6 @@ __device__ inline void route_rank_wg(int E, int K, float* pw, int t, int nthr) {
     case 2: route_rank_wg_g<2>(E, K, pw, t, nthr); break;
     default: route_rank_wg_g<1>(E, K, pw, t, nthr); break;
   }
-}
-
-// One wave's top-K from the keys route_rank_keys wrote (and a wave fence):
-// lane l ranks candidates l, l + 64, ... against all E keys; a candidate of
-// rank r < K writes itself to slot r (keys are distinct, masked ones are 0).
-__device__ inline void route_rank_wave(int E, int K, float* pw, int lane) {
-  const uint64_t* keys = route_keys(pw);
-  for (int q = 0; q < E; q += 64) {  // wave-uniform
-    const int e = lane + q;
-    const uint64_t mine = e < E ? keys[e] : ~0ull;
-    int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
-    int j = 0;
-    for (; j + 4 <= E; j += 4) {
-      c0 += keys[j] > mine;
-      c1 += keys[j + 1] > mine;
-      c2 += keys[j + 2] > mine;
-      c3 += keys[j + 3] > mine;
-    }
-    for (; j < E; j++) c0 += keys[j] > mine;
-    const int r = (c0 + c1) + (c2 + c3);
-    if (e < E && mine != 0ull && r < K) {
-      route_idx(pw)[r] = e;
-      route_wts(pw)[r] = route_probs(pw)[e];
-    }
-  }
-  wave_lds_fence();
 }
 
 // Renormalised routing weights w_k / sum(w), the sum sequential in slot order

@@ -303,3 +303,24 @@ def test_moe_ragged_hidden(dev, oracle, T):
     x = I.activations(seed + 4, T, dim)
     xb = I.activations(seed + 5, T, dim)
     check_moe(dev, oracle, layer, x, xb, ORDER_AVX2, "hidden 288 T=%d" % T)
+
+
+@pytest.mark.parametrize("dt", [Q.TYPE_Q4_K, Q.TYPE_Q5_K, Q.TYPE_Q6_K, Q.TYPE_Q8_0])
+@pytest.mark.parametrize("dim,hidden", [(1024, 288), (2048, 512)])
+def test_moe_t1_down_types(dev, oracle, dt, dim, hidden):
+    """One token at model widths (gate/up tiles of 8 and 4 rows per wave) for
+    every down type; hidden 288 leaves a K-quant down product with one
+    super-block per row (the last 32 elements dropped, as the reference
+    does)."""
+    E, K = 24, 6
+    ut = Q.TYPE_Q4_K
+    ue, de = I.BLOCK[ut][0], I.BLOCK[dt][0]
+    seed = 8100 + 10 * dt + dim // 1024
+    up = I.blocks(seed, ut, E * hidden * (dim // ue))
+    gate = I.blocks(seed + 1, ut, E * hidden * (dim // ue))
+    down = I.blocks(seed + 2, dt, E * dim * (hidden // de))
+    router = I.activations(seed + 3, E, dim, std=0.05)
+    layer = DevLayer(dev, dim, hidden, E, K, router, up, gate, down, ut, dt)
+    x = I.activations(seed + 4, 1, dim)
+    xb = I.activations(seed + 5, 1, dim)
+    check_moe(dev, oracle, layer, x, xb, ORDER_AVX2, "t1 %d/%d down %d" % (dim, hidden, dt))
