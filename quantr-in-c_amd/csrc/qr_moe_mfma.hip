@@ -273,10 +273,33 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
     aunit[k] = ch / 3;
   }
   const size_t asrc0 = (size_t)xrow[0] * xq_row;
+  // Q4_K / Q5_K: a row's stage is whole 16-byte chunks (rows and stages are
+  // multiples of 16 bytes) and every stage's 8 units exist, so each source is
+  // a stage-invariant address plus the stage's offset
+  constexpr bool ALN = TYPE == QR_T_Q4_K || TYPE == QR_T_Q5_K;
+  const uint8_t* wp[G::WI];
+  const uint8_t* ap[G::AI];
+  if constexpr (ALN) {
+#pragma unroll
+    for (int k = 0; k < G::WI; k++)
+      wp[k] = wroff[k] != ~0u ? wbase[k] + wroff[k] + 16 * wch[k] : a.W1 + ebase + row0;
+#pragma unroll
+    for (int k = 0; k < G::AI; k++) ap[k] = a.XQ + (asrc[k] != ~(size_t)0 ? asrc[k] : asrc0);
+  }
 
   auto issue = [&](int st) {
     const int slot = st % D;
     const uint32_t abase = lds_u32addr(smem + slot * G::AST) + (uint32_t)(wave * G::AI * 1024);
+    if constexpr (ALN) {
+      const size_t ao = (size_t)(8 * st) * kXQ;
+#pragma unroll
+      for (int k = 0; k < G::AI; k++) lds_dma16(ap[k] + ao, abase + (uint32_t)(k * 1024));
+      const uint32_t wlds = lds_u32addr(smem + G::O_W + (wave * D + slot) * G::WST);
+      const uint32_t s0 = (uint32_t)st * KST;
+#pragma unroll
+      for (int k = 0; k < G::WI; k++) lds_dma16(wp[k] + s0, wlds + (uint32_t)(k * 1024));
+      return;
+    }
 #pragma unroll
     for (int k = 0; k < G::AI; k++) {
       const bool ok = asrc[k] != ~(size_t)0 && 8 * st + aunit[k] < U;
