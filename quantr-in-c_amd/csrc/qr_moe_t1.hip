@@ -26,21 +26,6 @@
 
 namespace qr {
 
-// DMA `nbytes` from g into LDS s in whole 1 KiB instructions; lanes past the
-// end reload g's first 16 bytes into bytes nobody reads (s must hold the
-// rounded-up size).  Returns the number of instructions issued.
-__device__ inline int dma_bytes(const uint8_t* g, uint8_t* s, int nbytes, int lane) {
-  const uint32_t sbase = lds_u32addr(s);
-  const int n = (nbytes + 1023) >> 10;
-  for (int k = 0; k < n; k++) {
-    const int off = k * 1024 + lane * 16;
-    lds_dma16(g + (off < nbytes ? off : 0), sbase + (uint32_t)(k * 1024));
-  }
-  return n;
-}
-
-__host__ __device__ inline size_t kib_round(size_t b) { return (b + 1023) & ~(size_t)1023; }
-
 // ---------------------------------------------------------------------------
 // Router logits.
 // ---------------------------------------------------------------------------

@@ -273,6 +273,87 @@ __global__ __launch_bounds__(256) void k_rlogits4(const float* __restrict__ W,
     }
 }
 
+// Few tokens, the FMA-chain orders: one workgroup per router row e.  The row
+// and the T token rows arrive whole in LDS by DMA (row i at i RS floats, RS
+// = the row's whole KiB plus a LANES-float skew, so the chains of LANES
+// adjacent lanes and of different tokens read different banks); thread
+// t LANES + k then runs chain k of token t over the whole row with no
+// barrier, and the LANES chains are combined as in k_rlogits.
+template <int LANES>
+__global__ __launch_bounds__(256) void k_rlogits_row(const float* __restrict__ W,
+                                                     const float* __restrict__ X, int T, int E,
+                                                     int d, float* __restrict__ logits) {
+  extern __shared__ __align__(16) float sm[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int e = blockIdx.x;
+  const int rbytes = (int)kib_round((size_t)d * 4);
+  const int RS = rbytes / 4 + LANES;
+  // row i (0: W[e], 1 + t: X[t]) by wave i % 4
+  for (int i = wave; i <= T; i += 4) {
+    const float* src = i == 0 ? W + (size_t)e * d : X + (size_t)(i - 1) * d;
+    dma_bytes(reinterpret_cast<const uint8_t*>(src), reinterpret_cast<uint8_t*>(sm + i * RS),
+              d * 4, lane);
+  }
+  wait_vmcnt<0>();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  const int t = tid / LANES, k = tid % LANES;
+  if (tid >= ((T * LANES + 63) & ~63)) return;  // whole waves past the last token
+  const int tc = t < T ? t : T - 1;
+  const float* sw = sm;
+  const float* sx = sm + (1 + tc) * RS;
+  const int dm = d - d % LANES;
+  const float acc = lds_chain<LANES>(sw, sx, k, dm);
+  float v[LANES];
+  const int base = lane - k;
+#pragma unroll
+  for (int l = 0; l < LANES; l++) v[l] = __shfl(acc, base + l);
+  float sum = 0.0f;
+  if constexpr (LANES == 8) {
+#pragma unroll
+    for (int l = 0; l < 8; l++) sum += v[l];
+  } else {
+    float t8[8], t4[4];
+#pragma unroll
+    for (int l = 0; l < 8; l++) t8[l] = v[8 + l] + v[l];
+#pragma unroll
+    for (int l = 0; l < 4; l++) t4[l] = t8[4 + l] + t8[l];
+    const float a02 = t4[0] + t4[2];
+    const float a13 = t4[1] + t4[3];
+    sum += a02 + a13;
+  }
+  for (int j = dm; j < d; j++) sum += sw[j] * sx[j];
+  if (k == 0 && t < T) logits[(size_t)t * E + e] = sum;
+}
+
+template <int LANES>
+static size_t rlogits_row_lds(int T, int d) {
+  return (size_t)(T + 1) * (kib_round((size_t)d * 4) + 4 * LANES);
+}
+
+// Whether k_rlogits_row takes T tokens: LANES threads per token, the T + 1
+// rows within 160 KiB, and a wave's DMA within the vmcnt range.
+template <int LANES>
+static bool rlogits_row_ok(int T, int d) {
+  const int nkb = (int)(kib_round((size_t)d * 4) >> 10);
+  return T >= 1 && T * LANES <= 256 && rlogits_row_lds<LANES>(T, d) <= 160 * 1024 &&
+         ((T + 4) / 4) * nkb <= 63;
+}
+
+template <int LANES>
+static hipError_t rlogits_row_launch_t(const float* W, const float* X, int T, int E, int d,
+                                       float* logits, hipStream_t st) {
+  const size_t lds = rlogits_row_lds<LANES>(T, d);
+  static bool opted[64] = {false};
+  if (lds > 64 * 1024) {
+    const hipError_t e = lds_opt_in((const void*)k_rlogits_row<LANES>, opted);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(k_rlogits_row<LANES>, dim3(E), dim3(256), lds, st, W, X, T, E, d, logits);
+  return hipGetLastError();
+}
+
 bool rlogits_ok(int d) { return d > 0 && (d & 3) == 0; }
 
 template <int LANES, int NTB, int TT, int NRB, int RT, int NBUF>
@@ -335,10 +416,12 @@ hipError_t rlogits_launch(int order, const float* W, const float* X, int T, int 
   switch (order) {
     case QR_ORDER_SEQ: return rlogits_launch_t<1, 16, 1, 16, 1, 2>(W, X, T, E, d, logits, st);
     case QR_ORDER_AVX2:
+      if (rlogits_row_ok<8>(T, d)) return rlogits_row_launch_t<8>(W, X, T, E, d, logits, st);
       if (small) return rlogits_launch_t<8, 8, 2, 4, 1, 2>(W, X, T, E, d, logits, st);
       return rlogits_vec4() ? rlogits4_launch_t<8, 8, 2, 16, 1, 2>(W, X, T, E, d, logits, st)
                             : rlogits_launch_t<8, 4, 4, 8, 2, 2>(W, X, T, E, d, logits, st);
     default:
+      if (rlogits_row_ok<16>(T, d)) return rlogits_row_launch_t<16>(W, X, T, E, d, logits, st);
       if (small) return rlogits_launch_t<16, 4, 4, 4, 1, 2>(W, X, T, E, d, logits, st);
       return rlogits_vec4() ? rlogits4_launch_t<16, 4, 4, 16, 1, 2>(W, X, T, E, d, logits, st)
                             : rlogits_launch_t<16, 4, 4, 4, 4, 2>(W, X, T, E, d, logits, st);

@@ -183,6 +183,10 @@ def test_route_topk_probs(dev, oracle, order):
     (544, 5, 3, 3, ORDER_AVX2),        # E below one wave, few tokens
     (2048, 128, 8, 100, ORDER_AVX512), # the 16-token x 16-row tiles, ragged token tile
     (1056, 128, 8, 70, ORDER_SEQ),     # sequential order, ragged tiles
+    (2048, 128, 8, 16, ORDER_AVX512),  # one router row per workgroup: 16 tokens x 16 lanes
+    (1056, 60, 4, 9, ORDER_AVX512),    # ... rows of 4224 bytes (a partial last KiB)
+    (2048, 128, 8, 18, ORDER_AVX2),    # ... the most tokens whose rows fit 160 KiB
+    (2048, 128, 8, 19, ORDER_AVX2),    # one token more: the tiled kernel
 ])
 def test_route_shapes(dev, oracle, dim, E, K, T, order):
     """Tiled router logits + workgroup rank routing at widths with a partial
