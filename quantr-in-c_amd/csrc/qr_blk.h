@@ -208,6 +208,20 @@ __device__ inline void lds_dma16(const void* src, uint32_t lds) {
       : "v"(src), "s"(lds)
       : "memory");
 }
+// The same with the non-temporal hint, for bytes read once (weight streams):
+// they are the first lines L2 gives up, so data that every workgroup re-reads
+// (the activation) stays cached across launches.
+__device__ inline void lds_dma16_nt(const void* src, uint32_t lds) {
+  int save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(src), "s"(lds)
+      : "memory");
+}
 // The LDS byte address of a pointer into LDS, wave-uniform.
 __device__ inline uint32_t lds_u32addr(const void* p) {
   return __builtin_amdgcn_readfirstlane(
@@ -221,19 +235,22 @@ __device__ inline void tile_dma(const uint8_t* g, uint8_t* s, int valid, int lan
 #pragma unroll
   for (int k = 0; k < NCH; k++) {
     const int off = k * 1024 + lane * 16;
-    lds_dma16(g + (off < valid ? off : 0), sbase + (uint32_t)(k * 1024));
+    lds_dma16_nt(g + (off < valid ? off : 0), sbase + (uint32_t)(k * 1024));
   }
 }
 
 // DMA `nbytes` from g into LDS s in whole 1 KiB instructions; lanes past the
 // end reload g's first 16 bytes into bytes nobody reads (s must hold the
 // rounded-up size).  Returns the number of instructions issued.
+// NT: with the non-temporal hint (bytes read once).
+template <bool NT = false>
 __device__ inline int dma_bytes(const uint8_t* g, uint8_t* s, int nbytes, int lane) {
   const uint32_t sbase = lds_u32addr(s);
   const int n = (nbytes + 1023) >> 10;
   for (int k = 0; k < n; k++) {
     const int off = k * 1024 + lane * 16;
-    lds_dma16(g + (off < nbytes ? off : 0), sbase + (uint32_t)(k * 1024));
+    if constexpr (NT) lds_dma16_nt(g + (off < nbytes ? off : 0), sbase + (uint32_t)(k * 1024));
+    else lds_dma16(g + (off < nbytes ? off : 0), sbase + (uint32_t)(k * 1024));
   }
   return n;
 }

@@ -38,7 +38,7 @@ __global__ __launch_bounds__(64) void k_router1(const float* __restrict__ W,
   const size_t rbytes = kib_round((size_t)d * 4);
   float* sw = reinterpret_cast<float*>(smem);
   float* sx = reinterpret_cast<float*>(smem + rbytes);
-  dma_bytes(reinterpret_cast<const uint8_t*>(W + (size_t)e * d), smem, d * 4, lane);
+  dma_bytes<true>(reinterpret_cast<const uint8_t*>(W + (size_t)e * d), smem, d * 4, lane);
   dma_bytes(reinterpret_cast<const uint8_t*>(xb), smem + rbytes, d * 4, lane);
   wait_vmcnt<0>();
   if constexpr (LANES == 1) {
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(64 * kBlkWaves) void k_gateup1(GateUp1Args a) {
       const int o = c * 1024 + lane * 16;
       const uint8_t* src = o < 32 * BB ? (o < valid ? ub + o : ub)
                                        : (o - 32 * BB < valid ? gb + (o - 32 * BB) : ub);
-      lds_dma16(src, sbase + (uint32_t)(c * 1024));
+      lds_dma16_nt(src, sbase + (uint32_t)(c * 1024));
     }
   }
 
@@ -298,7 +298,7 @@ __global__ __launch_bounds__(1024) void k_down1(Down1Args a) {
     const size_t a0 = gs & ~(size_t)15;
     const uint8_t* W = a.down + (size_t)e * a.slice;
     const int nbytes = (int)(gs + (size_t)RWt * sh.rb - a0);
-    const int nt = dma_bytes(W + a0, stage, nbytes, lane);
+    const int nt = dma_bytes<true>(W + a0, stage, nbytes, lane);
     // hb staged (loads complete in order: only the tile's DMA may be in flight)
     switch (nt) {
       case 1: wait_vmcnt<1>(); break;

@@ -64,8 +64,9 @@ __global__ __launch_bounds__(256) void k_rlogits(const float* __restrict__ W,
       const int i = wave + 4 * n;
       const float* src = i < RW ? W + (size_t)min(r0 + i, E - 1) * d
                                 : X + (size_t)min(t0 + i - RW, T - 1) * d;
-      lds_dma16(reinterpret_cast<const uint8_t*>(src + c * kRlCk) + (o < nb ? o : 0),
-                lds_u32addr(sm + b * BUF + i * kRlRs));
+      const uint8_t* g = reinterpret_cast<const uint8_t*>(src + c * kRlCk) + (o < nb ? o : 0);
+      if (i < RW) lds_dma16_nt(g, lds_u32addr(sm + b * BUF + i * kRlRs));  // router rows: read once
+      else lds_dma16(g, lds_u32addr(sm + b * BUF + i * kRlRs));
     }
   };
 
@@ -187,8 +188,9 @@ __global__ __launch_bounds__(256) void k_rlogits4(const float* __restrict__ W,
       const int i = wave + 4 * n;
       const float* src = i < RW ? W + (size_t)min(r0 + i, E - 1) * d
                                 : X + (size_t)min(t0 + i - RW, T - 1) * d;
-      lds_dma16(reinterpret_cast<const uint8_t*>(src + c * kRlCk) + (o < nb ? o : 0),
-                lds_u32addr(sm + b * BUF + i * kRlRs));
+      const uint8_t* g = reinterpret_cast<const uint8_t*>(src + c * kRlCk) + (o < nb ? o : 0);
+      if (i < RW) lds_dma16_nt(g, lds_u32addr(sm + b * BUF + i * kRlRs));  // router rows: read once
+      else lds_dma16(g, lds_u32addr(sm + b * BUF + i * kRlRs));
     }
   };
 
@@ -292,8 +294,12 @@ __global__ __launch_bounds__(256) void k_rlogits_row(const float* __restrict__ W
   // row i (0: W[e], 1 + t: X[t]) by wave i % 4
   for (int i = wave; i <= T; i += 4) {
     const float* src = i == 0 ? W + (size_t)e * d : X + (size_t)(i - 1) * d;
-    dma_bytes(reinterpret_cast<const uint8_t*>(src), reinterpret_cast<uint8_t*>(sm + i * RS),
-              d * 4, lane);
+    if (i == 0)  // the router row: read once
+      dma_bytes<true>(reinterpret_cast<const uint8_t*>(src), reinterpret_cast<uint8_t*>(sm), d * 4,
+                      lane);
+    else
+      dma_bytes(reinterpret_cast<const uint8_t*>(src), reinterpret_cast<uint8_t*>(sm + i * RS),
+                d * 4, lane);
   }
   wait_vmcnt<0>();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
