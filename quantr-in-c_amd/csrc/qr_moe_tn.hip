@@ -64,9 +64,8 @@ __global__ __launch_bounds__(256) void k_rlogits(const float* __restrict__ W,
       const int i = wave + 4 * n;
       const float* src = i < RW ? W + (size_t)min(r0 + i, E - 1) * d
                                 : X + (size_t)min(t0 + i - RW, T - 1) * d;
-      const uint8_t* g = reinterpret_cast<const uint8_t*>(src + c * kRlCk) + (o < nb ? o : 0);
-      if (i < RW) lds_dma16_nt(g, lds_u32addr(sm + b * BUF + i * kRlRs));  // router rows: read once
-      else lds_dma16(g, lds_u32addr(sm + b * BUF + i * kRlRs));
+      lds_dma16(reinterpret_cast<const uint8_t*>(src + c * kRlCk) + (o < nb ? o : 0),
+                lds_u32addr(sm + b * BUF + i * kRlRs));
     }
   };
 
@@ -188,9 +187,8 @@ __global__ __launch_bounds__(256) void k_rlogits4(const float* __restrict__ W,
       const int i = wave + 4 * n;
       const float* src = i < RW ? W + (size_t)min(r0 + i, E - 1) * d
                                 : X + (size_t)min(t0 + i - RW, T - 1) * d;
-      const uint8_t* g = reinterpret_cast<const uint8_t*>(src + c * kRlCk) + (o < nb ? o : 0);
-      if (i < RW) lds_dma16_nt(g, lds_u32addr(sm + b * BUF + i * kRlRs));  // router rows: read once
-      else lds_dma16(g, lds_u32addr(sm + b * BUF + i * kRlRs));
+      lds_dma16(reinterpret_cast<const uint8_t*>(src + c * kRlCk) + (o < nb ? o : 0),
+                lds_u32addr(sm + b * BUF + i * kRlRs));
     }
   };
 
