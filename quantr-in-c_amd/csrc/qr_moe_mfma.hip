@@ -160,6 +160,7 @@ struct MfmaArgs {
   uint8_t* QO;
   int qperm;
   int skinny;             // work items of at most 4 pairs take the skinny form
+  int wnt;                // weight DMA with the non-temporal hint (weights read about once)
 };
 
 template <int TYPE, bool GATEUP, int NJ, int RA, int D, int NW>
@@ -296,8 +297,13 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
       for (int k = 0; k < G::AI; k++) lds_dma16(ap[k] + ao, abase + (uint32_t)(k * 1024));
       const uint32_t wlds = lds_u32addr(smem + G::O_W + (wave * D + slot) * G::WST);
       const uint32_t s0 = (uint32_t)st * KST;
+      if (a.wnt) {
 #pragma unroll
-      for (int k = 0; k < G::WI; k++) lds_dma16(wp[k] + s0, wlds + (uint32_t)(k * 1024));
+        for (int k = 0; k < G::WI; k++) lds_dma16_nt(wp[k] + s0, wlds + (uint32_t)(k * 1024));
+      } else {
+#pragma unroll
+        for (int k = 0; k < G::WI; k++) lds_dma16(wp[k] + s0, wlds + (uint32_t)(k * 1024));
+      }
       return;
     }
 #pragma unroll
@@ -323,7 +329,8 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
           W = wbase[k];
         }
       }
-      lds_dma16(W + off, wlds + (uint32_t)(k * 1024));
+      if (a.wnt) lds_dma16_nt(W + off, wlds + (uint32_t)(k * 1024));
+      else lds_dma16(W + off, wlds + (uint32_t)(k * 1024));
     }
   };
 
@@ -680,6 +687,10 @@ hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const ui
     }
     a.skinny = knob;
   }
+  // items of up to 16 pairs: an expert rarely has more than one, so its rows
+  // are read about once and the hint keeps the activation records cached;
+  // with 32-pair items hot experts are re-read by several items
+  a.wnt = tile <= 16;
   switch (type) {
     case QR_T_Q4_K: return gateup ? mfma_launch_nj<QR_T_Q4_K, true>(a, items, tile, st)
                                   : mfma_launch_nj<QR_T_Q4_K, false>(a, items, tile, st);
