@@ -115,6 +115,17 @@ __device__ inline Slots make_slots(int U, int lane) {
   return s;
 }
 
+// 16 weight bytes read once, with the non-temporal hint (the weight stream
+// is the first L2 gives up, so the activation stays cached).
+typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+__device__ inline uint4 ld_nt16(const uint8_t* p) {
+  const u32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ inline uint32_t ld_nt4(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
+
 // Load tile rows [r0, r0 + RWt) of matrix W ([rows][rb], `total` bytes).
 template <int TYPE>
 __device__ inline void load_tile(const uint8_t* __restrict__ W, size_t total, int r0, int RWt,
@@ -128,13 +139,13 @@ __device__ inline void load_tile(const uint8_t* __restrict__ W, size_t total, in
         const uint8_t* blk =
             W + (size_t)(r0 + sl.row[i]) * sh.rb + (size_t)(sl.u[i] >> 3) * BB;
         const int s = sl.u[i] & 7;
-        R.hdr[i] = *reinterpret_cast<const uint4*>(blk);
+        R.hdr[i] = ld_nt16(blk);
         if constexpr (TYPE == QR_T_Q4_K) {
-          R.qs[i] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * s);
+          R.qs[i] = ld_nt16(blk + 16 + 16 * s);
           R.qh[i] = 0;
         } else {
-          R.qs[i] = *reinterpret_cast<const uint4*>(blk + 48 + 16 * s);
-          R.qh[i] = *reinterpret_cast<const uint32_t*>(blk + 16 + 4 * s);
+          R.qs[i] = ld_nt16(blk + 48 + 16 * s);
+          R.qh[i] = ld_nt4(blk + 16 + 4 * s);
         }
       } else {
         R.hdr[i] = make_uint4(0, 0, 0, 0);
@@ -152,7 +163,7 @@ __device__ inline void load_tile(const uint8_t* __restrict__ W, size_t total, in
       uint4 v = make_uint4(0, 0, 0, 0);
       if (off < ge) {
         if (off + 16 <= total) {
-          v = *reinterpret_cast<const uint4*>(W + off);
+          v = ld_nt16(W + off);
         } else {  // the matrix ends inside this chunk: no load leaves it
           uint32_t w[4];
 #pragma unroll
