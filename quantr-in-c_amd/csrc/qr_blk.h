@@ -89,18 +89,24 @@ __device__ inline void act_prefetch(const float* __restrict__ x, size_t xstride,
 }
 
 // xs (optional): the activation already staged in LDS, group gi's 8 floats
-// at xs + 8 gi (see stage_act_dma); then every pass reads from there.
+// at xs + 8 gi (see stage_act_dma); then every pass reads from there.  tid /
+// nthr (optional): the caller's index among the nthr threads that quantize
+// (a multiple of 64, so quads never straddle waves); default the whole
+// workgroup.
 template <bool NIB>
 __device__ inline void quantize_act_blk(const float* __restrict__ x, size_t xstride, int nt,
                                         int d, uint8_t* lds, const ActPre& pre,
-                                        const float* xs = nullptr) {
+                                        const float* xs = nullptr, int tid = -1, int nthr = 0) {
   const int nxb = d >> 5;
   const int per_tok = nxb * 4;
   const int total = nt * per_tok;
   const size_t tokb = act_tok_bytes(d);
-  const int nthr = blockDim.x;  // a multiple of 64: quads never straddle waves
+  if (tid < 0) {
+    tid = (int)threadIdx.x;
+    nthr = (int)blockDim.x;
+  }
   for (int base = 0; base < total; base += nthr) {
-    const int gi = base + (int)threadIdx.x;
+    const int gi = base + tid;
     const bool live = gi < total;
     const int t = live ? gi / per_tok : 0;
     const int g = live ? gi - t * per_tok : 0;
@@ -265,28 +271,34 @@ constexpr size_t kXsMax = 16 * 1024;
 
 // Stage the fp32 activation of nt tokens into LDS xs by DMA, laid out for
 // quantize_act_blk: 8-element group gi = t * (d / 8) + g at xs + 32 gi bytes.
-// A workgroup of 256 threads quantizes group gi = pass * 256 + thread, so wave
-// w stages the 2 KiB of groups its own threads read in each pass (2 DMA
-// instructions per pass; lanes past the last group reload group 0).  Returns
-// the number of DMA instructions issued (2 per pass).  Call with all 64 lanes.
+// The nw waves that quantize (64 nw threads, group gi = pass * 64 nw +
+// thread) each stage the 2 KiB of groups their own threads read in each pass,
+// `wave` being the caller's index among them: 2 DMA instructions per pass,
+// none that starts past the last group (d a multiple of 256 keeps every
+// instruction within the groups); lanes past the last group reload group 0.
+// Returns the number of DMA instructions issued.  Call with all 64 lanes.
 __device__ inline int stage_act_dma(const float* __restrict__ x, size_t xstride, int nt, int d,
-                                    uint8_t* xs, int wave, int lane) {
+                                    uint8_t* xs, int wave, int lane, int nw = 4) {
   const int per_tok = d >> 3;
   const int total = nt * per_tok;
-  const int passes = (total + 255) >> 8;
+  const int pt = 64 * nw;
+  const int passes = (total + pt - 1) / pt;
   const uint32_t xbase = lds_u32addr(xs);
+  int issued = 0;
   for (int p = 0; p < passes; p++) {
 #pragma unroll
     for (int k = 0; k < 2; k++) {
-      const int first = p * 256 + wave * 64 + k * 32;  // first group of this instruction
+      const int first = p * pt + wave * 64 + k * 32;  // first group of this instruction
+      if (first >= total) continue;  // wave-uniform
       int gi = first + (lane >> 1);
       gi = gi < total ? gi : 0;
       const int t = gi / per_tok, g = gi - t * per_tok;
       lds_dma16(x + (size_t)t * xstride + (size_t)g * 8 + 4 * (lane & 1),
                 xbase + (uint32_t)(first * 32));
+      issued++;
     }
   }
-  return 2 * passes;
+  return issued;
 }
 
 // Wait until at most N of the wave's vector memory operations are in flight.

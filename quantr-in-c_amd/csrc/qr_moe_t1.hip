@@ -137,24 +137,25 @@ __global__ __launch_bounds__(64 * kBlkWaves) void k_gateup1(GateUp1Args a) {
   float* pw = reinterpret_cast<float*>(smem + o_pw);
   uint8_t* slot = smem + o_slots + (size_t)wave * SB;
 
-  // 1. the activation's DMA first, then the expf table's load
-  stage_act_dma(a.xb, (size_t)a.dim, 1, a.dim, smem, wave, lane);
+  // 1. routing: wave 0 computes the softmax and the rank keys while waves
+  //    1 .. kBlkWaves - 1 stage the activation by DMA and quantize it (each
+  //    its own groups: its own DMA's completion is all it waits for); after
+  //    the barrier every thread ranks the E candidates (route_rank_wg);
+  //    workgroup 0 publishes the routing
   const ExpTab tab = qr_expf_tab();
-  // 2. routing: wave 0 computes the softmax and the rank keys while the other
-  //    waves quantize the activation; after the barrier every thread ranks
-  //    the E candidates (route_rank_wg); workgroup 0 publishes the routing
   const int* sidx = route_idx(pw);
   if (wave == 0) {
     float pv[4];
     route_softmax(a.logits, a.E, pw, lane, nullptr, tab, pv);
     route_rank_keys(pv, a.E, a.K, pw, lane);
+  } else {
+    stage_act_dma(a.xb, (size_t)a.dim, 1, a.dim, smem, wave - 1, lane, kBlkWaves - 1);
+    wait_vmcnt<0>();
+    ActPre pre;
+    quantize_act_blk<BlkFmt<TYPE>::kNib>(a.xb, (size_t)a.dim, 1, a.dim, act, pre,
+                                         reinterpret_cast<const float*>(smem),
+                                         (int)threadIdx.x - 64, 64 * (kBlkWaves - 1));
   }
-  // 3. quantize the staged activation (every wave's own part has landed once
-  //    its DMA is done)
-  wait_vmcnt<0>();
-  ActPre pre;
-  quantize_act_blk<BlkFmt<TYPE>::kNib>(a.xb, (size_t)a.dim, 1, a.dim, act, pre,
-                                       reinterpret_cast<const float*>(smem));
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   route_rank_wg(a.E, a.K, pw, (int)threadIdx.x, (int)blockDim.x);
@@ -164,7 +165,7 @@ __global__ __launch_bounds__(64 * kBlkWaves) void k_gateup1(GateUp1Args a) {
   const int e = wave_on ? __builtin_amdgcn_readfirstlane(sidx[k]) : -1;
   const bool ok = wave_on && e >= 0 && e < a.E;  // uniform per wave
   if (!ok) return;  // no barriers below
-  // 4. the weight tile: up rows r0.. at slot bytes [0, RB rb), the same gate
+  // 2. the weight tile: up rows r0.. at slot bytes [0, RB rb), the same gate
   //    rows at [32 BB, 32 BB + RB rb): lane l reads its block at l * BB
   {
     const int rows = min(RB, a.hidden - r0);
