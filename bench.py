@@ -291,8 +291,8 @@ def main():
                     help="skip the GEMV headline (profiling runs of the MoE leg; value is null)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the sharding "
-              "design is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: there is no multi-GPU path; run with --gpus 1",
+              file=sys.stderr)
         sys.exit(2)
 
     dev = Q.Device(0)

@@ -11,8 +11,8 @@
  * stderr, the reference's convention (src/quant.c:443-446, 470-473).  The
  * `threads` arguments are OpenMP widths on the CPU and are ignored here.
  *
- * Each entry names the reference interface it replaces.  How a build of the
- * reference binds them (kernels.c / runtime.c / model.c) is in INTEGRATION.md.
+ * Each entry names the reference interface it replaces; a build of the
+ * reference binds them at those call sites (kernels.c / runtime.c / model.c).
  */
 #ifndef QR_DROPIN_H
 #define QR_DROPIN_H
