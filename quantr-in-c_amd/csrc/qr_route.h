@@ -10,45 +10,9 @@ namespace qr {
 
 constexpr float kMask = -1e9f;  // src/runtime.c:211, 221
 
-// (value, index) candidate order of the reference's argmax scan: a larger
-// value wins; equal values go to the lower index; index -1 (nothing yet)
-// loses to any real candidate.
-__device__ inline bool cand_better(float ov, int oi, float v, int i) {
-  return ov > v || (ov == v && oi >= 0 && (i < 0 || oi < i));
-}
-template <int CTRL>
-__device__ inline void cand_step(float& v, int& i) {
-  const float ov = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                                 0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-  const int oi = __builtin_amdgcn_update_dpp(-1, i, CTRL, 0xF, 0xF, false);
-  if (cand_better(ov, oi, v, i)) {
-    v = ov;
-    i = oi;
-  }
-}
-// Best candidate of the wave, returned in every lane: butterflies inside each
-// 16-lane row (DPP quad xor 1, xor 2, half-row mirror, row mirror), then the
-// four row winners read with readlane and combined in row order.
-__device__ inline void wave_best(float& v, int& i) {
-  cand_step<0xB1>(v, i);
-  cand_step<0x4E>(v, i);
-  cand_step<0x141>(v, i);
-  cand_step<0x140>(v, i);
-  float bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-  int bi = __builtin_amdgcn_readlane(i, 0);
-#pragma unroll
-  for (int r = 1; r < 4; r++) {
-    const float ov =
-        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * r));
-    const int oi = __builtin_amdgcn_readlane(i, 16 * r);
-    if (cand_better(ov, oi, bv, bi)) {
-      bv = ov;
-      bi = oi;
-    }
-  }
-  v = bv;
-  i = bi;
-}
+// Maximum of v over the wave, in every lane: DPP butterflies inside each 16-lane
+// row (quad xor 1, xor 2, half-row mirror, row mirror), then the four row
+// maxima read with readlane.  A max, so the order of the steps is free.
 __device__ inline float wave_max(float v) {
   auto step = [&](float o) { v = o > v ? o : v; };
   step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
@@ -143,7 +107,8 @@ __device__ inline void route_softmax(const float* __restrict__ lg, int E, float*
       for (int k = 0; k < 8; k++) cur[k] = *reinterpret_cast<const float4*>(pw + 4 * k);
     }
     for (int e = 0; e < e32; e += 32) {
-      if (e + 32 < e32) {
+      const bool more = e + 32 < e32;
+      if (more) {
 #pragma unroll
         for (int k = 0; k < 8; k++) nxt[k] = *reinterpret_cast<const float4*>(pw + e + 32 + 4 * k);
       }
@@ -154,8 +119,10 @@ __device__ inline void route_softmax(const float* __restrict__ lg, int E, float*
         sum += cur[k].z;
         sum += cur[k].w;
       }
+      if (more) {
 #pragma unroll
-      for (int k = 0; k < 8; k++) cur[k] = nxt[k];
+        for (int k = 0; k < 8; k++) cur[k] = nxt[k];
+      }
     }
     for (int e = e32; e < E; e++) sum += pw[e];
     inv = 1.0f / sum;
