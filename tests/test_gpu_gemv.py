@@ -211,3 +211,27 @@ def test_dropin_quantize_and_ops(oracle):
     p = out.copy()
     lib.qr_ops_softmax(_fp(p), 128)
     assert_bits_equal(p, oracle.softmax(out), "ops softmax")
+
+
+@pytest.mark.parametrize("qtype,n", [(Q.TYPE_Q4_K, 32000), (Q.TYPE_Q6_K, 4096), (Q.TYPE_Q8_0, 4096)])
+def test_gemv_graph_replays(dev, qtype, n):
+    """The GEMV captured into a HIP graph (as bench.py times it): four replays,
+    each after an eager clear of the output and a synchronization, every one
+    bit-exact with the eager launch (block engine for Q4_K, streaming engine
+    for Q6_K / Q8_0)."""
+    d = 2048
+    W = I.blocks(9100 + qtype, qtype, n * (d // I.BLOCK[qtype][0]))
+    X = I.activations(9200 + qtype, 1, d)
+    wb, xb, yb = dev.upload(W), dev.upload(X), dev.alloc(n * 4)
+    dev.gemv(qtype, wb.ptr, xb.ptr, yb.ptr, n, d, 1)
+    want = dev.download(yb, (n,), np.float32)
+    g = dev.capture(lambda: dev.gemv(qtype, wb.ptr, xb.ptr, yb.ptr, n, d, 1))
+    try:
+        for r in range(4):
+            dev.write(yb, np.full(n, np.nan, np.float32))
+            dev.sync()
+            dev.graph_launch(g)
+            dev.sync()
+            assert_bits_equal(dev.download(yb, (n,), np.float32), want, "replay %d" % r)
+    finally:
+        dev.graph_destroy(g)

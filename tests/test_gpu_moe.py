@@ -328,3 +328,31 @@ def test_moe_t1_down_types(dev, oracle, dt, dim, hidden):
     x = I.activations(seed + 4, 1, dim)
     xb = I.activations(seed + 5, 1, dim)
     check_moe(dev, oracle, layer, x, xb, ORDER_AVX2, "t1 %d/%d down %d" % (dim, hidden, dt))
+
+
+@pytest.mark.parametrize("T", [1, 16, 64])
+def test_moe_graph_replays(dev, oracle, T):
+    """The MoE layer captured into a HIP graph (as bench.py times it) at the
+    one-token, skinny/16-pair and 32-pair sizes: three replays, each after an
+    eager reset of the residual x and a synchronization, every one bit-exact
+    with the eager layer (itself checked against the oracle)."""
+    layer, m = random_layer(dev, "a")
+    x = I.activations(9300 + T, T, m["dim"])
+    xb = I.activations(9301 + T, T, m["dim"])
+    want, _, _ = run_moe(dev, layer, x, xb, ORDER_AVX2)
+    keep = []
+    ref, _, _ = oracle.moe_forward(x, xb, layer.oracle_layer(keep), order=ORDER_AVX2,
+                                   dot_order=ORDER_SEQ, threads=16)
+    assert_bits_equal(want, ref, "eager layer T=%d" % T)
+    xd, xbd = dev.upload(x), dev.upload(xb)
+    g = dev.capture(lambda: dev.moe_forward(layer.L, xd.ptr, xbd.ptr, T, ORDER_AVX2))
+    try:
+        for r in range(3):
+            dev.write(xd, x)
+            dev.sync()
+            dev.graph_launch(g)
+            dev.sync()
+            assert_bits_equal(dev.download(xd, (T, m["dim"]), np.float32), want,
+                              "replay %d T=%d" % (r, T))
+    finally:
+        dev.graph_destroy(g)
