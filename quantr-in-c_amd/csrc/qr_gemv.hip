@@ -402,7 +402,7 @@ constexpr size_t kLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
 bool gemv_blk_ok(int type, int d, int nt) {
   if (type != QR_T_Q4_K && type != QR_T_Q5_K) return false;
   const int nb = d >> 8;
-  if (nb < 1 || nb > 64 || (d & 3) || nt > 2) return false;  // more tokens: register spills
+  if (nb < 1 || nb > 64 || (d & 3) || nt > 4) return false;
   return blk_lds_bytes_t(type, d, nt, 1, false) <= kLdsMax;
 }
 
@@ -496,7 +496,7 @@ static hipError_t launch_blk_t(const GemvArgs& a, hipStream_t st) {
 
 template <int TYPE, int NT>
 static hipError_t launch_any_t(const GemvArgs& a, hipStream_t st) {
-  if constexpr ((TYPE == QR_T_Q4_K || TYPE == QR_T_Q5_K) && NT <= 2) {
+  if constexpr ((TYPE == QR_T_Q4_K || TYPE == QR_T_Q5_K) && NT <= 4) {
     if (gemv_blk_ok(TYPE, a.d, NT)) return launch_blk_t<TYPE, NT>(a, st);
   }
   if constexpr (NT <= 4) {
