@@ -314,10 +314,11 @@ int device_cus() {
 }
 
 // Workgroups per CU of the streaming kernels (QR_STREAM_WG_PER_CU overrides,
-// 1..16, for tuning sweeps; 0: the default).  Default 3, or as many as fit
-// in LDS: measured on 32000 x 2048 Q6_K / Q8_0 and the 151936 x 2048 Q6_K
-// lm_head, 3 per CU streams 4.3 TB/s where 2 and 4 give 3.6-4.0 and 1 gives
-// 2.6.
+// 1..16, for tuning sweeps; 0: the default).  Default 3 for one or two
+// tokens, 2 for more, or as many as fit in LDS: measured on 32000 x 2048 Q6_K
+// / Q8_0 and the 151936 x 2048 Q6_K lm_head, 3 per CU streams 4.3 TB/s for
+// one token where 2 and 4 give 3.6-4.0 and 1 gives 2.6; with 4 tokens 2 per
+// CU takes 28.9 us where 3 takes 33.8 (Q6_K) and 40.8 (Q8_0).
 static int stream_wg_per_cu() {
   static int v = -1;
   if (v < 0) {
@@ -347,8 +348,9 @@ static hipError_t launch_stream_t(const GemvArgs& a, hipStream_t st) {
   const int want = (ntiles + kStreamWaves - 1) / kStreamWaves;
   int per_cu = stream_wg_per_cu();
   if (per_cu == 0) {
-    per_cu = lds > 0 ? (int)((160 * 1024) / lds) : 3;
-    per_cu = per_cu < 1 ? 1 : (per_cu > 3 ? 3 : per_cu);
+    constexpr int kDefault = NT > 2 ? 2 : 3;  // measured: 4 tokens run best at 2 per CU
+    per_cu = lds > 0 ? (int)((160 * 1024) / lds) : kDefault;
+    per_cu = per_cu < 1 ? 1 : (per_cu > kDefault ? kDefault : per_cu);
   }
   const int cap = device_cus() * per_cu;
   const int grid = want < cap ? want : cap;
