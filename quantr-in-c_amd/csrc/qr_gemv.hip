@@ -320,12 +320,11 @@ int device_cus() {
 // one token where 2 and 4 give 3.6-4.0 and 1 gives 2.6; with 4 tokens 2 per
 // CU takes 28.9 us where 3 takes 33.8 (Q6_K) and 40.8 (Q8_0).
 static int stream_wg_per_cu() {
-  static int v = -1;
-  if (v < 0) {
+  static const int v = [] {  // read once; thread-safe initialisation
     const char* e = getenv("QR_STREAM_WG_PER_CU");
-    int x = e ? atoi(e) : 0;
-    v = (x >= 1 && x <= 16) ? x : 0;
-  }
+    const int x = e ? atoi(e) : 0;
+    return (x >= 1 && x <= 16) ? x : 0;
+  }();
   return v;
 }
 
@@ -420,31 +419,31 @@ static int env_knob(const char* name, int lo, int hi, int dflt) {
   const int x = e ? atoi(e) : 0;
   return (x >= lo && x <= hi) ? x : dflt;
 }
+// each knob is read once, with thread-safe initialisation
 static int blk_depth() {
-  static int v = 0;
-  if (!v) v = env_knob("QR_BLK_DEPTH", 1, 2, 1);
+  static const int v = env_knob("QR_BLK_DEPTH", 1, 2, 1);
   return v;
 }
 static int blk_wg_per_cu() {
-  static int v = -1;
-  if (v < 0) v = env_knob("QR_BLK_WG_PER_CU", 1, 16, 0);
+  static const int v = env_knob("QR_BLK_WG_PER_CU", 1, 16, 0);
   return v;
 }
 // QR_BLK_XS: 1 stages the activation through LDS by DMA, 2 loads it into
 // registers (less LDS per workgroup); default 1.
 static int blk_xs_mode() {
-  static int v = 0;
-  if (!v) v = env_knob("QR_BLK_XS", 1, 2, 1);
+  static const int v = env_knob("QR_BLK_XS", 1, 2, 1);
   return v;
 }
 
 // Opt a kernel into LDS beyond 64 KiB, once per device.
-hipError_t lds_opt_in(const void* fn, bool* done) {
+// done[dev] records the opt-in per device (several host threads may race to
+// make it; the attribute call is idempotent).
+hipError_t lds_opt_in(const void* fn, std::atomic<bool>* done) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-  if (!done[dev]) {
+  if (!done[dev].load(std::memory_order_acquire)) {
     // the dynamic allowance is what the kernel's static LDS leaves of the CU's
     hipFuncAttributes fa;
     e = hipFuncGetAttributes(&fa, fn);
@@ -453,14 +452,14 @@ hipError_t lds_opt_in(const void* fn, bool* done) {
     if (stat >= kLdsMax) return hipErrorInvalidValue;
     e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kLdsMax - stat));
     if (e != hipSuccess) return e;
-    done[dev] = true;
+    done[dev].store(true, std::memory_order_release);
   }
   return hipSuccess;
 }
 
 template <int TYPE, int NT, int D, bool XS>
 static hipError_t launch_blk_d(const GemvArgs& a, int grid, size_t lds, hipStream_t st) {
-  static bool opted[64] = {false};
+  static std::atomic<bool> opted[64];
   if (lds > 64 * 1024) {
     hipError_t e = lds_opt_in((const void*)k_gemv_blk<TYPE, NT, D, XS>, opted);
     if (e != hipSuccess) return e;

@@ -4,6 +4,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+
+#include <atomic>
 #include <stdint.h>
 
 #include "../../include/qr_hip.h"
@@ -17,7 +19,7 @@ bool gemv_blk_ok(int type, int d, int nt);
 int device_cus();
 // Let kernel fn use up to 160 KiB of dynamic LDS on the current device (once
 // per device; done[] is the caller's per-device flag array of 64 entries).
-hipError_t lds_opt_in(const void* fn, bool* done);
+hipError_t lds_opt_in(const void* fn, std::atomic<bool>* done);
 int gemv_rows_per_wg(int type, int n, int d, int nt);
 hipError_t gemv_launch(int type, const void* W, const float* X, float* Y, int n, int d, int nt,
                        int xstride, int ystride, int32_t* acc, int32_t* accb, hipStream_t st);

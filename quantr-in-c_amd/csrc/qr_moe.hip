@@ -608,12 +608,11 @@ static hipError_t combine_launch(float* x, const float* y, const int32_t* inv, c
 // Average pairs per expert from which the grouped products use MFMA
 // (QR_MFMA_MIN_PAIRS overrides, for tuning sweeps).
 static int mfma_min_pairs() {
-  static int v = -1;
-  if (v < 0) {
+  static const int v = [] {  // read once; thread-safe initialisation
     const char* e = getenv("QR_MFMA_MIN_PAIRS");
     const int x = e ? atoi(e) : 0;
-    v = x > 0 ? x : 1;
-  }
+    return x > 0 ? x : 1;
+  }();
   return v;
 }
 #define kMfmaPairsPerExpert mfma_min_pairs()

@@ -577,12 +577,11 @@ hipError_t quant_rows_launch(const float* x, int xstride, int nrows, int cols, b
 // Pairs per work item: 16 while experts see few pairs each (less padding of
 // the 16-pair MFMA tile), 32 beyond (half the weight re-reads).
 int mfma_tile(int T, int K, int E) {
-  static int forced = -1;
-  if (forced < 0) {
+  static const int forced = [] {  // read once; thread-safe initialisation
     const char* s = getenv("QR_MFMA_TILE");
     const int v = s ? atoi(s) : 0;
-    forced = (v == 16 || v == 32) ? v : 0;
-  }
+    return (v == 16 || v == 32) ? v : 0;
+  }();
   if (forced) return forced;
   return (long)T * K >= 16L * E ? 32 : 16;
 }
@@ -593,7 +592,7 @@ static hipError_t mfma_launch_t(const MfmaArgs& a, int items, hipStream_t st) {
   if constexpr (G::LDS > 160 * 1024) {
     return mfma_launch_t<TYPE, GATEUP, NJ, 2, 4>(a, items, st);  // the shape that always fits
   } else {
-    static bool opted[64] = {false};
+    static std::atomic<bool> opted[64];
     dim3 grid((a.rows + G::MR - 1) / G::MR, items);
     if (grid.x == 0 || grid.y == 0) return hipSuccess;
     if (G::LDS > 64 * 1024) {
@@ -612,21 +611,26 @@ static hipError_t mfma_launch_t(const MfmaArgs& a, int items, hipStream_t st) {
 // both products with 32-pair items, the 24-unit down product always -- and
 // two slots for gate/up with 16-pair items, whose eight stages are latency
 // bound.  QR_MFMA_GU / QR_MFMA_DN ("NW,D") override, for tuning sweeps.
-static void mfma_shape(bool gateup, int tile, int* nw, int* d) {
-  static int cfg[2][2] = {{-1, -1}, {-1, -1}};
-  int* c = cfg[gateup ? 1 : 0];
-  if (c[0] < 0) {
-    c[0] = 0;
-    const char* s = getenv(gateup ? "QR_MFMA_GU" : "QR_MFMA_DN");
-    int x = 0, y = 0;
-    if (s && sscanf(s, "%d,%d", &x, &y) == 2 && (x == 4 || x == 8) && (y >= 1 && y <= 3)) {
-      c[0] = x;
-      c[1] = y;
-    }
+struct ShapeKnob {
+  int nw = 0, d = 0;  // nw == 0: no override
+};
+static ShapeKnob shape_knob(const char* name) {
+  ShapeKnob k;
+  const char* s = getenv(name);
+  int x = 0, y = 0;
+  if (s && sscanf(s, "%d,%d", &x, &y) == 2 && (x == 4 || x == 8) && (y >= 1 && y <= 3)) {
+    k.nw = x;
+    k.d = y;
   }
-  if (c[0] > 0) {
-    *nw = c[0];
-    *d = c[1];
+  return k;
+}
+static void mfma_shape(bool gateup, int tile, int* nw, int* d) {
+  // read once each; thread-safe initialisation
+  static const ShapeKnob gu = shape_knob("QR_MFMA_GU"), dn = shape_knob("QR_MFMA_DN");
+  const ShapeKnob& c = gateup ? gu : dn;
+  if (c.nw > 0) {
+    *nw = c.nw;
+    *d = c.d;
   } else {
     *nw = 4;
     *d = (gateup && tile == 16) ? 2 : 1;
@@ -680,11 +684,11 @@ hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const ui
   a.QO = QO;
   a.qperm = qperm ? 1 : 0;
   {
-    static int knob = -1;  // QR_MFMA_SKINNY=0 turns the skinny form off (tuning sweeps)
-    if (knob < 0) {
+    // QR_MFMA_SKINNY=0 turns the skinny form off (tuning sweeps); read once
+    static const int knob = [] {
       const char* e = getenv("QR_MFMA_SKINNY");
-      knob = (e && e[0] == '0') ? 0 : 1;
-    }
+      return (e && e[0] == '0') ? 0 : 1;
+    }();
     a.skinny = knob;
   }
   // items of up to 16 pairs: an expert rarely has more than one, so its rows

@@ -387,18 +387,10 @@ bool down1v2_ok(int type, int K, int dim, int hidden) {
 
 template <int TYPE>
 static hipError_t down1_launch_t(const Down1Args& a, int grid, size_t lds, hipStream_t st) {
-  static bool opted[64] = {false};
+  static std::atomic<bool> opted[64];
   if (lds > 64 * 1024) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
+    const hipError_t e = lds_opt_in((const void*)k_down1<TYPE>, opted);
     if (e != hipSuccess) return e;
-    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-    if (!opted[dev]) {
-      e = hipFuncSetAttribute((const void*)k_down1<TYPE>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      if (e != hipSuccess) return e;
-      opted[dev] = true;
-    }
   }
   hipLaunchKernelGGL(k_down1<TYPE>, dim3(grid), dim3(64 * a.K), lds, st, a);
   return hipGetLastError();

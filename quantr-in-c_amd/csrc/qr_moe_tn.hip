@@ -349,7 +349,7 @@ template <int LANES>
 static hipError_t rlogits_row_launch_t(const float* W, const float* X, int T, int E, int d,
                                        float* logits, hipStream_t st) {
   const size_t lds = rlogits_row_lds<LANES>(T, d);
-  static bool opted[64] = {false};
+  static std::atomic<bool> opted[64];
   if (lds > 64 * 1024) {
     const hipError_t e = lds_opt_in((const void*)k_rlogits_row<LANES>, opted);
     if (e != hipSuccess) return e;
@@ -366,7 +366,7 @@ static hipError_t rlogits4_launch_t(const float* W, const float* X, int T, int E
   constexpr int TW = NTB * TT, RW = NRB * RT;
   constexpr size_t lds = rlogits_lds<TW, RW, NBUF>();
   static_assert(lds <= 160 * 1024, "LDS");
-  static bool opted[64] = {false};
+  static std::atomic<bool> opted[64];
   if (lds > 64 * 1024) {
     const hipError_t e =
         lds_opt_in((const void*)k_rlogits4<LANES, NTB, TT, NRB, RT, NBUF>, opted);
@@ -384,7 +384,7 @@ static hipError_t rlogits_launch_t(const float* W, const float* X, int T, int E,
   constexpr int TW = NTB * TT, RW = NRB * RT;
   constexpr size_t lds = rlogits_lds<TW, RW, NBUF>();
   static_assert(lds <= 160 * 1024, "LDS");
-  static bool opted[64] = {false};
+  static std::atomic<bool> opted[64];
   if (lds > 64 * 1024) {
     const hipError_t e =
         lds_opt_in((const void*)k_rlogits<LANES, NTB, TT, NRB, RT, NBUF>, opted);
@@ -398,12 +398,11 @@ static hipError_t rlogits_launch_t(const float* W, const float* X, int T, int E,
 
 // QR_RLOGITS_VEC4=0 selects the one-chain-per-thread kernels (tuning sweeps).
 static bool rlogits_vec4() {
-  static int v = -1;
-  if (v < 0) {
+  static const bool v = [] {  // read once; thread-safe initialisation
     const char* e = getenv("QR_RLOGITS_VEC4");
-    v = (e && e[0] == '0') ? 0 : 1;
-  }
-  return v == 1;
+    return !(e && e[0] == '0');
+  }();
+  return v;
 }
 
 // Tiles of 16 tokens x 4 router rows for few tokens (more workgroups for the
