@@ -24,6 +24,16 @@
 extern "C" {
 #endif
 
+/* The reference build whose arithmetic the results match (the router's
+ * KernelOps.matmul order and the Q8_0 dot order; see qr_hip.h):
+ * QR_ORDER_SEQ the Makefile's -std=c99 build, QR_ORDER_AVX2 the CI's
+ * -mavx2 -mfma build, QR_ORDER_AVX512 a build with -mavx512f. */
+#ifndef QR_ORDER_SEQ
+#define QR_ORDER_SEQ 0
+#define QR_ORDER_AVX2 1
+#define QR_ORDER_AVX512 2
+#endif
+
 /* Field-for-field the layout of KernelOps (include/kernels.h:6-12), so a
  * table of these functions can be used where the reference takes KernelOps. */
 typedef struct {
@@ -34,10 +44,11 @@ typedef struct {
     const char* name;
 } qr_kernel_ops;
 
-/* Select the GPU and the router's fp32 accumulation order (QR_ORDER_SEQ /
- * QR_ORDER_AVX2 / QR_ORDER_AVX512 of qr_hip.h; use the order of the CPU build
- * the results are to match).  Optional: the first call of any entry below
- * initialises device 0 with QR_ORDER_AVX2.  Returns 0 or a qr_status. */
+/* Select the GPU and the reference build to match (QR_ORDER_SEQ /
+ * QR_ORDER_AVX2 / QR_ORDER_AVX512): it sets the router's fp32 accumulation
+ * order and the Q8_0 dot order of every entry below.  Optional: the first
+ * call of any entry initialises device 0 with QR_ORDER_AVX2 (the CI build).
+ * Returns 0 or a qr_status. */
 int qr_dropin_init(int device, int router_order);
 void qr_dropin_shutdown(void);
 
@@ -49,7 +60,14 @@ int qr_gpu_available(void);
 /* Replaces matmul_q_fused (include/quant.h:91-92, src/quant.c:441-523):
  * out[n] = W[n x d] . x[d] for F32, Q8_0, Q4_K, Q5_K, Q6_K weights; x is
  * quantized to Q8_0 once per call; NULL weights and unknown types give
- * zeros.  Q4_K is the corrected dot (see qr_hip.h). */
+ * zeros.  Q8_0 dots follow the build selected by qr_dropin_init.  Q4_K is the
+ * corrected dot (see qr_hip.h).
+ *
+ * Weight registry: the first call that sees a weight pointer uploads the
+ * matrix; later calls with the same pointer and size reuse the device copy
+ * while the host bytes at both ends of the matrix still hash the same.
+ * Weights must not change in place while registered;
+ * qr_dropin_release_weights drops every copy. */
 void qr_matmul_q_fused(float* out, const float* x, const void* w, uint32_t type, int n, int d,
                        int threads);
 

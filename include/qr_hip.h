@@ -46,13 +46,22 @@ typedef enum {
 #define QR_TYPE_Q5_K 13
 #define QR_TYPE_Q6_K 14
 
-/* fp32 accumulation order of the router / F32 GEMV, one per reference build:
- * SEQ    matmul_ref and the -std=c99 build's matmul_omp (src/kernels.c:18-28)
- * AVX2   matmul_omp built -mavx2 -mfma (src/kernels.c:50-65)
- * AVX512 matmul_omp built -mavx512f    (src/kernels.c:38-49)              */
+/* The reference build whose fp32 accumulation orders a call reproduces:
+ *   SEQ    the Makefile's -std=c99 build: matmul_ref (src/kernels.c:18-28) and
+ *          the scalar Q8_0 dot (src/quant.c:279-285);
+ *   AVX2   the CI's -mavx2 -mfma build: matmul_omp's 8 FMA chains
+ *          (src/kernels.c:50-65) and the Q8_0 dot's 8 lane accumulators,
+ *          updated by a multiply then an add (src/quant.c:245-277);
+ *   AVX512 a build with -mavx512f: matmul_omp's 16 FMA chains
+ *          (src/kernels.c:38-49) and the Q8_0 dot's 8 lanes updated by fused
+ *          multiply-adds (src/quant.c:268-269).
+ * K-quant dots are scalar in every build and do not depend on the order.
+ * (The same values are defined in qr_dropin.h.) */
+#ifndef QR_ORDER_SEQ
 #define QR_ORDER_SEQ 0
 #define QR_ORDER_AVX2 1
 #define QR_ORDER_AVX512 2
+#endif
 
 typedef struct qr_ctx qr_ctx;
 
@@ -77,10 +86,17 @@ int qr_memset(qr_ctx* ctx, void* dst, int value, size_t bytes);
 int qr_timer_start(qr_ctx* ctx);
 int qr_timer_stop(qr_ctx* ctx, float* ms);
 /* HIP graph capture of the context stream: calls between begin and end are
- * recorded, not run; the instantiated graph replays them back to back.  Only
- * calls that allocate nothing and set no memory may be captured (qr_gemv,
- * qr_matmul_f32, qr_softmax, and qr_moe_forward once it has run for the same
- * or a larger T outside capture). */
+ * recorded, not run; the instantiated graph replays them back to back.
+ * Calls that would allocate, free, synchronize or record a memset while the
+ * stream is capturing return QR_ERR_INVALID instead (qr_malloc, qr_free,
+ * the synchronous copies, qr_timer_stop, qr_weights_upload*, and qr_moe_route /
+ * qr_moe_forward when they need more scratch than any earlier call).  The
+ * scratch a call needs depends on the layer (dim, hidden, E, K, the shared
+ * expert) as well as on T: run the largest captured call once outside
+ * capture first.  Scratch that a larger call outgrows is kept until
+ * qr_ctx_destroy, so graphs captured earlier stay valid.  qr_gemv with NULL
+ * weights zero-fills with a kernel and qr_memset uses a fill kernel while
+ * capturing, so neither records a memset node. */
 int qr_capture_begin(qr_ctx* ctx);
 int qr_capture_end(qr_ctx* ctx, void** graph);
 int qr_graph_launch(qr_ctx* ctx, void* graph);
@@ -106,6 +122,12 @@ int qr_gemv_ex(qr_ctx* ctx, uint32_t type, const void* w, const float* x, int xs
                float* y, int ystride, int n, int d, int nt, int32_t* acc, int32_t* accb);
 int qr_gemv(qr_ctx* ctx, uint32_t type, const void* w, const float* x, float* y, int n, int d,
             int nt);
+/* qr_gemv_ex for the reference build `order` (QR_ORDER_*): Q8_0 weights use
+ * that build's dot order; other types are the same in every build.
+ * qr_gemv_ex is qr_gemv_ord with QR_ORDER_SEQ. */
+int qr_gemv_ord(qr_ctx* ctx, int order, uint32_t type, const void* w, const float* x,
+                int xstride, float* y, int ystride, int n, int d, int nt, int32_t* acc,
+                int32_t* accb);
 
 /* fp32 GEMV in a reference accumulation order (router logits):
  * y[t][r] = sum_j w[r][j] * x[t][j]. */
@@ -161,6 +183,9 @@ int qr_moe_dispatch(qr_ctx* ctx, const int32_t* idx, int T, int K, int E, int32_
 
 /* The whole layer for T tokens: x[t] += sum_k w[t][k] * expert(xb[t]) in slot
  * order (src/runtime.c:242-269), plus the shared expert when present.
+ * `order` is the reference build (QR_ORDER_*): the router's accumulation
+ * order and, for Q8_0 experts, the dot order.  The shared expert has no
+ * reference counterpart and always uses the sequential order.
  * idx_out / w_out (optional, [T][K]) receive the routing. */
 int qr_moe_forward(qr_ctx* ctx, const qr_moe_layer* L, float* x, const float* xb, int T,
                    int order, int32_t* idx_out, float* w_out);
@@ -168,13 +193,19 @@ int qr_moe_forward(qr_ctx* ctx, const qr_moe_layer* L, float* x, const float* xb
 /* ---- weight registry (host pointer -> device copy) ---------------------- */
 
 /* Upload `bytes` from host memory once and return the device copy; later
- * calls with the same host pointer return the same copy (the registry keys
- * on the host address and size).  Copies live until released. */
+ * calls with the same host pointer return the same copy.  The registry keys
+ * on the host address; an entry is reused only for the same size and while
+ * the first and last 64 bytes of the host memory still hash to what was
+ * uploaded (so a freed and reused address with other contents is uploaded
+ * again).  Weights are expected not to change in place while registered
+ * (the reference's mmap).  Copies live until released. */
 int qr_weights_upload(qr_ctx* ctx, const void* host, size_t bytes, const void** dev);
 /* Upload nparts host blocks of part_bytes each into one contiguous device
  * tensor (part i at offset i * part_bytes), registered under `key`: the
  * per-expert weight tensors of src/model.c:421-433 that are not one 3-D
- * slab. */
+ * slab.  The entry remembers a digest of the part pointers, the part size and
+ * the two ends of every part: a later call under the same key with other
+ * parts (or other contents) gathers again. */
 int qr_weights_upload_parts(qr_ctx* ctx, const void* key, const void* const* parts,
                             size_t part_bytes, int nparts, const void** dev);
 int qr_weights_lookup(qr_ctx* ctx, const void* host, const void** dev);

@@ -218,8 +218,9 @@ int qro_row_accum(uint32_t type, const void* row, const void* xq8, int d,
     return units;
 }
 
-/* src/quant.c:279-285 (SEQ) and src/quant.c:245-277 (AVX2, no AVX-512: the
- * per-lane update is a multiply then an add). */
+/* src/quant.c:279-285 (SEQ) and src/quant.c:245-277 (8 lanes): the AVX2 build
+ * updates a lane with a multiply then an add (src/quant.c:271), a build with
+ * AVX-512 enabled with one fused multiply-add (src/quant.c:269). */
 static float dot_q8_0(const uint8_t* a, const uint8_t* b, int d, int order) {
     int nb = d / QK8, i, k;
     float sum = 0.0f;
@@ -244,8 +245,12 @@ static float dot_q8_0(const uint8_t* a, const uint8_t* b, int d, int order) {
                          (int8_t)pa[2 * k + 1] * (int8_t)pb[2 * k + 1];
                 int hi = (int8_t)pa[16 + 2 * k] * (int8_t)pb[16 + 2 * k] +
                          (int8_t)pa[17 + 2 * k] * (int8_t)pb[17 + 2 * k];
-                float p = (float)(lo + hi) * dd;
-                acc[k] = p + acc[k];
+                if (order == QRO_ORDER_AVX512) {
+                    acc[k] = fmaf((float)(lo + hi), dd, acc[k]);
+                } else {
+                    float p = (float)(lo + hi) * dd;
+                    acc[k] = p + acc[k];
+                }
             }
         }
         for (k = 0; k < 8; k++) sum += acc[k];

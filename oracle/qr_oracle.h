@@ -14,8 +14,9 @@
  *                               65536 codes / special floats), round-trip laws
  *   qro_quantize_row_q8_0       golden vectors from the compiled reference
  *   qro_dequantize_row          golden vectors (types 8, 12, 13, 14)
- *   qro_vec_dot Q8_0 SEQ/AVX2   golden vectors from the -std=c99 and the
- *                               -mavx2 -mfma builds of the reference
+ *   qro_vec_dot Q8_0 SEQ/AVX2/  golden vectors from the -std=c99, the
+ *              AVX512           -mavx2 -mfma and the -mavx512f builds of the
+ *                               reference
  *   qro_vec_dot Q5_K, Q6_K      golden vectors
  *   qro_vec_dot Q4_K            the reference's Q4_K dot is defective; the
  *                               corrected form equals the reference's Q5_K dot
@@ -56,8 +57,10 @@ extern "C" {
  * AVX2:   the -mavx2 -mfma build (.github/workflows/ci.yml:21): matmul_omp's
  *         8-lane FMA chains (src/kernels.c:50-65) and vec_dot_q8_0_q8_0's
  *         8-lane accumulators (src/quant.c:245-277).
- * AVX512: matmul_omp's 16-lane FMA chains + _mm512_reduce_add_ps tree
- *         (src/kernels.c:38-49), for an -mavx512f build. */
+ * AVX512: an -mavx512f build: matmul_omp's 16-lane FMA chains +
+ *         _mm512_reduce_add_ps tree (src/kernels.c:38-49), and
+ *         vec_dot_q8_0_q8_0's 8 lanes updated by fused multiply-adds
+ *         (src/quant.c:268-269). */
 #define QRO_ORDER_SEQ 0
 #define QRO_ORDER_AVX2 1
 #define QRO_ORDER_AVX512 2

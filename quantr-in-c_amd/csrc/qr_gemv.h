@@ -220,6 +220,71 @@ __device__ inline int dot_q8_unit(const uint32_t w[8], const int8_t* xa) {
   return dot_q8_regs(w, xv);
 }
 
+// ---------------------------------------------------------------------------
+// Q8_0 dot orders of the reference builds (vec_dot_q8_0_q8_0,
+// src/quant.c:242-288).  The integer products are the same; the fp32
+// accumulation differs:
+//   kQ8Seq     -std=c99 build: per block isum, sum += (isum * da) * db,
+//              blocks in order (src/quant.c:279-285);
+//   kQ8Avx2    -mavx2 -mfma build: 8 int32 lanes per block, lane k holding the
+//              products of bytes 2k, 2k+1, 16+2k, 17+2k (madd of the low and
+//              high 16 bytes, src/quant.c:249-264); lane accumulators
+//              acc_k = (lane_k * (da * db)) + acc_k, a multiply then an add
+//              (src/quant.c:271); finally 0 + acc_0 + ... + acc_7
+//              (src/quant.c:274-276);
+//   kQ8Avx512  a build with AVX-512 enabled: the same lanes, each updated by
+//              one fused multiply-add (src/quant.c:268-269).
+// The values equal QR_ORDER_SEQ / _AVX2 / _AVX512: one order names one build.
+// ---------------------------------------------------------------------------
+constexpr int kQ8Seq = 0;
+constexpr int kQ8Avx2 = 1;
+constexpr int kQ8Avx512 = 2;
+// Term slots per unit: one fp32 term, or (lane orders) the 8 lane sums as
+// floats plus the block's da * db.
+__host__ __device__ constexpr int q8_slots(int type, int q8o) {
+  return (type == QR_T_Q8_0 && q8o != kQ8Seq) ? 9 : 1;
+}
+
+// The 8 lane sums of one Q8_0 block (natural byte order in w and x): lane k
+// gathers bytes {2k, 2k+1} of dword k/2 and of dword 4 + k/2 into one dword
+// (v_perm) and takes one 4-wide dot.
+__device__ inline void q8_lanes(const uint32_t w[8], const uint32_t xv[8], int l[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const uint32_t sel = (k & 1) ? 0x07060302u : 0x05040100u;
+    const uint32_t pw = __builtin_amdgcn_perm(w[4 + (k >> 1)], w[k >> 1], sel);
+    const uint32_t px = __builtin_amdgcn_perm(xv[4 + (k >> 1)], xv[k >> 1], sel);
+    l[k] = sdot4(pw, px, 0);
+  }
+}
+
+// One lane accumulator of a row in a lane order: acc over the units' lane-k
+// sums f[u] and scales dd[u], unit 0 first.
+template <int Q8O>
+__device__ inline float q8_lane_update(float f, float dd, float acc) {
+  if constexpr (Q8O == kQ8Avx512) return __builtin_fmaf(f, dd, acc);
+  else return f * dd + acc;  // contraction is off: a multiply, then an add
+}
+
+// A row's value in a lane order from its term slots: tp[k * ts + u] holds
+// lane k's sum of unit u (k < 8) and tp[8 * ts + u] the unit's da * db.  The
+// 8 accumulators advance together, then are added 0..7 into 0.0f.
+template <int Q8O>
+__device__ inline float q8_row_sum(const float* tp, int ts, int U) {
+  float acc[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) acc[k] = 0.0f;
+  for (int u = 0; u < U; u++) {
+    const float dd = tp[8 * ts + u];
+#pragma unroll
+    for (int k = 0; k < 8; k++) acc[k] = q8_lane_update<Q8O>(tp[k * ts + u], dd, acc[k]);
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; k++) s += acc[k];
+  return s;
+}
+
 // fp32 terms, in the reference's operation order (contraction is off).
 // Q4_K/Q5_K: (sc*isum - m*bsum) * bd   (src/quant.c:399)
 __device__ inline float term_q45(uint32_t hdr0, uint32_t sbyte, int isum, int bsum, float bd) {
@@ -317,6 +382,37 @@ __device__ inline void direct_unit_terms(uint4 hdr, uint4 qs, uint32_t qh, int u
   }
 }
 
+// Q8_0 unit u of a row staged in LDS, in a lane order: for each activation row
+// tok0 + t, slot[t][k * ts] = lane k's sum (k < 8), slot[t][8 * ts] = da * db,
+// where slot[t] = dst + t * tstep.  isum_out receives the unit's int32 sum.
+template <int NT>
+__device__ inline void q8_unit_lanes(int row_lds, int u, const UnitSrc& S, int tok0, float* dst,
+                                     size_t tstep, int ts, int32_t* isum_out) {
+  const int o = row_lds + u * QR_Q8_BYTES;
+  const uint32_t* T = S.tile;
+  const float da = qr_h2f(lds_u32(T, o) & 0xFFFFu);
+  uint32_t w[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) w[k] = lds_u32(T, o + 2 + 4 * k);
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int a = (tok0 + t) * S.nxb + u;
+    uint32_t xv[8];
+    act8_from_lds(S.act.q + (size_t)a * 32, xv);
+    int l[8];
+    q8_lanes(w, xv, l);
+    float* sp = dst + (size_t)t * tstep;
+    int is = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      sp[(size_t)k * ts] = (float)l[k];
+      is += l[k];
+    }
+    sp[(size_t)8 * ts] = da * S.act.bd[a];  // fp16_to_fp32(a.d) * fp16_to_fp32(b.d)
+    isum_out[t] = is;
+  }
+}
+
 template <int TYPE, int NT>
 __device__ inline void unit_terms(const uint8_t* __restrict__ wrow, int row_lds, int u,
                                   const UnitSrc& S, int tok0, float* terms_out,
@@ -375,6 +471,31 @@ __device__ inline float row_sum(const float* tp, int U) {
   float s = 0.0f;
   for (int u = 0; u < U; u++) s += tp[u];
   return s;
+}
+
+// A row's value from its term slots: the sequential sum, or (Q8_0 lane
+// orders) the lane accumulators of slots [9][ts].
+template <int TYPE, int Q8O>
+__device__ inline float row_value(const float* tp, int ts, int U) {
+  if constexpr (q8_slots(TYPE, Q8O) == 9) return q8_row_sum<Q8O>(tp, ts, U);
+  else return row_sum(tp, U);
+}
+
+// Terms of unit u of one row for NT activation rows into term slots: row
+// block t at dst + t * tstep, unit u at [u] (one slot per unit) or at
+// [k * ts + u] (lane orders).  isum_out receives the int32 sums.
+template <int TYPE, int NT, int Q8O>
+__device__ inline void unit_to_slots(const uint8_t* __restrict__ wrow, int row_lds, int u,
+                                     const UnitSrc& S, int tok0, float* dst, size_t tstep, int ts,
+                                     int32_t* isum_out) {
+  if constexpr (q8_slots(TYPE, Q8O) == 9) {
+    q8_unit_lanes<NT>(row_lds, u, S, tok0, dst + u, tstep, ts, isum_out);
+  } else {
+    float tv[NT];
+    unit_terms<TYPE, NT>(wrow, row_lds, u, S, tok0, tv, isum_out);
+#pragma unroll
+    for (int t = 0; t < NT; t++) dst[(size_t)t * tstep + u] = tv[t];
+  }
 }
 
 }  // namespace qr

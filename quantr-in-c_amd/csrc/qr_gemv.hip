@@ -34,9 +34,11 @@ struct GemvArgs {
   int32_t* accb;         // optional [nt][units] activation block sums
 };
 
-// LDS layout: act q | act bd | act bs | terms | staged tile.
-__host__ __device__ inline size_t gemv_lds_layout(int type, int d, int nt, int R, size_t* o_bd,
-                                                  size_t* o_bs, size_t* o_terms, size_t* o_tile) {
+// LDS layout: act q | act bd | act bs | terms | staged tile.  Terms are
+// [nt][R][slots][U + 1] floats (slots: q8_slots).
+__host__ __device__ inline size_t gemv_lds_layout(int type, int q8o, int d, int nt, int R,
+                                                  size_t* o_bd, size_t* o_bs, size_t* o_terms,
+                                                  size_t* o_tile) {
   const int nxb = d / 32;
   const int U = qr_units(type, d);
   size_t off = align16((size_t)nt * nxb * 32);
@@ -45,13 +47,13 @@ __host__ __device__ inline size_t gemv_lds_layout(int type, int d, int nt, int R
   *o_bs = off;
   off = align16(off + (size_t)nt * nxb * 4);
   *o_terms = off;
-  off = align16(off + (size_t)nt * R * (U + 1) * 4);
+  off = align16(off + (size_t)nt * R * q8_slots(type, q8o) * (U + 1) * 4);
   *o_tile = off;
   if (type == QR_T_Q8_0 || type == QR_T_Q6_K) off += stage_bytes((size_t)R * qr_wrow_bytes(type, d));
   return off;
 }
 
-template <int TYPE, int NT>
+template <int TYPE, int NT, int Q8O>
 __global__ __launch_bounds__(kWg) void k_gemv(GemvArgs g) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int d = g.d;
@@ -63,7 +65,8 @@ __global__ __launch_bounds__(kWg) void k_gemv(GemvArgs g) {
   if (R <= 0) return;
 
   size_t o_bd, o_bs, o_terms, o_tile;
-  gemv_lds_layout(TYPE, d, NT, g.rows_per_wg, &o_bd, &o_bs, &o_terms, &o_tile);
+  gemv_lds_layout(TYPE, Q8O, d, NT, g.rows_per_wg, &o_bd, &o_bs, &o_terms, &o_tile);
+  constexpr int SL = q8_slots(TYPE, Q8O);
   UnitSrc S;
   S.act.q = reinterpret_cast<int8_t*>(smem);
   S.act.bd = reinterpret_cast<float*>(smem + o_bd);
@@ -89,15 +92,13 @@ __global__ __launch_bounds__(kWg) void k_gemv(GemvArgs g) {
   for (int fu = wave * 64 + lane; fu < total_units; fu += nwaves * 64) {
     const int row = fu / U;
     const int u = fu - row * U;
-    float tv[NT];
     int32_t is[NT];
-    unit_terms<TYPE, NT>(g.W + gstart + (size_t)row * rb, lds_base + row * (int)rb, u, S, 0, tv,
-                         is);
+    unit_to_slots<TYPE, NT, Q8O>(g.W + gstart + (size_t)row * rb, lds_base + row * (int)rb, u, S,
+                                 0, terms + (size_t)row * SL * tstride,
+                                 (size_t)g.rows_per_wg * SL * tstride, tstride, is);
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-      terms[((size_t)t * g.rows_per_wg + row) * tstride + u] = tv[t];
+    for (int t = 0; t < NT; t++)
       if (g.acc) g.acc[((size_t)t * g.n + r0 + row) * U + u] = is[t];
-    }
     if (g.accb && blockIdx.x == 0 && row == 0) {
 #pragma unroll
       for (int t = 0; t < NT; t++) g.accb[(size_t)t * U + u] = S.act.bs[t * nxb + u];
@@ -107,8 +108,8 @@ __global__ __launch_bounds__(kWg) void k_gemv(GemvArgs g) {
 
   for (int i = threadIdx.x; i < R * NT; i += blockDim.x) {
     const int t = i / R, row = i - t * R;
-    g.Y[(size_t)t * g.ystride + r0 + row] =
-        row_sum(terms + ((size_t)t * g.rows_per_wg + row) * tstride, U);
+    g.Y[(size_t)t * g.ystride + r0 + row] = row_value<TYPE, Q8O>(
+        terms + ((size_t)t * g.rows_per_wg + row) * SL * tstride, tstride, U);
   }
 }
 
@@ -118,10 +119,10 @@ __global__ __launch_bounds__(kWg) void k_gemv(GemvArgs g) {
 // activation blocks in registers and the next tile's loads in flight while it
 // sums.  NS = 1 when every slot of a lane has the same unit (U divides 64).
 // ---------------------------------------------------------------------------
-template <int TYPE, int NT, int NS>
+template <int TYPE, int NT, int NS, int Q8O>
 __global__ __launch_bounds__(64 * kStreamWaves) void k_gemv_stream(GemvArgs g) {
   extern __shared__ __align__(16) uint8_t smem[];
-  const TileShape sh = tile_shape(TYPE, g.d);
+  const TileShape sh = tile_shape(TYPE, g.d, Q8O);
   const StreamLds L = stream_lds(TYPE, NT, sh);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   uint8_t* slice = smem + (size_t)wave * L.slice;
@@ -153,14 +154,36 @@ __global__ __launch_bounds__(64 * kStreamWaves) void k_gemv_stream(GemvArgs g) {
       stage_regs<TYPE>(R, stage, lane);
       wave_lds_sync();
     }
-    tile_terms<TYPE, NT, NS>(R, sl, RWt, r0, sh, A, stage, terms, g.acc, g.n);
+    tile_terms<TYPE, NT, NS, Q8O>(R, sl, RWt, r0, sh, A, stage, terms, g.acc, g.n);
     wave_lds_sync();
     const int next = tile + tstep;
     if (next < ntiles)
       load_tile<TYPE>(g.W, total, next * sh.RW, min(sh.RW, g.n - next * sh.RW), sh, sl, lane, R);
-    for (int i = lane; i < RWt * NT; i += 64) {
-      const int t = i / RWt, row = i - t * RWt;
-      g.Y[(size_t)t * g.ystride + r0 + row] = row_sum_seq(terms + (t * sh.RW + row) * sh.TS, sh.U);
+    if constexpr (q8_slots(TYPE, Q8O) == 9) {
+      // eight lanes per (token, row): lane k runs accumulator k, then the
+      // row's first lane adds the eight into 0.0f in lane order (groups of
+      // eight lanes stay whole: RWt * NT * 8 and 64 are multiples of 8)
+      for (int i = lane; i < RWt * NT * 8; i += 64) {
+        const int rt = i >> 3, k = i & 7;
+        const int t = rt / RWt, row = rt - t * RWt;
+        const float acc = q8_chain<Q8O>(terms + (t * sh.RW + row) * 9 * sh.TS, sh.TS, sh.U, k);
+        const int base = lane & ~7;
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = __shfl(acc, base + j);
+        if (k == 0) {
+          float sum = 0.0f;
+#pragma unroll
+          for (int j = 0; j < 8; j++) sum += v[j];
+          g.Y[(size_t)t * g.ystride + r0 + row] = sum;
+        }
+      }
+    } else {
+      for (int i = lane; i < RWt * NT; i += 64) {
+        const int t = i / RWt, row = i - t * RWt;
+        g.Y[(size_t)t * g.ystride + r0 + row] =
+            row_sum_seq(terms + (t * sh.RW + row) * sh.TS, sh.U);
+      }
     }
     if (next >= ntiles) break;
     wave_lds_sync();
@@ -293,9 +316,9 @@ __global__ __launch_bounds__(64 * kBlkWaves) void k_gemv_blk(GemvArgs g) {
 // ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
-size_t gemv_lds_bytes(int type, int d, int nt, int R) {
+size_t gemv_lds_bytes(int type, int q8o, int d, int nt, int R) {
   size_t a, b, c, e;
-  return gemv_lds_layout(type, d, nt, R, &a, &b, &c, &e);
+  return gemv_lds_layout(type, q8o, d, nt, R, &a, &b, &c, &e);
 }
 
 // Compute units of the current device (cached per device).
@@ -313,24 +336,9 @@ int device_cus() {
   return cached[dev];
 }
 
-// Workgroups per CU of the streaming kernels (QR_STREAM_WG_PER_CU overrides,
-// 1..16, for tuning sweeps; 0: the default).  Default 3 for one or two
-// tokens, 2 for more, or as many as fit in LDS: measured on 32000 x 2048 Q6_K
-// / Q8_0 and the 151936 x 2048 Q6_K lm_head, 3 per CU streams 4.3 TB/s for
-// one token where 2 and 4 give 3.6-4.0 and 1 gives 2.6; with 4 tokens 2 per
-// CU takes 28.9 us where 3 takes 33.8 (Q6_K) and 40.8 (Q8_0).
-static int stream_wg_per_cu() {
-  static const int v = [] {  // read once; thread-safe initialisation
-    const char* e = getenv("QR_STREAM_WG_PER_CU");
-    const int x = e ? atoi(e) : 0;
-    return (x >= 1 && x <= 16) ? x : 0;
-  }();
-  return v;
-}
-
-bool gemv_stream_ok(int type, int d, int nt) {
+bool gemv_stream_ok(int type, int q8o, int d, int nt) {
   if (type == QR_T_F32) return false;
-  const TileShape sh = tile_shape(type, d);
+  const TileShape sh = tile_shape(type, d, q8o);
   if (sh.RW < 1 || (d & 3)) return false;
   // activation registers: nt blocks per distinct slot unit (1 when U divides
   // 64, else kUPL); more than 4 blocks per lane spill
@@ -339,27 +347,30 @@ bool gemv_stream_ok(int type, int d, int nt) {
   return stream_lds(type, nt, sh).total <= 64 * 1024;
 }
 
-template <int TYPE, int NT>
+// Workgroups per CU of the streaming kernel: 3 for one or two tokens, 2 for
+// more, fewer where LDS does not hold that many.  Measured on 32000 x 2048
+// Q6_K / Q8_0 and the 151936 x 2048 Q6_K lm_head: 3 per CU streams 4.3 TB/s
+// for one token where 2 and 4 give 3.6-4.0 and 1 gives 2.6; with 4 tokens 2
+// per CU takes 28.9 us where 3 takes 33.8 (Q6_K) and 40.8 (Q8_0).
+template <int TYPE, int NT, int Q8O>
 static hipError_t launch_stream_t(const GemvArgs& a, hipStream_t st) {
-  const TileShape sh = tile_shape(TYPE, a.d);
+  const TileShape sh = tile_shape(TYPE, a.d, Q8O);
   const size_t lds = stream_lds(TYPE, NT, sh).total;
   const int ntiles = (a.n + sh.RW - 1) / sh.RW;
   const int want = (ntiles + kStreamWaves - 1) / kStreamWaves;
-  int per_cu = stream_wg_per_cu();
-  if (per_cu == 0) {
-    constexpr int kDefault = NT > 2 ? 2 : 3;  // measured: 4 tokens run best at 2 per CU
-    per_cu = lds > 0 ? (int)((160 * 1024) / lds) : kDefault;
-    per_cu = per_cu < 1 ? 1 : (per_cu > kDefault ? kDefault : per_cu);
-  }
+  constexpr int kDefault = NT > 2 ? 2 : 3;
+  int per_cu = lds > 0 ? (int)((160 * 1024) / lds) : kDefault;
+  per_cu = per_cu < 1 ? 1 : (per_cu > kDefault ? kDefault : per_cu);
   const int cap = device_cus() * per_cu;
   const int grid = want < cap ? want : cap;
   if (grid <= 0) return hipSuccess;
   if (64 % sh.U == 0) {
-    hipLaunchKernelGGL((k_gemv_stream<TYPE, NT, 1>), dim3(grid), dim3(64 * kStreamWaves), lds, st, a);
+    hipLaunchKernelGGL((k_gemv_stream<TYPE, NT, 1, Q8O>), dim3(grid), dim3(64 * kStreamWaves), lds,
+                       st, a);
   } else {
     if constexpr (NT == 1)
-      hipLaunchKernelGGL((k_gemv_stream<TYPE, 1, kUPL>), dim3(grid), dim3(64 * kStreamWaves), lds,
-                         st, a);
+      hipLaunchKernelGGL((k_gemv_stream<TYPE, 1, kUPL, Q8O>), dim3(grid), dim3(64 * kStreamWaves),
+                         lds, st, a);
     else
       return hipErrorInvalidValue;  // excluded by gemv_stream_ok
   }
@@ -369,23 +380,23 @@ static hipError_t launch_stream_t(const GemvArgs& a, hipStream_t st) {
 // Rows per workgroup: enough workgroups to cover the 256 CUs several times,
 // at most 16 units per thread, and an LDS footprint that leaves room for
 // several workgroups per CU.
-int gemv_rows_per_wg(int type, int n, int d, int nt) {
+int gemv_rows_per_wg(int type, int q8o, int n, int d, int nt) {
   const int U = qr_units(type, d);
   int R = 64;
   while (R > 1 && ((n + R - 1) / R < 1024 || (size_t)R * U > 16 * kWg)) R >>= 1;
-  while (R > 1 && gemv_lds_bytes(type, d, nt, R) > 48 * 1024) R >>= 1;
+  while (R > 1 && gemv_lds_bytes(type, q8o, d, nt, R) > 48 * 1024) R >>= 1;
   return R;
 }
 
-template <int TYPE, int NT>
+template <int TYPE, int NT, int Q8O>
 static hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
-  const size_t lds = gemv_lds_bytes(TYPE, a.d, NT, a.rows_per_wg);
+  const size_t lds = gemv_lds_bytes(TYPE, Q8O, a.d, NT, a.rows_per_wg);
   const int U = qr_units(TYPE, a.d);
   int threads = ((a.rows_per_wg * U + 63) / 64) * 64;
   threads = threads < 64 ? 64 : (threads > kWg ? kWg : threads);
   const int grid = (a.n + a.rows_per_wg - 1) / a.rows_per_wg;
   if (lds > 64 * 1024) return hipErrorInvalidValue;  // dynamic LDS without an opt-in
-  hipLaunchKernelGGL((k_gemv<TYPE, NT>), dim3(grid), dim3(threads), lds, st, a);
+  hipLaunchKernelGGL((k_gemv<TYPE, NT, Q8O>), dim3(grid), dim3(threads), lds, st, a);
   return hipGetLastError();
 }
 
@@ -405,34 +416,6 @@ bool gemv_blk_ok(int type, int d, int nt) {
   const int nb = d >> 8;
   if (nb < 1 || nb > 64 || (d & 3) || nt > 4) return false;
   return blk_lds_bytes_t(type, d, nt, 1, false) <= kLdsMax;
-}
-
-// Tuning knobs of the block-per-lane kernel for sweeps: QR_BLK_DEPTH (1 or 2
-// tiles in flight per wave) and QR_BLK_WG_PER_CU (1..16 workgroups per CU;
-// default: 2, or 1 where two do not fit in LDS).  Two per CU give the 32000 x
-// 2048 Q4_K GEMV 2048 waves for 4000 tiles, two tiles each with the second
-// streaming while the first is reduced: 9.33 us per launch against 9.75 us
-// with three per CU (a third of the waves with a second tile, the rest
-// contending) and 10.96 us with one.
-static int env_knob(const char* name, int lo, int hi, int dflt) {
-  const char* e = getenv(name);
-  const int x = e ? atoi(e) : 0;
-  return (x >= lo && x <= hi) ? x : dflt;
-}
-// each knob is read once, with thread-safe initialisation
-static int blk_depth() {
-  static const int v = env_knob("QR_BLK_DEPTH", 1, 2, 1);
-  return v;
-}
-static int blk_wg_per_cu() {
-  static const int v = env_knob("QR_BLK_WG_PER_CU", 1, 16, 0);
-  return v;
-}
-// QR_BLK_XS: 1 stages the activation through LDS by DMA, 2 loads it into
-// registers (less LDS per workgroup); default 1.
-static int blk_xs_mode() {
-  static const int v = env_knob("QR_BLK_XS", 1, 2, 1);
-  return v;
 }
 
 // Opt a kernel into LDS beyond 64 KiB, once per device.
@@ -468,58 +451,58 @@ static hipError_t launch_blk_d(const GemvArgs& a, int grid, size_t lds, hipStrea
   return hipGetLastError();
 }
 
+// One tile in flight per wave (D = 1) and two workgroups per CU (one where two
+// do not fit in LDS).  Two per CU give the 32000 x 2048 Q4_K GEMV 2048 waves
+// for 4000 tiles, two tiles each with the second streaming while the first is
+// reduced: 9.33 us per launch against 9.75 us with three per CU (a third of
+// the waves with a second tile, the rest contending) and 10.96 us with one.
+// Two tiles in flight per wave measured slower (9.8 against 8.74 us).  The
+// activation is staged through LDS by DMA when it fits kXsMax, else loaded
+// into registers (d = 5632 at 3 or 4 tokens).
 template <int TYPE, int NT>
 static hipError_t launch_blk_t(const GemvArgs& a, hipStream_t st) {
   const int nb = a.d >> 8;
   const int RB = 64 / nb;
-  int D = blk_depth();
-  const bool xs = blk_xs_mode() == 1 && blk_xs_bytes(a.d, NT) <= kXsMax;
-  if (blk_lds_bytes<TYPE>(a.d, NT, D, xs) > kLdsMax) D = 1;
-  const size_t lds = blk_lds_bytes<TYPE>(a.d, NT, D, xs);
+  const bool xs = blk_xs_bytes(a.d, NT) <= kXsMax;
+  const size_t lds = blk_lds_bytes<TYPE>(a.d, NT, 1, xs);
   if (lds > kLdsMax) return hipErrorInvalidValue;  // excluded by gemv_blk_ok
   const int ntiles = (a.n + RB - 1) / RB;
   const int want = (ntiles + kBlkWaves - 1) / kBlkWaves;
-  int per_cu = blk_wg_per_cu();
-  if (per_cu == 0) {
-    per_cu = (int)(kLdsMax / lds);
-    per_cu = per_cu < 1 ? 1 : (per_cu > 2 ? 2 : per_cu);
-  }
+  int per_cu = (int)(kLdsMax / lds);
+  per_cu = per_cu < 1 ? 1 : (per_cu > 2 ? 2 : per_cu);
   const int cap = device_cus() * per_cu;
   const int grid = want < cap ? want : cap;
   if (grid <= 0) return hipSuccess;
-  if (xs) {
-    if (D == 2) return launch_blk_d<TYPE, NT, 2, true>(a, grid, lds, st);
-    return launch_blk_d<TYPE, NT, 1, true>(a, grid, lds, st);
-  }
-  if (D == 2) return launch_blk_d<TYPE, NT, 2, false>(a, grid, lds, st);
+  if (xs) return launch_blk_d<TYPE, NT, 1, true>(a, grid, lds, st);
   return launch_blk_d<TYPE, NT, 1, false>(a, grid, lds, st);
 }
 
-template <int TYPE, int NT>
+template <int TYPE, int NT, int Q8O>
 static hipError_t launch_any_t(const GemvArgs& a, hipStream_t st) {
   if constexpr ((TYPE == QR_T_Q4_K || TYPE == QR_T_Q5_K) && NT <= 4) {
     if (gemv_blk_ok(TYPE, a.d, NT)) return launch_blk_t<TYPE, NT>(a, st);
   }
   if constexpr (NT <= 4) {
-    if (gemv_stream_ok(TYPE, a.d, NT)) return launch_stream_t<TYPE, NT>(a, st);
+    if (gemv_stream_ok(TYPE, Q8O, a.d, NT)) return launch_stream_t<TYPE, NT, Q8O>(a, st);
   }
-  return launch_t<TYPE, NT>(a, st);
+  return launch_t<TYPE, NT, Q8O>(a, st);
 }
 
-template <int TYPE>
+template <int TYPE, int Q8O>
 static hipError_t launch_nt(const GemvArgs& a, int nt, hipStream_t st) {
   switch (nt) {
-    case 1: return launch_any_t<TYPE, 1>(a, st);
-    case 2: return launch_any_t<TYPE, 2>(a, st);
-    case 3: return launch_any_t<TYPE, 3>(a, st);
-    case 4: return launch_any_t<TYPE, 4>(a, st);
-    case 8: return launch_any_t<TYPE, 8>(a, st);
+    case 1: return launch_any_t<TYPE, 1, Q8O>(a, st);
+    case 2: return launch_any_t<TYPE, 2, Q8O>(a, st);
+    case 3: return launch_any_t<TYPE, 3, Q8O>(a, st);
+    case 4: return launch_any_t<TYPE, 4, Q8O>(a, st);
+    case 8: return launch_any_t<TYPE, 8, Q8O>(a, st);
     default: return hipErrorInvalidValue;
   }
 }
 
-hipError_t gemv_launch(int type, const void* W, const float* X, float* Y, int n, int d, int nt,
-                       int xstride, int ystride, int32_t* acc, int32_t* accb, hipStream_t st) {
+hipError_t gemv_launch(int type, int q8o, const void* W, const float* X, float* Y, int n, int d,
+                       int nt, int xstride, int ystride, int32_t* acc, int32_t* accb,
+                       hipStream_t st) {
   GemvArgs a;
   a.W = static_cast<const uint8_t*>(W);
   a.X = X;
@@ -528,14 +511,20 @@ hipError_t gemv_launch(int type, const void* W, const float* X, float* Y, int n,
   a.d = d;
   a.xstride = xstride;
   a.ystride = ystride;
-  a.rows_per_wg = gemv_rows_per_wg(type, n, d, nt);
+  a.rows_per_wg = gemv_rows_per_wg(type, q8o, n, d, nt);
   a.acc = acc;
   a.accb = accb;
   switch (type) {
-    case QR_T_Q4_K: return launch_nt<QR_T_Q4_K>(a, nt, st);
-    case QR_T_Q5_K: return launch_nt<QR_T_Q5_K>(a, nt, st);
-    case QR_T_Q6_K: return launch_nt<QR_T_Q6_K>(a, nt, st);
-    case QR_T_Q8_0: return launch_nt<QR_T_Q8_0>(a, nt, st);
+    case QR_T_Q4_K: return launch_nt<QR_T_Q4_K, kQ8Seq>(a, nt, st);
+    case QR_T_Q5_K: return launch_nt<QR_T_Q5_K, kQ8Seq>(a, nt, st);
+    case QR_T_Q6_K: return launch_nt<QR_T_Q6_K, kQ8Seq>(a, nt, st);
+    case QR_T_Q8_0:
+      switch (q8o) {
+        case kQ8Seq: return launch_nt<QR_T_Q8_0, kQ8Seq>(a, nt, st);
+        case kQ8Avx2: return launch_nt<QR_T_Q8_0, kQ8Avx2>(a, nt, st);
+        case kQ8Avx512: return launch_nt<QR_T_Q8_0, kQ8Avx512>(a, nt, st);
+        default: return hipErrorInvalidValue;
+      }
     default: return hipErrorInvalidValue;
   }
 }

@@ -13,16 +13,19 @@
 namespace qr {
 
 // qr_gemv.hip
-size_t gemv_lds_bytes(int type, int d, int nt, int R);
-bool gemv_stream_ok(int type, int d, int nt);
+// q8o: the Q8_0 dot order (kQ8Seq / kQ8Avx2 / kQ8Avx512 of qr_gemv.h, equal to
+// QR_ORDER_*); it only changes Q8_0 weights.
+size_t gemv_lds_bytes(int type, int q8o, int d, int nt, int R);
+bool gemv_stream_ok(int type, int q8o, int d, int nt);
 bool gemv_blk_ok(int type, int d, int nt);
 int device_cus();
 // Let kernel fn use up to 160 KiB of dynamic LDS on the current device (once
 // per device; done[] is the caller's per-device flag array of 64 entries).
 hipError_t lds_opt_in(const void* fn, std::atomic<bool>* done);
-int gemv_rows_per_wg(int type, int n, int d, int nt);
-hipError_t gemv_launch(int type, const void* W, const float* X, float* Y, int n, int d, int nt,
-                       int xstride, int ystride, int32_t* acc, int32_t* accb, hipStream_t st);
+int gemv_rows_per_wg(int type, int q8o, int n, int d, int nt);
+hipError_t gemv_launch(int type, int q8o, const void* W, const float* X, float* Y, int n, int d,
+                       int nt, int xstride, int ystride, int32_t* acc, int32_t* accb,
+                       hipStream_t st);
 hipError_t gemv_f32_launch(int order, const float* W, const float* X, float* Y, int n, int d,
                            int nt, int xstride, int ystride, hipStream_t st);
 hipError_t quantize_q8_0_launch(const float* x, void* y, long nblocks, hipStream_t st);

@@ -203,10 +203,10 @@ struct ExpertArgs {
   int E, K, P;
 };
 
-__host__ __device__ inline size_t expert_lds_layout(int type, int cols, int nt, int R, int nmat,
-                                                    size_t* o_bd, size_t* o_bs, size_t* o_terms,
-                                                    size_t* o_tile, size_t* o_rows,
-                                                    size_t* tile_stride) {
+__host__ __device__ inline size_t expert_lds_layout(int type, int q8o, int cols, int nt, int R,
+                                                    int nmat, size_t* o_bd, size_t* o_bs,
+                                                    size_t* o_terms, size_t* o_tile,
+                                                    size_t* o_rows, size_t* tile_stride) {
   const int nxb = cols / 32;
   const int U = qr_units(type, cols);
   size_t off = align16((size_t)nt * nxb * 32);
@@ -217,7 +217,7 @@ __host__ __device__ inline size_t expert_lds_layout(int type, int cols, int nt, 
   *o_rows = off;
   off = align16(off + (size_t)nt * 4);
   *o_terms = off;
-  off = align16(off + (size_t)nmat * nt * R * (U + 1) * 4);
+  off = align16(off + (size_t)nmat * nt * R * q8_slots(type, q8o) * (U + 1) * 4);
   *o_tile = off;
   *tile_stride = 0;
   if (type == QR_T_Q8_0 || type == QR_T_Q6_K) {
@@ -257,7 +257,7 @@ __device__ inline bool expert_item(const ExpertArgs& a, int item, int NT, int* e
   return *e >= 0 && *e < a.E && *np > 0;
 }
 
-template <int TYPE, int NT, bool GATEUP>
+template <int TYPE, int NT, bool GATEUP, int Q8O>
 __global__ __launch_bounds__(256) void k_expert(ExpertArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   int e, p0, np;
@@ -271,7 +271,9 @@ __global__ __launch_bounds__(256) void k_expert(ExpertArgs a) {
   const int U = qr_units(TYPE, cols);
   const size_t rb = qr_wrow_bytes(TYPE, cols);
   size_t o_bd, o_bs, o_terms, o_tile, o_rows, tstr;
-  expert_lds_layout(TYPE, cols, NT, R0, NMAT, &o_bd, &o_bs, &o_terms, &o_tile, &o_rows, &tstr);
+  expert_lds_layout(TYPE, Q8O, cols, NT, R0, NMAT, &o_bd, &o_bs, &o_terms, &o_tile, &o_rows,
+                    &tstr);
+  constexpr int SL = q8_slots(TYPE, Q8O);
   UnitSrc S;
   S.act.q = reinterpret_cast<int8_t*>(smem);
   S.act.bd = reinterpret_cast<float*>(smem + o_bd);
@@ -314,81 +316,87 @@ __global__ __launch_bounds__(256) void k_expert(ExpertArgs a) {
     const int u = rem - row * U;
     UnitSrc Sm = S;
     Sm.tile = reinterpret_cast<const uint32_t*>(smem + o_tile + m * tstr);
-    float tv[NT];
     int32_t is[NT];
-    unit_terms<TYPE, NT>(Wm[m] + gstart + (size_t)row * rb, lds_base + row * (int)rb, u, Sm, 0,
-                         tv, is);
-#pragma unroll
-    for (int t = 0; t < NT; t++) terms[(((size_t)m * NT + t) * R0 + row) * tstride + u] = tv[t];
+    unit_to_slots<TYPE, NT, Q8O>(Wm[m] + gstart + (size_t)row * rb, lds_base + row * (int)rb, u,
+                                 Sm, 0, terms + (((size_t)m * NT) * R0 + row) * SL * tstride,
+                                 (size_t)R0 * SL * tstride, tstride, is);
   }
   __syncthreads();
 
   for (int i = threadIdx.x; i < np * R; i += blockDim.x) {
     const int t = i / R, row = i - t * R;
-    const float v1 = row_sum(terms + ((size_t)t * R0 + row) * tstride, U);
+    const float v1 = row_value<TYPE, Q8O>(terms + ((size_t)t * R0 + row) * SL * tstride, tstride, U);
     float out = v1;
     if constexpr (GATEUP) {
-      const float v2 = row_sum(terms + (((size_t)NT + t) * R0 + row) * tstride, U);
+      const float v2 = row_value<TYPE, Q8O>(
+          terms + (((size_t)NT + t) * R0 + row) * SL * tstride, tstride, U);
       out = qr_silu(v1) * v2;
     }
     a.Y[(size_t)(p0 + t) * a.ystride + r0 + row] = out;
   }
 }
 
-static int expert_rows_per_wg(int type, int rows, int cols, int nt, int nmat) {
+static int expert_rows_per_wg(int type, int q8o, int rows, int cols, int nt, int nmat) {
   const int U = qr_units(type, cols);
   int R = 64;
   size_t a, b, c, d, e, f;
   while (R > 1 && ((size_t)nmat * R * U > 16 * 256 ||
-                   expert_lds_layout(type, cols, nt, R, nmat, &a, &b, &c, &d, &e, &f) > 48 * 1024 ||
+                   expert_lds_layout(type, q8o, cols, nt, R, nmat, &a, &b, &c, &d, &e, &f) >
+                       48 * 1024 ||
                    (rows + R - 1) / R < 64))
     R >>= 1;
   return R;
 }
 
-template <int TYPE, int NT, bool GATEUP>
+template <int TYPE, int NT, bool GATEUP, int Q8O>
 static hipError_t expert_launch_t(ExpertArgs a, int items, hipStream_t st) {
   constexpr int NMAT = GATEUP ? 2 : 1;
-  a.rows_per_wg = expert_rows_per_wg(TYPE, a.rows, a.cols, NT, NMAT);
+  a.rows_per_wg = expert_rows_per_wg(TYPE, Q8O, a.rows, a.cols, NT, NMAT);
   size_t o1, o2, o3, o4, o5, o6;
-  const size_t lds =
-      expert_lds_layout(TYPE, a.cols, NT, a.rows_per_wg, NMAT, &o1, &o2, &o3, &o4, &o5, &o6);
+  const size_t lds = expert_lds_layout(TYPE, Q8O, a.cols, NT, a.rows_per_wg, NMAT, &o1, &o2, &o3,
+                                       &o4, &o5, &o6);
   const int U = qr_units(TYPE, a.cols);
   int threads = ((NMAT * a.rows_per_wg * U + 63) / 64) * 64;
   threads = threads < 64 ? 64 : (threads > 256 ? 256 : threads);
   dim3 grid((a.rows + a.rows_per_wg - 1) / a.rows_per_wg, items);
   if (grid.x == 0 || grid.y == 0) return hipSuccess;
   if (lds > 64 * 1024) return hipErrorInvalidValue;  // dynamic LDS without an opt-in
-  hipLaunchKernelGGL((k_expert<TYPE, NT, GATEUP>), grid, dim3(threads), lds, st, a);
+  hipLaunchKernelGGL((k_expert<TYPE, NT, GATEUP, Q8O>), grid, dim3(threads), lds, st, a);
   return hipGetLastError();
 }
 
-template <int TYPE, bool GATEUP>
+template <int TYPE, bool GATEUP, int Q8O>
 static hipError_t expert_launch_nt(const ExpertArgs& a, int nt, int items, hipStream_t st) {
   switch (nt) {
-    case 1: return expert_launch_t<TYPE, 1, GATEUP>(a, items, st);
-    case 2: return expert_launch_t<TYPE, 2, GATEUP>(a, items, st);
-    case 4: return expert_launch_t<TYPE, 4, GATEUP>(a, items, st);
-    case 8: return expert_launch_t<TYPE, 8, GATEUP>(a, items, st);
+    case 1: return expert_launch_t<TYPE, 1, GATEUP, Q8O>(a, items, st);
+    case 2: return expert_launch_t<TYPE, 2, GATEUP, Q8O>(a, items, st);
+    case 4: return expert_launch_t<TYPE, 4, GATEUP, Q8O>(a, items, st);
+    case 8: return expert_launch_t<TYPE, 8, GATEUP, Q8O>(a, items, st);
     default: return hipErrorInvalidValue;
   }
 }
 
-static hipError_t expert_launch(int type, bool gateup, const ExpertArgs& a, int nt, int items,
-                                hipStream_t st) {
+template <int TYPE, int Q8O>
+static hipError_t expert_launch_g(bool gateup, const ExpertArgs& a, int nt, int items,
+                                  hipStream_t st) {
+  return gateup ? expert_launch_nt<TYPE, true, Q8O>(a, nt, items, st)
+                : expert_launch_nt<TYPE, false, Q8O>(a, nt, items, st);
+}
+
+// q8o: the Q8_0 dot order (kQ8Seq / kQ8Avx2 / kQ8Avx512); other types ignore it.
+static hipError_t expert_launch(int type, int q8o, bool gateup, const ExpertArgs& a, int nt,
+                                int items, hipStream_t st) {
   switch (type) {
-    case QR_T_Q4_K:
-      return gateup ? expert_launch_nt<QR_T_Q4_K, true>(a, nt, items, st)
-                    : expert_launch_nt<QR_T_Q4_K, false>(a, nt, items, st);
-    case QR_T_Q5_K:
-      return gateup ? expert_launch_nt<QR_T_Q5_K, true>(a, nt, items, st)
-                    : expert_launch_nt<QR_T_Q5_K, false>(a, nt, items, st);
-    case QR_T_Q6_K:
-      return gateup ? expert_launch_nt<QR_T_Q6_K, true>(a, nt, items, st)
-                    : expert_launch_nt<QR_T_Q6_K, false>(a, nt, items, st);
+    case QR_T_Q4_K: return expert_launch_g<QR_T_Q4_K, kQ8Seq>(gateup, a, nt, items, st);
+    case QR_T_Q5_K: return expert_launch_g<QR_T_Q5_K, kQ8Seq>(gateup, a, nt, items, st);
+    case QR_T_Q6_K: return expert_launch_g<QR_T_Q6_K, kQ8Seq>(gateup, a, nt, items, st);
     case QR_T_Q8_0:
-      return gateup ? expert_launch_nt<QR_T_Q8_0, true>(a, nt, items, st)
-                    : expert_launch_nt<QR_T_Q8_0, false>(a, nt, items, st);
+      switch (q8o) {
+        case kQ8Seq: return expert_launch_g<QR_T_Q8_0, kQ8Seq>(gateup, a, nt, items, st);
+        case kQ8Avx2: return expert_launch_g<QR_T_Q8_0, kQ8Avx2>(gateup, a, nt, items, st);
+        case kQ8Avx512: return expert_launch_g<QR_T_Q8_0, kQ8Avx512>(gateup, a, nt, items, st);
+        default: return hipErrorInvalidValue;
+      }
     default: return hipErrorInvalidValue;
   }
 }
@@ -409,9 +417,9 @@ struct DownArgs {
   const float* sgl;    // its gate logit (scalar)
 };
 
-__host__ __device__ inline size_t down1_lds_layout(int type, int hidden, int K, int R, size_t* o_bd,
-                                                   size_t* o_bs, size_t* o_terms, size_t* o_tile,
-                                                   size_t* tile_stride) {
+__host__ __device__ inline size_t down1_lds_layout(int type, int q8o, int hidden, int K, int R,
+                                                   size_t* o_bd, size_t* o_bs, size_t* o_terms,
+                                                   size_t* o_tile, size_t* tile_stride) {
   const int nxb = hidden / 32;
   const int U = qr_units(type, hidden);
   size_t off = align16((size_t)K * nxb * 32);
@@ -420,7 +428,7 @@ __host__ __device__ inline size_t down1_lds_layout(int type, int hidden, int K, 
   *o_bs = off;
   off = align16(off + (size_t)K * nxb * 4);
   *o_terms = off;
-  off = align16(off + (size_t)K * R * (U + 1) * 4);
+  off = align16(off + (size_t)K * R * q8_slots(type, q8o) * (U + 1) * 4);
   *o_tile = off;
   *tile_stride = 0;
   if (type == QR_T_Q8_0 || type == QR_T_Q6_K) {
@@ -430,7 +438,7 @@ __host__ __device__ inline size_t down1_lds_layout(int type, int hidden, int K, 
   return off;
 }
 
-template <int TYPE>
+template <int TYPE, int Q8O>
 __global__ __launch_bounds__(256) void k_down_combine1(DownArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int R0 = a.rows_per_wg;
@@ -441,7 +449,8 @@ __global__ __launch_bounds__(256) void k_down_combine1(DownArgs a) {
   const int U = qr_units(TYPE, a.hidden);
   const size_t rb = qr_wrow_bytes(TYPE, a.hidden);
   size_t o_bd, o_bs, o_terms, o_tile, tstr;
-  down1_lds_layout(TYPE, a.hidden, K, R0, &o_bd, &o_bs, &o_terms, &o_tile, &tstr);
+  down1_lds_layout(TYPE, Q8O, a.hidden, K, R0, &o_bd, &o_bs, &o_terms, &o_tile, &tstr);
+  constexpr int SL = q8_slots(TYPE, Q8O);
   UnitSrc S;
   S.act.q = reinterpret_cast<int8_t*>(smem);
   S.act.bd = reinterpret_cast<float*>(smem + o_bd);
@@ -474,16 +483,15 @@ __global__ __launch_bounds__(256) void k_down_combine1(DownArgs a) {
     const int rem = fu - k * per_k;
     const int row = rem / U;
     const int u = rem - row * U;
-    float tv[1] = {0.0f};
     int32_t is[1];
-    if (valid(k)) {
+    if (valid(k)) {  // an invalid slot's terms are never read
       UnitSrc Sk = S;
       Sk.tile = reinterpret_cast<const uint32_t*>(smem + o_tile + k * tstr);
       const uint8_t* Wk = a.W + (size_t)a.idx[k] * a.slice;
-      unit_terms<TYPE, 1>(Wk + gstart + (size_t)row * rb, lds_base + row * (int)rb, u, Sk, k, tv,
-                          is);
+      unit_to_slots<TYPE, 1, Q8O>(Wk + gstart + (size_t)row * rb, lds_base + row * (int)rb, u, Sk,
+                                  k, terms + ((size_t)k * R0 + row) * SL * tstride, 0, tstride,
+                                  is);
     }
-    terms[((size_t)k * R0 + row) * tstride + u] = tv[0];
   }
   __syncthreads();
 
@@ -491,7 +499,8 @@ __global__ __launch_bounds__(256) void k_down_combine1(DownArgs a) {
     float acc = 0.0f;  // xb2 = 0 (src/runtime.c:242)
     for (int k = 0; k < K; k++) {
       if (!valid(k)) continue;
-      const float y = row_sum(terms + ((size_t)k * R0 + row) * tstride, U);
+      const float y =
+          row_value<TYPE, Q8O>(terms + ((size_t)k * R0 + row) * SL * tstride, tstride, U);
       acc += y * a.wts[k];
     }
     if (a.ysh) {
@@ -502,37 +511,44 @@ __global__ __launch_bounds__(256) void k_down_combine1(DownArgs a) {
   }
 }
 
-static int down1_rows_per_wg(int type, int dim, int hidden, int K) {
+static int down1_rows_per_wg(int type, int q8o, int dim, int hidden, int K) {
   const int U = qr_units(type, hidden);
   int R = 64;
   size_t a, b, c, d, e;
   while (R > 1 && ((size_t)K * R * U > 16 * 256 ||
-                   down1_lds_layout(type, hidden, K, R, &a, &b, &c, &d, &e) > 48 * 1024 ||
+                   down1_lds_layout(type, q8o, hidden, K, R, &a, &b, &c, &d, &e) > 48 * 1024 ||
                    (dim + R - 1) / R < 256))
     R >>= 1;
   return R;
 }
 
-template <int TYPE>
+template <int TYPE, int Q8O>
 static hipError_t down1_launch_t(DownArgs a, hipStream_t st) {
-  a.rows_per_wg = down1_rows_per_wg(TYPE, a.dim, a.hidden, a.K);
+  a.rows_per_wg = down1_rows_per_wg(TYPE, Q8O, a.dim, a.hidden, a.K);
   size_t o1, o2, o3, o4, o5;
-  const size_t lds = down1_lds_layout(TYPE, a.hidden, a.K, a.rows_per_wg, &o1, &o2, &o3, &o4, &o5);
+  const size_t lds =
+      down1_lds_layout(TYPE, Q8O, a.hidden, a.K, a.rows_per_wg, &o1, &o2, &o3, &o4, &o5);
   const int U = qr_units(TYPE, a.hidden);
   int threads = ((a.K * a.rows_per_wg * U + 63) / 64) * 64;
   threads = threads < 64 ? 64 : (threads > 256 ? 256 : threads);
   const int grid = (a.dim + a.rows_per_wg - 1) / a.rows_per_wg;
   if (lds > 64 * 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_down_combine1<TYPE>, dim3(grid), dim3(threads), lds, st, a);
+  hipLaunchKernelGGL((k_down_combine1<TYPE, Q8O>), dim3(grid), dim3(threads), lds, st, a);
   return hipGetLastError();
 }
 
-static hipError_t down1_launch(int type, const DownArgs& a, hipStream_t st) {
+static hipError_t down1_launch(int type, int q8o, const DownArgs& a, hipStream_t st) {
   switch (type) {
-    case QR_T_Q4_K: return down1_launch_t<QR_T_Q4_K>(a, st);
-    case QR_T_Q5_K: return down1_launch_t<QR_T_Q5_K>(a, st);
-    case QR_T_Q6_K: return down1_launch_t<QR_T_Q6_K>(a, st);
-    case QR_T_Q8_0: return down1_launch_t<QR_T_Q8_0>(a, st);
+    case QR_T_Q4_K: return down1_launch_t<QR_T_Q4_K, kQ8Seq>(a, st);
+    case QR_T_Q5_K: return down1_launch_t<QR_T_Q5_K, kQ8Seq>(a, st);
+    case QR_T_Q6_K: return down1_launch_t<QR_T_Q6_K, kQ8Seq>(a, st);
+    case QR_T_Q8_0:
+      switch (q8o) {
+        case kQ8Seq: return down1_launch_t<QR_T_Q8_0, kQ8Seq>(a, st);
+        case kQ8Avx2: return down1_launch_t<QR_T_Q8_0, kQ8Avx2>(a, st);
+        case kQ8Avx512: return down1_launch_t<QR_T_Q8_0, kQ8Avx512>(a, st);
+        default: return hipErrorInvalidValue;
+      }
     default: return hipErrorInvalidValue;
   }
 }
@@ -605,17 +621,8 @@ static hipError_t combine_launch(float* x, const float* y, const int32_t* inv, c
 // ---------------------------------------------------------------------------
 // The layer.
 // ---------------------------------------------------------------------------
-// Average pairs per expert from which the grouped products use MFMA
-// (QR_MFMA_MIN_PAIRS overrides, for tuning sweeps).
-static int mfma_min_pairs() {
-  static const int v = [] {  // read once; thread-safe initialisation
-    const char* e = getenv("QR_MFMA_MIN_PAIRS");
-    const int x = e ? atoi(e) : 0;
-    return x > 0 ? x : 1;
-  }();
-  return v;
-}
-#define kMfmaPairsPerExpert mfma_min_pairs()
+// Average pairs per expert from which the grouped products use MFMA.
+constexpr int kMfmaPairsPerExpert = 1;
 
 static int pick_tile(int P, int E) {
   const double avg = (double)P / E;
@@ -639,7 +646,7 @@ static hipError_t shared_expert(const qr_moe_layer* L, const float* xb, int T, c
   g.E = 1;
   g.K = 1;
   g.P = T;
-  hipError_t e = expert_launch((int)L->sh_up_type, true, g, nt, (T + nt - 1) / nt, st);
+  hipError_t e = expert_launch((int)L->sh_up_type, kQ8Seq, true, g, nt, (T + nt - 1) / nt, st);
   if (e != hipSuccess) return e;
   ExpertArgs dn = g;
   dn.W1 = static_cast<const uint8_t*>(L->sh_down);
@@ -650,7 +657,7 @@ static hipError_t shared_expert(const qr_moe_layer* L, const float* xb, int T, c
   dn.xstride = L->sh_hidden;
   dn.Y = s.ysh;
   dn.ystride = L->dim;
-  e = expert_launch((int)L->sh_down_type, false, dn, nt, (T + nt - 1) / nt, st);
+  e = expert_launch((int)L->sh_down_type, kQ8Seq, false, dn, nt, (T + nt - 1) / nt, st);
   if (e != hipSuccess) return e;
   // gate logit: sequential dot (one row) for every token
   return gemv_f32_launch(QR_ORDER_SEQ, L->sh_gate_inp, xb, s.sgl, 1, L->dim, T, L->dim, 1, st);
@@ -663,10 +670,17 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
   const size_t su = qr_wrow_bytes((int)L->up_type, L->dim) * (size_t)L->hidden;
   const size_t sd = qr_wrow_bytes((int)L->down_type, L->hidden) * (size_t)L->dim;
   hipError_t e;
+  // `order` names the reference build: the router's accumulation order and
+  // the Q8_0 dot order (kQ8* equal QR_ORDER_*).  Q8_0 experts in a lane order
+  // run on the grouped GEMV kernels below, the only ones that form lane
+  // accumulators.
+  const int q8o = order;
+  const bool q8_lanes = order != QR_ORDER_SEQ &&
+                        (L->up_type == QR_T_Q8_0 || L->down_type == QR_T_Q8_0);
 
   // One token: logits, then gate/up with the routing done in every wave, then
   // down + combine (qr_moe_t1.hip): three launches, no routing kernel.
-  if (T == 1 && router1_ok(L->dim) && gateup1_ok((int)L->up_type, L->dim, E, K) &&
+  if (!q8_lanes && T == 1 && router1_ok(L->dim) && gateup1_ok((int)L->up_type, L->dim, E, K) &&
       L->up_type == L->gate_type && down1v2_ok((int)L->down_type, K, L->dim, L->hidden) &&
       (reinterpret_cast<uintptr_t>(L->router) & 15) == 0 &&
       (reinterpret_cast<uintptr_t>(xb) & 15) == 0) {
@@ -685,7 +699,7 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
 
   // Many tokens on int8 MFMA: tiled logits; routing + xb records; dispatch;
   // gate/up writing hb records; down; combine.
-  if (T > 1 && P >= kMfmaPairsPerExpert * E && mfma_type_ok((int)L->up_type) &&
+  if (!q8_lanes && T > 1 && P >= kMfmaPairsPerExpert * E && mfma_type_ok((int)L->up_type) &&
       mfma_type_ok((int)L->down_type) && rlogits_ok(L->dim) && E <= 256 && K <= 16 &&
       (reinterpret_cast<uintptr_t>(L->router) & 15) == 0) {
     const int kTile = mfma_tile(T, K, E);  // pairs per MFMA work item
@@ -737,7 +751,7 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
 
   if (T == 1) {
     g.mode = kModeSingle;
-    e = expert_launch((int)L->up_type, true, g, 1, K, st);
+    e = expert_launch((int)L->up_type, q8o, true, g, 1, K, st);
     if (e != hipSuccess) return e;
     if (sh) {
       e = shared_expert(L, xb, T, s, st);
@@ -756,11 +770,11 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
     dn.x = x;
     dn.ysh = sh ? s.ysh : nullptr;
     dn.sgl = s.sgl;
-    return down1_launch((int)L->down_type, dn, st);
+    return down1_launch((int)L->down_type, q8o, dn, st);
   }
 
   // Many pairs per expert: grouped products on int8 MFMA (qr_moe_mfma.hip).
-  if (P >= kMfmaPairsPerExpert * E && mfma_type_ok((int)L->up_type) &&
+  if (!q8_lanes && P >= kMfmaPairsPerExpert * E && mfma_type_ok((int)L->up_type) &&
       mfma_type_ok((int)L->down_type)) {
     const int kTile = mfma_tile(T, K, E);  // pairs per MFMA work item
     e = moe_dispatch_launch(s.idx, T, K, E, kTile, s.counts, s.offsets, s.tiles, s.perm, s.inv, st);
@@ -786,7 +800,7 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
   const int items = (P + nt - 1) / nt + E;  // >= sum_e ceil(count_e / nt)
   g.mode = kModeDispatched;
   g.x_by_token = 1;
-  e = expert_launch((int)L->up_type, true, g, nt, items, st);
+  e = expert_launch((int)L->up_type, q8o, true, g, nt, items, st);
   if (e != hipSuccess) return e;
   ExpertArgs dn = g;
   dn.W1 = static_cast<const uint8_t*>(L->down);
@@ -799,7 +813,7 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
   dn.Y = s.y;
   dn.ystride = L->dim;
   dn.x_by_token = 0;
-  e = expert_launch((int)L->down_type, false, dn, nt, items, st);
+  e = expert_launch((int)L->down_type, q8o, false, dn, nt, items, st);
   if (e != hipSuccess) return e;
   }
   if (sh) {

@@ -576,15 +576,7 @@ hipError_t quant_rows_launch(const float* x, int xstride, int nrows, int cols, b
 
 // Pairs per work item: 16 while experts see few pairs each (less padding of
 // the 16-pair MFMA tile), 32 beyond (half the weight re-reads).
-int mfma_tile(int T, int K, int E) {
-  static const int forced = [] {  // read once; thread-safe initialisation
-    const char* s = getenv("QR_MFMA_TILE");
-    const int v = s ? atoi(s) : 0;
-    return (v == 16 || v == 32) ? v : 0;
-  }();
-  if (forced) return forced;
-  return (long)T * K >= 16L * E ? 32 : 16;
-}
+int mfma_tile(int T, int K, int E) { return (long)T * K >= 16L * E ? 32 : 16; }
 
 template <int TYPE, bool GATEUP, int NJ, int D, int NW>
 static hipError_t mfma_launch_t(const MfmaArgs& a, int items, hipStream_t st) {
@@ -605,47 +597,16 @@ static hipError_t mfma_launch_t(const MfmaArgs& a, int items, hipStream_t st) {
   }
 }
 
-// Kernel shape (waves per workgroup NW, each on 16 rows; ring depth D) per
-// product.  Measured on the Qwen3-30B-A3B layer: one slot (the least LDS, the
-// most workgroups per CU) wins where the epilogue's VALU work dominates --
-// both products with 32-pair items, the 24-unit down product always -- and
-// two slots for gate/up with 16-pair items, whose eight stages are latency
-// bound.  QR_MFMA_GU / QR_MFMA_DN ("NW,D") override, for tuning sweeps.
-struct ShapeKnob {
-  int nw = 0, d = 0;  // nw == 0: no override
-};
-static ShapeKnob shape_knob(const char* name) {
-  ShapeKnob k;
-  const char* s = getenv(name);
-  int x = 0, y = 0;
-  if (s && sscanf(s, "%d,%d", &x, &y) == 2 && (x == 4 || x == 8) && (y >= 1 && y <= 3)) {
-    k.nw = x;
-    k.d = y;
-  }
-  return k;
-}
-static void mfma_shape(bool gateup, int tile, int* nw, int* d) {
-  // read once each; thread-safe initialisation
-  static const ShapeKnob gu = shape_knob("QR_MFMA_GU"), dn = shape_knob("QR_MFMA_DN");
-  const ShapeKnob& c = gateup ? gu : dn;
-  if (c.nw > 0) {
-    *nw = c.nw;
-    *d = c.d;
-  } else {
-    *nw = 4;
-    *d = (gateup && tile == 16) ? 2 : 1;
-  }
-}
-
+// Kernel shape per product: 4 waves per workgroup, each on 16 rows, and a
+// ring of D stages.  Measured on the Qwen3-30B-A3B layer: one slot (the least
+// LDS, the most workgroups per CU) wins where the epilogue's VALU work
+// dominates -- both products with 32-pair items, the 24-unit down product
+// always -- and two slots for gate/up with 16-pair items, whose eight stages
+// are latency bound.
 template <int TYPE, bool GATEUP, int NJ>
 static hipError_t mfma_launch_shape(const MfmaArgs& a, int items, hipStream_t st) {
-  int nw, d;
-  mfma_shape(GATEUP, 16 * NJ, &nw, &d);
-  if (nw == 8) return d == 3 ? mfma_launch_t<TYPE, GATEUP, NJ, 3, 8>(a, items, st)
-                             : mfma_launch_t<TYPE, GATEUP, NJ, 2, 8>(a, items, st);
-  if (d == 1) return mfma_launch_t<TYPE, GATEUP, NJ, 1, 4>(a, items, st);
-  return d == 3 ? mfma_launch_t<TYPE, GATEUP, NJ, 3, 4>(a, items, st)
-                : mfma_launch_t<TYPE, GATEUP, NJ, 2, 4>(a, items, st);
+  if (GATEUP && NJ == 1) return mfma_launch_t<TYPE, GATEUP, NJ, 2, 4>(a, items, st);
+  return mfma_launch_t<TYPE, GATEUP, NJ, 1, 4>(a, items, st);
 }
 
 template <int TYPE, bool GATEUP>
@@ -683,14 +644,7 @@ hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const ui
   a.ystride = ystride;
   a.QO = QO;
   a.qperm = qperm ? 1 : 0;
-  {
-    // QR_MFMA_SKINNY=0 turns the skinny form off (tuning sweeps); read once
-    static const int knob = [] {
-      const char* e = getenv("QR_MFMA_SKINNY");
-      return (e && e[0] == '0') ? 0 : 1;
-    }();
-    a.skinny = knob;
-  }
+  a.skinny = 1;
   // items of up to 16 pairs: an expert rarely has more than one, so its rows
   // are read about once and the hint keeps the activation records cached;
   // with 32-pair items hot experts are re-read by several items

@@ -396,15 +396,6 @@ static hipError_t rlogits_launch_t(const float* W, const float* X, int T, int E,
   return hipGetLastError();
 }
 
-// QR_RLOGITS_VEC4=0 selects the one-chain-per-thread kernels (tuning sweeps).
-static bool rlogits_vec4() {
-  static const bool v = [] {  // read once; thread-safe initialisation
-    const char* e = getenv("QR_RLOGITS_VEC4");
-    return !(e && e[0] == '0');
-  }();
-  return v;
-}
-
 // Tiles of 16 tokens x 4 router rows for few tokens (more workgroups for the
 // same work; one chain per thread); 16 x 16 tiles with four chains per thread
 // beyond (a quarter of the LDS read instructions); two chunk buffers (deeper
@@ -421,13 +412,11 @@ hipError_t rlogits_launch(int order, const float* W, const float* X, int T, int 
     case QR_ORDER_AVX2:
       if (rlogits_row_ok<8>(T, d)) return rlogits_row_launch_t<8>(W, X, T, E, d, logits, st);
       if (small) return rlogits_launch_t<8, 8, 2, 4, 1, 2>(W, X, T, E, d, logits, st);
-      return rlogits_vec4() ? rlogits4_launch_t<8, 8, 2, 16, 1, 2>(W, X, T, E, d, logits, st)
-                            : rlogits_launch_t<8, 4, 4, 8, 2, 2>(W, X, T, E, d, logits, st);
+      return rlogits4_launch_t<8, 8, 2, 16, 1, 2>(W, X, T, E, d, logits, st);
     default:
       if (rlogits_row_ok<16>(T, d)) return rlogits_row_launch_t<16>(W, X, T, E, d, logits, st);
       if (small) return rlogits_launch_t<16, 4, 4, 4, 1, 2>(W, X, T, E, d, logits, st);
-      return rlogits_vec4() ? rlogits4_launch_t<16, 4, 4, 16, 1, 2>(W, X, T, E, d, logits, st)
-                            : rlogits_launch_t<16, 4, 4, 4, 4, 2>(W, X, T, E, d, logits, st);
+      return rlogits4_launch_t<16, 4, 4, 16, 1, 2>(W, X, T, E, d, logits, st);
   }
 }
 

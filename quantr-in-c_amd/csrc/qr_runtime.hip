@@ -9,14 +9,44 @@
 #include <cstring>
 #include <mutex>
 #include <unordered_map>
+#include <vector>
 
 #include "qr_common.h"
 #include "qr_internal.h"
 
+// A registered weight tensor: its device copy, its size, and a 64-bit digest
+// of what it was uploaded from (the first and last up to 64 bytes of each
+// host range, and for gathered tensors the part pointers and size).
 struct RegEntry {
-  void* dev;
-  size_t bytes;
+  void* dev = nullptr;
+  size_t bytes = 0;
+  uint64_t digest = 0;
+  bool gathered = false;
 };
+
+// FNV-1a over `n` bytes, continuing from h.
+static uint64_t fnv(uint64_t h, const void* p, size_t n) {
+  const uint8_t* b = static_cast<const uint8_t*>(p);
+  for (size_t i = 0; i < n; i++) h = (h ^ b[i]) * 0x100000001B3ull;
+  return h;
+}
+
+// Digest of host range [host, host + bytes): its length and its two ends.
+static uint64_t range_digest(uint64_t h, const void* host, size_t bytes) {
+  const size_t n = bytes < 64 ? bytes : 64;
+  h = fnv(h, &bytes, sizeof(bytes));
+  h = fnv(h, host, n);
+  return fnv(h, static_cast<const uint8_t*>(host) + bytes - n, n);
+}
+
+static uint64_t parts_digest(const void* const* parts, size_t part_bytes, int nparts) {
+  uint64_t h = 0xCBF29CE484222325ull;
+  for (int i = 0; i < nparts; i++) {
+    h = fnv(h, &parts[i], sizeof(parts[i]));
+    h = range_digest(h, parts[i], part_bytes);
+  }
+  return h;
+}
 
 struct qr_ctx {
   int device = 0;
@@ -25,8 +55,12 @@ struct qr_ctx {
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   std::mutex mu;
   std::unordered_map<const void*, RegEntry> registry;
-  void* moe_scratch = nullptr;
-  size_t moe_scratch_bytes = 0;
+  // Device scratch of the MoE and router calls.  A buffer that a larger call
+  // supersedes is retired, not freed: graphs captured earlier may still
+  // point at it.  Retired buffers are freed by qr_ctx_destroy.
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+  std::vector<void*> retired;
 };
 
 namespace {
@@ -62,7 +96,65 @@ int set_device(qr_ctx* c) {
   return QR_OK;
 }
 
+// True while the context's stream is being captured into a graph.  Calls that
+// would allocate, free, synchronize or record a memset node refuse then.
+bool capturing(qr_ctx* c) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(c->stream, &st) != hipSuccess) return false;
+  return st != hipStreamCaptureStatusNone;
+}
+
+#define QR_NO_CAPTURE(c, who)                                                               \
+  do {                                                                                      \
+    if (capturing(c))                                                                       \
+      return fail(QR_ERR_INVALID, "%s: not allowed while the stream is being captured "    \
+                  "(it allocates, synchronizes or sets memory)", who);                      \
+  } while (0)
+
+// At least `need` bytes of context scratch.  Growing is refused under capture;
+// the superseded buffer is retired (freed at qr_ctx_destroy), and the new one
+// is at least 1.5 x the old, so at most a few buffers are ever retired.
+int ctx_scratch(qr_ctx* c, size_t need, const char* who, void** out) {
+  if (need > c->scratch_bytes) {
+    if (capturing(c))
+      return fail(QR_ERR_INVALID,
+                  "%s: needs %zu bytes of scratch, more than any earlier call; run it once "
+                  "outside graph capture first",
+                  who, need);
+    if (set_device(c) != QR_OK) return QR_ERR_HIP;
+    size_t want = c->scratch_bytes + c->scratch_bytes / 2;
+    if (want < need) want = need;
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess) return fail(QR_ERR_NOMEM, "%s: scratch of %zu bytes: %s", who, want,
+                                     hipGetErrorString(e));
+    if (c->scratch) c->retired.push_back(c->scratch);
+    c->scratch = p;
+    c->scratch_bytes = want;
+  }
+  *out = c->scratch;
+  return QR_OK;
+}
+
 // ---- small kernels ---------------------------------------------------------
+// out[t * stride + i] = 0 for i < n, t < rows: the zero output of a call with
+// no weights, as a kernel (no memset node in a captured graph).
+__global__ void k_zero_rows(float* __restrict__ out, int n, int rows, int stride) {
+  const long total = (long)n * rows;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (long)gridDim.x * blockDim.x) {
+    const int t = (int)(i / n);
+    out[(size_t)t * stride + (i - (long)t * n)] = 0.0f;
+  }
+}
+
+// dst[i] = v for i < n bytes: qr_memset under graph capture.
+__global__ void k_fill_u8(uint8_t* __restrict__ dst, uint8_t v, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = v;
+}
+
 __global__ void k_copy16(uint4* __restrict__ dst, const uint4* __restrict__ src, size_t n16) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
        i += (size_t)gridDim.x * blockDim.x)
@@ -138,7 +230,8 @@ int qr_ctx_destroy(qr_ctx* c) {
   set_device(c);
   (void)hipStreamSynchronize(c->stream);
   for (auto& kv : c->registry) (void)hipFree(kv.second.dev);
-  if (c->moe_scratch) (void)hipFree(c->moe_scratch);
+  if (c->scratch) (void)hipFree(c->scratch);
+  for (void* p : c->retired) (void)hipFree(p);
   if (c->ev0) (void)hipEventDestroy(c->ev0);
   if (c->ev1) (void)hipEventDestroy(c->ev1);
   if (c->own) (void)hipStreamDestroy(c->own);
@@ -163,6 +256,7 @@ int qr_sync(qr_ctx* c) {
 int qr_malloc(qr_ctx* c, size_t bytes, void** p) {
   if (!c || !p) return fail(QR_ERR_INVALID, "qr_malloc: null argument");
   *p = nullptr;
+  QR_NO_CAPTURE(c, "qr_malloc");
   if (set_device(c) != QR_OK) return QR_ERR_HIP;
   hipError_t e = hipMalloc(p, bytes ? bytes : 16);
   if (e != hipSuccess) return fail(QR_ERR_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
@@ -172,6 +266,7 @@ int qr_malloc(qr_ctx* c, size_t bytes, void** p) {
 int qr_free(qr_ctx* c, void* p) {
   if (!c) return fail(QR_ERR_INVALID, "qr_free: null ctx");
   if (!p) return QR_OK;
+  QR_NO_CAPTURE(c, "qr_free");
   QR_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
   QR_HIP(hipFree(p), "hipFree");
   return QR_OK;
@@ -180,6 +275,7 @@ int qr_free(qr_ctx* c, void* p) {
 int qr_memcpy_h2d(qr_ctx* c, void* dst, const void* src, size_t n) {
   if (!c || (n && (!dst || !src))) return fail(QR_ERR_INVALID, "qr_memcpy_h2d: null argument");
   if (!n) return QR_OK;
+  QR_NO_CAPTURE(c, "qr_memcpy_h2d");
   QR_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D");
   QR_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
   return QR_OK;
@@ -188,6 +284,7 @@ int qr_memcpy_h2d(qr_ctx* c, void* dst, const void* src, size_t n) {
 int qr_memcpy_d2h(qr_ctx* c, void* dst, const void* src, size_t n) {
   if (!c || (n && (!dst || !src))) return fail(QR_ERR_INVALID, "qr_memcpy_d2h: null argument");
   if (!n) return QR_OK;
+  QR_NO_CAPTURE(c, "qr_memcpy_d2h");
   QR_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H");
   QR_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
   return QR_OK;
@@ -203,6 +300,14 @@ int qr_memcpy_d2d(qr_ctx* c, void* dst, const void* src, size_t n) {
 int qr_memset(qr_ctx* c, void* dst, int v, size_t n) {
   if (!c || (n && !dst)) return fail(QR_ERR_INVALID, "qr_memset: null argument");
   if (!n) return QR_OK;
+  if (capturing(c)) {  // a fill kernel: no memset node in the graph
+    size_t grid = (n + 255) / 256;
+    if (grid > 4096) grid = 4096;
+    hipLaunchKernelGGL(k_fill_u8, dim3((unsigned)grid), dim3(256), 0, c->stream,
+                       static_cast<uint8_t*>(dst), (uint8_t)v, n);
+    QR_HIP(hipGetLastError(), "k_fill_u8");
+    return QR_OK;
+  }
   QR_HIP(hipMemsetAsync(dst, v, n, c->stream), "hipMemsetAsync");
   return QR_OK;
 }
@@ -215,6 +320,7 @@ int qr_timer_start(qr_ctx* c) {
 
 int qr_timer_stop(qr_ctx* c, float* ms) {
   if (!c || !ms) return fail(QR_ERR_INVALID, "qr_timer_stop: null argument");
+  QR_NO_CAPTURE(c, "qr_timer_stop");
   QR_HIP(hipEventRecord(c->ev1, c->stream), "hipEventRecord");
   QR_HIP(hipEventSynchronize(c->ev1), "hipEventSynchronize");
   QR_HIP(hipEventElapsedTime(ms, c->ev0, c->ev1), "hipEventElapsedTime");
@@ -281,9 +387,11 @@ int qr_quantize_q8_0(qr_ctx* c, const float* x, void* y, long n) {
   return QR_OK;
 }
 
-int qr_gemv_ex(qr_ctx* c, uint32_t type, const void* w, const float* x, int xstride, float* y,
-               int ystride, int n, int d, int nt, int32_t* acc, int32_t* accb) {
+int qr_gemv_ord(qr_ctx* c, int order, uint32_t type, const void* w, const float* x, int xstride,
+                float* y, int ystride, int n, int d, int nt, int32_t* acc, int32_t* accb) {
   if (!c) return fail(QR_ERR_INVALID, "qr_gemv: null ctx");
+  if (order < QR_ORDER_SEQ || order > QR_ORDER_AVX512)
+    return fail(QR_ERR_INVALID, "qr_gemv: order %d", order);
   if (!known_type(type)) return fail(QR_ERR_INVALID, "qr_gemv: unknown type %u", type);
   if (n < 0 || d < 0) return fail(QR_ERR_INVALID, "qr_gemv: negative size");
   if (!(nt == 1 || nt == 2 || nt == 3 || nt == 4 || nt == 8))
@@ -292,8 +400,12 @@ int qr_gemv_ex(qr_ctx* c, uint32_t type, const void* w, const float* x, int xstr
   if (!x || !y) return fail(QR_ERR_INVALID, "qr_gemv: null x or y");
   if (xstride < d || ystride < n) return fail(QR_ERR_INVALID, "qr_gemv: stride below size");
   if (!w) {  // src/quant.c:443-446: no weights -> zero output
-    for (int t = 0; t < nt; t++)
-      QR_HIP(hipMemsetAsync(y + (size_t)t * ystride, 0, (size_t)n * 4, c->stream), "hipMemsetAsync");
+    const long total = (long)n * nt;
+    long grid = (total + 255) / 256;
+    if (grid > 1024) grid = 1024;
+    hipLaunchKernelGGL(k_zero_rows, dim3((unsigned)grid), dim3(256), 0, c->stream, y, n, nt,
+                       ystride);
+    QR_HIP(hipGetLastError(), "k_zero_rows");
     return QR_OK;
   }
   if (type == QR_T_F32) {
@@ -305,13 +417,19 @@ int qr_gemv_ex(qr_ctx* c, uint32_t type, const void* w, const float* x, int xstr
   if (!aligned(w, 16)) return fail(QR_ERR_INVALID, "qr_gemv: weights must be 16-byte aligned");
   if (!aligned(x, 16) || (nt > 1 && (xstride & 3)))
     return fail(QR_ERR_INVALID, "qr_gemv: x must be 16-byte aligned (and xstride a multiple of 4)");
-  const int R = qr::gemv_rows_per_wg((int)type, n, d, nt);
-  if (!qr::gemv_blk_ok((int)type, d, nt) && !qr::gemv_stream_ok((int)type, d, nt) &&
-      qr::gemv_lds_bytes((int)type, d, nt, R) > 64 * 1024)
+  const int R = qr::gemv_rows_per_wg((int)type, order, n, d, nt);
+  if (!qr::gemv_blk_ok((int)type, d, nt) && !qr::gemv_stream_ok((int)type, order, d, nt) &&
+      qr::gemv_lds_bytes((int)type, order, d, nt, R) > 64 * 1024)
     return fail(QR_ERR_UNSUPPORTED, "qr_gemv: d=%d nt=%d exceeds the LDS budget", d, nt);
-  QR_HIP(qr::gemv_launch((int)type, w, x, y, n, d, nt, xstride, ystride, acc, accb, c->stream),
+  QR_HIP(qr::gemv_launch((int)type, order, w, x, y, n, d, nt, xstride, ystride, acc, accb,
+                         c->stream),
          "k_gemv");
   return QR_OK;
+}
+
+int qr_gemv_ex(qr_ctx* c, uint32_t type, const void* w, const float* x, int xstride, float* y,
+               int ystride, int n, int d, int nt, int32_t* acc, int32_t* accb) {
+  return qr_gemv_ord(c, QR_ORDER_SEQ, type, w, x, xstride, y, ystride, n, d, nt, acc, accb);
 }
 
 int qr_gemv(qr_ctx* c, uint32_t type, const void* w, const float* x, float* y, int n, int d,
@@ -402,11 +520,12 @@ int qr_moe_route(qr_ctx* c, const qr_moe_layer* L, const float* xb, int T, int o
   if (T < 0) return fail(QR_ERR_INVALID, "qr_moe_route: T < 0");
   if (T == 0) return QR_OK;
   if (!xb || !idx || !wts) return fail(QR_ERR_INVALID, "qr_moe_route: null pointer");
-  float* logits = nullptr;
-  QR_HIP(hipMallocAsync((void**)&logits, (size_t)T * L->n_experts * 4, c->stream), "hipMallocAsync");
-  hipError_t e = qr::moe_route_launch(L, xb, T, order, logits, probs, idx, wts, c->stream);
-  (void)hipFreeAsync(logits, c->stream);
-  QR_HIP(e, "moe_route");
+  void* logits = nullptr;
+  rc = ctx_scratch(c, (size_t)T * L->n_experts * 4, "qr_moe_route", &logits);
+  if (rc) return rc;
+  QR_HIP(qr::moe_route_launch(L, xb, T, order, static_cast<float*>(logits), probs, idx, wts,
+                              c->stream),
+         "moe_route");
   return QR_OK;
 }
 
@@ -435,19 +554,11 @@ int qr_moe_forward(qr_ctx* c, const qr_moe_layer* L, float* x, const float* xb, 
   if (T == 0) return QR_OK;
   if (!x || !xb) return fail(QR_ERR_INVALID, "qr_moe_forward: null x / xb");
   if (!aligned(xb, 16) || !aligned(x, 16)) return fail(QR_ERR_INVALID, "qr_moe_forward: x/xb alignment");
-  const size_t need = qr::moe_scratch_bytes(L, T);
-  if (need > c->moe_scratch_bytes) {
-    if (set_device(c) != QR_OK) return QR_ERR_HIP;
-    QR_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    if (c->moe_scratch) (void)hipFree(c->moe_scratch);
-    c->moe_scratch = nullptr;
-    c->moe_scratch_bytes = 0;
-    hipError_t e = hipMalloc(&c->moe_scratch, need);
-    if (e != hipSuccess) return fail(QR_ERR_NOMEM, "qr_moe_forward: scratch %zu bytes", need);
-    c->moe_scratch_bytes = need;
-  }
+  void* base = nullptr;
+  rc = ctx_scratch(c, qr::moe_scratch_bytes(L, T), "qr_moe_forward", &base);
+  if (rc) return rc;
   qr::MoeScratch s;
-  qr::moe_scratch_carve(c->moe_scratch, L, T, &s);
+  qr::moe_scratch_carve(base, L, T, &s);
   QR_HIP(qr::moe_forward_launch(L, x, xb, T, order, s, c->stream), "moe_forward");
   const size_t kb = (size_t)T * L->n_used;
   if (idx_out) QR_HIP(hipMemcpyAsync(idx_out, s.idx, kb * 4, hipMemcpyDeviceToDevice, c->stream), "copy idx");
@@ -458,13 +569,17 @@ int qr_moe_forward(qr_ctx* c, const qr_moe_layer* L, float* x, const float* xb, 
 // ---- registry -----------------------------------------------------------------
 int qr_weights_upload(qr_ctx* c, const void* host, size_t bytes, const void** dev) {
   if (!c || !host || !dev) return fail(QR_ERR_INVALID, "qr_weights_upload: null argument");
+  QR_NO_CAPTURE(c, "qr_weights_upload");
   std::lock_guard<std::mutex> lk(c->mu);
   auto it = c->registry.find(host);
   if (it != c->registry.end()) {
-    if (it->second.bytes >= bytes) {
+    const RegEntry& r = it->second;
+    if (!r.gathered && r.bytes == bytes &&
+        r.digest == range_digest(0xCBF29CE484222325ull, host, bytes)) {
       *dev = it->second.dev;
       return QR_OK;
     }
+    (void)hipStreamSynchronize(c->stream);  // work still reading the old copy
     (void)hipFree(it->second.dev);
     c->registry.erase(it);
   }
@@ -478,7 +593,11 @@ int qr_weights_upload(qr_ctx* c, const void* host, size_t bytes, const void** de
     (void)hipFree(p);
     return hip_fail(e, "qr_weights_upload: copy");
   }
-  c->registry[host] = RegEntry{p, bytes};
+  RegEntry r;
+  r.dev = p;
+  r.bytes = bytes;
+  r.digest = range_digest(0xCBF29CE484222325ull, host, bytes);
+  c->registry[host] = r;
   *dev = p;
   return QR_OK;
 }
@@ -490,14 +609,17 @@ int qr_weights_upload_parts(qr_ctx* c, const void* key, const void* const* parts
   for (int i = 0; i < nparts; i++)
     if (!parts[i]) return fail(QR_ERR_INVALID, "qr_weights_upload_parts: null part %d", i);
   const size_t bytes = part_bytes * (size_t)nparts;
+  QR_NO_CAPTURE(c, "qr_weights_upload_parts");
   std::lock_guard<std::mutex> lk(c->mu);
   auto it = c->registry.find(key);
   if (it != c->registry.end()) {
-    if (it->second.bytes >= bytes) {
-      *dev = it->second.dev;
+    const RegEntry& r = it->second;
+    if (r.gathered && r.bytes == bytes && r.digest == parts_digest(parts, part_bytes, nparts)) {
+      *dev = r.dev;
       return QR_OK;
     }
-    (void)hipFree(it->second.dev);
+    (void)hipStreamSynchronize(c->stream);  // work still reading the old copy
+    (void)hipFree(r.dev);
     c->registry.erase(it);
   }
   if (set_device(c) != QR_OK) return QR_ERR_HIP;
@@ -512,7 +634,12 @@ int qr_weights_upload_parts(qr_ctx* c, const void* key, const void* const* parts
     (void)hipFree(p);
     return hip_fail(e, "qr_weights_upload_parts: copy");
   }
-  c->registry[key] = RegEntry{p, bytes};
+  RegEntry r;
+  r.dev = p;
+  r.bytes = bytes;
+  r.digest = parts_digest(parts, part_bytes, nparts);
+  r.gathered = true;
+  c->registry[key] = r;
   *dev = p;
   return QR_OK;
 }

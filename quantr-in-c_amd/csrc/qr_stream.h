@@ -37,13 +37,15 @@ struct TileShape {
   int RW;  // rows per wave tile; 0 when the row does not fit one tile
   int TS;  // LDS stride of one row's terms, in floats (16-byte aligned rows)
   int rb;  // bytes per row
+  int SL;  // term slots per unit (q8_slots: 9 for the Q8_0 lane orders)
 };
 
 // Rows per tile: as many whole rows as kUPL unit slots per lane cover, and for
 // staged formats as many as kCPL chunks per lane hold with the up to 15 bytes
 // of misalignment in front and the slack dword that unaligned LDS reads touch.
-__host__ __device__ inline TileShape tile_shape(int type, int d) {
+__host__ __device__ inline TileShape tile_shape(int type, int d, int q8o = kQ8Seq) {
   TileShape s;
+  s.SL = q8_slots(type, q8o);
   s.U = qr_units(type, d);
   s.rb = (int)qr_wrow_bytes(type, d);
   s.TS = ((s.U + 3) & ~3) + 4;
@@ -56,10 +58,10 @@ __host__ __device__ inline TileShape tile_shape(int type, int d) {
   return s;
 }
 
-// Bytes of one wave's LDS slice: the term rows, then (staged formats) the
-// staged tile.
+// Bytes of one wave's LDS slice: the term rows ([nt][RW][SL][TS] floats),
+// then (staged formats) the staged tile.
 __host__ __device__ inline size_t wave_terms_bytes(int nt, const TileShape& s) {
-  return align16((size_t)nt * s.RW * s.TS * 4);
+  return align16((size_t)nt * s.RW * s.SL * s.TS * 4);
 }
 __host__ __device__ inline size_t wave_slice_bytes(int type, int nt, const TileShape& s) {
   const bool direct = type == QR_T_Q4_K || type == QR_T_Q5_K;
@@ -367,8 +369,9 @@ __device__ inline void quantize_lane_act_wave(const float* __restrict__ X, const
 
 // Terms of every valid slot into terms[t][row][u] (t < NT).  `stage` is the
 // staged tile whose byte 0 is matrix byte (r0 * rb) & ~15.  Optional acc
-// receives the int32 unit sums ([NT][n][U]).
-template <int TYPE, int NT, int NS>
+// receives the int32 unit sums ([NT][n][U]).  Q8_0 in a lane order (Q8O)
+// writes the unit's 8 lane sums and da * db into terms[t][row][k][u] instead.
+template <int TYPE, int NT, int NS, int Q8O = kQ8Seq>
 __device__ inline void tile_terms(const TileRegs<TYPE>& R, const Slots& sl, int RWt, int r0,
                                   const TileShape& sh, const LaneAct<NT, NS>& A,
                                   const uint32_t* stage, float* terms, int32_t* acc, int n) {
@@ -416,14 +419,29 @@ __device__ inline void tile_terms(const TileRegs<TYPE>& R, const Slots& sl, int 
 #pragma unroll
         for (int t = 0; t < NT; t++) {
           const ActBlock& a = A.a[t][ai];
-          const int isum = dot_q8_regs(w, a.q);
-          tv[t] = term_q8(dh, isum, a.bd);
-          is[t] = isum;
+          if constexpr (Q8O != kQ8Seq) {
+            int l[8];
+            q8_lanes(w, a.q, l);
+            float* sp = terms + ((t * sh.RW + sl.row[i]) * 9) * sh.TS + u;
+            int isum = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+              sp[k * sh.TS] = (float)l[k];
+              isum += l[k];
+            }
+            sp[8 * sh.TS] = qr_h2f(dh) * a.bd;  // fp16_to_fp32(a.d) * fp16_to_fp32(b.d)
+            tv[t] = 0.0f;
+            is[t] = isum;
+          } else {
+            const int isum = dot_q8_regs(w, a.q);
+            tv[t] = term_q8(dh, isum, a.bd);
+            is[t] = isum;
+          }
         }
       }
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        terms[(t * sh.RW + sl.row[i]) * sh.TS + u] = tv[t];
+        if (q8_slots(TYPE, Q8O) == 1) terms[(t * sh.RW + sl.row[i]) * sh.TS + u] = tv[t];
         if (acc) acc[((size_t)t * n + r0 + sl.row[i]) * sh.U + u] = is[t];
       }
     }
@@ -458,6 +476,27 @@ __device__ inline float row_sum_seq(const float* tp, int U) {
   }
   for (; u < U; u++) s += tp[u];
   return s;
+}
+
+// Lane accumulator k of a row in a Q8_0 lane order (`tp` = the row's [9][ts]
+// slots, 16-byte aligned, ts a multiple of 4): acc over units 0..U-1, the
+// slot reads four units at a time.
+template <int Q8O>
+__device__ inline float q8_chain(const float* tp, int ts, int U, int k) {
+  const float* f = tp + k * ts;
+  const float* dd = tp + 8 * ts;
+  float acc = 0.0f;
+  int u = 0;
+  for (; u + 4 <= U; u += 4) {
+    const float4 fv = *reinterpret_cast<const float4*>(f + u);
+    const float4 dv = *reinterpret_cast<const float4*>(dd + u);
+    acc = q8_lane_update<Q8O>(fv.x, dv.x, acc);
+    acc = q8_lane_update<Q8O>(fv.y, dv.y, acc);
+    acc = q8_lane_update<Q8O>(fv.z, dv.z, acc);
+    acc = q8_lane_update<Q8O>(fv.w, dv.w, acc);
+  }
+  for (; u < U; u++) acc = q8_lane_update<Q8O>(f[u], dd[u], acc);
+  return acc;
 }
 
 }  // namespace qr

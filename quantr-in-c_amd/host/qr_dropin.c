@@ -122,7 +122,7 @@ void qr_matmul_q_fused(float* out, const float* x, const void* w, uint32_t type,
     yd = (float*)staging(1, (size_t)n * sizeof(float));
     if (rc == QR_OK && (!xd || !yd)) rc = QR_ERR_NOMEM;
     if (rc == QR_OK) rc = qr_memcpy_h2d(g_ctx, xd, x, (size_t)d * sizeof(float));
-    if (rc == QR_OK) rc = qr_gemv(g_ctx, type, wd, xd, yd, n, d, 1);
+    if (rc == QR_OK) rc = qr_gemv_ord(g_ctx, g_order, type, wd, xd, d, yd, n, n, d, 1, NULL, NULL);
     if (rc == QR_OK) rc = qr_memcpy_d2h(g_ctx, out, yd, (size_t)n * sizeof(float));
     pthread_mutex_unlock(&g_mu);
     if (rc != QR_OK) {

@@ -64,6 +64,8 @@ _SIGS = {
     "qr_gemv_ex": (C.c_int, [_vp, C.c_uint32, _vp, _vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int,
                              C.c_int, _vp, _vp]),
     "qr_gemv": (C.c_int, [_vp, C.c_uint32, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
+    "qr_gemv_ord": (C.c_int, [_vp, C.c_int, C.c_uint32, _vp, _vp, C.c_int, _vp, C.c_int, C.c_int,
+                              C.c_int, C.c_int, _vp, _vp]),
     "qr_matmul_f32": (C.c_int, [_vp, C.c_int, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
     "qr_softmax": (C.c_int, [_vp, _vp, C.c_int, C.c_int]),
     "qr_row_bytes": (C.c_size_t, [C.c_uint32, C.c_int]),
@@ -182,6 +184,10 @@ class Device:
         self._check(self.lib.qr_memcpy_h2d(self.ctx, _vp(ptr + offset), _ptr(arr), arr.nbytes),
                     "h2d")
 
+    def memset(self, buf, value, nbytes):
+        ptr = buf.ptr if isinstance(buf, DevBuf) else buf
+        self._check(self.lib.qr_memset(self.ctx, _vp(ptr), value, nbytes), "qr_memset")
+
     def copy(self, dst, src, nbytes):
         self._check(self.lib.qr_memcpy_d2d(self.ctx, _vp(dst), _vp(src), nbytes), "d2d")
 
@@ -209,6 +215,9 @@ class Device:
         self._check(rc, "qr_capture_end")
         return g.value
 
+    def last_error(self):
+        return self.lib.qr_last_error().decode(errors="replace")
+
     def graph_launch(self, g):
         self._check(self.lib.qr_graph_launch(self.ctx, _vp(g)), "qr_graph_launch")
 
@@ -220,10 +229,11 @@ class Device:
         self._check(self.lib.qr_quantize_q8_0(self.ctx, _vp(x_ptr), _vp(y_ptr), n), "qr_quantize_q8_0")
 
     def gemv(self, qtype, w_ptr, x_ptr, y_ptr, n, d, nt=1, xstride=None, ystride=None,
-             acc_ptr=None, accb_ptr=None):
-        self._check(self.lib.qr_gemv_ex(self.ctx, qtype, _vp(w_ptr), _vp(x_ptr),
-                                         xstride or d, _vp(y_ptr), ystride or n, n, d, nt,
-                                         _vp(acc_ptr), _vp(accb_ptr)), "qr_gemv_ex")
+             acc_ptr=None, accb_ptr=None, order=ORDER_SEQ):
+        """qr_gemv_ord: `order` is the reference build (only Q8_0 depends on it)."""
+        self._check(self.lib.qr_gemv_ord(self.ctx, order, qtype, _vp(w_ptr), _vp(x_ptr),
+                                          xstride or d, _vp(y_ptr), ystride or n, n, d, nt,
+                                          _vp(acc_ptr), _vp(accb_ptr)), "qr_gemv_ord")
 
     def matmul_f32(self, order, w_ptr, x_ptr, y_ptr, n, d, nt=1):
         self._check(self.lib.qr_matmul_f32(self.ctx, order, _vp(w_ptr), _vp(x_ptr), _vp(y_ptr),

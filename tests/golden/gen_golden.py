@@ -76,7 +76,7 @@ def gen_dequant(r):
     save("dequant.npz", **out)
 
 
-def gen_dots(rc, ra):
+def gen_dots(rc, ra, r5):
     out = {}
     for d in (2048, 768):
         x = I.activations(300 + d, 4, d)
@@ -97,6 +97,11 @@ def gen_dots(rc, ra):
             mc = [rc.matmul_q_fused(x[j], Wr, tr, W.shape[0], d, threads=4) for j in range(4)]
             out["dot_c99_%d_%d" % (t, d)] = np.array(vc, np.float32)
             out["dot_avx2_%d_%d" % (t, d)] = np.array(va, np.float32)
+            if r5 is not None and t == I.TYPE_Q8_0:
+                # the AVX-512 build updates the Q8_0 dot's 8 lanes by fused multiply-adds
+                v5 = [[r5.vec_dot(tr, Wr[i], xq_c[j], d) for j in range(4)]
+                      for i in range(W.shape[0])]
+                out["dot_avx512_%d_%d" % (t, d)] = np.array(v5, np.float32)
             out["mm_c99_%d_%d" % (t, d)] = np.array(mc, np.float32).T.copy()
     save("dots.npz", **out)
 
@@ -116,7 +121,7 @@ def gen_router(rc, ra, r5):
     save("router.npz", **out)
 
 
-def gen_moe(rc, ra):
+def gen_moe(rc, ra, r5):
     out = {}
     for name in I.MOE_CASES:
         m = I.moe_inputs(name)
@@ -125,7 +130,10 @@ def gen_moe(rc, ra):
         up, gate = m["up"], m["gate"]
         if ut == I.TYPE_Q4_K:  # the reference's sound Q5_K path computes corrected Q4_K
             up, gate, ut = I.q4k_to_q5k(up), I.q4k_to_q5k(gate), I.TYPE_Q5_K
-        for tag, lib, backend in (("c99", rc, BACKEND_REF), ("avx2", ra, BACKEND_AVX2)):
+        builds = [("c99", rc, BACKEND_REF), ("avx2", ra, BACKEND_AVX2)]
+        if r5 is not None:
+            builds.append(("avx512", r5, BACKEND_AVX512))
+        for tag, lib, backend in builds:
             xb, xo = lib.moe_layer(m["x"], m["dim"], m["hidden"], m["E"], m["K"], m["router"], up, ut,
                                    gate, ut, m["down"], m["down_type"], backend=backend, threads=4)
             out["xb_%s_%s" % (name, tag)] = xb
@@ -137,12 +145,14 @@ def main():
     rc, ra = RefLib("c99"), RefLib("avx2")
     assert rc.lib.refdrv_has_avx2_paths() == 0 and ra.lib.refdrv_has_avx2_paths() == 1
     r5 = RefLib("avx512") if cpu_has("avx512f") else None
+    if r5 is not None:
+        assert r5.lib.refdrv_has_avx512_paths() == 1
     gen_fp16(rc)
     gen_q8(rc)
     gen_dequant(rc)
-    gen_dots(rc, ra)
+    gen_dots(rc, ra, r5)
     gen_router(rc, ra, r5)
-    gen_moe(rc, ra)
+    gen_moe(rc, ra, r5)
 
 
 if __name__ == "__main__":

@@ -50,13 +50,63 @@ def _check_gemv(dev, oracle, qtype, W, X, n, d, nt, check_acc=True):
             assert (accb[t] == bsum).all(), "activation block sums tok %d" % t
 
 
+@pytest.mark.parametrize("nt", [1, 4])
 @pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("n,d", [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632)])
-def test_gemv_tinyllama_shapes_nt1(dev, oracle, qtype, n, d):
-    """TinyLlama-1.1B layer shapes, weights N(0, 0.02) quantized, x N(0, 1)."""
+def test_gemv_tinyllama_shapes(dev, oracle, qtype, n, d, nt):
+    """TinyLlama-1.1B layer shapes, weights N(0, 0.02) quantized, x N(0, 1), at
+    batch 1 and the speculative-verify width 4 (2048 x 5632 at 4 tokens takes
+    the block engine's register-staged activation path for Q4_K / Q5_K)."""
     W = synth.weights(1000 + n + d + qtype, n, d, qtype)
-    X = synth.normal(7, (1, d))
-    _check_gemv(dev, oracle, qtype, W, X, n, d, 1, check_acc=(n * d <= 2048 * 2048))
+    X = synth.normal(7 + nt, (nt, d))
+    _check_gemv(dev, oracle, qtype, W, X, n, d, nt, check_acc=(n * d <= 2048 * 2048))
+
+
+@pytest.mark.parametrize("order", [ORDER_AVX2, ORDER_AVX512])
+@pytest.mark.parametrize("n,d,nt", [(n, d, nt) for (n, d) in ((2048, 2048), (256, 2048),
+                                                            (2048, 5632), (37, 1408))
+                                    for nt in (1, 2, 4, 8) if not (d > 2048 and nt == 8)])
+def test_gemv_q8_0_build_orders(dev, oracle, order, nt, n, d):
+    """Q8_0 in the dot order of the -mavx2 -mfma build (8 lane accumulators,
+    multiply then add, src/quant.c:245-277) and of an -mavx512f build (the
+    lanes updated by fused multiply-adds): fp32 outputs and int32 unit sums
+    bit-exact with the oracle, whose lane orders the reference builds pin
+    (test_oracle_golden.py); one token on the streaming engine, more on the
+    general kernel."""
+    W = synth.weights(2000 + n + d + order, n, d, Q.TYPE_Q8_0)
+    X = synth.normal(2100 + nt, (nt, d))
+    units = d // 32
+    wb, xb, yb = dev.upload(W), dev.upload(X), dev.alloc(nt * n * 4)
+    acc, accb = dev.alloc(nt * n * units * 4), dev.alloc(nt * units * 4)
+    dev.gemv(Q.TYPE_Q8_0, wb.ptr, xb.ptr, yb.ptr, n, d, nt, acc_ptr=acc.ptr, accb_ptr=accb.ptr,
+             order=order)
+    y = dev.download(yb, (nt, n), np.float32)
+    want = oracle.matmul_q_fused(X, W, Q.TYPE_Q8_0, n, d, threads=16, order=order)
+    assert_bits_equal(y, want.reshape(nt, n), "Q8_0 order %d %dx%d nt=%d" % (order, n, d, nt))
+    seq = oracle.matmul_q_fused(X, W, Q.TYPE_Q8_0, n, d, threads=16, order=ORDER_SEQ)
+    assert (bits(want) != bits(seq)).any(), "the orders must differ on these inputs"
+    got_acc = dev.download(acc, (nt, n, units), np.int32)
+    for t in range(nt):
+        xq = oracle.quantize_q8_0(X[t])
+        for r in range(0, n, max(1, n // 64)):
+            isum, _ = oracle.row_accum(Q.TYPE_Q8_0, W[r], xq, d)
+            assert (got_acc[t, r] == isum).all(), "int sums row %d tok %d" % (r, t)
+
+
+@pytest.mark.parametrize("d", [2048, 768])
+def test_gemv_q8_0_orders_vs_reference_builds(dev, golden, d):
+    """The Q8_0 GEMV in each build's order against the dots the compiled
+    reference builds wrote (tests/golden/dots.npz): -std=c99, -mavx2 -mfma and
+    -mavx512f."""
+    g = golden("dots.npz")
+    X = I.activations(300 + d, 4, d)
+    W = I.dot_set(200 + Q.TYPE_Q8_0 + d, Q.TYPE_Q8_0, 15, d)
+    n = W.shape[0]
+    wb, xb, yb = dev.upload(W), dev.upload(X), dev.alloc(4 * n * 4)
+    for order, key in ((ORDER_SEQ, "c99"), (ORDER_AVX2, "avx2"), (ORDER_AVX512, "avx512")):
+        dev.gemv(Q.TYPE_Q8_0, wb.ptr, xb.ptr, yb.ptr, n, d, 4, order=order)
+        got = dev.download(yb, (4, n), np.float32).T
+        assert_bits_equal(got, g["dot_%s_8_%d" % (key, d)], "Q8_0 GEMV vs %s build" % key)
 
 
 @pytest.mark.parametrize("qtype", (Q.TYPE_Q4_K, Q.TYPE_Q5_K, Q.TYPE_Q6_K))
@@ -186,12 +236,17 @@ def test_dropin_matmul_q_fused(oracle, qtype):
     # earlier tests, whose freed arrays may share W's address.
     lib.qr_dropin_release_weights()
     try:
-        for _ in range(2):  # second call reuses the registered device copy
-            lib.qr_matmul_q_fused(_fp(out), _fp(x), _fp(W), qtype, n, d, 8)
-            assert_bits_equal(out, oracle.matmul_q_fused(x, W, qtype, n, d), "drop-in")
+        # qr_dropin_init selects the reference build whose arithmetic to match
+        for order in (ORDER_SEQ, ORDER_AVX2, ORDER_AVX512):
+            assert lib.qr_dropin_init(0, order) == 0
+            want = oracle.matmul_q_fused(x, W, qtype, n, d, order=order)
+            for _ in range(2):  # second call reuses the registered device copy
+                lib.qr_matmul_q_fused(_fp(out), _fp(x), _fp(W), qtype, n, d, 8)
+                assert_bits_equal(out, want, "drop-in order %d" % order)
         lib.qr_matmul_q_fused(_fp(out), _fp(x), None, qtype, n, d, 8)
         assert (out == 0).all()
     finally:
+        lib.qr_dropin_init(0, ORDER_AVX2)
         lib.qr_dropin_release_weights()
 
 
@@ -235,3 +290,97 @@ def test_gemv_graph_replays(dev, qtype, n):
             assert_bits_equal(dev.download(yb, (n,), np.float32), want, "replay %d" % r)
     finally:
         dev.graph_destroy(g)
+
+
+# ---- graph-capture contract (include/qr_hip.h) -----------------------------
+def _capture_raw(dev, fn):
+    """Begin capture, run fn (its exception is returned), end capture and
+    destroy the graph."""
+    lib = dev.lib
+    assert lib.qr_capture_begin(dev.ctx) == 0
+    err = None
+    try:
+        fn()
+    except Q.QrError as e:
+        err = e
+    g = C.c_void_p()
+    assert lib.qr_capture_end(dev.ctx, C.byref(g)) == 0, dev.last_error()
+    lib.qr_graph_destroy(g)
+    return err
+
+
+def test_capture_refuses_allocation_and_sync(dev):
+    """Calls that would allocate or synchronize refuse while capturing; the
+    capture itself stays usable."""
+    err = _capture_raw(dev, lambda: dev.alloc(1024))
+    assert err is not None and "captured" in str(err)
+    buf = dev.alloc(64)
+    err = _capture_raw(dev, lambda: dev.download(buf, 16, np.float32))
+    assert err is not None and "captured" in str(err)
+
+
+def test_capture_null_weights_zero_fill(dev):
+    """qr_gemv with NULL weights writes zeros by a kernel, so the captured
+    graph zeroes y on every replay (no memset node)."""
+    n, d = 300, 256
+    xb = dev.upload(np.ones((2, d), np.float32))
+    yb = dev.alloc(2 * n * 4)
+    g = dev.capture(lambda: dev.gemv(Q.TYPE_Q4_K, None, xb.ptr, yb.ptr, n, d, 2))
+    try:
+        for r in range(3):
+            dev.write(yb, np.full(2 * n, 5.0, np.float32))
+            dev.sync()
+            dev.graph_launch(g)
+            dev.sync()
+            assert (dev.download(yb, 2 * n, np.float32) == 0).all(), "replay %d" % r
+    finally:
+        dev.graph_destroy(g)
+
+
+def test_capture_memset_is_a_kernel(dev):
+    """qr_memset under capture records a fill kernel; replays refill."""
+    buf = dev.alloc(1000)
+    g = dev.capture(lambda: dev.memset(buf, 0x5A, 1000))
+    try:
+        for r in range(3):
+            dev.write(buf, np.zeros(1000, np.uint8))
+            dev.sync()
+            dev.graph_launch(g)
+            dev.sync()
+            assert (dev.download(buf, 1000, np.uint8) == 0x5A).all()
+    finally:
+        dev.graph_destroy(g)
+
+
+# ---- weight registry keying -------------------------------------------------
+def test_registry_reuploads_changed_contents(dev):
+    """An entry is reused only while the host bytes at both ends still match:
+    the same address holding other weights is uploaded again."""
+    lib = dev.lib
+    W = np.ascontiguousarray(synth.weights(4400, 64, 256, Q.TYPE_Q4_K))
+    p1 = C.c_void_p()
+    assert lib.qr_weights_upload(dev.ctx, _fp(W), W.nbytes, C.byref(p1)) == 0
+    p2 = C.c_void_p()
+    assert lib.qr_weights_upload(dev.ctx, _fp(W), W.nbytes, C.byref(p2)) == 0
+    assert p1.value == p2.value  # unchanged: reused
+    W[-1, -1] ^= 0xFF  # change the last byte in place
+    assert lib.qr_weights_upload(dev.ctx, _fp(W), W.nbytes, C.byref(p2)) == 0
+    got = dev.download(p2.value, W.shape, np.uint8)
+    assert (got == W).all()
+    lib.qr_weights_release(dev.ctx, _fp(W))
+
+
+def test_registry_parts_regather(dev):
+    """A gathered tensor remembers its parts: the same key with other parts
+    gathers again instead of returning the first gather."""
+    lib = dev.lib
+    parts_a = [np.full(256, i, np.uint8) for i in range(4)]
+    parts_b = [np.full(256, 10 + i, np.uint8) for i in range(4)]
+    key = np.zeros(1, np.uint8)
+    for parts in (parts_a, parts_b):
+        arr = (C.c_void_p * 4)(*[p.ctypes.data for p in parts])
+        out = C.c_void_p()
+        assert lib.qr_weights_upload_parts(dev.ctx, _fp(key), arr, 256, 4, C.byref(out)) == 0
+        got = dev.download(out.value, 1024, np.uint8)
+        assert (got == np.concatenate(parts)).all()
+    lib.qr_weights_release(dev.ctx, _fp(key))

@@ -2,9 +2,9 @@
 
 Bit-exact: router top-k indices and weights, dispatch permutation, and the
 layer output (the oracle's per-token block, src/runtime.c:202-269, which the
-CPU suite pins to the reference's own forward_runtime).  Quantized dots run in
-the sequential order on the GPU, so the oracle is asked for that dot order;
-the router runs in the order under test.
+CPU suite pins to the reference's own forward_runtime).  The order argument
+names the reference build: the router's accumulation order and the Q8_0 dot
+order; the oracle is asked for the same build.
 """
 import ctypes as C
 
@@ -56,10 +56,11 @@ def run_moe(dev, layer, x, xb, order):
 
 
 def check_moe(dev, oracle, layer, x, xb, order, what):
+    """The layer in the reference build `order` (router and Q8_0 dot orders)."""
     got, gi, gw = run_moe(dev, layer, x, xb, order)
     keep = []
     want, wi, ww = oracle.moe_forward(x, xb, layer.oracle_layer(keep), order=order,
-                                      dot_order=ORDER_SEQ, threads=16)
+                                      dot_order=order, threads=16)
     assert (gi == wi).all(), "%s: routing indices differ" % what
     assert_bits_equal(gw, ww, what + " routing weights")
     assert_bits_equal(got, want, what + " layer output")
@@ -82,17 +83,18 @@ def test_moe_golden_shapes(dev, oracle, name, order, T):
     check_moe(dev, oracle, layer, x, xb, order, "case %s T=%d" % (name, T))
 
 
-def test_moe_matches_reference_fixture(dev, golden):
-    """End to end against the reference's forward_runtime output (fixture),
-    for the Q4_K / Q6_K and Q5_K / Q6_K cases (no Q8_0 experts: the reference's
-    AVX2 build uses a lane order for Q8_0 dots that the GPU does not run)."""
+@pytest.mark.parametrize("name", sorted(I.MOE_CASES))
+def test_moe_matches_reference_fixture(dev, golden, name):
+    """End to end against the reference's own forward_runtime output
+    (tests/golden/moe.npz) of each build: -std=c99, -mavx2 -mfma and
+    -mavx512f, with Q4_K / Q6_K, Q8_0 / Q8_0 (lane-order Q8_0 dots in the
+    vector builds) and Q5_K / Q6_K experts."""
     g = golden("moe.npz")
-    for name in ("a", "c"):
-        layer, m = random_layer(dev, name)
-        for build, order in (("c99", ORDER_SEQ), ("avx2", ORDER_AVX2)):
-            xb = g["xb_%s_%s" % (name, build)]
-            got, _, _ = run_moe(dev, layer, m["x"], xb, order)
-            assert_bits_equal(got, g["xo_%s_%s" % (name, build)], "reference %s/%s" % (name, build))
+    layer, m = random_layer(dev, name)
+    for build, order in (("c99", ORDER_SEQ), ("avx2", ORDER_AVX2), ("avx512", ORDER_AVX512)):
+        xb = g["xb_%s_%s" % (name, build)]
+        got, _, _ = run_moe(dev, layer, m["x"], xb, order)
+        assert_bits_equal(got, g["xo_%s_%s" % (name, build)], "reference %s/%s" % (name, build))
 
 
 _QWEN3 = {}
@@ -147,10 +149,11 @@ def test_moe_qwen15_shared_expert(dev, oracle):
                   up_type=Q.TYPE_Q4_K, down_type=Q.TYPE_Q4_K)
     layer = DevLayer(dev, dim, hidden, E, K, router, up, gate, down, Q.TYPE_Q4_K, Q.TYPE_Q8_0,
                      shared=shared)
-    for T in (1, 8, 64):
+    for T, order in ((1, ORDER_SEQ), (8, ORDER_SEQ), (64, ORDER_SEQ), (1, ORDER_AVX2),
+                     (64, ORDER_AVX2)):
         xb = synth.normal(4100 + T, (T, dim))
         x = synth.normal(4200 + T, (T, dim))
-        check_moe(dev, oracle, layer, x, xb, ORDER_SEQ, "qwen1.5 T=%d" % T)
+        check_moe(dev, oracle, layer, x, xb, order, "qwen1.5 T=%d order %d" % (T, order))
 
 
 @pytest.mark.parametrize("order", [ORDER_SEQ, ORDER_AVX2])
@@ -252,7 +255,6 @@ def test_dropin_moe_block(dev, oracle):
     down_parts = [np.array(m["down"][e * sd:(e + 1) * sd]) for e in range(E)]
     down_p = (C.c_void_p * E)(*[a.ctypes.data for a in down_parts[::-1]][::-1])
     assert lib.qr_dropin_init(0, ORDER_SEQ) == 0
-    lib.qr_dropin_release_weights()  # host addresses of earlier tests may be reused
     x0 = I.activations(990, 1, dim)[0]
     xb = I.activations(991, 1, dim)[0]
     x = x0.copy()
@@ -268,10 +270,11 @@ def test_dropin_moe_block(dev, oracle):
     lib.qr_dropin_release_weights()
 
 
+@pytest.mark.parametrize("order", [ORDER_SEQ, ORDER_AVX2, ORDER_AVX512])
 @pytest.mark.parametrize("ut,dt", [(Q.TYPE_Q4_K, Q.TYPE_Q4_K), (Q.TYPE_Q5_K, Q.TYPE_Q5_K),
                                    (Q.TYPE_Q4_K, Q.TYPE_Q8_0), (Q.TYPE_Q8_0, Q.TYPE_Q6_K)])
 @pytest.mark.parametrize("T", [1, 5, 48])
-def test_moe_type_pairs(dev, oracle, ut, dt, T):
+def test_moe_type_pairs(dev, oracle, ut, dt, T, order):
     """Every expert weight-type pair through the one-token, grouped-GEMV and
     grouped-MFMA paths (T = 1, 5, 48 with 20 experts top-6: 0.3, 1.5 and 14
     pairs per expert), random block bytes; E = 20 is not a multiple of the
@@ -286,7 +289,7 @@ def test_moe_type_pairs(dev, oracle, ut, dt, T):
     layer = DevLayer(dev, dim, hidden, E, K, router, up, gate, down, ut, dt)
     x = I.activations(seed + 4 + T, T, dim)
     xb = I.activations(seed + 5 + T, T, dim)
-    check_moe(dev, oracle, layer, x, xb, ORDER_AVX2, "types %d/%d T=%d" % (ut, dt, T))
+    check_moe(dev, oracle, layer, x, xb, order, "types %d/%d T=%d order %d" % (ut, dt, T, order))
 
 
 @pytest.mark.parametrize("T", [24, 70])
@@ -356,3 +359,40 @@ def test_moe_graph_replays(dev, oracle, T):
                               "replay %d T=%d" % (r, T))
     finally:
         dev.graph_destroy(g)
+
+
+def test_capture_moe_growth_refused(oracle):
+    """On a fresh context, a captured qr_moe_forward that needs scratch
+    refuses (it would allocate); after one eager call of the same size the
+    capture succeeds, and scratch grown later keeps the earlier graph valid."""
+    d = Q.Device(0)
+    try:
+        layer, m = random_layer(d, "a")
+        T = 16
+        x = I.activations(9600, T, m["dim"])
+        xb = I.activations(9601, T, m["dim"])
+        xd, xbd = d.upload(x), d.upload(xb)
+        lib = d.lib
+        assert lib.qr_capture_begin(d.ctx) == 0
+        rc = lib.qr_moe_forward(d.ctx, C.byref(layer.L), xd.ptr, xbd.ptr, T, ORDER_AVX2, None, None)
+        msg = d.last_error()
+        g = C.c_void_p()
+        assert lib.qr_capture_end(d.ctx, C.byref(g)) == 0
+        lib.qr_graph_destroy(g)
+        assert rc == -1 and "outside graph capture" in msg
+        want, _, _ = run_moe(d, layer, x, xb, ORDER_AVX2)  # eager: allocates the scratch
+        d.write(xd, x)
+        g = d.capture(lambda: d.moe_forward(layer.L, xd.ptr, xbd.ptr, T, ORDER_AVX2))
+        try:
+            run_moe(d, layer, I.activations(9602, 64, m["dim"]), I.activations(9603, 64, m["dim"]),
+                    ORDER_AVX2)  # grows the scratch; the graph's buffer is kept
+            for r in range(2):
+                d.write(xd, x)
+                d.sync()
+                d.graph_launch(g)
+                d.sync()
+                assert_bits_equal(d.download(xd, (T, m["dim"]), np.float32), want, "replay %d" % r)
+        finally:
+            d.graph_destroy(g)
+    finally:
+        d.close()

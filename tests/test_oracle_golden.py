@@ -1,8 +1,8 @@
 """The oracle (oracle/qr_oracle.c) against the reference's own outputs.
 
 The fixtures in tests/golden/ were written by tests/golden/gen_golden.py from
-the reference's sources compiled as they are (both the Makefile's -std=c99
-flavour and the CI's -mavx2 -mfma flavour).  Every comparison is bit-exact.
+the reference's sources compiled as they are (the Makefile's -std=c99
+flavour, the CI's -mavx2 -mfma flavour and an -mavx512f flavour).  Every comparison is bit-exact.
 """
 import numpy as np
 import pytest
@@ -74,6 +74,12 @@ def test_vec_dot(oracle, golden, qtype, d):
     avx = np.array([[oracle.vec_dot(qtype, W[i], xq[j], d, ORDER_AVX2) for j in range(4)]
                     for i in range(W.shape[0])], np.float32)
     assert_bits_equal(avx, g["dot_avx2_%d_%d" % (qtype, d)], "AVX2 vs -mavx2 -mfma build")
+    if qtype == I.TYPE_Q8_0:
+        # the -mavx512f build updates the 8 lanes with fused multiply-adds
+        v5 = np.array([[oracle.vec_dot(qtype, W[i], xq[j], d, ORDER_AVX512) for j in range(4)]
+                       for i in range(W.shape[0])], np.float32)
+        assert_bits_equal(v5, g["dot_avx512_%d_%d" % (qtype, d)], "AVX512 vs -mavx512f build")
+        assert (bits(v5) != bits(avx)).any() and (bits(avx) != bits(seq)).any()
     mm = np.stack([oracle.matmul_q_fused(x[j], W, qtype, W.shape[0], d, threads=4)
                    for j in range(4)], axis=1)
     assert_bits_equal(mm, g["mm_c99_%d_%d" % (qtype, d)], "matmul_q_fused")
@@ -104,7 +110,7 @@ def _layer(oracle, keep, m):
 
 
 @pytest.mark.parametrize("name", sorted(I.MOE_CASES))
-@pytest.mark.parametrize("build", ["c99", "avx2"])
+@pytest.mark.parametrize("build", ["c99", "avx2", "avx512"])
 def test_moe_block(oracle, golden, name, build):
     """The reference's MoE block (src/runtime.c:202-269) run through its own
     forward_runtime: routing, SwiGLU experts, slot-order combine, residual."""
@@ -114,7 +120,7 @@ def test_moe_block(oracle, golden, name, build):
     keep = []
     L = _layer(oracle, keep, m)
     xb = g["xb_%s_%s" % (name, build)]
-    order = ORDER_SEQ if build == "c99" else ORDER_AVX2
+    order = {"c99": ORDER_SEQ, "avx2": ORDER_AVX2, "avx512": ORDER_AVX512}[build]
     xo, idx, w = oracle.moe_forward(m["x"], xb, L, order=order, dot_order=order, threads=4)
     assert_bits_equal(xo, g["xo_%s_%s" % (name, build)], "MoE block %s/%s" % (name, build))
     assert (idx >= 0).all() and (idx < m["E"]).all()
