@@ -190,6 +190,20 @@ int qr_moe_dispatch(qr_ctx* ctx, const int32_t* idx, int T, int K, int E, int32_
 int qr_moe_forward(qr_ctx* ctx, const qr_moe_layer* L, float* x, const float* xb, int T,
                    int order, int32_t* idx_out, float* w_out);
 
+/* qr_moe_forward without any allocation: no reference counterpart; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, same
+ * results as qr_moe_forward.  Its scratch is one fixed device array of
+ * QR_NOALLOC_SCRATCH_BYTES per GPU, held from library load until the process
+ * ends; a call whose layer and T need more returns QR_ERR_INVALID (about
+ * 111 KiB per token at the Qwen3-30B-A3B shape: up to T = 150).  Every call on
+ * one GPU, from any context, shares that array: calls that overlap on one GPU
+ * (other streams, other threads) race, so serialize them.  It calls no
+ * hipMalloc / hipFree. */
+#define QR_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+int qr_moe_forward_noalloc(qr_ctx* ctx, const qr_moe_layer* L, float* x, const float* xb, int T,
+                           int order, int32_t* idx_out, float* w_out);
+
 /* ---- weight registry (host pointer -> device copy) ---------------------- */
 
 /* Upload `bytes` from host memory once and return the device copy; later

@@ -58,9 +58,12 @@ struct qr_ctx {
   // Device scratch of the MoE and router calls.  A buffer that a larger call
   // supersedes is retired, not freed: graphs captured earlier may still
   // point at it.  Retired buffers are freed by qr_ctx_destroy.
-  void* scratch = nullptr;
-  size_t scratch_bytes = 0;
+  void* work = nullptr;
+  size_t work_bytes = 0;
   std::vector<void*> retired;
+  // Device address of this GPU's copy of the static `scratch` array
+  // (qr_moe_forward_noalloc).
+  void* static_scratch = nullptr;
 };
 
 namespace {
@@ -115,24 +118,52 @@ bool capturing(qr_ctx* c) {
 // the superseded buffer is retired (freed at qr_ctx_destroy), and the new one
 // is at least 1.5 x the old, so at most a few buffers are ever retired.
 int ctx_scratch(qr_ctx* c, size_t need, const char* who, void** out) {
-  if (need > c->scratch_bytes) {
+  if (need > c->work_bytes) {
     if (capturing(c))
       return fail(QR_ERR_INVALID,
                   "%s: needs %zu bytes of scratch, more than any earlier call; run it once "
                   "outside graph capture first",
                   who, need);
     if (set_device(c) != QR_OK) return QR_ERR_HIP;
-    size_t want = c->scratch_bytes + c->scratch_bytes / 2;
+    size_t want = c->work_bytes + c->work_bytes / 2;
     if (want < need) want = need;
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, want);
     if (e != hipSuccess) return fail(QR_ERR_NOMEM, "%s: scratch of %zu bytes: %s", who, want,
                                      hipGetErrorString(e));
-    if (c->scratch) c->retired.push_back(c->scratch);
-    c->scratch = p;
-    c->scratch_bytes = want;
+    if (c->work) c->retired.push_back(c->work);
+    c->work = p;
+    c->work_bytes = want;
   }
-  *out = c->scratch;
+  *out = c->work;
+  return QR_OK;
+}
+
+// ---- the static scratch of qr_moe_forward_noalloc ---------------------------
+// A file-scope device array: every GPU the library runs on holds its own copy
+// (QR_NOALLOC_SCRATCH_BYTES) from code-object load until the process ends.
+// Host code never uses the name `scratch` as an address (on the host it is a
+// stand-in, not device memory): qr_ctx_create looks up this device's copy
+// with hipGetSymbolAddress, once per device, and every use goes through that
+// pointer.  Calls on one GPU share the array; it keeps the last call's
+// contents (the MoE kernels write every scratch word they read, so nothing
+// has to start at zero).
+__device__ __align__(256) uint8_t scratch[QR_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_sym_mu;
+void* g_sym_ptr[64] = {};  // per device; set once, with that device current
+
+// This device's address of `scratch`; c's device is current.
+int static_scratch_addr(int device, void** out) {
+  if (device < 0 || device >= 64) return fail(QR_ERR_INVALID, "device %d out of range", device);
+  std::lock_guard<std::mutex> lk(g_sym_mu);
+  if (!g_sym_ptr[device]) {
+    void* p = nullptr;
+    QR_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(QR_ERR_HIP, "hipGetSymbolAddress(scratch): null address");
+    g_sym_ptr[device] = p;
+  }
+  *out = g_sym_ptr[device];
   return QR_OK;
 }
 
@@ -221,6 +252,14 @@ int qr_ctx_create(int device, qr_ctx** out) {
     return hip_fail(e, "qr_ctx_create");
   }
   c->stream = c->own;
+  const int rs = static_scratch_addr(device, &c->static_scratch);
+  if (rs != QR_OK) {
+    (void)hipEventDestroy(c->ev0);
+    (void)hipEventDestroy(c->ev1);
+    (void)hipStreamDestroy(c->own);
+    delete c;
+    return rs;
+  }
   *out = c;
   return QR_OK;
 }
@@ -230,7 +269,7 @@ int qr_ctx_destroy(qr_ctx* c) {
   set_device(c);
   (void)hipStreamSynchronize(c->stream);
   for (auto& kv : c->registry) (void)hipFree(kv.second.dev);
-  if (c->scratch) (void)hipFree(c->scratch);
+  if (c->work) (void)hipFree(c->work);
   for (void* p : c->retired) (void)hipFree(p);
   if (c->ev0) (void)hipEventDestroy(c->ev0);
   if (c->ev1) (void)hipEventDestroy(c->ev1);
@@ -559,6 +598,36 @@ int qr_moe_forward(qr_ctx* c, const qr_moe_layer* L, float* x, const float* xb, 
   if (rc) return rc;
   qr::MoeScratch s;
   qr::moe_scratch_carve(base, L, T, &s);
+  QR_HIP(qr::moe_forward_launch(L, x, xb, T, order, s, c->stream), "moe_forward");
+  const size_t kb = (size_t)T * L->n_used;
+  if (idx_out) QR_HIP(hipMemcpyAsync(idx_out, s.idx, kb * 4, hipMemcpyDeviceToDevice, c->stream), "copy idx");
+  if (w_out) QR_HIP(hipMemcpyAsync(w_out, s.wts, kb * 4, hipMemcpyDeviceToDevice, c->stream), "copy wts");
+  return QR_OK;
+}
+
+int qr_moe_forward_noalloc(qr_ctx* c, const qr_moe_layer* L, float* x, const float* xb, int T,
+                           int order, int32_t* idx_out, float* w_out) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_moe_forward_noalloc: null ctx");
+  int rc = check_layer(L, "qr_moe_forward_noalloc");
+  if (rc) return rc;
+  rc = check_experts(L, "qr_moe_forward_noalloc");
+  if (rc) return rc;
+  if (order < QR_ORDER_SEQ || order > QR_ORDER_AVX512)
+    return fail(QR_ERR_INVALID, "qr_moe_forward_noalloc: order %d", order);
+  if (T < 0) return fail(QR_ERR_INVALID, "qr_moe_forward_noalloc: T < 0");
+  if (T == 0) return QR_OK;
+  if (!x || !xb) return fail(QR_ERR_INVALID, "qr_moe_forward_noalloc: null x / xb");
+  if (!aligned(xb, 16) || !aligned(x, 16))
+    return fail(QR_ERR_INVALID, "qr_moe_forward_noalloc: x/xb alignment");
+  const size_t need = qr::moe_scratch_bytes(L, T);
+  if (need > (size_t)QR_NOALLOC_SCRATCH_BYTES)
+    return fail(QR_ERR_INVALID,
+                "qr_moe_forward_noalloc: T=%d on this layer needs %zu bytes of scratch, above "
+                "the fixed %d (use qr_moe_forward, or fewer tokens per call)",
+                T, need, (int)QR_NOALLOC_SCRATCH_BYTES);
+  if (!c->static_scratch) return fail(QR_ERR_HIP, "qr_moe_forward_noalloc: no scratch address");
+  qr::MoeScratch s;
+  qr::moe_scratch_carve(c->static_scratch, L, T, &s);
   QR_HIP(qr::moe_forward_launch(L, x, xb, T, order, s, c->stream), "moe_forward");
   const size_t kb = (size_t)T * L->n_used;
   if (idx_out) QR_HIP(hipMemcpyAsync(idx_out, s.idx, kb * 4, hipMemcpyDeviceToDevice, c->stream), "copy idx");

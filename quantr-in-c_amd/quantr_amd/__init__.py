@@ -72,6 +72,8 @@ _SIGS = {
     "qr_moe_route": (C.c_int, [_vp, C.POINTER(MoeLayer), _vp, C.c_int, C.c_int, _vp, _vp, _vp]),
     "qr_moe_dispatch": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp]),
     "qr_moe_forward": (C.c_int, [_vp, C.POINTER(MoeLayer), _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
+    "qr_moe_forward_noalloc": (C.c_int, [_vp, C.POINTER(MoeLayer), _vp, _vp, C.c_int, C.c_int,
+                                         _vp, _vp]),
     "qr_weights_upload": (C.c_int, [_vp, _vp, C.c_size_t, C.POINTER(_vp)]),
     "qr_weights_upload_parts": (C.c_int, [_vp, _vp, _vp, C.c_size_t, C.c_int, C.POINTER(_vp)]),
     "qr_weights_lookup": (C.c_int, [_vp, _vp, C.POINTER(_vp)]),
