@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 0, 8, 12, 13, 14
 ORDER_SEQ, ORDER_AVX2, ORDER_AVX512 = 0, 1, 2
 # KernelBackend values (include/types.h:99-108)
-BACKEND_REF, BACKEND_AVX2, BACKEND_AVX512 = 0, 1, 2
+BACKEND_REF, BACKEND_AVX2, BACKEND_AVX512, BACKEND_GPU = 0, 1, 2, 7
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
@@ -250,6 +250,13 @@ class RefLib:
         L.matmul_q_fused.argtypes = [_f32p, _f32p, C.c_void_p, C.c_uint32, C.c_int, C.c_int, C.c_int]
         L.refdrv_matmul.argtypes = [C.c_int, _f32p, _f32p, _f32p, C.c_int, C.c_int]
         L.refdrv_softmax.argtypes = [C.c_int, _f32p, C.c_int]
+        L.refdrv_matmul_q_fused.argtypes = [_f32p, _f32p, C.c_void_p, C.c_uint32, C.c_int,
+                                            C.c_int, C.c_int]
+        if hasattr(L, "refgpu_bind"):  # the GPU-bound builds (ref_gpu_bind.c)
+            L.refgpu_bind.restype = C.c_int
+            L.refgpu_bind.argtypes = [C.c_int]
+            L.refgpu_take_calls.restype = C.c_int
+            L.refgpu_take_calls.argtypes = []
         L.refdrv_moe_layer.restype = C.c_int
         L.refdrv_moe_layer.argtypes = [_f32p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
                                        C.c_int, C.c_int, _f32p, C.c_void_p, C.c_uint32,
@@ -277,6 +284,13 @@ class RefLib:
         out = np.zeros(n, np.float32)
         self.lib.matmul_q_fused(out, np.ascontiguousarray(x, np.float32),
                                 _ptr(np.ascontiguousarray(w)), qtype, n, d, threads)
+        return out
+
+    def matmul_q_fused_cross(self, x, w, qtype, n, d, threads=1):
+        """matmul_q_fused called from another file (wrapped in the GPU-bound builds)."""
+        out = np.zeros(n, np.float32)
+        self.lib.refdrv_matmul_q_fused(out, np.ascontiguousarray(x, np.float32),
+                                       _ptr(np.ascontiguousarray(w)), qtype, n, d, threads)
         return out
 
     def matmul(self, backend, x, w, n, d):

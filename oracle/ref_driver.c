@@ -43,6 +43,14 @@ int refdrv_has_avx512_paths(void) {
 #endif
 }
 
+/* matmul_q_fused called from this file: in the GPU-bound builds
+ * (ref_gpu_bind.c) the linker sends it to qr_matmul_q_fused, in the plain
+ * builds it is the reference's own. */
+void refdrv_matmul_q_fused(float* out, const float* x, const void* w, uint32_t type, int n, int d,
+                           int threads) {
+    matmul_q_fused(out, x, w, type, n, d, threads);
+}
+
 /* KernelOps.matmul / softmax / rmsnorm of a backend (src/kernels.c:209-214). */
 void refdrv_matmul(int backend, float* out, const float* x, const float* w, int n, int d) {
     kernels_for_backend((KernelBackend)backend)->matmul(out, x, w, n, d, 1);
