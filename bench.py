@@ -7,18 +7,28 @@ Headline (one JSON line on stdout): Q4_K decode GEMV weight GB/s on the
 over one of 16 distinct weight copies (592 MB in total, more than the 256 MB
 Infinity Cache), with the activation already resident in HBM.  The K timed
 steps are replayed from a HIP graph between two synchronizations and timed
-with HIP events on the launch stream.
+with HIP events on the launch stream.  Beside it: a plain read of the same
+bytes (the rate a single kernel streaming them once reaches).
 
-The same line carries the Qwen3-30B-A3B-shaped MoE layer (2048 wide, 128
-experts top-8, ffn 768, gate/up Q4_K, down Q6_K, Zipf(1.1) expert skew) in
-tokens/s at T = 1, 16 and 512, rotating over 48 layer copies like a 48-layer
-decode, and the CPU baseline: the reference's own matmul_q_fused and MoE block
-(oracle/_ref, its sources compiled with the CI flags) timed on this host's cores.
+Extra keys of the same line:
+  gemv_sweep   Q8_0 at the TinyLlama-1.1B layer shapes (1 token), and Q4_K /
+               Q5_K / Q6_K at those shapes plus 32000 x 2048, 1 and 4 tokens;
+               each shape rotates over distinct matrices filling > 590 MB;
+  moe_qwen3    the Qwen3-30B-A3B-shaped MoE layer (2048 wide, 128 experts
+               top-8, ffn 768, gate/up Q4_K, down Q6_K, Zipf(1.1) expert skew)
+               in tokens/s at T = 1, 16 and 512, rotating over 48 layer copies
+               (router included) like a 48-layer decode;
+  moe_qwen15   the Qwen1.5-MoE-A2.7B-shaped layer (60 experts top-4, ffn 1408,
+               shared expert ffn 5632 with a sigmoid gate) at T = 1 and 64;
+  cpu_baseline the reference's own matmul_q_fused and MoE block (oracle/_ref,
+               its sources compiled with the CI flags) on this host's cores at
+               1, 8 and all available threads: 3 warm-ups, then the median.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-moe] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-moe] [--no-cpu] [--no-sweep]
 """
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -33,18 +43,19 @@ from quantr_amd import synth  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
 METRIC = "Q4_K GEMV weight GB/s (% HBM peak); MoE layer tokens/s at 30B-A3B shape"
+TNAME = {Q.TYPE_Q8_0: "Q8_0", Q.TYPE_Q4_K: "Q4_K", Q.TYPE_Q5_K: "Q5_K", Q.TYPE_Q6_K: "Q6_K"}
+TINYLLAMA = [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632)]
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def host_cores():
+def host_cpus():
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        return os.cpu_count() or 1
 
 
 def cpu_model():
@@ -55,44 +66,6 @@ def cpu_model():
     except OSError:
         pass
     return "unknown"
-
-
-# ---------------------------------------------------------------------------
-# GEMV headline
-# ---------------------------------------------------------------------------
-def gemv_alg_bytes(qtype, n, d, nt=1):
-    """Weights + Q8_0 activation + fp32 output per launch."""
-    return n * synth.row_bytes(qtype, d) + nt * ((d // 32) * 34 + 4 * n)
-
-
-def bench_gemv(dev, qtype, n, d, nt, steps, warmup, copies=16, seed=1):
-    rb = synth.row_bytes(qtype, d)
-    wbytes = n * rb
-    W = synth.weights(seed, n, d, qtype)
-    wbuf = dev.alloc(wbytes * copies)
-    dev.write(wbuf, W)
-    for c in range(1, copies):
-        dev.copy(wbuf.ptr + c * wbytes, wbuf.ptr, wbytes)
-    xb = dev.upload(synth.normal(seed + 1, (nt, d)))
-    yb = dev.alloc(nt * n * 4)
-    for i in range(warmup):
-        dev.gemv(qtype, wbuf.ptr + (i % copies) * wbytes, xb.ptr, yb.ptr, n, d, nt)
-    dev.sync()
-
-    def record():
-        for i in range(steps):
-            dev.gemv(qtype, wbuf.ptr + (i % copies) * wbytes, xb.ptr, yb.ptr, n, d, nt)
-
-    g = dev.capture(record)
-    dev.graph_launch(g)  # one untimed replay
-    dev.sync()
-    ms = timed_replays(dev, g)
-    dev.graph_destroy(g)
-    wbuf.free()
-    s = ms / 1e3 / steps
-    return dict(ms_per_step=ms / steps, weight_gbps=wbytes / s / 1e9,
-                alg_bytes=gemv_alg_bytes(qtype, n, d, nt),
-                achieved_gbps=gemv_alg_bytes(qtype, n, d, nt) / s / 1e9)
 
 
 def timed_replays(dev, g, reps=5):
@@ -106,6 +79,24 @@ def timed_replays(dev, g, reps=5):
         t.append(dev.timer_stop())
     dev.sync()
     return float(np.median(t))
+
+
+def graph_ms(dev, launch, steps, reps=5):
+    """Per-launch ms of launch(i), i < steps, captured once and replayed."""
+    g = dev.capture(lambda: [launch(i) for i in range(steps)])
+    dev.graph_launch(g)  # one untimed replay
+    dev.sync()
+    ms = timed_replays(dev, g, reps)
+    dev.graph_destroy(g)
+    return ms / steps
+
+
+# ---------------------------------------------------------------------------
+# GEMV
+# ---------------------------------------------------------------------------
+def gemv_alg_bytes(qtype, n, d, nt=1):
+    """Weights + Q8_0 activation + fp32 output per launch."""
+    return n * synth.row_bytes(qtype, d) + nt * ((d // 32) * 34 + 4 * n)
 
 
 def copy_calibration(dev, nbytes=512 << 20):
@@ -125,59 +116,180 @@ def copy_calibration(dev, nbytes=512 << 20):
     return dict(bytes=nbytes, ms=ms, gbps=2 * nbytes / (ms / 1e3) / 1e9)
 
 
+def bench_headline(dev, steps, warmup, copies=16):
+    """Q4_K 32000 x 2048 at 1 and 4 tokens over 16 weight copies, and a plain
+    read of the same bytes."""
+    qtype, n, d = Q.TYPE_Q4_K, 32000, 2048
+    wbytes = n * synth.row_bytes(qtype, d)
+    wbuf = dev.alloc(wbytes * copies)
+    dev.write(wbuf, synth.weights(1, n, d, qtype))
+    for c in range(1, copies):
+        dev.copy(wbuf.ptr + c * wbytes, wbuf.ptr, wbytes)
+    out = {}
+    for nt in (1, 4):
+        xb = dev.upload(synth.normal(2, (nt, d)))
+        yb = dev.alloc(nt * n * 4)
+        launch = lambda i: dev.gemv(qtype, wbuf.ptr + (i % copies) * wbytes, xb.ptr, yb.ptr,  # noqa: E731
+                                    n, d, nt)
+        for i in range(warmup):
+            launch(i)
+        dev.sync()
+        ms = graph_ms(dev, launch, steps if nt == 1 else max(steps // 2, 20))
+        alg = gemv_alg_bytes(qtype, n, d, nt)
+        out[nt] = dict(ms_per_step=ms, weight_gbps=wbytes / (ms / 1e3) / 1e9, alg_bytes=alg,
+                       achieved_gbps=alg / (ms / 1e3) / 1e9)
+    sink = dev.alloc(16)
+    rd = lambda i: dev.read_kernel(wbuf.ptr + (i % copies) * wbytes, wbytes, sink.ptr)  # noqa: E731
+    for i in range(warmup):
+        rd(i)
+    dev.sync()
+    ms = graph_ms(dev, rd, steps)
+    out["read"] = dict(ms_per_step=ms, bytes=wbytes, gbps=wbytes / (ms / 1e3) / 1e9)
+    wbuf.free()
+    return out
+
+
+def bench_sweep(dev, types, warmup, pool_bytes=600 << 20, max_steps=2048):
+    """Every (type, shape, tokens) of the Q8_0 and K-quant GEMV configs.  Each
+    type's weights fill a pool of > 590 MB (copies of its largest matrix); a
+    launch reads n rows at a row-aligned offset, consecutive launches at
+    consecutive offsets, so one replay streams the whole pool once."""
+    res = {}
+    for qtype in types:
+        for d in (2048, 5632):
+            shapes = [(n, dd) for (n, dd) in TINYLLAMA if dd == d]
+            if qtype != Q.TYPE_Q8_0 and d == 2048:
+                shapes.append((32000, 2048))  # the K-quant sweep's lm_head
+            nmax = max(n for n, _ in shapes)
+            rb = synth.row_bytes(qtype, d)
+            W = synth.weights(100 + qtype + d, nmax, d, qtype)
+            copies = max(1, math.ceil(pool_bytes / W.nbytes))
+            pool = dev.alloc(W.nbytes * copies)
+            dev.write(pool, W)
+            for c in range(1, copies):
+                dev.copy(pool.ptr + c * W.nbytes, pool.ptr, W.nbytes)
+            prows = nmax * copies
+            for n, _ in shapes:
+                for nt in ((1,) if qtype == Q.TYPE_Q8_0 else (1, 4)):
+                    nmat = prows // n  # row-aligned matrices in the pool
+                    wb = n * rb
+                    steps = int(min(max(64, nmat), max_steps))
+                    xb = dev.upload(synth.normal(3 + nt, (nt, d)))
+                    yb = dev.alloc(nt * n * 4)
+                    launch = lambda i: dev.gemv(qtype, pool.ptr + (i % nmat) * wb, xb.ptr,  # noqa: E731
+                                                yb.ptr, n, d, nt)
+                    for i in range(warmup):
+                        launch(i)
+                    dev.sync()
+                    ms = graph_ms(dev, launch, steps, reps=3)
+                    alg = gemv_alg_bytes(qtype, n, d, nt)
+                    key = "%s_%dx%d_t%d" % (TNAME[qtype], n, d, nt)
+                    res[key] = dict(us=round(ms * 1e3, 3),
+                                    weight_gbps=round(wb / (ms / 1e3) / 1e9, 1),
+                                    alg_bytes=alg,
+                                    achieved_gbps=round(alg / (ms / 1e3) / 1e9, 1),
+                                    frac=round(alg / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+                                    launches=steps)
+                    log("bench: %-22s %8.2f us  %7.0f GB/s  frac %.3f" % (
+                        key, ms * 1e3, alg / (ms / 1e3) / 1e9, res[key]["frac"]))
+                    xb.free()
+                    yb.free()
+            pool.free()
+    return res
+
+
 # ---------------------------------------------------------------------------
-# MoE layer
+# MoE layers
 # ---------------------------------------------------------------------------
 QWEN3 = dict(dim=2048, hidden=768, E=128, K=8)
+QWEN15 = dict(dim=2048, hidden=1408, E=60, K=4, sh=5632)
 
 
 def build_qwen3(dev, layers):
     dim, hidden, E, K = QWEN3["dim"], QWEN3["hidden"], QWEN3["E"], QWEN3["K"]
     t0 = time.time()
     router, u, _ = synth.zipf_router(3000, E, dim)
-    parts = [synth.weights(3001, E * hidden, dim, Q.TYPE_Q4_K),
+    parts = [router,
+             synth.weights(3001, E * hidden, dim, Q.TYPE_Q4_K),
              synth.weights(3002, E * hidden, dim, Q.TYPE_Q4_K),
              synth.weights(3003, E * dim, hidden, Q.TYPE_Q6_K)]
     log("bench: Qwen3 layer weights built in %.1fs" % (time.time() - t0))
-    sizes = [p.nbytes for p in parts]
-    per_layer = sum(sizes)
+    offs = np.cumsum([0] + [p.nbytes for p in parts])
+    per_layer = int(offs[-1])
     slab = dev.alloc(per_layer * layers)
-    off = 0
-    for p in parts:
-        dev.write(slab, p, off)
-        off += p.nbytes
+    for p, o in zip(parts, offs):
+        dev.write(slab, p, int(o))
     for l in range(1, layers):
         dev.copy(slab.ptr + l * per_layer, slab.ptr, per_layer)
-    rbuf = dev.upload(router)
     Ls = []
     for l in range(layers):
-        base = slab.ptr + l * per_layer
-        Ls.append(Q.MoeLayer(dim, hidden, E, K, rbuf.ptr, base, base + sizes[0],
-                             base + sizes[0] + sizes[1], Q.TYPE_Q4_K, Q.TYPE_Q4_K, Q.TYPE_Q6_K))
-    expert_bytes = sum(sizes) // E
-    return dict(layers=Ls, slab=slab, rbuf=rbuf, u=u, router=router, parts=parts,
-                expert_bytes=expert_bytes, per_layer=per_layer)
+        b = slab.ptr + l * per_layer
+        Ls.append(Q.MoeLayer(dim, hidden, E, K, b, b + int(offs[1]), b + int(offs[2]),
+                             b + int(offs[3]), Q.TYPE_Q4_K, Q.TYPE_Q4_K, Q.TYPE_Q6_K))
+    expert_bytes = (per_layer - router.nbytes) // E
+    return dict(layers=Ls, slab=slab, u=u, parts=parts, expert_bytes=expert_bytes,
+                per_layer=per_layer, shape=QWEN3, shared_bytes=0)
 
 
-def moe_alg_bytes(T, touched, expert_bytes):
-    dim, E = QWEN3["dim"], QWEN3["E"]
-    return 4 * E * dim + touched * expert_bytes + 2 * 4 * T * dim
+def build_qwen15(dev, layers):
+    dim, hidden, E, K, SH = (QWEN15[k] for k in ("dim", "hidden", "E", "K", "sh"))
+    t0 = time.time()
+    parts = [synth.normal(4000, (E, dim), 0.02),
+             synth.weights(4001, E * hidden, dim, Q.TYPE_Q4_K),
+             synth.weights(4002, E * hidden, dim, Q.TYPE_Q4_K),
+             synth.weights(4003, E * dim, hidden, Q.TYPE_Q8_0),
+             synth.normal(4004, (dim,), 0.02),
+             synth.weights(4005, SH, dim, Q.TYPE_Q4_K),
+             synth.weights(4006, SH, dim, Q.TYPE_Q4_K),
+             synth.weights(4007, dim, SH, Q.TYPE_Q4_K)]
+    log("bench: Qwen1.5 layer weights built in %.1fs" % (time.time() - t0))
+    offs = np.cumsum([0] + [(p.nbytes + 255) // 256 * 256 for p in parts])
+    per_layer = int(offs[-1])
+    slab = dev.alloc(per_layer * layers)
+    for p, o in zip(parts, offs):
+        dev.write(slab, p, int(o))
+    for l in range(1, layers):
+        dev.copy(slab.ptr + l * per_layer, slab.ptr, per_layer)
+    Ls = []
+    for l in range(layers):
+        b = [slab.ptr + l * per_layer + int(o) for o in offs[:-1]]
+        L = Q.MoeLayer(dim, hidden, E, K, b[0], b[1], b[2], b[3], Q.TYPE_Q4_K, Q.TYPE_Q4_K,
+                       Q.TYPE_Q8_0)
+        L.sh_hidden = SH
+        L.sh_gate_inp, L.sh_up, L.sh_gate, L.sh_down = b[4], b[5], b[6], b[7]
+        L.sh_up_type = L.sh_gate_type = L.sh_down_type = Q.TYPE_Q4_K
+        Ls.append(L)
+    expert_bytes = sum(p.nbytes for p in parts[1:4]) // E
+    shared_bytes = sum(p.nbytes for p in parts[4:])
+    return dict(layers=Ls, slab=slab, u=None, parts=parts, expert_bytes=expert_bytes,
+                per_layer=per_layer, shape=QWEN15, shared_bytes=shared_bytes)
 
 
-def bench_moe(dev, M, T, steps, warmup, nbatches=8, order=Q.ORDER_AVX2):
-    dim, E, K = QWEN3["dim"], QWEN3["E"], QWEN3["K"]
+def moe_alg_bytes(M, T, touched):
+    """Router + touched experts + shared expert + activations in and out."""
+    sh = M["shape"]
+    return 4 * sh["E"] * sh["dim"] + touched * M["expert_bytes"] + M["shared_bytes"] + \
+        2 * 4 * T * sh["dim"]
+
+
+def bench_moe(dev, M, T, steps, warmup, order, nbatches=8, seed=7000):
+    sh = M["shape"]
+    dim, E, K = sh["dim"], sh["E"], sh["K"]
     Ls = M["layers"]
-    xb_all = np.concatenate([synth.zipf_tokens(7000 + 31 * T + b, T, dim, M["u"])
-                             for b in range(nbatches)])
+    if M["u"] is not None:
+        xb_all = np.concatenate([synth.zipf_tokens(seed + 31 * T + b, T, dim, M["u"])
+                                 for b in range(nbatches)])
+    else:
+        xb_all = synth.normal(seed + 31 * T, (nbatches * T, dim))
     xbb = dev.upload(xb_all)
-    xs = dev.upload(synth.normal(7500 + T, (nbatches * T, dim)))
+    xs = dev.upload(synth.normal(seed + 500 + T, (nbatches * T, dim)))
     # routing of each batch (for the algorithmic byte count: touched experts)
     idxb, wtb = dev.alloc(nbatches * T * K * 4), dev.alloc(nbatches * T * K * 4)
     dev.moe_route(Ls[0], xbb.ptr, nbatches * T, order, None, idxb.ptr, wtb.ptr)
     idx = dev.download(idxb, (nbatches, T * K), np.int32)
     touched = float(np.mean([np.unique(r).size for r in idx]))
     counts = np.bincount(idx[0], minlength=E)
-    step_bytes = moe_alg_bytes(T, touched, M["expert_bytes"])
+    step_bytes = moe_alg_bytes(M, T, touched)
 
     def one(i):
         b = i % nbatches
@@ -187,80 +299,71 @@ def bench_moe(dev, M, T, steps, warmup, nbatches=8, order=Q.ORDER_AVX2):
     for i in range(max(warmup, 1)):
         one(i)
     dev.sync()
-    g = dev.capture(lambda: [one(i) for i in range(steps)])
-    dev.graph_launch(g)
-    dev.sync()
-    ms = timed_replays(dev, g)
-    dev.graph_destroy(g)
-    s = ms / 1e3 / steps
-    return dict(T=T, ms_per_step=ms / steps, tokens_per_s=T / s,
-                touched_experts=touched, max_tokens_per_expert=int(counts.max()),
-                alg_bytes=int(step_bytes), achieved_gbps=step_bytes / s / 1e9,
+    ms = graph_ms(dev, one, steps)
+    s = ms / 1e3
+    return dict(T=T, ms_per_step=ms, tokens_per_s=T / s, touched_experts=touched,
+                max_tokens_per_expert=int(counts.max()), alg_bytes=int(step_bytes),
+                achieved_gbps=step_bytes / s / 1e9,
                 roofline_frac=step_bytes / s / 1e9 / HBM_PEAK_GBPS)
 
 
 # ---------------------------------------------------------------------------
 # CPU baseline: the reference's own code on this host
 # ---------------------------------------------------------------------------
-def cpu_baseline_gemv(seconds, cores):
+def thread_counts(cpus):
+    return sorted({1, min(8, cpus), cpus})
+
+
+def cpu_baseline_gemv(cpus, reps=30, copies=16):
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as O
     n, d = 32000, 2048
-    try:
-        ref = O.RefLib("avx2")
-        kind = "reference"
-        call = lambda out, x, w: ref.lib.matmul_q_fused(out, x, w.ctypes.data_as(O.C.c_void_p),  # noqa: E731
-                                                         12, n, d, cores)
-    except FileNotFoundError:
-        orc = O.Oracle()
-        kind = "port"
-        call = lambda out, x, w: orc.lib.qro_matmul_q_fused_batch(  # noqa: E731
-            out, x, w.ctypes.data_as(O.C.c_void_p), 12, n, d, 1, cores, O.ORDER_SEQ)
-    copies = 8  # 296 MB of weights: beyond the host's last-level cache
-    Ws = [synth.weights(90 + c, n, d, Q.TYPE_Q4_K) for c in range(copies)]
+    ref = O.RefLib("avx2")
+    W = synth.weights(90, n, d, Q.TYPE_Q4_K)
+    Ws = [W] + [W.copy() for _ in range(copies - 1)]  # 590 MB: beyond the host's caches
     x = synth.normal(91, (d,))
-    out = np.zeros(n, np.float32)
-    call(out, x, Ws[0])  # warm-up
-    t0 = time.perf_counter()
-    calls = 0
-    while time.perf_counter() - t0 < seconds or calls < 3:
-        call(out, x, Ws[calls % copies])
-        calls += 1
-    dt = (time.perf_counter() - t0) / calls
-    wbytes = n * synth.row_bytes(Q.TYPE_Q4_K, d)
-    return dict(value=wbytes / dt / 1e9, unit="GB/s", cores=cores, kind=kind,
-                sample="%d calls of matmul_q_fused Q4_K 32000x2048 over 8 weight copies (%s, "
-                       "-O3 -std=c99 -mavx2 -mfma, OpenMP %d threads, %s); the reference's "
-                       "Q4_K dot returns invalid values but does the same work"
-                       % (calls, "oracle/_ref" if kind == "reference" else "oracle port", cores,
-                          cpu_model()),
-                ms_per_call=dt * 1e3)
+    wbytes = W.nbytes
+    by = {}
+    for th in thread_counts(cpus):
+        t = ref.gemv_bench(x, Ws, Q.TYPE_Q4_K, n, d, th, 3, reps)
+        by[th] = dict(gbps=round(wbytes / float(np.median(t)) / 1e9, 2),
+                      ms=round(float(np.median(t)) * 1e3, 3))
+        log("bench: CPU matmul_q_fused Q4_K 32000x2048, %d threads: %.1f GB/s (%.2f ms)"
+            % (th, by[th]["gbps"], by[th]["ms"]))
+    return dict(value=by[cpus]["gbps"], unit="GB/s", cores=cpus, kind="reference",
+                sample="matmul_q_fused Q4_K 32000x2048 (oracle/_ref: the reference's sources, "
+                       "-O3 -std=c99 -mavx2 -mfma, OpenMP), 16 rotating weight copies (590 MB), "
+                       "3 warm-ups then the median of %d calls per thread count; %s, %d CPUs "
+                       "available to this process of %d; the reference's Q4_K dot returns "
+                       "invalid values but does the same work" % (reps, cpu_model(), cpus,
+                                                                  os.cpu_count() or 0),
+                by_threads={str(k): v for k, v in by.items()})
 
 
-def cpu_baseline_moe(M, tokens, cores):
+def cpu_baseline_moe(M, cpus, reps=24, copies=4):
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as O
-    dim, hidden, E, K = QWEN3["dim"], QWEN3["hidden"], QWEN3["E"], QWEN3["K"]
-    up, gate, down = M["parts"]
-    x = synth.zipf_tokens(9000, tokens, dim, M["u"])
-    try:
-        ref = O.RefLib("avx2")
-        t0 = time.perf_counter()
-        ref.moe_layer(x, dim, hidden, E, K, M["router"], up, Q.TYPE_Q4_K, gate, Q.TYPE_Q4_K,
-                      down, Q.TYPE_Q6_K, backend=O.BACKEND_AVX2, threads=cores)
-        kind = "reference"
-    except FileNotFoundError:
-        orc = O.Oracle()
-        keep = []
-        L = orc.make_layer(keep, dim, hidden, E, K, M["router"], up, Q.TYPE_Q4_K, gate,
-                           Q.TYPE_Q4_K, down, Q.TYPE_Q6_K)
-        t0 = time.perf_counter()
-        orc.moe_forward(x, x, L, order=O.ORDER_AVX2, threads=cores)
-        kind = "port"
-    dt = time.perf_counter() - t0
-    return dict(value=tokens / dt, unit="tokens/s", cores=cores, kind=kind,
-                sample="%d tokens through forward_runtime's MoE block, one token per call as "
-                       "the reference runs them (Qwen3 shape, %d OpenMP threads)" % (tokens, cores))
+    sh = M["shape"]
+    dim, hidden, E, K = sh["dim"], sh["hidden"], sh["E"], sh["K"]
+    router, up, gate, down = M["parts"][:4]
+    ref = O.RefLib("avx2")
+    cp = lambda a: [a] + [a.copy() for _ in range(copies - 1)]  # noqa: E731
+    R, U, G, D = cp(router), cp(up), cp(gate), cp(down)
+    x = synth.zipf_tokens(9000, 16, dim, M["u"])
+    by = {}
+    for th in thread_counts(cpus):
+        t = ref.moe_bench(x, dim, hidden, E, K, R, U, Q.TYPE_Q4_K, G, Q.TYPE_Q4_K, D,
+                          Q.TYPE_Q6_K, O.BACKEND_AVX2, th, 3, reps)
+        med = float(np.median(t))
+        by[th] = dict(tokens_per_s=round(1.0 / med, 1), ms_per_token=round(med * 1e3, 3))
+        log("bench: CPU MoE block (Qwen3 shape), %d threads: %.1f tokens/s (%.2f ms per token)"
+            % (th, 1.0 / med, med * 1e3))
+    return dict(value=by[cpus]["tokens_per_s"], unit="tokens/s", cores=cpus, kind="reference",
+                sample="forward_runtime's MoE block (oracle/_ref, CI flags, OpenMP), one token per "
+                       "call as the reference runs tokens (so T = 1, 16 and 512 share this rate), "
+                       "layer weights rotating over %d copies (1.6 GB), set-up outside the timed "
+                       "region, 3 warm-ups then the median of %d calls" % (copies, reps),
+                by_threads={str(k): v for k, v in by.items()})
 
 
 # ---------------------------------------------------------------------------
@@ -281,14 +384,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--sweep-types", default="Q8_0,Q4_K,Q5_K,Q6_K")
     ap.add_argument("--moe-layers", type=int, default=48)
     ap.add_argument("--moe-t", default="1,16,512",
-                    help="token counts of the MoE leg (comma-separated), e.g. 16 for a profile")
+                    help="token counts of the Qwen3 MoE leg (comma-separated)")
     ap.add_argument("--moe-steps", type=int, default=0,
                     help="layers timed per token count (0: the defaults, 100 / 100 / 20)")
+    ap.add_argument("--no-qwen15", action="store_true")
     ap.add_argument("--no-gemv", action="store_true",
-                    help="skip the GEMV headline (profiling runs of the MoE leg; value is null)")
+                    help="skip the GEMV headline (profiling runs of other legs; value is null)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: there is no multi-GPU path; run with --gpus 1",
@@ -298,48 +403,66 @@ def main():
     dev = Q.Device(0)
     cal = copy_calibration(dev)
     log("bench: copy kernel %.0f GB/s (read+write) over %d MB" % (cal["gbps"], cal["bytes"] >> 20))
-    g = g4 = None
+    h = None
     if not args.no_gemv:
-        g = bench_gemv(dev, Q.TYPE_Q4_K, 32000, 2048, 1, args.steps, args.warmup)
+        h = bench_headline(dev, args.steps, args.warmup)
+        g, g4, rd = h[1], h[4], h["read"]
         log("bench: Q4_K 32000x2048 T=1: %.3f us/launch, %.0f GB/s weights, %.0f GB/s algorithmic"
             % (g["ms_per_step"] * 1e3, g["weight_gbps"], g["achieved_gbps"]))
-        # the same GEMV for 4 tokens (the survey's K-quant config at NT = 4): not the headline
-        g4 = bench_gemv(dev, Q.TYPE_Q4_K, 32000, 2048, 4, max(args.steps // 2, 20), args.warmup)
+        log("bench: plain read of the same %d bytes: %.3f us, %.0f GB/s" % (
+            rd["bytes"], rd["ms_per_step"] * 1e3, rd["gbps"]))
         log("bench: Q4_K 32000x2048 T=4: %.3f us/launch, %.0f GB/s weights"
             % (g4["ms_per_step"] * 1e3, g4["weight_gbps"]))
 
-    moe = None
+    sweep = None
+    if not args.no_sweep:
+        names = {v: k for k, v in TNAME.items()}
+        types = [names[t.strip()] for t in args.sweep_types.split(",") if t.strip()]
+        sweep = bench_sweep(dev, types, min(args.warmup, 5))
+
+    moe = moe15 = None
+    M = None
     if not args.no_moe:
         M = build_qwen3(dev, args.moe_layers)
         moe = {}
         default_steps = {1: max(args.steps, 100), 16: 100, 512: 20}
         for T in [int(t) for t in args.moe_t.split(",") if t.strip()]:
             steps = args.moe_steps or default_steps.get(T, 20)
-            r = bench_moe(dev, M, T, steps, 3)
+            r = bench_moe(dev, M, T, steps, 3, Q.ORDER_AVX2)
             moe["T%d" % T] = r
             log("bench: MoE Qwen3 T=%d: %.1f us/layer, %.0f tokens/s, %.1f experts touched, "
                 "%.0f GB/s (%.1f%% of HBM peak)" % (T, r["ms_per_step"] * 1e3, r["tokens_per_s"],
                                                    r["touched_experts"], r["achieved_gbps"],
                                                    100 * r["roofline_frac"]))
+        M["slab"].free()
+        if not args.no_qwen15:
+            M15 = build_qwen15(dev, 8)
+            moe15 = {}
+            for T, steps in ((1, 100), (64, 40)):
+                r = bench_moe(dev, M15, T, steps, 3, Q.ORDER_SEQ, seed=8000)
+                moe15["T%d" % T] = r
+                log("bench: MoE Qwen1.5 T=%d: %.1f us/layer, %.0f tokens/s, %.1f experts touched, "
+                    "%.0f GB/s (%.1f%% of HBM peak)" % (T, r["ms_per_step"] * 1e3,
+                                                       r["tokens_per_s"], r["touched_experts"],
+                                                       r["achieved_gbps"],
+                                                       100 * r["roofline_frac"]))
+            M15["slab"].free()
 
-    cores = host_cores()
+    cpus = host_cpus()
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline_gemv(args.cpu_seconds, cores)
-        log("bench: CPU baseline %.1f GB/s (%s, %d cores)" % (cpu["value"], cpu["kind"], cores))
-        if moe is not None:
-            cpu_moe = cpu_baseline_moe(M, 16, cores)
-            moe["cpu_baseline"] = cpu_moe
-            log("bench: CPU MoE baseline %.1f tokens/s (%s)" % (cpu_moe["value"], cpu_moe["kind"]))
+        cpu = cpu_baseline_gemv(cpus)
+        if M is not None:
+            moe["cpu_baseline"] = cpu_baseline_moe(M, cpus)
 
     out = {
         "metric": METRIC,
-        "value": round(g["weight_gbps"], 2) if g else None,
+        "value": round(h[1]["weight_gbps"], 2) if h else None,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(g["ms_per_step"], 6) if g else None,
+        "ms_per_step": round(h[1]["ms_per_step"], 6) if h else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -348,16 +471,25 @@ def main():
         "config": {"workload": "Q4_K decode GEMV 32000x2048 (lm_head of the K-quant sweep), "
                                "1 token, 16 rotating weight copies", "n": 32000, "d": 2048,
                    "qtype": "Q4_K", "tokens": 1},
-        "roofline": {"bound": "hbm", "achieved": round(g["achieved_gbps"], 2),
+        "roofline": {"bound": "hbm", "achieved": round(h[1]["achieved_gbps"], 2),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(g["achieved_gbps"] / HBM_PEAK_GBPS, 4),
-                     "traffic": load_traffic()} if g else None,
+                     "frac": round(h[1]["achieved_gbps"] / HBM_PEAK_GBPS, 4),
+                     "traffic": load_traffic(),
+                     "read_ceiling": {
+                         "note": "a plain read of the same weight bytes, 16 rotating copies",
+                         "us": round(h["read"]["ms_per_step"] * 1e3, 3),
+                         "gbps": round(h["read"]["gbps"], 1),
+                         "gemv_over_read": round(h["read"]["ms_per_step"] / h[1]["ms_per_step"],
+                                                 4)}} if h else None,
         "cpu_baseline": cpu,
         "gemv_q4k_32000x2048_t4": {
-            "ms_per_step": round(g4["ms_per_step"], 6), "weight_gbps": round(g4["weight_gbps"], 2),
-            "alg_bytes": g4["alg_bytes"], "achieved_gbps": round(g4["achieved_gbps"], 2),
-            "roofline_frac": round(g4["achieved_gbps"] / HBM_PEAK_GBPS, 4)} if g else None,
+            "ms_per_step": round(h[4]["ms_per_step"], 6),
+            "weight_gbps": round(h[4]["weight_gbps"], 2), "alg_bytes": h[4]["alg_bytes"],
+            "achieved_gbps": round(h[4]["achieved_gbps"], 2),
+            "roofline_frac": round(h[4]["achieved_gbps"] / HBM_PEAK_GBPS, 4)} if h else None,
+        "gemv_sweep": sweep,
         "moe_qwen3": moe,
+        "moe_qwen15": moe15,
         "copy_kernel_gbps": round(cal["gbps"], 1),
     }
     print(json.dumps(out), flush=True)

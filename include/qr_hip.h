@@ -104,6 +104,10 @@ int qr_graph_destroy(void* graph);
 /* A plain streaming copy kernel (dst = src, 16-byte chunks): the reference
  * point for hardware byte counters. */
 int qr_copy_kernel(qr_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* A plain streaming read of `bytes` (16-byte chunks, each read once): the
+ * achievable rate for a kernel that reads the same bytes once.  sink is a
+ * 4-byte device word it may write. */
+int qr_read_kernel(qr_ctx* ctx, const void* src, size_t bytes, void* sink);
 
 /* ---- quantized GEMV ------------------------------------------------------ */
 

@@ -257,6 +257,14 @@ class RefLib:
             L.refgpu_bind.argtypes = [C.c_int]
             L.refgpu_take_calls.restype = C.c_int
             L.refgpu_take_calls.argtypes = []
+        L.refdrv_moe_bench.restype = C.c_int
+        L.refdrv_moe_bench.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                       C.c_int, C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p,
+                                       C.c_uint32, C.c_void_p, C.c_uint32, C.c_int, C.c_int,
+                                       C.c_int, C.c_int, C.c_void_p]
+        L.refdrv_gemv_bench.restype = C.c_int
+        L.refdrv_gemv_bench.argtypes = [_f32p, C.c_void_p, C.c_int, C.c_uint32, C.c_int, C.c_int,
+                                        C.c_int, C.c_int, C.c_int, _f32p, C.c_void_p]
         L.refdrv_moe_layer.restype = C.c_int
         L.refdrv_moe_layer.argtypes = [_f32p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
                                        C.c_int, C.c_int, _f32p, C.c_void_p, C.c_uint32,
@@ -319,3 +327,30 @@ class RefLib:
         if rc != 0:
             raise RuntimeError("refdrv_moe_layer failed: %d" % rc)
         return xb, xo
+
+    def moe_bench(self, x_in, dim, hidden, E, K, routers, ups, up_type, gates, gate_type, downs,
+                  down_type, backend, threads, warmup, reps):
+        """Seconds of each timed forward_runtime call over len(ups) MoE layers."""
+        x_in = np.ascontiguousarray(x_in, np.float32)
+        L = len(ups)
+        arr = lambda bufs: (C.c_void_p * L)(*[b.ctypes.data for b in bufs])  # noqa: E731
+        times = np.zeros(reps, np.float64)
+        rc = self.lib.refdrv_moe_bench(x_in, x_in.shape[0], dim, hidden, E, K, L, arr(routers),
+                                       arr(ups), up_type, arr(gates), gate_type, arr(downs),
+                                       down_type, backend, threads, warmup, reps,
+                                       times.ctypes.data_as(C.c_void_p))
+        if rc != 0:
+            raise RuntimeError("refdrv_moe_bench failed: %d" % rc)
+        return times
+
+    def gemv_bench(self, x, copies, qtype, n, d, threads, warmup, reps):
+        """Seconds of each timed matmul_q_fused call, rotating over `copies`."""
+        ptrs = (C.c_void_p * len(copies))(*[c.ctypes.data for c in copies])
+        out = np.zeros(n, np.float32)
+        times = np.zeros(reps, np.float64)
+        rc = self.lib.refdrv_gemv_bench(np.ascontiguousarray(x, np.float32), ptrs, len(copies),
+                                        qtype, n, d, threads, warmup, reps, out,
+                                        times.ctypes.data_as(C.c_void_p))
+        if rc != 0:
+            raise RuntimeError("refdrv_gemv_bench failed: %d" % rc)
+        return times

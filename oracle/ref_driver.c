@@ -10,8 +10,10 @@
  * in-memory Transformer.  Nothing here computes; every number comes from the
  * reference's own code.
  */
+#define _POSIX_C_SOURCE 199309L
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #include "kernels.h"
 #include "model.h"
@@ -174,5 +176,157 @@ int refdrv_moe_layer(const float* x_in, float* xb_out, float* x_out, int T, int 
     free(ew1[0]);
     free(ew2[0]);
     free(ew3[0]);
+    return 0;
+}
+
+/*
+ * Timing of the reference's MoE block for the CPU baseline: a one-layer model
+ * whose layer weights rotate over `nlayers` copies (copy l: router_l[l],
+ * up_l[l], gate_l[l], down_l[l], each an [E][rows][cols] tensor), built once
+ * outside the timed region (malloc_run_state and runtime_init included), then
+ * `warmup` untimed and `reps` timed forward_runtime calls; call i runs copy
+ * i % nlayers on token row x_in[i % T].  times[r] receives call r's
+ * CLOCK_MONOTONIC seconds.  One layer per call, fed from the embedding row:
+ * the reference's Q4_K dot returns invalid values, which a second layer's
+ * router would turn into an out-of-range expert index.
+ */
+int refdrv_moe_bench(const float* x_in, int T, int dim, int hidden, int E, int K, int nlayers,
+                     const float* const* router_l, const void* const* up_l, uint32_t up_type,
+                     const void* const* gate_l, uint32_t gate_type, const void* const* down_l,
+                     uint32_t down_type, int backend, int threads, int warmup, int reps,
+                     double* times) {
+    Transformer t;
+    RuntimeContext rt;
+    RuntimeOptions opt;
+    float *ones, **rms, **nulls, **router;
+    float ***ew1, ***ew2, ***ew3;
+    uint32_t *t_up, *t_down, *t_gate;
+    size_t s_up, s_gate, s_down;
+    int l, e, i;
+    struct timespec a, b;
+
+    if (E > 256 || K > 16 || K > E || nlayers < 1 || T < 1) return -1;
+    memset(&t, 0, sizeof(t));
+    t.config.dim = dim;
+    t.config.hidden_dim = hidden;
+    t.config.n_layers = 1;
+    t.config.n_heads = 1;
+    while (dim / t.config.n_heads > 512 || dim % t.config.n_heads) t.config.n_heads++;
+    t.config.n_kv_heads = t.config.n_heads;
+    t.config.vocab_size = 1;
+    t.config.seq_len = 1;
+    t.config.rope_freq_base = 10000.0f;
+    t.config.expert_count = E;
+    t.config.expert_used_count = K;
+
+    ones = (float*)malloc((size_t)dim * sizeof(float));
+    rms = (float**)malloc((size_t)nlayers * sizeof(float*));
+    nulls = (float**)calloc((size_t)nlayers, sizeof(float*));
+    router = (float**)malloc((size_t)nlayers * sizeof(float*));
+    ew1 = (float***)malloc((size_t)nlayers * sizeof(float**));
+    ew2 = (float***)malloc((size_t)nlayers * sizeof(float**));
+    ew3 = (float***)malloc((size_t)nlayers * sizeof(float**));
+    t_up = (uint32_t*)malloc((size_t)nlayers * sizeof(uint32_t));
+    t_down = (uint32_t*)malloc((size_t)nlayers * sizeof(uint32_t));
+    t_gate = (uint32_t*)malloc((size_t)nlayers * sizeof(uint32_t));
+    if (!ones || !rms || !nulls || !router || !ew1 || !ew2 || !ew3 || !t_up || !t_down || !t_gate)
+        return -2;
+    for (i = 0; i < dim; i++) ones[i] = 1.0f;
+    s_up = (up_type == 8 ? (size_t)(dim / 32) * 34 : up_type == 12 ? (size_t)(dim / 256) * 144
+            : up_type == 13 ? (size_t)(dim / 256) * 176 : (size_t)(dim / 256) * 210) * (size_t)hidden;
+    s_gate = (gate_type == 8 ? (size_t)(dim / 32) * 34 : gate_type == 12 ? (size_t)(dim / 256) * 144
+              : gate_type == 13 ? (size_t)(dim / 256) * 176 : (size_t)(dim / 256) * 210) * (size_t)hidden;
+    s_down = (down_type == 8 ? (size_t)(hidden / 32) * 34 : down_type == 12 ? (size_t)(hidden / 256) * 144
+              : down_type == 13 ? (size_t)(hidden / 256) * 176 : (size_t)(hidden / 256) * 210) * (size_t)dim;
+    for (l = 0; l < nlayers; l++) {
+        rms[l] = ones;
+        router[l] = (float*)router_l[l];
+        ew1[l] = (float**)malloc((size_t)E * sizeof(float*));
+        ew2[l] = (float**)malloc((size_t)E * sizeof(float*));
+        ew3[l] = (float**)malloc((size_t)E * sizeof(float*));
+        if (!ew1[l] || !ew2[l] || !ew3[l]) return -2;
+        for (e = 0; e < E; e++) {
+            ew1[l][e] = (float*)((const char*)up_l[l] + (size_t)e * s_up);
+            ew3[l][e] = (float*)((const char*)gate_l[l] + (size_t)e * s_gate);
+            ew2[l][e] = (float*)((const char*)down_l[l] + (size_t)e * s_down);
+        }
+        t_up[l] = up_type;
+        t_down[l] = down_type;
+        t_gate[l] = gate_type;
+    }
+    t.weights.token_embedding_table = (float*)x_in;
+    t.weights.token_embd_type = 0;
+    t.weights.token_embd_row_bytes = (size_t)dim * sizeof(float);
+    t.weights.rms_att_weight = rms;
+    t.weights.rms_ffn_weight = rms;
+    t.weights.wq = nulls;
+    t.weights.wk = nulls;
+    t.weights.wv = nulls;
+    t.weights.wo = nulls;
+    t.weights.rms_final_weight = ones;
+    t.weights.wcls = NULL;
+    t.weights.ffn_gate_inp = router;
+    t.weights.expert_w1 = ew1;
+    t.weights.expert_w2 = ew2;
+    t.weights.expert_w3 = ew3;
+    t.weights.exp_w1_type = t_up;
+    t.weights.exp_w2_type = t_down;
+    t.weights.exp_w3_type = t_gate;
+    malloc_run_state(&t.state, &t.config);
+    memset(&opt, 0, sizeof(opt));
+    opt.backend = (KernelBackend)backend;
+    opt.num_threads = threads;
+    runtime_init(&rt, opt);
+
+    for (i = 0; i < warmup + reps; i++) {
+        l = i % nlayers;  /* the layer's weights: copy l */
+        t.weights.ffn_gate_inp = router + l;
+        t.weights.expert_w1 = ew1 + l;
+        t.weights.expert_w2 = ew2 + l;
+        t.weights.expert_w3 = ew3 + l;
+        t.weights.exp_w1_type = t_up + l;
+        t.weights.exp_w2_type = t_down + l;
+        t.weights.exp_w3_type = t_gate + l;
+        clock_gettime(CLOCK_MONOTONIC, &a);
+        forward_runtime(&rt, &t, i % T, 0);
+        clock_gettime(CLOCK_MONOTONIC, &b);
+        if (i >= warmup)
+            times[i - warmup] = (double)(b.tv_sec - a.tv_sec) + 1e-9 * (double)(b.tv_nsec - a.tv_nsec);
+    }
+
+    free_run_state(&t.state);
+    for (l = 0; l < nlayers; l++) {
+        free(ew1[l]);
+        free(ew2[l]);
+        free(ew3[l]);
+    }
+    free(ones);
+    free(rms);
+    free(nulls);
+    free(router);
+    free(ew1);
+    free(ew2);
+    free(ew3);
+    free(t_up);
+    free(t_down);
+    free(t_gate);
+    return 0;
+}
+
+/* CLOCK_MONOTONIC seconds of each of `reps` matmul_q_fused calls after
+ * `warmup` untimed ones; call i uses weight copy i % ncopies. */
+int refdrv_gemv_bench(const float* x, const void* const* w_copies, int ncopies, uint32_t type,
+                      int n, int d, int threads, int warmup, int reps, float* out,
+                      double* times) {
+    struct timespec a, b;
+    int i;
+    if (ncopies < 1) return -1;
+    for (i = 0; i < warmup + reps; i++) {
+        clock_gettime(CLOCK_MONOTONIC, &a);
+        matmul_q_fused(out, x, w_copies[i % ncopies], type, n, d, threads);
+        clock_gettime(CLOCK_MONOTONIC, &b);
+        if (i >= warmup)
+            times[i - warmup] = (double)(b.tv_sec - a.tv_sec) + 1e-9 * (double)(b.tv_nsec - a.tv_nsec);
+    }
     return 0;
 }

@@ -88,12 +88,20 @@ __device__ inline void act_prefetch(const float* __restrict__ x, size_t xstride,
   act_load8(x, xstride, nt, d, (int)threadIdx.x, pre.v);
 }
 
-// xs (optional): the activation already staged in LDS, group gi's 8 floats
-// at xs + 8 gi (see stage_act_dma); then every pass reads from there.  tid /
-// nthr (optional): the caller's index among the nthr threads that quantize
-// (a multiple of 64, so quads never straddle waves); default the whole
-// workgroup.
-template <bool NIB>
+// Where the fp32 values come from (a compile-time choice on purpose: a
+// function that may also issue global loads makes the compiler wait for all
+// vector memory operations before the values it reads -- vmcnt(0) -- which
+// would include the weight DMA a caller has in flight):
+//   kActGlobal  the first pass uses `pre`, later passes load from x;
+//   kActLds     the activation is staged in LDS at xs, group gi's 8 floats at
+//               xs + 8 gi (see stage_act_dma), and every pass reads there;
+//   kActRegs    one pass, from `pre` only (the caller guarantees that one
+//               pass covers the activation: nt * d / 8 <= nthr).
+// tid / nthr (optional): the caller's index among the nthr threads that
+// quantize (a multiple of 64, so quads never straddle waves); default the
+// whole workgroup.
+enum { kActGlobal = 0, kActLds = 1, kActRegs = 2 };
+template <bool NIB, int SRC = kActGlobal>
 __device__ inline void quantize_act_blk(const float* __restrict__ x, size_t xstride, int nt,
                                         int d, uint8_t* lds, const ActPre& pre,
                                         const float* xs = nullptr, int tid = -1, int nthr = 0) {
@@ -111,7 +119,10 @@ __device__ inline void quantize_act_blk(const float* __restrict__ x, size_t xstr
     const int t = live ? gi / per_tok : 0;
     const int g = live ? gi - t * per_tok : 0;
     float v[8];
-    if (xs) {
+    if constexpr (SRC == kActRegs) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = pre.v[i];
+    } else if constexpr (SRC == kActLds) {
       const float4* p = reinterpret_cast<const float4*>(xs + (size_t)(live ? gi : 0) * 8);
       const float4 u0 = p[0], u1 = p[1];
       v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w;
@@ -178,6 +189,7 @@ __device__ inline void quantize_act_blk(const float* __restrict__ x, size_t xstr
         reinterpret_cast<int*>(ab + 44)[0] = s;
       }
     }
+    if constexpr (SRC == kActRegs) break;
   }
 }
 

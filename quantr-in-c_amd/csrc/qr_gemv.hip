@@ -194,23 +194,27 @@ __global__ __launch_bounds__(64 * kStreamWaves) void k_gemv_stream(GemvArgs g) {
 // ---------------------------------------------------------------------------
 // Block-per-lane GEMV for Q4_K / Q5_K (qr_blk.h): each wave walks tiles of
 // RB = 64/nb rows with lane = super-block.  A tile's bytes come into the
-// wave's LDS slot by DMA (coalesced 1 KiB instructions), D tiles in flight per
-// wave; the lane reads its block from the slot, and the slot is refilled with
-// the tile D steps ahead before the lane's terms are formed.
+// wave's LDS slot by DMA (coalesced 1 KiB instructions), one tile in flight
+// per wave; the lane copies its block out of the slot, the slot is refilled
+// with the wave's next tile, and only then are the lane's terms formed, so the
+// next tile streams while this one is reduced.
 //
 // Start-up: the activation's DMA into an LDS staging area goes first (XS),
-// then the first D tiles' DMA; each wave then waits only for its own part of
-// the activation (loads complete in issue order: at most NCH x tiles-issued
-// operations still in flight) and the workgroup quantizes it from LDS, while
-// the weight stream is already on its way.  Without staging (large
-// activations) the activation is loaded into registers before the tile DMA.
+// then the first tile's DMA; each wave waits only for its own part of the
+// activation (loads complete in issue order: at most NCH operations -- the
+// tile's -- still in flight) and the workgroup quantizes it from LDS, while
+// the weight stream is already on its way.  The quantizer reads only LDS, so
+// the compiler has no vector load of its own to wait for and the tile DMA
+// stays in flight across it.  Without staging (large activations) the
+// activation is loaded into registers before the tile DMA.  ACC: the parity
+// mode (int32 unit sums written out).
 // ---------------------------------------------------------------------------
 template <int TYPE>
 __host__ __device__ constexpr size_t blk_slot_bytes() {
   return (size_t)64 * BlkFmt<TYPE>::kBytes;
 }
 
-template <int TYPE, int NT, int D, bool XS>
+template <int TYPE, int NT, bool XS, bool ACC>
 __global__ __launch_bounds__(64 * kBlkWaves) void k_gemv_blk(GemvArgs g) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int BB = BlkFmt<TYPE>::kBytes;
@@ -227,88 +231,88 @@ __global__ __launch_bounds__(64 * kBlkWaves) void k_gemv_blk(GemvArgs g) {
   const size_t tokb = act_tok_bytes(g.d);
   const int ntiles = (g.n + RB - 1) / RB;
   const int tstep = gridDim.x * kBlkWaves;
+  const size_t total = (size_t)g.n * rb;
   int tile = blockIdx.x * kBlkWaves + wave;
   const size_t tile_bytes = (size_t)RB * rb;
   const size_t xsb = XS ? blk_xs_bytes(g.d, NT) : 0;
   float* xs = reinterpret_cast<float*>(smem);
   uint8_t* act = smem + xsb;
-  uint8_t* slots = act + align16((size_t)NT * tokb) + (size_t)wave * D * SB;
+  uint8_t* slot = act + align16((size_t)NT * tokb) + (size_t)wave * SB;
+  const uint32_t sbase = lds_u32addr(slot);
 
-  auto dma = [&](int s, int t) {
-    if (t < ntiles) {
-      const int rows = min(RB, g.n - t * RB);
-      tile_dma<NCH>(g.W + (size_t)t * tile_bytes, slots + s * SB, rows * (int)rb, lane);
+  // DMA of tile t into the slot: NCH KiB (64 blocks) from the tile's start
+  // when they all lie inside the matrix (bytes past the tile's rows land in
+  // slot bytes that only lanes without a row read); otherwise lanes past the
+  // tile's end are clamped (tile_dma)
+  auto dma = [&](int t) {
+    if (t >= ntiles) return;
+    const uint8_t* src = g.W + (size_t)t * tile_bytes;
+    if ((size_t)t * tile_bytes + (size_t)NCH * 1024 <= total) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot's earlier reads are done
+#pragma unroll
+      for (int k = 0; k < NCH; k++)
+        lds_dma16_nt(src + k * 1024 + lane * 16, sbase + (uint32_t)(k * 1024));
+    } else {
+      tile_dma<NCH>(src, slot, (g.n - t * RB) * (int)rb, lane);
     }
   };
   ActPre pre;
   if constexpr (XS) {
     stage_act_dma(g.X, (size_t)g.xstride, NT, g.d, smem, wave, lane);
-    int issued = 0;
-#pragma unroll
-    for (int s = 0; s < D; s++) {
-      issued += tile + s * tstep < ntiles;
-      dma(s, tile + s * tstep);
-    }
-    if (issued == 0) wait_vmcnt<0>();
-    else if (issued == 1) wait_vmcnt<NCH>();
-    else wait_vmcnt<2 * NCH>();
-    quantize_act_blk<BlkFmt<TYPE>::kNib>(g.X, (size_t)g.xstride, NT, g.d, act, pre, xs);
+    const bool has = tile < ntiles;
+    dma(tile);
+    if (has) wait_vmcnt<NCH>();
+    else wait_vmcnt<0>();
+    quantize_act_blk<BlkFmt<TYPE>::kNib, kActLds>(g.X, (size_t)g.xstride, NT, g.d, act, pre, xs);
   } else {
     // the compiler's wait for these loads also covers the first tile's DMA
     act_prefetch(g.X, (size_t)g.xstride, NT, g.d, pre);
-    dma(0, tile);
+    dma(tile);
     quantize_act_blk<BlkFmt<TYPE>::kNib>(g.X, (size_t)g.xstride, NT, g.d, act, pre);
-#pragma unroll
-    for (int s = 1; s < D; s++) dma(s, tile + s * tstep);
   }
   // LDS-only barrier: the tile DMA stays in flight across it
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
-  if (g.accb && blockIdx.x == 0) {
-    for (int i = threadIdx.x; i < NT * U; i += blockDim.x) {
-      const int t = i / U, u = i - t * U;
-      g.accb[i] = reinterpret_cast<const int*>(act + (size_t)t * tokb + act_off(u) + 44)[0];
+  if constexpr (ACC) {
+    if (g.accb && blockIdx.x == 0) {
+      for (int i = threadIdx.x; i < NT * U; i += blockDim.x) {
+        const int t = i / U, u = i - t * U;
+        g.accb[i] = reinterpret_cast<const int*>(act + (size_t)t * tokb + act_off(u) + 44)[0];
+      }
     }
   }
   if (tile >= ntiles) return;  // no barriers below
 
   for (;;) {
+    wait_vmcnt<0>();
+    uint4 c[NCH];
+    {
+      const uint4* q = reinterpret_cast<const uint4*>(slot + (size_t)lane * BB);
 #pragma unroll
-    for (int s = 0; s < D; s++) {
-      const int cur = tile + s * tstep;
-      if (cur < ntiles) {
-        // the slot's tile is complete once no more than the later tiles'
-        // DMA (issued after it) is in flight
-        if (D == 2 && cur + tstep < ntiles) wait_vmcnt<NCH>();
-        else wait_vmcnt<0>();
-        uint4 c[NCH];
-        {
-          const uint4* q = reinterpret_cast<const uint4*>(slots + s * SB + (size_t)lane * BB);
+      for (int k = 0; k < NCH; k++) c[k] = q[k];
+    }
+    const int cur = tile;
+    tile += tstep;
+    dma(tile);
+    const int row = cur * RB + rl;
+    const bool live = lane_on && row < g.n;
+    float terms[NT][8];
+    int32_t isums[NT][8];
+    blk_terms<TYPE, NT>(c, b, act, tokb, terms, isums);
+    if constexpr (ACC) {
+      if (g.acc && live) {
 #pragma unroll
-          for (int k = 0; k < NCH; k++) c[k] = q[k];
-        }
-        dma(s, cur + D * tstep);
-        const int row = cur * RB + rl;
-        const bool live = lane_on && row < g.n;
-        float terms[NT][8];
-        int32_t isums[NT][8];
-        blk_terms<TYPE, NT>(c, b, act, tokb, terms, isums);
-        if (g.acc && live) {
+        for (int t = 0; t < NT; t++)
 #pragma unroll
-          for (int t = 0; t < NT; t++)
-#pragma unroll
-            for (int q = 0; q < 8; q++)
-              g.acc[((size_t)t * g.n + row) * U + 8 * b + q] = isums[t][q];
-        }
-        float y[NT];
-        blk_chain<NT>(terms, b, nb, y);
-        if (live && b == nb - 1) {
-#pragma unroll
-          for (int t = 0; t < NT; t++) g.Y[(size_t)t * g.ystride + row] = y[t];
-        }
+          for (int q = 0; q < 8; q++) g.acc[((size_t)t * g.n + row) * U + 8 * b + q] = isums[t][q];
       }
     }
-    tile += D * tstep;
+    float y[NT];
+    blk_chain<NT>(terms, b, nb, y);
+    if (live && b == nb - 1) {
+#pragma unroll
+      for (int t = 0; t < NT; t++) g.Y[(size_t)t * g.ystride + row] = y[t];
+    }
     if (tile >= ntiles) break;
   }
 }
@@ -440,23 +444,22 @@ hipError_t lds_opt_in(const void* fn, std::atomic<bool>* done) {
   return hipSuccess;
 }
 
-template <int TYPE, int NT, int D, bool XS>
-static hipError_t launch_blk_d(const GemvArgs& a, int grid, size_t lds, hipStream_t st) {
+template <int TYPE, int NT, bool XS, bool ACC>
+static hipError_t launch_blk_k(const GemvArgs& a, int grid, size_t lds, hipStream_t st) {
   static std::atomic<bool> opted[64];
   if (lds > 64 * 1024) {
-    hipError_t e = lds_opt_in((const void*)k_gemv_blk<TYPE, NT, D, XS>, opted);
+    hipError_t e = lds_opt_in((const void*)k_gemv_blk<TYPE, NT, XS, ACC>, opted);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((k_gemv_blk<TYPE, NT, D, XS>), dim3(grid), dim3(64 * kBlkWaves), lds, st, a);
+  hipLaunchKernelGGL((k_gemv_blk<TYPE, NT, XS, ACC>), dim3(grid), dim3(64 * kBlkWaves), lds, st, a);
   return hipGetLastError();
 }
 
-// One tile in flight per wave (D = 1) and two workgroups per CU (one where two
-// do not fit in LDS).  Two per CU give the 32000 x 2048 Q4_K GEMV 2048 waves
-// for 4000 tiles, two tiles each with the second streaming while the first is
-// reduced: 9.33 us per launch against 9.75 us with three per CU (a third of
-// the waves with a second tile, the rest contending) and 10.96 us with one.
-// Two tiles in flight per wave measured slower (9.8 against 8.74 us).  The
+// One tile in flight per wave and as many workgroups per CU as LDS holds, up
+// to three.  Measured on the 32000 x 2048 Q4_K GEMV: three per CU (48 KiB
+// each) take 8.39 us per launch against 8.65 us at two; two tiles in flight
+// per wave measured slower (9.2 us and more: the memory system then serves
+// every wave's tiles late, and the arithmetic bunches at the end).  The
 // activation is staged through LDS by DMA when it fits kXsMax, else loaded
 // into registers (d = 5632 at 3 or 4 tokens).
 template <int TYPE, int NT>
@@ -469,12 +472,15 @@ static hipError_t launch_blk_t(const GemvArgs& a, hipStream_t st) {
   const int ntiles = (a.n + RB - 1) / RB;
   const int want = (ntiles + kBlkWaves - 1) / kBlkWaves;
   int per_cu = (int)(kLdsMax / lds);
-  per_cu = per_cu < 1 ? 1 : (per_cu > 2 ? 2 : per_cu);
+  per_cu = per_cu < 1 ? 1 : (per_cu > 3 ? 3 : per_cu);
   const int cap = device_cus() * per_cu;
   const int grid = want < cap ? want : cap;
   if (grid <= 0) return hipSuccess;
-  if (xs) return launch_blk_d<TYPE, NT, 1, true>(a, grid, lds, st);
-  return launch_blk_d<TYPE, NT, 1, false>(a, grid, lds, st);
+  const bool acc = a.acc || a.accb;
+  if (xs) return acc ? launch_blk_k<TYPE, NT, true, true>(a, grid, lds, st)
+                     : launch_blk_k<TYPE, NT, true, false>(a, grid, lds, st);
+  return acc ? launch_blk_k<TYPE, NT, false, true>(a, grid, lds, st)
+             : launch_blk_k<TYPE, NT, false, false>(a, grid, lds, st);
 }
 
 template <int TYPE, int NT, int Q8O>

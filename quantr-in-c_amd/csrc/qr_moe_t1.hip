@@ -152,7 +152,7 @@ __global__ __launch_bounds__(64 * kBlkWaves) void k_gateup1(GateUp1Args a) {
     stage_act_dma(a.xb, (size_t)a.dim, 1, a.dim, smem, wave - 1, lane, kBlkWaves - 1);
     wait_vmcnt<0>();
     ActPre pre;
-    quantize_act_blk<BlkFmt<TYPE>::kNib>(a.xb, (size_t)a.dim, 1, a.dim, act, pre,
+    quantize_act_blk<BlkFmt<TYPE>::kNib, kActLds>(a.xb, (size_t)a.dim, 1, a.dim, act, pre,
                                          reinterpret_cast<const float*>(smem),
                                          (int)threadIdx.x - 64, 64 * (kBlkWaves - 1));
   }

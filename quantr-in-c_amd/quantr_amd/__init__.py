@@ -56,6 +56,7 @@ _SIGS = {
     "qr_timer_start": (C.c_int, [_vp]),
     "qr_timer_stop": (C.c_int, [_vp, C.POINTER(C.c_float)]),
     "qr_copy_kernel": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
+    "qr_read_kernel": (C.c_int, [_vp, _vp, C.c_size_t, _vp]),
     "qr_capture_begin": (C.c_int, [_vp]),
     "qr_capture_end": (C.c_int, [_vp, C.POINTER(_vp)]),
     "qr_graph_launch": (C.c_int, [_vp, _vp]),
@@ -259,6 +260,9 @@ class Device:
 
     def copy_kernel(self, dst, src, nbytes):
         self._check(self.lib.qr_copy_kernel(self.ctx, _vp(dst), _vp(src), nbytes), "qr_copy_kernel")
+
+    def read_kernel(self, src, nbytes, sink):
+        self._check(self.lib.qr_read_kernel(self.ctx, _vp(src), nbytes, _vp(sink)), "qr_read_kernel")
 
     def test_expf(self, x_ptr, y_ptr, n):
         self._check(self.lib.qr_test_expf(self.ctx, _vp(x_ptr), _vp(y_ptr), n), "qr_test_expf")
