@@ -53,6 +53,31 @@ class MoeLayer(C.Structure):
     ]
 
 
+class OModel(C.Structure):
+    """qro_model (oracle/qr_oracle.h)."""
+    _fields_ = [
+        ("dim", C.c_int), ("n_layers", C.c_int), ("n_heads", C.c_int), ("n_kv_heads", C.c_int),
+        ("head_dim", C.c_int), ("vocab", C.c_int), ("seq_len", C.c_int), ("rope_base", C.c_float),
+        ("kv_type", C.c_int), ("tok_embd", C.c_void_p), ("tok_type", C.c_uint32),
+        ("tok_row_bytes", C.c_size_t), ("rms_att", C.c_void_p), ("rms_ffn", C.c_void_p),
+        ("wq", C.c_void_p), ("wk", C.c_void_p), ("wv", C.c_void_p), ("wo", C.c_void_p),
+        ("wtype", C.c_void_p), ("moe", C.c_void_p), ("rms_final", C.c_void_p),
+        ("wcls", C.c_void_p), ("wcls_type", C.c_uint32),
+    ]
+
+
+KV_F32, KV_Q8_0 = 0, 2
+
+
+def _parr(keep, arrs):
+    """A C array of pointers to the numpy arrays (kept alive in `keep`)."""
+    arrs = [None if a is None else np.ascontiguousarray(a) for a in arrs]
+    keep.extend(a for a in arrs if a is not None)
+    p = (C.c_void_p * len(arrs))(*[None if a is None else a.ctypes.data for a in arrs])
+    keep.append(p)
+    return p
+
+
 def build_oracle():
     """Compile liboracle.so (and oracle/_ref when the reference checkout exists)."""
     import subprocess
@@ -95,6 +120,15 @@ class Oracle:
         L.qro_moe_forward.argtypes = [_f32p, _f32p, C.c_int, C.POINTER(MoeLayer), C.c_int,
                                       C.c_int, C.c_int, C.c_void_p, C.c_void_p]
         L.qro_shared_expert.argtypes = [_f32p, _f32p, C.POINTER(MoeLayer), C.c_int]
+        L.qro_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_int]
+        L.qro_rope.argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
+        L.qro_rope_table.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_float]
+        L.qro_kv_row_bytes.restype = C.c_size_t
+        L.qro_kv_row_bytes.argtypes = [C.c_int, C.c_int]
+        L.qro_attention.argtypes = [_f32p, _f32p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_int,
+                                    C.c_int, C.c_int, C.c_int, C.c_int, _f32p]
+        L.qro_forward.argtypes = [C.POINTER(OModel), C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                                  C.c_int, _f32p, _f32p]
         L.qro_moe_dispatch.restype = C.c_int
         L.qro_moe_dispatch.argtypes = [_i32p, C.c_int, C.c_int, C.c_int, _i32p, _i32p, _i32p, _i32p]
 
@@ -214,6 +248,90 @@ class Oracle:
         self.lib.qro_shared_expert(y, np.ascontiguousarray(xb, np.float32), C.byref(layer), threads)
         return y
 
+    # --- the decode step (oracle/qr_oracle_decode.c)
+    def rmsnorm(self, x, w):
+        x = np.ascontiguousarray(x, np.float32)
+        o = np.zeros_like(x)
+        self.lib.qro_rmsnorm(o, x, np.ascontiguousarray(w, np.float32), x.size)
+        return o
+
+    def rope(self, q, k, head_dim, n_kv_heads, pos, base):
+        q = np.array(q, np.float32)
+        k = np.array(k, np.float32)
+        if k.size < q.size:  # apply_rope reads k up to kv_dim only
+            k = np.concatenate([k, np.zeros(q.size - k.size, np.float32)])
+        self.lib.qro_rope(q, k, q.size, head_dim, n_kv_heads, pos, base)
+        return q, k
+
+    def rope_table(self, qlen, head_dim, pos, base):
+        cs = np.zeros(qlen, np.float32)
+        self.lib.qro_rope_table(cs, qlen, head_dim, pos, base)
+        return cs
+
+    def kv_row_bytes(self, kv_type, kv_dim):
+        return self.lib.qro_kv_row_bytes(kv_type, kv_dim)
+
+    def attention(self, q, kc, vc, kv_type, pos, n_heads, n_kv_heads, head_dim):
+        """kc / vc: [pos+1][row bytes] uint8 (fp32 rows as bytes for KV_F32)."""
+        q = np.ascontiguousarray(q, np.float32)
+        kc = np.ascontiguousarray(kc)
+        vc = np.ascontiguousarray(vc)
+        out = np.zeros(n_heads * head_dim, np.float32)
+        att = np.zeros(n_heads * (pos + 1), np.float32)
+        self.lib.qro_attention(out, q, _ptr(kc), _ptr(vc), kc.nbytes // (pos + 1), kv_type, pos,
+                               n_heads, n_kv_heads, head_dim, att)
+        return out, att.reshape(n_heads, pos + 1)
+
+    @staticmethod
+    def make_model(keep, m, kv_type):
+        """qro_model of a decode model dict (tests/golden/inputs.py decode_model)."""
+        L = m["n_layers"]
+        lay = m["layers"]
+        moes = (MoeLayer * L)()
+        for l in range(L):
+            ml = Oracle.make_layer(keep, m["dim"], m["hidden"], m["E"], m["K"], lay[l]["router"],
+                                   lay[l]["up"], m["up_type"], lay[l]["gate"], m["up_type"],
+                                   lay[l]["down"], m["down_type"])
+            moes[l] = ml
+        keep.append(moes)
+        wtype = np.array([t for l in range(L) for t in m["wtype"]], np.uint32)
+        tok = np.ascontiguousarray(m["tok_embd"])
+        keep.extend([wtype, tok])
+        om = OModel()
+        om.dim, om.n_layers, om.n_heads = m["dim"], L, m["n_heads"]
+        om.n_kv_heads, om.head_dim, om.vocab = m["n_kv_heads"], m["head_dim"], m["vocab"]
+        om.seq_len, om.rope_base, om.kv_type = m["seq_len"], m["rope_base"], kv_type
+        om.tok_embd, om.tok_type = tok.ctypes.data, m["tok_type"]
+        om.tok_row_bytes = tok.nbytes // m["vocab"]
+        om.rms_att = C.cast(_parr(keep, [x["rms_att"] for x in lay]), C.c_void_p)
+        om.rms_ffn = C.cast(_parr(keep, [x["rms_ffn"] for x in lay]), C.c_void_p)
+        for f in ("wq", "wk", "wv", "wo"):
+            setattr(om, f, C.cast(_parr(keep, [x[f] for x in lay]), C.c_void_p))
+        om.wtype = wtype.ctypes.data
+        om.moe = C.cast(moes, C.c_void_p)
+        rf = np.ascontiguousarray(m["rms_final"], np.float32)
+        wc = np.ascontiguousarray(m["wcls"])
+        keep.extend([rf, wc])
+        om.rms_final, om.wcls, om.wcls_type = rf.ctypes.data, wc.ctypes.data, m["wcls_type"]
+        return om
+
+    def forward_seq(self, m, tokens, order, kv_type=KV_F32):
+        """qro_forward for tokens at positions 0..n-1: (logits [n][vocab], x [n][dim])."""
+        keep = []
+        om = self.make_model(keep, m, kv_type)
+        kvd = m["n_kv_heads"] * m["head_dim"]
+        rs = self.kv_row_bytes(kv_type, kvd)
+        kc = np.zeros(m["n_layers"] * m["seq_len"] * rs, np.uint8)
+        vc = np.zeros_like(kc)
+        lg = np.zeros((len(tokens), m["vocab"]), np.float32)
+        xs = np.zeros((len(tokens), m["dim"]), np.float32)
+        for i, tok in enumerate(tokens):
+            x = np.zeros(m["dim"], np.float32)
+            lo = np.zeros(m["vocab"], np.float32)
+            self.lib.qro_forward(C.byref(om), _ptr(kc), _ptr(vc), int(tok), i, order, x, lo)
+            lg[i], xs[i] = lo, x
+        return lg, xs
+
     def dispatch(self, idx, E):
         idx = np.ascontiguousarray(idx, np.int32)
         T, K = idx.shape
@@ -265,6 +383,12 @@ class RefLib:
         L.refdrv_gemv_bench.restype = C.c_int
         L.refdrv_gemv_bench.argtypes = [_f32p, C.c_void_p, C.c_int, C.c_uint32, C.c_int, C.c_int,
                                         C.c_int, C.c_int, C.c_int, _f32p, C.c_void_p]
+        L.refdrv_forward.restype = C.c_int
+        L.refdrv_forward.argtypes = [C.c_int] * 7 + [C.c_float, C.c_int, C.c_int, C.c_void_p,
+                                                     C.c_uint32, C.c_size_t] + \
+            [C.c_void_p] * 7 + [C.c_void_p] * 4 + [C.c_uint32] * 3 + \
+            [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
+             _f32p, C.c_void_p]
         L.refdrv_moe_layer.restype = C.c_int
         L.refdrv_moe_layer.argtypes = [_f32p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
                                        C.c_int, C.c_int, _f32p, C.c_void_p, C.c_uint32,
@@ -354,3 +478,30 @@ class RefLib:
         if rc != 0:
             raise RuntimeError("refdrv_gemv_bench failed: %d" % rc)
         return times
+
+    def forward(self, m, tokens, backend, threads=1, kv_type=0):
+        """The reference's forward_runtime on decode model m (tests/golden/inputs.py)
+        for tokens at positions 0..n-1: (logits [n][vocab], x [n][dim])."""
+        keep = []
+        lay = m["layers"]
+        L = m["n_layers"]
+        wtype = np.array([t for l in range(L) for t in m["wtype"]], np.uint32)
+        tok = np.ascontiguousarray(m["tok_embd"])
+        toks = np.array(tokens, np.int32)
+        keep.extend([wtype, tok, toks])
+        P = lambda key: _parr(keep, [x[key] for x in lay])  # noqa: E731
+        lg = np.zeros((len(tokens), m["vocab"]), np.float32)
+        xs = np.zeros((len(tokens), m["dim"]), np.float32)
+        rf = np.ascontiguousarray(m["rms_final"], np.float32)
+        wc = np.ascontiguousarray(m["wcls"])
+        keep.extend([rf, wc])
+        rc = self.lib.refdrv_forward(
+            m["dim"], m["hidden"], L, m["n_heads"], m["n_kv_heads"], m["vocab"], m["seq_len"],
+            m["rope_base"], m["E"], m["K"], tok.ctypes.data, m["tok_type"], tok.nbytes // m["vocab"],
+            P("rms_att"), P("rms_ffn"), P("wq"), P("wk"), P("wv"), P("wo"), wtype.ctypes.data,
+            P("router"), P("up"), P("gate"), P("down"), m["up_type"], m["up_type"], m["down_type"],
+            rf.ctypes.data, wc.ctypes.data, m["wcls_type"], toks.ctypes.data, len(tokens), kv_type,
+            backend, threads, lg, xs.ctypes.data)
+        if rc != 0:
+            raise RuntimeError("refdrv_forward failed: %d" % rc)
+        return lg, xs

@@ -123,6 +123,40 @@ void qro_shared_expert(float* y, const float* xb, const qro_moe_layer* L, int th
 int qro_moe_dispatch(const int32_t* idx, int T, int K, int E, int32_t* counts,
                      int32_t* offsets, int32_t* perm, int32_t* inv);
 
+/* ---- the single-token decode step (qr_oracle_decode.c) ------------------ */
+#define QRO_KV_F32 0
+#define QRO_KV_Q8_0 2
+
+typedef struct {
+    int dim, n_layers, n_heads, n_kv_heads, head_dim, vocab, seq_len;
+    float rope_base;
+    int kv_type;                 /* QRO_KV_F32 or QRO_KV_Q8_0 */
+    const void* tok_embd;        /* [vocab] rows of tok_row_bytes */
+    uint32_t tok_type;
+    size_t tok_row_bytes;
+    const float* const* rms_att; /* [L] -> [dim] */
+    const float* const* rms_ffn;
+    const void* const* wq;       /* [L] -> [n_heads*head_dim][dim] */
+    const void* const* wk;       /* [L] -> [n_kv_heads*head_dim][dim] */
+    const void* const* wv;
+    const void* const* wo;       /* [L] -> [dim][n_heads*head_dim] */
+    const uint32_t* wtype;       /* [L][4]: wq, wk, wv, wo */
+    const qro_moe_layer* moe;    /* [L] */
+    const float* rms_final;
+    const void* wcls;            /* [vocab][dim] */
+    uint32_t wcls_type;
+} qro_model;
+
+void qro_rmsnorm(float* o, const float* x, const float* w, int n);
+void qro_rope(float* q, float* k, int qlen, int head_dim, int n_kv_heads, int pos, float base);
+void qro_rope_table(float* cs, int qlen, int head_dim, int pos, float base);
+size_t qro_kv_row_bytes(int kv_type, int kv_dim);
+void qro_kv_store(void* row, const float* src, int kv_dim, int kv_type);
+void qro_attention(float* out, const float* q, const void* kc, const void* vc, size_t row_stride,
+                   int kv_type, int pos, int n_heads, int n_kv_heads, int head_dim, float* att);
+void qro_forward(const qro_model* m, void* kc, void* vc, int token, int pos, int order, float* x,
+                 float* logits);
+
 #ifdef __cplusplus
 }
 #endif

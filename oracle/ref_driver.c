@@ -330,3 +330,133 @@ int refdrv_gemv_bench(const float* x, const void* const* w_copies, int ncopies, 
     }
     return 0;
 }
+
+/*
+ * The reference's forward_runtime on a caller-supplied model, for n_tokens
+ * tokens at positions 0 .. n_tokens-1 (the KV cache fills as it goes).
+ * Per-layer tensors are arrays of L pointers (NULL allowed where the reference
+ * allows it); wtype[l * 4 + {0,1,2,3}] are the types of wq, wk, wv, wo; MoE
+ * experts are [E][rows][cols] tensors sliced as src/model.c:412-419 does.
+ * kv_type: the reference's RunState.kv_cache_type (0 fp32, 1 fp16).
+ * logits_out: [n_tokens][vocab]; x_out (optional): the residual after the
+ * last layer, [n_tokens][dim].
+ */
+int refdrv_forward(int dim, int hidden, int n_layers, int n_heads, int n_kv_heads, int vocab,
+                   int seq_len, float rope_base, int E, int K, const void* tok_embd,
+                   uint32_t tok_type, size_t tok_row_bytes, const float* const* rms_att,
+                   const float* const* rms_ffn, const void* const* wq, const void* const* wk,
+                   const void* const* wv, const void* const* wo, const uint32_t* wtype,
+                   const float* const* router, const void* const* up, const void* const* gate,
+                   const void* const* down, uint32_t up_type, uint32_t gate_type,
+                   uint32_t down_type, const float* rms_final, const void* wcls,
+                   uint32_t wcls_type, const int* tokens, int n_tokens, int kv_type, int backend,
+                   int threads, float* logits_out, float* x_out) {
+    Transformer t;
+    RuntimeContext rt;
+    RuntimeOptions opt;
+    float ***ew1, ***ew2, ***ew3;
+    uint32_t *tq, *tk, *tv, *to, *t_up, *t_down, *t_gate;
+    size_t s_up, s_gate, s_down;
+    int l, e, i;
+
+    if (E > 256 || K > 16 || K > E) return -1;
+    memset(&t, 0, sizeof(t));
+    t.config.dim = dim;
+    t.config.hidden_dim = hidden;
+    t.config.n_layers = n_layers;
+    t.config.n_heads = n_heads;
+    t.config.n_kv_heads = n_kv_heads;
+    t.config.vocab_size = vocab;
+    t.config.seq_len = seq_len;
+    t.config.rope_freq_base = rope_base;
+    t.config.expert_count = E;
+    t.config.expert_used_count = K;
+
+    ew1 = (float***)malloc((size_t)n_layers * sizeof(float**));
+    ew2 = (float***)malloc((size_t)n_layers * sizeof(float**));
+    ew3 = (float***)malloc((size_t)n_layers * sizeof(float**));
+    tq = (uint32_t*)malloc((size_t)n_layers * sizeof(uint32_t) * 7);
+    if (!ew1 || !ew2 || !ew3 || !tq) return -2;
+    tk = tq + n_layers;
+    tv = tk + n_layers;
+    to = tv + n_layers;
+    t_up = to + n_layers;
+    t_down = t_up + n_layers;
+    t_gate = t_down + n_layers;
+    s_up = (up_type == 8 ? (size_t)(dim / 32) * 34 : up_type == 12 ? (size_t)(dim / 256) * 144
+            : up_type == 13 ? (size_t)(dim / 256) * 176 : up_type == 14 ? (size_t)(dim / 256) * 210
+            : (size_t)dim * 4) * (size_t)hidden;
+    s_gate = (gate_type == 8 ? (size_t)(dim / 32) * 34 : gate_type == 12 ? (size_t)(dim / 256) * 144
+              : gate_type == 13 ? (size_t)(dim / 256) * 176 : gate_type == 14 ? (size_t)(dim / 256) * 210
+              : (size_t)dim * 4) * (size_t)hidden;
+    s_down = (down_type == 8 ? (size_t)(hidden / 32) * 34 : down_type == 12 ? (size_t)(hidden / 256) * 144
+              : down_type == 13 ? (size_t)(hidden / 256) * 176 : down_type == 14 ? (size_t)(hidden / 256) * 210
+              : (size_t)hidden * 4) * (size_t)dim;
+    for (l = 0; l < n_layers; l++) {
+        tq[l] = wtype[4 * l];
+        tk[l] = wtype[4 * l + 1];
+        tv[l] = wtype[4 * l + 2];
+        to[l] = wtype[4 * l + 3];
+        t_up[l] = up_type;
+        t_down[l] = down_type;
+        t_gate[l] = gate_type;
+        ew1[l] = ew2[l] = ew3[l] = NULL;
+        if (E > 0) {
+            ew1[l] = (float**)malloc((size_t)E * sizeof(float*));
+            ew2[l] = (float**)malloc((size_t)E * sizeof(float*));
+            ew3[l] = (float**)malloc((size_t)E * sizeof(float*));
+            if (!ew1[l] || !ew2[l] || !ew3[l]) return -2;
+            for (e = 0; e < E; e++) {
+                ew1[l][e] = (float*)((const char*)up[l] + (size_t)e * s_up);
+                ew3[l][e] = (float*)((const char*)gate[l] + (size_t)e * s_gate);
+                ew2[l][e] = (float*)((const char*)down[l] + (size_t)e * s_down);
+            }
+        }
+    }
+    t.weights.token_embedding_table = (float*)tok_embd;
+    t.weights.token_embd_type = tok_type;
+    t.weights.token_embd_row_bytes = tok_row_bytes;
+    t.weights.rms_att_weight = (float**)rms_att;
+    t.weights.rms_ffn_weight = (float**)rms_ffn;
+    t.weights.wq = (float**)wq;
+    t.weights.wk = (float**)wk;
+    t.weights.wv = (float**)wv;
+    t.weights.wo = (float**)wo;
+    t.weights.wq_type = tq;
+    t.weights.wk_type = tk;
+    t.weights.wv_type = tv;
+    t.weights.wo_type = to;
+    t.weights.rms_final_weight = (float*)rms_final;
+    t.weights.wcls = (float*)wcls;
+    t.weights.wcls_type = wcls_type;
+    t.weights.ffn_gate_inp = (float**)router;
+    t.weights.expert_w1 = ew1;
+    t.weights.expert_w2 = ew2;
+    t.weights.expert_w3 = ew3;
+    t.weights.exp_w1_type = t_up;
+    t.weights.exp_w2_type = t_down;
+    t.weights.exp_w3_type = t_gate;
+    if (kv_type == 0) malloc_run_state(&t.state, &t.config);
+    else malloc_run_state_kv(&t.state, &t.config, kv_type);
+    memset(&opt, 0, sizeof(opt));
+    opt.backend = (KernelBackend)backend;
+    opt.num_threads = threads;
+    runtime_init(&rt, opt);
+
+    for (i = 0; i < n_tokens; i++) {
+        float* lg = forward_runtime(&rt, &t, tokens[i], i);
+        memcpy(logits_out + (size_t)i * vocab, lg, (size_t)vocab * sizeof(float));
+        if (x_out) memcpy(x_out + (size_t)i * dim, t.state.x, (size_t)dim * sizeof(float));
+    }
+    free_run_state(&t.state);
+    for (l = 0; l < n_layers; l++) {
+        free(ew1[l]);
+        free(ew2[l]);
+        free(ew3[l]);
+    }
+    free(ew1);
+    free(ew2);
+    free(ew3);
+    free(tq);
+    return 0;
+}

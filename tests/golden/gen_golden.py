@@ -141,6 +141,23 @@ def gen_moe(rc, ra, r5):
     save("moe.npz", **out)
 
 
+def gen_decode(rc, ra, r5):
+    """forward_runtime of the small decode models, token by token from
+    position 0, in each build (fp32 KV cache: the reference's working type)."""
+    out = {}
+    for name in I.DECODE_CASES:
+        m = I.decode_model(name)
+        out["sha_" + name] = np.array(I.decode_digest(m))
+        builds = [("c99", rc, BACKEND_REF), ("avx2", ra, BACKEND_AVX2)]
+        if r5 is not None:
+            builds.append(("avx512", r5, BACKEND_AVX512))
+        for tag, lib, backend in builds:
+            lg, xs = lib.forward(m, m["tokens"], backend, threads=2)
+            out["logits_%s_%s" % (name, tag)] = lg
+            out["x_%s_%s" % (name, tag)] = xs
+    save("decode.npz", **out)
+
+
 def main():
     rc, ra = RefLib("c99"), RefLib("avx2")
     assert rc.lib.refdrv_has_avx2_paths() == 0 and ra.lib.refdrv_has_avx2_paths() == 1
@@ -153,6 +170,7 @@ def main():
     gen_dots(rc, ra, r5)
     gen_router(rc, ra, r5)
     gen_moe(rc, ra, r5)
+    gen_decode(rc, ra, r5)
 
 
 if __name__ == "__main__":

@@ -137,3 +137,63 @@ def q8_edge_rows():
     rng = np.random.default_rng(77)
     rows.append((rng.standard_normal(64) * 1e-5).astype(np.float32))    # amax near fp16 min normal * 127
     return np.stack(rows).astype(np.float32)
+
+
+# ---- the single-token decode step ------------------------------------------
+# Small MoE models run through the reference's own forward_runtime
+# (gen_golden.py) and through the decoders under test.  head_dim is
+# dim / n_heads, which is what the reference can express (src/runtime.c:102);
+# expert up / gate are Q5_K (the reference's Q4_K dot is defective).
+# (dim, n_heads, n_kv_heads, layers, E, K, hidden, vocab, wq/wk/wv/wo types,
+#  token-embedding type, lm_head type, tokens)
+TYPE_F32 = 0
+DECODE_CASES = {
+    "a": (256, 4, 2, 2, 8, 2, 256, 300, (TYPE_Q8_0, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0), TYPE_Q8_0,
+          TYPE_Q6_K, [3, 17, 101, 42, 250, 7, 7, 199]),
+    "b": (512, 8, 2, 2, 16, 4, 256, 200, (TYPE_Q6_K, TYPE_F32, TYPE_Q8_0, TYPE_Q5_K), TYPE_Q6_K,
+          TYPE_Q8_0, [0, 199, 55, 55, 120]),
+}
+
+
+def _rows(seed, qtype, rows, cols):
+    if qtype == TYPE_F32:
+        return activations(seed, rows, cols, std=0.05)
+    elems, bb = BLOCK[qtype]
+    return blocks(seed, qtype, rows * (cols // elems)).reshape(rows, (cols // elems) * bb)
+
+
+def decode_model(name):
+    """The seeded weights of decode case `name` (numpy, host order)."""
+    dim, H, KVH, L, E, K, hidden, vocab, wt, tt, ct, tokens = DECODE_CASES[name]
+    hd = dim // H
+    seed = 9000 + 100 * (ord(name) - ord("a"))
+    m = dict(dim=dim, n_heads=H, n_kv_heads=KVH, head_dim=hd, n_layers=L, E=E, K=K,
+             hidden=hidden, vocab=vocab, seq_len=max(16, len(tokens)), rope_base=1e6,
+             wtype=list(wt), tok_type=tt, wcls_type=ct, tokens=list(tokens),
+             up_type=TYPE_Q5_K, down_type=TYPE_Q6_K)
+    m["tok_embd"] = _rows(seed, tt, vocab, dim)
+    m["wcls"] = _rows(seed + 1, ct, vocab, dim)
+    m["rms_final"] = (1.0 + activations(seed + 2, 1, dim, std=0.1)[0]).astype(np.float32)
+    layers = []
+    for l in range(L):
+        s = seed + 10 + 20 * l
+        lay = dict(
+            rms_att=(1.0 + activations(s, 1, dim, std=0.1)[0]).astype(np.float32),
+            rms_ffn=(1.0 + activations(s + 1, 1, dim, std=0.1)[0]).astype(np.float32),
+            wq=_rows(s + 2, wt[0], H * hd, dim), wk=_rows(s + 3, wt[1], KVH * hd, dim),
+            wv=_rows(s + 4, wt[2], KVH * hd, dim), wo=_rows(s + 5, wt[3], dim, H * hd),
+            router=activations(s + 6, E, dim, std=0.05),
+            up=blocks(s + 7, TYPE_Q5_K, E * hidden * (dim // 256)),
+            gate=blocks(s + 8, TYPE_Q5_K, E * hidden * (dim // 256)),
+            down=blocks(s + 9, TYPE_Q6_K, E * dim * (hidden // 256)))
+        layers.append(lay)
+    m["layers"] = layers
+    return m
+
+
+def decode_digest(m):
+    arrs = [m["tok_embd"], m["wcls"], m["rms_final"]]
+    for lay in m["layers"]:
+        arrs += [lay[k] for k in ("rms_att", "rms_ffn", "wq", "wk", "wv", "wo", "router", "up",
+                                  "gate", "down")]
+    return digest(*arrs)

@@ -124,3 +124,49 @@ def test_moe_block(oracle, golden, name, build):
     xo, idx, w = oracle.moe_forward(m["x"], xb, L, order=order, dot_order=order, threads=4)
     assert_bits_equal(xo, g["xo_%s_%s" % (name, build)], "MoE block %s/%s" % (name, build))
     assert (idx >= 0).all() and (idx < m["E"]).all()
+
+
+@pytest.mark.parametrize("name", sorted(I.DECODE_CASES))
+@pytest.mark.parametrize("build", ["c99", "avx2", "avx512"])
+def test_decode_step(oracle, golden, name, build):
+    """The oracle's decode step (oracle/qr_oracle_decode.c) against the
+    reference's own forward_runtime (src/runtime.c:94-288) on a two-layer MoE
+    model, token by token from position 0 (fp32 KV cache, head_dim =
+    dim / n_heads): embedding dequantization, RMSNorm, Q/K/V, RoPE, the
+    attention over the growing cache, Wo and the residual, the MoE block, the
+    final norm and the lm_head -- logits and residual bit-exact."""
+    g = golden("decode.npz")
+    m = I.decode_model(name)
+    assert I.decode_digest(m) == str(g["sha_" + name])
+    key = "logits_%s_%s" % (name, build)
+    if key not in g:
+        pytest.skip("fixture written without an -mavx512f build")
+    order = {"c99": ORDER_SEQ, "avx2": ORDER_AVX2, "avx512": ORDER_AVX512}[build]
+    lg, xs = oracle.forward_seq(m, m["tokens"], order)
+    assert_bits_equal(lg, g[key], "logits %s/%s" % (name, build))
+    assert_bits_equal(xs, g["x_%s_%s" % (name, build)], "residual %s/%s" % (name, build))
+
+
+def test_rope_table_matches_rope(oracle):
+    """The per-position cos / sin table (what the device decoder reads) gives
+    the same rotation as apply_rope's per-call powf / cosf / sinf: rotating with
+    the table in the reference's operation order reproduces qro_rope bit for
+    bit (q of 8 heads of 64, k of 2 kv heads, positions 0, 1, 4095)."""
+    qlen, hd, kvh, base = 512, 64, 2, 1e6
+    q0 = I.activations(77, 1, qlen)[0]
+    k0 = I.activations(78, 1, kvh * hd)[0]
+    for pos in (0, 1, 4095):
+        q, k = oracle.rope(q0, k0, hd, kvh, pos, base)
+        cs = oracle.rope_table(qlen, hd, pos, base)
+        c, s = cs[0::2], cs[1::2]
+        a, b = q0[0::2], q0[1::2]
+        qt = np.empty_like(q0)
+        qt[0::2] = (a * c - b * s).astype(np.float32)
+        qt[1::2] = (a * s + b * c).astype(np.float32)
+        # numpy float32 ops round once each, in the same order as the C code
+        assert_bits_equal(q, qt, "q at pos %d" % pos)
+        ka, kb = k0[0::2], k0[1::2]
+        kt = k0.copy()
+        kt[0::2] = ka * c[: kvh * hd // 2] - kb * s[: kvh * hd // 2]
+        kt[1::2] = ka * s[: kvh * hd // 2] + kb * c[: kvh * hd // 2]
+        assert_bits_equal(k[: kvh * hd], kt, "k at pos %d" % pos)
