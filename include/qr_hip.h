@@ -208,6 +208,118 @@ int qr_moe_forward(qr_ctx* ctx, const qr_moe_layer* L, float* x, const float* xb
 int qr_moe_forward_noalloc(qr_ctx* ctx, const qr_moe_layer* L, float* x, const float* xb, int T,
                            int order, int32_t* idx_out, float* w_out);
 
+/* ---- single-token decode step (forward_runtime, src/runtime.c:94-288) ---- */
+
+/* KV cache row formats.  F32 is the reference's kv_cache_type 0
+ * (src/runtime.c:74-92).  Q8_0 rows are quantize_row_q8_0 (src/quant.c:143-158)
+ * of each position's kv_dim values, read back as qs * d like dequantize_row:
+ * the reference's own type 2 is declared but unimplemented (kv_store_row
+ * writes fp32 into a buffer sized at one byte per element, src/runtime.c:74-84
+ * against src/model.c:82-88). */
+#define QR_KV_F32 0
+#define QR_KV_Q8_0 2
+
+/* Bytes of one position's K (or V) row: kv_dim floats, or kv_dim / 32 Q8_0
+ * blocks; 0 for a bad type or size. */
+size_t qr_kv_row_bytes(int kv_type, int kv_dim);
+
+/* dequantize_row (src/quant.c:160-240) of `rows` rows of n elements each
+ * (row stride qr_row_bytes(type, n)); a null src or an unknown type gives
+ * zeros, as there.  out is [rows][n] fp32. */
+int qr_dequantize(qr_ctx* ctx, uint32_t type, const void* src, int rows, int n, float* out);
+
+/* rmsnorm_ref (src/kernels.c:170-180): o = w * (x * (1 / sqrtf(sum x^2 / n +
+ * 1e-5))), the sum of squares formed in index order.  With add non-null, x +=
+ * add first (the residual of src/runtime.c:196-198) and x is updated.
+ * n <= 8192. */
+int qr_rmsnorm(qr_ctx* ctx, float* o, float* x, const float* add, const float* w, int n);
+
+/* The attention of forward_runtime (src/runtime.c:136-193) over positions
+ * 0..npos-1 of a paged cache: position t's row is at page ptab[t / page],
+ * slot t % page (rows of qr_kv_row_bytes(kv_type, n_kv_heads * head_dim)
+ * bytes, kv head h's elements at h * head_dim).  Scores are dot_ref
+ * (src/kernels.c:162-168) times 1 / sqrtf(head_dim), softmax_ref per head,
+ * then each output element sums att * v over the positions in order.
+ * q, out: [n_heads][head_dim]; att: scratch [n_heads][npos] (left holding the
+ * normalised weights).  head_dim a multiple of 32 up to 512; npos <= 32768. */
+int qr_attention(qr_ctx* ctx, const float* q, const void* kc, const void* vc,
+                 const int32_t* ptab, int page, int kv_type, int npos, int n_heads,
+                 int n_kv_heads, int head_dim, float* att, float* out);
+
+/* One transformer layer's device weights (src/model.c:358-434): attention
+ * projections [rows][cols] in GGUF row order (wq [n_heads * head_dim][dim],
+ * wk / wv [n_kv_heads * head_dim][dim], wo [dim][n_heads * head_dim]) and the
+ * MoE block (moe.dim == dim). */
+typedef struct {
+    const float* rms_att;  /* [dim] */
+    const float* rms_ffn;  /* [dim] */
+    const void* wq;
+    const void* wk;
+    const void* wv;
+    const void* wo;
+    uint32_t wq_type, wk_type, wv_type, wo_type;
+    qr_moe_layer moe;
+} qr_layer;
+
+/* A MoE decoder's device weights (Config / TransformerWeights,
+ * include/types.h).  head_dim is explicit; the reference fixes it at
+ * dim / n_heads (src/runtime.c:102), which this generalises.  tok_embd holds
+ * vocab rows of qr_row_bytes(tok_type, dim) bytes; wcls is [vocab][dim].
+ * `layers` is a host array of n_layers entries (copied at creation). */
+typedef struct {
+    int dim;
+    int n_heads;
+    int n_kv_heads;
+    int head_dim;
+    int n_layers;
+    int vocab;
+    int seq_len;     /* KV cache capacity in positions */
+    float rope_base; /* rope_freq_base; <= 0 means 10000 */
+    const void* tok_embd;
+    uint32_t tok_type;
+    const float* rms_final;
+    const void* wcls;
+    uint32_t wcls_type;
+    const qr_layer* layers;
+} qr_model;
+
+typedef struct qr_decoder qr_decoder;
+
+/* Replay the decode step as one HIP graph (captured on the second call and
+ * again whenever logits / x_out change). */
+#define QR_DEC_GRAPH 1
+
+/* A decoder over `model` (its weights stay the caller's): the activations, a
+ * paged KV cache of seq_len positions per layer (pages of `page` positions,
+ * 0 = 256; identity page table), and the RoPE cos / sin of every position,
+ * computed at creation with the host C library's powf / cosf / sinf as
+ * apply_rope calls them (src/runtime.c:19-41; its frequency index runs over
+ * the whole q vector, as there).  `order` is the reference build
+ * (QR_ORDER_*): the order of the fp32 matmuls and the router, and of the
+ * Q8_0 dot. */
+int qr_decoder_create(qr_ctx* ctx, const qr_model* model, int kv_type, int order, int page,
+                      int flags, qr_decoder** out);
+int qr_decoder_destroy(qr_decoder* dec);
+
+/* Replace the page table: table is host [n_layers][pages_per_layer], each
+ * layer a permutation of 0 .. pages_per_layer - 1. */
+int qr_decoder_set_pages(qr_decoder* dec, const int32_t* table);
+int qr_decoder_pages(const qr_decoder* dec, int* pages_per_layer, int* page);
+
+/* Fill positions [pos0, pos0 + n) of layer `layer`'s cache from fp32 K and V
+ * values (device [n][n_kv_heads * head_dim], after RoPE): a prefill. */
+int qr_decoder_kv_write(qr_decoder* dec, int layer, int pos0, int n, const float* k,
+                        const float* v);
+/* Device addresses of the K and V rows of one position (synchronous). */
+int qr_decoder_kv_rows(const qr_decoder* dec, int layer, int pos, const void** krow,
+                       const void** vrow);
+
+/* forward_runtime (src/runtime.c:94-288) for `token` at position `pos`: the
+ * cache must hold positions 0 .. pos-1; this step writes position pos.
+ * logits: device [vocab]; x_out (optional): device [dim], the residual after
+ * the last layer.  Enqueued on the context's stream. */
+int qr_decoder_forward(qr_decoder* dec, int token, int pos, float* logits, float* x_out);
+
 /* ---- weight registry (host pointer -> device copy) ---------------------- */
 
 /* Upload `bytes` from host memory once and return the device copy; later

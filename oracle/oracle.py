@@ -127,6 +127,7 @@ class Oracle:
         L.qro_kv_row_bytes.argtypes = [C.c_int, C.c_int]
         L.qro_attention.argtypes = [_f32p, _f32p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_int,
                                     C.c_int, C.c_int, C.c_int, C.c_int, _f32p]
+        L.qro_kv_store.argtypes = [C.c_void_p, _f32p, C.c_int, C.c_int]
         L.qro_forward.argtypes = [C.POINTER(OModel), C.c_void_p, C.c_void_p, C.c_int, C.c_int,
                                   C.c_int, _f32p, _f32p]
         L.qro_moe_dispatch.restype = C.c_int
@@ -331,6 +332,33 @@ class Oracle:
             self.lib.qro_forward(C.byref(om), _ptr(kc), _ptr(vc), int(tok), i, order, x, lo)
             lg[i], xs[i] = lo, x
         return lg, xs
+
+    def forward_cached(self, m, kc, vc, tokens, pos0, order, kv_type):
+        """qro_forward for tokens at positions pos0, pos0 + 1, ... over a cache
+        that already holds positions 0 .. pos0 - 1 (kc / vc: uint8
+        [n_layers * seq_len * row bytes], updated in place)."""
+        keep = []
+        om = self.make_model(keep, m, kv_type)
+        lg = np.zeros((len(tokens), m["vocab"]), np.float32)
+        xs = np.zeros((len(tokens), m["dim"]), np.float32)
+        for i, tok in enumerate(tokens):
+            x = np.zeros(m["dim"], np.float32)
+            lo = np.zeros(m["vocab"], np.float32)
+            self.lib.qro_forward(C.byref(om), _ptr(kc), _ptr(vc), int(tok), pos0 + i, order, x,
+                                 lo)
+            lg[i], xs[i] = lo, x
+        return lg, xs
+
+    def kv_rows(self, vals, kv_type):
+        """Cache rows (uint8 [n][row bytes]) of fp32 values [n][kv_dim]:
+        qro_kv_store of each row."""
+        vals = np.ascontiguousarray(vals, np.float32)
+        n, kvd = vals.shape
+        rs = self.kv_row_bytes(kv_type, kvd)
+        out = np.zeros((n, rs), np.uint8)
+        for t in range(n):
+            self.lib.qro_kv_store(_ptr(out[t]), vals[t], kvd, kv_type)
+        return out
 
     def dispatch(self, idx, E):
         idx = np.ascontiguousarray(idx, np.int32)

@@ -1,0 +1,953 @@
+// qr_decode.hip -- quantr-in-c's single-token decode step (forward_runtime,
+// src/runtime.c:94-288) on gfx950, bit-exact with the reference's arithmetic:
+//
+//   x  = dequantize_row(token embedding)                 src/runtime.c:108-113
+//   per layer:
+//     xb = rmsnorm_ref(x, rms_att)                        src/kernels.c:170-180
+//     q, k, v = Wq xb, Wk xb, Wv xb     (matmul_q)         src/runtime.c:124-126
+//     apply_rope(q, k)                                     src/runtime.c:19-41
+//     K[pos], V[pos] = k, v             (fp32 or Q8_0 rows)
+//     att[h][t] = dot_ref(q_h, K[t]_h) / sqrt(head_dim)    src/runtime.c:136-160
+//     att[h] = softmax_ref(att[h])                         src/runtime.c:162-168
+//     o_h[i] = sum over t, in order, of att[h][t] V[t]_h[i] src/runtime.c:170-193
+//     x += Wo o;  xb = rmsnorm_ref(x, rms_ffn)             src/runtime.c:195-200
+//     x += MoE(xb)                                         src/runtime.c:202-269
+//   logits = wcls rmsnorm_ref(x, rms_final)               src/runtime.c:286-287
+//
+// The sums the reference forms one term at a time (rmsnorm's sum of squares,
+// softmax's denominator, each attention output element over the positions)
+// are formed the same way here: one lane adds the terms in order, while other
+// lanes produce the terms (squares, exponentials, attention-weighted values)
+// into LDS ahead of it.  The cos / sin of RoPE come from a table the decoder
+// builds at set-up with the host C library's powf / cosf / sinf, the
+// functions apply_rope calls, for every position of the cache.
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "qr_common.h"
+#include "qr_internal.h"
+
+namespace qr {
+
+// ---------------------------------------------------------------------------
+// Element e of a row of `type` (dequantize_row, src/quant.c:160-240).
+// ---------------------------------------------------------------------------
+__device__ inline float deq_elem(const uint8_t* __restrict__ row, int type, int e) {
+  if (type == QR_T_F32) return reinterpret_cast<const float*>(row)[e];
+  if (type == QR_T_Q8_0) {
+    const uint8_t* b = row + (size_t)(e >> 5) * QR_Q8_BYTES;
+    const float d = qr_h2f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+    return (float)(int8_t)b[2 + (e & 31)] * d;
+  }
+  const int i = e >> 8, j = (e & 255) >> 5, l = e & 31;
+  if (type == QR_T_Q6_K) {
+    const uint8_t* b = row + (size_t)i * QR_Q6K_BYTES;
+    const float d = qr_h2f((uint32_t)b[208] | ((uint32_t)b[209] << 8));
+    const float sc = (float)(int8_t)b[192 + j] * d;
+    const int ql = (b[(j * 32 + l) >> 1] >> ((l & 1) * 4)) & 0xF;
+    const int qh = (b[128 + ((j * 32 + l) >> 2)] >> (((j * 32 + l) & 3) * 2)) & 3;
+    return (float)((ql | (qh << 4)) - 32) * sc;
+  }
+  // Q4_K / Q5_K
+  const int bb = type == QR_T_Q4_K ? QR_Q4K_BYTES : QR_Q5K_BYTES;
+  const uint8_t* b = row + (size_t)i * bb;
+  const float d = qr_h2f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+  const float dmin = qr_h2f((uint32_t)b[2] | ((uint32_t)b[3] << 8));
+  const float sc = (float)(b[4 + j] & 63) * d;
+  const float m = (float)(b[4 + j] >> 6) * dmin;
+  const int qs0 = type == QR_T_Q4_K ? 16 : 48;
+  int q = (b[qs0 + ((j * 32 + l) >> 1)] >> ((l & 1) * 4)) & 0xF;
+  if (type == QR_T_Q5_K) q |= ((b[16 + ((j * 32 + l) >> 3)] >> ((j * 32 + l) & 7)) & 1) << 4;
+  return (float)q * sc - m;
+}
+
+// out[r][e] = element e of row r (nrows rows of row_bytes; whole blocks of n;
+// unknown types give zeros, as dequantize_row does).
+__global__ __launch_bounds__(256) void k_dequant_rows(const uint8_t* __restrict__ src, int type,
+                                                      size_t row_bytes, int nrows, int n,
+                                                      float* __restrict__ out) {
+  const long total = (long)nrows * n;
+  for (long gi = (long)blockIdx.x * blockDim.x + threadIdx.x; gi < total;
+       gi += (long)gridDim.x * blockDim.x) {
+    const int r = (int)(gi / n), e = (int)(gi - (long)r * n);
+    const bool known = type == QR_T_F32 || type == QR_T_Q8_0 || type == QR_T_Q4_K ||
+                       type == QR_T_Q5_K || type == QR_T_Q6_K;
+    out[gi] = known ? deq_elem(src + (size_t)r * row_bytes, type, e) : 0.0f;
+  }
+}
+
+// The embedding row of the state's token (src/runtime.c:108-113).
+__global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ tab, int type,
+                                               size_t row_bytes, const int32_t* __restrict__ st,
+                                               int n, float* __restrict__ x) {
+  const int token = st[0];
+  const uint8_t* row = tab + (size_t)token * row_bytes;
+  for (int e = threadIdx.x; e < n; e += blockDim.x) x[e] = deq_elem(row, type, e);
+}
+
+// ---------------------------------------------------------------------------
+// rmsnorm_ref (src/kernels.c:170-180), optionally after x += add (the
+// residual of src/runtime.c:196-198): the squares go to LDS in parallel, lane
+// 0 adds them in order, the workgroup scales.  n <= kNormMax.
+// ---------------------------------------------------------------------------
+constexpr int kNormMax = 8192;
+
+__global__ __launch_bounds__(256) void k_rmsnorm(float* __restrict__ x,
+                                                 const float* __restrict__ add,
+                                                 const float* __restrict__ w, int n,
+                                                 float* __restrict__ o) {
+  __shared__ __align__(16) float sq[kNormMax];
+  __shared__ float scale_s;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    float xi = x[i];
+    if (add) {
+      xi = xi + add[i];
+      x[i] = xi;
+    }
+    sq[i] = xi * xi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float ss = 0.0f;
+    int i = 0;
+    for (; i + 16 <= n; i += 16) {
+      float4 v[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) v[k] = *reinterpret_cast<const float4*>(sq + i + 4 * k);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        ss += v[k].x;
+        ss += v[k].y;
+        ss += v[k].z;
+        ss += v[k].w;
+      }
+    }
+    for (; i < n; i++) ss += sq[i];
+    ss = ss / (float)n + 1e-5f;
+    scale_s = 1.0f / sqrtf(ss);
+  }
+  __syncthreads();
+  const float scale = scale_s;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) o[i] = w[i] * (x[i] * scale);
+}
+
+// ---------------------------------------------------------------------------
+// apply_rope (src/runtime.c:19-41) of q (qd) and k (the first kvd of its
+// pairs) with the position's cos / sin, then the K and V rows of the
+// position: fp32 copies or quantize_row_q8_0 (src/quant.c:143-158) blocks.
+// One workgroup; kvd <= kRopeKvMax.
+// ---------------------------------------------------------------------------
+constexpr int kRopeKvMax = 4096;
+
+__device__ inline void q8_block_store(const float* __restrict__ v, uint8_t* __restrict__ out) {
+  float amax = 0.0f;
+  for (int j = 0; j < 32; j++) {
+    const float av = __builtin_fabsf(v[j]);
+    amax = av > amax ? av : amax;
+  }
+  const float dd = amax / 127.0f;
+  const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+  const uint32_t dh = qr_f2h(dd);
+  out[0] = (uint8_t)(dh & 0xFFu);
+  out[1] = (uint8_t)(dh >> 8);
+  for (int j = 0; j < 32; j++) out[2 + j] = (uint8_t)(int8_t)(int)__builtin_rintf(v[j] * id);
+}
+
+// Where position t's row of one layer's K or V cache lives: pages of `page`
+// positions, logical page t / page at physical page ptab[t / page].
+struct KvView {
+  const uint8_t* base;  // K or V pages
+  const int32_t* ptab;  // this layer's page table
+  int page;
+  size_t row_bytes;
+  int kv_type;
+  __device__ const uint8_t* row(int t) const {
+    const int pp = ptab[t / page];
+    return base + ((size_t)pp * page + (size_t)(t % page)) * row_bytes;
+  }
+};
+
+// npos = st[1] + 1 when the position comes from device state (a captured
+// decode step), else the argument.
+__device__ inline int npos_of(const int32_t* st, int npos) { return st ? st[1] + 1 : npos; }
+
+__global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ q, const float* __restrict__ k,
+                                                 const float* __restrict__ v,
+                                                 const float* __restrict__ rope,
+                                                 const int32_t* __restrict__ st, int qd, int kvd,
+                                                 KvView K, uint8_t* __restrict__ vbase) {
+  __shared__ __align__(16) float ks[kRopeKvMax];
+  __shared__ __align__(16) float vs[kRopeKvMax];
+  const int pos = st[1];
+  const float* cs = rope + (size_t)pos * qd;
+  for (int p = threadIdx.x; p < qd / 2; p += blockDim.x) {
+    const int i = 2 * p;
+    const float c = cs[i], s = cs[i + 1];
+    const float q0 = q[i], q1 = q[i + 1];
+    q[i] = q0 * c - q1 * s;
+    q[i + 1] = q0 * s + q1 * c;
+    if (i < kvd) {
+      const float k0 = k[i], k1 = k[i + 1];
+      ks[i] = k0 * c - k1 * s;
+      ks[i + 1] = k0 * s + k1 * c;
+    }
+  }
+  for (int i = threadIdx.x; i < kvd; i += blockDim.x) vs[i] = v[i];
+  __syncthreads();
+  uint8_t* krow = const_cast<uint8_t*>(K.row(pos));
+  uint8_t* vrow = vbase + (size_t)(krow - K.base);
+  if (K.kv_type == QR_KV_Q8_0) {
+    const int nb = kvd / 32;
+    for (int b = threadIdx.x; b < 2 * nb; b += blockDim.x) {
+      const bool isv = b >= nb;
+      const int bi = isv ? b - nb : b;
+      q8_block_store((isv ? vs : ks) + 32 * bi, (isv ? vrow : krow) + (size_t)bi * QR_Q8_BYTES);
+    }
+  } else {
+    float* kf = reinterpret_cast<float*>(krow);
+    float* vf = reinterpret_cast<float*>(vrow);
+    for (int i = threadIdx.x; i < kvd; i += blockDim.x) {
+      kf[i] = ks[i];
+      vf[i] = vs[i];
+    }
+  }
+}
+
+// Rows [t0, t0 + n) of one layer's K and V caches from fp32 values
+// (src [n][kvd]): fp32 copies or quantize_row_q8_0 blocks.  One thread per
+// 32-element block.
+__global__ __launch_bounds__(256) void k_kv_write(const float* __restrict__ ksrc,
+                                                  const float* __restrict__ vsrc, int t0, int n,
+                                                  int kvd, KvView K, uint8_t* __restrict__ vbase) {
+  const int nb = kvd / 32;
+  const long total = 2L * n * nb;
+  for (long g = (long)blockIdx.x * blockDim.x + threadIdx.x; g < total;
+       g += (long)gridDim.x * blockDim.x) {
+    const bool isv = g >= (long)n * nb;
+    const long r = isv ? g - (long)n * nb : g;
+    const int t = (int)(r / nb), b = (int)(r - (long)t * nb);
+    const float* src = (isv ? vsrc : ksrc) + (size_t)t * kvd + 32 * b;
+    uint8_t* krow = const_cast<uint8_t*>(K.row(t0 + t));
+    uint8_t* row = isv ? vbase + (size_t)(krow - K.base) : krow;
+    if (K.kv_type == QR_KV_Q8_0) {
+      float vals[32];
+      for (int j = 0; j < 32; j++) vals[j] = src[j];
+      q8_block_store(vals, row + (size_t)b * QR_Q8_BYTES);
+    } else {
+      float* dst = reinterpret_cast<float*>(row) + 32 * b;
+      for (int j = 0; j < 32; j++) dst[j] = src[j];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Attention (src/runtime.c:136-193).
+// ---------------------------------------------------------------------------
+constexpr int kHdMax = 512;          // the reference's own bound (kh_buf[512], src/runtime.c:145)
+constexpr int kSoftMaxMax = 32768;   // positions: the softmax's exponentials stay in LDS
+constexpr size_t kDecLdsMax = 160 * 1024;
+
+// att[h][t] = dot_ref(q_h, K[t]_kvh) * inv_sqrt for the kv_mul query heads of
+// kv head blockIdx.y and positions [64 blockIdx.x, +64): the K tile is
+// dequantized once into LDS (rows padded to hd + 1 floats), then one thread
+// per (head, position) adds the hd products in order.  Dynamic LDS:
+// (64 (hd + 1) + kv_mul hd) floats.
+constexpr int kScTile = 64;
+
+__global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q, KvView K,
+                                                     const int32_t* __restrict__ st, int npos_arg,
+                                                     int kv_mul, int hd, float inv_sqrt,
+                                                     int att_stride, float* __restrict__ att) {
+  extern __shared__ __align__(16) float sm[];
+  const int npos = npos_of(st, npos_arg);
+  const int t0 = blockIdx.x * kScTile;
+  if (t0 >= npos) return;
+  const int kvh = blockIdx.y;
+  const int ks = hd + 1;
+  float* kt = sm;
+  float* qs = sm + kScTile * ks;
+  const int nt = min(kScTile, npos - t0);
+  for (int i = threadIdx.x; i < kv_mul * hd; i += blockDim.x)
+    qs[i] = q[(size_t)kvh * kv_mul * hd + i];
+  if (K.kv_type == QR_KV_Q8_0) {
+    const int bpr = hd / 32;
+    for (int j = threadIdx.x; j < nt * bpr; j += blockDim.x) {
+      const int tt = j / bpr, b = j - tt * bpr;
+      const uint16_t* hw =
+          reinterpret_cast<const uint16_t*>(K.row(t0 + tt) + (size_t)(kvh * bpr + b) * QR_Q8_BYTES);
+      const float d = qr_h2f(hw[0]);
+      float* dst = kt + tt * ks + 32 * b;
+#pragma unroll
+      for (int w = 0; w < 16; w++) {
+        const uint32_t u = hw[1 + w];
+        dst[2 * w] = (float)(int8_t)(u & 0xFFu) * d;
+        dst[2 * w + 1] = (float)(int8_t)(u >> 8) * d;
+      }
+    }
+  } else {
+    for (int j = threadIdx.x; j < nt * hd; j += blockDim.x) {
+      const int tt = j / hd, i = j - tt * hd;
+      kt[tt * ks + i] = reinterpret_cast<const float*>(K.row(t0 + tt))[(size_t)kvh * hd + i];
+    }
+  }
+  __syncthreads();
+  for (int p = threadIdx.x; p < kv_mul * kScTile; p += blockDim.x) {
+    const int m = p / kScTile, tt = p - m * kScTile;
+    if (tt >= nt) continue;
+    const float* qh = qs + m * hd;
+    const float* kr = kt + tt * ks;
+    float s = 0.0f;
+    for (int i = 0; i < hd; i++) s += qh[i] * kr[i];
+    att[(size_t)(kvh * kv_mul + m) * att_stride + t0 + tt] = s * inv_sqrt;
+  }
+}
+
+// softmax_ref (src/kernels.c:191-207) of each head's npos scores, one
+// workgroup per head: the max over the workgroup (order-free: a max is
+// exact), the exponentials into LDS in parallel, lane 0 adds them in order,
+// then the workgroup scales.  Dynamic LDS: npos floats (the cache capacity).
+__global__ __launch_bounds__(256) void k_attn_softmax(float* __restrict__ att, int att_stride,
+                                                      const int32_t* __restrict__ st,
+                                                      int npos_arg) {
+  extern __shared__ __align__(16) float e[];
+  __shared__ float red[4];
+  __shared__ float inv_s;
+  const int npos = npos_of(st, npos_arg);
+  float* a = att + (size_t)blockIdx.x * att_stride;
+  const ExpTab tab = qr_expf_tab();
+  float mx = a[0];
+  for (int i = threadIdx.x; i < npos; i += blockDim.x) {
+    const float v = a[i];
+    mx = v > mx ? v : mx;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v = __shfl_xor(mx, o);
+    mx = v > mx ? v : mx;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); w++) mx = red[w] > mx ? red[w] : mx;
+  // every lane runs the same number of rounds: the table lookup of
+  // qr_expf_w reads other lanes
+  const int rounds = (npos + blockDim.x - 1) / blockDim.x;
+  for (int r = 0; r < rounds; r++) {
+    const int i = r * blockDim.x + threadIdx.x;
+    const float v = i < npos ? a[i] : 0.0f;
+    const float ev = qr_expf_w(v - mx, tab);
+    if (i < npos) e[i] = ev;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float sum = 0.0f;
+    int i = 0;
+    for (; i + 16 <= npos; i += 16) {
+      float4 v[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) v[k] = *reinterpret_cast<const float4*>(e + i + 4 * k);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        sum += v[k].x;
+        sum += v[k].y;
+        sum += v[k].z;
+        sum += v[k].w;
+      }
+    }
+    for (; i < npos; i++) sum += e[i];
+    inv_s = 1.0f / sum;
+  }
+  __syncthreads();
+  const float inv = inv_s;
+  for (int i = threadIdx.x; i < npos; i += blockDim.x) a[i] = e[i] * inv;
+}
+
+// o_h[c] = sum over t = 0 .. npos-1, in order, of att[h][t] * V[t]_kvh[c]
+// (src/runtime.c:182-190: each product rounded, then added).  A workgroup
+// owns kValCols elements of one head.  Waves 1..7 form the products of a
+// block of kValBlk positions into LDS (element-major, so one ds_read_b128
+// gives an element four consecutive positions) while lanes 0..31 of wave 0
+// add the previous block's products in position order.  grid
+// (hd / kValCols, n_heads), 512 threads.
+constexpr int kValCols = 32;
+constexpr int kValBlk = 128;
+constexpr int kValPitch = kValBlk + 4;
+
+__global__ __launch_bounds__(512) void k_attn_values(const float* __restrict__ att, int att_stride,
+                                                     KvView V, const int32_t* __restrict__ st,
+                                                     int npos_arg, int kv_mul, int hd,
+                                                     float* __restrict__ out) {
+  __shared__ __align__(16) float prod[2][kValCols * kValPitch];
+  const int npos = npos_of(st, npos_arg);
+  const int h = blockIdx.y;
+  const int c0 = blockIdx.x * kValCols;
+  const int kvh = h / kv_mul;
+  const float* a = att + (size_t)h * att_stride;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nblk = (npos + kValBlk - 1) / kValBlk;
+  // products of block b into buffer b & 1: item j = (position tt = j % kValBlk,
+  // elements 4 (j / kValBlk) .. +3)
+  auto produce = [&](int b) {
+    float* pb = prod[b & 1];
+    const int t0 = b * kValBlk;
+    for (int j = threadIdx.x - 64; j < kValBlk * (kValCols / 4); j += 448) {
+      const int tt = j % kValBlk, cg = j / kValBlk;
+      const int t = t0 + tt;
+      float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+      if (t < npos) {
+        const float at = a[t];
+        const uint8_t* row = V.row(t);
+        const int e0 = kvh * hd + c0 + 4 * cg;
+        float v0, v1, v2, v3;
+        if (V.kv_type == QR_KV_Q8_0) {
+          const uint8_t* blk = row + (size_t)(e0 >> 5) * QR_Q8_BYTES;
+          const uint16_t* hw = reinterpret_cast<const uint16_t*>(blk);
+          const float d = qr_h2f(hw[0]);
+          const int o = (e0 & 31) >> 1;  // even element offset -> halfword index
+          const uint32_t u0 = hw[1 + o], u1 = hw[2 + o];
+          v0 = (float)(int8_t)(u0 & 0xFFu) * d;
+          v1 = (float)(int8_t)(u0 >> 8) * d;
+          v2 = (float)(int8_t)(u1 & 0xFFu) * d;
+          v3 = (float)(int8_t)(u1 >> 8) * d;
+        } else {
+          const float4 f = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(row) + e0);
+          v0 = f.x;
+          v1 = f.y;
+          v2 = f.z;
+          v3 = f.w;
+        }
+        p0 = at * v0;
+        p1 = at * v1;
+        p2 = at * v2;
+        p3 = at * v3;
+      }
+      const int c = 4 * cg;
+      pb[(c + 0) * kValPitch + tt] = p0;
+      pb[(c + 1) * kValPitch + tt] = p1;
+      pb[(c + 2) * kValPitch + tt] = p2;
+      pb[(c + 3) * kValPitch + tt] = p3;
+    }
+  };
+  float acc = 0.0f;
+  if (wave > 0) produce(0);
+  __syncthreads();
+  for (int b = 0; b < nblk; b++) {
+    if (wave > 0) {
+      if (b + 1 < nblk) produce(b + 1);
+    } else if (lane < kValCols) {
+      const float* pb = prod[b & 1] + lane * kValPitch;
+      const int cnt = min(kValBlk, npos - b * kValBlk);
+      if (cnt == kValBlk) {
+#pragma unroll
+        for (int tt = 0; tt < kValBlk; tt += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(pb + tt);
+          acc += v.x;
+          acc += v.y;
+          acc += v.z;
+          acc += v.w;
+        }
+      } else {
+        for (int tt = 0; tt < cnt; tt++) acc += pb[tt];
+      }
+    }
+    __syncthreads();
+  }
+  if (wave == 0 && lane < kValCols) out[(size_t)h * hd + c0 + lane] = acc;
+}
+
+}  // namespace qr
+
+// ===========================================================================
+// Host side.
+// ===========================================================================
+using namespace qr;
+
+struct qr_decoder {
+  qr_ctx* ctx = nullptr;
+  int device = 0;
+  int dim = 0, nh = 0, nkv = 0, hd = 0, nl = 0, vocab = 0, cap = 0;
+  int qd = 0, kvd = 0, kv_mul = 0;
+  const void* tok_embd = nullptr;
+  uint32_t tok_type = 0;
+  size_t tok_row = 0;
+  const float* rms_final = nullptr;
+  const void* wcls = nullptr;
+  uint32_t wcls_type = 0;
+  std::vector<qr_layer> layers;
+  int kv_type = QR_KV_Q8_0, order = QR_ORDER_SEQ, page = 0, ppl = 0, flags = 0;
+  size_t row_bytes = 0;
+  uint8_t* kc = nullptr;  // K pages, all layers
+  uint8_t* vc = nullptr;  // V pages, all layers
+  size_t layer_pages_bytes = 0;
+  int32_t* ptab = nullptr;  // [layer][ppl]
+  float* rope = nullptr;    // [cap][qd]
+  int32_t* st = nullptr;    // token, pos
+  float *x = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
+  float *ao = nullptr, *att = nullptr;
+  uint8_t* moe_base = nullptr;  // MoE scratch, carved per layer
+  void* mem = nullptr;  // activations, state, page table, RoPE table, MoE scratch
+  size_t sc_lds = 0;    // k_attn_scores' dynamic LDS
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  float* graph_logits = nullptr;
+  float* graph_xout = nullptr;
+  int calls = 0;
+};
+
+namespace {
+
+std::atomic<bool> g_sc_opt[64];
+std::atomic<bool> g_sm_opt[64];
+
+#define DEC_HIP(call, what)                                                        \
+  do {                                                                             \
+    hipError_t e_ = (call);                                                        \
+    if (e_ != hipSuccess) return set_error(QR_ERR_HIP, "%s: %s", what, hipGetErrorString(e_)); \
+  } while (0)
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+KvView kv_view(const qr_decoder* d, int layer, bool values) {
+  KvView K;
+  K.base = (values ? d->vc : d->kc) + (size_t)layer * d->layer_pages_bytes;
+  K.ptab = d->ptab + (size_t)layer * d->ppl;
+  K.page = d->page;
+  K.row_bytes = d->row_bytes;
+  K.kv_type = d->kv_type;
+  return K;
+}
+
+// out[n] = W x for one token: matmul_q (src/runtime.c:58-70): fp32 weights
+// go through the build's KernelOps.matmul order, quantized ones through the
+// fused GEMV with the build's Q8_0 dot order.
+hipError_t matmul_q_dev(const void* w, uint32_t type, int order, const float* x, float* y, int n,
+                        int dd, hipStream_t s) {
+  if (type == QR_T_F32)
+    return gemv_f32_launch(order, static_cast<const float*>(w), x, y, n, dd, 1, dd, n, s);
+  return gemv_launch((int)type, order, w, x, y, n, dd, 1, dd, n, nullptr, nullptr, s);
+}
+
+// The decode step's kernels, in order, on stream s (the state holds the
+// token and the position).
+hipError_t enqueue_step(qr_decoder* d, float* logits, float* xout, hipStream_t s) {
+  hipError_t e;
+  const int dim = d->dim;
+  hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s,
+                     static_cast<const uint8_t*>(d->tok_embd), (int)d->tok_type, d->tok_row,
+                     d->st, dim, d->x);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const float inv_sqrt = 1.0f / sqrtf((float)d->hd);
+  for (int l = 0; l < d->nl; l++) {
+    const qr_layer& L = d->layers[l];
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), 0, s, d->x, (const float*)nullptr,
+                       L.rms_att, dim, d->xb);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = matmul_q_dev(L.wq, L.wq_type, d->order, d->xb, d->q, d->qd, dim, s))) return e;
+    if ((e = matmul_q_dev(L.wk, L.wk_type, d->order, d->xb, d->k, d->kvd, dim, s))) return e;
+    if ((e = matmul_q_dev(L.wv, L.wv_type, d->order, d->xb, d->v, d->kvd, dim, s))) return e;
+    const KvView K = kv_view(d, l, false), V = kv_view(d, l, true);
+    hipLaunchKernelGGL(k_rope_kv, dim3(1), dim3(256), 0, s, d->q, d->k, d->v, d->rope, d->st,
+                       d->qd, d->kvd, K, const_cast<uint8_t*>(V.base));
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_scores, dim3((d->cap + kScTile - 1) / kScTile, d->nkv), dim3(256),
+                       d->sc_lds, s, d->q, K, d->st, 0, d->kv_mul, d->hd, inv_sqrt, d->cap,
+                       d->att);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_softmax, dim3(d->nh), dim3(256), (size_t)d->cap * 4, s, d->att,
+                       d->cap, d->st, 0);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_values, dim3(d->hd / kValCols, d->nh), dim3(512), 0, s, d->att,
+                       d->cap, V, d->st, 0, d->kv_mul, d->hd, d->ao);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = matmul_q_dev(L.wo, L.wo_type, d->order, d->ao, d->xb2, dim, d->qd, s))) return e;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), 0, s, d->x, (const float*)d->xb2,
+                       L.rms_ffn, dim, d->xb);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    MoeScratch ms;
+    moe_scratch_carve(d->moe_base, &L.moe, 1, &ms);
+    if ((e = moe_forward_launch(&L.moe, d->x, d->xb, 1, d->order, ms, s))) return e;
+  }
+  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), 0, s, d->x, (const float*)nullptr,
+                     d->rms_final, dim, d->xb);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if ((e = matmul_q_dev(d->wcls, d->wcls_type, d->order, d->xb, logits, d->vocab, dim, s)))
+    return e;
+  if (xout) {
+    if ((e = hipMemcpyAsync(xout, d->x, (size_t)dim * 4, hipMemcpyDeviceToDevice, s))) return e;
+  }
+  return hipSuccess;
+}
+
+__global__ void k_set_state(int32_t* st, int token, int pos) {
+  if (threadIdx.x == 0) {
+    st[0] = token;
+    st[1] = pos;
+  }
+}
+
+void drop_graph(qr_decoder* d) {
+  if (d->exec) (void)hipGraphExecDestroy(d->exec);
+  if (d->graph) (void)hipGraphDestroy(d->graph);
+  d->exec = nullptr;
+  d->graph = nullptr;
+}
+
+int check_layer_weights(const qr_model* m, int l, int order) {
+  const qr_layer& L = m->layers[l];
+  const int hd = m->head_dim, qd = m->n_heads * hd, kvd = m->n_kv_heads * hd;
+  if (!L.rms_att || !L.rms_ffn || !L.wq || !L.wk || !L.wv || !L.wo)
+    return set_error(QR_ERR_INVALID, "qr_decoder_create: layer %d has a null tensor", l);
+  int rc;
+  if ((rc = gemv_check(L.wq_type, order, L.wq, qd, m->dim, "qr_decoder_create: wq"))) return rc;
+  if ((rc = gemv_check(L.wk_type, order, L.wk, kvd, m->dim, "qr_decoder_create: wk"))) return rc;
+  if ((rc = gemv_check(L.wv_type, order, L.wv, kvd, m->dim, "qr_decoder_create: wv"))) return rc;
+  if ((rc = gemv_check(L.wo_type, order, L.wo, m->dim, qd, "qr_decoder_create: wo"))) return rc;
+  if ((rc = moe_check(&L.moe, "qr_decoder_create: moe"))) return rc;
+  if (L.moe.dim != m->dim)
+    return set_error(QR_ERR_INVALID, "qr_decoder_create: layer %d moe.dim %d != dim %d", l,
+                     L.moe.dim, m->dim);
+  return QR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t qr_kv_row_bytes(int kv_type, int kv_dim) {
+  if (kv_dim <= 0) return 0;
+  if (kv_type == QR_KV_Q8_0) return kv_dim % 32 ? 0 : (size_t)(kv_dim / 32) * QR_Q8_BYTES;
+  if (kv_type == QR_KV_F32) return (size_t)kv_dim * 4;
+  return 0;
+}
+
+int qr_dequantize(qr_ctx* c, uint32_t type, const void* src, int rows, int n, float* out) {
+  if (!c) return set_error(QR_ERR_INVALID, "qr_dequantize: null ctx");
+  if (rows < 0 || n < 0) return set_error(QR_ERR_INVALID, "qr_dequantize: negative size");
+  if ((long)rows * n == 0) return QR_OK;
+  if (!out) return set_error(QR_ERR_INVALID, "qr_dequantize: null out");
+  const size_t rb = qr_row_bytes(type, n);
+  const bool known = type == QR_T_F32 || type == QR_T_Q8_0 || type == QR_T_Q4_K ||
+                     type == QR_T_Q5_K || type == QR_T_Q6_K;
+  if (known && n % qr_block_elems((int)type))
+    return set_error(QR_ERR_INVALID, "qr_dequantize: n=%d is not whole blocks", n);
+  DEC_HIP(hipSetDevice(ctx_device(c)), "hipSetDevice");
+  long grid = ((long)rows * n + 255) / 256;
+  if (grid > 4096) grid = 4096;
+  // no source (src/quant.c:161-164) or an unknown type: zeros
+  hipLaunchKernelGGL(k_dequant_rows, dim3((unsigned)grid), dim3(256), 0, ctx_stream(c),
+                     static_cast<const uint8_t*>(src), src ? (int)type : -1, rb, rows, n, out);
+  DEC_HIP(hipGetLastError(), "k_dequant_rows");
+  return QR_OK;
+}
+
+int qr_rmsnorm(qr_ctx* c, float* o, float* x, const float* add, const float* w, int n) {
+  if (!c) return set_error(QR_ERR_INVALID, "qr_rmsnorm: null ctx");
+  if (n <= 0 || n > kNormMax) return set_error(QR_ERR_INVALID, "qr_rmsnorm: n=%d (1..%d)", n, kNormMax);
+  if (!o || !x || !w) return set_error(QR_ERR_INVALID, "qr_rmsnorm: null pointer");
+  DEC_HIP(hipSetDevice(ctx_device(c)), "hipSetDevice");
+  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), 0, ctx_stream(c), x, add, w, n, o);
+  DEC_HIP(hipGetLastError(), "k_rmsnorm");
+  return QR_OK;
+}
+
+int qr_attention(qr_ctx* c, const float* q, const void* kc, const void* vc, const int32_t* ptab,
+                 int page, int kv_type, int npos, int n_heads, int n_kv_heads, int head_dim,
+                 float* att, float* out) {
+  if (!c) return set_error(QR_ERR_INVALID, "qr_attention: null ctx");
+  if (!q || !kc || !vc || !ptab || !att || !out)
+    return set_error(QR_ERR_INVALID, "qr_attention: null pointer");
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads)
+    return set_error(QR_ERR_INVALID, "qr_attention: heads %d / kv heads %d", n_heads, n_kv_heads);
+  if (head_dim <= 0 || head_dim % kValCols || head_dim > kHdMax)
+    return set_error(QR_ERR_INVALID, "qr_attention: head_dim %d (a multiple of 32, <= %d)",
+                     head_dim, kHdMax);
+  if (page <= 0) return set_error(QR_ERR_INVALID, "qr_attention: page %d", page);
+  const size_t rb = qr_kv_row_bytes(kv_type, n_kv_heads * head_dim);
+  if (!rb) return set_error(QR_ERR_INVALID, "qr_attention: kv_type %d", kv_type);
+  if (npos <= 0 || npos > kSoftMaxMax)
+    return set_error(QR_ERR_INVALID, "qr_attention: npos %d (1..%d)", npos, kSoftMaxMax);
+  if (!al16(kc) || !al16(vc)) return set_error(QR_ERR_INVALID, "qr_attention: cache alignment");
+  const int kv_mul = n_heads / n_kv_heads;
+  const size_t sc_lds = ((size_t)kScTile * (head_dim + 1) + (size_t)kv_mul * head_dim) * 4;
+  if (sc_lds > kDecLdsMax) return set_error(QR_ERR_UNSUPPORTED, "qr_attention: head group too large");
+  DEC_HIP(hipSetDevice(ctx_device(c)), "hipSetDevice");
+  DEC_HIP(lds_opt_in((const void*)k_attn_scores, g_sc_opt), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_softmax, g_sm_opt), "lds opt-in");
+  KvView K;
+  K.base = static_cast<const uint8_t*>(kc);
+  K.ptab = ptab;
+  K.page = page;
+  K.row_bytes = rb;
+  K.kv_type = kv_type;
+  KvView V = K;
+  V.base = static_cast<const uint8_t*>(vc);
+  hipStream_t s = ctx_stream(c);
+  const float inv_sqrt = 1.0f / sqrtf((float)head_dim);
+  hipLaunchKernelGGL(k_attn_scores, dim3((npos + kScTile - 1) / kScTile, n_kv_heads), dim3(256),
+                     sc_lds, s, q, K, (const int32_t*)nullptr, npos, kv_mul, head_dim, inv_sqrt,
+                     npos, att);
+  DEC_HIP(hipGetLastError(), "k_attn_scores");
+  hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads), dim3(256), (size_t)npos * 4, s, att, npos,
+                     (const int32_t*)nullptr, npos);
+  DEC_HIP(hipGetLastError(), "k_attn_softmax");
+  hipLaunchKernelGGL(k_attn_values, dim3(head_dim / kValCols, n_heads), dim3(512), 0, s, att, npos,
+                     V, (const int32_t*)nullptr, npos, kv_mul, head_dim, out);
+  DEC_HIP(hipGetLastError(), "k_attn_values");
+  return QR_OK;
+}
+
+int qr_decoder_create(qr_ctx* c, const qr_model* m, int kv_type, int order, int page, int flags,
+                      qr_decoder** out) {
+  if (!out) return set_error(QR_ERR_INVALID, "qr_decoder_create: null out");
+  *out = nullptr;
+  if (!c || !m || !m->layers) return set_error(QR_ERR_INVALID, "qr_decoder_create: null argument");
+  if (order < QR_ORDER_SEQ || order > QR_ORDER_AVX512)
+    return set_error(QR_ERR_INVALID, "qr_decoder_create: order %d", order);
+  if (flags & ~QR_DEC_GRAPH) return set_error(QR_ERR_INVALID, "qr_decoder_create: flags %d", flags);
+  const int dim = m->dim, nh = m->n_heads, nkv = m->n_kv_heads, hd = m->head_dim;
+  if (dim <= 0 || dim > kNormMax || m->n_layers <= 0 || m->vocab <= 0 || m->seq_len <= 0)
+    return set_error(QR_ERR_INVALID, "qr_decoder_create: dim %d, layers %d, vocab %d, seq_len %d",
+                     dim, m->n_layers, m->vocab, m->seq_len);
+  if (nh <= 0 || nkv <= 0 || nh % nkv)
+    return set_error(QR_ERR_INVALID, "qr_decoder_create: heads %d / kv heads %d", nh, nkv);
+  if (hd <= 0 || hd % kValCols || hd > kHdMax)
+    return set_error(QR_ERR_INVALID, "qr_decoder_create: head_dim %d (a multiple of 32, <= %d)",
+                     hd, kHdMax);
+  const int qd = nh * hd, kvd = nkv * hd;
+  if (kvd > kRopeKvMax || qd > kNormMax)
+    return set_error(QR_ERR_UNSUPPORTED, "qr_decoder_create: q length %d / kv length %d", qd, kvd);
+  if (m->seq_len > kSoftMaxMax)
+    return set_error(QR_ERR_UNSUPPORTED, "qr_decoder_create: seq_len %d (<= %d)", m->seq_len,
+                     kSoftMaxMax);
+  const size_t rb = qr_kv_row_bytes(kv_type, kvd);
+  if (!rb) return set_error(QR_ERR_INVALID, "qr_decoder_create: kv_type %d", kv_type);
+  if (page <= 0) page = 256;
+  if (!m->tok_embd || !m->rms_final || !m->wcls)
+    return set_error(QR_ERR_INVALID, "qr_decoder_create: null embedding / final norm / wcls");
+  const bool tok_known = m->tok_type == QR_T_F32 || m->tok_type == QR_T_Q8_0 ||
+                         m->tok_type == QR_T_Q4_K || m->tok_type == QR_T_Q5_K ||
+                         m->tok_type == QR_T_Q6_K;
+  if (!tok_known || dim % qr_block_elems((int)m->tok_type))
+    return set_error(QR_ERR_INVALID, "qr_decoder_create: embedding type %u at dim %d", m->tok_type,
+                     dim);
+  int rc = gemv_check(m->wcls_type, order, m->wcls, m->vocab, dim, "qr_decoder_create: wcls");
+  if (rc) return rc;
+  for (int l = 0; l < m->n_layers; l++)
+    if ((rc = check_layer_weights(m, l, order))) return rc;
+  const int kv_mul = nh / nkv;
+  const size_t sc_lds = ((size_t)kScTile * (hd + 1) + (size_t)kv_mul * hd) * 4;
+  if (sc_lds > kDecLdsMax) return set_error(QR_ERR_UNSUPPORTED, "qr_decoder_create: head group too large");
+
+  DEC_HIP(hipSetDevice(ctx_device(c)), "hipSetDevice");
+  DEC_HIP(lds_opt_in((const void*)k_attn_scores, g_sc_opt), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_softmax, g_sm_opt), "lds opt-in");
+  qr_decoder* d = new (std::nothrow) qr_decoder();
+  if (!d) return set_error(QR_ERR_NOMEM, "qr_decoder_create: host allocation");
+  d->ctx = c;
+  d->device = ctx_device(c);
+  d->dim = dim;
+  d->nh = nh;
+  d->nkv = nkv;
+  d->hd = hd;
+  d->nl = m->n_layers;
+  d->vocab = m->vocab;
+  d->cap = m->seq_len;
+  d->qd = qd;
+  d->kvd = kvd;
+  d->kv_mul = kv_mul;
+  d->tok_embd = m->tok_embd;
+  d->tok_type = m->tok_type;
+  d->tok_row = qr_row_bytes(m->tok_type, dim);
+  d->rms_final = m->rms_final;
+  d->wcls = m->wcls;
+  d->wcls_type = m->wcls_type;
+  d->layers.assign(m->layers, m->layers + m->n_layers);
+  d->kv_type = kv_type;
+  d->order = order;
+  d->page = page;
+  d->ppl = (m->seq_len + page - 1) / page;
+  d->flags = flags;
+  d->row_bytes = rb;
+  d->sc_lds = sc_lds;
+  d->layer_pages_bytes = (size_t)d->ppl * page * rb;
+  d->layer_pages_bytes = (d->layer_pages_bytes + 255) & ~(size_t)255;
+
+  // one allocation: activations, state, page table, RoPE table, MoE scratch
+  size_t moe_bytes = 0;
+  for (int l = 0; l < d->nl; l++) {
+    const size_t b = moe_scratch_bytes(&d->layers[l].moe, 1);
+    if (b > moe_bytes) moe_bytes = b;
+  }
+  auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  const size_t o_x = 0, o_xb = o_x + up(dim * 4), o_xb2 = o_xb + up(dim * 4);
+  const size_t o_q = o_xb2 + up(dim * 4), o_k = o_q + up(qd * 4), o_v = o_k + up(qd * 4);
+  const size_t o_ao = o_v + up(qd * 4), o_att = o_ao + up(qd * 4);
+  const size_t o_st = o_att + up((size_t)nh * d->cap * 4), o_pt = o_st + 256;
+  const size_t o_rope = o_pt + up((size_t)d->nl * d->ppl * 4);
+  const size_t o_moe = o_rope + up((size_t)d->cap * qd * 4);
+  const size_t total = o_moe + up(moe_bytes);
+  hipError_t e = hipMalloc(&d->mem, total);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&d->kc), d->layer_pages_bytes * d->nl);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&d->vc), d->layer_pages_bytes * d->nl);
+  if (e != hipSuccess) {
+    qr_decoder_destroy(d);
+    return set_error(QR_ERR_NOMEM, "qr_decoder_create: device allocation: %s", hipGetErrorString(e));
+  }
+  uint8_t* b = static_cast<uint8_t*>(d->mem);
+  d->x = reinterpret_cast<float*>(b + o_x);
+  d->xb = reinterpret_cast<float*>(b + o_xb);
+  d->xb2 = reinterpret_cast<float*>(b + o_xb2);
+  d->q = reinterpret_cast<float*>(b + o_q);
+  d->k = reinterpret_cast<float*>(b + o_k);
+  d->v = reinterpret_cast<float*>(b + o_v);
+  d->ao = reinterpret_cast<float*>(b + o_ao);
+  d->att = reinterpret_cast<float*>(b + o_att);
+  d->st = reinterpret_cast<int32_t*>(b + o_st);
+  d->ptab = reinterpret_cast<int32_t*>(b + o_pt);
+  d->rope = reinterpret_cast<float*>(b + o_rope);
+  d->moe_base = b + o_moe;  // sized for the largest layer, carved per layer
+
+  // identity page table, RoPE table with the host C library's powf / cosf /
+  // sinf (apply_rope, src/runtime.c:19-41): pair p of position t at
+  // [t][2p], [t][2p + 1]
+  std::vector<int32_t> pt((size_t)d->nl * d->ppl);
+  for (int l = 0; l < d->nl; l++)
+    for (int i = 0; i < d->ppl; i++) pt[(size_t)l * d->ppl + i] = i;
+  const float base = m->rope_base > 0.0f ? m->rope_base : 10000.0f;
+  std::vector<float> freq(qd / 2), tab((size_t)d->cap * qd);
+  for (int i = 0; i < qd; i += 2) freq[i / 2] = powf(base, -((float)i / (float)hd));
+  for (int t = 0; t < d->cap; t++)
+    for (int i = 0; i < qd; i += 2) {
+      const float theta = (float)t * freq[i / 2];
+      tab[(size_t)t * qd + i] = cosf(theta);
+      tab[(size_t)t * qd + i + 1] = sinf(theta);
+    }
+  hipStream_t s = ctx_stream(c);
+  e = hipMemcpyAsync(d->ptab, pt.data(), pt.size() * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(d->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) {
+    qr_decoder_destroy(d);
+    return set_error(QR_ERR_HIP, "qr_decoder_create: upload: %s", hipGetErrorString(e));
+  }
+  *out = d;
+  return QR_OK;
+}
+
+int qr_decoder_destroy(qr_decoder* d) {
+  if (!d) return QR_OK;
+  (void)hipSetDevice(d->device);
+  if (d->ctx) (void)hipStreamSynchronize(ctx_stream(d->ctx));
+  drop_graph(d);
+  if (d->kc) (void)hipFree(d->kc);
+  if (d->vc) (void)hipFree(d->vc);
+  if (d->mem) (void)hipFree(d->mem);
+  delete d;
+  return QR_OK;
+}
+
+int qr_decoder_set_pages(qr_decoder* d, const int32_t* table) {
+  if (!d || !table) return set_error(QR_ERR_INVALID, "qr_decoder_set_pages: null argument");
+  for (int l = 0; l < d->nl; l++) {
+    std::vector<char> seen(d->ppl, 0);
+    for (int i = 0; i < d->ppl; i++) {
+      const int32_t p = table[(size_t)l * d->ppl + i];
+      if (p < 0 || p >= d->ppl || seen[p])
+        return set_error(QR_ERR_INVALID,
+                         "qr_decoder_set_pages: layer %d is not a permutation of 0..%d", l,
+                         d->ppl - 1);
+      seen[p] = 1;
+    }
+  }
+  DEC_HIP(hipSetDevice(d->device), "hipSetDevice");
+  hipStream_t s = ctx_stream(d->ctx);
+  DEC_HIP(hipMemcpyAsync(d->ptab, table, (size_t)d->nl * d->ppl * 4, hipMemcpyHostToDevice, s),
+          "page table upload");
+  DEC_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
+  return QR_OK;
+}
+
+int qr_decoder_pages(const qr_decoder* d, int* pages_per_layer, int* page) {
+  if (!d) return set_error(QR_ERR_INVALID, "qr_decoder_pages: null decoder");
+  if (pages_per_layer) *pages_per_layer = d->ppl;
+  if (page) *page = d->page;
+  return QR_OK;
+}
+
+int qr_decoder_kv_write(qr_decoder* d, int layer, int pos0, int n, const float* k, const float* v) {
+  if (!d || !k || !v) return set_error(QR_ERR_INVALID, "qr_decoder_kv_write: null argument");
+  if (layer < 0 || layer >= d->nl || pos0 < 0 || n < 0 || pos0 + n > d->cap)
+    return set_error(QR_ERR_INVALID, "qr_decoder_kv_write: layer %d, positions [%d, %d) of %d",
+                     layer, pos0, pos0 + n, d->cap);
+  if (n == 0) return QR_OK;
+  DEC_HIP(hipSetDevice(d->device), "hipSetDevice");
+  const KvView K = kv_view(d, layer, false), V = kv_view(d, layer, true);
+  long grid = (2L * n * (d->kvd / 32) + 255) / 256;
+  if (grid > 4096) grid = 4096;
+  hipLaunchKernelGGL(k_kv_write, dim3((unsigned)grid), dim3(256), 0, ctx_stream(d->ctx), k, v,
+                     pos0, n, d->kvd, K, const_cast<uint8_t*>(V.base));
+  DEC_HIP(hipGetLastError(), "k_kv_write");
+  return QR_OK;
+}
+
+int qr_decoder_kv_rows(const qr_decoder* d, int layer, int pos, const void** krow,
+                       const void** vrow) {
+  if (!d || !krow || !vrow) return set_error(QR_ERR_INVALID, "qr_decoder_kv_rows: null argument");
+  if (layer < 0 || layer >= d->nl || pos < 0 || pos >= d->cap)
+    return set_error(QR_ERR_INVALID, "qr_decoder_kv_rows: layer %d pos %d", layer, pos);
+  // the page table is host-known only through set_pages; read it back
+  int32_t pp = 0;
+  DEC_HIP(hipSetDevice(d->device), "hipSetDevice");
+  DEC_HIP(hipMemcpy(&pp, d->ptab + (size_t)layer * d->ppl + pos / d->page, 4,
+                    hipMemcpyDeviceToHost),
+          "page table read");
+  const size_t off = (size_t)layer * d->layer_pages_bytes +
+                     ((size_t)pp * d->page + (size_t)(pos % d->page)) * d->row_bytes;
+  *krow = d->kc + off;
+  *vrow = d->vc + off;
+  return QR_OK;
+}
+
+int qr_decoder_forward(qr_decoder* d, int token, int pos, float* logits, float* x_out) {
+  if (!d || !logits) return set_error(QR_ERR_INVALID, "qr_decoder_forward: null argument");
+  if (token < 0 || token >= d->vocab)
+    return set_error(QR_ERR_INVALID, "qr_decoder_forward: token %d (vocab %d)", token, d->vocab);
+  if (pos < 0 || pos >= d->cap)
+    return set_error(QR_ERR_INVALID, "qr_decoder_forward: pos %d (seq_len %d)", pos, d->cap);
+  if (!al16(logits) || (x_out && !al16(x_out)))
+    return set_error(QR_ERR_INVALID, "qr_decoder_forward: output alignment");
+  DEC_HIP(hipSetDevice(d->device), "hipSetDevice");
+  hipStream_t s = ctx_stream(d->ctx);
+  if (ctx_capturing(d->ctx) && (d->flags & QR_DEC_GRAPH))
+    return set_error(QR_ERR_INVALID, "qr_decoder_forward: a graph decoder cannot be captured");
+  hipLaunchKernelGGL(k_set_state, dim3(1), dim3(64), 0, s, d->st, token, pos);
+  DEC_HIP(hipGetLastError(), "k_set_state");
+  d->calls++;
+  if (!(d->flags & QR_DEC_GRAPH) || d->calls == 1) {
+    // eager (the first call of a graph decoder also sets every kernel's
+    // attributes outside capture)
+    DEC_HIP(enqueue_step(d, logits, x_out, s), "decode step");
+    return QR_OK;
+  }
+  if (!d->exec || d->graph_logits != logits || d->graph_xout != x_out) {
+    drop_graph(d);
+    DEC_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    const hipError_t e = enqueue_step(d, logits, x_out, s);
+    hipGraph_t g = nullptr;
+    const hipError_t e2 = hipStreamEndCapture(s, &g);
+    if (e != hipSuccess || e2 != hipSuccess) {
+      if (g) (void)hipGraphDestroy(g);
+      return set_error(QR_ERR_HIP, "qr_decoder_forward: capture: %s",
+                       hipGetErrorString(e != hipSuccess ? e : e2));
+    }
+    d->graph = g;
+    DEC_HIP(hipGraphInstantiate(&d->exec, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    d->graph_logits = logits;
+    d->graph_xout = x_out;
+  }
+  DEC_HIP(hipGraphLaunch(d->exec, s), "hipGraphLaunch");
+  return QR_OK;
+}
+
+}  // extern "C"

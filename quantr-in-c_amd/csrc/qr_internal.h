@@ -12,6 +12,18 @@
 
 namespace qr {
 
+// qr_runtime.hip: context internals used by other translation units.
+// set_error records the calling thread's qr_last_error() message and returns
+// code.  moe_check validates a MoE layer as qr_moe_forward does; gemv_check
+// validates one weight matrix [n][d] of `type` for a one-token GEMV in
+// `order` (w may be null: the GEMV then writes zeros).
+int set_error(int code, const char* fmt, ...);
+hipStream_t ctx_stream(qr_ctx* c);
+int ctx_device(qr_ctx* c);
+bool ctx_capturing(qr_ctx* c);
+int moe_check(const qr_moe_layer* L, const char* who);
+int gemv_check(uint32_t type, int order, const void* w, int n, int d, const char* who);
+
 // qr_gemv.hip
 // q8o: the Q8_0 dot order (kQ8Seq / kQ8Avx2 / kQ8Avx512 of qr_gemv.h, equal to
 // QR_ORDER_*); it only changes Q8_0 weights.

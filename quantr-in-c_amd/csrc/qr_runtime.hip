@@ -224,6 +224,20 @@ __global__ void k_test_expf(const float* __restrict__ x, float* __restrict__ y, 
 
 }  // namespace
 
+// Context internals for the other translation units (qr_internal.h).
+namespace qr {
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+hipStream_t ctx_stream(qr_ctx* c) { return c->stream; }
+int ctx_device(qr_ctx* c) { return c->device; }
+bool ctx_capturing(qr_ctx* c) { return capturing(c); }
+}  // namespace qr
+
 extern "C" {
 
 const char* qr_last_error(void) { return g_err; }
@@ -579,6 +593,31 @@ static int check_experts(const qr_moe_layer* L, const char* who) {
   }
   return QR_OK;
 }
+
+}  // extern "C"
+
+namespace qr {
+int moe_check(const qr_moe_layer* L, const char* who) {
+  const int rc = check_layer(L, who);
+  return rc ? rc : check_experts(L, who);
+}
+
+int gemv_check(uint32_t type, int order, const void* w, int n, int d, const char* who) {
+  if (!known_type(type)) return fail(QR_ERR_INVALID, "%s: unknown weight type %u", who, type);
+  if (n <= 0 || d <= 0) return fail(QR_ERR_INVALID, "%s: weight shape %d x %d", who, n, d);
+  if (type == QR_T_F32) return QR_OK;
+  if (d % qr_block_elems((int)type))
+    return fail(QR_ERR_INVALID, "%s: d=%d is not whole blocks of type %u", who, d, type);
+  if (w && !aligned(w, 16)) return fail(QR_ERR_INVALID, "%s: weights must be 16-byte aligned", who);
+  const int R = gemv_rows_per_wg((int)type, order, n, d, 1);
+  if (!gemv_blk_ok((int)type, d, 1) && !gemv_stream_ok((int)type, order, d, 1) &&
+      gemv_lds_bytes((int)type, order, d, 1, R) > 64 * 1024)
+    return fail(QR_ERR_UNSUPPORTED, "%s: d=%d exceeds the GEMV's LDS budget", who, d);
+  return QR_OK;
+}
+}  // namespace qr
+
+extern "C" {
 
 int qr_moe_route(qr_ctx* c, const qr_moe_layer* L, const float* xb, int T, int order,
                  float* probs, int32_t* idx, float* wts) {

@@ -38,6 +38,28 @@ class MoeLayer(C.Structure):
     ]
 
 
+class Layer(C.Structure):
+    """qr_layer (include/qr_hip.h); pointers are device addresses."""
+    _fields_ = [
+        ("rms_att", _vp), ("rms_ffn", _vp), ("wq", _vp), ("wk", _vp), ("wv", _vp), ("wo", _vp),
+        ("wq_type", C.c_uint32), ("wk_type", C.c_uint32), ("wv_type", C.c_uint32),
+        ("wo_type", C.c_uint32), ("moe", MoeLayer),
+    ]
+
+
+class Model(C.Structure):
+    """qr_model (include/qr_hip.h); `layers` is a host array of Layer."""
+    _fields_ = [
+        ("dim", C.c_int), ("n_heads", C.c_int), ("n_kv_heads", C.c_int), ("head_dim", C.c_int),
+        ("n_layers", C.c_int), ("vocab", C.c_int), ("seq_len", C.c_int), ("rope_base", C.c_float),
+        ("tok_embd", _vp), ("tok_type", C.c_uint32), ("rms_final", _vp), ("wcls", _vp),
+        ("wcls_type", C.c_uint32), ("layers", C.POINTER(Layer)),
+    ]
+
+
+KV_F32, KV_Q8_0 = 0, 2
+DEC_GRAPH = 1
+
 _SIGS = {
     "qr_last_error": (C.c_char_p, []),
     "qr_version": (C.c_char_p, []),
@@ -81,6 +103,19 @@ _SIGS = {
     "qr_weights_release": (C.c_int, [_vp, _vp]),
     "qr_weights_release_all": (C.c_int, [_vp]),
     "qr_test_expf": (C.c_int, [_vp, _vp, _vp, C.c_long]),
+    "qr_kv_row_bytes": (C.c_size_t, [C.c_int, C.c_int]),
+    "qr_dequantize": (C.c_int, [_vp, C.c_uint32, _vp, C.c_int, C.c_int, _vp]),
+    "qr_rmsnorm": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int]),
+    "qr_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
+                               C.c_int, C.c_int, _vp, _vp]),
+    "qr_decoder_create": (C.c_int, [_vp, C.POINTER(Model), C.c_int, C.c_int, C.c_int, C.c_int,
+                                    C.POINTER(_vp)]),
+    "qr_decoder_destroy": (C.c_int, [_vp]),
+    "qr_decoder_set_pages": (C.c_int, [_vp, _vp]),
+    "qr_decoder_pages": (C.c_int, [_vp, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "qr_decoder_kv_write": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "qr_decoder_kv_rows": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(_vp), C.POINTER(_vp)]),
+    "qr_decoder_forward": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp]),
     # drop-ins (include/qr_dropin.h)
     "qr_dropin_init": (C.c_int, [C.c_int, C.c_int]),
     "qr_dropin_shutdown": (None, []),
@@ -266,6 +301,122 @@ class Device:
 
     def test_expf(self, x_ptr, y_ptr, n):
         self._check(self.lib.qr_test_expf(self.ctx, _vp(x_ptr), _vp(y_ptr), n), "qr_test_expf")
+
+    def dequantize(self, qtype, src_ptr, rows, n, out_ptr):
+        self._check(self.lib.qr_dequantize(self.ctx, qtype, _vp(src_ptr), rows, n, _vp(out_ptr)),
+                    "qr_dequantize")
+
+    def rmsnorm(self, o_ptr, x_ptr, w_ptr, n, add_ptr=None):
+        self._check(self.lib.qr_rmsnorm(self.ctx, _vp(o_ptr), _vp(x_ptr), _vp(add_ptr), _vp(w_ptr),
+                                        n), "qr_rmsnorm")
+
+    def attention(self, q_ptr, kc_ptr, vc_ptr, ptab_ptr, page, kv_type, npos, n_heads,
+                  n_kv_heads, head_dim, att_ptr, out_ptr):
+        self._check(self.lib.qr_attention(self.ctx, _vp(q_ptr), _vp(kc_ptr), _vp(vc_ptr),
+                                          _vp(ptab_ptr), page, kv_type, npos, n_heads, n_kv_heads,
+                                          head_dim, _vp(att_ptr), _vp(out_ptr)), "qr_attention")
+
+
+class Decoder:
+    """qr_decoder over a model whose weights are already on the device.
+
+    `model` is a Model whose `layers` points at a ctypes array this object
+    keeps alive."""
+
+    def __init__(self, dev, model, layers, kv_type=KV_Q8_0, order=ORDER_SEQ, page=0, flags=0):
+        self.dev = dev
+        self._layers = layers
+        self._model = model
+        h = _vp()
+        dev._check(dev.lib.qr_decoder_create(dev.ctx, C.byref(model), kv_type, order, page, flags,
+                                             C.byref(h)), "qr_decoder_create")
+        self.h = h.value
+
+    def pages(self):
+        n, p = C.c_int(), C.c_int()
+        self.dev._check(self.dev.lib.qr_decoder_pages(_vp(self.h), C.byref(n), C.byref(p)),
+                        "qr_decoder_pages")
+        return n.value, p.value
+
+    def set_pages(self, table):
+        t = np.ascontiguousarray(table, dtype=np.int32)
+        self.dev._check(self.dev.lib.qr_decoder_set_pages(_vp(self.h), _ptr(t)),
+                        "qr_decoder_set_pages")
+
+    def kv_write(self, layer, pos0, n, k_ptr, v_ptr):
+        self.dev._check(self.dev.lib.qr_decoder_kv_write(_vp(self.h), layer, pos0, n, _vp(k_ptr),
+                                                         _vp(v_ptr)), "qr_decoder_kv_write")
+
+    def kv_rows(self, layer, pos):
+        k, v = _vp(), _vp()
+        self.dev._check(self.dev.lib.qr_decoder_kv_rows(_vp(self.h), layer, pos, C.byref(k),
+                                                        C.byref(v)), "qr_decoder_kv_rows")
+        return k.value, v.value
+
+    def forward(self, token, pos, logits_ptr, x_ptr=None):
+        self.dev._check(self.dev.lib.qr_decoder_forward(_vp(self.h), token, pos,
+                                                        _vp(logits_ptr), _vp(x_ptr)),
+                        "qr_decoder_forward")
+
+    def close(self):
+        if self.h is not None:
+            self.dev.lib.qr_decoder_destroy(_vp(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def upload_decode_model(dev, m):
+    """Model + Layer array for a decoder from a dict of weights.
+
+    m holds the sizes (dim, n_heads, n_kv_heads, head_dim, n_layers, vocab,
+    seq_len, rope_base, E, K, hidden), the types (tok_type, wcls_type,
+    wtype = (wq, wk, wv, wo), up_type (also gate), down_type) and the tensors
+    (tok_embd, rms_final, wcls, and per layer rms_att, rms_ffn, wq, wk, wv,
+    wo, router, up, gate, down).  A tensor is a numpy array (uploaded here) or
+    an int device address (used as is).  Returns (model, layers, keep); keep
+    holds the device buffers and must outlive the decoder."""
+    keep = []
+
+    def dptr(a):
+        if isinstance(a, (int, np.integer)):
+            return int(a)
+        if isinstance(a, DevBuf):
+            keep.append(a)
+            return a.ptr
+        b = dev.upload(np.ascontiguousarray(a))
+        keep.append(b)
+        return b.ptr
+
+    L = m["n_layers"]
+    layers = (Layer * L)()
+    wt = m["wtype"]
+    for l in range(L):
+        lw = m["layers"][l]
+        y = layers[l]
+        y.rms_att, y.rms_ffn = dptr(lw["rms_att"]), dptr(lw["rms_ffn"])
+        y.wq, y.wk, y.wv, y.wo = (dptr(lw[k]) for k in ("wq", "wk", "wv", "wo"))
+        y.wq_type, y.wk_type, y.wv_type, y.wo_type = wt
+        e = y.moe
+        e.dim, e.hidden, e.n_experts, e.n_used = m["dim"], m["hidden"], m["E"], m["K"]
+        e.router = dptr(lw["router"])
+        e.up, e.gate, e.down = dptr(lw["up"]), dptr(lw["gate"]), dptr(lw["down"])
+        e.up_type = e.gate_type = m["up_type"]
+        e.down_type = m["down_type"]
+    mo = Model()
+    mo.dim, mo.n_heads, mo.n_kv_heads = m["dim"], m["n_heads"], m["n_kv_heads"]
+    mo.head_dim, mo.n_layers, mo.vocab = m["head_dim"], L, m["vocab"]
+    mo.seq_len, mo.rope_base = m["seq_len"], m["rope_base"]
+    mo.tok_embd, mo.tok_type = dptr(m["tok_embd"]), m["tok_type"]
+    mo.rms_final = dptr(m["rms_final"])
+    mo.wcls, mo.wcls_type = dptr(m["wcls"]), m["wcls_type"]
+    mo.layers = C.cast(layers, C.POINTER(Layer))
+    keep.append(layers)
+    return mo, layers, keep
 
 
 def declared_symbols():

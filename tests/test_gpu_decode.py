@@ -1,0 +1,193 @@
+"""GPU parity of the single-token decode step (forward_runtime,
+src/runtime.c:94-288) and its ops, through the C ABI.
+
+- The decoder against the reference's own logits (tests/golden/decode.npz,
+  written by the compiled reference's forward_runtime): two-layer MoE models,
+  token by token from position 0, fp32 KV cache, every build -- bit-exact.
+- The decoder at a Qwen3-30B-A3B-like head shape the reference cannot express
+  (head_dim 128 with q_dim != dim, GQA 4:1) over a prefilled Q8_0 cache with
+  a permuted page table, against the oracle's restatement -- bit-exact.
+- The ops alone (dequantize, rmsnorm, attention) against the oracle.
+"""
+import numpy as np
+import pytest
+
+import inputs as I
+import quantr_amd as Q
+from conftest import assert_bits_equal
+from oracle import ORDER_AVX2, ORDER_AVX512, ORDER_SEQ
+
+pytestmark = pytest.mark.gpu
+
+BUILDS = {"c99": ORDER_SEQ, "avx2": ORDER_AVX2, "avx512": ORDER_AVX512}
+
+
+def make_decoder(dev, m, kv_type, order, page=0, flags=0):
+    model, layers, keep = Q.upload_decode_model(dev, m)
+    d = Q.Decoder(dev, model, layers, kv_type=kv_type, order=order, page=page, flags=flags)
+    d._keep = keep
+    return d
+
+
+def run_tokens(dev, d, m, tokens, pos0=0):
+    lg_d, x_d = dev.alloc(4 * m["vocab"]), dev.alloc(4 * m["dim"])
+    lg = np.zeros((len(tokens), m["vocab"]), np.float32)
+    xs = np.zeros((len(tokens), m["dim"]), np.float32)
+    for i, t in enumerate(tokens):
+        d.forward(int(t), pos0 + i, lg_d.ptr, x_d.ptr)
+        lg[i] = dev.download(lg_d, m["vocab"], np.float32)
+        xs[i] = dev.download(x_d, m["dim"], np.float32)
+    return lg, xs
+
+
+@pytest.mark.parametrize("graph", [0, Q.DEC_GRAPH], ids=["eager", "graph"])
+@pytest.mark.parametrize("build", list(BUILDS))
+@pytest.mark.parametrize("name", list(I.DECODE_CASES))
+def test_decoder_matches_reference_logits(dev, golden, name, build, graph):
+    g = golden("decode.npz")
+    m = I.decode_model(name)
+    assert I.decode_digest(m) == str(g["sha_" + name])
+    key = "logits_%s_%s" % (name, build)
+    if key not in g:
+        pytest.skip("fixture written without an -mavx512f build")
+    print("decode case %s build %s graph %d" % (name, build, graph), flush=True)
+    d = make_decoder(dev, m, Q.KV_F32, BUILDS[build], flags=graph)
+    lg, xs = run_tokens(dev, d, m, m["tokens"])
+    d.close()
+    assert_bits_equal(xs, g["x_%s_%s" % (name, build)], "residual %s/%s" % (name, build))
+    assert_bits_equal(lg, g[key], "logits %s/%s" % (name, build))
+
+
+def prefilled(oracle, m, npre, seed):
+    """Seeded N(0, 1) K / V values for positions 0 .. npre-1 of every layer
+    and the oracle's contiguous cache holding them."""
+    L, kvd = m["n_layers"], m["n_kv_heads"] * m["head_dim"]
+    rng = np.random.default_rng(seed)
+    kv = rng.standard_normal((L, 2, npre, kvd)).astype(np.float32)
+    rs = oracle.kv_row_bytes(Q.KV_Q8_0, kvd)
+    kc = np.zeros((L, m["seq_len"], rs), np.uint8)
+    vc = np.zeros_like(kc)
+    for l in range(L):
+        kc[l, :npre] = oracle.kv_rows(kv[l, 0], Q.KV_Q8_0)
+        vc[l, :npre] = oracle.kv_rows(kv[l, 1], Q.KV_Q8_0)
+    return kv, kc, vc
+
+
+@pytest.mark.parametrize("graph", [0, Q.DEC_GRAPH], ids=["eager", "graph"])
+@pytest.mark.parametrize("order", [ORDER_SEQ, ORDER_AVX2])
+def test_decoder_q8_cache_head128(dev, oracle, order, graph):
+    """Qwen3-like heads (head_dim 128, q_dim 1024 != dim 512, 8 heads over 2
+    kv heads) over a Q8_0 cache prefilled to 517 positions through a permuted
+    page table (pages of 64), then three decode steps at 517..519: logits,
+    residual and the cache rows the steps wrote, bit-exact with the oracle."""
+    m = I.qwen3_small_model(n_layers=2, seq_len=640)
+    npre = 517
+    kv, kc, vc = prefilled(oracle, m, npre, seed=41)
+    print("decode head128 order %d graph %d" % (order, graph), flush=True)
+    d = make_decoder(dev, m, Q.KV_Q8_0, order, page=64, flags=graph)
+    ppl, page = d.pages()
+    assert (ppl, page) == (10, 64)
+    rng = np.random.default_rng(5)
+    d.set_pages(np.stack([rng.permutation(ppl) for _ in range(m["n_layers"])]).astype(np.int32))
+    for l in range(m["n_layers"]):
+        kb, vb = dev.upload(kv[l, 0]), dev.upload(kv[l, 1])
+        d.kv_write(l, 0, npre, kb.ptr, vb.ptr)
+    rs = kc.shape[2]
+    # the prefill's rows are the oracle's quantize_row_q8_0 rows
+    for l, t in ((0, 0), (1, 63), (1, 64), (0, npre - 1)):
+        kr, vr = d.kv_rows(l, t)
+        assert np.array_equal(dev.download(kr, rs, np.uint8), kc[l, t])
+        assert np.array_equal(dev.download(vr, rs, np.uint8), vc[l, t])
+    toks = [11, 319, 200]
+    lg, xs = run_tokens(dev, d, m, toks, pos0=npre)
+    wl, wx = oracle.forward_cached(m, kc.reshape(-1), vc.reshape(-1), toks, npre, order,
+                                   Q.KV_Q8_0)
+    for l in range(m["n_layers"]):
+        for t in range(npre, npre + len(toks)):
+            kr, vr = d.kv_rows(l, t)
+            assert np.array_equal(dev.download(kr, rs, np.uint8), kc[l, t]), (l, t)
+            assert np.array_equal(dev.download(vr, rs, np.uint8), vc[l, t]), (l, t)
+    d.close()
+    assert_bits_equal(xs, wx, "residual")
+    assert_bits_equal(lg, wl, "logits")
+
+
+@pytest.mark.parametrize("qtype", [Q.TYPE_F32, Q.TYPE_Q8_0, Q.TYPE_Q4_K, Q.TYPE_Q5_K,
+                                   Q.TYPE_Q6_K])
+def test_dequantize(dev, oracle, qtype):
+    """dequantize_row (src/quant.c:160-240) of 7 rows of 512: bit-exact."""
+    rows, n = 7, 512
+    src = I._rows(60 + qtype, qtype, rows, n)
+    out = dev.alloc(rows * n * 4)
+    sb = dev.upload(src)
+    dev.dequantize(qtype, sb.ptr, rows, n, out.ptr)
+    got = dev.download(out, (rows, n), np.float32)
+    want = np.stack([oracle.dequantize(np.ascontiguousarray(src[r]).view(np.uint8), qtype, n)
+                     for r in range(rows)])
+    assert_bits_equal(got, want, "dequantize type %d" % qtype)
+
+
+@pytest.mark.parametrize("n", [64, 2048, 5120, 8192])
+def test_rmsnorm(dev, oracle, n):
+    """rmsnorm_ref (src/kernels.c:170-180), alone and after the residual add:
+    bit-exact."""
+    x = I.activations(70, 1, n)[0]
+    a = I.activations(71, 1, n, std=0.5)[0]
+    w = (1.0 + I.activations(72, 1, n, std=0.1)[0]).astype(np.float32)
+    xd, ad, wd, od = dev.upload(x), dev.upload(a), dev.upload(w), dev.alloc(4 * n)
+    dev.rmsnorm(od.ptr, xd.ptr, wd.ptr, n)
+    assert_bits_equal(dev.download(od, n, np.float32), oracle.rmsnorm(x, w), "rmsnorm")
+    dev.rmsnorm(od.ptr, xd.ptr, wd.ptr, n, add_ptr=ad.ptr)
+    xs = (x + a).astype(np.float32)
+    assert_bits_equal(dev.download(xd, n, np.float32), xs, "residual")
+    assert_bits_equal(dev.download(od, n, np.float32), oracle.rmsnorm(xs, w), "rmsnorm(x + a)")
+
+
+@pytest.mark.parametrize("kv_type", [Q.KV_F32, Q.KV_Q8_0])
+@pytest.mark.parametrize("npos,H,KVH,hd", [(1, 4, 4, 64), (130, 8, 2, 128), (4097, 32, 4, 128),
+                                           (300, 4, 1, 512)])
+def test_attention(dev, oracle, kv_type, npos, H, KVH, hd):
+    """The attention of src/runtime.c:136-193 over a paged cache (pages of 128
+    in reversed order): weights and outputs bit-exact with the oracle,
+    including the Qwen3-30B-A3B shape (32 heads over 4, head_dim 128) at 4097
+    positions and head_dim 512 (the reference's kh_buf bound)."""
+    kvd = KVH * hd
+    rng = np.random.default_rng(npos + hd)
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    kv = rng.standard_normal((2, npos, kvd)).astype(np.float32)
+    kc, vc = oracle.kv_rows(kv[0], kv_type), oracle.kv_rows(kv[1], kv_type)
+    print("attention npos %d H %d KVH %d hd %d kv %d" % (npos, H, KVH, hd, kv_type), flush=True)
+    page = 128
+    npages = (npos + page - 1) // page
+    ptab = np.arange(npages, dtype=np.int32)[::-1].copy()
+    rs = kc.shape[1]
+    kp = np.zeros((npages * page, rs), np.uint8)
+    vp = np.zeros_like(kp)
+    for t in range(npos):
+        slot = ptab[t // page] * page + t % page
+        kp[slot], vp[slot] = kc[t], vc[t]
+    qd, kd, vd, pd = dev.upload(q), dev.upload(kp), dev.upload(vp), dev.upload(ptab)
+    att, out = dev.alloc(4 * H * npos), dev.alloc(4 * H * hd)
+    dev.attention(qd.ptr, kd.ptr, vd.ptr, pd.ptr, page, kv_type, npos, H, KVH, hd, att.ptr,
+                  out.ptr)
+    wo, wa = oracle.attention(q, kc, vc, kv_type, npos - 1, H, KVH, hd)
+    assert_bits_equal(dev.download(att, (H, npos), np.float32), wa, "weights")
+    assert_bits_equal(dev.download(out, H * hd, np.float32), wo, "output")
+
+
+def test_decoder_rejects_bad_arguments(dev):
+    m = I.qwen3_small_model(n_layers=1, seq_len=64)
+    model, layers, keep = Q.upload_decode_model(dev, m)
+    with pytest.raises(Q.QrError, match="head_dim"):
+        model.head_dim = 100
+        Q.Decoder(dev, model, layers)
+    model.head_dim = 128
+    d = Q.Decoder(dev, model, layers, page=16)
+    lg = dev.alloc(4 * m["vocab"])
+    with pytest.raises(Q.QrError, match="pos"):
+        d.forward(1, 64, lg.ptr)
+    with pytest.raises(Q.QrError, match="token"):
+        d.forward(m["vocab"], 0, lg.ptr)
+    with pytest.raises(Q.QrError, match="permutation"):
+        d.set_pages(np.zeros((1, 4), np.int32))
+    d.close()

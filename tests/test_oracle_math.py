@@ -155,3 +155,71 @@ def test_synth_quantizers(oracle, qtype, tol):
     assert np.abs(deq - w).max() <= tol * np.abs(w).max()
     if qtype == 8:  # the reference routine itself
         assert (q == np.stack([oracle.quantize_q8_0(r) for r in w])).all()
+
+
+@pytest.mark.parametrize("kv_type", [0, 2])
+def test_attention_closed_form(oracle, kv_type):
+    """qro_attention at a shape the reference cannot express (head_dim 128,
+    8 query heads over 2 kv heads, 37 positions) against softmax(q K^T /
+    sqrt(hd)) V in float64 over the cache's own values (the Q8_0 rows read
+    back as qs * d): a wrong kv-head mapping, scale or transposition fails."""
+    H, KVH, hd, npos = 8, 2, 128, 37
+    rng = np.random.default_rng(31)
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    kv = rng.standard_normal((2, npos, KVH * hd)).astype(np.float32)
+    kc, vc = oracle.kv_rows(kv[0], kv_type), oracle.kv_rows(kv[1], kv_type)
+    if kv_type == 2:
+        kf = np.stack([oracle.dequantize(r, 8, KVH * hd) for r in kc]).astype(np.float64)
+        vf = np.stack([oracle.dequantize(r, 8, KVH * hd) for r in vc]).astype(np.float64)
+    else:
+        kf, vf = kv[0].astype(np.float64), kv[1].astype(np.float64)
+    out, att = oracle.attention(q, kc, vc, kv_type, npos - 1, H, KVH, hd)
+    for h in range(H):
+        g = h // (H // KVH)
+        s = kf[:, g * hd:(g + 1) * hd] @ q[h * hd:(h + 1) * hd].astype(np.float64) / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        np.testing.assert_allclose(att[h], p, rtol=2e-5, atol=1e-7)
+        o = p @ vf[:, g * hd:(g + 1) * hd]
+        np.testing.assert_allclose(out[h * hd:(h + 1) * hd], o, rtol=1e-4, atol=2e-6)
+
+
+def test_rope_closed_form(oracle):
+    """apply_rope's rotation (src/runtime.c:19-41) in float64: pair i of q
+    (over the whole q vector) and of k (only below kv_dim) turns by
+    pos * base^(-i / head_dim); position 0 is the identity."""
+    qlen, hd, kvh, base = 1024, 128, 2, 1e6
+    rng = np.random.default_rng(32)
+    q0 = rng.standard_normal(qlen).astype(np.float32)
+    k0 = rng.standard_normal(kvh * hd).astype(np.float32)
+    q, k = oracle.rope(q0, k0, hd, kvh, 0, base)
+    assert np.array_equal(q, q0) and np.array_equal(k[: kvh * hd], k0)
+    for pos in (1, 77, 4095):
+        q, k = oracle.rope(q0, k0, hd, kvh, pos, base)
+        i = np.arange(0, qlen, 2, dtype=np.float64)
+        th = pos * base ** (-i / hd)
+        c, s = np.cos(th), np.sin(th)
+        a, b = q0[0::2].astype(np.float64), q0[1::2].astype(np.float64)
+        # float32 theta carries a relative error of a few ulp of pos * freq
+        tol = 4e-7 * pos * np.abs(np.hypot(a, b)) + 1e-6
+        assert np.all(np.abs(q[0::2] - (a * c - b * s)) <= tol)
+        assert np.all(np.abs(q[1::2] - (a * s + b * c)) <= tol)
+        n = kvh * hd // 2
+        ka, kb = k0[0::2].astype(np.float64), k0[1::2].astype(np.float64)
+        assert np.all(np.abs(k[: kvh * hd][0::2] - (ka * c[:n] - kb * s[:n])) <= tol[:n] + 1e-6)
+        assert np.all(k[kvh * hd:] == 0)
+
+
+def test_forward_cached_from_empty_equals_forward_seq(oracle):
+    """The cached-forward helper over an empty cache is forward_seq (the path
+    the golden logits pin), at the head_dim-128 shape."""
+    import inputs as I
+    m = I.qwen3_small_model(n_layers=1, seq_len=16)
+    toks = [5, 300, 17]
+    lg, xs = oracle.forward_seq(m, toks, 0, kv_type=2)
+    rs = oracle.kv_row_bytes(2, m["n_kv_heads"] * m["head_dim"])
+    kc = np.zeros(m["n_layers"] * m["seq_len"] * rs, np.uint8)
+    vc = np.zeros_like(kc)
+    lg2, xs2 = oracle.forward_cached(m, kc, vc, toks, 0, 0, 2)
+    assert np.array_equal(lg.view(np.uint32), lg2.view(np.uint32))
+    assert np.array_equal(xs.view(np.uint32), xs2.view(np.uint32))
