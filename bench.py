@@ -20,11 +20,17 @@ Extra keys of the same line:
                (router included) like a 48-layer decode;
   moe_qwen15   the Qwen1.5-MoE-A2.7B-shaped layer (60 experts top-4, ffn 1408,
                shared expert ffn 5632 with a sigmoid gate) at T = 1 and 64;
+  decode_qwen3 the whole single-token decode step of a Qwen3-30B-A3B-shaped
+               model (48 layers, 32 query / 4 kv heads of 128, the MoE layer
+               above, 151936-row Q6_K lm_head) over a Q8_0 paged KV cache
+               prefilled to 4096 positions, replayed as one HIP graph per
+               token, in tokens/s with its algorithmic bytes;
   cpu_baseline the reference's own matmul_q_fused and MoE block (oracle/_ref,
                its sources compiled with the CI flags) on this host's cores at
                1, 8 and all available threads: 3 warm-ups, then the median.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-moe] [--no-cpu] [--no-sweep]
+                    [--no-decode] [--decode-steps N]
 """
 import argparse
 import json
@@ -308,6 +314,117 @@ def bench_moe(dev, M, T, steps, warmup, order, nbatches=8, seed=7000):
 
 
 # ---------------------------------------------------------------------------
+# Full decode step
+# ---------------------------------------------------------------------------
+QWEN3_DEC = dict(dim=2048, n_heads=32, n_kv_heads=4, head_dim=128, vocab=151936, prefill=4096)
+
+
+def _tiled(dev, rows_blob, n_rows):
+    """A device tensor of n_rows rows made by repeating rows_blob's rows."""
+    r, rb = rows_blob.shape
+    buf = dev.alloc(n_rows * rb)
+    dev.write(buf, rows_blob)
+    done = r
+    while done < n_rows:
+        k = min(done, n_rows - done)
+        dev.copy(buf.ptr + done * rb, buf.ptr, k * rb)
+        done += k
+    return buf
+
+
+def build_decoder(dev, M, cap):
+    """The Qwen3-30B-A3B-shaped decoder: 48 layers of attention (wq / wk / wo
+    Q4_K, wv Q6_K, 32 query heads over 4 kv heads of 128) on top of the MoE
+    layers M, a Q4_K embedding and a Q6_K lm_head of 151936 rows (8192
+    distinct rows repeated), and a Q8_0 KV cache of `cap` positions."""
+    c = QWEN3_DEC
+    dim, H, KVH, hd, V = c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["vocab"]
+    qd, kvd = H * hd, KVH * hd
+    L = len(M["layers"])
+    t0 = time.time()
+    parts = [synth.weights(5001, qd, dim, Q.TYPE_Q4_K), synth.weights(5002, kvd, dim, Q.TYPE_Q4_K),
+             synth.weights(5003, kvd, dim, Q.TYPE_Q6_K), synth.weights(5004, dim, qd, Q.TYPE_Q4_K),
+             (1.0 + synth.normal(5005, (dim,), 0.1)).astype(np.float32),
+             (1.0 + synth.normal(5006, (dim,), 0.1)).astype(np.float32)]
+    offs = np.cumsum([0] + [(p.nbytes + 255) // 256 * 256 for p in parts])
+    per_layer = int(offs[-1])
+    slab = dev.alloc(per_layer * L)
+    for p, o in zip(parts, offs):
+        dev.write(slab, p, int(o))
+    for l in range(1, L):
+        dev.copy(slab.ptr + l * per_layer, slab.ptr, per_layer)
+    emb = _tiled(dev, synth.weights(5010, 8192, dim, Q.TYPE_Q4_K), V)
+    wcls = _tiled(dev, synth.weights(5011, 8192, dim, Q.TYPE_Q6_K), V)
+    rmsf = dev.upload((1.0 + synth.normal(5012, (dim,), 0.1)).astype(np.float32))
+    log("bench: decoder weights built in %.1fs" % (time.time() - t0))
+    layers = []
+    for l in range(L):
+        b = [slab.ptr + l * per_layer + int(o) for o in offs[:-1]]
+        ml = M["layers"][l]
+        layers.append(dict(wq=b[0], wk=b[1], wv=b[2], wo=b[3], rms_att=b[4], rms_ffn=b[5],
+                           router=ml.router, up=ml.up, gate=ml.gate, down=ml.down))
+    m = dict(dim=dim, n_heads=H, n_kv_heads=KVH, head_dim=hd, n_layers=L, vocab=V, seq_len=cap,
+             rope_base=1e6, tok_embd=emb.ptr, tok_type=Q.TYPE_Q4_K, rms_final=rmsf.ptr,
+             wcls=wcls.ptr, wcls_type=Q.TYPE_Q6_K,
+             wtype=(Q.TYPE_Q4_K, Q.TYPE_Q4_K, Q.TYPE_Q6_K, Q.TYPE_Q4_K),
+             E=M["shape"]["E"], K=M["shape"]["K"], hidden=M["shape"]["hidden"],
+             up_type=Q.TYPE_Q4_K, down_type=Q.TYPE_Q6_K, layers=layers)
+    attn_bytes = sum(p.nbytes for p in parts[:4]) + 2 * 4 * dim
+    return m, [slab, emb, wcls, rmsf], attn_bytes
+
+
+def bench_decode(dev, M, steps, warmup, order):
+    """tokens/s of the whole single-token decode step (graph replay), at
+    positions prefill, prefill + 1, ... over a Q8_0 cache prefilled with
+    seeded N(0, 1) keys and values; the token ids are a seeded random
+    sequence (the step does not wait for its own argmax)."""
+    c = QWEN3_DEC
+    P = c["prefill"]
+    cap = P + warmup + steps + 1
+    m, bufs, attn_bytes = build_decoder(dev, M, cap)
+    model, layers, keep = Q.upload_decode_model(dev, m)
+    t0 = time.time()
+    d = Q.Decoder(dev, model, layers, kv_type=Q.KV_Q8_0, order=order, page=256,
+                  flags=Q.DEC_GRAPH)
+    log("bench: decoder created (RoPE table, cache) in %.1fs" % (time.time() - t0))
+    kvd = c["n_kv_heads"] * c["head_dim"]
+    kb = dev.upload(synth.normal(5020, (P, kvd)))
+    vb = dev.upload(synth.normal(5021, (P, kvd)))
+    for l in range(m["n_layers"]):
+        d.kv_write(l, 0, P, kb.ptr, vb.ptr)
+    kb.free()
+    vb.free()
+    toks = np.random.default_rng(5030).integers(0, c["vocab"], size=warmup + steps)
+    lg = dev.alloc(4 * c["vocab"])
+    for i in range(warmup):
+        d.forward(int(toks[i]), P + i, lg.ptr)
+    dev.sync()
+    dev.timer_start()
+    for i in range(warmup, warmup + steps):
+        d.forward(int(toks[i]), P + i, lg.ptr)
+    ms = dev.timer_stop() / steps
+    logits = dev.download(lg, c["vocab"], np.float32)
+    d.close()
+    for b in bufs:
+        b.free()
+    # algorithmic bytes per step: attention weights and norms, router and the
+    # K experts of every layer, the KV rows read (mean position of the timed
+    # steps), the embedding row and the lm_head
+    L, dim = m["n_layers"], c["dim"]
+    npos = P + warmup + (steps + 1) / 2.0
+    rs = (kvd // 32) * 34
+    sh = M["shape"]
+    step_bytes = (L * (attn_bytes + 4 * sh["E"] * dim + sh["K"] * M["expert_bytes"]) +
+                  L * 2 * npos * rs + synth.row_bytes(Q.TYPE_Q4_K, dim) +
+                  c["vocab"] * synth.row_bytes(Q.TYPE_Q6_K, dim) + 4 * dim)
+    s = ms / 1e3
+    return dict(ms_per_step=ms, tokens_per_s=1.0 / s, layers=L, positions=npos,
+                alg_bytes=int(step_bytes), achieved_gbps=step_bytes / s / 1e9,
+                roofline_frac=step_bytes / s / 1e9 / HBM_PEAK_GBPS,
+                finite_logits=bool(np.isfinite(logits).all()))
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline: the reference's own code on this host
 # ---------------------------------------------------------------------------
 def thread_counts(cpus):
@@ -392,6 +509,8 @@ def main():
     ap.add_argument("--moe-steps", type=int, default=0,
                     help="layers timed per token count (0: the defaults, 100 / 100 / 20)")
     ap.add_argument("--no-qwen15", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-steps", type=int, default=32)
     ap.add_argument("--no-gemv", action="store_true",
                     help="skip the GEMV headline (profiling runs of other legs; value is null)")
     args = ap.parse_args()
@@ -420,7 +539,7 @@ def main():
         types = [names[t.strip()] for t in args.sweep_types.split(",") if t.strip()]
         sweep = bench_sweep(dev, types, min(args.warmup, 5))
 
-    moe = moe15 = None
+    moe = moe15 = dec = None
     M = None
     if not args.no_moe:
         M = build_qwen3(dev, args.moe_layers)
@@ -434,6 +553,12 @@ def main():
                 "%.0f GB/s (%.1f%% of HBM peak)" % (T, r["ms_per_step"] * 1e3, r["tokens_per_s"],
                                                    r["touched_experts"], r["achieved_gbps"],
                                                    100 * r["roofline_frac"]))
+        if not args.no_decode:
+            dec = bench_decode(dev, M, args.decode_steps, 3, Q.ORDER_AVX2)
+            log("bench: decode step Qwen3-30B-A3B shape, %d layers at ~%.0f positions: %.3f ms, "
+                "%.1f tokens/s, %.0f GB/s algorithmic (%.1f%% of HBM peak)" % (
+                    dec["layers"], dec["positions"], dec["ms_per_step"], dec["tokens_per_s"],
+                    dec["achieved_gbps"], 100 * dec["roofline_frac"]))
         M["slab"].free()
         if not args.no_qwen15:
             M15 = build_qwen15(dev, 8)
@@ -490,6 +615,7 @@ def main():
         "gemv_sweep": sweep,
         "moe_qwen3": moe,
         "moe_qwen15": moe15,
+        "decode_qwen3": dec,
         "copy_kernel_gbps": round(cal["gbps"], 1),
     }
     print(json.dumps(out), flush=True)

@@ -235,13 +235,13 @@ int qr_dequantize(qr_ctx* ctx, uint32_t type, const void* src, int rows, int n, 
 int qr_rmsnorm(qr_ctx* ctx, float* o, float* x, const float* add, const float* w, int n);
 
 /* The attention of forward_runtime (src/runtime.c:136-193) over positions
- * 0..npos-1 of a paged cache: position t's row is at page ptab[t / page],
+ * 0..npos-1 of a paged cache (page a power of two): position t's row is at page ptab[t / page],
  * slot t % page (rows of qr_kv_row_bytes(kv_type, n_kv_heads * head_dim)
  * bytes, kv head h's elements at h * head_dim).  Scores are dot_ref
  * (src/kernels.c:162-168) times 1 / sqrtf(head_dim), softmax_ref per head,
  * then each output element sums att * v over the positions in order.
  * q, out: [n_heads][head_dim]; att: scratch [n_heads][npos] (left holding the
- * normalised weights).  head_dim a multiple of 32 up to 512; npos <= 32768. */
+ * normalised weights).  head_dim a multiple of 32 up to 512; npos <= 22528. */
 int qr_attention(qr_ctx* ctx, const float* q, const void* kc, const void* vc,
                  const int32_t* ptab, int page, int kv_type, int npos, int n_heads,
                  int n_kv_heads, int head_dim, float* att, float* out);
@@ -291,7 +291,7 @@ typedef struct qr_decoder qr_decoder;
 
 /* A decoder over `model` (its weights stay the caller's): the activations, a
  * paged KV cache of seq_len positions per layer (pages of `page` positions,
- * 0 = 256; identity page table), and the RoPE cos / sin of every position,
+ * a power of two, 0 = 256; identity page table), and the RoPE cos / sin of every position,
  * computed at creation with the host C library's powf / cosf / sinf as
  * apply_rope calls them (src/runtime.c:19-41; its frequency index runs over
  * the whole q vector, as there).  `order` is the reference build

@@ -87,58 +87,137 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ tab, 
 }
 
 // ---------------------------------------------------------------------------
+// Sequential sums.  The reference adds n terms one at a time (rmsnorm's sum
+// of squares, softmax's denominator); lane 0 does the same here, reading the
+// terms from LDS sixteen at a time while earlier reads are still in flight.
+// The terms are produced in parallel beforehand.
+// ---------------------------------------------------------------------------
+__device__ inline float seq_sum_lds(const float* __restrict__ p, int n) {
+  float s = 0.0f;
+  int i = 0;
+  for (; i + 16 <= n; i += 16) {
+    float4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[k] = *reinterpret_cast<const float4*>(p + i + 4 * k);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      s += v[k].x;
+      s += v[k].y;
+      s += v[k].z;
+      s += v[k].w;
+    }
+  }
+  for (; i < n; i++) s += p[i];
+  return s;
+}
+
+// ---------------------------------------------------------------------------
 // rmsnorm_ref (src/kernels.c:170-180), optionally after x += add (the
-// residual of src/runtime.c:196-198): the squares go to LDS in parallel, lane
-// 0 adds them in order, the workgroup scales.  n <= kNormMax.
+// residual of src/runtime.c:196-198).  Every thread loads its share of x (and
+// add, w) at once, the squares go to LDS, lane 0 adds them in order, the
+// workgroup scales from registers.  n <= kNormMax; VEC: n % 4 == 0.
 // ---------------------------------------------------------------------------
 constexpr int kNormMax = 8192;
+constexpr int kNormThreads = 512;
+constexpr int kNormPer = kNormMax / 4 / kNormThreads;  // float4 per thread
 
-__global__ __launch_bounds__(256) void k_rmsnorm(float* __restrict__ x,
-                                                 const float* __restrict__ add,
-                                                 const float* __restrict__ w, int n,
-                                                 float* __restrict__ o) {
+template <bool VEC>
+__global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ x,
+                                                          const float* __restrict__ add,
+                                                          const float* __restrict__ w, int n,
+                                                          float* __restrict__ o) {
   __shared__ __align__(16) float sq[kNormMax];
   __shared__ float scale_s;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    float xi = x[i];
-    if (add) {
-      xi = xi + add[i];
-      x[i] = xi;
-    }
-    sq[i] = xi * xi;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float ss = 0.0f;
-    int i = 0;
-    for (; i + 16 <= n; i += 16) {
-      float4 v[4];
+  if constexpr (VEC) {
+    const int n4 = n >> 2;
+    float4* x4 = reinterpret_cast<float4*>(x);
+    float4 xv[kNormPer], wv[kNormPer], av[kNormPer];
 #pragma unroll
-      for (int k = 0; k < 4; k++) v[k] = *reinterpret_cast<const float4*>(sq + i + 4 * k);
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        ss += v[k].x;
-        ss += v[k].y;
-        ss += v[k].z;
-        ss += v[k].w;
+    for (int j = 0; j < kNormPer; j++) {
+      const int i4 = threadIdx.x + j * kNormThreads;
+      if (i4 < n4) {
+        xv[j] = x4[i4];
+        wv[j] = reinterpret_cast<const float4*>(w)[i4];
+        if (add) av[j] = reinterpret_cast<const float4*>(add)[i4];
       }
     }
-    for (; i < n; i++) ss += sq[i];
-    ss = ss / (float)n + 1e-5f;
-    scale_s = 1.0f / sqrtf(ss);
+#pragma unroll
+    for (int j = 0; j < kNormPer; j++) {
+      const int i4 = threadIdx.x + j * kNormThreads;
+      if (i4 < n4) {
+        if (add) {
+          xv[j].x = xv[j].x + av[j].x;
+          xv[j].y = xv[j].y + av[j].y;
+          xv[j].z = xv[j].z + av[j].z;
+          xv[j].w = xv[j].w + av[j].w;
+          x4[i4] = xv[j];
+        }
+        float4 q;
+        q.x = xv[j].x * xv[j].x;
+        q.y = xv[j].y * xv[j].y;
+        q.z = xv[j].z * xv[j].z;
+        q.w = xv[j].w * xv[j].w;
+        reinterpret_cast<float4*>(sq)[i4] = q;
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float ss = seq_sum_lds(sq, n);
+      ss = ss / (float)n + 1e-5f;
+      scale_s = 1.0f / sqrtf(ss);
+    }
+    __syncthreads();
+    const float scale = scale_s;
+#pragma unroll
+    for (int j = 0; j < kNormPer; j++) {
+      const int i4 = threadIdx.x + j * kNormThreads;
+      if (i4 < n4) {
+        float4 r;
+        r.x = wv[j].x * (xv[j].x * scale);
+        r.y = wv[j].y * (xv[j].y * scale);
+        r.z = wv[j].z * (xv[j].z * scale);
+        r.w = wv[j].w * (xv[j].w * scale);
+        reinterpret_cast<float4*>(o)[i4] = r;
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      float xi = x[i];
+      if (add) {
+        xi = xi + add[i];
+        x[i] = xi;
+      }
+      sq[i] = xi * xi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float ss = seq_sum_lds(sq, n);
+      ss = ss / (float)n + 1e-5f;
+      scale_s = 1.0f / sqrtf(ss);
+    }
+    __syncthreads();
+    const float scale = scale_s;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) o[i] = w[i] * (x[i] * scale);
   }
-  __syncthreads();
-  const float scale = scale_s;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) o[i] = w[i] * (x[i] * scale);
+}
+
+hipError_t rmsnorm_launch(float* x, const float* add, const float* w, int n, float* o,
+                          hipStream_t s) {
+  const bool vec = (n & 3) == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                                     reinterpret_cast<uintptr_t>(o) |
+                                     reinterpret_cast<uintptr_t>(add)) & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL(k_rmsnorm<true>, dim3(1), dim3(kNormThreads), 0, s, x, add, w, n, o);
+  else
+    hipLaunchKernelGGL(k_rmsnorm<false>, dim3(1), dim3(kNormThreads), 0, s, x, add, w, n, o);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
 // apply_rope (src/runtime.c:19-41) of q (qd) and k (the first kvd of its
 // pairs) with the position's cos / sin, then the K and V rows of the
 // position: fp32 copies or quantize_row_q8_0 (src/quant.c:143-158) blocks.
-// One workgroup; kvd <= kRopeKvMax.
 // ---------------------------------------------------------------------------
-constexpr int kRopeKvMax = 4096;
 
 __device__ inline void q8_block_store(const float* __restrict__ v, uint8_t* __restrict__ out) {
   float amax = 0.0f;
@@ -159,12 +238,13 @@ __device__ inline void q8_block_store(const float* __restrict__ v, uint8_t* __re
 struct KvView {
   const uint8_t* base;  // K or V pages
   const int32_t* ptab;  // this layer's page table
-  int page;
+  int page;             // a power of two
+  int page_shift;       // log2(page)
   size_t row_bytes;
   int kv_type;
   __device__ const uint8_t* row(int t) const {
-    const int pp = ptab[t / page];
-    return base + ((size_t)pp * page + (size_t)(t % page)) * row_bytes;
+    const int pp = ptab[t >> page_shift];
+    return base + (((size_t)pp << page_shift) + (size_t)(t & (page - 1))) * row_bytes;
   }
 };
 
@@ -172,45 +252,63 @@ struct KvView {
 // decode step), else the argument.
 __device__ inline int npos_of(const int32_t* st, int npos) { return st ? st[1] + 1 : npos; }
 
+// One thread per q pair (threads 0 .. qd/2 - 1), then one per 32-element
+// block of k and of v (2 kvd / 32 threads): k's pairs rotate in registers,
+// then the block is stored as fp32 or as a quantize_row_q8_0 block.  grid
+// ceil((qd / 2 + 2 kvd / 32) / 256).
 __global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ q, const float* __restrict__ k,
                                                  const float* __restrict__ v,
                                                  const float* __restrict__ rope,
                                                  const int32_t* __restrict__ st, int qd, int kvd,
                                                  KvView K, uint8_t* __restrict__ vbase) {
-  __shared__ __align__(16) float ks[kRopeKvMax];
-  __shared__ __align__(16) float vs[kRopeKvMax];
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
   const int pos = st[1];
   const float* cs = rope + (size_t)pos * qd;
-  for (int p = threadIdx.x; p < qd / 2; p += blockDim.x) {
-    const int i = 2 * p;
-    const float c = cs[i], s = cs[i + 1];
-    const float q0 = q[i], q1 = q[i + 1];
-    q[i] = q0 * c - q1 * s;
-    q[i + 1] = q0 * s + q1 * c;
-    if (i < kvd) {
-      const float k0 = k[i], k1 = k[i + 1];
-      ks[i] = k0 * c - k1 * s;
-      ks[i + 1] = k0 * s + k1 * c;
+  const int np = qd >> 1, nb = kvd >> 5;
+  if (g < np) {
+    const float2 c2 = reinterpret_cast<const float2*>(cs)[g];
+    const float2 q2 = reinterpret_cast<const float2*>(q)[g];
+    float2 r;
+    r.x = q2.x * c2.x - q2.y * c2.y;
+    r.y = q2.x * c2.y + q2.y * c2.x;
+    reinterpret_cast<float2*>(q)[g] = r;
+    return;
+  }
+  const int b = g - np;
+  if (b >= 2 * nb) return;
+  const bool isv = b >= nb;
+  const int bi = isv ? b - nb : b;
+  float vals[32];
+  const float4* src = reinterpret_cast<const float4*>((isv ? v : k) + 32 * bi);
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const float4 f = src[j];
+    vals[4 * j] = f.x;
+    vals[4 * j + 1] = f.y;
+    vals[4 * j + 2] = f.z;
+    vals[4 * j + 3] = f.w;
+  }
+  if (!isv) {
+    const float4* c4 = reinterpret_cast<const float4*>(cs + 32 * bi);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float4 c = c4[j];  // cos, sin of two pairs
+      const float k0 = vals[4 * j], k1 = vals[4 * j + 1], k2 = vals[4 * j + 2], k3 = vals[4 * j + 3];
+      vals[4 * j] = k0 * c.x - k1 * c.y;
+      vals[4 * j + 1] = k0 * c.y + k1 * c.x;
+      vals[4 * j + 2] = k2 * c.z - k3 * c.w;
+      vals[4 * j + 3] = k2 * c.w + k3 * c.z;
     }
   }
-  for (int i = threadIdx.x; i < kvd; i += blockDim.x) vs[i] = v[i];
-  __syncthreads();
   uint8_t* krow = const_cast<uint8_t*>(K.row(pos));
-  uint8_t* vrow = vbase + (size_t)(krow - K.base);
+  uint8_t* row = isv ? vbase + (size_t)(krow - K.base) : krow;
   if (K.kv_type == QR_KV_Q8_0) {
-    const int nb = kvd / 32;
-    for (int b = threadIdx.x; b < 2 * nb; b += blockDim.x) {
-      const bool isv = b >= nb;
-      const int bi = isv ? b - nb : b;
-      q8_block_store((isv ? vs : ks) + 32 * bi, (isv ? vrow : krow) + (size_t)bi * QR_Q8_BYTES);
-    }
+    q8_block_store(vals, row + (size_t)bi * QR_Q8_BYTES);
   } else {
-    float* kf = reinterpret_cast<float*>(krow);
-    float* vf = reinterpret_cast<float*>(vrow);
-    for (int i = threadIdx.x; i < kvd; i += blockDim.x) {
-      kf[i] = ks[i];
-      vf[i] = vs[i];
-    }
+    float4* dst = reinterpret_cast<float4*>(reinterpret_cast<float*>(row) + 32 * bi);
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      dst[j] = make_float4(vals[4 * j], vals[4 * j + 1], vals[4 * j + 2], vals[4 * j + 3]);
   }
 }
 
@@ -245,14 +343,14 @@ __global__ __launch_bounds__(256) void k_kv_write(const float* __restrict__ ksrc
 // Attention (src/runtime.c:136-193).
 // ---------------------------------------------------------------------------
 constexpr int kHdMax = 512;          // the reference's own bound (kh_buf[512], src/runtime.c:145)
-constexpr int kSoftMaxMax = 32768;   // positions: the softmax's exponentials stay in LDS
 constexpr size_t kDecLdsMax = 160 * 1024;
 
 // att[h][t] = dot_ref(q_h, K[t]_kvh) * inv_sqrt for the kv_mul query heads of
 // kv head blockIdx.y and positions [64 blockIdx.x, +64): the K tile is
-// dequantized once into LDS (rows padded to hd + 1 floats), then one thread
-// per (head, position) adds the hd products in order.  Dynamic LDS:
-// (64 (hd + 1) + kv_mul hd) floats.
+// dequantized once into LDS (rows padded to hd + 4 floats), then one thread
+// per (head, position) adds the hd products in order; a thread runs the
+// chains of heads m and m + 4 side by side, which share the K row.  Dynamic
+// LDS: (64 (hd + 4) + kv_mul hd) floats.
 constexpr int kScTile = 64;
 
 __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q, KvView K,
@@ -264,195 +362,320 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
   const int t0 = blockIdx.x * kScTile;
   if (t0 >= npos) return;
   const int kvh = blockIdx.y;
-  const int ks = hd + 1;
+  const int ks = hd + 4;
   float* kt = sm;
   float* qs = sm + kScTile * ks;
   const int nt = min(kScTile, npos - t0);
-  for (int i = threadIdx.x; i < kv_mul * hd; i += blockDim.x)
-    qs[i] = q[(size_t)kvh * kv_mul * hd + i];
+  for (int i = threadIdx.x * 4; i < kv_mul * hd; i += blockDim.x * 4)
+    *reinterpret_cast<float4*>(qs + i) =
+        *reinterpret_cast<const float4*>(q + (size_t)kvh * kv_mul * hd + i);
   if (K.kv_type == QR_KV_Q8_0) {
     const int bpr = hd / 32;
     for (int j = threadIdx.x; j < nt * bpr; j += blockDim.x) {
       const int tt = j / bpr, b = j - tt * bpr;
       const uint16_t* hw =
           reinterpret_cast<const uint16_t*>(K.row(t0 + tt) + (size_t)(kvh * bpr + b) * QR_Q8_BYTES);
-      const float d = qr_h2f(hw[0]);
+      uint32_t u[17];
+#pragma unroll
+      for (int w = 0; w < 17; w++) u[w] = hw[w];
+      const float d = qr_h2f(u[0]);
       float* dst = kt + tt * ks + 32 * b;
 #pragma unroll
-      for (int w = 0; w < 16; w++) {
-        const uint32_t u = hw[1 + w];
-        dst[2 * w] = (float)(int8_t)(u & 0xFFu) * d;
-        dst[2 * w + 1] = (float)(int8_t)(u >> 8) * d;
+      for (int w = 0; w < 8; w++) {
+        float4 f;
+        f.x = (float)(int8_t)(u[1 + 2 * w] & 0xFFu) * d;
+        f.y = (float)(int8_t)(u[1 + 2 * w] >> 8) * d;
+        f.z = (float)(int8_t)(u[2 + 2 * w] & 0xFFu) * d;
+        f.w = (float)(int8_t)(u[2 + 2 * w] >> 8) * d;
+        *reinterpret_cast<float4*>(dst + 4 * w) = f;
       }
     }
   } else {
-    for (int j = threadIdx.x; j < nt * hd; j += blockDim.x) {
+    for (int j = threadIdx.x * 4; j < nt * hd; j += blockDim.x * 4) {
       const int tt = j / hd, i = j - tt * hd;
-      kt[tt * ks + i] = reinterpret_cast<const float*>(K.row(t0 + tt))[(size_t)kvh * hd + i];
+      *reinterpret_cast<float4*>(kt + tt * ks + i) = *reinterpret_cast<const float4*>(
+          reinterpret_cast<const float*>(K.row(t0 + tt)) + (size_t)kvh * hd + i);
     }
   }
   __syncthreads();
-  for (int p = threadIdx.x; p < kv_mul * kScTile; p += blockDim.x) {
+  const int P = kv_mul * kScTile;
+  for (int p = threadIdx.x; p < P; p += 2 * blockDim.x) {
     const int m = p / kScTile, tt = p - m * kScTile;
-    if (tt >= nt) continue;
-    const float* qh = qs + m * hd;
+    const bool two = p + (int)blockDim.x < P;  // head m + 4, same position
     const float* kr = kt + tt * ks;
-    float s = 0.0f;
-    for (int i = 0; i < hd; i++) s += qh[i] * kr[i];
-    att[(size_t)(kvh * kv_mul + m) * att_stride + t0 + tt] = s * inv_sqrt;
-  }
-}
-
-// softmax_ref (src/kernels.c:191-207) of each head's npos scores, one
-// workgroup per head: the max over the workgroup (order-free: a max is
-// exact), the exponentials into LDS in parallel, lane 0 adds them in order,
-// then the workgroup scales.  Dynamic LDS: npos floats (the cache capacity).
-__global__ __launch_bounds__(256) void k_attn_softmax(float* __restrict__ att, int att_stride,
-                                                      const int32_t* __restrict__ st,
-                                                      int npos_arg) {
-  extern __shared__ __align__(16) float e[];
-  __shared__ float red[4];
-  __shared__ float inv_s;
-  const int npos = npos_of(st, npos_arg);
-  float* a = att + (size_t)blockIdx.x * att_stride;
-  const ExpTab tab = qr_expf_tab();
-  float mx = a[0];
-  for (int i = threadIdx.x; i < npos; i += blockDim.x) {
-    const float v = a[i];
-    mx = v > mx ? v : mx;
-  }
-  for (int o = 32; o > 0; o >>= 1) {
-    const float v = __shfl_xor(mx, o);
-    mx = v > mx ? v : mx;
-  }
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-  __syncthreads();
-  mx = red[0];
-  for (int w = 1; w < (int)(blockDim.x >> 6); w++) mx = red[w] > mx ? red[w] : mx;
-  // every lane runs the same number of rounds: the table lookup of
-  // qr_expf_w reads other lanes
-  const int rounds = (npos + blockDim.x - 1) / blockDim.x;
-  for (int r = 0; r < rounds; r++) {
-    const int i = r * blockDim.x + threadIdx.x;
-    const float v = i < npos ? a[i] : 0.0f;
-    const float ev = qr_expf_w(v - mx, tab);
-    if (i < npos) e[i] = ev;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float sum = 0.0f;
-    int i = 0;
-    for (; i + 16 <= npos; i += 16) {
-      float4 v[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) v[k] = *reinterpret_cast<const float4*>(e + i + 4 * k);
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        sum += v[k].x;
-        sum += v[k].y;
-        sum += v[k].z;
-        sum += v[k].w;
+    const float* q0 = qs + m * hd;
+    const float* q1 = q0 + 4 * hd;
+    float s0 = 0.0f, s1 = 0.0f;
+    if (two) {
+      for (int i = 0; i < hd; i += 4) {
+        const float4 kv = *reinterpret_cast<const float4*>(kr + i);
+        const float4 a = *reinterpret_cast<const float4*>(q0 + i);
+        const float4 c = *reinterpret_cast<const float4*>(q1 + i);
+        s0 += a.x * kv.x;
+        s1 += c.x * kv.x;
+        s0 += a.y * kv.y;
+        s1 += c.y * kv.y;
+        s0 += a.z * kv.z;
+        s1 += c.z * kv.z;
+        s0 += a.w * kv.w;
+        s1 += c.w * kv.w;
+      }
+    } else {
+      for (int i = 0; i < hd; i += 4) {
+        const float4 kv = *reinterpret_cast<const float4*>(kr + i);
+        const float4 a = *reinterpret_cast<const float4*>(q0 + i);
+        s0 += a.x * kv.x;
+        s0 += a.y * kv.y;
+        s0 += a.z * kv.z;
+        s0 += a.w * kv.w;
       }
     }
-    for (; i < npos; i++) sum += e[i];
-    inv_s = 1.0f / sum;
+    if (tt < nt) {
+      att[(size_t)(kvh * kv_mul + m) * att_stride + t0 + tt] = s0 * inv_sqrt;
+      if (two) att[(size_t)(kvh * kv_mul + m + 4) * att_stride + t0 + tt] = s1 * inv_sqrt;
+    }
   }
-  __syncthreads();
-  const float inv = inv_s;
-  for (int i = threadIdx.x; i < npos; i += blockDim.x) a[i] = e[i] * inv;
 }
 
+// softmax_ref (src/kernels.c:191-207) of one head's scores, then
 // o_h[c] = sum over t = 0 .. npos-1, in order, of att[h][t] * V[t]_kvh[c]
-// (src/runtime.c:182-190: each product rounded, then added).  A workgroup
-// owns kValCols elements of one head.  Waves 1..7 form the products of a
-// block of kValBlk positions into LDS (element-major, so one ds_read_b128
-// gives an element four consecutive positions) while lanes 0..31 of wave 0
-// add the previous block's products in position order.  grid
-// (hd / kValCols, n_heads), 512 threads.
+// (src/runtime.c:182-190: each product rounded, then added), for kValCols
+// elements c of head blockIdx.y.  grid (hd / kValCols, n_heads), 512 threads.
+//
+//  1. The scores go to LDS; their max over the workgroup (a max is exact, so
+//     its order does not matter; seeded with the first score, strict '>');
+//     the exponentials in parallel, in place.
+//  2. Lane 0 adds the exponentials in order (the softmax denominator) while
+//     waves 1 and 2 start loading the V values of the first two position
+//     blocks.
+//  3. Waves 1 and 2 form the products (e[t] * inv) * v of a block of kValBlk
+//     positions into LDS, element-major (one ds_read_b128 gives an element
+//     four consecutive positions), while lanes 0..31 of wave 0 add the
+//     previous block's products in position order.  Each block's V loads are
+//     issued two blocks ahead of their use.  Waves 3..7 only help in step 1.
+// Dynamic LDS: npos floats (the exponentials), then ceil(npos / page) ints
+// (this layer's page table).  att is only read.
 constexpr int kValCols = 32;
-constexpr int kValBlk = 128;
+constexpr int kValBlk = 256;
 constexpr int kValPitch = kValBlk + 4;
+constexpr int kSvThreads = 512;
+constexpr int kAttnMaxPos = 22528;  // exponentials (LDS) beside the product buffers
 
-__global__ __launch_bounds__(512) void k_attn_values(const float* __restrict__ att, int att_stride,
-                                                     KvView V, const int32_t* __restrict__ st,
-                                                     int npos_arg, int kv_mul, int hd,
-                                                     float* __restrict__ out) {
+// Producer threads (waves 1 and 2) take positions pid and pid + 128 of a
+// block: the raw V values of their kValCols elements.
+constexpr int kSvProd = 128;
+constexpr int kSvPer = kValBlk / kSvProd;
+struct SvRegs {
+  uint32_t r[kSvPer][kValCols];  // Q8_0: [0] = d, [1..8] = the 32 qs bytes; fp32: the values
+};
+
+// V.row(t) with the page table read from LDS (pt), so that a row's address
+// does not wait on a global load.
+__device__ inline const uint8_t* kv_row_lds(const KvView& V, const int32_t* pt, int t) {
+  return V.base + (((size_t)pt[t >> V.page_shift] << V.page_shift) + (size_t)(t & (V.page - 1))) *
+                      V.row_bytes;
+}
+
+// Every producer loads (positions past the end read the last row and are
+// ignored): with no branch around them the loads' count is static, so a later
+// use waits only for its own loads.
+template <int KVT>
+__device__ inline void sv_load(SvRegs& R, const KvView& V, const int32_t* pt, int b, int npos,
+                               int pid, int kvh, int hd, int c0) {
+  const int e0 = kvh * hd + c0;
+#pragma unroll
+  for (int u = 0; u < kSvPer; u++) {
+    const int t = min(b * kValBlk + pid + u * kSvProd, npos - 1);
+    const uint8_t* row = kv_row_lds(V, pt, t);
+    if constexpr (KVT == QR_KV_Q8_0) {
+      const uint8_t* blk = row + (size_t)(e0 >> 5) * QR_Q8_BYTES;
+      R.r[u][0] = *reinterpret_cast<const uint16_t*>(blk);
+      __builtin_memcpy(&R.r[u][1], blk + 2, 32);  // 2-byte aligned
+    } else {
+      const uint4* f = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(row) + e0);
+#pragma unroll
+      for (int j = 0; j < kValCols / 4; j++) {
+        const uint4 w = f[j];
+        R.r[u][4 * j] = w.x;
+        R.r[u][4 * j + 1] = w.y;
+        R.r[u][4 * j + 2] = w.z;
+        R.r[u][4 * j + 3] = w.w;
+      }
+    }
+  }
+}
+
+template <int KVT>
+__device__ inline void sv_produce(const SvRegs& R, int b, int npos, int pid,
+                                  const float* __restrict__ e, float inv, float* __restrict__ pb) {
+#pragma unroll
+  for (int u = 0; u < kSvPer; u++) {
+    const int tt = pid + u * kSvProd;
+    const int t = b * kValBlk + tt;
+    const float at = t < npos ? e[t] * inv : 0.0f;  // softmax_ref's x[i] *= inv
+    if constexpr (KVT == QR_KV_Q8_0) {
+      const float d = qr_h2f(R.r[u][0]);
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const uint32_t w = R.r[u][1 + j];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float v = (float)(int8_t)((w >> (8 * q)) & 0xFFu) * d;
+          pb[(4 * j + q) * kValPitch + tt] = at * v;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < kValCols; c++) pb[c * kValPitch + tt] = at * __uint_as_float(R.r[u][c]);
+    }
+  }
+}
+
+__device__ inline void sv_chain(const float* __restrict__ pb, int cnt, float& acc) {
+  if (cnt == kValBlk) {
+#pragma unroll
+    for (int tt = 0; tt < kValBlk; tt += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(pb + tt);
+      acc += v.x;
+      acc += v.y;
+      acc += v.z;
+      acc += v.w;
+    }
+  } else {
+    for (int tt = 0; tt < cnt; tt++) acc += pb[tt];
+  }
+}
+
+template <int KVT>
+__global__ __launch_bounds__(kSvThreads) void k_attn_sv(const float* __restrict__ att,
+                                                        int att_stride,
+                                                        KvView V, const int32_t* __restrict__ st,
+                                                        int npos_arg, int lds_cap, int kv_mul,
+                                                        int hd, float* __restrict__ out) {
+  extern __shared__ __align__(16) float e[];
   __shared__ __align__(16) float prod[2][kValCols * kValPitch];
+  __shared__ float red[kSvThreads / 64];
+  __shared__ float inv_s;
   const int npos = npos_of(st, npos_arg);
+  int32_t* pt = reinterpret_cast<int32_t*>(e + lds_cap);
+  for (int i = threadIdx.x; i < (npos + V.page - 1) / V.page; i += kSvThreads) pt[i] = V.ptab[i];
   const int h = blockIdx.y;
   const int c0 = blockIdx.x * kValCols;
   const int kvh = h / kv_mul;
   const float* a = att + (size_t)h * att_stride;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int nblk = (npos + kValBlk - 1) / kValBlk;
-  // products of block b into buffer b & 1: item j = (position tt = j % kValBlk,
-  // elements 4 (j / kValBlk) .. +3)
-  auto produce = [&](int b) {
-    float* pb = prod[b & 1];
-    const int t0 = b * kValBlk;
-    for (int j = threadIdx.x - 64; j < kValBlk * (kValCols / 4); j += 448) {
-      const int tt = j % kValBlk, cg = j / kValBlk;
-      const int t = t0 + tt;
-      float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
-      if (t < npos) {
-        const float at = a[t];
-        const uint8_t* row = V.row(t);
-        const int e0 = kvh * hd + c0 + 4 * cg;
-        float v0, v1, v2, v3;
-        if (V.kv_type == QR_KV_Q8_0) {
-          const uint8_t* blk = row + (size_t)(e0 >> 5) * QR_Q8_BYTES;
-          const uint16_t* hw = reinterpret_cast<const uint16_t*>(blk);
-          const float d = qr_h2f(hw[0]);
-          const int o = (e0 & 31) >> 1;  // even element offset -> halfword index
-          const uint32_t u0 = hw[1 + o], u1 = hw[2 + o];
-          v0 = (float)(int8_t)(u0 & 0xFFu) * d;
-          v1 = (float)(int8_t)(u0 >> 8) * d;
-          v2 = (float)(int8_t)(u1 & 0xFFu) * d;
-          v3 = (float)(int8_t)(u1 >> 8) * d;
-        } else {
-          const float4 f = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(row) + e0);
-          v0 = f.x;
-          v1 = f.y;
-          v2 = f.z;
-          v3 = f.w;
-        }
-        p0 = at * v0;
-        p1 = at * v1;
-        p2 = at * v2;
-        p3 = at * v3;
-      }
-      const int c = 4 * cg;
-      pb[(c + 0) * kValPitch + tt] = p0;
-      pb[(c + 1) * kValPitch + tt] = p1;
-      pb[(c + 2) * kValPitch + tt] = p2;
-      pb[(c + 3) * kValPitch + tt] = p3;
-    }
-  };
-  float acc = 0.0f;
-  if (wave > 0) produce(0);
-  __syncthreads();
-  for (int b = 0; b < nblk; b++) {
-    if (wave > 0) {
-      if (b + 1 < nblk) produce(b + 1);
-    } else if (lane < kValCols) {
-      const float* pb = prod[b & 1] + lane * kValPitch;
-      const int cnt = min(kValBlk, npos - b * kValBlk);
-      if (cnt == kValBlk) {
+  const int pid = threadIdx.x - 64;  // producer index: waves 1 and 2 (pid < kSvProd)
+  const bool producer = wave > 0 && pid < kSvProd;
+  const ExpTab tab = qr_expf_tab();
+
+  // 1. scores -> LDS and their max; eight loads in flight per thread
+  float mx = a[0];
+  for (int base = 0; base < npos; base += 8 * kSvThreads) {
+    float v[8];
 #pragma unroll
-        for (int tt = 0; tt < kValBlk; tt += 4) {
-          const float4 v = *reinterpret_cast<const float4*>(pb + tt);
-          acc += v.x;
-          acc += v.y;
-          acc += v.z;
-          acc += v.w;
-        }
-      } else {
-        for (int tt = 0; tt < cnt; tt++) acc += pb[tt];
+    for (int k = 0; k < 8; k++) v[k] = a[min(base + k * kSvThreads + (int)threadIdx.x, npos - 1)];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int i = base + k * kSvThreads + threadIdx.x;
+      if (i < npos) {
+        e[i] = v[k];
+        mx = v[k] > mx ? v[k] : mx;
       }
     }
-    __syncthreads();
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v = __shfl_xor(mx, o);
+    mx = v > mx ? v : mx;
+  }
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int w = 1; w < kSvThreads / 64; w++) mx = red[w] > mx ? red[w] : mx;
+  // every lane runs the same number of rounds (qr_expf_w reads other lanes)
+  const int rounds = (npos + kSvThreads - 1) / kSvThreads;
+  for (int r = 0; r < rounds; r++) {
+    const int i = r * kSvThreads + threadIdx.x;
+    const float v = i < npos ? e[i] : 0.0f;
+    const float ev = qr_expf_w(v - mx, tab);
+    if (i < npos) e[i] = ev;
+  }
+  __syncthreads();
+
+  // 2. the denominator; the first V loads
+  SvRegs A, B;
+  if (producer) {
+    sv_load<KVT>(A, V, pt, 0, npos, pid, kvh, hd, c0);
+    sv_load<KVT>(B, V, pt, 1, npos, pid, kvh, hd, c0);
+  } else if (wave == 0 && lane == 0) {
+    inv_s = 1.0f / seq_sum_lds(e, npos);
+  }
+  __syncthreads();
+  const float inv = inv_s;
+
+  // 3. products two blocks ahead of the loads, one block ahead of the adds.
+  // The adding wave and the producing waves run separate loops that pass
+  // the same barriers in the same number (each wave takes one side): the
+  // producers' loop then holds only unconditional loads, so each product
+  // waits for its own block's loads alone.
+  const int nblk = (npos + kValBlk - 1) / kValBlk;
+  float acc = 0.0f;
+  if (producer) {
+    sv_produce<KVT>(A, 0, npos, pid, e, inv, prod[0]);
+    sv_load<KVT>(A, V, pt, 2, npos, pid, kvh, hd, c0);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    for (int b = 0; b < nblk; b += 2) {
+      if (lane < kValCols) sv_chain(prod[0] + lane * kValPitch, min(kValBlk, npos - b * kValBlk), acc);
+      __syncthreads();
+      if (b + 1 >= nblk) break;
+      if (lane < kValCols)
+        sv_chain(prod[1] + lane * kValPitch, min(kValBlk, npos - (b + 1) * kValBlk), acc);
+      __syncthreads();
+    }
+  } else if (producer) {
+    for (int b = 0; b < nblk; b += 2) {
+      sv_produce<KVT>(B, b + 1, npos, pid, e, inv, prod[1]);
+      sv_load<KVT>(B, V, pt, b + 3, npos, pid, kvh, hd, c0);
+      __syncthreads();
+      if (b + 1 >= nblk) break;
+      sv_produce<KVT>(A, b + 2, npos, pid, e, inv, prod[0]);
+      sv_load<KVT>(A, V, pt, b + 4, npos, pid, kvh, hd, c0);
+      __syncthreads();
+    }
+  } else {
+    for (int b = 0; b < nblk; b += 2) {
+      __syncthreads();
+      if (b + 1 >= nblk) break;
+      __syncthreads();
+    }
   }
   if (wave == 0 && lane < kValCols) out[(size_t)h * hd + c0 + lane] = acc;
+}
+
+// k_attn_sv's dynamic LDS for a cache of cap positions in pages of `page`,
+// and whether it fits beside the kernel's static LDS.
+inline size_t sv_lds_bytes(int cap, int page) {
+  return (size_t)cap * 4 + (size_t)((cap + page - 1) / page) * 4;
+}
+hipError_t sv_launch(const float* att, int att_stride, const KvView& V, const int32_t* st,
+                     int npos, int lds_cap, int n_heads, int kv_mul, int hd, float* out,
+                     hipStream_t s) {
+  const dim3 grid(hd / kValCols, n_heads);
+  const size_t lds = sv_lds_bytes(lds_cap, V.page);
+  if (V.kv_type == QR_KV_Q8_0)
+    hipLaunchKernelGGL(k_attn_sv<QR_KV_Q8_0>, grid, dim3(kSvThreads), lds, s, att, att_stride, V,
+                       st, npos, lds_cap, kv_mul, hd, out);
+  else
+    hipLaunchKernelGGL(k_attn_sv<QR_KV_F32>, grid, dim3(kSvThreads), lds, s, att, att_stride, V,
+                       st, npos, lds_cap, kv_mul, hd, out);
+  return hipGetLastError();
+}
+
+inline bool sv_lds_ok(int cap, int page) {
+  const size_t stat = sizeof(float) * (2 * kValCols * kValPitch + kSvThreads / 64 + 1);
+  return sv_lds_bytes(cap, page) + stat <= kDecLdsMax;
 }
 
 }  // namespace qr
@@ -498,6 +721,7 @@ namespace {
 
 std::atomic<bool> g_sc_opt[64];
 std::atomic<bool> g_sm_opt[64];
+std::atomic<bool> g_sm_opt2[64];
 
 #define DEC_HIP(call, what)                                                        \
   do {                                                                             \
@@ -512,6 +736,7 @@ KvView kv_view(const qr_decoder* d, int layer, bool values) {
   K.base = (values ? d->vc : d->kc) + (size_t)layer * d->layer_pages_bytes;
   K.ptab = d->ptab + (size_t)layer * d->ppl;
   K.page = d->page;
+  K.page_shift = __builtin_ctz((unsigned)d->page);
   K.row_bytes = d->row_bytes;
   K.kv_type = d->kv_type;
   return K;
@@ -539,37 +764,28 @@ hipError_t enqueue_step(qr_decoder* d, float* logits, float* xout, hipStream_t s
   const float inv_sqrt = 1.0f / sqrtf((float)d->hd);
   for (int l = 0; l < d->nl; l++) {
     const qr_layer& L = d->layers[l];
-    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), 0, s, d->x, (const float*)nullptr,
-                       L.rms_att, dim, d->xb);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = rmsnorm_launch(d->x, nullptr, L.rms_att, dim, d->xb, s))) return e;
     if ((e = matmul_q_dev(L.wq, L.wq_type, d->order, d->xb, d->q, d->qd, dim, s))) return e;
     if ((e = matmul_q_dev(L.wk, L.wk_type, d->order, d->xb, d->k, d->kvd, dim, s))) return e;
     if ((e = matmul_q_dev(L.wv, L.wv_type, d->order, d->xb, d->v, d->kvd, dim, s))) return e;
     const KvView K = kv_view(d, l, false), V = kv_view(d, l, true);
-    hipLaunchKernelGGL(k_rope_kv, dim3(1), dim3(256), 0, s, d->q, d->k, d->v, d->rope, d->st,
-                       d->qd, d->kvd, K, const_cast<uint8_t*>(V.base));
+    hipLaunchKernelGGL(k_rope_kv, dim3((d->qd / 2 + 2 * (d->kvd / 32) + 255) / 256), dim3(256), 0,
+                       s, d->q, d->k, d->v, d->rope, d->st, d->qd, d->kvd, K,
+                       const_cast<uint8_t*>(V.base));
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_scores, dim3((d->cap + kScTile - 1) / kScTile, d->nkv), dim3(256),
                        d->sc_lds, s, d->q, K, d->st, 0, d->kv_mul, d->hd, inv_sqrt, d->cap,
                        d->att);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_softmax, dim3(d->nh), dim3(256), (size_t)d->cap * 4, s, d->att,
-                       d->cap, d->st, 0);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_values, dim3(d->hd / kValCols, d->nh), dim3(512), 0, s, d->att,
-                       d->cap, V, d->st, 0, d->kv_mul, d->hd, d->ao);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = sv_launch(d->att, d->cap, V, d->st, 0, d->cap, d->nh, d->kv_mul, d->hd, d->ao, s)))
+      return e;
     if ((e = matmul_q_dev(L.wo, L.wo_type, d->order, d->ao, d->xb2, dim, d->qd, s))) return e;
-    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), 0, s, d->x, (const float*)d->xb2,
-                       L.rms_ffn, dim, d->xb);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = rmsnorm_launch(d->x, d->xb2, L.rms_ffn, dim, d->xb, s))) return e;
     MoeScratch ms;
     moe_scratch_carve(d->moe_base, &L.moe, 1, &ms);
     if ((e = moe_forward_launch(&L.moe, d->x, d->xb, 1, d->order, ms, s))) return e;
   }
-  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), 0, s, d->x, (const float*)nullptr,
-                     d->rms_final, dim, d->xb);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if ((e = rmsnorm_launch(d->x, nullptr, d->rms_final, dim, d->xb, s))) return e;
   if ((e = matmul_q_dev(d->wcls, d->wcls_type, d->order, d->xb, logits, d->vocab, dim, s)))
     return e;
   if (xout) {
@@ -645,8 +861,7 @@ int qr_rmsnorm(qr_ctx* c, float* o, float* x, const float* add, const float* w, 
   if (n <= 0 || n > kNormMax) return set_error(QR_ERR_INVALID, "qr_rmsnorm: n=%d (1..%d)", n, kNormMax);
   if (!o || !x || !w) return set_error(QR_ERR_INVALID, "qr_rmsnorm: null pointer");
   DEC_HIP(hipSetDevice(ctx_device(c)), "hipSetDevice");
-  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), 0, ctx_stream(c), x, add, w, n, o);
-  DEC_HIP(hipGetLastError(), "k_rmsnorm");
+  DEC_HIP(rmsnorm_launch(x, add, w, n, o, ctx_stream(c)), "k_rmsnorm");
   return QR_OK;
 }
 
@@ -661,22 +876,27 @@ int qr_attention(qr_ctx* c, const float* q, const void* kc, const void* vc, cons
   if (head_dim <= 0 || head_dim % kValCols || head_dim > kHdMax)
     return set_error(QR_ERR_INVALID, "qr_attention: head_dim %d (a multiple of 32, <= %d)",
                      head_dim, kHdMax);
-  if (page <= 0) return set_error(QR_ERR_INVALID, "qr_attention: page %d", page);
+  if (page <= 0 || (page & (page - 1)))
+    return set_error(QR_ERR_INVALID, "qr_attention: page %d (a power of two)", page);
   const size_t rb = qr_kv_row_bytes(kv_type, n_kv_heads * head_dim);
   if (!rb) return set_error(QR_ERR_INVALID, "qr_attention: kv_type %d", kv_type);
-  if (npos <= 0 || npos > kSoftMaxMax)
-    return set_error(QR_ERR_INVALID, "qr_attention: npos %d (1..%d)", npos, kSoftMaxMax);
+  if (npos <= 0 || npos > kAttnMaxPos)
+    return set_error(QR_ERR_INVALID, "qr_attention: npos %d (1..%d)", npos, kAttnMaxPos);
+  if (!sv_lds_ok(npos, page))
+    return set_error(QR_ERR_UNSUPPORTED, "qr_attention: %d positions in pages of %d", npos, page);
   if (!al16(kc) || !al16(vc)) return set_error(QR_ERR_INVALID, "qr_attention: cache alignment");
   const int kv_mul = n_heads / n_kv_heads;
-  const size_t sc_lds = ((size_t)kScTile * (head_dim + 1) + (size_t)kv_mul * head_dim) * 4;
+  const size_t sc_lds = ((size_t)kScTile * (head_dim + 4) + (size_t)kv_mul * head_dim) * 4;
   if (sc_lds > kDecLdsMax) return set_error(QR_ERR_UNSUPPORTED, "qr_attention: head group too large");
   DEC_HIP(hipSetDevice(ctx_device(c)), "hipSetDevice");
   DEC_HIP(lds_opt_in((const void*)k_attn_scores, g_sc_opt), "lds opt-in");
-  DEC_HIP(lds_opt_in((const void*)k_attn_softmax, g_sm_opt), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_Q8_0>, g_sm_opt), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_F32>, g_sm_opt2), "lds opt-in");
   KvView K;
   K.base = static_cast<const uint8_t*>(kc);
   K.ptab = ptab;
   K.page = page;
+  K.page_shift = __builtin_ctz((unsigned)page);
   K.row_bytes = rb;
   K.kv_type = kv_type;
   KvView V = K;
@@ -687,12 +907,10 @@ int qr_attention(qr_ctx* c, const float* q, const void* kc, const void* vc, cons
                      sc_lds, s, q, K, (const int32_t*)nullptr, npos, kv_mul, head_dim, inv_sqrt,
                      npos, att);
   DEC_HIP(hipGetLastError(), "k_attn_scores");
-  hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads), dim3(256), (size_t)npos * 4, s, att, npos,
-                     (const int32_t*)nullptr, npos);
-  DEC_HIP(hipGetLastError(), "k_attn_softmax");
-  hipLaunchKernelGGL(k_attn_values, dim3(head_dim / kValCols, n_heads), dim3(512), 0, s, att, npos,
-                     V, (const int32_t*)nullptr, npos, kv_mul, head_dim, out);
-  DEC_HIP(hipGetLastError(), "k_attn_values");
+  DEC_HIP(sv_launch(att, npos, V, nullptr, npos, npos, n_heads, kv_mul, head_dim, out, s),
+          "k_attn_sv");
+  // the normalised weights, in place of the scores (the same softmax_ref)
+  DEC_HIP(softmax_launch(att, n_heads, npos, s), "k_softmax");
   return QR_OK;
 }
 
@@ -714,14 +932,17 @@ int qr_decoder_create(qr_ctx* c, const qr_model* m, int kv_type, int order, int 
     return set_error(QR_ERR_INVALID, "qr_decoder_create: head_dim %d (a multiple of 32, <= %d)",
                      hd, kHdMax);
   const int qd = nh * hd, kvd = nkv * hd;
-  if (kvd > kRopeKvMax || qd > kNormMax)
-    return set_error(QR_ERR_UNSUPPORTED, "qr_decoder_create: q length %d / kv length %d", qd, kvd);
-  if (m->seq_len > kSoftMaxMax)
+  if (m->seq_len > kAttnMaxPos)
     return set_error(QR_ERR_UNSUPPORTED, "qr_decoder_create: seq_len %d (<= %d)", m->seq_len,
-                     kSoftMaxMax);
+                     kAttnMaxPos);
   const size_t rb = qr_kv_row_bytes(kv_type, kvd);
   if (!rb) return set_error(QR_ERR_INVALID, "qr_decoder_create: kv_type %d", kv_type);
   if (page <= 0) page = 256;
+  if (page & (page - 1))
+    return set_error(QR_ERR_INVALID, "qr_decoder_create: page %d (a power of two)", page);
+  if (!sv_lds_ok(m->seq_len, page))
+    return set_error(QR_ERR_UNSUPPORTED, "qr_decoder_create: seq_len %d in pages of %d",
+                     m->seq_len, page);
   if (!m->tok_embd || !m->rms_final || !m->wcls)
     return set_error(QR_ERR_INVALID, "qr_decoder_create: null embedding / final norm / wcls");
   const bool tok_known = m->tok_type == QR_T_F32 || m->tok_type == QR_T_Q8_0 ||
@@ -735,12 +956,13 @@ int qr_decoder_create(qr_ctx* c, const qr_model* m, int kv_type, int order, int 
   for (int l = 0; l < m->n_layers; l++)
     if ((rc = check_layer_weights(m, l, order))) return rc;
   const int kv_mul = nh / nkv;
-  const size_t sc_lds = ((size_t)kScTile * (hd + 1) + (size_t)kv_mul * hd) * 4;
+  const size_t sc_lds = ((size_t)kScTile * (hd + 4) + (size_t)kv_mul * hd) * 4;
   if (sc_lds > kDecLdsMax) return set_error(QR_ERR_UNSUPPORTED, "qr_decoder_create: head group too large");
 
   DEC_HIP(hipSetDevice(ctx_device(c)), "hipSetDevice");
   DEC_HIP(lds_opt_in((const void*)k_attn_scores, g_sc_opt), "lds opt-in");
-  DEC_HIP(lds_opt_in((const void*)k_attn_softmax, g_sm_opt), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_Q8_0>, g_sm_opt), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_F32>, g_sm_opt2), "lds opt-in");
   qr_decoder* d = new (std::nothrow) qr_decoder();
   if (!d) return set_error(QR_ERR_NOMEM, "qr_decoder_create: host allocation");
   d->ctx = c;
