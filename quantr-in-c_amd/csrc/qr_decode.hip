@@ -919,6 +919,8 @@ int qr_decoder_create(qr_ctx* c, const qr_model* m, int kv_type, int order, int 
   if (!out) return set_error(QR_ERR_INVALID, "qr_decoder_create: null out");
   *out = nullptr;
   if (!c || !m || !m->layers) return set_error(QR_ERR_INVALID, "qr_decoder_create: null argument");
+  if (ctx_capturing(c))
+    return set_error(QR_ERR_INVALID, "qr_decoder_create: not allowed while the stream is captured");
   if (order < QR_ORDER_SEQ || order > QR_ORDER_AVX512)
     return set_error(QR_ERR_INVALID, "qr_decoder_create: order %d", order);
   if (flags & ~QR_DEC_GRAPH) return set_error(QR_ERR_INVALID, "qr_decoder_create: flags %d", flags);
