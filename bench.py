@@ -155,17 +155,22 @@ def bench_headline(dev, steps, warmup, copies=16):
     return out
 
 
-def bench_sweep(dev, types, warmup, pool_bytes=600 << 20, max_steps=2048):
-    """Every (type, shape, tokens) of the Q8_0 and K-quant GEMV configs.  Each
-    type's weights fill a pool of > 590 MB (copies of its largest matrix); a
-    launch reads n rows at a row-aligned offset, consecutive launches at
-    consecutive offsets, so one replay streams the whole pool once."""
+def bench_sweep(dev, types, warmup, pool_bytes=600 << 20, max_steps=2048, only=None):
+    """Every (type, shape, tokens) of the Q8_0 and K-quant GEMV configs (or
+    only the (n, d) shapes in `only`).  Each type's weights fill a pool of
+    > 590 MB (copies of its largest matrix); a launch reads n rows at a
+    row-aligned offset, consecutive launches at consecutive offsets, so one
+    replay streams the whole pool once."""
     res = {}
     for qtype in types:
         for d in (2048, 5632):
             shapes = [(n, dd) for (n, dd) in TINYLLAMA if dd == d]
             if qtype != Q.TYPE_Q8_0 and d == 2048:
                 shapes.append((32000, 2048))  # the K-quant sweep's lm_head
+            if only is not None:
+                shapes = [sh for sh in shapes if sh in only]
+            if not shapes:
+                continue
             nmax = max(n for n, _ in shapes)
             rb = synth.row_bytes(qtype, d)
             W = synth.weights(100 + qtype + d, nmax, d, qtype)
@@ -503,6 +508,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--sweep-types", default="Q8_0,Q4_K,Q5_K,Q6_K")
+    ap.add_argument("--sweep-shapes", default="",
+                    help="restrict the sweep to these NxD shapes (comma-separated; profiling runs)")
     ap.add_argument("--moe-layers", type=int, default=48)
     ap.add_argument("--moe-t", default="1,16,512",
                     help="token counts of the Qwen3 MoE leg (comma-separated)")
@@ -537,7 +544,11 @@ def main():
     if not args.no_sweep:
         names = {v: k for k, v in TNAME.items()}
         types = [names[t.strip()] for t in args.sweep_types.split(",") if t.strip()]
-        sweep = bench_sweep(dev, types, min(args.warmup, 5))
+        only = None
+        if args.sweep_shapes.strip():
+            only = {tuple(int(v) for v in sh.lower().split("x"))
+                    for sh in args.sweep_shapes.split(",") if sh.strip()}
+        sweep = bench_sweep(dev, types, min(args.warmup, 5), only=only)
 
     moe = moe15 = dec = None
     M = None
