@@ -1,8 +1,8 @@
 """INTEGRATION.md's binding compiles as written.
 
 The C blocks of INTEGRATION.md are compiled, in order, against the reference's
-own include/ headers and include/qr_dropin.h, each in the reference source
-file it belongs to (src/kernels.c, src/runtime.c, src/model.c), with
+own include/ headers and include/qr_dropin.h / qr_hip.h, each in the reference
+source file it belongs to (src/kernels.c, src/runtime.c, src/model.c), with
 -std=c99 -Wall -Werror, both with and without -DQR_GPU; every qr_* symbol the
 objects use must be exported by libqr_hip.so.  The preludes stand for what
 those reference files already define above the edited lines (their static
@@ -54,7 +54,7 @@ static size_t ggml_type_row_size(uint32_t type, size_t ne0) {
 """,
 }
 # INTEGRATION.md's C blocks, in order, and the reference file each edits
-FILES = ["kernels", "runtime", "runtime", "model"]
+FILES = ["kernels", "runtime", "runtime", "model", "runtime"]
 
 
 def _blocks():
