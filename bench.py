@@ -18,6 +18,9 @@ Extra keys of the same line:
                top-8, ffn 768, gate/up Q4_K, down Q6_K, Zipf(1.1) expert skew)
                in tokens/s at T = 1, 16 and 512, rotating over 48 layer copies
                (router included) like a 48-layer decode;
+               (`paths`: the layer at T = 2 ... 64 with each expert product forced, the
+               grouped GEMV against the int8 MFMA products: the crossover the default
+               path choice follows);
   moe_qwen15   the Qwen1.5-MoE-A2.7B-shaped layer (60 experts top-4, ffn 1408,
                shared expert ffn 5632 with a sigmoid gate) at T = 1 and 64;
   decode_qwen3 the whole single-token decode step of a Qwen3-30B-A3B-shaped
@@ -48,6 +51,13 @@ import quantr_amd as Q  # noqa: E402
 from quantr_amd import synth  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
+# fp32 VALU lane operations per second without packed instructions: 256 CUs x 4 SIMDs x 16
+# lanes x 2.4 GHz (the published 157.3 TFLOP/s counts packed FMAs as 4 flops per lane)
+VALU_PEAK_OPS = 256 * 64 * 2.4e9
+# fp32 operations per (output row, token, 32-element unit) that the reference's dot rounds
+# one by one: (sc * isum - m * bsum) * bd added on (Q4_K / Q5_K), sc * isum * bd added on
+# (Q6_K), isum * (da * db) added on (Q8_0), each after the int -> float conversion
+TERM_OPS = {Q.TYPE_Q4_K: 6, Q.TYPE_Q5_K: 6, Q.TYPE_Q6_K: 4, Q.TYPE_Q8_0: 4}
 METRIC = "Q4_K GEMV weight GB/s (% HBM peak); MoE layer tokens/s at 30B-A3B shape"
 TNAME = {Q.TYPE_Q8_0: "Q8_0", Q.TYPE_Q4_K: "Q4_K", Q.TYPE_Q5_K: "Q5_K", Q.TYPE_Q6_K: "Q6_K"}
 TINYLLAMA = [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632)]
@@ -239,7 +249,8 @@ def build_qwen3(dev, layers):
                              b + int(offs[3]), Q.TYPE_Q4_K, Q.TYPE_Q4_K, Q.TYPE_Q6_K))
     expert_bytes = (per_layer - router.nbytes) // E
     return dict(layers=Ls, slab=slab, u=u, parts=parts, expert_bytes=expert_bytes,
-                per_layer=per_layer, shape=QWEN3, shared_bytes=0)
+                per_layer=per_layer, shape=QWEN3, shared_bytes=0,
+                types=(Q.TYPE_Q4_K, Q.TYPE_Q6_K, None))
 
 
 def build_qwen15(dev, layers):
@@ -273,7 +284,8 @@ def build_qwen15(dev, layers):
     expert_bytes = sum(p.nbytes for p in parts[1:4]) // E
     shared_bytes = sum(p.nbytes for p in parts[4:])
     return dict(layers=Ls, slab=slab, u=None, parts=parts, expert_bytes=expert_bytes,
-                per_layer=per_layer, shape=QWEN15, shared_bytes=shared_bytes)
+                per_layer=per_layer, shape=QWEN15, shared_bytes=shared_bytes,
+                types=(Q.TYPE_Q4_K, Q.TYPE_Q8_0, Q.TYPE_Q4_K))
 
 
 def moe_alg_bytes(M, T, touched):
@@ -281,6 +293,18 @@ def moe_alg_bytes(M, T, touched):
     sh = M["shape"]
     return 4 * sh["E"] * sh["dim"] + touched * M["expert_bytes"] + M["shared_bytes"] + \
         2 * 4 * T * sh["dim"]
+
+
+def moe_term_ops(M, T):
+    """fp32 VALU operations the layer's expert products must perform at T tokens
+    (one rounded operation per TERM_OPS step, per output row, token slot and unit)."""
+    sh = M["shape"]
+    ut, dt, st = M["types"]
+    dim, hid, K = sh["dim"], sh["hidden"], sh["K"]
+    ops = T * K * (2 * hid * (dim // 32) * TERM_OPS[ut] + dim * (hid // 32) * TERM_OPS[dt])
+    if st is not None:
+        ops += T * (2 * sh["sh"] * (dim // 32) + dim * (sh["sh"] // 32)) * TERM_OPS[st]
+    return ops
 
 
 def bench_moe(dev, M, T, steps, warmup, order, nbatches=8, seed=7000):
@@ -312,10 +336,15 @@ def bench_moe(dev, M, T, steps, warmup, order, nbatches=8, seed=7000):
     dev.sync()
     ms = graph_ms(dev, one, steps)
     s = ms / 1e3
+    ops = moe_term_ops(M, T)
+    hbm_us = step_bytes / (HBM_PEAK_GBPS * 1e9) * 1e6
+    valu_us = ops / VALU_PEAK_OPS * 1e6
     return dict(T=T, ms_per_step=ms, tokens_per_s=T / s, touched_experts=touched,
                 max_tokens_per_expert=int(counts.max()), alg_bytes=int(step_bytes),
                 achieved_gbps=step_bytes / s / 1e9,
-                roofline_frac=step_bytes / s / 1e9 / HBM_PEAK_GBPS)
+                roofline_frac=step_bytes / s / 1e9 / HBM_PEAK_GBPS,
+                term_ops=int(ops), hbm_bound_us=round(hbm_us, 2), valu_bound_us=round(valu_us, 2),
+                bound_frac=round(max(hbm_us, valu_us) / (ms * 1e3), 4))
 
 
 # ---------------------------------------------------------------------------
@@ -517,6 +546,8 @@ def main():
                     help="layers timed per token count (0: the defaults, 100 / 100 / 20)")
     ap.add_argument("--no-qwen15", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-crossover", action="store_true",
+                    help="skip the grouped-GEMV / MFMA comparison of the Qwen3 MoE leg")
     ap.add_argument("--decode-steps", type=int, default=32)
     ap.add_argument("--no-gemv", action="store_true",
                     help="skip the GEMV headline (profiling runs of other legs; value is null)")
@@ -561,9 +592,23 @@ def main():
             r = bench_moe(dev, M, T, steps, 3, Q.ORDER_AVX2)
             moe["T%d" % T] = r
             log("bench: MoE Qwen3 T=%d: %.1f us/layer, %.0f tokens/s, %.1f experts touched, "
-                "%.0f GB/s (%.1f%% of HBM peak)" % (T, r["ms_per_step"] * 1e3, r["tokens_per_s"],
-                                                   r["touched_experts"], r["achieved_gbps"],
-                                                   100 * r["roofline_frac"]))
+                "%.0f GB/s (%.1f%% of HBM peak); bounds HBM %.1f us, VALU %.1f us -> frac %.3f"
+                % (T, r["ms_per_step"] * 1e3, r["tokens_per_s"], r["touched_experts"],
+                   r["achieved_gbps"], 100 * r["roofline_frac"], r["hbm_bound_us"],
+                   r["valu_bound_us"], r["bound_frac"]))
+        if not args.no_crossover:
+            paths = {}
+            for T in (2, 4, 8, 16, 32, 64):
+                row = {}
+                for name, path in (("gemv", Q.MOE_PATH_GEMV), ("mfma", Q.MOE_PATH_MFMA)):
+                    dev.set_moe_path(path)
+                    r = bench_moe(dev, M, T, 30, 3, Q.ORDER_AVX2)
+                    row[name + "_us"] = round(r["ms_per_step"] * 1e3, 2)
+                dev.set_moe_path(Q.MOE_PATH_AUTO)
+                paths["T%d" % T] = row
+                log("bench: MoE Qwen3 T=%d expert products: grouped GEMV %.1f us, int8 MFMA %.1f us"
+                    % (T, row["gemv_us"], row["mfma_us"]))
+            moe["paths"] = paths
         if not args.no_decode:
             dec = bench_decode(dev, M, args.decode_steps, 3, Q.ORDER_AVX2)
             log("bench: decode step Qwen3-30B-A3B shape, %d layers at ~%.0f positions: %.3f ms, "

@@ -73,6 +73,16 @@ int qr_ctx_create(int device, qr_ctx** out);
 int qr_ctx_destroy(qr_ctx* ctx);
 /* Use an existing hipStream_t (NULL restores the context's own stream). */
 int qr_ctx_set_stream(qr_ctx* ctx, void* hip_stream);
+
+/* The expert products of this context's MoE calls with T > 1 tokens (no
+ * reference counterpart: the reference has one CPU loop).  AUTO and MFMA take
+ * the int8 MFMA products where both expert types have an MFMA form (measured
+ * faster than the grouped GEMV at every T >= 2 at the Qwen3-30B-A3B shape);
+ * GEMV forces the grouped GEMV.  Results are identical on every path. */
+#define QR_MOE_PATH_AUTO 0
+#define QR_MOE_PATH_GEMV 1
+#define QR_MOE_PATH_MFMA 2
+int qr_ctx_set_moe_path(qr_ctx* ctx, int path);
 void* qr_ctx_get_stream(qr_ctx* ctx);
 int qr_sync(qr_ctx* ctx);
 int qr_malloc(qr_ctx* ctx, size_t bytes, void** dptr);

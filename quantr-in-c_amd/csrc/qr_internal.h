@@ -69,8 +69,9 @@ hipError_t moe_route_launch(const qr_moe_layer* L, const float* xb, int T, int o
 hipError_t moe_dispatch_launch(const int32_t* idx, int T, int K, int E, int tile, int32_t* counts,
                                int32_t* offsets, int32_t* tiles, int32_t* perm, int32_t* inv,
                                hipStream_t st);
+// path: QR_MOE_PATH_* (include/qr_hip.h); AUTO picks by the pairs per expert.
 hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, int T, int order,
-                              const MoeScratch& s, hipStream_t st);
+                              const MoeScratch& s, hipStream_t st, int path = QR_MOE_PATH_AUTO);
 hipError_t softmax_launch(float* x, int rows, int n, hipStream_t st);
 
 // qr_moe_t1.hip

@@ -64,6 +64,8 @@ struct qr_ctx {
   // Device address of this GPU's copy of the static `scratch` array
   // (qr_moe_forward_noalloc).
   void* static_scratch = nullptr;
+  // QR_MOE_PATH_* for this context's MoE calls with T > 1.
+  int moe_path = QR_MOE_PATH_AUTO;
 };
 
 namespace {
@@ -306,6 +308,14 @@ int qr_ctx_destroy(qr_ctx* c) {
   if (c->ev1) (void)hipEventDestroy(c->ev1);
   if (c->own) (void)hipStreamDestroy(c->own);
   delete c;
+  return QR_OK;
+}
+
+int qr_ctx_set_moe_path(qr_ctx* c, int path) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_ctx_set_moe_path: null ctx");
+  if (path < QR_MOE_PATH_AUTO || path > QR_MOE_PATH_MFMA)
+    return fail(QR_ERR_INVALID, "qr_ctx_set_moe_path: path %d", path);
+  c->moe_path = path;
   return QR_OK;
 }
 
@@ -668,7 +678,7 @@ int qr_moe_forward(qr_ctx* c, const qr_moe_layer* L, float* x, const float* xb, 
   if (rc) return rc;
   qr::MoeScratch s;
   qr::moe_scratch_carve(base, L, T, &s);
-  QR_HIP(qr::moe_forward_launch(L, x, xb, T, order, s, c->stream), "moe_forward");
+  QR_HIP(qr::moe_forward_launch(L, x, xb, T, order, s, c->stream, c->moe_path), "moe_forward");
   const size_t kb = (size_t)T * L->n_used;
   if (idx_out) QR_HIP(hipMemcpyAsync(idx_out, s.idx, kb * 4, hipMemcpyDeviceToDevice, c->stream), "copy idx");
   if (w_out) QR_HIP(hipMemcpyAsync(w_out, s.wts, kb * 4, hipMemcpyDeviceToDevice, c->stream), "copy wts");
@@ -698,7 +708,7 @@ int qr_moe_forward_noalloc(qr_ctx* c, const qr_moe_layer* L, float* x, const flo
   if (!c->static_scratch) return fail(QR_ERR_HIP, "qr_moe_forward_noalloc: no scratch address");
   qr::MoeScratch s;
   qr::moe_scratch_carve(c->static_scratch, L, T, &s);
-  QR_HIP(qr::moe_forward_launch(L, x, xb, T, order, s, c->stream), "moe_forward");
+  QR_HIP(qr::moe_forward_launch(L, x, xb, T, order, s, c->stream, c->moe_path), "moe_forward");
   const size_t kb = (size_t)T * L->n_used;
   if (idx_out) QR_HIP(hipMemcpyAsync(idx_out, s.idx, kb * 4, hipMemcpyDeviceToDevice, c->stream), "copy idx");
   if (w_out) QR_HIP(hipMemcpyAsync(w_out, s.wts, kb * 4, hipMemcpyDeviceToDevice, c->stream), "copy wts");

@@ -58,6 +58,7 @@ class Model(C.Structure):
 
 
 KV_F32, KV_Q8_0 = 0, 2
+MOE_PATH_AUTO, MOE_PATH_GEMV, MOE_PATH_MFMA = 0, 1, 2
 DEC_GRAPH = 1
 
 _SIGS = {
@@ -68,6 +69,7 @@ _SIGS = {
     "qr_ctx_destroy": (C.c_int, [_vp]),
     "qr_ctx_set_stream": (C.c_int, [_vp, _vp]),
     "qr_ctx_get_stream": (_vp, [_vp]),
+    "qr_ctx_set_moe_path": (C.c_int, [_vp, C.c_int]),
     "qr_sync": (C.c_int, [_vp]),
     "qr_malloc": (C.c_int, [_vp, C.c_size_t, C.POINTER(_vp)]),
     "qr_free": (C.c_int, [_vp, _vp]),
@@ -198,6 +200,10 @@ class Device:
         if self.ctx is not None:
             self.lib.qr_ctx_destroy(_vp(self.ctx))
             self.ctx = None
+
+    def set_moe_path(self, path):
+        """QR_MOE_PATH_*: 0 auto, 1 grouped GEMV, 2 int8 MFMA (T > 1)."""
+        self._check(self.lib.qr_ctx_set_moe_path(self.ctx, path), "qr_ctx_set_moe_path")
 
     # ---- memory
     def alloc(self, nbytes):

@@ -124,6 +124,22 @@ def test_moe_qwen3_shape(dev, oracle, T, order):
     check_moe(dev, oracle, layer, x, xb, order, "qwen3 T=%d" % T)
 
 
+@pytest.mark.parametrize("path", [Q.MOE_PATH_GEMV, Q.MOE_PATH_MFMA], ids=["gemv", "mfma"])
+@pytest.mark.parametrize("T", [2, 5, 16, 64])
+def test_moe_qwen3_forced_path(dev, oracle, T, path):
+    """Either expert product at any token count (qr_ctx_set_moe_path): the
+    grouped GEMV at counts where the default takes the MFMA products and the
+    reverse; bit-exact either way."""
+    layer, u = qwen3_layer(dev)
+    xb = synth.zipf_tokens(3300 + T, T, 2048, u)
+    x = synth.normal(3400 + T, (T, 2048))
+    dev.set_moe_path(path)
+    try:
+        check_moe(dev, oracle, layer, x, xb, ORDER_AVX2, "qwen3 T=%d path %d" % (T, path))
+    finally:
+        dev.set_moe_path(Q.MOE_PATH_AUTO)
+
+
 def test_moe_qwen3_t512_routing_and_output(dev, oracle):
     """T = 512: routing and dispatch bit-exact; output bit-exact on every token."""
     layer, u = qwen3_layer(dev)
