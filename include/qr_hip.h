@@ -330,6 +330,67 @@ int qr_decoder_kv_rows(const qr_decoder* dec, int layer, int pos, const void** k
  * the last layer.  Enqueued on the context's stream. */
 int qr_decoder_forward(qr_decoder* dec, int token, int pos, float* logits, float* x_out);
 
+/* ---- GGUF files (src/gguf.c, src/model.c:253-449) ----------------------- */
+
+/* A parsed GGUF container.  qr_gguf_parse reads a buffer the caller keeps
+ * alive; qr_gguf_open maps a file read-only (load_transformer's mmap,
+ * src/model.c:451-470).  Both accept and refuse exactly what
+ * gguf_init_from_buffer (src/gguf.c:50-177) does: magic "GGUF", at most 65536
+ * key/values and tensors, strings of at most 1 MiB, arrays of at most
+ * 1,000,000 entries, at most 4 dimensions, known key/value types,
+ * general.alignment (u32 or u64; 0 or absent: 32), every tensor starting
+ * inside the buffer.  Host-only: no device is needed. */
+typedef struct qr_gguf qr_gguf;
+int qr_gguf_parse(const void* data, size_t size, qr_gguf** out);
+int qr_gguf_open(const char* path, qr_gguf** out);
+int qr_gguf_close(qr_gguf* g);
+int qr_gguf_info(const qr_gguf* g, uint32_t* version, uint64_t* n_tensors, uint64_t* n_kv,
+                 uint64_t* alignment, uint64_t* data_offset);
+/* Tensor i: name, GGML type, dimensions (ne[0] innermost; ne has 4 entries)
+ * and its data in the buffer. */
+int qr_gguf_tensor(const qr_gguf* g, uint64_t i, const char** name, uint32_t* type,
+                   uint32_t* n_dims, uint64_t* ne, const void** data);
+int64_t qr_gguf_find(const qr_gguf* g, const char* name); /* index, or -1 */
+/* gguf_get_val_u32 / _f32 / _str (src/gguf.c:211-269): the first key of that
+ * name holding that type, else the default (NULL for strings). */
+uint32_t qr_gguf_get_u32(const qr_gguf* g, const char* key, uint32_t def);
+float qr_gguf_get_f32(const qr_gguf* g, const char* key, float def);
+const char* qr_gguf_get_str(const qr_gguf* g, const char* key);
+int64_t qr_gguf_get_arr_len(const qr_gguf* g, const char* key); /* -1 if absent */
+
+/* The decoder model of a MoE GGUF as HOST pointers into the buffer, mapped as
+ * load_gguf_transformer does (src/model.c:253-449): {arch}.embedding_length,
+ * block_count, attention.head_count(_kv), expert_count, expert_used_count,
+ * expert_feed_forward_length, rope.freq_base (default 1e6); token_embd,
+ * output_norm, output (else tied to token_embd), blk.N.attn_norm / ffn_norm /
+ * attn_q / attn_k / attn_v / attn_output / ffn_gate_inp, and the experts with
+ * expert_w1 = ffn_up_exps (the SiLU slot), expert_w3 = ffn_gate_exps,
+ * expert_w2 = ffn_down_exps as one 3-D tensor each or per-expert tensors
+ * (then the pointers are expert 0's; see qr_gguf_expert_host).  Beyond the
+ * reference: head_dim is attention.key_length when the file states it
+ * (else dim / n_heads, as there); vocab is the tokenizer's token count, else
+ * the embedding's rows; every tensor's shape and type is checked, all
+ * layers on every call.  Returns n_layers; fills `layers` only when
+ * max_layers >= n_layers. */
+int qr_gguf_model_host(const qr_gguf* g, int seq_len, qr_model* model, qr_layer* layers,
+                       int max_layers);
+/* Expert e of layer `layer`: host pointers to its up, down and gate matrices. */
+int qr_gguf_expert_host(const qr_gguf* g, int layer, int e, const void** up, const void** down,
+                        const void** gate);
+
+/* The same model copied to the device: every tensor the decoder reads in one
+ * allocation (each tensor 256-byte aligned; per-expert tensors gathered
+ * into one range per kind, expert e at e * slice, as a 3-D tensor is laid
+ * out; a tied output shares the embedding's copy).  Returns a qr_model of
+ * device pointers for qr_decoder_create.  The copy owns its memory: the
+ * qr_gguf may be closed after loading, two loads are two copies, and
+ * qr_gguf_model_free releases one of them (after the context stream has
+ * drained; no decoder built on it may be used afterwards). */
+typedef struct qr_gguf_model qr_gguf_model;
+int qr_gguf_load(qr_ctx* ctx, const qr_gguf* g, int seq_len, qr_gguf_model** out);
+const qr_model* qr_gguf_model_get(const qr_gguf_model* m);
+int qr_gguf_model_free(qr_gguf_model* m);
+
 /* ---- weight registry (host pointer -> device copy) ---------------------- */
 
 /* Upload `bytes` from host memory once and return the device copy; later

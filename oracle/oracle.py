@@ -411,6 +411,15 @@ class RefLib:
         L.refdrv_gemv_bench.restype = C.c_int
         L.refdrv_gemv_bench.argtypes = [_f32p, C.c_void_p, C.c_int, C.c_uint32, C.c_int, C.c_int,
                                         C.c_int, C.c_int, C.c_int, _f32p, C.c_void_p]
+        L.refdrv_gguf_parse.restype = C.c_int
+        L.refdrv_gguf_parse.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_int, C.c_void_p,
+                                        C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.refdrv_gguf_vals.restype = C.c_int
+        L.refdrv_gguf_vals.argtypes = [C.c_void_p, C.c_size_t, C.c_char_p, C.c_uint32, C.c_float,
+                                       C.c_void_p, C.c_void_p, C.c_char_p, C.c_int]
+        L.refdrv_load_gguf.restype = C.c_int
+        L.refdrv_load_gguf.argtypes = [C.c_char_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.c_void_p]
         L.refdrv_forward.restype = C.c_int
         L.refdrv_forward.argtypes = [C.c_int] * 7 + [C.c_float, C.c_int, C.c_int, C.c_void_p,
                                                      C.c_uint32, C.c_size_t] + \
@@ -506,6 +515,53 @@ class RefLib:
         if rc != 0:
             raise RuntimeError("refdrv_gemv_bench failed: %d" % rc)
         return times
+
+    def gguf_parse(self, data, max_t=4096):
+        """gguf_init_from_buffer on data: None when refused, else (hdr dict,
+        list of tensor dicts with the data offset from the buffer start)."""
+        buf = C.create_string_buffer(bytes(data), len(data))
+        hdr = np.zeros(5, np.uint64)
+        names = C.create_string_buffer(96 * max_t)
+        types = np.zeros(max_t, np.uint32)
+        nd = np.zeros(max_t, np.uint32)
+        ne = np.zeros(4 * max_t, np.uint64)
+        off = np.zeros(max_t, np.uint64)
+        rc = self.lib.refdrv_gguf_parse(C.cast(buf, C.c_void_p), len(data), _ptr(hdr), max_t, names,
+                                        _ptr(types), _ptr(nd), _ptr(ne), _ptr(off))
+        if rc != 0:
+            return None
+        h = dict(version=int(hdr[0]), n_tensors=int(hdr[1]), n_kv=int(hdr[2]),
+                 alignment=int(hdr[3]), data_offset=int(hdr[4]))
+        ts = []
+        for i in range(min(h["n_tensors"], max_t)):
+            nm = names.raw[96 * i:96 * (i + 1)].split(b"\0")[0].decode()
+            ts.append(dict(name=nm, type=int(types[i]), n_dims=int(nd[i]),
+                           ne=[int(v) for v in ne[4 * i:4 * i + 4]], offset=int(off[i])))
+        return h, ts
+
+    def gguf_vals(self, data, key, def_u32=7, def_f32=-1.5):
+        buf = C.create_string_buffer(bytes(data), len(data))
+        u = np.zeros(1, np.uint32)
+        f = np.zeros(1, np.float32)
+        out = C.create_string_buffer(512)
+        rc = self.lib.refdrv_gguf_vals(C.cast(buf, C.c_void_p), len(data), key.encode(), def_u32,
+                                       def_f32, _ptr(u), _ptr(f), out, 512)
+        if rc != 0:
+            return None
+        return int(u[0]), float(f[0]), out.value.decode()
+
+    def load_gguf(self, path, n_layers, n_experts):
+        """load_transformer of a .gguf path: (cfg, rope_base, offsets, types,
+        token_embd_row_bytes) as refdrv_load_gguf lays them out."""
+        cfg = np.zeros(9, np.int32)
+        rope = np.zeros(1, np.float32)
+        off = np.zeros(3 + 7 * n_layers + 3 * n_layers * n_experts, np.int64)
+        types = np.zeros(2 + 7 * n_layers, np.uint32)
+        rb = np.zeros(1, np.uint64)
+        n = self.lib.refdrv_load_gguf(path.encode(), _ptr(cfg), _ptr(rope), _ptr(off), _ptr(types),
+                                      _ptr(rb))
+        assert n == len(off), (n, len(off))
+        return cfg, float(rope[0]), off, types, int(rb[0])
 
     def forward(self, m, tokens, backend, threads=1, kv_type=0):
         """The reference's forward_runtime on decode model m (tests/golden/inputs.py)

@@ -460,3 +460,113 @@ int refdrv_forward(int dim, int hidden, int n_layers, int n_heads, int n_kv_head
     free(tq);
     return 0;
 }
+
+/* ---- GGUF (src/gguf.c, src/model.c:253-449) ------------------------------ */
+#include "gguf.h"
+
+/* gguf_init_from_buffer on the caller's bytes.  hdr receives version,
+ * tensor_count, kv_count, alignment, data_offset; for the first max_t tensors:
+ * the name (NUL-terminated, 96 bytes per entry, truncated), type, n_dims, ne[4]
+ * and the data pointer's offset from buf.  Returns 0, or -1 when the
+ * reference's parser refuses the buffer. */
+int refdrv_gguf_parse(void* buf, size_t size, uint64_t* hdr, int max_t, char* names,
+                      uint32_t* types, uint32_t* ndims, uint64_t* ne, uint64_t* data_off) {
+    gguf_context* g = gguf_init_from_buffer(buf, size);
+    uint64_t i;
+    if (!g) return -1;
+    hdr[0] = g->version;
+    hdr[1] = g->tensor_count;
+    hdr[2] = g->kv_count;
+    hdr[3] = g->alignment;
+    hdr[4] = g->data_offset;
+    for (i = 0; i < g->tensor_count && (int)i < max_t; i++) {
+        int j;
+        strncpy(names + 96 * i, g->tensors[i].name, 95);
+        names[96 * i + 95] = '\0';
+        types[i] = g->tensors[i].type;
+        ndims[i] = g->tensors[i].n_dims;
+        for (j = 0; j < 4; j++) ne[4 * i + j] = g->tensors[i].ne[j];
+        data_off[i] = (uint64_t)((const char*)g->tensors[i].data - (const char*)buf);
+    }
+    gguf_free(g);
+    return 0;
+}
+
+/* gguf_get_val_u32 / _f32 / _str of one key (the string copied into out,
+ * cap bytes; "" when absent).  Returns -1 when the buffer does not parse. */
+int refdrv_gguf_vals(void* buf, size_t size, const char* key, uint32_t def_u32, float def_f32,
+                     uint32_t* u32, float* f32, char* out, int cap) {
+    gguf_context* g = gguf_init_from_buffer(buf, size);
+    const char* s;
+    if (!g) return -1;
+    *u32 = gguf_get_val_u32(g, key, def_u32);
+    *f32 = gguf_get_val_f32(g, key, def_f32);
+    s = gguf_get_val_str(g, key);
+    out[0] = '\0';
+    if (s && cap > 0) {
+        strncpy(out, s, (size_t)cap - 1);
+        out[cap - 1] = '\0';
+    }
+    gguf_free(g);
+    return 0;
+}
+
+/* load_transformer (src/model.c:451-481) of a .gguf file: cfg receives dim,
+ * hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len,
+ * expert_count, expert_used_count; rope the freq base.  off receives the file
+ * offset of every weight pointer the loader set (-1 when NULL), in this order:
+ * token_embedding_table, rms_final_weight, wcls, then per layer rms_att, rms_ffn,
+ * wq, wk, wv, wo, ffn_gate_inp, then per layer and expert w1, w2, w3.
+ * types: token_embd_type, wcls_type, then per layer wq, wk, wv, wo, exp_w1,
+ * exp_w2, exp_w3 types; row_bytes: token_embd_row_bytes.  The file must be a
+ * valid MoE GGUF (the reference exits otherwise). */
+int refdrv_load_gguf(const char* path, int* cfg, float* rope, int64_t* off, uint32_t* types,
+                     uint64_t* row_bytes) {
+    Transformer t;
+    int l, e, n = 0, m = 0;
+    const char* base;
+    load_transformer(&t, path);
+    base = (const char*)t.mapped_data;
+#define OFF(p) ((p) ? (int64_t)((const char*)(p) - base) : (int64_t)-1)
+    cfg[0] = t.config.dim;
+    cfg[1] = t.config.hidden_dim;
+    cfg[2] = t.config.n_layers;
+    cfg[3] = t.config.n_heads;
+    cfg[4] = t.config.n_kv_heads;
+    cfg[5] = t.config.vocab_size;
+    cfg[6] = t.config.seq_len;
+    cfg[7] = t.config.expert_count;
+    cfg[8] = t.config.expert_used_count;
+    *rope = t.config.rope_freq_base;
+    off[n++] = OFF(t.weights.token_embedding_table);
+    off[n++] = OFF(t.weights.rms_final_weight);
+    off[n++] = OFF(t.weights.wcls);
+    types[m++] = t.weights.token_embd_type;
+    types[m++] = t.weights.wcls_type;
+    *row_bytes = t.weights.token_embd_row_bytes;
+    for (l = 0; l < t.config.n_layers; l++) {
+        off[n++] = OFF(t.weights.rms_att_weight[l]);
+        off[n++] = OFF(t.weights.rms_ffn_weight[l]);
+        off[n++] = OFF(t.weights.wq[l]);
+        off[n++] = OFF(t.weights.wk[l]);
+        off[n++] = OFF(t.weights.wv[l]);
+        off[n++] = OFF(t.weights.wo[l]);
+        off[n++] = t.config.expert_count > 0 ? OFF(t.weights.ffn_gate_inp[l]) : -1;
+        types[m++] = t.weights.wq_type[l];
+        types[m++] = t.weights.wk_type[l];
+        types[m++] = t.weights.wv_type[l];
+        types[m++] = t.weights.wo_type[l];
+        types[m++] = t.weights.exp_w1_type[l];
+        types[m++] = t.weights.exp_w2_type[l];
+        types[m++] = t.weights.exp_w3_type[l];
+    }
+    for (l = 0; l < t.config.n_layers; l++)
+        for (e = 0; e < t.config.expert_count; e++) {
+            off[n++] = OFF(t.weights.expert_w1[l][e]);
+            off[n++] = OFF(t.weights.expert_w2[l][e]);
+            off[n++] = OFF(t.weights.expert_w3[l][e]);
+        }
+#undef OFF
+    free_transformer(&t);
+    return n;
+}

@@ -227,6 +227,10 @@ __global__ void k_test_expf(const float* __restrict__ x, float* __restrict__ y, 
 }  // namespace
 
 // Context internals for the other translation units (qr_internal.h).
+// The host C layer's (host/qr_gguf.c) way to set qr_last_error(); local to
+// the library (not a qr_* symbol, so the export map keeps it hidden).
+extern "C" int qrint_set_error(int code, const char* msg) { return fail(code, "%s", msg); }
+
 namespace qr {
 int set_error(int code, const char* fmt, ...) {
   va_list ap;

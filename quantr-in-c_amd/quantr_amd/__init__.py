@@ -118,6 +118,25 @@ _SIGS = {
     "qr_decoder_kv_write": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "qr_decoder_kv_rows": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(_vp), C.POINTER(_vp)]),
     "qr_decoder_forward": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp]),
+    "qr_gguf_parse": (C.c_int, [_vp, C.c_size_t, C.POINTER(_vp)]),
+    "qr_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
+    "qr_gguf_close": (C.c_int, [_vp]),
+    "qr_gguf_info": (C.c_int, [_vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
+                               C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                               C.POINTER(C.c_uint64)]),
+    "qr_gguf_tensor": (C.c_int, [_vp, C.c_uint64, C.POINTER(C.c_char_p), C.POINTER(C.c_uint32),
+                                 C.POINTER(C.c_uint32), C.POINTER(C.c_uint64), C.POINTER(_vp)]),
+    "qr_gguf_find": (C.c_int64, [_vp, C.c_char_p]),
+    "qr_gguf_get_u32": (C.c_uint32, [_vp, C.c_char_p, C.c_uint32]),
+    "qr_gguf_get_f32": (C.c_float, [_vp, C.c_char_p, C.c_float]),
+    "qr_gguf_get_str": (C.c_char_p, [_vp, C.c_char_p]),
+    "qr_gguf_get_arr_len": (C.c_int64, [_vp, C.c_char_p]),
+    "qr_gguf_model_host": (C.c_int, [_vp, C.c_int, C.POINTER(Model), C.POINTER(Layer), C.c_int]),
+    "qr_gguf_expert_host": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(_vp), C.POINTER(_vp),
+                                      C.POINTER(_vp)]),
+    "qr_gguf_load": (C.c_int, [_vp, _vp, C.c_int, C.POINTER(_vp)]),
+    "qr_gguf_model_get": (C.POINTER(Model), [_vp]),
+    "qr_gguf_model_free": (C.c_int, [_vp]),
     # drop-ins (include/qr_dropin.h)
     "qr_dropin_init": (C.c_int, [C.c_int, C.c_int]),
     "qr_dropin_shutdown": (None, []),
@@ -367,6 +386,130 @@ class Decoder:
     def close(self):
         if self.h is not None:
             self.dev.lib.qr_decoder_destroy(_vp(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Gguf:
+    """A parsed GGUF container (host only).  From bytes (kept alive here) or a
+    file path (mapped read-only by the library)."""
+
+    def __init__(self, data=None, path=None, lib=None):
+        self.lib = lib or load()
+        h = _vp()
+        if isinstance(data, (str, os.PathLike)):
+            data, path = None, os.fspath(data)
+        if path is not None:
+            rc = self.lib.qr_gguf_open(path.encode(), C.byref(h))
+            self._buf = None
+        else:
+            self._buf = C.create_string_buffer(bytes(data), len(data))
+            rc = self.lib.qr_gguf_parse(C.cast(self._buf, _vp), len(data), C.byref(h))
+        if rc != 0:
+            raise QrError("GGUF parse failed (%d): %s" % (
+                rc, self.lib.qr_last_error().decode(errors="replace")))
+        self.h = h.value
+
+    @property
+    def base(self):
+        """Address of the parsed bytes (buffer form only)."""
+        return C.addressof(self._buf) if self._buf is not None else None
+
+    def info(self):
+        v, nt, nk, al, do = C.c_uint32(), C.c_uint64(), C.c_uint64(), C.c_uint64(), C.c_uint64()
+        self.lib.qr_gguf_info(_vp(self.h), C.byref(v), C.byref(nt), C.byref(nk), C.byref(al),
+                              C.byref(do))
+        return dict(version=v.value, n_tensors=nt.value, n_kv=nk.value, alignment=al.value,
+                    data_offset=do.value)
+
+    def tensor(self, i):
+        name, typ, nd = C.c_char_p(), C.c_uint32(), C.c_uint32()
+        ne, data = (C.c_uint64 * 4)(), _vp()
+        rc = self.lib.qr_gguf_tensor(_vp(self.h), i, C.byref(name), C.byref(typ), C.byref(nd), ne,
+                                     C.byref(data))
+        if rc != 0:
+            raise QrError("qr_gguf_tensor(%d) failed" % i)
+        return dict(name=name.value.decode(), type=typ.value, n_dims=nd.value, ne=list(ne),
+                    data=data.value)
+
+    def tensors(self):
+        return [self.tensor(i) for i in range(self.info()["n_tensors"])]
+
+    def u32(self, key, default=0):
+        return self.lib.qr_gguf_get_u32(_vp(self.h), key.encode(), default)
+
+    def f32(self, key, default=0.0):
+        return self.lib.qr_gguf_get_f32(_vp(self.h), key.encode(), default)
+
+    def str(self, key):
+        v = self.lib.qr_gguf_get_str(_vp(self.h), key.encode())
+        return None if v is None else v.decode()
+
+    def arr_len(self, key):
+        return self.lib.qr_gguf_get_arr_len(_vp(self.h), key.encode())
+
+    def model_host(self, seq_len=0):
+        """(Model, Layer array) of host pointers into the buffer."""
+        m = Model()
+        n = self.lib.qr_gguf_model_host(_vp(self.h), seq_len, C.byref(m), None, 0)
+        if n <= 0:
+            raise QrError("qr_gguf_model_host failed (%d): %s" % (
+                n, self.lib.qr_last_error().decode(errors="replace")))
+        layers = (Layer * n)()
+        n2 = self.lib.qr_gguf_model_host(_vp(self.h), seq_len, C.byref(m), layers, n)
+        if n2 != n:
+            raise QrError("qr_gguf_model_host failed (%d)" % n2)
+        return m, layers
+
+    def expert_host(self, layer, e):
+        up, down, gate = _vp(), _vp(), _vp()
+        rc = self.lib.qr_gguf_expert_host(_vp(self.h), layer, e, C.byref(up), C.byref(down),
+                                          C.byref(gate))
+        if rc != 0:
+            raise QrError("qr_gguf_expert_host failed")
+        return up.value, down.value, gate.value
+
+    def load(self, dev, seq_len):
+        """A GgufModel: the model uploaded to dev's GPU."""
+        return GgufModel(dev, self, seq_len)
+
+    def close(self):
+        if self.h is not None:
+            self.lib.qr_gguf_close(_vp(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class GgufModel:
+    """qr_gguf_load: a qr_model of device pointers in one device allocation
+    this object owns (the Gguf may be closed after loading)."""
+
+    def __init__(self, dev, g, seq_len):
+        self.dev, self.g = dev, g
+        h = _vp()
+        dev._check(dev.lib.qr_gguf_load(dev.ctx, _vp(g.h), seq_len, C.byref(h)), "qr_gguf_load")
+        self.h = h.value
+        mp = dev.lib.qr_gguf_model_get(_vp(self.h))
+        self.model = mp.contents
+        self.layers = self.model.layers
+
+    def decoder(self, kv_type=KV_Q8_0, order=ORDER_SEQ, page=0, flags=0):
+        return Decoder(self.dev, self.model, self, kv_type=kv_type, order=order, page=page,
+                       flags=flags)
+
+    def close(self):
+        if self.h is not None:
+            self.dev.lib.qr_gguf_model_free(_vp(self.h))
             self.h = None
 
     def __del__(self):
