@@ -133,27 +133,36 @@ def copy_calibration(dev, nbytes=512 << 20):
 
 
 def bench_headline(dev, steps, warmup, copies=16):
-    """Q4_K 32000 x 2048 at 1 and 4 tokens over 16 weight copies, and a plain
-    read of the same bytes."""
+    """Q4_K 32000 x 2048 at 1 and 4 tokens over 16 weight copies, in the tiled
+    layout (qr_weights_tile, made once before timing: the same bytes permuted)
+    and in the reference's row-major layout, and a plain read of the same
+    bytes."""
     qtype, n, d = Q.TYPE_Q4_K, 32000, 2048
     wbytes = n * synth.row_bytes(qtype, d)
     wbuf = dev.alloc(wbytes * copies)
+    tbuf = dev.alloc(wbytes * copies)
     dev.write(wbuf, synth.weights(1, n, d, qtype))
     for c in range(1, copies):
         dev.copy(wbuf.ptr + c * wbytes, wbuf.ptr, wbytes)
+    for c in range(copies):
+        dev.tile(qtype, wbuf.ptr + c * wbytes, tbuf.ptr + c * wbytes, n, d)
+    dev.sync()
     out = {}
-    for nt in (1, 4):
-        xb = dev.upload(synth.normal(2, (nt, d)))
-        yb = dev.alloc(nt * n * 4)
-        launch = lambda i: dev.gemv(qtype, wbuf.ptr + (i % copies) * wbytes, xb.ptr, yb.ptr,  # noqa: E731
-                                    n, d, nt)
-        for i in range(warmup):
-            launch(i)
-        dev.sync()
-        ms = graph_ms(dev, launch, steps if nt == 1 else max(steps // 2, 20))
-        alg = gemv_alg_bytes(qtype, n, d, nt)
-        out[nt] = dict(ms_per_step=ms, weight_gbps=wbytes / (ms / 1e3) / 1e9, alg_bytes=alg,
-                       achieved_gbps=alg / (ms / 1e3) / 1e9)
+    for layout, buf, ty in (("tiled", tbuf, qtype | Q.TILED), ("rows", wbuf, qtype)):
+        for nt in (1, 4):
+            xb = dev.upload(synth.normal(2, (nt, d)))
+            yb = dev.alloc(nt * n * 4)
+            launch = lambda i: dev.gemv(ty, buf.ptr + (i % copies) * wbytes, xb.ptr,  # noqa: E731
+                                        yb.ptr, n, d, nt)
+            for i in range(warmup):
+                launch(i)
+            dev.sync()
+            ms = graph_ms(dev, launch, steps if nt == 1 else max(steps // 2, 20))
+            alg = gemv_alg_bytes(qtype, n, d, nt)
+            out[(layout, nt)] = dict(ms_per_step=ms, weight_gbps=wbytes / (ms / 1e3) / 1e9,
+                                     alg_bytes=alg, achieved_gbps=alg / (ms / 1e3) / 1e9)
+            xb.free()
+            yb.free()
     sink = dev.alloc(16)
     rd = lambda i: dev.read_kernel(wbuf.ptr + (i % copies) * wbytes, wbytes, sink.ptr)  # noqa: E731
     for i in range(warmup):
@@ -162,6 +171,7 @@ def bench_headline(dev, steps, warmup, copies=16):
     ms = graph_ms(dev, rd, steps)
     out["read"] = dict(ms_per_step=ms, bytes=wbytes, gbps=wbytes / (ms / 1e3) / 1e9)
     wbuf.free()
+    tbuf.free()
     return out
 
 
@@ -215,6 +225,40 @@ def bench_sweep(dev, types, warmup, pool_bytes=600 << 20, max_steps=2048, only=N
                         key, ms * 1e3, alg / (ms / 1e3) / 1e9, res[key]["frac"]))
                     xb.free()
                     yb.free()
+            if qtype in (Q.TYPE_Q4_K, Q.TYPE_Q5_K):
+                # the same shapes in the tiled layout: a pool of tiled copies of the
+                # first n rows
+                for n, _ in shapes:
+                    wb = n * rb
+                    copies_t = max(1, math.ceil(pool_bytes / wb))
+                    tpool = dev.alloc(wb * copies_t)
+                    dev.tile(qtype, pool.ptr, tpool.ptr, n, d)
+                    for c in range(1, copies_t):
+                        dev.copy(tpool.ptr + c * wb, tpool.ptr, wb)
+                    for nt in (1, 4):
+                        steps = int(min(max(64, copies_t), max_steps))
+                        xb = dev.upload(synth.normal(3 + nt, (nt, d)))
+                        yb = dev.alloc(nt * n * 4)
+                        launch = lambda i: dev.gemv(qtype | Q.TILED,  # noqa: E731
+                                                    tpool.ptr + (i % copies_t) * wb, xb.ptr,
+                                                    yb.ptr, n, d, nt)
+                        for i in range(warmup):
+                            launch(i)
+                        dev.sync()
+                        ms = graph_ms(dev, launch, steps, reps=3)
+                        alg = gemv_alg_bytes(qtype, n, d, nt)
+                        key = "%s_%dx%d_t%d_tiled" % (TNAME[qtype], n, d, nt)
+                        res[key] = dict(us=round(ms * 1e3, 3),
+                                        weight_gbps=round(wb / (ms / 1e3) / 1e9, 1),
+                                        alg_bytes=alg,
+                                        achieved_gbps=round(alg / (ms / 1e3) / 1e9, 1),
+                                        frac=round(alg / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+                                        launches=steps)
+                        log("bench: %-28s %8.2f us  %7.0f GB/s  frac %.3f" % (
+                            key, ms * 1e3, alg / (ms / 1e3) / 1e9, res[key]["frac"]))
+                        xb.free()
+                        yb.free()
+                    tpool.free()
             pool.free()
     return res
 
@@ -385,6 +429,12 @@ def build_decoder(dev, M, cap):
     slab = dev.alloc(per_layer * L)
     for p, o in zip(parts, offs):
         dev.write(slab, p, int(o))
+    # wq / wk / wo (Q4_K) in the tiled layout, as qr_gguf_load stores them
+    for j, (rows, cols) in ((0, (qd, dim)), (1, (kvd, dim)), (3, (dim, qd))):
+        tmp = dev.upload(parts[j])
+        dev.tile(Q.TYPE_Q4_K, tmp.ptr, slab.ptr + int(offs[j]), rows, cols)
+        dev.sync()
+        tmp.free()
     for l in range(1, L):
         dev.copy(slab.ptr + l * per_layer, slab.ptr, per_layer)
     emb = _tiled(dev, synth.weights(5010, 8192, dim, Q.TYPE_Q4_K), V)
@@ -400,7 +450,8 @@ def build_decoder(dev, M, cap):
     m = dict(dim=dim, n_heads=H, n_kv_heads=KVH, head_dim=hd, n_layers=L, vocab=V, seq_len=cap,
              rope_base=1e6, tok_embd=emb.ptr, tok_type=Q.TYPE_Q4_K, rms_final=rmsf.ptr,
              wcls=wcls.ptr, wcls_type=Q.TYPE_Q6_K,
-             wtype=(Q.TYPE_Q4_K, Q.TYPE_Q4_K, Q.TYPE_Q6_K, Q.TYPE_Q4_K),
+             wtype=(Q.TYPE_Q4_K | Q.TILED, Q.TYPE_Q4_K | Q.TILED, Q.TYPE_Q6_K,
+                    Q.TYPE_Q4_K | Q.TILED),
              E=M["shape"]["E"], K=M["shape"]["K"], hidden=M["shape"]["hidden"],
              up_type=Q.TYPE_Q4_K, down_type=Q.TYPE_Q6_K, layers=layers)
     attn_bytes = sum(p.nbytes for p in parts[:4]) + 2 * 4 * dim
@@ -519,7 +570,7 @@ def cpu_baseline_moe(M, cpus, reps=24, copies=4):
 
 # ---------------------------------------------------------------------------
 def load_traffic():
-    p = os.path.join(REPO, "profiles", "k_gemv_blk_q4k_32000x2048_traffic.json")
+    p = os.path.join(REPO, "profiles", "k_gemv_tiled_q4k_32000x2048_traffic.json")
     if not os.path.exists(p):
         return None
     try:
@@ -563,13 +614,15 @@ def main():
     h = None
     if not args.no_gemv:
         h = bench_headline(dev, args.steps, args.warmup)
-        g, g4, rd = h[1], h[4], h["read"]
-        log("bench: Q4_K 32000x2048 T=1: %.3f us/launch, %.0f GB/s weights, %.0f GB/s algorithmic"
-            % (g["ms_per_step"] * 1e3, g["weight_gbps"], g["achieved_gbps"]))
+        for layout in ("tiled", "rows"):
+            for nt in (1, 4):
+                g = h[(layout, nt)]
+                log("bench: Q4_K 32000x2048 %s T=%d: %.3f us/launch, %.0f GB/s weights, "
+                    "%.0f GB/s algorithmic" % (layout, nt, g["ms_per_step"] * 1e3,
+                                              g["weight_gbps"], g["achieved_gbps"]))
+        rd = h["read"]
         log("bench: plain read of the same %d bytes: %.3f us, %.0f GB/s" % (
             rd["bytes"], rd["ms_per_step"] * 1e3, rd["gbps"]))
-        log("bench: Q4_K 32000x2048 T=4: %.3f us/launch, %.0f GB/s weights"
-            % (g4["ms_per_step"] * 1e3, g4["weight_gbps"]))
 
     sweep = None
     if not args.no_sweep:
@@ -636,38 +689,45 @@ def main():
         if M is not None:
             moe["cpu_baseline"] = cpu_baseline_moe(M, cpus)
 
+    h1 = h[("tiled", 1)] if h else None
+
+    def gkey(layout, nt):
+        g = h[(layout, nt)]
+        return {"ms_per_step": round(g["ms_per_step"], 6),
+                "weight_gbps": round(g["weight_gbps"], 2), "alg_bytes": g["alg_bytes"],
+                "achieved_gbps": round(g["achieved_gbps"], 2),
+                "roofline_frac": round(g["achieved_gbps"] / HBM_PEAK_GBPS, 4)}
     out = {
         "metric": METRIC,
-        "value": round(h[1]["weight_gbps"], 2) if h else None,
+        "value": round(h1["weight_gbps"], 2) if h else None,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(h[1]["ms_per_step"], 6) if h else None,
+        "ms_per_step": round(h1["ms_per_step"], 6) if h else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic",
         "config": {"workload": "Q4_K decode GEMV 32000x2048 (lm_head of the K-quant sweep), "
-                               "1 token, 16 rotating weight copies", "n": 32000, "d": 2048,
-                   "qtype": "Q4_K", "tokens": 1},
-        "roofline": {"bound": "hbm", "achieved": round(h[1]["achieved_gbps"], 2),
+                               "1 token, 16 rotating weight copies in the tiled layout "
+                               "(qr_weights_tile, made before timing)", "n": 32000, "d": 2048,
+                   "qtype": "Q4_K", "tokens": 1, "layout": "tiled"},
+        "roofline": {"bound": "hbm", "achieved": round(h1["achieved_gbps"], 2),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(h[1]["achieved_gbps"] / HBM_PEAK_GBPS, 4),
+                     "frac": round(h1["achieved_gbps"] / HBM_PEAK_GBPS, 4),
                      "traffic": load_traffic(),
                      "read_ceiling": {
                          "note": "a plain read of the same weight bytes, 16 rotating copies",
                          "us": round(h["read"]["ms_per_step"] * 1e3, 3),
                          "gbps": round(h["read"]["gbps"], 1),
-                         "gemv_over_read": round(h["read"]["ms_per_step"] / h[1]["ms_per_step"],
+                         "gemv_over_read": round(h["read"]["ms_per_step"] / h1["ms_per_step"],
                                                  4)}} if h else None,
         "cpu_baseline": cpu,
-        "gemv_q4k_32000x2048_t4": {
-            "ms_per_step": round(h[4]["ms_per_step"], 6),
-            "weight_gbps": round(h[4]["weight_gbps"], 2), "alg_bytes": h[4]["alg_bytes"],
-            "achieved_gbps": round(h[4]["achieved_gbps"], 2),
-            "roofline_frac": round(h[4]["achieved_gbps"] / HBM_PEAK_GBPS, 4)} if h else None,
+        "gemv_q4k_32000x2048_t4": gkey("tiled", 4) if h else None,
+        "gemv_q4k_32000x2048_rows_t1": gkey("rows", 1) if h else None,
+        "gemv_q4k_32000x2048_rows_t4": gkey("rows", 4) if h else None,
         "gemv_sweep": sweep,
         "moe_qwen3": moe,
         "moe_qwen15": moe15,

@@ -143,6 +143,21 @@ int qr_gemv_ord(qr_ctx* ctx, int order, uint32_t type, const void* w, const floa
                 int xstride, float* y, int ystride, int n, int d, int nt, int32_t* acc,
                 int32_t* accb);
 
+/* The tiled layout of a Q4_K / Q5_K matrix: the same bytes as the
+ * reference's row-major super-blocks, permuted so that the GEMV streams each
+ * wave's tile in the order it is consumed (no reference counterpart; the
+ * results are the same bits).  A tile is 64 / (d / 256) rows; within it, the
+ * k-th 16-byte chunk of every super-block is stored together (header chunk
+ * first).  Pass `type | QR_TILED` to qr_gemv / qr_gemv_ex / qr_gemv_ord (no
+ * integer sums) and in a decoder model's wq / wk / wv / wo / wcls types.
+ * qr_weights_tile writes the tiled copy of an n x d matrix (d a multiple of
+ * 256, at most 16384) into dst, qr_weights_untile the reverse; device
+ * pointers, 16-byte aligned, not overlapping; enqueued on the context
+ * stream.  qr_row_bytes(type | QR_TILED, d) is the plain row size. */
+#define QR_TILED 0x100u
+int qr_weights_tile(qr_ctx* ctx, uint32_t type, const void* src, void* dst, int n, int d);
+int qr_weights_untile(qr_ctx* ctx, uint32_t type, const void* src, void* dst, int n, int d);
+
 /* fp32 GEMV in a reference accumulation order (router logits):
  * y[t][r] = sum_j w[r][j] * x[t][j]. */
 int qr_matmul_f32(qr_ctx* ctx, int order, const float* w, const float* x, float* y, int n, int d,
@@ -381,7 +396,9 @@ int qr_gguf_expert_host(const qr_gguf* g, int layer, int e, const void** up, con
 /* The same model copied to the device: every tensor the decoder reads in one
  * allocation (each tensor 256-byte aligned; per-expert tensors gathered
  * into one range per kind, expert e at e * slice, as a 3-D tensor is laid
- * out; a tied output shares the embedding's copy).  Returns a qr_model of
+ * out; a tied output shares the embedding's copy; Q4_K / Q5_K attention
+ * projections and output matrices with at most 64 super-blocks per row are
+ * stored tiled and their types carry QR_TILED).  Returns a qr_model of
  * device pointers for qr_decoder_create.  The copy owns its memory: the
  * qr_gguf may be closed after loading, two loads are two copies, and
  * qr_gguf_model_free releases one of them (after the context stream has

@@ -749,6 +749,8 @@ hipError_t matmul_q_dev(const void* w, uint32_t type, int order, const float* x,
                         int dd, hipStream_t s) {
   if (type == QR_T_F32)
     return gemv_f32_launch(order, static_cast<const float*>(w), x, y, n, dd, 1, dd, n, s);
+  if (type & QR_TILED)
+    return gemv_tiled_launch((int)(type & ~(uint32_t)QR_TILED), w, x, y, n, dd, 1, dd, n, s);
   return gemv_launch((int)type, order, w, x, y, n, dd, 1, dd, n, nullptr, nullptr, s);
 }
 

@@ -32,7 +32,16 @@ struct GemvArgs {
   int rows_per_wg;
   int32_t* acc;          // optional [nt][n][units] int32 unit sums
   int32_t* accb;         // optional [nt][units] activation block sums
+  // tiled layout (qr_tiled.h): super-blocks per row, rows per full tile,
+  // tiles, bytes of a full tile -- set on the host
+  int t_nb, t_rb, t_ntiles;
+  size_t t_tile_bytes;
 };
+}  // namespace qr
+
+#include "qr_tiled.h"
+
+namespace qr {
 
 // LDS layout: act q | act bd | act bs | terms | staged tile.  Terms are
 // [nt][R][slots][U + 1] floats (slots: q8_slots).
@@ -504,6 +513,125 @@ static hipError_t launch_nt(const GemvArgs& a, int nt, hipStream_t st) {
     case 8: return launch_any_t<TYPE, 8, Q8O>(a, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Tiled-layout GEMV (qr_tiled.h).
+// ---------------------------------------------------------------------------
+size_t tiled_lds_bytes(int type, int d, int nt, int nw) {
+  const int nch = type == QR_T_Q4_K ? TiledFmt<QR_T_Q4_K>::kChunks : TiledFmt<QR_T_Q5_K>::kChunks;
+  return align16((size_t)nt * act_tok_bytes(d)) + (size_t)nw * nch * 1024;
+}
+
+bool gemv_tiled_ok(int type, int d, int nt) {
+  if (type != QR_T_Q4_K && type != QR_T_Q5_K) return false;
+  if (d <= 0 || (d & 255) || (d >> 8) > 64) return false;
+  if (!(nt >= 1 && nt <= 4) && nt != 8) return false;
+  return tiled_lds_bytes(type, d, nt == 8 ? 4 : nt, 4) <= kLdsMax;
+}
+
+template <int TYPE, int NT, int NW, int PRO>
+static hipError_t launch_tiled_k(const GemvArgs& a, int grid, size_t lds, hipStream_t st) {
+  static std::atomic<bool> opted[64];
+  if (lds > 64 * 1024) {
+    hipError_t e = lds_opt_in((const void*)k_gemv_tiled<TYPE, NT, NW, PRO>, opted);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((k_gemv_tiled<TYPE, NT, NW, PRO>), dim3(grid), dim3(64 * NW), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int TYPE, int NT, int NW>
+static hipError_t launch_tiled_nw(const GemvArgs& a, int grid, size_t lds, hipStream_t st) {
+  constexpr int QW = NW < 4 ? NW : 4;
+  const int groups = NT * (a.d >> 3);
+  if (groups <= 64 * QW) return launch_tiled_k<TYPE, NT, NW, kProAsm1>(a, grid, lds, st);
+  if (groups <= 128 * QW) return launch_tiled_k<TYPE, NT, NW, kProAsm2>(a, grid, lds, st);
+  return launch_tiled_k<TYPE, NT, NW, kProLate>(a, grid, lds, st);
+}
+
+// Waves per workgroup: 8 where two such workgroups fit a CU's LDS and the
+// tiles give every CU one, else 4 (four quantizing waves either way).  The
+// grid is at most what stays resident (as many workgroups per CU as LDS
+// holds, up to 4); the waves then walk their tiles.  Measured on the
+// 32000 x 2048 Q4_K GEMV (4000 tiles): 8 waves, two workgroups per CU (every
+// wave one tile), 7.65 us; 4 waves, four per CU, 7.9 us; 16 waves, one per
+// CU, 8.3 us.
+template <int TYPE, int NT>
+static hipError_t launch_tiled_t(const GemvArgs& a, hipStream_t st) {
+  const TiledGeom g = tiled_geom(TYPE, a.n, a.d);
+  if (g.ntiles <= 0) return hipSuccess;
+  const int cus = device_cus();
+  const int nw =
+      (2 * tiled_lds_bytes(TYPE, a.d, NT, 8) <= kLdsMax && (g.ntiles + 7) / 8 >= cus) ? 8 : 4;
+  const size_t lds = tiled_lds_bytes(TYPE, a.d, NT, nw);
+  int per_cu = (int)(kLdsMax / lds);
+  per_cu = per_cu < 1 ? 1 : (per_cu > 4 ? 4 : per_cu);
+  const int want = (g.ntiles + nw - 1) / nw;
+  const int grid = want < cus * per_cu ? want : cus * per_cu;
+  if (nw == 8) return launch_tiled_nw<TYPE, NT, 8>(a, grid, lds, st);
+  return launch_tiled_nw<TYPE, NT, 4>(a, grid, lds, st);
+}
+
+template <int TYPE>
+static hipError_t launch_tiled_type(GemvArgs a, int nt, hipStream_t st) {
+  switch (nt) {
+    case 1: return launch_tiled_t<TYPE, 1>(a, st);
+    case 2: return launch_tiled_t<TYPE, 2>(a, st);
+    case 3: return launch_tiled_t<TYPE, 3>(a, st);
+    case 4: return launch_tiled_t<TYPE, 4>(a, st);
+    case 8: {  // two launches of four tokens
+      hipError_t e = launch_tiled_t<TYPE, 4>(a, st);
+      if (e != hipSuccess) return e;
+      a.X += (size_t)4 * a.xstride;
+      a.Y += (size_t)4 * a.ystride;
+      return launch_tiled_t<TYPE, 4>(a, st);
+    }
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, int n, int d,
+                             int nt, int xstride, int ystride, hipStream_t st) {
+  GemvArgs a;
+  a.W = static_cast<const uint8_t*>(W);
+  a.X = X;
+  a.Y = Y;
+  a.n = n;
+  a.d = d;
+  a.xstride = xstride;
+  a.ystride = ystride;
+  a.rows_per_wg = 0;
+  a.acc = nullptr;
+  a.accb = nullptr;
+  const TiledGeom g = tiled_geom(type, n, d);
+  a.t_nb = g.nb;
+  a.t_rb = g.RB;
+  a.t_ntiles = g.ntiles;
+  a.t_tile_bytes = g.tile_bytes;
+  if (type == QR_T_Q4_K) return launch_tiled_type<QR_T_Q4_K>(a, nt, st);
+  if (type == QR_T_Q5_K) return launch_tiled_type<QR_T_Q5_K>(a, nt, st);
+  return hipErrorInvalidValue;
+}
+
+hipError_t tile_pack_launch(int type, const void* src, void* dst, int n, int d, bool reverse,
+                            hipStream_t st) {
+  const long nch = type == QR_T_Q4_K ? TiledFmt<QR_T_Q4_K>::kChunks : TiledFmt<QR_T_Q5_K>::kChunks;
+  const long total = (long)n * (d >> 8) * nch;
+  if (total <= 0) return hipSuccess;
+  long grid = (total + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  const uint8_t* s = static_cast<const uint8_t*>(src);
+  uint8_t* o = static_cast<uint8_t*>(dst);
+  if (type == QR_T_Q4_K)
+    hipLaunchKernelGGL(k_tile_pack<QR_T_Q4_K>, dim3((unsigned)grid), dim3(256), 0, st, s, o, n, d,
+                       reverse ? 1 : 0);
+  else if (type == QR_T_Q5_K)
+    hipLaunchKernelGGL(k_tile_pack<QR_T_Q5_K>, dim3((unsigned)grid), dim3(256), 0, st, s, o, n, d,
+                       reverse ? 1 : 0);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 hipError_t gemv_launch(int type, int q8o, const void* W, const float* X, float* Y, int n, int d,

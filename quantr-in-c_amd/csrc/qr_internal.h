@@ -38,6 +38,12 @@ int gemv_rows_per_wg(int type, int q8o, int n, int d, int nt);
 hipError_t gemv_launch(int type, int q8o, const void* W, const float* X, float* Y, int n, int d,
                        int nt, int xstride, int ystride, int32_t* acc, int32_t* accb,
                        hipStream_t st);
+// Tiled layout (qr_tiled.h): type is the base type (QR_T_Q4_K / QR_T_Q5_K).
+bool gemv_tiled_ok(int type, int d, int nt);
+hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, int n, int d,
+                             int nt, int xstride, int ystride, hipStream_t st);
+hipError_t tile_pack_launch(int type, const void* src, void* dst, int n, int d, bool reverse,
+                            hipStream_t st);
 hipError_t gemv_f32_launch(int order, const float* W, const float* X, float* Y, int n, int d,
                            int nt, int xstride, int ystride, hipStream_t st);
 hipError_t quantize_q8_0_launch(const float* x, void* y, long nblocks, hipStream_t st);

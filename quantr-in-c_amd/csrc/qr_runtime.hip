@@ -471,8 +471,41 @@ int qr_read_kernel(qr_ctx* c, const void* src, size_t bytes, void* sink) {
 }
 
 size_t qr_row_bytes(uint32_t type, int d) {
+  type &= ~(uint32_t)QR_TILED;  // the tiled layout keeps the row size
   if (d < 0 || !known_type(type)) return 0;
   return qr_wrow_bytes((int)type, d);
+}
+
+static int tile_args(uint32_t type, const void* src, void* dst, int n, int d, const char* who) {
+  if (type != QR_T_Q4_K && type != QR_T_Q5_K)
+    return fail(QR_ERR_UNSUPPORTED, "%s: type %u has no tiled layout (Q4_K, Q5_K)", who, type);
+  if (n < 0 || d <= 0 || (d & 255) || (d >> 8) > 64)
+    return fail(QR_ERR_UNSUPPORTED, "%s: shape %d x %d (d a multiple of 256, at most 16384)", who,
+                n, d);
+  if (n > 0 && (!src || !dst)) return fail(QR_ERR_INVALID, "%s: null pointer", who);
+  if (!aligned(src, 16) || !aligned(dst, 16))
+    return fail(QR_ERR_INVALID, "%s: src and dst must be 16-byte aligned", who);
+  const size_t bytes = qr_wrow_bytes((int)type, d) * (size_t)n;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(src), b = reinterpret_cast<uintptr_t>(dst);
+  if (n > 0 && a < b + bytes && b < a + bytes)
+    return fail(QR_ERR_INVALID, "%s: src and dst overlap", who);
+  return QR_OK;
+}
+
+int qr_weights_tile(qr_ctx* c, uint32_t type, const void* src, void* dst, int n, int d) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_weights_tile: null ctx");
+  int rc = tile_args(type, src, dst, n, d, "qr_weights_tile");
+  if (rc) return rc;
+  QR_HIP(qr::tile_pack_launch((int)type, src, dst, n, d, false, c->stream), "k_tile_pack");
+  return QR_OK;
+}
+
+int qr_weights_untile(qr_ctx* c, uint32_t type, const void* src, void* dst, int n, int d) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_weights_untile: null ctx");
+  int rc = tile_args(type, src, dst, n, d, "qr_weights_untile");
+  if (rc) return rc;
+  QR_HIP(qr::tile_pack_launch((int)type, src, dst, n, d, true, c->stream), "k_tile_pack");
+  return QR_OK;
 }
 
 int qr_quantize_q8_0(qr_ctx* c, const float* x, void* y, long n) {
@@ -490,6 +523,8 @@ int qr_gemv_ord(qr_ctx* c, int order, uint32_t type, const void* w, const float*
   if (!c) return fail(QR_ERR_INVALID, "qr_gemv: null ctx");
   if (order < QR_ORDER_SEQ || order > QR_ORDER_AVX512)
     return fail(QR_ERR_INVALID, "qr_gemv: order %d", order);
+  const bool tiled = (type & QR_TILED) != 0;
+  type &= ~(uint32_t)QR_TILED;
   if (!known_type(type)) return fail(QR_ERR_INVALID, "qr_gemv: unknown type %u", type);
   if (n < 0 || d < 0) return fail(QR_ERR_INVALID, "qr_gemv: negative size");
   if (!(nt == 1 || nt == 2 || nt == 3 || nt == 4 || nt == 8))
@@ -506,6 +541,8 @@ int qr_gemv_ord(qr_ctx* c, int order, uint32_t type, const void* w, const float*
     QR_HIP(hipGetLastError(), "k_zero_rows");
     return QR_OK;
   }
+  if (tiled && type != QR_T_Q4_K && type != QR_T_Q5_K)
+    return fail(QR_ERR_UNSUPPORTED, "qr_gemv: type %u has no tiled layout", type);
   if (type == QR_T_F32) {
     if (acc || accb) return fail(QR_ERR_INVALID, "qr_gemv: F32 has no integer sums");
     QR_HIP(qr::gemv_f32_launch(QR_ORDER_SEQ, static_cast<const float*>(w), x, y, n, d, nt,
@@ -515,6 +552,14 @@ int qr_gemv_ord(qr_ctx* c, int order, uint32_t type, const void* w, const float*
   if (!aligned(w, 16)) return fail(QR_ERR_INVALID, "qr_gemv: weights must be 16-byte aligned");
   if (!aligned(x, 16) || (nt > 1 && (xstride & 3)))
     return fail(QR_ERR_INVALID, "qr_gemv: x must be 16-byte aligned (and xstride a multiple of 4)");
+  if (tiled) {
+    if (acc || accb) return fail(QR_ERR_UNSUPPORTED, "qr_gemv: no integer sums on tiled weights");
+    if (!qr::gemv_tiled_ok((int)type, d, nt))
+      return fail(QR_ERR_UNSUPPORTED, "qr_gemv: tiled type %u at d=%d nt=%d", type, d, nt);
+    QR_HIP(qr::gemv_tiled_launch((int)type, w, x, y, n, d, nt, xstride, ystride, c->stream),
+           "k_gemv_tiled");
+    return QR_OK;
+  }
   const int R = qr::gemv_rows_per_wg((int)type, order, n, d, nt);
   if (!qr::gemv_blk_ok((int)type, d, nt) && !qr::gemv_stream_ok((int)type, order, d, nt) &&
       qr::gemv_lds_bytes((int)type, order, d, nt, R) > 64 * 1024)
@@ -617,6 +662,14 @@ int moe_check(const qr_moe_layer* L, const char* who) {
 }
 
 int gemv_check(uint32_t type, int order, const void* w, int n, int d, const char* who) {
+  if (type & QR_TILED) {
+    type &= ~(uint32_t)QR_TILED;
+    if (n <= 0 || d <= 0) return fail(QR_ERR_INVALID, "%s: weight shape %d x %d", who, n, d);
+    if (!gemv_tiled_ok((int)type, d, 1))
+      return fail(QR_ERR_UNSUPPORTED, "%s: tiled type %u at d=%d", who, type, d);
+    if (w && !aligned(w, 16)) return fail(QR_ERR_INVALID, "%s: weights must be 16-byte aligned", who);
+    return QR_OK;
+  }
   if (!known_type(type)) return fail(QR_ERR_INVALID, "%s: unknown weight type %u", who, type);
   if (n <= 0 || d <= 0) return fail(QR_ERR_INVALID, "%s: weight shape %d x %d", who, n, d);
   if (type == QR_T_F32) return QR_OK;

@@ -528,6 +528,8 @@ typedef struct {
     const void* src;
     size_t bytes, off;
     const void** fix;
+    uint32_t* tile_type;  /* non-NULL: stored in the tiled layout, this type gets QR_TILED */
+    int rows, cols;
 } copy_op;
 
 typedef struct {
@@ -553,6 +555,8 @@ static int plan_add(copy_plan* p, const void* src, size_t bytes, const void** fi
     p->op[p->n].bytes = bytes;
     p->op[p->n].off = p->end;
     p->op[p->n].fix = fix;
+    p->op[p->n].tile_type = NULL;
+    p->op[p->n].rows = p->op[p->n].cols = 0;
     p->n++;
     p->end += bytes;
     return QR_OK;
@@ -568,6 +572,21 @@ int qr_gguf_model_free(qr_gguf_model* gm) {
 
 const qr_model* qr_gguf_model_get(const qr_gguf_model* gm) { return gm ? &gm->model : NULL; }
 
+/* Q4_K / Q5_K matrices whose rows are whole super-blocks (at most 64) are
+ * stored tiled (qr_weights_tile): the decoder's GEMV streams them faster. */
+static int tileable(uint32_t type, int cols) {
+    return (type == QR_TYPE_Q4_K || type == QR_TYPE_Q5_K) && cols > 0 && cols % 256 == 0 &&
+           cols / 256 <= 64;
+}
+
+static void plan_tile(copy_plan* p, uint32_t* type, int rows, int cols) {
+    copy_op* o = &p->op[p->n - 1];
+    if (!tileable(*type, cols)) return;
+    o->tile_type = type;
+    o->rows = rows;
+    o->cols = cols;
+}
+
 /* The copy plan of every tensor the decoder reads: the tied output shares
  * the embedding; per-expert tensors are gathered into one range per kind
  * (expert e at e * slice), as a 3-D tensor is laid out. */
@@ -579,8 +598,10 @@ static int plan_model(const qr_gguf* g, qr_gguf_model* gm, copy_plan* p) {
     do { if ((rc = plan_add(p, (src), (bytes), (const void**)(fix), 1)) != QR_OK) return rc; } while (0)
     ADD(m->tok_embd, qr_row_bytes(m->tok_type, m->dim) * (size_t)m->vocab, &m->tok_embd);
     ADD(m->rms_final, (size_t)m->dim * 4, &m->rms_final);
-    if (!tied)
+    if (!tied) {
         ADD(m->wcls, qr_row_bytes(m->wcls_type, m->dim) * (size_t)m->vocab, &m->wcls);
+        plan_tile(p, &m->wcls_type, m->vocab, m->dim);
+    }
     for (l = 0; l < m->n_layers; l++) {
         qr_layer* y = &gm->layers[l];
         qr_moe_layer* e = &y->moe;
@@ -591,9 +612,13 @@ static int plan_model(const qr_gguf* g, qr_gguf_model* gm, copy_plan* p) {
         ADD(y->rms_att, (size_t)m->dim * 4, &y->rms_att);
         ADD(y->rms_ffn, (size_t)m->dim * 4, &y->rms_ffn);
         ADD(y->wq, qr_row_bytes(y->wq_type, m->dim) * (size_t)qd, &y->wq);
+        plan_tile(p, &y->wq_type, qd, m->dim);
         ADD(y->wk, qr_row_bytes(y->wk_type, m->dim) * (size_t)kvd, &y->wk);
+        plan_tile(p, &y->wk_type, kvd, m->dim);
         ADD(y->wv, qr_row_bytes(y->wv_type, m->dim) * (size_t)kvd, &y->wv);
+        plan_tile(p, &y->wv_type, kvd, m->dim);
         ADD(y->wo, qr_row_bytes(y->wo_type, qd) * (size_t)m->dim, &y->wo);
+        plan_tile(p, &y->wo_type, m->dim, qd);
         ADD(e->router, (size_t)e->n_experts * (size_t)m->dim * 4, &e->router);
         if (e->n_experts > 1 && qr_gguf_expert_host(g, l, 1, &u1, &d1, &g1) != QR_OK)
             return QR_ERR_INVALID;
@@ -627,6 +652,8 @@ int qr_gguf_load(qr_ctx* ctx, const qr_gguf* g, int seq_len, qr_gguf_model** out
     qr_gguf_model* gm;
     copy_plan plan = {NULL, 0, 0, 0};
     int L, i, rc, tied;
+    void* stage = NULL;
+    size_t stage_bytes = 0;
     if (!out) return QR_ERR_INVALID;
     *out = NULL;
     if (!ctx || !g) return QR_ERR_INVALID;
@@ -654,17 +681,37 @@ int qr_gguf_load(qr_ctx* ctx, const qr_gguf* g, int seq_len, qr_gguf_model** out
     gm->slab_bytes = plan.end;
     rc = qr_malloc(ctx, plan.end, &gm->slab);
     if (rc != QR_OK) goto fail;
+    for (i = 0; i < plan.n; i++) /* the staging buffer of the tiled tensors */
+        if (plan.op[i].tile_type && plan.op[i].bytes > stage_bytes) stage_bytes = plan.op[i].bytes;
+    if (stage_bytes) {
+        rc = qr_malloc(ctx, stage_bytes, &stage);
+        if (rc != QR_OK) goto fail;
+    }
     for (i = 0; i < plan.n; i++) {
         char* dst = (char*)gm->slab + plan.op[i].off;
-        rc = qr_memcpy_h2d(ctx, dst, plan.op[i].src, plan.op[i].bytes);
-        if (rc != QR_OK) goto fail;
-        if (plan.op[i].fix) *plan.op[i].fix = dst;
+        const copy_op* o = &plan.op[i];
+        if (o->tile_type) {
+            rc = qr_memcpy_h2d(ctx, stage, o->src, o->bytes);
+            if (rc == QR_OK) rc = qr_weights_tile(ctx, *o->tile_type, stage, dst, o->rows, o->cols);
+            if (rc == QR_OK) rc = qr_sync(ctx);  /* the stage is reused by the next tensor */
+            if (rc != QR_OK) goto fail;
+            *o->tile_type |= QR_TILED;
+        } else {
+            rc = qr_memcpy_h2d(ctx, dst, o->src, o->bytes);
+            if (rc != QR_OK) goto fail;
+        }
+        if (o->fix) *o->fix = dst;
+    }
+    if (stage) {
+        (void)qr_free(ctx, stage);
+        stage = NULL;
     }
     if (tied) gm->model.wcls = gm->model.tok_embd;  /* the embedding's device copy */
     free(plan.op);
     *out = gm;
     return QR_OK;
 fail:
+    if (stage) (void)qr_free(ctx, stage);
     free(plan.op);
     qr_gguf_model_free(gm);
     return rc;

@@ -17,6 +17,7 @@ HEADERS = [os.path.join(REPO_DIR, "include", "qr_hip.h"),
            os.path.join(REPO_DIR, "include", "qr_dropin.h")]
 
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 0, 8, 12, 13, 14
+TILED = 0x100  # OR'ed into a Q4_K / Q5_K type: the weights are in the tiled layout
 ORDER_SEQ, ORDER_AVX2, ORDER_AVX512 = 0, 1, 2
 
 _vp = C.c_void_p
@@ -100,6 +101,8 @@ _SIGS = {
     "qr_moe_forward_noalloc": (C.c_int, [_vp, C.POINTER(MoeLayer), _vp, _vp, C.c_int, C.c_int,
                                          _vp, _vp]),
     "qr_weights_upload": (C.c_int, [_vp, _vp, C.c_size_t, C.POINTER(_vp)]),
+    "qr_weights_tile": (C.c_int, [_vp, C.c_uint32, _vp, _vp, C.c_int, C.c_int]),
+    "qr_weights_untile": (C.c_int, [_vp, C.c_uint32, _vp, _vp, C.c_int, C.c_int]),
     "qr_weights_upload_parts": (C.c_int, [_vp, _vp, _vp, C.c_size_t, C.c_int, C.POINTER(_vp)]),
     "qr_weights_lookup": (C.c_int, [_vp, _vp, C.POINTER(_vp)]),
     "qr_weights_release": (C.c_int, [_vp, _vp]),
@@ -297,6 +300,13 @@ class Device:
         self._check(self.lib.qr_gemv_ord(self.ctx, order, qtype, _vp(w_ptr), _vp(x_ptr),
                                           xstride or d, _vp(y_ptr), ystride or n, n, d, nt,
                                           _vp(acc_ptr), _vp(accb_ptr)), "qr_gemv_ord")
+
+    def tile(self, qtype, src_ptr, dst_ptr, n, d, reverse=False):
+        """qr_weights_tile (or qr_weights_untile): the tiled copy of an n x d
+        Q4_K / Q5_K matrix; pass qtype | TILED to gemv for it."""
+        f = self.lib.qr_weights_untile if reverse else self.lib.qr_weights_tile
+        self._check(f(self.ctx, qtype, _vp(src_ptr), _vp(dst_ptr), n, d),
+                    "qr_weights_untile" if reverse else "qr_weights_tile")
 
     def matmul_f32(self, order, w_ptr, x_ptr, y_ptr, n, d, nt=1):
         self._check(self.lib.qr_matmul_f32(self.ctx, order, _vp(w_ptr), _vp(x_ptr), _vp(y_ptr),

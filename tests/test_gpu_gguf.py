@@ -7,7 +7,8 @@ qr_gguf_open / qr_gguf_parse, qr_gguf_load and qr_decoder_*.
   alignment; from memory and from an mmap'd file): the decoder's logits and
   residual are the reference's own, bit-exact, for every build.
 - A Qwen3-like head shape (attention.key_length 128, q_dim != dim) over a
-  Q8_0 cache: identical to the same weights handed over as plain pointers.
+  Q8_0 cache, its Q4_K / Q5_K projections stored tiled by the loader:
+  identical to the same weights handed over as plain row-major pointers.
 - A load owns its device copy: the file may be closed, and freeing one of
   two loads leaves the other working.
 """
@@ -76,6 +77,14 @@ def test_gguf_head128_matches_pointer_model(dev, split):
     print("gguf head128 split %d" % split, flush=True)
     gm = gf.load(dev, m["seq_len"])
     assert gm.model.head_dim == 128 and gm.model.n_heads == 8
+    # the Q4_K / Q5_K projections are stored tiled (wq Q4_K, wo Q5_K here)
+    wt = m["wtype"]
+    for l in range(2):
+        y = gm.layers[l]
+        for got, want in ((y.wq_type, wt[0]), (y.wk_type, wt[1]), (y.wv_type, wt[2]),
+                          (y.wo_type, wt[3])):
+            tiled = want in (Q.TYPE_Q4_K, Q.TYPE_Q5_K)
+            assert got == (want | Q.TILED if tiled else want)
     toks = [3, 250, 17, 99, 4]
     d = gm.decoder(kv_type=Q.KV_Q8_0, order=ORDER_AVX2, page=64)
     lg, xs = run_tokens(dev, d, m, toks)
