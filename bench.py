@@ -27,7 +27,9 @@ Extra keys of the same line:
                model (48 layers, 32 query / 4 kv heads of 128, the MoE layer
                above, 151936-row Q6_K lm_head) over a Q8_0 paged KV cache
                prefilled to 4096 positions, replayed as one HIP graph per
-               token, in tokens/s with its algorithmic bytes;
+               token, in tokens/s with its algorithmic bytes; and the batched
+               prefill of a 512-token prompt (qr_decoder_prefill, chunks of
+               128) in tokens/s;
   cpu_baseline the reference's own matmul_q_fused and MoE block (oracle/_ref,
                its sources compiled with the CI flags) on this host's cores at
                1, 8 and all available threads: 3 warm-ups, then the median.
@@ -394,7 +396,8 @@ def bench_moe(dev, M, T, steps, warmup, order, nbatches=8, seed=7000):
 # ---------------------------------------------------------------------------
 # Full decode step
 # ---------------------------------------------------------------------------
-QWEN3_DEC = dict(dim=2048, n_heads=32, n_kv_heads=4, head_dim=128, vocab=151936, prefill=4096)
+QWEN3_DEC = dict(dim=2048, n_heads=32, n_kv_heads=4, head_dim=128, vocab=151936, prefill=4096,
+                 prefill_prompt=512)
 
 
 def _tiled(dev, rows_blob, n_rows):
@@ -489,6 +492,15 @@ def bench_decode(dev, M, steps, warmup, order):
         d.forward(int(toks[i]), P + i, lg.ptr)
     ms = dev.timer_stop() / steps
     logits = dev.download(lg, c["vocab"], np.float32)
+    # prompt prefill: 512 prompt tokens at positions 0 .. 511 in chunks of 128
+    # (qr_decoder_prefill; the workspace is allocated by an untimed first call)
+    pn = c["prefill_prompt"]
+    ptoks = np.random.default_rng(5031).integers(0, c["vocab"], size=pn)
+    d.prefill(ptoks[:128], 0, lg.ptr)
+    dev.sync()
+    dev.timer_start()
+    d.prefill(ptoks, 0, lg.ptr)
+    pms = dev.timer_stop()
     d.close()
     for b in bufs:
         b.free()
@@ -504,6 +516,9 @@ def bench_decode(dev, M, steps, warmup, order):
                   c["vocab"] * synth.row_bytes(Q.TYPE_Q6_K, dim) + 4 * dim)
     s = ms / 1e3
     return dict(ms_per_step=ms, tokens_per_s=1.0 / s, layers=L, positions=npos,
+                prefill=dict(tokens=int(pn), chunk=128, ms=round(pms, 3),
+                             tokens_per_s=round(pn / (pms / 1e3), 1),
+                             speedup_vs_decode=round((pn / (pms / 1e3)) * s, 2)),
                 alg_bytes=int(step_bytes), achieved_gbps=step_bytes / s / 1e9,
                 roofline_frac=step_bytes / s / 1e9 / HBM_PEAK_GBPS,
                 finite_logits=bool(np.isfinite(logits).all()))
@@ -668,6 +683,10 @@ def main():
                 "%.1f tokens/s, %.0f GB/s algorithmic (%.1f%% of HBM peak)" % (
                     dec["layers"], dec["positions"], dec["ms_per_step"], dec["tokens_per_s"],
                     dec["achieved_gbps"], 100 * dec["roofline_frac"]))
+            pf = dec["prefill"]
+            log("bench: prefill of %d prompt tokens (chunks of %d): %.2f ms, %.0f tokens/s, "
+                "%.1fx the decode step's rate" % (pf["tokens"], pf["chunk"], pf["ms"],
+                                                   pf["tokens_per_s"], pf["speedup_vs_decode"]))
         M["slab"].free()
         if not args.no_qwen15:
             M15 = build_qwen15(dev, 8)

@@ -345,6 +345,26 @@ int qr_decoder_kv_rows(const qr_decoder* dec, int layer, int pos, const void** k
  * the last layer.  Enqueued on the context's stream. */
 int qr_decoder_forward(qr_decoder* dec, int token, int pos, float* logits, float* x_out);
 
+/* Prompt prefill and speculative verification (prefill_runtime,
+ * src/runtime.c:294-304, which calls forward_runtime once per token; the
+ * verify loop of src/speculative.c:107-140 does the same): tokens[0..n) (a
+ * host array) at positions pos0 .. pos0 + n - 1, in chunks of `chunk` tokens
+ * (0: QR_PREFILL_CHUNK; at most QR_PREFILL_MAX_CHUNK).  Each chunk goes
+ * through every layer at once: the projections as multi-row int8 MFMA
+ * products, RoPE and the cache stores for all its positions, attention with
+ * one query per token (each over the positions up to its own), the MoE layer
+ * at T tokens.  The cache rows of every position are written; logits
+ * (optional, device) receive the last token's [vocab] logits, or with
+ * QR_PREFILL_ALL_LOGITS every token's [n][vocab]; x_out (optional) the last
+ * token's residual.  Every result equals n calls of qr_decoder_forward bit
+ * for bit.  Allocates a workspace on first use (not under stream capture);
+ * enqueued on the context stream. */
+#define QR_PREFILL_ALL_LOGITS 1
+#define QR_PREFILL_CHUNK 128
+#define QR_PREFILL_MAX_CHUNK 1024
+int qr_decoder_prefill(qr_decoder* dec, const int32_t* tokens, int n, int pos0, int chunk,
+                       float* logits, float* x_out, int flags);
+
 /* ---- GGUF files (src/gguf.c, src/model.c:253-449) ----------------------- */
 
 /* A parsed GGUF container.  qr_gguf_parse reads a buffer the caller keeps

@@ -77,11 +77,13 @@ __global__ __launch_bounds__(256) void k_dequant_rows(const uint8_t* __restrict_
   }
 }
 
-// The embedding row of the state's token (src/runtime.c:108-113).
+// The embedding row of the state's token (src/runtime.c:108-113); workgroup
+// t takes token t of a batch (state st[2 t], row x + t n).
 __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ tab, int type,
                                                size_t row_bytes, const int32_t* __restrict__ st,
                                                int n, float* __restrict__ x) {
-  const int token = st[0];
+  const int token = st[2 * blockIdx.x];
+  x += (size_t)blockIdx.x * n;
   const uint8_t* row = tab + (size_t)token * row_bytes;
   for (int e = threadIdx.x; e < n; e += blockDim.x) x[e] = deq_elem(row, type, e);
 }
@@ -116,6 +118,7 @@ __device__ inline float seq_sum_lds(const float* __restrict__ p, int n) {
 // residual of src/runtime.c:196-198).  Every thread loads its share of x (and
 // add, w) at once, the squares go to LDS, lane 0 adds them in order, the
 // workgroup scales from registers.  n <= kNormMax; VEC: n % 4 == 0.
+// Workgroup r normalizes row r of a batch (x, add, o advanced by r n).
 // ---------------------------------------------------------------------------
 constexpr int kNormMax = 8192;
 constexpr int kNormThreads = 512;
@@ -128,6 +131,9 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ x,
                                                           float* __restrict__ o) {
   __shared__ __align__(16) float sq[kNormMax];
   __shared__ float scale_s;
+  x += (size_t)blockIdx.x * n;
+  o += (size_t)blockIdx.x * n;
+  if (add) add += (size_t)blockIdx.x * n;
   if constexpr (VEC) {
     const int n4 = n >> 2;
     float4* x4 = reinterpret_cast<float4*>(x);
@@ -202,14 +208,14 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ x,
 }
 
 hipError_t rmsnorm_launch(float* x, const float* add, const float* w, int n, float* o,
-                          hipStream_t s) {
+                          hipStream_t s, int rows = 1) {
   const bool vec = (n & 3) == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
                                      reinterpret_cast<uintptr_t>(o) |
                                      reinterpret_cast<uintptr_t>(add)) & 15) == 0;
   if (vec)
-    hipLaunchKernelGGL(k_rmsnorm<true>, dim3(1), dim3(kNormThreads), 0, s, x, add, w, n, o);
+    hipLaunchKernelGGL(k_rmsnorm<true>, dim3(rows), dim3(kNormThreads), 0, s, x, add, w, n, o);
   else
-    hipLaunchKernelGGL(k_rmsnorm<false>, dim3(1), dim3(kNormThreads), 0, s, x, add, w, n, o);
+    hipLaunchKernelGGL(k_rmsnorm<false>, dim3(rows), dim3(kNormThreads), 0, s, x, add, w, n, o);
   return hipGetLastError();
 }
 
@@ -255,14 +261,18 @@ __device__ inline int npos_of(const int32_t* st, int npos) { return st ? st[1] +
 // One thread per q pair (threads 0 .. qd/2 - 1), then one per 32-element
 // block of k and of v (2 kvd / 32 threads): k's pairs rotate in registers,
 // then the block is stored as fp32 or as a quantize_row_q8_0 block.  grid
-// ceil((qd / 2 + 2 kvd / 32) / 256).
+// (ceil((qd / 2 + 2 kvd / 32) / 256), tokens): blockIdx.y takes token t of a
+// batch (q + t qd, k and v + t kvd, state st[2 t]).
 __global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ q, const float* __restrict__ k,
                                                  const float* __restrict__ v,
                                                  const float* __restrict__ rope,
                                                  const int32_t* __restrict__ st, int qd, int kvd,
                                                  KvView K, uint8_t* __restrict__ vbase) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
-  const int pos = st[1];
+  q += (size_t)blockIdx.y * qd;
+  k += (size_t)blockIdx.y * kvd;
+  v += (size_t)blockIdx.y * kvd;
+  const int pos = st[2 * blockIdx.y + 1];
   const float* cs = rope + (size_t)pos * qd;
   const int np = qd >> 1, nb = kvd >> 5;
   if (g < np) {
@@ -358,6 +368,11 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
                                                      int kv_mul, int hd, float inv_sqrt,
                                                      int att_stride, float* __restrict__ att) {
   extern __shared__ __align__(16) float sm[];
+  // blockIdx.z: token t of a batch (q + t n_heads hd, att + t n_heads att_stride, st + 2 t)
+  const int nh = gridDim.y * kv_mul;
+  q += (size_t)blockIdx.z * nh * hd;
+  att += (size_t)blockIdx.z * nh * att_stride;
+  if (st) st += 2 * blockIdx.z;
   const int npos = npos_of(st, npos_arg);
   const int t0 = blockIdx.x * kScTile;
   if (t0 >= npos) return;
@@ -556,6 +571,10 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_sv(const float* __restrict_
   __shared__ __align__(16) float prod[2][kValCols * kValPitch];
   __shared__ float red[kSvThreads / 64];
   __shared__ float inv_s;
+  // blockIdx.z: token t of a batch (att + t n_heads att_stride, out + t n_heads hd, st + 2 t)
+  att += (size_t)blockIdx.z * gridDim.y * att_stride;
+  out += (size_t)blockIdx.z * gridDim.y * hd;
+  if (st) st += 2 * blockIdx.z;
   const int npos = npos_of(st, npos_arg);
   int32_t* pt = reinterpret_cast<int32_t*>(e + lds_cap);
   for (int i = threadIdx.x; i < (npos + V.page - 1) / V.page; i += kSvThreads) pt[i] = V.ptab[i];
@@ -654,6 +673,112 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_sv(const float* __restrict_
   if (wave == 0 && lane < kValCols) out[(size_t)h * hd + c0 + lane] = acc;
 }
 
+// The same attention values for a prompt chunk: many queries (tokens) over
+// contexts that are short at first.  Workgroup (head blockIdx.x, token
+// blockIdx.y of a batch: att + (t n_heads + h) att_stride, out + (t n_heads +
+// h) hd, state st[2 t]); lane c < hd owns output column c and runs its chain
+// over the positions itself, reading V straight from the cache (the rows of
+// a kv head are shared by its query heads and by the chunk's tokens, so they
+// come from L2).  softmax_ref as in k_attn_sv: the max over the workgroup,
+// the exponentials in parallel, lane 0 adds them in order; then each
+// position's weight e_t * inv once into LDS.  o[c] = sum over t in order of
+// (e_t * inv) * v_t[c], each product rounded, then added.  Dynamic LDS:
+// lds_cap floats, then the page table.
+template <int KVT>
+__global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ att,
+                                                      int att_stride, KvView V,
+                                                      const int32_t* __restrict__ st, int lds_cap,
+                                                      int kv_mul, int hd, float* __restrict__ out) {
+  extern __shared__ __align__(16) float e[];
+  __shared__ float red[8];
+  __shared__ float inv_s;
+  const int nh = gridDim.x, h = blockIdx.x, z = blockIdx.y;
+  att += ((size_t)z * nh + h) * att_stride;
+  out += ((size_t)z * nh + h) * hd;
+  const int npos = st[2 * z + 1] + 1;
+  const int nthr = blockDim.x, tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  int32_t* pt = reinterpret_cast<int32_t*>(e + lds_cap);
+  for (int i = tid; i < (npos + V.page - 1) / V.page; i += nthr) pt[i] = V.ptab[i];
+  const ExpTab tab = qr_expf_tab();
+  float mx = att[0];
+  for (int i = tid; i < npos; i += nthr) {
+    const float v = att[i];
+    e[i] = v;
+    mx = v > mx ? v : mx;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v = __shfl_xor(mx, o);
+    mx = v > mx ? v : mx;
+  }
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (int w = 1; w < (nthr >> 6); w++) mx = red[w] > mx ? red[w] : mx;
+  // every lane runs the same number of rounds (qr_expf_w reads other lanes)
+  const int rounds = (npos + nthr - 1) / nthr;
+  for (int r = 0; r < rounds; r++) {
+    const int i = r * nthr + tid;
+    const float v = i < npos ? e[i] : 0.0f;
+    const float ev = qr_expf_w(v - mx, tab);
+    if (i < npos) e[i] = ev;
+  }
+  __syncthreads();
+  if (tid == 0) inv_s = 1.0f / seq_sum_lds(e, npos);
+  __syncthreads();
+  const float inv = inv_s;
+  for (int i = tid; i < npos; i += nthr) e[i] = e[i] * inv;  // softmax_ref's x[i] *= inv
+  __syncthreads();
+  if (tid >= hd) return;
+  const int col = (h / kv_mul) * hd + tid;
+  float acc = 0.0f;
+  constexpr int U = 8;  // positions whose values are loaded ahead of their adds
+  int t = 0;
+  for (; t + U <= npos; t += U) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const uint8_t* row = kv_row_lds(V, pt, t + u);
+      if constexpr (KVT == QR_KV_Q8_0) {
+        const uint8_t* blk = row + (size_t)(col >> 5) * QR_Q8_BYTES;
+        const float d = qr_h2f(*reinterpret_cast<const uint16_t*>(blk));
+        v[u] = (float)(int8_t)blk[2 + (col & 31)] * d;
+      } else {
+        v[u] = reinterpret_cast<const float*>(row)[col];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) acc += e[t + u] * v[u];
+  }
+  for (; t < npos; t++) {
+    const uint8_t* row = kv_row_lds(V, pt, t);
+    float v;
+    if constexpr (KVT == QR_KV_Q8_0) {
+      const uint8_t* blk = row + (size_t)(col >> 5) * QR_Q8_BYTES;
+      v = (float)(int8_t)blk[2 + (col & 31)] * qr_h2f(*reinterpret_cast<const uint16_t*>(blk));
+    } else {
+      v = reinterpret_cast<const float*>(row)[col];
+    }
+    acc += e[t] * v;
+  }
+  out[tid] = acc;
+}
+
+hipError_t sv_rows_launch(const float* att, int att_stride, const KvView& V, const int32_t* st,
+                          int lds_cap, int n_heads, int kv_mul, int hd, float* out, int tokens,
+                          hipStream_t s) {
+  const dim3 grid(n_heads, tokens);
+  const int threads = ((hd + 63) / 64) * 64;
+  const size_t lds = (size_t)lds_cap * 4 + (size_t)((lds_cap + V.page - 1) / V.page) * 4;
+  if (V.kv_type == QR_KV_Q8_0)
+    hipLaunchKernelGGL(k_attn_sv_rows<QR_KV_Q8_0>, grid, dim3(threads), lds, s, att, att_stride, V,
+                       st, lds_cap, kv_mul, hd, out);
+  else
+    hipLaunchKernelGGL(k_attn_sv_rows<QR_KV_F32>, grid, dim3(threads), lds, s, att, att_stride, V,
+                       st, lds_cap, kv_mul, hd, out);
+  return hipGetLastError();
+}
+
 // k_attn_sv's dynamic LDS for a cache of cap positions in pages of `page`,
 // and whether it fits beside the kernel's static LDS.
 inline size_t sv_lds_bytes(int cap, int page) {
@@ -661,8 +786,8 @@ inline size_t sv_lds_bytes(int cap, int page) {
 }
 hipError_t sv_launch(const float* att, int att_stride, const KvView& V, const int32_t* st,
                      int npos, int lds_cap, int n_heads, int kv_mul, int hd, float* out,
-                     hipStream_t s) {
-  const dim3 grid(hd / kValCols, n_heads);
+                     hipStream_t s, int tokens = 1) {
+  const dim3 grid(hd / kValCols, n_heads, tokens);
   const size_t lds = sv_lds_bytes(lds_cap, V.page);
   if (V.kv_type == QR_KV_Q8_0)
     hipLaunchKernelGGL(k_attn_sv<QR_KV_Q8_0>, grid, dim3(kSvThreads), lds, s, att, att_stride, V,
@@ -715,6 +840,17 @@ struct qr_decoder {
   float* graph_logits = nullptr;
   float* graph_xout = nullptr;
   int calls = 0;
+  // prefill workspace (the first qr_decoder_prefill allocates it): chunk
+  // activations of up to pcap tokens, the prompt's states, MFMA records and
+  // dispatch lists, MoE scratch
+  void* pmem = nullptr;
+  int pcap = 0;
+  float *px = nullptr, *pxb = nullptr, *pxb2 = nullptr, *pq = nullptr, *pk = nullptr;
+  float *pv = nullptr, *pao = nullptr, *patt = nullptr;
+  int32_t* pst = nullptr;   // [cap][2]: token, position of every prompt position
+  uint8_t* prec = nullptr;  // activation records [pcap][max(dim, q_dim) / 32]
+  int32_t *poff = nullptr, *pperm = nullptr, *ptiles = nullptr;
+  uint8_t* pmoe = nullptr;
 };
 
 namespace {
@@ -722,6 +858,8 @@ namespace {
 std::atomic<bool> g_sc_opt[64];
 std::atomic<bool> g_sm_opt[64];
 std::atomic<bool> g_sm_opt2[64];
+std::atomic<bool> g_rows_opt[64];
+std::atomic<bool> g_rows_opt2[64];
 
 #define DEC_HIP(call, what)                                                        \
   do {                                                                             \
@@ -792,6 +930,93 @@ hipError_t enqueue_step(qr_decoder* d, float* logits, float* xout, hipStream_t s
     return e;
   if (xout) {
     if ((e = hipMemcpyAsync(xout, d->x, (size_t)dim * 4, hipMemcpyDeviceToDevice, s))) return e;
+  }
+  return hipSuccess;
+}
+
+// A single-"expert" dispatch of T rows for the grouped MFMA product:
+// offsets {0, T}, the identity permutation, tiles {0, ceil(T / tile)}.
+__global__ __launch_bounds__(256) void k_rows_dispatch(int T, int tile, int32_t* off,
+                                                       int32_t* perm, int32_t* tiles) {
+  for (int i = threadIdx.x; i < T; i += blockDim.x) perm[i] = i;
+  if (threadIdx.x == 0) {
+    off[0] = 0;
+    off[1] = T;
+    tiles[0] = 0;
+    tiles[1] = (T + tile - 1) / tile;
+  }
+}
+
+// y[t][.] = W x[t] for T rows of x (a prompt chunk), each row exactly as
+// matmul_q_dev computes it for one token: fp32 weights through the build's
+// order with all T rows at once; K-quant (row-major or tiled) and C99-order
+// Q8_0 weights as one grouped int8 MFMA product (qr_moe_mfma.hip, the rows
+// dispatched to a single "expert"), whose per-row terms and order are the
+// fused dot's; Q8_0 in a lane order through the GEMV, four rows per launch.
+hipError_t matmul_rows_dev(qr_decoder* d, const void* w, uint32_t type, const float* x, float* y,
+                           int n, int dd, int T, hipStream_t s) {
+  hipError_t e;
+  if (type == QR_T_F32)
+    return gemv_f32_launch(d->order, static_cast<const float*>(w), x, y, n, dd, T, dd, n, s);
+  const bool tiled = (type & QR_TILED) != 0;
+  const uint32_t base = type & ~(uint32_t)QR_TILED;
+  const bool lanes = base == QR_T_Q8_0 && d->order != QR_ORDER_SEQ;
+  if (!lanes && T >= 2 && mfma_type_ok((int)base) && dd % 256 == 0 && (dd >> 8) <= 64) {
+    const int tile = T >= 32 ? 32 : 16;
+    if ((e = quant_rows_launch(x, dd, T, dd, base != QR_T_Q8_0, d->prec, s))) return e;
+    hipLaunchKernelGGL(k_rows_dispatch, dim3(1), dim3(256), 0, s, T, tile, d->poff, d->pperm,
+                       d->ptiles);
+    if ((e = hipGetLastError())) return e;
+    const size_t slice = qr_wrow_bytes((int)base, dd) * (size_t)n;
+    return expert_mfma_launch((int)base, false, static_cast<const uint8_t*>(w), nullptr, slice, 1,
+                              1, n, dd, d->prec, 1, d->poff, d->pperm, d->ptiles, y, n,
+                              (T + tile - 1) / tile + 1, tile, nullptr, false, s, tiled);
+  }
+  for (int t0 = 0; t0 < T; t0 += 4) {
+    const int nt = T - t0 < 4 ? T - t0 : 4;
+    if (tiled)
+      e = gemv_tiled_launch((int)base, w, x + (size_t)t0 * dd, y + (size_t)t0 * n, n, dd, nt, dd, n,
+                            s);
+    else
+      e = gemv_launch((int)base, d->order, w, x + (size_t)t0 * dd, y + (size_t)t0 * n, n, dd, nt,
+                      dd, n, nullptr, nullptr, s);
+    if (e) return e;
+  }
+  return hipSuccess;
+}
+
+// One prompt chunk of T tokens (states st[2 T]) through every layer: the
+// decode step's kernels with a token dimension, the projections as T-row
+// products, the MoE layer at T tokens.  Leaves the chunk's residuals in px.
+hipError_t enqueue_prefill_chunk(qr_decoder* d, int T, const int32_t* st, hipStream_t s) {
+  hipError_t e;
+  const int dim = d->dim;
+  hipLaunchKernelGGL(k_embed, dim3(T), dim3(256), 0, s, static_cast<const uint8_t*>(d->tok_embd),
+                     (int)d->tok_type, d->tok_row, st, dim, d->px);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const float inv_sqrt = 1.0f / sqrtf((float)d->hd);
+  for (int l = 0; l < d->nl; l++) {
+    const qr_layer& L = d->layers[l];
+    if ((e = rmsnorm_launch(d->px, nullptr, L.rms_att, dim, d->pxb, s, T))) return e;
+    if ((e = matmul_rows_dev(d, L.wq, L.wq_type, d->pxb, d->pq, d->qd, dim, T, s))) return e;
+    if ((e = matmul_rows_dev(d, L.wk, L.wk_type, d->pxb, d->pk, d->kvd, dim, T, s))) return e;
+    if ((e = matmul_rows_dev(d, L.wv, L.wv_type, d->pxb, d->pv, d->kvd, dim, T, s))) return e;
+    const KvView K = kv_view(d, l, false), V = kv_view(d, l, true);
+    hipLaunchKernelGGL(k_rope_kv, dim3((d->qd / 2 + 2 * (d->kvd / 32) + 255) / 256, T), dim3(256),
+                       0, s, d->pq, d->pk, d->pv, d->rope, st, d->qd, d->kvd, K,
+                       const_cast<uint8_t*>(V.base));
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_scores, dim3((d->cap + kScTile - 1) / kScTile, d->nkv, T), dim3(256),
+                       d->sc_lds, s, d->pq, K, st, 0, d->kv_mul, d->hd, inv_sqrt, d->cap, d->patt);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = sv_rows_launch(d->patt, d->cap, V, st, d->cap, d->nh, d->kv_mul, d->hd, d->pao, T,
+                            s)))
+      return e;
+    if ((e = matmul_rows_dev(d, L.wo, L.wo_type, d->pao, d->pxb2, dim, d->qd, T, s))) return e;
+    if ((e = rmsnorm_launch(d->px, d->pxb2, L.rms_ffn, dim, d->pxb, s, T))) return e;
+    MoeScratch ms;
+    moe_scratch_carve(d->pmoe, &L.moe, T, &ms);
+    if ((e = moe_forward_launch(&L.moe, d->px, d->pxb, T, d->order, ms, s))) return e;
   }
   return hipSuccess;
 }
@@ -967,6 +1192,8 @@ int qr_decoder_create(qr_ctx* c, const qr_model* m, int kv_type, int order, int 
   DEC_HIP(lds_opt_in((const void*)k_attn_scores, g_sc_opt), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_Q8_0>, g_sm_opt), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_F32>, g_sm_opt2), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_sv_rows<QR_KV_Q8_0>, g_rows_opt), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_sv_rows<QR_KV_F32>, g_rows_opt2), "lds opt-in");
   qr_decoder* d = new (std::nothrow) qr_decoder();
   if (!d) return set_error(QR_ERR_NOMEM, "qr_decoder_create: host allocation");
   d->ctx = c;
@@ -1069,6 +1296,7 @@ int qr_decoder_destroy(qr_decoder* d) {
   if (d->kc) (void)hipFree(d->kc);
   if (d->vc) (void)hipFree(d->vc);
   if (d->mem) (void)hipFree(d->mem);
+  if (d->pmem) (void)hipFree(d->pmem);
   delete d;
   return QR_OK;
 }
@@ -1132,6 +1360,118 @@ int qr_decoder_kv_rows(const qr_decoder* d, int layer, int pos, const void** kro
                      ((size_t)pp * d->page + (size_t)(pos % d->page)) * d->row_bytes;
   *krow = d->kc + off;
   *vrow = d->vc + off;
+  return QR_OK;
+}
+
+
+// The prefill workspace for chunks of up to `chunk` tokens.
+static int prefill_workspace(qr_decoder* d, int chunk) {
+  if (d->pmem && d->pcap >= chunk) return QR_OK;
+  if (d->pmem) {
+    (void)hipStreamSynchronize(ctx_stream(d->ctx));
+    (void)hipFree(d->pmem);
+    d->pmem = nullptr;
+    d->pcap = 0;
+  }
+  auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  const size_t T = (size_t)chunk;
+  size_t moe_bytes = 0;
+  for (int l = 0; l < d->nl; l++) {
+    const size_t b = moe_scratch_bytes(&d->layers[l].moe, chunk);
+    if (b > moe_bytes) moe_bytes = b;
+  }
+  const int wide = d->qd > d->dim ? d->qd : d->dim;
+  const size_t o_x = 0, o_xb = o_x + up(T * d->dim * 4), o_xb2 = o_xb + up(T * d->dim * 4);
+  const size_t o_q = o_xb2 + up(T * d->dim * 4), o_k = o_q + up(T * d->qd * 4);
+  const size_t o_v = o_k + up(T * d->kvd * 4), o_ao = o_v + up(T * d->kvd * 4);
+  const size_t o_att = o_ao + up(T * d->qd * 4);
+  const size_t o_st = o_att + up(T * d->nh * (size_t)d->cap * 4);
+  const size_t o_rec = o_st + up((size_t)d->cap * 8);
+  const size_t o_off = o_rec + up(T * (size_t)(wide / 32) * 48);
+  const size_t o_perm = o_off + 256, o_tiles = o_perm + up(T * 4);
+  const size_t o_moe = o_tiles + 256, total = o_moe + up(moe_bytes);
+  void* p = nullptr;
+  const hipError_t e = hipMalloc(&p, total);
+  if (e != hipSuccess)
+    return set_error(QR_ERR_NOMEM, "qr_decoder_prefill: workspace of %zu bytes: %s", total,
+                     hipGetErrorString(e));
+  uint8_t* b = static_cast<uint8_t*>(p);
+  d->pmem = p;
+  d->pcap = chunk;
+  d->px = reinterpret_cast<float*>(b + o_x);
+  d->pxb = reinterpret_cast<float*>(b + o_xb);
+  d->pxb2 = reinterpret_cast<float*>(b + o_xb2);
+  d->pq = reinterpret_cast<float*>(b + o_q);
+  d->pk = reinterpret_cast<float*>(b + o_k);
+  d->pv = reinterpret_cast<float*>(b + o_v);
+  d->pao = reinterpret_cast<float*>(b + o_ao);
+  d->patt = reinterpret_cast<float*>(b + o_att);
+  d->pst = reinterpret_cast<int32_t*>(b + o_st);
+  d->prec = b + o_rec;
+  d->poff = reinterpret_cast<int32_t*>(b + o_off);
+  d->pperm = reinterpret_cast<int32_t*>(b + o_perm);
+  d->ptiles = reinterpret_cast<int32_t*>(b + o_tiles);
+  d->pmoe = b + o_moe;
+  return QR_OK;
+}
+
+int qr_decoder_prefill(qr_decoder* d, const int32_t* tokens, int n, int pos0, int chunk,
+                       float* logits, float* x_out, int flags) {
+  if (!d || (n > 0 && !tokens)) return set_error(QR_ERR_INVALID, "qr_decoder_prefill: null argument");
+  if (n < 0 || pos0 < 0 || pos0 + n > d->cap)
+    return set_error(QR_ERR_INVALID, "qr_decoder_prefill: positions [%d, %d) of %d", pos0,
+                     pos0 + n, d->cap);
+  if (flags & ~QR_PREFILL_ALL_LOGITS)
+    return set_error(QR_ERR_INVALID, "qr_decoder_prefill: flags %#x", flags);
+  if (chunk < 0 || chunk > QR_PREFILL_MAX_CHUNK)
+    return set_error(QR_ERR_INVALID, "qr_decoder_prefill: chunk %d (1 .. %d, 0 for %d)", chunk,
+                     QR_PREFILL_MAX_CHUNK, QR_PREFILL_CHUNK);
+  if ((logits && !al16(logits)) || (x_out && !al16(x_out)))
+    return set_error(QR_ERR_INVALID, "qr_decoder_prefill: output alignment");
+  for (int i = 0; i < n; i++)
+    if (tokens[i] < 0 || tokens[i] >= d->vocab)
+      return set_error(QR_ERR_INVALID, "qr_decoder_prefill: token %d at %d (vocab %d)", tokens[i],
+                       i, d->vocab);
+  if (n == 0) return QR_OK;
+  if (ctx_capturing(d->ctx))
+    return set_error(QR_ERR_INVALID, "qr_decoder_prefill: not under stream capture");
+  if (chunk == 0) chunk = QR_PREFILL_CHUNK;
+  if (chunk > n) chunk = n;
+  DEC_HIP(hipSetDevice(d->device), "hipSetDevice");
+  int rc = prefill_workspace(d, chunk);
+  if (rc) return rc;
+  hipStream_t s = ctx_stream(d->ctx);
+  // every prompt position's (token, position), uploaded once
+  std::vector<int32_t> st((size_t)2 * n);
+  for (int i = 0; i < n; i++) {
+    st[2 * (size_t)i] = tokens[i];
+    st[2 * (size_t)i + 1] = pos0 + i;
+  }
+  DEC_HIP(hipMemcpyAsync(d->pst, st.data(), st.size() * 4, hipMemcpyHostToDevice, s),
+          "prefill state upload");
+  DEC_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
+  const int dim = d->dim;
+  for (int c0 = 0; c0 < n; c0 += chunk) {
+    const int T = n - c0 < chunk ? n - c0 : chunk;
+    DEC_HIP(enqueue_prefill_chunk(d, T, d->pst + 2 * (size_t)c0, s), "prefill chunk");
+    const bool last = c0 + T == n;
+    if (logits && (flags & QR_PREFILL_ALL_LOGITS)) {
+      // final norm of every row (x itself is left as is), then the lm_head rows
+      DEC_HIP(rmsnorm_launch(d->px, nullptr, d->rms_final, dim, d->pxb, s, T), "k_rmsnorm");
+      DEC_HIP(matmul_rows_dev(d, d->wcls, d->wcls_type, d->pxb, logits + (size_t)c0 * d->vocab,
+                              d->vocab, dim, T, s),
+              "lm_head");
+    } else if (logits && last) {
+      float* xl = d->px + (size_t)(T - 1) * dim;
+      DEC_HIP(rmsnorm_launch(xl, nullptr, d->rms_final, dim, d->pxb, s), "k_rmsnorm");
+      DEC_HIP(matmul_q_dev(d->wcls, d->wcls_type, d->order, d->pxb, logits, d->vocab, dim, s),
+              "lm_head");
+    }
+    if (last && x_out)
+      DEC_HIP(hipMemcpyAsync(x_out, d->px + (size_t)(T - 1) * dim, (size_t)dim * 4,
+                             hipMemcpyDeviceToDevice, s),
+              "x_out copy");
+  }
   return QR_OK;
 }
 

@@ -498,4 +498,20 @@ __device__ inline void unit_to_slots(const uint8_t* __restrict__ wrow, int row_l
   }
 }
 
+// Arguments of the GEMV kernels (qr_gemv.hip, qr_tiled.h).
+struct GemvArgs {
+  const uint8_t* W;      // [n][row_bytes], 16-byte aligned
+  const float* X;        // [nt][xstride]
+  float* Y;              // [nt][ystride]
+  int n, d;
+  int xstride, ystride;
+  int rows_per_wg;
+  int32_t* acc;          // optional [nt][n][units] int32 unit sums
+  int32_t* accb;         // optional [nt][units] activation block sums
+  // tiled layout (qr_tiled.h): super-blocks per row, rows per full tile,
+  // tiles, bytes of a full tile -- set on the host
+  int t_nb, t_rb, t_ntiles;
+  size_t t_tile_bytes;
+};
+
 }  // namespace qr

@@ -18,30 +18,12 @@
 #include "qr_internal.h"
 #include "qr_stream.h"
 #include "qr_blk.h"
+#include "qr_tiled.h"
 
 namespace qr {
 
 constexpr int kWg = 256;
 
-struct GemvArgs {
-  const uint8_t* W;      // [n][row_bytes], 16-byte aligned
-  const float* X;        // [nt][xstride]
-  float* Y;              // [nt][ystride]
-  int n, d;
-  int xstride, ystride;
-  int rows_per_wg;
-  int32_t* acc;          // optional [nt][n][units] int32 unit sums
-  int32_t* accb;         // optional [nt][units] activation block sums
-  // tiled layout (qr_tiled.h): super-blocks per row, rows per full tile,
-  // tiles, bytes of a full tile -- set on the host
-  int t_nb, t_rb, t_ntiles;
-  size_t t_tile_bytes;
-};
-}  // namespace qr
-
-#include "qr_tiled.h"
-
-namespace qr {
 
 // LDS layout: act q | act bd | act bs | terms | staged tile.  Terms are
 // [nt][R][slots][U + 1] floats (slots: q8_slots).

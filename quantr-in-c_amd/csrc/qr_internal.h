@@ -112,6 +112,6 @@ hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const ui
                               size_t slice, int E, int K, int rows, int cols, const uint8_t* XQ,
                               int x_by_token, const int32_t* offsets, const int32_t* perm,
                               const int32_t* tiles, float* Y, int ystride, int items, int tile,
-                              uint8_t* QO, bool qperm, hipStream_t st);
+                              uint8_t* QO, bool qperm, hipStream_t st, bool tiled = false);
 
 }  // namespace qr

@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "qr_blk.h"
+#include "qr_tiled.h"
 #include "qr_tokens.h"
 #include "qr_internal.h"
 
@@ -161,6 +162,10 @@ struct MfmaArgs {
   int qperm;
   int skinny;             // work items of at most 4 pairs take the skinny form
   int wnt;                // weight DMA with the non-temporal hint (weights read about once)
+  // Q4_K / Q5_K weights in the tiled layout (qr_tiled.h): rows per tile and
+  // bytes per full tile; 0 for the row-major layout
+  int t_rb;
+  size_t t_tile_bytes;
 };
 
 template <int TYPE, bool GATEUP, int NJ, int RA, int D, int NW>
@@ -247,6 +252,7 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
   const uint8_t* wbase[G::WI];  // the chunk's matrix, at the expert's slice
   uint32_t wroff[G::WI];        // its row's offset in the slice, or ~0 (no row)
   int wch[G::WI];
+  int wrow[G::WI];              // its row, or -1
 #pragma unroll
   for (int k = 0; k < G::WI; k++) {
     const int c = k * 64 + lane;
@@ -256,6 +262,7 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
     wch[k] = rem - rr * NCH;
     const int row = rw0 + rr;
     wroff[k] = (c < G::WCH && row < a.rows) ? (uint32_t)row * (uint32_t)rb : ~0u;
+    wrow[k] = (c < G::WCH && row < a.rows) ? row : -1;
     wbase[k] = ((GATEUP && m == 1) ? a.W2 : a.W1) + ebase;
   }
   // Activation chunk c = (wave AI + k) 64 + lane: pair c / APC, chunk c % APC
@@ -280,10 +287,25 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
   constexpr bool ALN = TYPE == QR_T_Q4_K || TYPE == QR_T_Q5_K;
   const uint8_t* wp[G::WI];
   const uint8_t* ap[G::AI];
+  // In the tiled layout the stage's chunk ch of row r is chunk ch of lane
+  // (r % RB) nb + stage of tile r / RB: tile start + 16 (ch L + lane), L the
+  // tile's lanes, so a stage advances the address by 16 bytes instead of a
+  // super-block.
   if constexpr (ALN) {
+    const int nbk = a.cols >> 8;
 #pragma unroll
-    for (int k = 0; k < G::WI; k++)
-      wp[k] = wroff[k] != ~0u ? wbase[k] + wroff[k] + 16 * wch[k] : a.W1 + ebase + row0;
+    for (int k = 0; k < G::WI; k++) {
+      if (wroff[k] == ~0u) {
+        wp[k] = a.t_rb ? a.W1 + ebase : a.W1 + ebase + row0;
+      } else if (a.t_rb) {
+        const int r = wrow[k], t = r / a.t_rb;
+        const int L = min(a.t_rb, a.rows - t * a.t_rb) * nbk;
+        wp[k] = wbase[k] + (size_t)t * a.t_tile_bytes + (size_t)16 * wch[k] * L +
+                (size_t)16 * (r - t * a.t_rb) * nbk;
+      } else {
+        wp[k] = wbase[k] + wroff[k] + 16 * wch[k];
+      }
+    }
 #pragma unroll
     for (int k = 0; k < G::AI; k++) ap[k] = a.XQ + (asrc[k] != ~(size_t)0 ? asrc[k] : asrc0);
   }
@@ -296,7 +318,7 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
 #pragma unroll
       for (int k = 0; k < G::AI; k++) lds_dma16(ap[k] + ao, abase + (uint32_t)(k * 1024));
       const uint32_t wlds = lds_u32addr(smem + G::O_W + (wave * D + slot) * G::WST);
-      const uint32_t s0 = (uint32_t)st * KST;
+      const uint32_t s0 = (uint32_t)st * (a.t_rb ? 16u : (uint32_t)KST);
       if (a.wnt) {
 #pragma unroll
         for (int k = 0; k < G::WI; k++) lds_dma16_nt(wp[k] + s0, wlds + (uint32_t)(k * 1024));
@@ -619,7 +641,7 @@ hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const ui
                               size_t slice, int E, int K, int rows, int cols, const uint8_t* XQ,
                               int x_by_token, const int32_t* offsets, const int32_t* perm,
                               const int32_t* tiles, float* Y, int ystride, int items, int tile,
-                              uint8_t* QO, bool qperm, hipStream_t st) {
+                              uint8_t* QO, bool qperm, hipStream_t st, bool tiled) {
   if (tile != 16 && tile != 32) return hipErrorInvalidValue;
   if (slice >= ((size_t)1 << 32)) return hipErrorInvalidValue;  // 32-bit offsets in a slice
   if (QO && (!gateup || (rows & 31) || (reinterpret_cast<uintptr_t>(QO) & 15)))
@@ -645,6 +667,15 @@ hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const ui
   a.QO = QO;
   a.qperm = qperm ? 1 : 0;
   a.skinny = 1;
+  a.t_rb = 0;
+  a.t_tile_bytes = 0;
+  if (tiled) {  // Q4_K / Q5_K rows of whole super-blocks, at most 64 per row
+    if ((type != QR_T_Q4_K && type != QR_T_Q5_K) || (cols & 255) || (cols >> 8) > 64)
+      return hipErrorInvalidValue;
+    const TiledGeom tg = tiled_geom(type, rows, cols);
+    a.t_rb = tg.RB;
+    a.t_tile_bytes = tg.tile_bytes;
+  }
   // items of up to 16 pairs: an expert rarely has more than one, so its rows
   // are read about once and the hint keeps the activation records cached;
   // with 32-pair items hot experts are re-read by several items

@@ -61,6 +61,7 @@ class Model(C.Structure):
 KV_F32, KV_Q8_0 = 0, 2
 MOE_PATH_AUTO, MOE_PATH_GEMV, MOE_PATH_MFMA = 0, 1, 2
 DEC_GRAPH = 1
+PREFILL_ALL_LOGITS = 1
 
 _SIGS = {
     "qr_last_error": (C.c_char_p, []),
@@ -121,6 +122,8 @@ _SIGS = {
     "qr_decoder_kv_write": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "qr_decoder_kv_rows": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(_vp), C.POINTER(_vp)]),
     "qr_decoder_forward": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp]),
+    "qr_decoder_prefill": (C.c_int, [_vp, C.POINTER(C.c_int32), C.c_int, C.c_int, C.c_int, _vp, _vp,
+                                     C.c_int]),
     "qr_gguf_parse": (C.c_int, [_vp, C.c_size_t, C.POINTER(_vp)]),
     "qr_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
     "qr_gguf_close": (C.c_int, [_vp]),
@@ -392,6 +395,14 @@ class Decoder:
         self.dev._check(self.dev.lib.qr_decoder_forward(_vp(self.h), token, pos,
                                                         _vp(logits_ptr), _vp(x_ptr)),
                         "qr_decoder_forward")
+
+    def prefill(self, tokens, pos0, logits_ptr=None, x_ptr=None, chunk=0, all_logits=False):
+        """qr_decoder_prefill: tokens at positions pos0 .. pos0 + len - 1."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        self.dev._check(self.dev.lib.qr_decoder_prefill(
+            _vp(self.h), t.ctypes.data_as(C.POINTER(C.c_int32)), len(t), pos0, chunk,
+            _vp(logits_ptr), _vp(x_ptr), PREFILL_ALL_LOGITS if all_logits else 0),
+            "qr_decoder_prefill")
 
     def close(self):
         if self.h is not None:

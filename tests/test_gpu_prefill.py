@@ -1,0 +1,147 @@
+"""GPU parity of the batched prompt prefill / speculative verify
+(qr_decoder_prefill; prefill_runtime, src/runtime.c:294-304, and the verify
+loop of src/speculative.c:107-140 both call forward_runtime once per token).
+
+- The two decode.npz models: the whole token sequence in one call (and in
+  chunks of 3 and of 1) gives the reference's own logits for every position
+  and its last residual, bit for bit, in every build.
+- A prefill followed by single-token steps continues exactly as the
+  sequential decode does.
+- A Qwen3-like head shape over a Q8_0 cache in permuted pages of 64: 300
+  prompt tokens in chunks of 128 (the MFMA row products, three chunks) give the
+  logits, residual and cache rows of 300 sequential decode steps, bit for bit;
+  also with the projections stored tiled (GGUF load).
+"""
+import numpy as np
+import pytest
+
+import gguf_writer as G
+import inputs as I
+import quantr_amd as Q
+from conftest import assert_bits_equal
+from oracle import ORDER_AVX2, ORDER_AVX512, ORDER_SEQ
+
+pytestmark = pytest.mark.gpu
+
+BUILDS = {"c99": ORDER_SEQ, "avx2": ORDER_AVX2, "avx512": ORDER_AVX512}
+
+
+def make_decoder(dev, m, kv_type, order, page=0, flags=0):
+    model, layers, keep = Q.upload_decode_model(dev, m)
+    d = Q.Decoder(dev, model, layers, kv_type=kv_type, order=order, page=page, flags=flags)
+    d._keep = keep
+    return d
+
+
+def sequential(dev, d, m, tokens, pos0=0):
+    lg_d, x_d = dev.alloc(4 * m["vocab"]), dev.alloc(4 * m["dim"])
+    lg = np.zeros((len(tokens), m["vocab"]), np.float32)
+    for i, t in enumerate(tokens):
+        d.forward(int(t), pos0 + i, lg_d.ptr, x_d.ptr)
+        lg[i] = dev.download(lg_d, m["vocab"], np.float32)
+    return lg, dev.download(x_d, m["dim"], np.float32)
+
+
+def prefill(dev, d, m, tokens, pos0=0, chunk=0):
+    n = len(tokens)
+    lg_d, x_d = dev.alloc(4 * m["vocab"] * n), dev.alloc(4 * m["dim"])
+    d.prefill(tokens, pos0, lg_d.ptr, x_d.ptr, chunk=chunk, all_logits=True)
+    return (dev.download(lg_d, (n, m["vocab"]), np.float32),
+            dev.download(x_d, m["dim"], np.float32))
+
+
+@pytest.mark.parametrize("chunk", [0, 3, 1])
+@pytest.mark.parametrize("build", list(BUILDS))
+@pytest.mark.parametrize("name", list(I.DECODE_CASES))
+def test_prefill_matches_reference_logits(dev, golden, name, build, chunk):
+    g = golden("decode.npz")
+    m = I.decode_model(name)
+    key = "logits_%s_%s" % (name, build)
+    if key not in g:
+        pytest.skip("fixture written without an -mavx512f build")
+    print("prefill case %s build %s chunk %d" % (name, build, chunk), flush=True)
+    d = make_decoder(dev, m, Q.KV_F32, BUILDS[build])
+    lg, x = prefill(dev, d, m, m["tokens"], chunk=chunk)
+    d.close()
+    assert_bits_equal(lg, g[key], "prefill logits %s/%s" % (name, build))
+    assert_bits_equal(x, g["x_%s_%s" % (name, build)][-1], "prefill residual")
+
+
+@pytest.mark.parametrize("name", list(I.DECODE_CASES))
+def test_prefill_then_decode(dev, golden, name):
+    """The first tokens by prefill (last logits only), the rest one step at a
+    time: the reference's logits at every following position."""
+    g = golden("decode.npz")
+    m = I.decode_model(name)
+    toks = m["tokens"]
+    k = len(toks) - 2
+    d = make_decoder(dev, m, Q.KV_F32, ORDER_AVX2, flags=Q.DEC_GRAPH)
+    lg_d = dev.alloc(4 * m["vocab"])
+    d.prefill(toks[:k], 0, lg_d.ptr)
+    first = dev.download(lg_d, m["vocab"], np.float32)
+    rest, _ = sequential(dev, d, m, toks[k:], pos0=k)
+    d.close()
+    want = g["logits_%s_avx2" % name]
+    assert_bits_equal(first, want[k - 1], "last prefill logits")
+    assert_bits_equal(rest, want[k:], "decode after prefill")
+
+
+def _kv_rows(dev, d, L, positions, rs):
+    out = []
+    for l in range(L):
+        for t in positions:
+            kr, vr = d.kv_rows(l, t)
+            out.append(dev.download(kr, rs, np.uint8))
+            out.append(dev.download(vr, rs, np.uint8))
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("source", ["pointers", "gguf_tiled"])
+def test_prefill_head128_chunks(dev, source):
+    """300 prompt tokens of a head_dim-128 model (q_dim 1024 != dim 512, GQA
+    4:1) over a Q8_0 cache in permuted pages of 64, prefilled in chunks of 128
+    (the projections as MFMA row products), against 300 sequential decode
+    steps: every token's logits, the last residual and the cache rows."""
+    m = I.qwen3_small_model(n_layers=2, seq_len=320)
+    rng = np.random.default_rng(9)
+    toks = rng.integers(0, m["vocab"], size=300).astype(np.int32)
+    order = ORDER_AVX2
+    ref = make_decoder(dev, m, Q.KV_Q8_0, order, page=64, flags=Q.DEC_GRAPH)
+    ppl, _ = ref.pages()
+    table = np.stack([rng.permutation(ppl) for _ in range(m["n_layers"])]).astype(np.int32)
+    ref.set_pages(table)
+    print("prefill head128 sequential reference", flush=True)
+    want_lg, want_x = sequential(dev, ref, m, toks)
+    rs = Q.load().qr_kv_row_bytes(Q.KV_Q8_0, m["n_kv_heads"] * m["head_dim"])
+    probe = [0, 63, 64, 127, 128, 200, 299]
+    want_kv = _kv_rows(dev, ref, m["n_layers"], probe, rs)
+    ref.close()
+    if source == "gguf_tiled":
+        gf = Q.Gguf(G.decode_model_gguf(m, head_dim_key=True)[0])
+        gm = gf.load(dev, m["seq_len"])
+        assert gm.layers[0].wq_type == Q.TYPE_Q4_K | Q.TILED
+        d = gm.decoder(kv_type=Q.KV_Q8_0, order=order, page=64)
+    else:
+        d = make_decoder(dev, m, Q.KV_Q8_0, order, page=64)
+    d.set_pages(table)
+    print("prefill head128 %s" % source, flush=True)
+    lg, x = prefill(dev, d, m, toks, chunk=128)
+    kv = _kv_rows(dev, d, m["n_layers"], probe, rs)
+    d.close()
+    assert_bits_equal(lg, want_lg, "prefill logits")
+    assert_bits_equal(x, want_x, "prefill residual")
+    assert np.array_equal(kv, want_kv)
+
+
+def test_prefill_bad_args(dev):
+    m = I.decode_model("a")
+    d = make_decoder(dev, m, Q.KV_F32, ORDER_SEQ)
+    lg = dev.alloc(4 * m["vocab"])
+    with pytest.raises(Q.QrError, match="positions"):
+        d.prefill([1, 2, 3], m["seq_len"] - 2, lg.ptr)
+    with pytest.raises(Q.QrError, match="token"):
+        d.prefill([1, m["vocab"]], 0, lg.ptr)
+    with pytest.raises(Q.QrError, match="chunk"):
+        d.prefill([1, 2], 0, lg.ptr, chunk=100000)
+    d.prefill([], 0, lg.ptr)  # nothing to do
+    d.close()
