@@ -683,7 +683,7 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_sv(const float* __restrict_
 // the exponentials in parallel, lane 0 adds them in order; then each
 // position's weight e_t * inv once into LDS.  o[c] = sum over t in order of
 // (e_t * inv) * v_t[c], each product rounded, then added.  Dynamic LDS:
-// lds_cap floats, then the page table.
+// lds_cap floats.
 template <int KVT>
 __global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ att,
                                                       int att_stride, KvView V,
@@ -698,8 +698,6 @@ __global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ 
   const int npos = st[2 * z + 1] + 1;
   const int nthr = blockDim.x, tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  int32_t* pt = reinterpret_cast<int32_t*>(e + lds_cap);
-  for (int i = tid; i < (npos + V.page - 1) / V.page; i += nthr) pt[i] = V.ptab[i];
   const ExpTab tab = qr_expf_tab();
   float mx = att[0];
   for (int i = tid; i < npos; i += nthr) {
@@ -738,7 +736,7 @@ __global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ 
     float v[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const uint8_t* row = kv_row_lds(V, pt, t + u);
+      const uint8_t* row = V.row(t + u);  // one address per wave: the page table by scalar loads
       if constexpr (KVT == QR_KV_Q8_0) {
         const uint8_t* blk = row + (size_t)(col >> 5) * QR_Q8_BYTES;
         const float d = qr_h2f(*reinterpret_cast<const uint16_t*>(blk));
@@ -751,7 +749,7 @@ __global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ 
     for (int u = 0; u < U; u++) acc += e[t + u] * v[u];
   }
   for (; t < npos; t++) {
-    const uint8_t* row = kv_row_lds(V, pt, t);
+    const uint8_t* row = V.row(t);
     float v;
     if constexpr (KVT == QR_KV_Q8_0) {
       const uint8_t* blk = row + (size_t)(col >> 5) * QR_Q8_BYTES;
@@ -769,7 +767,7 @@ hipError_t sv_rows_launch(const float* att, int att_stride, const KvView& V, con
                           hipStream_t s) {
   const dim3 grid(n_heads, tokens);
   const int threads = ((hd + 63) / 64) * 64;
-  const size_t lds = (size_t)lds_cap * 4 + (size_t)((lds_cap + V.page - 1) / V.page) * 4;
+  const size_t lds = (size_t)lds_cap * 4;
   if (V.kv_type == QR_KV_Q8_0)
     hipLaunchKernelGGL(k_attn_sv_rows<QR_KV_Q8_0>, grid, dim3(threads), lds, s, att, att_stride, V,
                        st, lds_cap, kv_mul, hd, out);
@@ -851,6 +849,8 @@ struct qr_decoder {
   uint8_t* prec = nullptr;  // activation records [pcap][max(dim, q_dim) / 32]
   int32_t *poff = nullptr, *pperm = nullptr, *ptiles = nullptr;
   uint8_t* pmoe = nullptr;
+  const float* prec_src = nullptr;  // the rows prec holds records of (nullptr: none)
+  int prec_perm = 0;
 };
 
 namespace {
@@ -953,8 +953,11 @@ __global__ __launch_bounds__(256) void k_rows_dispatch(int T, int tile, int32_t*
 // Q8_0 weights as one grouped int8 MFMA product (qr_moe_mfma.hip, the rows
 // dispatched to a single "expert"), whose per-row terms and order are the
 // fused dot's; Q8_0 in a lane order through the GEMV, four rows per launch.
+// The records of x are quantized unless `records` says the previous call
+// left those of the same x (and the same record order) in d->prec; the chunk's
+// single-expert dispatch lists are written once per chunk (prefill_rows_setup).
 hipError_t matmul_rows_dev(qr_decoder* d, const void* w, uint32_t type, const float* x, float* y,
-                           int n, int dd, int T, hipStream_t s) {
+                           int n, int dd, int T, hipStream_t s, bool records = false) {
   hipError_t e;
   if (type == QR_T_F32)
     return gemv_f32_launch(d->order, static_cast<const float*>(w), x, y, n, dd, T, dd, n, s);
@@ -962,11 +965,17 @@ hipError_t matmul_rows_dev(qr_decoder* d, const void* w, uint32_t type, const fl
   const uint32_t base = type & ~(uint32_t)QR_TILED;
   const bool lanes = base == QR_T_Q8_0 && d->order != QR_ORDER_SEQ;
   if (!lanes && T >= 2 && mfma_type_ok((int)base) && dd % 256 == 0 && (dd >> 8) <= 64) {
-    const int tile = T >= 32 ? 32 : 16;
-    if ((e = quant_rows_launch(x, dd, T, dd, base != QR_T_Q8_0, d->prec, s))) return e;
-    hipLaunchKernelGGL(k_rows_dispatch, dim3(1), dim3(256), 0, s, T, tile, d->poff, d->pperm,
-                       d->ptiles);
-    if ((e = hipGetLastError())) return e;
+    // 16-pair work items: a dense matrix has one "expert", so the items are
+    // what spreads it over the CUs (measured on a 128-token chunk of the
+    // Qwen3-30B-A3B-shaped model: 71 ms for 512 prompt tokens against 75 ms
+    // with 32-pair items)
+    const int tile = 16;
+    const int perm = base != QR_T_Q8_0;
+    if (!records || d->prec_src != x || d->prec_perm != perm) {
+      if ((e = quant_rows_launch(x, dd, T, dd, perm != 0, d->prec, s))) return e;
+      d->prec_src = x;
+      d->prec_perm = perm;
+    }
     const size_t slice = qr_wrow_bytes((int)base, dd) * (size_t)n;
     return expert_mfma_launch((int)base, false, static_cast<const uint8_t*>(w), nullptr, slice, 1,
                               1, n, dd, d->prec, 1, d->poff, d->pperm, d->ptiles, y, n,
@@ -991,6 +1000,12 @@ hipError_t matmul_rows_dev(qr_decoder* d, const void* w, uint32_t type, const fl
 hipError_t enqueue_prefill_chunk(qr_decoder* d, int T, const int32_t* st, hipStream_t s) {
   hipError_t e;
   const int dim = d->dim;
+  // the chunk's single-expert dispatch of its T rows (16-pair items, as
+  // matmul_rows_dev launches them)
+  hipLaunchKernelGGL(k_rows_dispatch, dim3(1), dim3(256), 0, s, T, 16, d->poff,
+                     d->pperm, d->ptiles);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  d->prec_src = nullptr;
   hipLaunchKernelGGL(k_embed, dim3(T), dim3(256), 0, s, static_cast<const uint8_t*>(d->tok_embd),
                      (int)d->tok_type, d->tok_row, st, dim, d->px);
   if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -998,9 +1013,11 @@ hipError_t enqueue_prefill_chunk(qr_decoder* d, int T, const int32_t* st, hipStr
   for (int l = 0; l < d->nl; l++) {
     const qr_layer& L = d->layers[l];
     if ((e = rmsnorm_launch(d->px, nullptr, L.rms_att, dim, d->pxb, s, T))) return e;
+    d->prec_src = nullptr;  // pxb has new rows: no records of them yet
     if ((e = matmul_rows_dev(d, L.wq, L.wq_type, d->pxb, d->pq, d->qd, dim, T, s))) return e;
-    if ((e = matmul_rows_dev(d, L.wk, L.wk_type, d->pxb, d->pk, d->kvd, dim, T, s))) return e;
-    if ((e = matmul_rows_dev(d, L.wv, L.wv_type, d->pxb, d->pv, d->kvd, dim, T, s))) return e;
+    // k and v read the records q's product left (same rows, same order)
+    if ((e = matmul_rows_dev(d, L.wk, L.wk_type, d->pxb, d->pk, d->kvd, dim, T, s, true))) return e;
+    if ((e = matmul_rows_dev(d, L.wv, L.wv_type, d->pxb, d->pv, d->kvd, dim, T, s, true))) return e;
     const KvView K = kv_view(d, l, false), V = kv_view(d, l, true);
     hipLaunchKernelGGL(k_rope_kv, dim3((d->qd / 2 + 2 * (d->kvd / 32) + 255) / 256, T), dim3(256),
                        0, s, d->pq, d->pk, d->pv, d->rope, st, d->qd, d->kvd, K,
