@@ -155,6 +155,19 @@ int qr_gemv_ord(qr_ctx* ctx, int order, uint32_t type, const void* w, const floa
  * pointers, 16-byte aligned, not overlapping; enqueued on the context
  * stream.  qr_row_bytes(type | QR_TILED, d) is the plain row size. */
 #define QR_TILED 0x100u
+
+/* llama.cpp / ggml's own K-quant layouts (ggml-common.h: block_q4_K with its
+ * 12 packed 6-bit scales and mins, block_q5_K, block_q6_K with 16 int8
+ * scales; 144 / 176 / 210 bytes), which the reference does not implement (its
+ * layouts are its own, src/quant.c:180-238): pass `QR_TYPE_Q4_K | QR_GGML`
+ * (Q5_K, Q6_K) to qr_gemv / qr_gemv_ex / qr_gemv_ord (no integer sums) and
+ * qr_dequantize.  The activation is quantized to Q8_K (quantize_row_q8_K_ref)
+ * and each row's dot follows ggml's generic ggml_vec_dot_q*_K_q8_K: eight
+ * lane sums and the min sum accumulated block by block, then added.
+ * qr_quantize_q8_k writes n / 256 block_q8_K (292 bytes: f32 d, i8 qs[256],
+ * i16 bsums[16]). */
+#define QR_GGML 0x200u
+int qr_quantize_q8_k(qr_ctx* ctx, const float* x, void* y, long n);
 int qr_weights_tile(qr_ctx* ctx, uint32_t type, const void* src, void* dst, int n, int d);
 int qr_weights_untile(qr_ctx* ctx, uint32_t type, const void* src, void* dst, int n, int d);
 

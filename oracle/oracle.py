@@ -132,6 +132,19 @@ class Oracle:
                                   C.c_int, _f32p, _f32p]
         L.qro_moe_dispatch.restype = C.c_int
         L.qro_moe_dispatch.argtypes = [_i32p, C.c_int, C.c_int, C.c_int, _i32p, _i32p, _i32p, _i32p]
+        # llama.cpp / ggml K-quant formats (qr_oracle_ggml.c)
+        L.qro_ggml_h2f.restype = C.c_float
+        L.qro_ggml_h2f.argtypes = [C.c_uint16]
+        L.qro_ggml_h2f_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_long]
+        L.qro_ggml_block_bytes.restype = C.c_size_t
+        L.qro_ggml_block_bytes.argtypes = [C.c_int]
+        L.qro_ggml_scale_min.argtypes = [C.c_void_p, _i32p, _i32p]
+        L.qro_ggml_dequantize_row.argtypes = [C.c_int, C.c_void_p, _f32p, C.c_int]
+        L.qro_quantize_row_q8_K.argtypes = [_f32p, C.c_void_p, C.c_int]
+        L.qro_ggml_block_ints.argtypes = [C.c_int, C.c_void_p, C.c_void_p, _i32p, _i32p]
+        L.qro_ggml_vec_dot.restype = C.c_float
+        L.qro_ggml_vec_dot.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int]
+        L.qro_ggml_matmul.argtypes = [_f32p, _f32p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int]
 
     # --- fp16 helpers, include/quant.h:53-77
     def h2f(self, h):
@@ -146,6 +159,47 @@ class Oracle:
 
     def f2h(self, f):
         return self.lib.qro_f2h(float(f))
+
+    # --- llama.cpp / ggml K-quants (not in the reference; qr_oracle_ggml.c)
+    def ggml_h2f_bits(self, codes):
+        codes = np.ascontiguousarray(codes, np.uint16)
+        out = np.empty(codes.size, np.float32)
+        self.lib.qro_ggml_h2f_batch(_ptr(codes), _ptr(out), codes.size)
+        return out.view(np.uint32)
+
+    def ggml_scale_min(self, scales12):
+        sc, mn = np.zeros(8, np.int32), np.zeros(8, np.int32)
+        self.lib.qro_ggml_scale_min(_ptr(np.ascontiguousarray(scales12, np.uint8)), sc, mn)
+        return sc, mn
+
+    def ggml_dequantize(self, blob, qtype, n):
+        out = np.zeros(n, np.float32)
+        self.lib.qro_ggml_dequantize_row(qtype, _ptr(np.ascontiguousarray(blob, np.uint8)), out, n)
+        return out
+
+    def quantize_q8_K(self, x):
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        out = np.zeros((x.size // 256) * 292, np.uint8)
+        self.lib.qro_quantize_row_q8_K(x, _ptr(out), x.size)
+        return out
+
+    def ggml_block_ints(self, qtype, blk, yb):
+        aux, sumi = np.zeros(8, np.int32), np.zeros(1, np.int32)
+        self.lib.qro_ggml_block_ints(qtype, _ptr(np.ascontiguousarray(blk, np.uint8)),
+                                     _ptr(np.ascontiguousarray(yb, np.uint8)), aux, sumi)
+        return aux, int(sumi[0])
+
+    def ggml_vec_dot(self, qtype, row, q8k, d):
+        return self.lib.qro_ggml_vec_dot(qtype, _ptr(np.ascontiguousarray(row, np.uint8)),
+                                         _ptr(np.ascontiguousarray(q8k, np.uint8)), d)
+
+    def ggml_matmul(self, x, w, qtype, n, d):
+        """x [nt, d] fp32, w [n][d/256 * block] bytes -> [nt, n]."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, d)
+        out = np.zeros((x.shape[0], n), np.float32)
+        self.lib.qro_ggml_matmul(out, x, _ptr(np.ascontiguousarray(w, np.uint8)), qtype, n, d,
+                                 x.shape[0])
+        return out
 
     # --- src/quant.c:143-158
     def quantize_q8_0(self, x):

@@ -1085,6 +1085,15 @@ int qr_dequantize(qr_ctx* c, uint32_t type, const void* src, int rows, int n, fl
   if (rows < 0 || n < 0) return set_error(QR_ERR_INVALID, "qr_dequantize: negative size");
   if ((long)rows * n == 0) return QR_OK;
   if (!out) return set_error(QR_ERR_INVALID, "qr_dequantize: null out");
+  if (type & QR_GGML) {  // llama.cpp / ggml K-quant blocks
+    const uint32_t base = type & ~(uint32_t)QR_GGML;
+    if ((base != QR_T_Q4_K && base != QR_T_Q5_K && base != QR_T_Q6_K) || n % 256)
+      return set_error(QR_ERR_INVALID, "qr_dequantize: ggml type %u, n=%d", base, n);
+    if (!src) return set_error(QR_ERR_INVALID, "qr_dequantize: null src");
+    DEC_HIP(hipSetDevice(ctx_device(c)), "hipSetDevice");
+    DEC_HIP(ggml_dequant_launch((int)base, src, rows, n, out, ctx_stream(c)), "k_ggml_dequant_rows");
+    return QR_OK;
+  }
   const size_t rb = qr_row_bytes(type, n);
   const bool known = type == QR_T_F32 || type == QR_T_Q8_0 || type == QR_T_Q4_K ||
                      type == QR_T_Q5_K || type == QR_T_Q6_K;

@@ -19,6 +19,7 @@
 #include "qr_stream.h"
 #include "qr_blk.h"
 #include "qr_tiled.h"
+#include "qr_ggml.h"
 
 namespace qr {
 
@@ -594,6 +595,95 @@ hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, 
   if (type == QR_T_Q4_K) return launch_tiled_type<QR_T_Q4_K>(a, nt, st);
   if (type == QR_T_Q5_K) return launch_tiled_type<QR_T_Q5_K>(a, nt, st);
   return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// llama.cpp / ggml K-quants against Q8_K (qr_ggml.h).
+// ---------------------------------------------------------------------------
+static size_t ggml_lds_bytes(int type, int d, int nt) {
+  const int ndma = type == kGgmlQ4 ? GgmlFmt<kGgmlQ4>::kDma
+                   : type == kGgmlQ5 ? GgmlFmt<kGgmlQ5>::kDma : GgmlFmt<kGgmlQ6>::kDma;
+  return align16((size_t)nt * q8k_tok_bytes(d)) + (size_t)4 * ndma * 1024;
+}
+
+bool gemv_ggml_ok(int type, int d, int nt) {
+  if (type != kGgmlQ4 && type != kGgmlQ5 && type != kGgmlQ6) return false;
+  if (d <= 0 || (d & 255) || (d >> 8) > 64) return false;
+  if (!(nt >= 1 && nt <= 4) && nt != 8) return false;
+  return ggml_lds_bytes(type, d, nt == 8 ? 4 : nt) <= kLdsMax;
+}
+
+template <int T, int NT>
+static hipError_t launch_ggml_t(const GemvArgs& a, hipStream_t st) {
+  static std::atomic<bool> opted[64];
+  const int nb = a.d >> 8, RB = 64 / nb;
+  const int ntiles = (a.n + RB - 1) / RB;
+  const size_t lds = ggml_lds_bytes(T, a.d, NT);
+  if (lds > 64 * 1024) {
+    hipError_t e = lds_opt_in((const void*)k_gemv_ggml<T, NT>, opted);
+    if (e != hipSuccess) return e;
+  }
+  int per_cu = (int)(kLdsMax / lds);
+  per_cu = per_cu < 1 ? 1 : (per_cu > 3 ? 3 : per_cu);
+  const int want = (ntiles + 3) / 4;
+  const int cap = device_cus() * per_cu;
+  const int grid = want < cap ? want : cap;
+  if (grid <= 0) return hipSuccess;
+  hipLaunchKernelGGL((k_gemv_ggml<T, NT>), dim3(grid), dim3(256), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int T>
+static hipError_t launch_ggml_type(GemvArgs a, int nt, hipStream_t st) {
+  switch (nt) {
+    case 1: return launch_ggml_t<T, 1>(a, st);
+    case 2: return launch_ggml_t<T, 2>(a, st);
+    case 3: return launch_ggml_t<T, 3>(a, st);
+    case 4: return launch_ggml_t<T, 4>(a, st);
+    case 8: {
+      hipError_t e = launch_ggml_t<T, 4>(a, st);
+      if (e != hipSuccess) return e;
+      a.X += (size_t)4 * a.xstride;
+      a.Y += (size_t)4 * a.ystride;
+      return launch_ggml_t<T, 4>(a, st);
+    }
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t gemv_ggml_launch(int type, const void* W, const float* X, float* Y, int n, int d, int nt,
+                            int xstride, int ystride, hipStream_t st) {
+  GemvArgs a{};
+  a.W = static_cast<const uint8_t*>(W);
+  a.X = X;
+  a.Y = Y;
+  a.n = n;
+  a.d = d;
+  a.xstride = xstride;
+  a.ystride = ystride;
+  if (type == kGgmlQ4) return launch_ggml_type<kGgmlQ4>(a, nt, st);
+  if (type == kGgmlQ5) return launch_ggml_type<kGgmlQ5>(a, nt, st);
+  if (type == kGgmlQ6) return launch_ggml_type<kGgmlQ6>(a, nt, st);
+  return hipErrorInvalidValue;
+}
+
+hipError_t quantize_q8k_launch(const float* x, void* y, long nblocks, hipStream_t st) {
+  if (nblocks <= 0) return hipSuccess;
+  const long grid = (nblocks + 3) / 4;
+  hipLaunchKernelGGL(k_quantize_q8k, dim3((unsigned)grid), dim3(256), 0, st, x,
+                     static_cast<uint8_t*>(y), nblocks);
+  return hipGetLastError();
+}
+
+hipError_t ggml_dequant_launch(int type, const void* src, int rows, int n, float* out,
+                               hipStream_t st) {
+  const size_t rb = (size_t)(n >> 8) * (type == kGgmlQ4 ? 144 : type == kGgmlQ5 ? 176 : 210);
+  long grid = ((long)rows * n + 255) / 256;
+  if (grid > 4096) grid = 4096;
+  if (grid <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_ggml_dequant_rows, dim3((unsigned)grid), dim3(256), 0, st,
+                     static_cast<const uint8_t*>(src), type, rb, rows, n, out);
+  return hipGetLastError();
 }
 
 hipError_t tile_pack_launch(int type, const void* src, void* dst, int n, int d, bool reverse,

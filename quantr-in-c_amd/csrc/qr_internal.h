@@ -44,6 +44,13 @@ hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, 
                              int nt, int xstride, int ystride, hipStream_t st);
 hipError_t tile_pack_launch(int type, const void* src, void* dst, int n, int d, bool reverse,
                             hipStream_t st);
+// llama.cpp / ggml K-quants (qr_ggml.h): type is 12 / 13 / 14 (Q4_K / Q5_K / Q6_K).
+bool gemv_ggml_ok(int type, int d, int nt);
+hipError_t gemv_ggml_launch(int type, const void* W, const float* X, float* Y, int n, int d, int nt,
+                            int xstride, int ystride, hipStream_t st);
+hipError_t quantize_q8k_launch(const float* x, void* y, long nblocks, hipStream_t st);
+hipError_t ggml_dequant_launch(int type, const void* src, int rows, int n, float* out,
+                               hipStream_t st);
 hipError_t gemv_f32_launch(int order, const float* W, const float* X, float* Y, int n, int d,
                            int nt, int xstride, int ystride, hipStream_t st);
 hipError_t quantize_q8_0_launch(const float* x, void* y, long nblocks, hipStream_t st);

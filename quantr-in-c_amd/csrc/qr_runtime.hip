@@ -471,7 +471,9 @@ int qr_read_kernel(qr_ctx* c, const void* src, size_t bytes, void* sink) {
 }
 
 size_t qr_row_bytes(uint32_t type, int d) {
-  type &= ~(uint32_t)QR_TILED;  // the tiled layout keeps the row size
+  // the tiled layout keeps the row size; ggml's K-quant blocks have the
+  // reference's sizes (144 / 176 / 210 bytes)
+  type &= ~(uint32_t)(QR_TILED | QR_GGML);
   if (d < 0 || !known_type(type)) return 0;
   return qr_wrow_bytes((int)type, d);
 }
@@ -508,6 +510,16 @@ int qr_weights_untile(qr_ctx* c, uint32_t type, const void* src, void* dst, int 
   return QR_OK;
 }
 
+int qr_quantize_q8_k(qr_ctx* c, const float* x, void* y, long n) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_quantize_q8_k: null ctx");
+  if (n < 0) return fail(QR_ERR_INVALID, "qr_quantize_q8_k: negative size");
+  const long nb = n / 256;
+  if (nb == 0) return QR_OK;
+  if (!x || !y) return fail(QR_ERR_INVALID, "qr_quantize_q8_k: null pointer");
+  QR_HIP(qr::quantize_q8k_launch(x, y, nb, c->stream), "k_quantize_q8k");
+  return QR_OK;
+}
+
 int qr_quantize_q8_0(qr_ctx* c, const float* x, void* y, long n) {
   if (!c) return fail(QR_ERR_INVALID, "qr_quantize_q8_0: null ctx");
   if (n < 0) return fail(QR_ERR_INVALID, "qr_quantize_q8_0: negative size");
@@ -524,8 +536,11 @@ int qr_gemv_ord(qr_ctx* c, int order, uint32_t type, const void* w, const float*
   if (order < QR_ORDER_SEQ || order > QR_ORDER_AVX512)
     return fail(QR_ERR_INVALID, "qr_gemv: order %d", order);
   const bool tiled = (type & QR_TILED) != 0;
-  type &= ~(uint32_t)QR_TILED;
+  const bool ggml = (type & QR_GGML) != 0;
+  type &= ~(uint32_t)(QR_TILED | QR_GGML);
   if (!known_type(type)) return fail(QR_ERR_INVALID, "qr_gemv: unknown type %u", type);
+  if (ggml && (tiled || (type != QR_T_Q4_K && type != QR_T_Q5_K && type != QR_T_Q6_K)))
+    return fail(QR_ERR_UNSUPPORTED, "qr_gemv: ggml type %u (Q4_K, Q5_K, Q6_K; not tiled)", type);
   if (n < 0 || d < 0) return fail(QR_ERR_INVALID, "qr_gemv: negative size");
   if (!(nt == 1 || nt == 2 || nt == 3 || nt == 4 || nt == 8))
     return fail(QR_ERR_UNSUPPORTED, "qr_gemv: nt=%d (supported 1,2,3,4,8)", nt);
@@ -552,6 +567,14 @@ int qr_gemv_ord(qr_ctx* c, int order, uint32_t type, const void* w, const float*
   if (!aligned(w, 16)) return fail(QR_ERR_INVALID, "qr_gemv: weights must be 16-byte aligned");
   if (!aligned(x, 16) || (nt > 1 && (xstride & 3)))
     return fail(QR_ERR_INVALID, "qr_gemv: x must be 16-byte aligned (and xstride a multiple of 4)");
+  if (ggml) {
+    if (acc || accb) return fail(QR_ERR_UNSUPPORTED, "qr_gemv: no integer sums on ggml weights");
+    if (!qr::gemv_ggml_ok((int)type, d, nt))
+      return fail(QR_ERR_UNSUPPORTED, "qr_gemv: ggml type %u at d=%d nt=%d", type, d, nt);
+    QR_HIP(qr::gemv_ggml_launch((int)type, w, x, y, n, d, nt, xstride, ystride, c->stream),
+           "k_gemv_ggml");
+    return QR_OK;
+  }
   if (tiled) {
     if (acc || accb) return fail(QR_ERR_UNSUPPORTED, "qr_gemv: no integer sums on tiled weights");
     if (!qr::gemv_tiled_ok((int)type, d, nt))

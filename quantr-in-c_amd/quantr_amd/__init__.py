@@ -18,6 +18,7 @@ HEADERS = [os.path.join(REPO_DIR, "include", "qr_hip.h"),
 
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 0, 8, 12, 13, 14
 TILED = 0x100  # OR'ed into a Q4_K / Q5_K type: the weights are in the tiled layout
+GGML = 0x200   # OR'ed into a Q4_K / Q5_K / Q6_K type: llama.cpp's block layout, Q8_K activations
 ORDER_SEQ, ORDER_AVX2, ORDER_AVX512 = 0, 1, 2
 
 _vp = C.c_void_p
@@ -88,6 +89,7 @@ _SIGS = {
     "qr_graph_launch": (C.c_int, [_vp, _vp]),
     "qr_graph_destroy": (C.c_int, [_vp]),
     "qr_quantize_q8_0": (C.c_int, [_vp, _vp, _vp, C.c_long]),
+    "qr_quantize_q8_k": (C.c_int, [_vp, _vp, _vp, C.c_long]),
     "qr_gemv_ex": (C.c_int, [_vp, C.c_uint32, _vp, _vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int,
                              C.c_int, _vp, _vp]),
     "qr_gemv": (C.c_int, [_vp, C.c_uint32, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
@@ -296,6 +298,10 @@ class Device:
     # ---- ops (device pointers)
     def quantize_q8_0(self, x_ptr, y_ptr, n):
         self._check(self.lib.qr_quantize_q8_0(self.ctx, _vp(x_ptr), _vp(y_ptr), n), "qr_quantize_q8_0")
+
+    def quantize_q8_k(self, x_ptr, y_ptr, n):
+        """qr_quantize_q8_k: n / 256 ggml block_q8_K (292 bytes each)."""
+        self._check(self.lib.qr_quantize_q8_k(self.ctx, _vp(x_ptr), _vp(y_ptr), n), "qr_quantize_q8_k")
 
     def gemv(self, qtype, w_ptr, x_ptr, y_ptr, n, d, nt=1, xstride=None, ystride=None,
              acc_ptr=None, accb_ptr=None, order=ORDER_SEQ):
