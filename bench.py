@@ -23,6 +23,8 @@ Extra keys of the same line:
                path choice follows);
   moe_qwen15   the Qwen1.5-MoE-A2.7B-shaped layer (60 experts top-4, ffn 1408,
                shared expert ffn 5632 with a sigmoid gate) at T = 1 and 64;
+  gemv_ggml    the llama.cpp-layout Q4_K / Q5_K / Q6_K GEMV (Q8_K activations,
+               ggml's dot order) on 32000 x 2048 at 1 and 4 tokens;
   decode_qwen3 the whole single-token decode step of a Qwen3-30B-A3B-shaped
                model (48 layers, 32 query / 4 kv heads of 128, the MoE layer
                above, 151936-row Q6_K lm_head) over a Q8_0 paged KV cache
@@ -262,6 +264,57 @@ def bench_sweep(dev, types, warmup, pool_bytes=600 << 20, max_steps=2048, only=N
                         yb.free()
                     tpool.free()
             pool.free()
+    return res
+
+
+def ggml_rows(seed, qtype, n, d):
+    """n rows of llama.cpp-layout blocks: random bytes with finite half scales
+    (d and dmin; Q6_K's d at bytes 208..209)."""
+    rng = np.random.default_rng(seed)
+    B = {Q.TYPE_Q4_K: 144, Q.TYPE_Q5_K: 176, Q.TYPE_Q6_K: 210}[qtype]
+    nb = n * (d // 256)
+    w = rng.integers(0, 256, (nb, B), dtype=np.uint8)
+    half = lambda: (rng.uniform(1e-4, 2e-2, nb) * rng.choice([-1.0, 1.0], nb)).astype(  # noqa: E731
+        np.float16).view(np.uint8).reshape(nb, 2)
+    if qtype == Q.TYPE_Q6_K:
+        w[:, 208:210] = half()
+    else:
+        w[:, 0:2] = half()
+        w[:, 2:4] = half()
+    return w.reshape(n, -1)
+
+
+def bench_ggml(dev, warmup, pool_bytes=600 << 20, steps=200):
+    """The llama.cpp-layout K-quant GEMV (QR_GGML, Q8_K activations) on the
+    32000 x 2048 lm_head shape at 1 and 4 tokens, over > 590 MB of copies."""
+    res = {}
+    n, d = 32000, 2048
+    for qtype in (Q.TYPE_Q4_K, Q.TYPE_Q5_K, Q.TYPE_Q6_K):
+        W = ggml_rows(900 + qtype, qtype, n, d)
+        copies = max(1, math.ceil(pool_bytes / W.nbytes))
+        pool = dev.alloc(W.nbytes * copies)
+        dev.write(pool, W)
+        for c in range(1, copies):
+            dev.copy(pool.ptr + c * W.nbytes, pool.ptr, W.nbytes)
+        for nt in (1, 4):
+            xb = dev.upload(synth.normal(5 + nt, (nt, d)))
+            yb = dev.alloc(nt * n * 4)
+            launch = lambda i: dev.gemv(qtype | Q.GGML, pool.ptr + (i % copies) * W.nbytes,  # noqa: E731
+                                        xb.ptr, yb.ptr, n, d, nt)
+            for i in range(warmup):
+                launch(i)
+            dev.sync()
+            ms = graph_ms(dev, launch, steps, reps=3)
+            alg = W.nbytes + nt * ((d // 256) * 292 + 4 * n)
+            key = "%s_ggml_%dx%d_t%d" % (TNAME[qtype], n, d, nt)
+            res[key] = dict(us=round(ms * 1e3, 3), weight_gbps=round(W.nbytes / (ms / 1e3) / 1e9, 1),
+                            alg_bytes=alg, achieved_gbps=round(alg / (ms / 1e3) / 1e9, 1),
+                            frac=round(alg / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4))
+            log("bench: %-28s %8.2f us  %7.0f GB/s  frac %.3f" % (
+                key, ms * 1e3, alg / (ms / 1e3) / 1e9, res[key]["frac"]))
+            xb.free()
+            yb.free()
+        pool.free()
     return res
 
 
@@ -615,6 +668,8 @@ def main():
     ap.add_argument("--no-crossover", action="store_true",
                     help="skip the grouped-GEMV / MFMA comparison of the Qwen3 MoE leg")
     ap.add_argument("--decode-steps", type=int, default=32)
+    ap.add_argument("--no-ggml", action="store_true",
+                    help="skip the llama.cpp-layout K-quant GEMV leg")
     ap.add_argument("--no-gemv", action="store_true",
                     help="skip the GEMV headline (profiling runs of other legs; value is null)")
     args = ap.parse_args()
@@ -648,6 +703,7 @@ def main():
             only = {tuple(int(v) for v in sh.lower().split("x"))
                     for sh in args.sweep_shapes.split(",") if sh.strip()}
         sweep = bench_sweep(dev, types, min(args.warmup, 5), only=only)
+    ggml = None if args.no_ggml else bench_ggml(dev, min(args.warmup, 5))
 
     moe = moe15 = dec = None
     M = None
@@ -748,6 +804,7 @@ def main():
         "gemv_q4k_32000x2048_rows_t1": gkey("rows", 1) if h else None,
         "gemv_q4k_32000x2048_rows_t4": gkey("rows", 4) if h else None,
         "gemv_sweep": sweep,
+        "gemv_ggml": ggml,
         "moe_qwen3": moe,
         "moe_qwen15": moe15,
         "decode_qwen3": dec,
