@@ -600,10 +600,12 @@ hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, 
 // ---------------------------------------------------------------------------
 // llama.cpp / ggml K-quants against Q8_K (qr_ggml.h).
 // ---------------------------------------------------------------------------
+static bool ggml_xs(int d, int nt) { return blk_xs_bytes(d, nt) <= kXsMax; }
 static size_t ggml_lds_bytes(int type, int d, int nt) {
   const int ndma = type == kGgmlQ4 ? GgmlFmt<kGgmlQ4>::kDma
                    : type == kGgmlQ5 ? GgmlFmt<kGgmlQ5>::kDma : GgmlFmt<kGgmlQ6>::kDma;
-  return align16((size_t)nt * q8k_tok_bytes(d)) + (size_t)4 * ndma * 1024;
+  return (ggml_xs(d, nt) ? blk_xs_bytes(d, nt) : 0) + align16((size_t)nt * q8k_tok_bytes(d)) +
+         (size_t)4 * ndma * 1024;
 }
 
 bool gemv_ggml_ok(int type, int d, int nt) {
@@ -613,14 +615,14 @@ bool gemv_ggml_ok(int type, int d, int nt) {
   return ggml_lds_bytes(type, d, nt == 8 ? 4 : nt) <= kLdsMax;
 }
 
-template <int T, int NT>
-static hipError_t launch_ggml_t(const GemvArgs& a, hipStream_t st) {
+template <int T, int NT, bool XS>
+static hipError_t launch_ggml_x(const GemvArgs& a, hipStream_t st) {
   static std::atomic<bool> opted[64];
   const int nb = a.d >> 8, RB = 64 / nb;
   const int ntiles = (a.n + RB - 1) / RB;
   const size_t lds = ggml_lds_bytes(T, a.d, NT);
   if (lds > 64 * 1024) {
-    hipError_t e = lds_opt_in((const void*)k_gemv_ggml<T, NT>, opted);
+    hipError_t e = lds_opt_in((const void*)k_gemv_ggml<T, NT, XS>, opted);
     if (e != hipSuccess) return e;
   }
   int per_cu = (int)(kLdsMax / lds);
@@ -629,8 +631,13 @@ static hipError_t launch_ggml_t(const GemvArgs& a, hipStream_t st) {
   const int cap = device_cus() * per_cu;
   const int grid = want < cap ? want : cap;
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((k_gemv_ggml<T, NT>), dim3(grid), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((k_gemv_ggml<T, NT, XS>), dim3(grid), dim3(256), lds, st, a);
   return hipGetLastError();
+}
+
+template <int T, int NT>
+static hipError_t launch_ggml_t(const GemvArgs& a, hipStream_t st) {
+  return ggml_xs(a.d, NT) ? launch_ggml_x<T, NT, true>(a, st) : launch_ggml_x<T, NT, false>(a, st);
 }
 
 template <int T>

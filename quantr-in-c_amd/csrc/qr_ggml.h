@@ -172,7 +172,7 @@ __device__ inline void ggml_block_ints(const uint32_t* lds, int o, const uint8_t
       const int* bs = reinterpret_cast<const int*>(act + (size_t)t * tokb + 260);
       int s = 0;
 #pragma unroll
-      for (int j = 0; j < 16; j++) s += bs[j] * mn[j >> 1];
+      for (int j = 0; j < 16; j++) s += __mul24(bs[j], mn[j >> 1]);  // |bs| < 2^11, mn < 64
       sumi[t] = s;
     }
     uint32_t H[8];
@@ -200,7 +200,8 @@ __device__ inline void ggml_block_ints(const uint32_t* lds, int o, const uint8_t
           const uint32_t* xt = reinterpret_cast<const uint32_t*>(act + (size_t)t * tokb);
           const int s0 = __builtin_amdgcn_sdot4((int)lo, (int)xt[(2 * g) * 8 + l], 0, false);
           const int s1 = __builtin_amdgcn_sdot4((int)hi, (int)xt[(2 * g + 1) * 8 + l], 0, false);
-          aux[t][l] += sc[2 * g] * s0 + sc[2 * g + 1] * s1;
+          // 24-bit products (full-rate): |s| < 2^13, sc < 64
+          aux[t][l] += __mul24(sc[2 * g], s0) + __mul24(sc[2 * g + 1], s1);
         }
       }
     }
@@ -240,7 +241,7 @@ __device__ inline void ggml_block_ints(const uint32_t* lds, int o, const uint8_t
             const int xv = (int)xt[m * 8 + l];
             const int s0 = __builtin_amdgcn_sdot4((int)(A[s] & 0x0000FFFFu), xv, 0, false);
             const int s1 = __builtin_amdgcn_sdot4((int)(A[s] & 0xFFFF0000u), xv, 0, false);
-            aux[t][l] += sc[2 * m] * s0 + sc[2 * m + 1] * s1;
+            aux[t][l] += __mul24(sc[2 * m], s0) + __mul24(sc[2 * m + 1], s1);  // |s| < 2^14
           }
         }
       }
@@ -252,8 +253,12 @@ __device__ inline void ggml_block_ints(const uint32_t* lds, int o, const uint8_t
 
 namespace qr {
 
-// The GEMV: persistent waves, one tile in flight per wave, NT tokens.
-template <int T, int NT>
+// The GEMV: persistent waves, one tile in flight per wave, NT tokens.  XS:
+// the fp32 activation is first moved into LDS by DMA, then each wave's first
+// tile DMA is issued, and the quantizer waits only for the activation (the
+// wave's operations complete in issue order); without XS (activations beyond
+// kXsMax) it is read and quantized before the first tile is requested.
+template <int T, int NT, bool XS>
 __global__ __launch_bounds__(256) void k_gemv_ggml(GemvArgs g) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int BB = GgmlFmt<T>::kBytes, NDMA = GgmlFmt<T>::kDma;
@@ -267,20 +272,35 @@ __global__ __launch_bounds__(256) void k_gemv_ggml(GemvArgs g) {
   const int ntiles = (g.n + RB - 1) / RB;
   const int tstep = gridDim.x * 4;
   int tile = blockIdx.x * 4 + wave;
-  uint8_t* act = smem;
-  uint8_t* slot = smem + align16((size_t)NT * tokb) + (size_t)wave * SB;
+  const size_t xsb = XS ? blk_xs_bytes(g.d, NT) : 0;
+  float* xs = reinterpret_cast<float*>(smem);
+  uint8_t* act = smem + xsb;
+  uint8_t* slot = act + align16((size_t)NT * tokb) + (size_t)wave * SB;
   const uint32_t* slot32 = reinterpret_cast<const uint32_t*>(slot);
   auto dma = [&](int t) {
     if (t >= ntiles) return;
     const int rows = min(RB, g.n - t * RB);
     tile_dma<NDMA>(g.W + (size_t)t * RB * rb, slot, rows * (int)rb, lane);
   };
-  // the activation first (every wave quantizes its share), then the stream
-  quantize_q8k_lds(g.X, (size_t)g.xstride, NT, g.d, act, wave, 4, lane);
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  if (tile >= ntiles) return;  // no barriers below
-  dma(tile);
+  if constexpr (XS) {
+    stage_act_dma(g.X, (size_t)g.xstride, NT, g.d, smem, wave, lane);
+    const bool has = tile < ntiles;
+    dma(tile);
+    if (has) wait_vmcnt<NDMA>();  // this wave's share of the activation has landed
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();  // ... and every wave's
+    quantize_q8k_lds(xs, (size_t)g.d, NT, g.d, act, wave, 4, lane);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (!has) return;  // no barriers below
+  } else {
+    // the activation first (every wave quantizes its share), then the stream
+    quantize_q8k_lds(g.X, (size_t)g.xstride, NT, g.d, act, wave, 4, lane);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (tile >= ntiles) return;  // no barriers below
+    dma(tile);
+  }
   const uint8_t* actb = act + (size_t)b * kQ8kBlk;
   for (;;) {
     wait_vmcnt<0>();

@@ -60,11 +60,6 @@ struct MF {
   static constexpr bool kMin = TYPE == QR_T_Q4_K || TYPE == QR_T_Q5_K;
 };
 
-// Spread the four nibbles of a 16-bit value to the low nibbles of 4 bytes.
-__device__ inline uint32_t nib16_to_bytes(uint32_t x) {
-  uint32_t t = (x | (x << 8)) & 0x00FF00FFu;
-  return (t | (t << 4)) & 0x0F0F0F0Fu;
-}
 // Four bits (bits 0..3 of x) to bit 4 of 4 bytes.
 __device__ inline uint32_t bits4_to_b4(uint32_t x) { return spread4(x) << 4; }
 
@@ -84,15 +79,39 @@ __device__ inline long unit_a(const uint32_t* wl, int o, int s, int kg) {
     const uint32_t od = ((t >> 1) & 1u) | ((t >> 2) & 2u) | ((t >> 3) & 4u) | ((t >> 4) & 8u);
     lo = (w & 0x0F0F0F0Fu) | bits4_to_b4(ev);
     hi = ((w >> 4) & 0x0F0F0F0Fu) | bits4_to_b4(od);
-  } else if constexpr (TYPE == QR_T_Q6_K) {
-    const uint32_t w = lds_u32(wl, o + 16 * s + 4 * kg);
-    const uint32_t h = lds_u32(wl, o + 128 + 8 * s + 2 * kg) & 0xFFFFu;
-    lo = (w & 0x0F0F0F0Fu) | (nib16_to_bytes(h & 0x3333u) << 4);
-    hi = ((w >> 4) & 0x0F0F0F0Fu) | (nib16_to_bytes((h >> 2) & 0x3333u) << 4);
-  } else {  // Q8_0: block s, bytes 2 + 8 kg .. +7
+  } else {  // Q8_0 (Q6_K: unit_a_q6): block s, bytes 2 + 8 kg .. +7
     lo = lds_u32(wl, o + QR_Q8_BYTES * s + 2 + 8 * kg);
     hi = lds_u32(wl, o + QR_Q8_BYTES * s + 6 + 8 * kg);
   }
+  return (long)((uint64_t)lo | ((uint64_t)hi << 32));
+}
+
+// Q6_K: a staged row starts at any even byte (210-byte stages), so the lane's
+// ql and qh words of every unit are read as aligned dword pairs at indices
+// fixed for the stage -- ql at dword w + 4 s shifted by wsh bytes, qh's 16
+// bits at dword h + 2 s picked by the byte selector hsel -- and the 2-bit
+// fields are moved to bits 4-5 of their bytes by shifts and masks.
+struct Q6Ref {
+  int w, h;
+  uint32_t wsh, hsel;
+};
+__device__ inline Q6Ref q6_ref(int o, int kg) {
+  Q6Ref q;
+  const int ow = o + 4 * kg, oh = o + 128 + 2 * kg;
+  q.w = ow >> 2;
+  q.wsh = (uint32_t)(ow & 3);
+  q.h = oh >> 2;
+  const uint32_t k = (uint32_t)(oh & 3);
+  q.hsel = k * 0x0101u + (k + 1) * 0x01010000u;  // bytes [k+1, k+1, k, k]
+  return q;
+}
+__device__ inline long unit_a_q6(const uint32_t* wl, const Q6Ref& q, int s) {
+  const uint32_t w = __builtin_amdgcn_alignbyte(wl[q.w + 4 * s + 1], wl[q.w + 4 * s], q.wsh);
+  // x: qh bytes b1 b1 b0 b0; element i's low pair sits in bits 4i..4i+1 of
+  // b1:b0, its high pair two bits up
+  const uint32_t x = __builtin_amdgcn_perm(wl[q.h + 2 * s + 1], wl[q.h + 2 * s], q.hsel);
+  const uint32_t lo = (w & 0x0F0F0F0Fu) | (((x << 4) & 0x00300030u) | (x & 0x30003000u));
+  const uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) | (((x << 2) & 0x00300030u) | ((x >> 2) & 0x30003000u));
   return (long)((uint64_t)lo | ((uint64_t)hi << 32));
 }
 
@@ -433,6 +452,13 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
 #pragma unroll
       for (int r = 0; r < RA; r++)
         hA[r] = (int)(((uint32_t)(rw0 + 16 * r + ln) * (uint32_t)rb + s0) & 15u);
+      Q6Ref q6[NMAT][RA];
+      if constexpr (TYPE == QR_T_Q6_K) {
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+          for (int r = 0; r < RA; r++) q6[m][r] = q6_ref((m * WR + 16 * r + ln) * G::SLOT + hA[r], kg);
+      }
       auto term_of = [&](float sc, float mn, int isum, float bd, float bsf, int bs) {
         if constexpr (MF<TYPE>::kMin) return (sc * (float)isum - mn * bsf) * bd;
         else if constexpr (TYPE == QR_T_Q6_K) return sc * (float)(isum - 32 * bs) * bd;
@@ -444,7 +470,8 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
         for (int m = 0; m < NMAT; m++)
 #pragma unroll
           for (int r = 0; r < RA; r++)
-            Wq[m][r] = unit_a<TYPE>(wl, (m * WR + 16 * r + ln) * G::SLOT + hA[r], s, kg);
+            if constexpr (TYPE == QR_T_Q6_K) Wq[m][r] = unit_a_q6(wl, q6[m][r], s);
+            else Wq[m][r] = unit_a<TYPE>(wl, (m * WR + 16 * r + ln) * G::SLOT + hA[r], s, kg);
         if constexpr (SK) {
           // A: pair ln / 4's quarter ln % 4 on A row ln (zeros in the other
           // k-groups); the term's pair is kg
@@ -578,6 +605,7 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
   else if (NJ == 1 || np <= 16) run(std::integral_constant<int, 1>{});
   else run(std::integral_constant<int, NJ>{});
 }
+
 
 // ---------------------------------------------------------------------------
 // Host side.
