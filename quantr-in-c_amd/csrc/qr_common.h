@@ -157,6 +157,48 @@ __device__ inline float qr_silu_w(float x, const ExpTab& T) {
   return x / (1.0f + qr_expf_w(-x, T));
 }
 
+// Sequential fp32 sums of LDS values (one lane): 256 values per read batch,
+// in two register buffers of 32 taken in turn, so the chain of adds does not
+// wait on LDS.
+__device__ inline void add32(const float4 (&v)[8], float& acc) {
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    acc += v[k].x;
+    acc += v[k].y;
+    acc += v[k].z;
+    acc += v[k].w;
+  }
+}
+__device__ inline void read32(const float* __restrict__ p, float4 (&v)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; k++) v[k] = *reinterpret_cast<const float4*>(p + 4 * k);
+}
+// 256 values (unrolled, so no buffer is carried across a loop iteration)
+__device__ inline void add256_lds(const float* __restrict__ p, float& s) {
+  float4 A[8], B[8];
+  read32(p, A);
+#pragma unroll
+  for (int t = 0; t < 256; t += 64) {
+    read32(p + t + 32, B);
+    add32(A, s);
+    if (t + 64 < 256) read32(p + t + 64, A);
+    add32(B, s);
+  }
+}
+__device__ inline float seq_sum_lds_long(const float* __restrict__ p, int n) {
+  float s = 0.0f;
+  int i = 0;
+  for (; i + 256 <= n; i += 256) add256_lds(p + i, s);
+  for (; i + 32 <= n; i += 32) {
+    float4 A[8];
+    read32(p + i, A);
+    add32(A, s);
+  }
+  for (; i < n; i++) s += p[i];
+  return s;
+}
+
+
 __host__ __device__ inline int qr_block_elems(int type) { return type == QR_T_Q8_0 ? 32 : 256; }
 __host__ __device__ inline int qr_block_bytes(int type) {
   return type == QR_T_Q8_0 ? QR_Q8_BYTES

@@ -98,46 +98,6 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ tab, 
 // attention, 42.7 against 44.2 us; RMSNorm's 2048 terms are faster in
 // batches of 16 (8.9 against 9.3 us).
 // ---------------------------------------------------------------------------
-__device__ inline void add32(const float4 (&v)[8], float& acc) {
-#pragma unroll
-  for (int k = 0; k < 8; k++) {
-    acc += v[k].x;
-    acc += v[k].y;
-    acc += v[k].z;
-    acc += v[k].w;
-  }
-}
-__device__ inline void read32(const float* __restrict__ p, float4 (&v)[8]) {
-#pragma unroll
-  for (int k = 0; k < 8; k++) v[k] = *reinterpret_cast<const float4*>(p + 4 * k);
-}
-// 256 values (unrolled, so no buffer is carried across a loop iteration)
-__device__ inline void add256_lds(const float* __restrict__ p, float& s) {
-  float4 A[8], B[8];
-  read32(p, A);
-#pragma unroll
-  for (int t = 0; t < 256; t += 64) {
-    read32(p + t + 32, B);
-    add32(A, s);
-    if (t + 64 < 256) read32(p + t + 64, A);
-    add32(B, s);
-  }
-}
-// Long sums (the softmax denominators over the positions): 256 values per
-// read batch.
-__device__ inline float seq_sum_lds_long(const float* __restrict__ p, int n) {
-  float s = 0.0f;
-  int i = 0;
-  for (; i + 256 <= n; i += 256) add256_lds(p + i, s);
-  for (; i + 32 <= n; i += 32) {
-    float4 A[8];
-    read32(p + i, A);
-    add32(A, s);
-  }
-  for (; i < n; i++) s += p[i];
-  return s;
-}
-
 // Short sums (RMSNorm's 2048 squares): 16 values per read batch.
 __device__ inline float seq_sum_lds(const float* __restrict__ p, int n) {
   float s = 0.0f;
@@ -1109,6 +1069,14 @@ int check_layer_weights(const qr_model* m, int l, int order) {
 }
 
 }  // namespace
+
+namespace qr {
+hipError_t rows_dispatch_launch(int T, int tile, int32_t* off, int32_t* perm, int32_t* tiles,
+                                hipStream_t st) {
+  hipLaunchKernelGGL(k_rows_dispatch, dim3(1), dim3(256), 0, st, T, tile, off, perm, tiles);
+  return hipGetLastError();
+}
+}  // namespace qr
 
 extern "C" {
 

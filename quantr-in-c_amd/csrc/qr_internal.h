@@ -73,6 +73,13 @@ struct MoeScratch {
   float* sgl;         // [T]             shared expert gate logit
   uint8_t* xq;        // [T][dim/32] quantized activation records (MFMA path)
   uint8_t* hq;        // [T*K][hidden/32] quantized hb records (MFMA path)
+  // the shared expert's own (empty without one)
+  float* ush;         // [T][sh_hidden]  its up rows (GEMV path)
+  uint8_t* xqs;       // [T][dim/32]     records of xb in its up type's order (MFMA path)
+  uint8_t* hqs;       // [T][sh_hidden/32] records of its hb (MFMA path)
+  int32_t* shoff;     // [2]   single-"expert" dispatch of the T tokens
+  int32_t* shtiles;   // [2]
+  int32_t* shperm;    // [T]
 };
 size_t moe_scratch_bytes(const qr_moe_layer* L, int T);
 void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s);
@@ -86,6 +93,10 @@ hipError_t moe_dispatch_launch(const int32_t* idx, int T, int K, int E, int tile
 hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, int T, int order,
                               const MoeScratch& s, hipStream_t st, int path = QR_MOE_PATH_AUTO);
 hipError_t softmax_launch(float* x, int rows, int n, hipStream_t st);
+// qr_decode.hip: a single-"expert" dispatch of T rows for the grouped MFMA
+// product (offsets {0, T}, the identity permutation, tiles {0, ceil(T / tile)}).
+hipError_t rows_dispatch_launch(int T, int tile, int32_t* off, int32_t* perm, int32_t* tiles,
+                                hipStream_t st);
 
 // qr_moe_t1.hip
 bool router1_ok(int dim);

@@ -54,6 +54,12 @@ size_t moe_scratch_bytes(const qr_moe_layer* L, int T) {
   b += a256((size_t)T * 4);
   b += a256((size_t)T * (L->dim / 32) * 48);
   b += a256(P * (size_t)(L->hidden / 32) * 48);
+  if (sh) {
+    b += a256((size_t)T * sh * 4);                  // ush
+    b += a256((size_t)T * (L->dim / 32) * 48);      // xqs
+    b += a256((size_t)T * (sh / 32) * 48);          // hqs
+    b += a256(2 * 4) * 2 + a256((size_t)T * 4);     // shoff, shtiles, shperm
+  }
   return b;
 }
 
@@ -81,6 +87,17 @@ void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s) 
   s->sgl = reinterpret_cast<float*>(take((size_t)T * 4));
   s->xq = take((size_t)T * (L->dim / 32) * 48);
   s->hq = take(P * (size_t)(L->hidden / 32) * 48);
+  s->ush = nullptr;
+  s->xqs = s->hqs = nullptr;
+  s->shoff = s->shtiles = s->shperm = nullptr;
+  if (sh) {
+    s->ush = reinterpret_cast<float*>(take((size_t)T * sh * 4));
+    s->xqs = take((size_t)T * (L->dim / 32) * 48);
+    s->hqs = take((size_t)T * (sh / 32) * 48);
+    s->shoff = reinterpret_cast<int32_t*>(take(2 * 4));
+    s->shtiles = reinterpret_cast<int32_t*>(take(2 * 4));
+    s->shperm = reinterpret_cast<int32_t*>(take((size_t)T * 4));
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -627,38 +644,100 @@ static int pick_tile(int P, int E) {
   return avg >= 6 ? 8 : avg >= 3 ? 4 : avg >= 1.5 ? 2 : 1;
 }
 
+// hb = silu(up . x) * (gate . x) of the shared expert's rows, from its up and
+// gate GEMV outputs (the gate/up products' own output formula).
+__global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ u, float* __restrict__ g,
+                                                  long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
+    g[i] = qr_silu(u[i]) * g[i];
+}
+
+static bool sh_gemv_type(int type) {
+  return type == QR_T_Q4_K || type == QR_T_Q5_K || type == QR_T_Q6_K || type == QR_T_Q8_0;
+}
+static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// The shared expert (a dense FFN every token takes) and its gate logit.  Its
+// dots are the routed experts' (C99 Q8_0 order, sequential gate logit):
+//   T <= 4  three GEMVs (up, gate, down) of T tokens on the GEMV engines and
+//           the silu product between them;
+//   T > 4   the grouped int8 MFMA products with one "expert" (the T tokens
+//           dispatched in order), gate/up leaving the down product's records;
+//   else    the grouped GEMV in dense mode.
 static hipError_t shared_expert(const qr_moe_layer* L, const float* xb, int T, const MoeScratch& s,
                                 hipStream_t st) {
-  const int nt = T >= 8 ? 8 : T >= 4 ? 4 : T >= 2 ? 2 : 1;
-  ExpertArgs g{};
-  g.W1 = static_cast<const uint8_t*>(L->sh_up);
-  g.W2 = static_cast<const uint8_t*>(L->sh_gate);
-  g.slice = 0;
-  g.rows = L->sh_hidden;
-  g.cols = L->dim;
-  g.X = xb;
-  g.xstride = L->dim;
-  g.Y = s.hbs;
-  g.ystride = L->sh_hidden;
-  g.mode = kModeDense;
-  g.E = 1;
-  g.K = 1;
-  g.P = T;
-  hipError_t e = expert_launch((int)L->sh_up_type, kQ8Seq, true, g, nt, (T + nt - 1) / nt, st);
-  if (e != hipSuccess) return e;
-  ExpertArgs dn = g;
-  dn.W1 = static_cast<const uint8_t*>(L->sh_down);
-  dn.W2 = nullptr;
-  dn.rows = L->dim;
-  dn.cols = L->sh_hidden;
-  dn.X = s.hbs;
-  dn.xstride = L->sh_hidden;
-  dn.Y = s.ysh;
-  dn.ystride = L->dim;
-  e = expert_launch((int)L->sh_down_type, kQ8Seq, false, dn, nt, (T + nt - 1) / nt, st);
-  if (e != hipSuccess) return e;
+  const int dim = L->dim, sh = L->sh_hidden;
+  const int ut = (int)L->sh_up_type, dt = (int)L->sh_down_type;
+  hipError_t e;
+  const bool same_up = L->sh_gate_type == L->sh_up_type;
+  const bool aligned = al16(L->sh_up) && al16(L->sh_gate) && al16(L->sh_down) && al16(xb);
+  if (T <= 4 && same_up && aligned && sh_gemv_type(ut) && sh_gemv_type(dt) &&
+      dim % qr_block_elems(ut) == 0 && sh % qr_block_elems(dt) == 0) {
+    if ((e = gemv_launch(ut, kQ8Seq, L->sh_up, xb, s.ush, sh, dim, T, dim, sh, nullptr, nullptr,
+                         st)) != hipSuccess)
+      return e;
+    if ((e = gemv_launch(ut, kQ8Seq, L->sh_gate, xb, s.hbs, sh, dim, T, dim, sh, nullptr, nullptr,
+                         st)) != hipSuccess)
+      return e;
+    const long n = (long)T * sh;
+    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s.ush,
+                       s.hbs, n);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = gemv_launch(dt, kQ8Seq, L->sh_down, s.hbs, s.ysh, dim, sh, T, sh, dim, nullptr,
+                         nullptr, st)) != hipSuccess)
+      return e;
+  } else if (T > 4 && same_up && aligned && mfma_type_ok(ut) && mfma_type_ok(dt) &&
+             dim % qr_block_elems(ut) == 0 && sh % 32 == 0 && sh % qr_block_elems(dt) == 0) {
+    const int tile = mfma_tile(T, 1, 1);
+    const int items = (T + tile - 1) / tile + 1;
+    if ((e = rows_dispatch_launch(T, tile, s.shoff, s.shperm, s.shtiles, st)) != hipSuccess)
+      return e;
+    if ((e = quant_rows_launch(xb, dim, T, dim, ut != QR_T_Q8_0, s.xqs, st)) != hipSuccess) return e;
+    const size_t su = qr_wrow_bytes(ut, dim) * (size_t)sh;
+    const size_t sd = qr_wrow_bytes(dt, sh) * (size_t)dim;
+    e = expert_mfma_launch(ut, true, static_cast<const uint8_t*>(L->sh_up),
+                           static_cast<const uint8_t*>(L->sh_gate), su, 1, 1, sh, dim, s.xqs, 0,
+                           s.shoff, s.shperm, s.shtiles, s.hbs, sh, items, tile, s.hqs,
+                           dt != QR_T_Q8_0, st);
+    if (e != hipSuccess) return e;
+    e = expert_mfma_launch(dt, false, static_cast<const uint8_t*>(L->sh_down), nullptr, sd, 1, 1,
+                           dim, sh, s.hqs, 0, s.shoff, s.shperm, s.shtiles, s.ysh, dim, items, tile,
+                           nullptr, false, st);
+    if (e != hipSuccess) return e;
+  } else {
+    const int nt = T >= 8 ? 8 : T >= 4 ? 4 : T >= 2 ? 2 : 1;
+    ExpertArgs g{};
+    g.W1 = static_cast<const uint8_t*>(L->sh_up);
+    g.W2 = static_cast<const uint8_t*>(L->sh_gate);
+    g.slice = 0;
+    g.rows = sh;
+    g.cols = dim;
+    g.X = xb;
+    g.xstride = dim;
+    g.Y = s.hbs;
+    g.ystride = sh;
+    g.mode = kModeDense;
+    g.E = 1;
+    g.K = 1;
+    g.P = T;
+    e = expert_launch(ut, kQ8Seq, true, g, nt, (T + nt - 1) / nt, st);
+    if (e != hipSuccess) return e;
+    ExpertArgs dn = g;
+    dn.W1 = static_cast<const uint8_t*>(L->sh_down);
+    dn.W2 = nullptr;
+    dn.rows = dim;
+    dn.cols = sh;
+    dn.X = s.hbs;
+    dn.xstride = sh;
+    dn.Y = s.ysh;
+    dn.ystride = dim;
+    e = expert_launch(dt, kQ8Seq, false, dn, nt, (T + nt - 1) / nt, st);
+    if (e != hipSuccess) return e;
+  }
   // gate logit: sequential dot (one row) for every token
-  return gemv_f32_launch(QR_ORDER_SEQ, L->sh_gate_inp, xb, s.sgl, 1, L->dim, T, L->dim, 1, st);
+  if (T == 1 && router1_ok(dim) && al16(L->sh_gate_inp) && al16(xb))
+    return router1_launch(QR_ORDER_SEQ, L->sh_gate_inp, xb, 1, dim, s.sgl, st);
+  return gemv_f32_launch(QR_ORDER_SEQ, L->sh_gate_inp, xb, s.sgl, 1, dim, T, dim, 1, st);
 }
 
 hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, int T, int order,

@@ -42,7 +42,12 @@ __global__ __launch_bounds__(64) void k_router1(const float* __restrict__ W,
   dma_bytes(reinterpret_cast<const uint8_t*>(xb), smem + rbytes, d * 4, lane);
   wait_vmcnt<0>();
   if constexpr (LANES == 1) {
-    if (lane == 0) logits[e] = lds_seq(sw, sx, d);  // matmul_ref, src/kernels.c:18-28
+    // matmul_ref, src/kernels.c:18-28: every product w[j] * x[j] rounded, then
+    // added in order -- the products formed by the whole wave in place, the
+    // chain of adds by lane 0
+    for (int j = lane; j < d; j += 64) sw[j] = sw[j] * sx[j];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (lane == 0) logits[e] = seq_sum_lds_long(sw, d);
   } else {
     // matmul_omp, src/kernels.c:38-65: LANES FMA chains, lanes combined in the
     // build's order, then the multiply-add tail

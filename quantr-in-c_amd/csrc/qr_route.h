@@ -316,23 +316,4 @@ __device__ inline float lds_chain(const float* w, const float* x, int k, int dm)
   return acc;
 }
 
-// Sequential mul-then-add over j < d out of LDS (matmul_ref order), 16 steps'
-// operands read before their adds.
-__device__ inline float lds_seq(const float* w, const float* x, int d) {
-  float s = 0.0f;
-  int j = 0;
-  for (; j + 16 <= d; j += 16) {
-    float wv[16], xv[16];
-#pragma unroll
-    for (int q = 0; q < 16; q++) {
-      wv[q] = w[j + q];
-      xv[q] = x[j + q];
-    }
-#pragma unroll
-    for (int q = 0; q < 16; q++) s += wv[q] * xv[q];
-  }
-  for (; j < d; j++) s += w[j] * x[j];
-  return s;
-}
-
 }  // namespace qr

@@ -165,8 +165,9 @@ def test_moe_qwen15_shared_expert(dev, oracle):
                   up_type=Q.TYPE_Q4_K, down_type=Q.TYPE_Q4_K)
     layer = DevLayer(dev, dim, hidden, E, K, router, up, gate, down, Q.TYPE_Q4_K, Q.TYPE_Q8_0,
                      shared=shared)
-    for T, order in ((1, ORDER_SEQ), (8, ORDER_SEQ), (64, ORDER_SEQ), (1, ORDER_AVX2),
-                     (64, ORDER_AVX2)):
+    # T <= 4: the shared expert on the GEMV engines; T > 4: on the MFMA products
+    for T, order in ((1, ORDER_SEQ), (3, ORDER_SEQ), (5, ORDER_AVX2), (8, ORDER_SEQ),
+                     (64, ORDER_SEQ), (1, ORDER_AVX2), (64, ORDER_AVX2)):
         xb = synth.normal(4100 + T, (T, dim))
         x = synth.normal(4200 + T, (T, dim))
         check_moe(dev, oracle, layer, x, xb, order, "qwen1.5 T=%d order %d" % (T, order))
