@@ -100,8 +100,11 @@ hipError_t rows_dispatch_launch(int T, int tile, int32_t* off, int32_t* perm, in
 
 // qr_moe_t1.hip
 bool router1_ok(int dim);
+// Router logits of T tokens (grid E x T), and with W2 the sequential-order dot
+// of the one row W2 with each token into out2[t] (E = 0: that dot alone).
 hipError_t router1_launch(int order, const float* W, const float* xb, int E, int d, float* logits,
-                          hipStream_t st);
+                          hipStream_t st, int T = 1, const float* W2 = nullptr,
+                          float* out2 = nullptr);
 bool gateup1_ok(int type, int dim, int E, int K);
 hipError_t gateup1_launch(int type, const void* up, const void* gate, size_t slice, int dim,
                           int hidden, int E, int K, const float* xb, const float* logits,

@@ -665,7 +665,7 @@ static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) =
 //           dispatched in order), gate/up leaving the down product's records;
 //   else    the grouped GEMV in dense mode.
 static hipError_t shared_expert(const qr_moe_layer* L, const float* xb, int T, const MoeScratch& s,
-                                hipStream_t st) {
+                                hipStream_t st, bool gate_done = false) {
   const int dim = L->dim, sh = L->sh_hidden;
   const int ut = (int)L->sh_up_type, dt = (int)L->sh_down_type;
   hipError_t e;
@@ -734,9 +734,11 @@ static hipError_t shared_expert(const qr_moe_layer* L, const float* xb, int T, c
     e = expert_launch(dt, kQ8Seq, false, dn, nt, (T + nt - 1) / nt, st);
     if (e != hipSuccess) return e;
   }
-  // gate logit: sequential dot (one row) for every token
-  if (T == 1 && router1_ok(dim) && al16(L->sh_gate_inp) && al16(xb))
-    return router1_launch(QR_ORDER_SEQ, L->sh_gate_inp, xb, 1, dim, s.sgl, st);
+  // gate logit: sequential dot (one row) for every token, one workgroup per
+  // token (unless the router's launch computed it beside the logits)
+  if (gate_done) return hipSuccess;
+  if (router1_ok(dim) && al16(L->sh_gate_inp) && al16(xb))
+    return router1_launch(QR_ORDER_SEQ, nullptr, xb, 0, dim, nullptr, st, T, L->sh_gate_inp, s.sgl);
   return gemv_f32_launch(QR_ORDER_SEQ, L->sh_gate_inp, xb, s.sgl, 1, dim, T, dim, 1, st);
 }
 
@@ -761,13 +763,16 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
       L->up_type == L->gate_type && down1v2_ok((int)L->down_type, K, L->dim, L->hidden) &&
       (reinterpret_cast<uintptr_t>(L->router) & 15) == 0 &&
       (reinterpret_cast<uintptr_t>(xb) & 15) == 0) {
-    e = router1_launch(order, L->router, xb, E, L->dim, s.logits, st);
+    // the shared expert's gate logit beside the router's (one more workgroup)
+    const bool sg = sh && (reinterpret_cast<uintptr_t>(L->sh_gate_inp) & 15) == 0;
+    e = router1_launch(order, L->router, xb, E, L->dim, s.logits, st, 1,
+                       sg ? static_cast<const float*>(L->sh_gate_inp) : nullptr, s.sgl);
     if (e != hipSuccess) return e;
     e = gateup1_launch((int)L->up_type, L->up, L->gate, su, L->dim, L->hidden, E, K, xb, s.logits,
                        s.idx, s.wts, s.hb, st);
     if (e != hipSuccess) return e;
     if (sh) {
-      e = shared_expert(L, xb, T, s, st);
+      e = shared_expert(L, xb, T, s, st, sg);
       if (e != hipSuccess) return e;
     }
     return down1v2_launch((int)L->down_type, L->down, sd, L->dim, L->hidden, E, K, s.hb, s.idx,

@@ -29,25 +29,51 @@ namespace qr {
 // ---------------------------------------------------------------------------
 // Router logits.
 // ---------------------------------------------------------------------------
+// matmul_ref (src/kernels.c:18-28) of one staged row: every product w[j] * x[j]
+// rounded, then added in order -- the products formed by the whole wave in
+// place (w becomes the products), the chain of adds by lane 0.
+__device__ inline float router_seq(float* sw, const float* sx, int d, int lane) {
+  const int d4 = d >> 2;  // d % 4 == 0 (router1_ok)
+#pragma unroll 4
+  for (int j = lane; j < d4; j += 64) {
+    float4 w = reinterpret_cast<const float4*>(sw)[j];
+    const float4 x = reinterpret_cast<const float4*>(sx)[j];
+    w.x = w.x * x.x;
+    w.y = w.y * x.y;
+    w.z = w.z * x.z;
+    w.w = w.w * x.w;
+    reinterpret_cast<float4*>(sw)[j] = w;
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  return seq_sum_lds_long(sw, d);  // lane 0's value is used
+}
+
+// Workgroup (e, t): logit e of token t (xb + t d, logits + t E).  With `W2`, the
+// workgroups e = E compute, in matmul_ref's order whatever LANES is, the dot
+// of the one row W2 with each token into out2[t] (the shared expert's gate
+// logit, computed beside the router's).
 template <int LANES>
 __global__ __launch_bounds__(64) void k_router1(const float* __restrict__ W,
-                                                const float* __restrict__ xb, int d,
-                                                float* __restrict__ logits) {
+                                                const float* __restrict__ xb, int d, int E,
+                                                float* __restrict__ logits,
+                                                const float* __restrict__ W2,
+                                                float* __restrict__ out2) {
   extern __shared__ __align__(16) uint8_t smem[];
-  const int e = blockIdx.x, lane = threadIdx.x;
+  const int e = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
   const size_t rbytes = kib_round((size_t)d * 4);
   float* sw = reinterpret_cast<float*>(smem);
   float* sx = reinterpret_cast<float*>(smem + rbytes);
-  dma_bytes<true>(reinterpret_cast<const uint8_t*>(W + (size_t)e * d), smem, d * 4, lane);
-  dma_bytes(reinterpret_cast<const uint8_t*>(xb), smem + rbytes, d * 4, lane);
+  const bool extra = e >= E;  // uniform
+  const float* row = extra ? W2 : W + (size_t)e * d;
+  dma_bytes<true>(reinterpret_cast<const uint8_t*>(row), smem, d * 4, lane);
+  dma_bytes(reinterpret_cast<const uint8_t*>(xb + (size_t)t * d), smem + rbytes, d * 4, lane);
   wait_vmcnt<0>();
-  if constexpr (LANES == 1) {
-    // matmul_ref, src/kernels.c:18-28: every product w[j] * x[j] rounded, then
-    // added in order -- the products formed by the whole wave in place, the
-    // chain of adds by lane 0
-    for (int j = lane; j < d; j += 64) sw[j] = sw[j] * sx[j];
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (lane == 0) logits[e] = seq_sum_lds_long(sw, d);
+  if (LANES == 1 || extra) {
+    const float s = router_seq(sw, sx, d, lane);
+    if (lane == 0) {
+      if (extra) out2[t] = s;
+      else logits[(size_t)t * E + e] = s;
+    }
   } else {
     // matmul_omp, src/kernels.c:38-65: LANES FMA chains, lanes combined in the
     // build's order, then the multiply-add tail
@@ -73,7 +99,7 @@ __global__ __launch_bounds__(64) void k_router1(const float* __restrict__ W,
         s += a02 + a13;
       }
       for (int j = dm; j < d; j++) s += sw[j] * sx[j];
-      logits[e] = s;
+      logits[(size_t)t * E + e] = s;
     }
   }
 }
@@ -81,14 +107,22 @@ __global__ __launch_bounds__(64) void k_router1(const float* __restrict__ W,
 bool router1_ok(int dim) { return dim > 0 && (dim & 3) == 0 && 2 * kib_round((size_t)dim * 4) <= 64 * 1024; }
 
 hipError_t router1_launch(int order, const float* W, const float* xb, int E, int d, float* logits,
-                          hipStream_t st) {
-  if ((reinterpret_cast<uintptr_t>(W) & 15) || (reinterpret_cast<uintptr_t>(xb) & 15))
+                          hipStream_t st, int T, const float* W2, float* out2) {
+  if ((E > 0 && (reinterpret_cast<uintptr_t>(W) & 15)) || (reinterpret_cast<uintptr_t>(xb) & 15) ||
+      (W2 && (reinterpret_cast<uintptr_t>(W2) & 15)) || T < 1)
     return hipErrorInvalidValue;
   const size_t lds = 2 * kib_round((size_t)d * 4);
+  const dim3 grid(E + (W2 ? 1 : 0), T);
   switch (order) {
-    case QR_ORDER_SEQ: hipLaunchKernelGGL(k_router1<1>, dim3(E), dim3(64), lds, st, W, xb, d, logits); break;
-    case QR_ORDER_AVX2: hipLaunchKernelGGL(k_router1<8>, dim3(E), dim3(64), lds, st, W, xb, d, logits); break;
-    default: hipLaunchKernelGGL(k_router1<16>, dim3(E), dim3(64), lds, st, W, xb, d, logits); break;
+    case QR_ORDER_SEQ:
+      hipLaunchKernelGGL(k_router1<1>, grid, dim3(64), lds, st, W, xb, d, E, logits, W2, out2);
+      break;
+    case QR_ORDER_AVX2:
+      hipLaunchKernelGGL(k_router1<8>, grid, dim3(64), lds, st, W, xb, d, E, logits, W2, out2);
+      break;
+    default:
+      hipLaunchKernelGGL(k_router1<16>, grid, dim3(64), lds, st, W, xb, d, E, logits, W2, out2);
+      break;
   }
   return hipGetLastError();
 }
