@@ -647,22 +647,30 @@ static hipError_t mfma_launch_t(const MfmaArgs& a, int items, hipStream_t st) {
   }
 }
 
-// Kernel shape per product: 4 waves per workgroup, each on 16 rows, and a
+// Kernel shape per product: NW waves per workgroup (4, or 2 where a single
+// expert's product would otherwise leave CUs idle), each on 16 rows, and a
 // ring of D stages.  Measured on the Qwen3-30B-A3B layer: one slot (the least
 // LDS, the most workgroups per CU) wins where the epilogue's VALU work
 // dominates -- both products with 32-pair items, the 24-unit down product
 // always -- and two slots for gate/up with 16-pair items, whose eight stages
 // are latency bound.
 template <int TYPE, bool GATEUP, int NJ>
-static hipError_t mfma_launch_shape(const MfmaArgs& a, int items, hipStream_t st) {
-  if (GATEUP && NJ == 1) return mfma_launch_t<TYPE, GATEUP, NJ, 2, 4>(a, items, st);
-  return mfma_launch_t<TYPE, GATEUP, NJ, 1, 4>(a, items, st);
+static hipError_t mfma_launch_shape(const MfmaArgs& a, int items, int nw, bool ring,
+                                    hipStream_t st) {
+  constexpr int D = (GATEUP && NJ == 1) ? 2 : 1;
+  if (nw == 2) {
+    if (ring) return mfma_launch_t<TYPE, GATEUP, NJ, 2, 2>(a, items, st);
+    return mfma_launch_t<TYPE, GATEUP, NJ, D, 2>(a, items, st);
+  }
+  if (ring) return mfma_launch_t<TYPE, GATEUP, NJ, 2, 4>(a, items, st);
+  return mfma_launch_t<TYPE, GATEUP, NJ, D, 4>(a, items, st);
 }
 
 template <int TYPE, bool GATEUP>
-static hipError_t mfma_launch_nj(const MfmaArgs& a, int items, int tile, hipStream_t st) {
-  if (tile == 32) return mfma_launch_shape<TYPE, GATEUP, 2>(a, items, st);
-  return mfma_launch_shape<TYPE, GATEUP, 1>(a, items, st);
+static hipError_t mfma_launch_nj(const MfmaArgs& a, int items, int tile, int nw, bool ring,
+                                 hipStream_t st) {
+  if (tile == 32) return mfma_launch_shape<TYPE, GATEUP, 2>(a, items, nw, ring, st);
+  return mfma_launch_shape<TYPE, GATEUP, 1>(a, items, nw, ring, st);
 }
 
 hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const uint8_t* W2,
@@ -708,15 +716,22 @@ hipError_t expert_mfma_launch(int type, bool gateup, const uint8_t* W1, const ui
   // are read about once and the hint keeps the activation records cached;
   // with 32-pair items hot experts are re-read by several items
   a.wnt = tile <= 16;
+  // one expert (a dense product): items - 1 = ceil(P / tile) exactly; with
+  // fewer than two workgroups of 64 rows per CU, workgroups of 32 rows
+  // and a two-slot ring for its long rows (each workgroup walks them alone)
+  int nw = 4;
+  if (E == 1 && (long)((rows + 63) / 64) * (items - 1) < 2L * device_cus()) nw = 2;
+  const int stages = type == QR_T_Q8_0 ? (cols / 32 + 7) / 8 : cols / 256;
+  const bool ring = E == 1 && stages >= 8;
   switch (type) {
-    case QR_T_Q4_K: return gateup ? mfma_launch_nj<QR_T_Q4_K, true>(a, items, tile, st)
-                                  : mfma_launch_nj<QR_T_Q4_K, false>(a, items, tile, st);
-    case QR_T_Q5_K: return gateup ? mfma_launch_nj<QR_T_Q5_K, true>(a, items, tile, st)
-                                  : mfma_launch_nj<QR_T_Q5_K, false>(a, items, tile, st);
-    case QR_T_Q6_K: return gateup ? mfma_launch_nj<QR_T_Q6_K, true>(a, items, tile, st)
-                                  : mfma_launch_nj<QR_T_Q6_K, false>(a, items, tile, st);
-    case QR_T_Q8_0: return gateup ? mfma_launch_nj<QR_T_Q8_0, true>(a, items, tile, st)
-                                  : mfma_launch_nj<QR_T_Q8_0, false>(a, items, tile, st);
+    case QR_T_Q4_K: return gateup ? mfma_launch_nj<QR_T_Q4_K, true>(a, items, tile, nw, ring, st)
+                                  : mfma_launch_nj<QR_T_Q4_K, false>(a, items, tile, nw, ring, st);
+    case QR_T_Q5_K: return gateup ? mfma_launch_nj<QR_T_Q5_K, true>(a, items, tile, nw, ring, st)
+                                  : mfma_launch_nj<QR_T_Q5_K, false>(a, items, tile, nw, ring, st);
+    case QR_T_Q6_K: return gateup ? mfma_launch_nj<QR_T_Q6_K, true>(a, items, tile, nw, ring, st)
+                                  : mfma_launch_nj<QR_T_Q6_K, false>(a, items, tile, nw, ring, st);
+    case QR_T_Q8_0: return gateup ? mfma_launch_nj<QR_T_Q8_0, true>(a, items, tile, nw, ring, st)
+                                  : mfma_launch_nj<QR_T_Q8_0, false>(a, items, tile, nw, ring, st);
     default: return hipErrorInvalidValue;
   }
 }
