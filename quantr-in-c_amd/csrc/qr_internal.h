@@ -106,9 +106,13 @@ hipError_t router1_launch(int order, const float* W, const float* xb, int E, int
                           hipStream_t st, int T = 1, const float* W2 = nullptr,
                           float* out2 = nullptr);
 bool gateup1_ok(int type, int dim, int E, int K);
+// With sh_up / sh_gate (the shared expert's rows, of the routed up type and
+// width), its hb = silu(sh_up . xb) * (sh_gate . xb) into hbs as well.
 hipError_t gateup1_launch(int type, const void* up, const void* gate, size_t slice, int dim,
                           int hidden, int E, int K, const float* xb, const float* logits,
-                          int32_t* idx, float* wts, float* hb, hipStream_t st);
+                          int32_t* idx, float* wts, float* hb, hipStream_t st,
+                          const void* sh_up = nullptr, const void* sh_gate = nullptr,
+                          int sh_hidden = 0, float* hbs = nullptr);
 bool down1v2_ok(int type, int K, int dim, int hidden);
 hipError_t down1v2_launch(int type, const void* down, size_t slice, int dim, int hidden, int E,
                           int K, const float* hb, const int32_t* idx, const float* wts, float* x,

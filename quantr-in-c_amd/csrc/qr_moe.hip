@@ -665,7 +665,7 @@ static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) =
 //           dispatched in order), gate/up leaving the down product's records;
 //   else    the grouped GEMV in dense mode.
 static hipError_t shared_expert(const qr_moe_layer* L, const float* xb, int T, const MoeScratch& s,
-                                hipStream_t st, bool gate_done = false) {
+                                hipStream_t st, bool gate_done = false, bool hbs_done = false) {
   const int dim = L->dim, sh = L->sh_hidden;
   const int ut = (int)L->sh_up_type, dt = (int)L->sh_down_type;
   hipError_t e;
@@ -673,16 +673,18 @@ static hipError_t shared_expert(const qr_moe_layer* L, const float* xb, int T, c
   const bool aligned = al16(L->sh_up) && al16(L->sh_gate) && al16(L->sh_down) && al16(xb);
   if (T <= 4 && same_up && aligned && sh_gemv_type(ut) && sh_gemv_type(dt) &&
       dim % qr_block_elems(ut) == 0 && sh % qr_block_elems(dt) == 0) {
-    if ((e = gemv_launch(ut, kQ8Seq, L->sh_up, xb, s.ush, sh, dim, T, dim, sh, nullptr, nullptr,
-                         st)) != hipSuccess)
-      return e;
-    if ((e = gemv_launch(ut, kQ8Seq, L->sh_gate, xb, s.hbs, sh, dim, T, dim, sh, nullptr, nullptr,
-                         st)) != hipSuccess)
-      return e;
-    const long n = (long)T * sh;
-    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s.ush,
-                       s.hbs, n);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (!hbs_done) {  // else the one-token gate/up launch wrote hbs
+      if ((e = gemv_launch(ut, kQ8Seq, L->sh_up, xb, s.ush, sh, dim, T, dim, sh, nullptr, nullptr,
+                           st)) != hipSuccess)
+        return e;
+      if ((e = gemv_launch(ut, kQ8Seq, L->sh_gate, xb, s.hbs, sh, dim, T, dim, sh, nullptr,
+                           nullptr, st)) != hipSuccess)
+        return e;
+      const long n = (long)T * sh;
+      hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s.ush,
+                         s.hbs, n);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     if ((e = gemv_launch(dt, kQ8Seq, L->sh_down, s.hbs, s.ysh, dim, sh, T, sh, dim, nullptr,
                          nullptr, st)) != hipSuccess)
       return e;
@@ -768,11 +770,18 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
     e = router1_launch(order, L->router, xb, E, L->dim, s.logits, st, 1,
                        sg ? static_cast<const float*>(L->sh_gate_inp) : nullptr, s.sgl);
     if (e != hipSuccess) return e;
+    // the shared expert's up/gate rows as more tiles of the same launch when
+    // they share the routed up type (its down product then on the GEMV)
+    const bool sg_up = sh && L->sh_up_type == L->up_type && L->sh_gate_type == L->up_type &&
+                       sh_gemv_type((int)L->sh_down_type) &&
+                       L->sh_hidden % qr_block_elems((int)L->sh_down_type) == 0 &&
+                       al16(L->sh_up) && al16(L->sh_gate) && al16(L->sh_down);
     e = gateup1_launch((int)L->up_type, L->up, L->gate, su, L->dim, L->hidden, E, K, xb, s.logits,
-                       s.idx, s.wts, s.hb, st);
+                       s.idx, s.wts, s.hb, st, sg_up ? L->sh_up : nullptr,
+                       sg_up ? L->sh_gate : nullptr, L->sh_hidden, s.hbs);
     if (e != hipSuccess) return e;
     if (sh) {
-      e = shared_expert(L, xb, T, s, st, sg);
+      e = shared_expert(L, xb, T, s, st, sg, sg_up);
       if (e != hipSuccess) return e;
     }
     return down1v2_launch((int)L->down_type, L->down, sd, L->dim, L->hidden, E, K, s.hb, s.idx,

@@ -140,6 +140,12 @@ struct GateUp1Args {
   int32_t* idx;         // [K] out (workgroup 0)
   float* wts;           // [K] out (workgroup 0)
   float* hb;            // [K][hidden]
+  // optional: the shared expert's up / gate rows (same type and width),
+  // computed as tiles after the routed ones into hbs
+  const uint8_t* sh_up;
+  const uint8_t* sh_gate;
+  int sh_hidden;        // 0: none
+  float* hbs;           // [sh_hidden]
 };
 
 // LDS: activation staging | activation (NIB/NAT) | routing row | slots
@@ -166,10 +172,13 @@ __global__ __launch_bounds__(64 * kBlkWaves) void k_gateup1(GateUp1Args a) {
   const int rl = l / nb, b = l - rl * nb;
   const size_t rb = (size_t)nb * BB;
   const int tiles_per_slot = (a.hidden + RB - 1) / RB;
+  const int routed = a.K * tiles_per_slot;  // then the shared expert's tiles
   const int tile = blockIdx.x * kBlkWaves + wave;
-  const bool wave_on = tile < a.K * tiles_per_slot;
-  const int k = wave_on ? tile / tiles_per_slot : 0;
-  const int r0 = (tile - k * tiles_per_slot) * RB;
+  const bool shared = tile >= routed;  // uniform per wave
+  const bool wave_on = tile < routed + (a.sh_hidden + RB - 1) / RB;
+  const int k = wave_on && !shared ? tile / tiles_per_slot : 0;
+  const int r0 = shared ? (tile - routed) * RB : (tile - k * tiles_per_slot) * RB;
+  const int nrows = shared ? a.sh_hidden : a.hidden;
   size_t o_act, o_pw, o_slots;
   gateup1_lds(TYPE, a.dim, &o_act, &o_pw, &o_slots);
   uint8_t* act = smem + o_act;
@@ -201,16 +210,17 @@ __global__ __launch_bounds__(64 * kBlkWaves) void k_gateup1(GateUp1Args a) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   if (blockIdx.x == 0 && wave == 0) route_write(pw, a.K, lane, a.idx, a.wts);
-  const int e = wave_on ? __builtin_amdgcn_readfirstlane(sidx[k]) : -1;
-  const bool ok = wave_on && e >= 0 && e < a.E;  // uniform per wave
+  const int e = wave_on && !shared ? __builtin_amdgcn_readfirstlane(sidx[k]) : -1;
+  const bool ok = wave_on && (shared || (e >= 0 && e < a.E));  // uniform per wave
   if (!ok) return;  // no barriers below
   // 2. the weight tile: up rows r0.. at slot bytes [0, RB rb), the same gate
   //    rows at [32 BB, 32 BB + RB rb): lane l reads its block at l * BB
   {
-    const int rows = min(RB, a.hidden - r0);
+    const int rows = min(RB, nrows - r0);
     const int valid = rows * (int)rb;
-    const uint8_t* ub = a.up + (size_t)e * a.slice + (size_t)r0 * rb;
-    const uint8_t* gb = a.gate + (size_t)e * a.slice + (size_t)r0 * rb;
+    const uint8_t* ub = shared ? a.sh_up + (size_t)r0 * rb : a.up + (size_t)e * a.slice + (size_t)r0 * rb;
+    const uint8_t* gb =
+        shared ? a.sh_gate + (size_t)r0 * rb : a.gate + (size_t)e * a.slice + (size_t)r0 * rb;
     const uint32_t sbase = lds_u32addr(slot);
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
@@ -236,8 +246,10 @@ __global__ __launch_bounds__(64 * kBlkWaves) void k_gateup1(GateUp1Args a) {
   const float g = __shfl(y[0], lane + 32);  // gate row chain of the same row
   const float sv = qr_silu_w(y[0], tab);  // every lane
   const int row = r0 + rl;
-  if (half == 0 && rl < RB && row < a.hidden && b == nb - 1)
-    a.hb[(size_t)k * a.hidden + row] = sv * g;
+  if (half == 0 && rl < RB && row < nrows && b == nb - 1) {
+    if (shared) a.hbs[row] = sv * g;
+    else a.hb[(size_t)k * a.hidden + row] = sv * g;
+  }
 }
 
 bool gateup1_ok(int type, int dim, int E, int K) {
@@ -250,7 +262,8 @@ bool gateup1_ok(int type, int dim, int E, int K) {
 
 hipError_t gateup1_launch(int type, const void* up, const void* gate, size_t slice, int dim,
                           int hidden, int E, int K, const float* xb, const float* logits,
-                          int32_t* idx, float* wts, float* hb, hipStream_t st) {
+                          int32_t* idx, float* wts, float* hb, hipStream_t st, const void* sh_up,
+                          const void* sh_gate, int sh_hidden, float* hbs) {
   GateUp1Args a;
   a.up = static_cast<const uint8_t*>(up);
   a.gate = static_cast<const uint8_t*>(gate);
@@ -264,8 +277,15 @@ hipError_t gateup1_launch(int type, const void* up, const void* gate, size_t sli
   a.idx = idx;
   a.wts = wts;
   a.hb = hb;
+  a.sh_up = static_cast<const uint8_t*>(sh_up);
+  a.sh_gate = static_cast<const uint8_t*>(sh_gate);
+  a.sh_hidden = sh_up && sh_gate && hbs ? sh_hidden : 0;
+  a.hbs = hbs;
+  if (a.sh_hidden && ((reinterpret_cast<uintptr_t>(sh_up) & 15) ||
+                      (reinterpret_cast<uintptr_t>(sh_gate) & 15)))
+    return hipErrorInvalidValue;
   const int RB = 32 / (dim >> 8);
-  const int tiles = K * ((hidden + RB - 1) / RB);
+  const int tiles = K * ((hidden + RB - 1) / RB) + (a.sh_hidden + RB - 1) / RB;
   const int grid = (tiles + kBlkWaves - 1) / kBlkWaves;
   size_t o1, o2, o3;
   const size_t lds = gateup1_lds(type, dim, &o1, &o2, &o3);
