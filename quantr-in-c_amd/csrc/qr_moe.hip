@@ -799,7 +799,16 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
       (reinterpret_cast<uintptr_t>(L->router) & 15) == 0) {
     const int kTile = mfma_tile(T, K, E);  // pairs per MFMA work item
     const bool perm_x = L->up_type != QR_T_Q8_0;
-    e = rlogits_launch(order, L->router, xb, T, E, L->dim, s.logits, st);
+    // the sequential order for up to 64 tokens: one workgroup per (row,
+    // token), the shared expert's gate logit beside them
+    bool sg = false;
+    if (order == QR_ORDER_SEQ && T <= 64 && router1_ok(L->dim) && al16(xb)) {
+      sg = sh && al16(L->sh_gate_inp);
+      e = router1_launch(order, L->router, xb, E, L->dim, s.logits, st, T,
+                         sg ? static_cast<const float*>(L->sh_gate_inp) : nullptr, s.sgl);
+    } else {
+      e = rlogits_launch(order, L->router, xb, T, E, L->dim, s.logits, st);
+    }
     if (e != hipSuccess) return e;
     e = route_rank_launch(s.logits, T, E, K, nullptr, s.idx, s.wts, xb, L->dim, perm_x, s.xq, st);
     if (e != hipSuccess) return e;
@@ -817,7 +826,7 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
                            L->dim, items, kTile, nullptr, false, st);
     if (e != hipSuccess) return e;
     if (sh) {
-      e = shared_expert(L, xb, T, s, st);
+      e = shared_expert(L, xb, T, s, st, sg);
       if (e != hipSuccess) return e;
     }
     return combine_launch(x, s.y, s.inv, s.wts, T, K, L->dim, sh ? s.ysh : nullptr, s.sgl, st);
