@@ -891,6 +891,19 @@ hipError_t matmul_q_dev(const void* w, uint32_t type, int order, const float* x,
   return gemv_launch((int)type, order, w, x, y, n, dd, 1, dd, n, nullptr, nullptr, s);
 }
 
+// wq and wk as one matrix of qd + kvd rows: the same type and width, wk's
+// bytes right after wq's (in the tiled layout, wq a whole number of tiles,
+// so the two tilings concatenate into the tiling of the stacked rows), and
+// the decoder's k buffer right after q -- one GEMV launch instead of two.
+static bool qk_stacked(const qr_decoder* d, const qr_layer& L) {
+  if (L.wq_type != L.wk_type || L.wq_type == QR_T_F32 || !L.wq || !L.wk) return false;
+  if (d->k != d->q + d->qd) return false;
+  const int base = (int)(L.wq_type & ~(uint32_t)QR_TILED);
+  if ((L.wq_type & QR_TILED) && d->qd % (64 / (d->dim >> 8)) != 0) return false;
+  const size_t qbytes = qr_wrow_bytes(base, d->dim) * (size_t)d->qd;
+  return static_cast<const uint8_t*>(L.wk) == static_cast<const uint8_t*>(L.wq) + qbytes;
+}
+
 // The decode step's kernels, in order, on stream s (the state holds the
 // token and the position).
 hipError_t enqueue_step(qr_decoder* d, float* logits, float* xout, hipStream_t s) {
@@ -904,8 +917,13 @@ hipError_t enqueue_step(qr_decoder* d, float* logits, float* xout, hipStream_t s
   for (int l = 0; l < d->nl; l++) {
     const qr_layer& L = d->layers[l];
     if ((e = rmsnorm_launch(d->x, nullptr, L.rms_att, dim, d->xb, s))) return e;
-    if ((e = matmul_q_dev(L.wq, L.wq_type, d->order, d->xb, d->q, d->qd, dim, s))) return e;
-    if ((e = matmul_q_dev(L.wk, L.wk_type, d->order, d->xb, d->k, d->kvd, dim, s))) return e;
+    if (qk_stacked(d, L)) {
+      if ((e = matmul_q_dev(L.wq, L.wq_type, d->order, d->xb, d->q, d->qd + d->kvd, dim, s)))
+        return e;
+    } else {
+      if ((e = matmul_q_dev(L.wq, L.wq_type, d->order, d->xb, d->q, d->qd, dim, s))) return e;
+      if ((e = matmul_q_dev(L.wk, L.wk_type, d->order, d->xb, d->k, d->kvd, dim, s))) return e;
+    }
     if ((e = matmul_q_dev(L.wv, L.wv_type, d->order, d->xb, d->v, d->kvd, dim, s))) return e;
     const KvView K = kv_view(d, l, false), V = kv_view(d, l, true);
     hipLaunchKernelGGL(k_rope_kv, dim3((d->qd / 2 + 2 * (d->kvd / 32) + 255) / 256), dim3(256), 0,

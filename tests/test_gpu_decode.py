@@ -112,6 +112,50 @@ def test_decoder_q8_cache_head128(dev, oracle, order, graph):
     assert_bits_equal(lg, wl, "logits")
 
 
+@pytest.mark.parametrize("tiled", [False, True], ids=["rows", "tiled"])
+def test_decoder_stacked_qk(dev, oracle, tiled):
+    """wq and wk of one type stored back to back (the decoder then runs them
+    as one GEMV of q_dim + kv_dim rows), row-major and in the tiled layout:
+    three decode steps over a Q8_0 cache, bit-exact with the oracle."""
+    m = I.qwen3_small_model(n_layers=2, seq_len=640)
+    H, KVH, hd, dim = m["n_heads"], m["n_kv_heads"], m["head_dim"], m["dim"]
+    wt = list(m["wtype"])
+    wt[1] = Q.TYPE_Q4_K
+    m["wtype"] = wt
+    keep = []
+    for l, lw in enumerate(m["layers"]):
+        lw["wk"] = I._rows(9700 + l, Q.TYPE_Q4_K, KVH * hd, dim)
+    npre = 130
+    kv, kc, vc = prefilled(oracle, m, npre, seed=43)
+    mdev = dict(m)
+    mdev["layers"] = [dict(lw) for lw in m["layers"]]
+    for lw in mdev["layers"]:
+        qb, kb = lw["wq"].reshape(-1), lw["wk"].reshape(-1)
+        both = dev.upload(np.concatenate([qb, kb]))
+        keep.append(both)
+        if tiled:
+            t = dev.alloc(qb.nbytes + kb.nbytes)
+            keep.append(t)
+            dev.tile(Q.TYPE_Q4_K, both.ptr, t.ptr, H * hd + KVH * hd, dim)
+            dev.sync()
+            both = t
+        lw["wq"], lw["wk"] = both.ptr, both.ptr + qb.nbytes
+    if tiled:
+        mdev["wtype"] = [wt[0] | Q.TILED, wt[1] | Q.TILED, wt[2], wt[3]]
+    print("decode stacked qk tiled %d" % tiled, flush=True)
+    d = make_decoder(dev, mdev, Q.KV_Q8_0, ORDER_AVX2, page=64)
+    for l in range(m["n_layers"]):
+        kb, vb = dev.upload(kv[l, 0]), dev.upload(kv[l, 1])
+        d.kv_write(l, 0, npre, kb.ptr, vb.ptr)
+    toks = [5, 300, 77]
+    lg, xs = run_tokens(dev, d, mdev, toks, pos0=npre)
+    d.close()
+    wl, wx = oracle.forward_cached(m, kc.reshape(-1), vc.reshape(-1), toks, npre, ORDER_AVX2,
+                                   Q.KV_Q8_0)
+    assert_bits_equal(xs, wx, "residual")
+    assert_bits_equal(lg, wl, "logits")
+
+
 @pytest.mark.parametrize("qtype", [Q.TYPE_F32, Q.TYPE_Q8_0, Q.TYPE_Q4_K, Q.TYPE_Q5_K,
                                    Q.TYPE_Q6_K])
 def test_dequantize(dev, oracle, qtype):
