@@ -366,12 +366,29 @@ constexpr size_t kDecLdsMax = 160 * 1024;
 // per (head, position) adds the hd products in order; a thread runs the
 // chains of heads m and m + 4 side by side, which share the K row.  Dynamic
 // LDS: (64 (hd + 4) + kv_mul hd) floats.
+//
+// ROPE (the decode step, one token): q and k arrive unrotated and this
+// kernel does k_rope_kv's work as well -- each workgroup rotates its query
+// heads while staging them, and the workgroup whose tile holds the current
+// position rotates kv head blockIdx.y's k, stores its K and V blocks in the
+// cache rows of that position and puts the K row (as the cache holds it) in
+// its LDS tile directly.
 constexpr int kScTile = 64;
 
+struct RopeArgs {
+  const float* rope;  // [cap][q_dim] (cos, sin) pairs
+  const float* k;     // [kv_dim] unrotated
+  const float* v;     // [kv_dim]
+  uint8_t* vbase;     // V pages (same layout as K's)
+  int qd;
+};
+
+template <bool ROPE>
 __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q, KvView K,
                                                      const int32_t* __restrict__ st, int npos_arg,
                                                      int kv_mul, int hd, float inv_sqrt,
-                                                     int att_stride, float* __restrict__ att) {
+                                                     int att_stride, float* __restrict__ att,
+                                                     RopeArgs R) {
   extern __shared__ __align__(16) float sm[];
   // blockIdx.z: token t of a batch (q + t n_heads hd, att + t n_heads att_stride, st + 2 t)
   const int nh = gridDim.y * kv_mul;
@@ -386,13 +403,75 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
   float* kt = sm;
   float* qs = sm + kScTile * ks;
   const int nt = min(kScTile, npos - t0);
-  for (int i = threadIdx.x * 4; i < kv_mul * hd; i += blockDim.x * 4)
-    *reinterpret_cast<float4*>(qs + i) =
-        *reinterpret_cast<const float4*>(q + (size_t)kvh * kv_mul * hd + i);
+  // ROPE: the current position's row within this tile, else -1
+  const int cur = ROPE ? npos - 1 - t0 : -1;
+  const float* cs = ROPE ? R.rope + (size_t)(npos - 1) * R.qd : nullptr;
+  for (int i = threadIdx.x * 4; i < kv_mul * hd; i += blockDim.x * 4) {
+    const size_t e = (size_t)kvh * kv_mul * hd + i;
+    float4 a = *reinterpret_cast<const float4*>(q + e);
+    if constexpr (ROPE) {  // k_rope_kv's rotation of two pairs
+      const float4 c = *reinterpret_cast<const float4*>(cs + e);
+      const float4 r = a;
+      a.x = r.x * c.x - r.y * c.y;
+      a.y = r.x * c.y + r.y * c.x;
+      a.z = r.z * c.z - r.w * c.w;
+      a.w = r.z * c.w + r.w * c.z;
+    }
+    *reinterpret_cast<float4*>(qs + i) = a;
+  }
+  if (ROPE && cur >= 0 && cur < kScTile && (int)threadIdx.x < 2 * (hd / 32)) {
+    // block b of kv head kvh's k (rotated) or v, at the current position
+    const int nbh = hd / 32;
+    const bool isv = (int)threadIdx.x >= nbh;
+    const int b = isv ? (int)threadIdx.x - nbh : (int)threadIdx.x;
+    const size_t e = (size_t)kvh * hd + 32 * b;
+    float vals[32];
+    const float4* src = reinterpret_cast<const float4*>((isv ? R.v : R.k) + e);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float4 f = src[j];
+      vals[4 * j] = f.x;
+      vals[4 * j + 1] = f.y;
+      vals[4 * j + 2] = f.z;
+      vals[4 * j + 3] = f.w;
+    }
+    if (!isv) {
+      const float4* c4 = reinterpret_cast<const float4*>(cs + e);
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const float4 c = c4[j];
+        const float k0 = vals[4 * j], k1 = vals[4 * j + 1], k2 = vals[4 * j + 2], k3 = vals[4 * j + 3];
+        vals[4 * j] = k0 * c.x - k1 * c.y;
+        vals[4 * j + 1] = k0 * c.y + k1 * c.x;
+        vals[4 * j + 2] = k2 * c.z - k3 * c.w;
+        vals[4 * j + 3] = k2 * c.w + k3 * c.z;
+      }
+    }
+    uint8_t* krow = const_cast<uint8_t*>(K.row(npos - 1));
+    uint8_t* row = isv ? R.vbase + (size_t)(krow - K.base) : krow;
+    float* dst = kt + cur * ks + 32 * b;
+    if (K.kv_type == QR_KV_Q8_0) {
+      uint8_t* blk = row + (size_t)(kvh * nbh + b) * QR_Q8_BYTES;
+      q8_block_store(vals, blk);
+      if (!isv) {  // the row as the cache holds it
+        const float d = qr_h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+#pragma unroll
+        for (int j = 0; j < 32; j++) dst[j] = (float)(int8_t)blk[2 + j] * d;
+      }
+    } else {
+      float* out = reinterpret_cast<float*>(row) + (size_t)kvh * hd + 32 * b;
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        out[j] = vals[j];
+        if (!isv) dst[j] = vals[j];
+      }
+    }
+  }
   if (K.kv_type == QR_KV_Q8_0) {
     const int bpr = hd / 32;
     for (int j = threadIdx.x; j < nt * bpr; j += blockDim.x) {
       const int tt = j / bpr, b = j - tt * bpr;
+      if (ROPE && tt == cur) continue;  // staged above
       const uint16_t* hw =
           reinterpret_cast<const uint16_t*>(K.row(t0 + tt) + (size_t)(kvh * bpr + b) * QR_Q8_BYTES);
       uint32_t u[17];
@@ -413,6 +492,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
   } else {
     for (int j = threadIdx.x * 4; j < nt * hd; j += blockDim.x * 4) {
       const int tt = j / hd, i = j - tt * hd;
+      if (ROPE && tt == cur) continue;  // staged above
       *reinterpret_cast<float4*>(kt + tt * ks + i) = *reinterpret_cast<const float4*>(
           reinterpret_cast<const float*>(K.row(t0 + tt)) + (size_t)kvh * hd + i);
     }
@@ -855,6 +935,7 @@ struct qr_decoder {
 namespace {
 
 std::atomic<bool> g_sc_opt[64];
+std::atomic<bool> g_sc_opt_r[64];
 std::atomic<bool> g_sm_opt[64];
 std::atomic<bool> g_sm_opt2[64];
 std::atomic<bool> g_rows_opt[64];
@@ -926,13 +1007,11 @@ hipError_t enqueue_step(qr_decoder* d, float* logits, float* xout, hipStream_t s
     }
     if ((e = matmul_q_dev(L.wv, L.wv_type, d->order, d->xb, d->v, d->kvd, dim, s))) return e;
     const KvView K = kv_view(d, l, false), V = kv_view(d, l, true);
-    hipLaunchKernelGGL(k_rope_kv, dim3((d->qd / 2 + 2 * (d->kvd / 32) + 255) / 256), dim3(256), 0,
-                       s, d->q, d->k, d->v, d->rope, d->st, d->qd, d->kvd, K,
-                       const_cast<uint8_t*>(V.base));
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_scores, dim3((d->cap + kScTile - 1) / kScTile, d->nkv), dim3(256),
-                       d->sc_lds, s, d->q, K, d->st, 0, d->kv_mul, d->hd, inv_sqrt, d->cap,
-                       d->att);
+    // RoPE, the position's K / V rows and the scores in one launch
+    const RopeArgs R{d->rope, d->k, d->v, const_cast<uint8_t*>(V.base), d->qd};
+    hipLaunchKernelGGL(k_attn_scores<true>, dim3((d->cap + kScTile - 1) / kScTile, d->nkv),
+                       dim3(256), d->sc_lds, s, d->q, K, d->st, 0, d->kv_mul, d->hd, inv_sqrt,
+                       d->cap, d->att, R);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = sv_launch(d->att, d->cap, V, d->st, 0, d->cap, d->nh, d->kv_mul, d->hd, d->ao, s)))
       return e;
@@ -1040,8 +1119,9 @@ hipError_t enqueue_prefill_chunk(qr_decoder* d, int T, const int32_t* st, hipStr
                        0, s, d->pq, d->pk, d->pv, d->rope, st, d->qd, d->kvd, K,
                        const_cast<uint8_t*>(V.base));
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_scores, dim3((d->cap + kScTile - 1) / kScTile, d->nkv, T), dim3(256),
-                       d->sc_lds, s, d->pq, K, st, 0, d->kv_mul, d->hd, inv_sqrt, d->cap, d->patt);
+    hipLaunchKernelGGL(k_attn_scores<false>, dim3((d->cap + kScTile - 1) / kScTile, d->nkv, T),
+                       dim3(256), d->sc_lds, s, d->pq, K, st, 0, d->kv_mul, d->hd, inv_sqrt, d->cap,
+                       d->patt, RopeArgs{});
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = sv_rows_launch(d->patt, d->cap, V, st, d->cap, d->nh, d->kv_mul, d->hd, d->pao, T,
                             s)))
@@ -1167,7 +1247,7 @@ int qr_attention(qr_ctx* c, const float* q, const void* kc, const void* vc, cons
   const size_t sc_lds = ((size_t)kScTile * (head_dim + 4) + (size_t)kv_mul * head_dim) * 4;
   if (sc_lds > kDecLdsMax) return set_error(QR_ERR_UNSUPPORTED, "qr_attention: head group too large");
   DEC_HIP(hipSetDevice(ctx_device(c)), "hipSetDevice");
-  DEC_HIP(lds_opt_in((const void*)k_attn_scores, g_sc_opt), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_scores<false>, g_sc_opt), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_Q8_0>, g_sm_opt), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_F32>, g_sm_opt2), "lds opt-in");
   KvView K;
@@ -1181,9 +1261,9 @@ int qr_attention(qr_ctx* c, const float* q, const void* kc, const void* vc, cons
   V.base = static_cast<const uint8_t*>(vc);
   hipStream_t s = ctx_stream(c);
   const float inv_sqrt = 1.0f / sqrtf((float)head_dim);
-  hipLaunchKernelGGL(k_attn_scores, dim3((npos + kScTile - 1) / kScTile, n_kv_heads), dim3(256),
-                     sc_lds, s, q, K, (const int32_t*)nullptr, npos, kv_mul, head_dim, inv_sqrt,
-                     npos, att);
+  hipLaunchKernelGGL(k_attn_scores<false>, dim3((npos + kScTile - 1) / kScTile, n_kv_heads),
+                     dim3(256), sc_lds, s, q, K, (const int32_t*)nullptr, npos, kv_mul, head_dim,
+                     inv_sqrt, npos, att, RopeArgs{});
   DEC_HIP(hipGetLastError(), "k_attn_scores");
   DEC_HIP(sv_launch(att, npos, V, nullptr, npos, npos, n_heads, kv_mul, head_dim, out, s),
           "k_attn_sv");
@@ -1240,7 +1320,8 @@ int qr_decoder_create(qr_ctx* c, const qr_model* m, int kv_type, int order, int 
   if (sc_lds > kDecLdsMax) return set_error(QR_ERR_UNSUPPORTED, "qr_decoder_create: head group too large");
 
   DEC_HIP(hipSetDevice(ctx_device(c)), "hipSetDevice");
-  DEC_HIP(lds_opt_in((const void*)k_attn_scores, g_sc_opt), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_scores<false>, g_sc_opt), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_scores<true>, g_sc_opt_r), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_Q8_0>, g_sm_opt), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_F32>, g_sm_opt2), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv_rows<QR_KV_Q8_0>, g_rows_opt), "lds opt-in");
