@@ -91,32 +91,8 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ tab, 
 // ---------------------------------------------------------------------------
 // Sequential sums.  The reference adds n terms one at a time (rmsnorm's sum
 // of squares, softmax's denominator, each attention value); one lane does the
-// same here, the terms produced in parallel beforehand and read from LDS in
-// batches while earlier reads are still in flight.  The long sums take 256
-// terms per batch in two register buffers of 32 (a buffer's reads are issued
-// before the other buffer's adds): measured on the 4097-position decode
-// attention, 42.7 against 44.2 us; RMSNorm's 2048 terms are faster in
-// batches of 16 (8.9 against 9.3 us).
-// ---------------------------------------------------------------------------
-// Short sums (RMSNorm's 2048 squares): 16 values per read batch.
-__device__ inline float seq_sum_lds(const float* __restrict__ p, int n) {
-  float s = 0.0f;
-  int i = 0;
-  for (; i + 16 <= n; i += 16) {
-    float4 v[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) v[k] = *reinterpret_cast<const float4*>(p + i + 4 * k);
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      s += v[k].x;
-      s += v[k].y;
-      s += v[k].z;
-      s += v[k].w;
-    }
-  }
-  for (; i < n; i++) s += p[i];
-  return s;
-}
+// same here (seq_sum_lds_long, qr_common.h), the terms produced in parallel
+// beforehand and read from LDS 32 adds ahead of their use.
 
 // ---------------------------------------------------------------------------
 // rmsnorm_ref (src/kernels.c:170-180), optionally after x += add (the
@@ -173,7 +149,7 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ x,
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-      float ss = seq_sum_lds(sq, n);
+      float ss = seq_sum_lds_long(sq, n);
       ss = ss / (float)n + 1e-5f;
       scale_s = 1.0f / sqrtf(ss);
     }
@@ -202,7 +178,7 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ x,
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-      float ss = seq_sum_lds(sq, n);
+      float ss = seq_sum_lds_long(sq, n);
       ss = ss / (float)n + 1e-5f;
       scale_s = 1.0f / sqrtf(ss);
     }
@@ -546,13 +522,14 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
 //     its order does not matter; seeded with the first score, strict '>');
 //     the exponentials in parallel, in place.
 //  2. Lane 0 adds the exponentials in order (the softmax denominator) while
-//     waves 1 and 2 start loading the V values of the first two position
-//     blocks.
-//  3. Waves 1 and 2 form the products (e[t] * inv) * v of a block of kValBlk
+//     waves 1, 2, 3 and 5 start loading the V values of the first two
+//     position blocks.
+//  3. Waves 1, 2, 3 and 5 form the products (e[t] * inv) * v of a block of kValBlk
 //     positions into LDS, element-major (one ds_read_b128 gives an element
 //     four consecutive positions), while lanes 0..31 of wave 0 add the
 //     previous block's products in position order.  Each block's V loads are
-//     issued two blocks ahead of their use.  Waves 3..7 only help in step 1.
+//     issued two blocks ahead of their use.  Waves 4, 6 and 7 only help in
+//     step 1.
 // Dynamic LDS: npos floats (the exponentials), then ceil(npos / page) ints
 // (this layer's page table).  att is only read.
 constexpr int kValCols = 32;
@@ -561,9 +538,9 @@ constexpr int kValPitch = kValBlk + 4;
 constexpr int kSvThreads = 512;
 constexpr int kAttnMaxPos = 22528;  // exponentials (LDS) beside the product buffers
 
-// Producer threads (waves 1 and 2) take positions pid and pid + 128 of a
-// block: the raw V values of their kValCols elements.
-constexpr int kSvProd = 128;
+// Producer threads (four waves) take position pid of a block: the raw V
+// values of their kValCols elements.
+constexpr int kSvProd = 256;
 constexpr int kSvPer = kValBlk / kSvProd;
 struct SvRegs {
   uint32_t r[kSvPer][kValCols];  // Q8_0: [0] = d, [1..8] = the 32 qs bytes; fp32: the values
@@ -662,8 +639,11 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_sv(const float* __restrict_
   const int kvh = h / kv_mul;
   const float* a = att + (size_t)h * att_stride;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int pid = threadIdx.x - 64;  // producer index: waves 1 and 2 (pid < kSvProd)
-  const bool producer = wave > 0 && pid < kSvProd;
+  // producers: waves 1, 2, 3 and 5 (pid 0..255); wave 4 would share wave 0's
+  // SIMD (a workgroup's waves go to the SIMDs in turn) and slow its chain
+  const int pw = wave < 4 ? wave - 1 : wave - 2;
+  const int pid = pw * 64 + lane;
+  const bool producer = wave != 0 && wave != 4 && pid < kSvProd;
   const ExpTab tab = qr_expf_tab();
 
   // 1. scores -> LDS and their max; eight loads in flight per thread
@@ -801,7 +781,7 @@ __global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ 
     if (i < npos) e[i] = ev;
   }
   __syncthreads();
-  if (tid == 0) inv_s = 1.0f / seq_sum_lds_long(e, npos);
+  if (tid == 0) inv_s = 1.0f / seq_sum_lds_short(e, npos);
   __syncthreads();
   const float inv = inv_s;
   for (int i = tid; i < npos; i += nthr) e[i] = e[i] * inv;  // softmax_ref's x[i] *= inv
