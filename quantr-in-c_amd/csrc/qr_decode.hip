@@ -789,12 +789,34 @@ __global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ 
   if (tid >= hd) return;
   const int col = (h / kv_mul) * hd + tid;
   float acc = 0.0f;
-  constexpr int U = 8;  // positions whose values are loaded ahead of their adds
+  constexpr int U = 32;  // positions whose values are loaded ahead of their adds
   int t = 0;
-  for (; t + U <= npos; t += U) {
-    float v[U];
+  // groups of U positions at t % U == 0 lie in one page when U <= page (both
+  // powers of two): one page-table read per group, the rows' addresses then
+  // known without waiting on a scalar load each
+  if (V.page >= U) {
+    for (; t + U <= npos; t += U) {
+      const uint8_t* row0 = V.row(t);
+      float v[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) {
+      for (int u = 0; u < U; u++) {
+        const uint8_t* row = row0 + (size_t)u * V.row_bytes;
+        if constexpr (KVT == QR_KV_Q8_0) {
+          const uint8_t* blk = row + (size_t)(col >> 5) * QR_Q8_BYTES;
+          const float d = qr_h2f(*reinterpret_cast<const uint16_t*>(blk));
+          v[u] = (float)(int8_t)blk[2 + (col & 31)] * d;
+        } else {
+          v[u] = reinterpret_cast<const float*>(row)[col];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++) acc += e[t + u] * v[u];
+    }
+  }
+  for (; t + 8 <= npos; t += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
       const uint8_t* row = V.row(t + u);  // one address per wave: the page table by scalar loads
       if constexpr (KVT == QR_KV_Q8_0) {
         const uint8_t* blk = row + (size_t)(col >> 5) * QR_Q8_BYTES;
@@ -805,7 +827,7 @@ __global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ 
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; u++) acc += e[t + u] * v[u];
+    for (int u = 0; u < 8; u++) acc += e[t + u] * v[u];
   }
   for (; t < npos; t++) {
     const uint8_t* row = V.row(t);

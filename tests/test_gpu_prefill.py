@@ -96,17 +96,18 @@ def _kv_rows(dev, d, L, positions, rs):
     return np.stack(out)
 
 
-@pytest.mark.parametrize("source", ["pointers", "gguf_tiled"])
-def test_prefill_head128_chunks(dev, source):
+@pytest.mark.parametrize("source,page", [("pointers", 64), ("gguf_tiled", 64), ("pointers", 16)])
+def test_prefill_head128_chunks(dev, source, page):
     """300 prompt tokens of a head_dim-128 model (q_dim 1024 != dim 512, GQA
-    4:1) over a Q8_0 cache in permuted pages of 64, prefilled in chunks of 128
+    4:1) over a Q8_0 cache in permuted pages of 64 (16: pages smaller than
+    the attention values' 32-position groups), prefilled in chunks of 128
     (the projections as MFMA row products), against 300 sequential decode
     steps: every token's logits, the last residual and the cache rows."""
     m = I.qwen3_small_model(n_layers=2, seq_len=320)
     rng = np.random.default_rng(9)
     toks = rng.integers(0, m["vocab"], size=300).astype(np.int32)
     order = ORDER_AVX2
-    ref = make_decoder(dev, m, Q.KV_Q8_0, order, page=64, flags=Q.DEC_GRAPH)
+    ref = make_decoder(dev, m, Q.KV_Q8_0, order, page=page, flags=Q.DEC_GRAPH)
     ppl, _ = ref.pages()
     table = np.stack([rng.permutation(ppl) for _ in range(m["n_layers"])]).astype(np.int32)
     ref.set_pages(table)
@@ -120,9 +121,9 @@ def test_prefill_head128_chunks(dev, source):
         gf = Q.Gguf(G.decode_model_gguf(m, head_dim_key=True)[0])
         gm = gf.load(dev, m["seq_len"])
         assert gm.layers[0].wq_type == Q.TYPE_Q4_K | Q.TILED
-        d = gm.decoder(kv_type=Q.KV_Q8_0, order=order, page=64)
+        d = gm.decoder(kv_type=Q.KV_Q8_0, order=order, page=page)
     else:
-        d = make_decoder(dev, m, Q.KV_Q8_0, order, page=64)
+        d = make_decoder(dev, m, Q.KV_Q8_0, order, page=page)
     d.set_pages(table)
     print("prefill head128 %s" % source, flush=True)
     lg, x = prefill(dev, d, m, toks, chunk=128)
