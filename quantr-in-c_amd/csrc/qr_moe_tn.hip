@@ -217,22 +217,65 @@ __global__ __launch_bounds__(256) void k_rlogits4(const float* __restrict__ W,
     const float* sw = sm + (c % NBUF) * BUF + (rb * RT) * kRlRs;
     const float* sx = sm + (c % NBUF) * BUF + (RW + tb * TT) * kRlRs;
     const int jend = min(dm, (c + 1) * kRlCk) - c * kRlCk;
-#pragma unroll 4
-    for (int j = 4 * cg; j < jend; j += LANES) {
-      float4 wv[RT], xv[TT];
+    if (jend == kRlCk) {
+      // a whole chunk, fully unrolled: step s (elements 4 cg + LANES s ..)
+      // reads its float4s P steps ahead into a register ring, the
+      // scheduling barriers keeping them there (left alone, the scheduler
+      // sinks each read to just before its FMAs and the wave waits on LDS
+      // every few FMAs); each accumulator's FMAs stay in element order
+      constexpr int NS = kRlCk / LANES, P = 4;
+      float4 wr[P][RT], xr[P][TT];
 #pragma unroll
-      for (int q = 0; q < RT; q++) wv[q] = *reinterpret_cast<const float4*>(sw + q * kRlRs + j);
+      for (int s = 0; s < P; s++) {
 #pragma unroll
-      for (int i = 0; i < TT; i++) xv[i] = *reinterpret_cast<const float4*>(sx + i * kRlRs + j);
+        for (int q = 0; q < RT; q++)
+          wr[s][q] = *reinterpret_cast<const float4*>(sw + q * kRlRs + 4 * cg + LANES * s);
 #pragma unroll
-      for (int i = 0; i < TT; i++)
+        for (int i = 0; i < TT; i++)
+          xr[s][i] = *reinterpret_cast<const float4*>(sx + i * kRlRs + 4 * cg + LANES * s);
+      }
 #pragma unroll
-        for (int q = 0; q < RT; q++) {
-          acc[i][q][0] = __builtin_fmaf(wv[q].x, xv[i].x, acc[i][q][0]);
-          acc[i][q][1] = __builtin_fmaf(wv[q].y, xv[i].y, acc[i][q][1]);
-          acc[i][q][2] = __builtin_fmaf(wv[q].z, xv[i].z, acc[i][q][2]);
-          acc[i][q][3] = __builtin_fmaf(wv[q].w, xv[i].w, acc[i][q][3]);
+      for (int s = 0; s < NS; s++) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < TT; i++)
+#pragma unroll
+          for (int q = 0; q < RT; q++) {
+            acc[i][q][0] = __builtin_fmaf(wr[s % P][q].x, xr[s % P][i].x, acc[i][q][0]);
+            acc[i][q][1] = __builtin_fmaf(wr[s % P][q].y, xr[s % P][i].y, acc[i][q][1]);
+            acc[i][q][2] = __builtin_fmaf(wr[s % P][q].z, xr[s % P][i].z, acc[i][q][2]);
+            acc[i][q][3] = __builtin_fmaf(wr[s % P][q].w, xr[s % P][i].w, acc[i][q][3]);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+        if (s + P < NS) {
+#pragma unroll
+          for (int q = 0; q < RT; q++)
+            wr[s % P][q] =
+                *reinterpret_cast<const float4*>(sw + q * kRlRs + 4 * cg + LANES * (s + P));
+#pragma unroll
+          for (int i = 0; i < TT; i++)
+            xr[s % P][i] =
+                *reinterpret_cast<const float4*>(sx + i * kRlRs + 4 * cg + LANES * (s + P));
         }
+      }
+    } else {
+#pragma unroll 4
+      for (int j = 4 * cg; j < jend; j += LANES) {
+        float4 wv[RT], xv[TT];
+#pragma unroll
+        for (int q = 0; q < RT; q++) wv[q] = *reinterpret_cast<const float4*>(sw + q * kRlRs + j);
+#pragma unroll
+        for (int i = 0; i < TT; i++) xv[i] = *reinterpret_cast<const float4*>(sx + i * kRlRs + j);
+#pragma unroll
+        for (int i = 0; i < TT; i++)
+#pragma unroll
+          for (int q = 0; q < RT; q++) {
+            acc[i][q][0] = __builtin_fmaf(wv[q].x, xv[i].x, acc[i][q][0]);
+            acc[i][q][1] = __builtin_fmaf(wv[q].y, xv[i].y, acc[i][q][1]);
+            acc[i][q][2] = __builtin_fmaf(wv[q].z, xv[i].z, acc[i][q][2]);
+            acc[i][q][3] = __builtin_fmaf(wv[q].w, xv[i].w, acc[i][q][3]);
+          }
+      }
     }
     if (c + NBUF < nch) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
