@@ -843,9 +843,146 @@ __global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ 
   out[tid] = acc;
 }
 
+// The same attention values with the query heads of one kv head together:
+// workgroup (kv head blockIdx.x, token blockIdx.y), thread j hd + c = query
+// head blockIdx.x kv_mul + j, column c.  Each head's softmax runs as in
+// k_attn_sv_rows (its max, exponentials, denominator by the head's first
+// thread, x *= inv); then the values in groups of kSgGrp positions: the
+// group's V values of the kv head are loaded into registers one group ahead,
+// dequantized into LDS once per workgroup, and every thread adds
+// e_j[t] * v[t][c] in position order -- the chains of k_attn_sv_rows, with
+// each V value read from L2 once per kv head instead of once per query head.
+// Dynamic LDS: kv_mul rows of ecap floats rounded up to 4 (the
+// exponentials), 2 x kSgGrp x hd
+// floats (the value tiles), ceil(ecap / page) ints (the page table).
+constexpr int kSgGrp = 32;
+constexpr int kSgPer = 4;  // values per thread and group (kSgGrp * hd / 1024)
+template <int KVT>
+__global__ __launch_bounds__(1024) void k_attn_sv_gqa(const float* __restrict__ att,
+                                                     int att_stride, KvView V,
+                                                     const int32_t* __restrict__ st, int ecap,
+                                                     int kv_mul, int hd,
+                                                     float* __restrict__ out) {
+  extern __shared__ __align__(16) float sm[];
+  __shared__ float red[16];
+  __shared__ float inv_s[16];
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int kvh = blockIdx.x, z = blockIdx.y;
+  const int nh = gridDim.x * kv_mul;
+  const int j = tid / hd, c = tid - j * hd;
+  const int h = kvh * kv_mul + j;
+  const int wph = hd >> 6;  // waves per head
+  const float* a = att + ((size_t)z * nh + h) * att_stride;
+  const int npos = st[2 * z + 1] + 1;
+  const int es = (ecap + 3) & ~3;  // 16-byte aligned rows (float4 reads)
+  float* e = sm + (size_t)j * es;
+  float* vs = sm + (size_t)kv_mul * es;  // [2][kSgGrp][hd]
+  int32_t* pt = reinterpret_cast<int32_t*>(vs + 2 * kSgGrp * hd);
+  const int npg = (npos + V.page - 1) / V.page;
+  for (int i = tid; i < npg; i += nthr) pt[i] = V.ptab[i];
+  const ExpTab tab = qr_expf_tab();
+  float mx = a[0];
+  for (int i = c; i < npos; i += hd) {
+    const float v = a[i];
+    e[i] = v;
+    mx = v > mx ? v : mx;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v = __shfl_xor(mx, o);
+    mx = v > mx ? v : mx;
+  }
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = red[j * wph];
+  for (int w = 1; w < wph; w++) mx = red[j * wph + w] > mx ? red[j * wph + w] : mx;
+  // every lane runs the same number of rounds (qr_expf_w reads other lanes)
+  const int rounds = (npos + hd - 1) / hd;
+  for (int r = 0; r < rounds; r++) {
+    const int i = r * hd + c;
+    const float v = i < npos ? e[i] : 0.0f;
+    const float ev = qr_expf_w(v - mx, tab);
+    if (i < npos) e[i] = ev;
+  }
+  __syncthreads();
+  if (c == 0) inv_s[j] = 1.0f / seq_sum_lds_short(e, npos);
+  __syncthreads();
+  const float inv = inv_s[j];
+  for (int i = c; i < npos; i += hd) e[i] = e[i] * inv;  // softmax_ref's x[i] *= inv
+  // (the barrier of the first group below orders these writes before the adds)
+
+  // value k of a group: position g0 + (tid + 1024 k) / hd, column (tid + 1024 k) % hd
+  const size_t col0 = (size_t)kvh * hd;
+  uint32_t rq[kSgPer], rd[kSgPer];
+  auto load = [&](int g0) {
+#pragma unroll
+    for (int k = 0; k < kSgPer; k++) {
+      const int idx = tid + 1024 * k;
+      const int u = idx / hd, cc = idx - u * hd;
+      const int t = min(g0 + u, npos - 1);  // past the end: reload the last row
+      const uint8_t* row = kv_row_lds(V, pt, t);
+      if constexpr (KVT == QR_KV_Q8_0) {
+        const uint8_t* blk = row + ((col0 + cc) >> 5) * QR_Q8_BYTES;
+        rd[k] = *reinterpret_cast<const uint16_t*>(blk);
+        rq[k] = (uint32_t)blk[2 + ((col0 + cc) & 31)];
+      } else {
+        rq[k] = reinterpret_cast<const uint32_t*>(row)[col0 + cc];
+      }
+    }
+  };
+  __syncthreads();  // the page table
+  load(0);
+  float acc = 0.0f;
+  int buf = 0;
+  for (int g0 = 0; g0 < npos; g0 += kSgGrp) {
+    float* vb = vs + buf * kSgGrp * hd;
+#pragma unroll
+    for (int k = 0; k < kSgPer; k++) {
+      const int idx = tid + 1024 * k;
+      float v;
+      if constexpr (KVT == QR_KV_Q8_0) v = (float)(int8_t)(uint8_t)rq[k] * qr_h2f((uint16_t)rd[k]);
+      else v = __uint_as_float(rq[k]);
+      vb[idx] = v;  // [u][cc] = idx
+    }
+    __syncthreads();
+    if (g0 + kSgGrp < npos) load(g0 + kSgGrp);
+    const int n = min(kSgGrp, npos - g0);
+    if (n == kSgGrp) {
+#pragma unroll
+      for (int u = 0; u < kSgGrp; u++) acc += e[g0 + u] * vb[u * hd + c];
+    } else {
+      for (int u = 0; u < n; u++) acc += e[g0 + u] * vb[u * hd + c];
+    }
+    buf ^= 1;
+  }
+  out[((size_t)z * nh + h) * hd + c] = acc;
+}
+
+// Whether k_attn_sv_gqa takes a chunk whose positions stop below ecap.
+inline size_t sv_gqa_lds(int ecap, int kv_mul, int hd, int page) {
+  return ((size_t)kv_mul * ((ecap + 3) & ~3) + 2 * (size_t)kSgGrp * hd) * 4 +
+         (size_t)((ecap + page - 1) / page) * 4;
+}
+inline bool sv_gqa_ok(int ecap, int kv_mul, int hd, int page) {
+  return hd == 128 && kv_mul == 8 && ecap >= 1 &&  // kSgPer: kSgGrp hd = 4 x 1024
+         sv_gqa_lds(ecap, kv_mul, hd, page) <= 160 * 1024;
+}
+
+// ecap: the chunk's positions end (every token's npos <= ecap).
 hipError_t sv_rows_launch(const float* att, int att_stride, const KvView& V, const int32_t* st,
                           int lds_cap, int n_heads, int kv_mul, int hd, float* out, int tokens,
-                          hipStream_t s) {
+                          hipStream_t s, int ecap = 0) {
+  if (ecap > 0 && sv_gqa_ok(ecap, kv_mul, hd, V.page)) {
+    const dim3 g(n_heads / kv_mul, tokens);
+    const size_t l = sv_gqa_lds(ecap, kv_mul, hd, V.page);
+    if (V.kv_type == QR_KV_Q8_0)
+      hipLaunchKernelGGL(k_attn_sv_gqa<QR_KV_Q8_0>, g, dim3(1024), l, s, att, att_stride, V, st,
+                         ecap, kv_mul, hd, out);
+    else
+      hipLaunchKernelGGL(k_attn_sv_gqa<QR_KV_F32>, g, dim3(1024), l, s, att, att_stride, V, st,
+                         ecap, kv_mul, hd, out);
+    return hipGetLastError();
+  }
   const dim3 grid(n_heads, tokens);
   const int threads = ((hd + 63) / 64) * 64;
   const size_t lds = (size_t)lds_cap * 4;
@@ -942,6 +1079,8 @@ std::atomic<bool> g_sm_opt[64];
 std::atomic<bool> g_sm_opt2[64];
 std::atomic<bool> g_rows_opt[64];
 std::atomic<bool> g_rows_opt2[64];
+std::atomic<bool> g_gqa_opt[64];
+std::atomic<bool> g_gqa_opt2[64];
 
 #define DEC_HIP(call, what)                                                        \
   do {                                                                             \
@@ -1095,7 +1234,9 @@ hipError_t matmul_rows_dev(qr_decoder* d, const void* w, uint32_t type, const fl
 // One prompt chunk of T tokens (states st[2 T]) through every layer: the
 // decode step's kernels with a token dimension, the projections as T-row
 // products, the MoE layer at T tokens.  Leaves the chunk's residuals in px.
-hipError_t enqueue_prefill_chunk(qr_decoder* d, int T, const int32_t* st, hipStream_t s) {
+// pend: one past the chunk's last position.
+hipError_t enqueue_prefill_chunk(qr_decoder* d, int T, const int32_t* st, int pend,
+                                 hipStream_t s) {
   hipError_t e;
   const int dim = d->dim;
   // the chunk's single-expert dispatch of its T rows (16-pair items, as
@@ -1126,7 +1267,7 @@ hipError_t enqueue_prefill_chunk(qr_decoder* d, int T, const int32_t* st, hipStr
                        d->patt, RopeArgs{});
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = sv_rows_launch(d->patt, d->cap, V, st, d->cap, d->nh, d->kv_mul, d->hd, d->pao, T,
-                            s)))
+                            s, pend)))
       return e;
     if ((e = matmul_rows_dev(d, L.wo, L.wo_type, d->pao, d->pxb2, dim, d->qd, T, s))) return e;
     if ((e = rmsnorm_launch(d->px, d->pxb2, L.rms_ffn, dim, d->pxb, s, T))) return e;
@@ -1328,6 +1469,8 @@ int qr_decoder_create(qr_ctx* c, const qr_model* m, int kv_type, int order, int 
   DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_F32>, g_sm_opt2), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv_rows<QR_KV_Q8_0>, g_rows_opt), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv_rows<QR_KV_F32>, g_rows_opt2), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_sv_gqa<QR_KV_Q8_0>, g_gqa_opt), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_sv_gqa<QR_KV_F32>, g_gqa_opt2), "lds opt-in");
   qr_decoder* d = new (std::nothrow) qr_decoder();
   if (!d) return set_error(QR_ERR_NOMEM, "qr_decoder_create: host allocation");
   d->ctx = c;
@@ -1587,7 +1730,8 @@ int qr_decoder_prefill(qr_decoder* d, const int32_t* tokens, int n, int pos0, in
   const int dim = d->dim;
   for (int c0 = 0; c0 < n; c0 += chunk) {
     const int T = n - c0 < chunk ? n - c0 : chunk;
-    DEC_HIP(enqueue_prefill_chunk(d, T, d->pst + 2 * (size_t)c0, s), "prefill chunk");
+    DEC_HIP(enqueue_prefill_chunk(d, T, d->pst + 2 * (size_t)c0, pos0 + c0 + T, s),
+            "prefill chunk");
     const bool last = c0 + T == n;
     if (logits && (flags & QR_PREFILL_ALL_LOGITS)) {
       // final norm of every row (x itself is left as is), then the lm_head rows

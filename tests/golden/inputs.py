@@ -199,13 +199,13 @@ def decode_digest(m):
     return digest(*arrs)
 
 
-def qwen3_small_model(seed=9500, n_layers=2, seq_len=640):
+def qwen3_small_model(seed=9500, n_layers=2, seq_len=640, n_kv_heads=2):
     """A Qwen3-30B-A3B-shaped decoder at reduced width: head_dim 128 with
-    q_dim (8 x 128) != dim (512), GQA 4:1, 8 experts top-2, gate/up Q4_K,
-    down Q6_K, mixed attention types, Q4_K embeddings and a Q6_K lm_head.
-    The reference cannot run it (head_dim = dim / n_heads there); the oracle's
-    restatement can."""
-    dim, H, KVH, hd, E, K, hidden, vocab = 512, 8, 2, 128, 8, 2, 256, 320
+    q_dim (8 x 128) != dim (512), GQA 4:1 (8:1 with n_kv_heads=1), 8 experts
+    top-2, gate/up Q4_K, down Q6_K, mixed attention types, Q4_K embeddings and
+    a Q6_K lm_head.  The reference cannot run it (head_dim = dim / n_heads
+    there); the oracle's restatement can."""
+    dim, H, KVH, hd, E, K, hidden, vocab = 512, 8, n_kv_heads, 128, 8, 2, 256, 320
     wt = (TYPE_Q4_K, TYPE_Q8_0, TYPE_Q6_K, TYPE_Q5_K)
     m = dict(dim=dim, n_heads=H, n_kv_heads=KVH, head_dim=hd, n_layers=n_layers, E=E, K=K,
              hidden=hidden, vocab=vocab, seq_len=seq_len, rope_base=1e6, wtype=list(wt),

@@ -134,6 +134,28 @@ def test_prefill_head128_chunks(dev, source, page):
     assert np.array_equal(kv, want_kv)
 
 
+@pytest.mark.parametrize("kv_type,page", [(Q.KV_Q8_0, 64), (Q.KV_F32, 16)],
+                         ids=["q8_0_pages64", "f32_pages16"])
+def test_prefill_gqa8_chunks(dev, kv_type, page):
+    """GQA 8:1 at head_dim 128, the shape whose prefill attention values run
+    the query heads of a kv head in one workgroup (V staged once for the
+    eight): 300 prompt tokens in chunks of 128 against 300 sequential decode
+    steps, every token's logits and the last residual bit for bit."""
+    m = I.qwen3_small_model(n_layers=2, seq_len=320, n_kv_heads=1)
+    rng = np.random.default_rng(19)
+    toks = rng.integers(0, m["vocab"], size=300).astype(np.int32)
+    ref = make_decoder(dev, m, kv_type, ORDER_AVX2, page=page, flags=Q.DEC_GRAPH)
+    print("prefill gqa8 sequential reference", flush=True)
+    want_lg, want_x = sequential(dev, ref, m, toks)
+    ref.close()
+    d = make_decoder(dev, m, kv_type, ORDER_AVX2, page=page)
+    print("prefill gqa8 chunks", flush=True)
+    lg, x = prefill(dev, d, m, toks, chunk=128)
+    d.close()
+    assert_bits_equal(lg, want_lg, "prefill logits")
+    assert_bits_equal(x, want_x, "prefill residual")
+
+
 def test_prefill_bad_args(dev):
     m = I.decode_model("a")
     d = make_decoder(dev, m, Q.KV_F32, ORDER_SEQ)
