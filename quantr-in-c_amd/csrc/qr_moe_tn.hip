@@ -95,20 +95,53 @@ __global__ __launch_bounds__(256) void k_rlogits(const float* __restrict__ W,
     const float* sw = sm + (c % NBUF) * BUF + (rb * RT) * kRlRs;
     const float* sx = sm + (c % NBUF) * BUF + (RW + tb * TT) * kRlRs;
     const int jend = min(dm, (c + 1) * kRlCk) - c * kRlCk;
-#pragma unroll 4
-    for (int j = k; j < jend; j += LANES) {
-      float wv[RT], xv[TT];
+    if (jend == kRlCk) {
+      // a whole chunk, fully unrolled, each step's reads P steps ahead of
+      // its adds in a register ring held there by scheduling barriers (as in
+      // k_rlogits4); every chain keeps its element order
+      constexpr int NS = kRlCk / LANES, P = 8;
+      float wr[P][RT], xr[P][TT];
 #pragma unroll
-      for (int q = 0; q < RT; q++) wv[q] = sw[q * kRlRs + j];
+      for (int s = 0; s < P; s++) {
 #pragma unroll
-      for (int i = 0; i < TT; i++) xv[i] = sx[i * kRlRs + j];
+        for (int q = 0; q < RT; q++) wr[s][q] = sw[q * kRlRs + k + LANES * s];
 #pragma unroll
-      for (int i = 0; i < TT; i++)
+        for (int i = 0; i < TT; i++) xr[s][i] = sx[i * kRlRs + k + LANES * s];
+      }
 #pragma unroll
-        for (int q = 0; q < RT; q++) {
-          if constexpr (LANES == 1) acc[i][q] += wv[q] * xv[i];
-          else acc[i][q] = __builtin_fmaf(wv[q], xv[i], acc[i][q]);
+      for (int s = 0; s < NS; s++) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < TT; i++)
+#pragma unroll
+          for (int q = 0; q < RT; q++) {
+            if constexpr (LANES == 1) acc[i][q] += wr[s % P][q] * xr[s % P][i];
+            else acc[i][q] = __builtin_fmaf(wr[s % P][q], xr[s % P][i], acc[i][q]);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+        if (s + P < NS) {
+#pragma unroll
+          for (int q = 0; q < RT; q++) wr[s % P][q] = sw[q * kRlRs + k + LANES * (s + P)];
+#pragma unroll
+          for (int i = 0; i < TT; i++) xr[s % P][i] = sx[i * kRlRs + k + LANES * (s + P)];
         }
+      }
+    } else {
+#pragma unroll 4
+      for (int j = k; j < jend; j += LANES) {
+        float wv[RT], xv[TT];
+#pragma unroll
+        for (int q = 0; q < RT; q++) wv[q] = sw[q * kRlRs + j];
+#pragma unroll
+        for (int i = 0; i < TT; i++) xv[i] = sx[i * kRlRs + j];
+#pragma unroll
+        for (int i = 0; i < TT; i++)
+#pragma unroll
+          for (int q = 0; q < RT; q++) {
+            if constexpr (LANES == 1) acc[i][q] += wv[q] * xv[i];
+            else acc[i][q] = __builtin_fmaf(wv[q], xv[i], acc[i][q]);
+          }
+      }
     }
     if (c + NBUF < nch) {
       // every thread is done with this buffer before chunk c + NBUF lands in it
@@ -449,7 +482,7 @@ hipError_t rlogits_launch(int order, const float* W, const float* X, int T, int 
       (reinterpret_cast<uintptr_t>(X) & 15))
     return hipErrorInvalidValue;
   if (T <= 0 || E <= 0) return hipSuccess;
-  const bool small = T <= 64;
+  const bool small = T <= 128;
   switch (order) {
     case QR_ORDER_SEQ: return rlogits_launch_t<1, 16, 1, 16, 1, 2>(W, X, T, E, d, logits, st);
     case QR_ORDER_AVX2:
