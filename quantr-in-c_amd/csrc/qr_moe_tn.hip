@@ -472,10 +472,11 @@ static hipError_t rlogits_launch_t(const float* W, const float* X, int T, int E,
   return hipGetLastError();
 }
 
-// Tiles of 16 tokens x 4 router rows for few tokens (more workgroups for the
-// same work; one chain per thread); 16 x 16 tiles with four chains per thread
-// beyond (a quarter of the LDS read instructions); two chunk buffers (deeper
-// rings measured no faster).
+// Tiles of 16 tokens x 4 router rows up to 128 tokens (more workgroups for
+// the same work -- 256 at 128 tokens and 128 experts, against 64 of 16 x 16;
+// one chain per thread); 16 x 16 tiles with four chains per thread beyond (a
+// quarter of the LDS read instructions); two chunk buffers (deeper rings
+// measured no faster).
 hipError_t rlogits_launch(int order, const float* W, const float* X, int T, int E, int d,
                           float* logits, hipStream_t st) {
   if (!rlogits_ok(d) || (reinterpret_cast<uintptr_t>(W) & 15) ||
