@@ -844,8 +844,8 @@ __global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ 
 }
 
 // The same attention values with the query heads of one kv head together:
-// workgroup (kv head blockIdx.x, token blockIdx.y), thread j hd + c = query
-// head blockIdx.x kv_mul + j, column c.  Each head's softmax runs as in
+// workgroup (kv head blockIdx.x, token blockIdx.y) of kv_mul hd threads,
+// thread j hd + c = query head blockIdx.x kv_mul + j, column c.  Each head's softmax runs as in
 // k_attn_sv_rows (its max, exponentials, denominator by the head's first
 // thread, x *= inv); then the values in groups of kSgGrp positions: the
 // group's V values of the kv head are loaded into registers one group ahead,
@@ -855,9 +855,10 @@ __global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ 
 // Dynamic LDS: kv_mul rows of ecap floats rounded up to 4 (the
 // exponentials), 2 x kSgGrp x hd
 // floats (the value tiles), ceil(ecap / page) ints (the page table).
+// kv_mul hd threads (a multiple of 64, at most 1024); NPER = kSgGrp / kv_mul
+// values per thread and group (kv_mul 4 or 8).
 constexpr int kSgGrp = 32;
-constexpr int kSgPer = 4;  // values per thread and group (kSgGrp * hd / 1024)
-template <int KVT>
+template <int KVT, int NPER>
 __global__ __launch_bounds__(1024) void k_attn_sv_gqa(const float* __restrict__ att,
                                                      int att_stride, KvView V,
                                                      const int32_t* __restrict__ st, int ecap,
@@ -911,13 +912,13 @@ __global__ __launch_bounds__(1024) void k_attn_sv_gqa(const float* __restrict__ 
   for (int i = c; i < npos; i += hd) e[i] = e[i] * inv;  // softmax_ref's x[i] *= inv
   // (the barrier of the first group below orders these writes before the adds)
 
-  // value k of a group: position g0 + (tid + 1024 k) / hd, column (tid + 1024 k) % hd
+  // value k of a group: position g0 + (tid + nthr k) / hd, column (tid + nthr k) % hd
   const size_t col0 = (size_t)kvh * hd;
-  uint32_t rq[kSgPer], rd[kSgPer];
+  uint32_t rq[NPER], rd[NPER];
   auto load = [&](int g0) {
 #pragma unroll
-    for (int k = 0; k < kSgPer; k++) {
-      const int idx = tid + 1024 * k;
+    for (int k = 0; k < NPER; k++) {
+      const int idx = tid + nthr * k;
       const int u = idx / hd, cc = idx - u * hd;
       const int t = min(g0 + u, npos - 1);  // past the end: reload the last row
       const uint8_t* row = kv_row_lds(V, pt, t);
@@ -937,8 +938,8 @@ __global__ __launch_bounds__(1024) void k_attn_sv_gqa(const float* __restrict__ 
   for (int g0 = 0; g0 < npos; g0 += kSgGrp) {
     float* vb = vs + buf * kSgGrp * hd;
 #pragma unroll
-    for (int k = 0; k < kSgPer; k++) {
-      const int idx = tid + 1024 * k;
+    for (int k = 0; k < NPER; k++) {
+      const int idx = tid + nthr * k;
       float v;
       if constexpr (KVT == QR_KV_Q8_0) v = (float)(int8_t)(uint8_t)rq[k] * qr_h2f((uint16_t)rd[k]);
       else v = __uint_as_float(rq[k]);
@@ -964,8 +965,35 @@ inline size_t sv_gqa_lds(int ecap, int kv_mul, int hd, int page) {
          (size_t)((ecap + page - 1) / page) * 4;
 }
 inline bool sv_gqa_ok(int ecap, int kv_mul, int hd, int page) {
-  return hd == 128 && kv_mul == 8 && ecap >= 1 &&  // kSgPer: kSgGrp hd = 4 x 1024
-         sv_gqa_lds(ecap, kv_mul, hd, page) <= 160 * 1024;
+  // kv_mul 1 and 2 (16 and 32 values per thread and group) would spill
+  return (kv_mul == 4 || kv_mul == 8) && hd % 64 == 0 &&
+         kv_mul * hd <= 1024 && ecap >= 1 && sv_gqa_lds(ecap, kv_mul, hd, page) <= 160 * 1024;
+}
+template <int KVT, int NPER>
+std::atomic<bool>* gqa_opt() {
+  static std::atomic<bool> f[64];
+  return f;
+}
+template <int KVT, int NPER>
+hipError_t gqa_launch(dim3 g, int threads, size_t lds, hipStream_t s, const float* att,
+                      int att_stride, const KvView& V, const int32_t* st, int ecap, int kv_mul,
+                      int hd, float* out) {
+  if (lds > 64 * 1024) {
+    const hipError_t e = lds_opt_in((const void*)k_attn_sv_gqa<KVT, NPER>, gqa_opt<KVT, NPER>());
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((k_attn_sv_gqa<KVT, NPER>), g, dim3(threads), lds, s, att, att_stride, V, st,
+                     ecap, kv_mul, hd, out);
+  return hipGetLastError();
+}
+template <int KVT>
+hipError_t gqa_launch_kv(dim3 g, size_t lds, hipStream_t s, const float* att, int att_stride,
+                         const KvView& V, const int32_t* st, int ecap, int kv_mul, int hd,
+                         float* out) {
+  const int threads = kv_mul * hd;
+  if (kv_mul == 8)
+    return gqa_launch<KVT, 4>(g, threads, lds, s, att, att_stride, V, st, ecap, kv_mul, hd, out);
+  return gqa_launch<KVT, 8>(g, threads, lds, s, att, att_stride, V, st, ecap, kv_mul, hd, out);
 }
 
 // ecap: the chunk's positions end (every token's npos <= ecap).
@@ -976,12 +1004,8 @@ hipError_t sv_rows_launch(const float* att, int att_stride, const KvView& V, con
     const dim3 g(n_heads / kv_mul, tokens);
     const size_t l = sv_gqa_lds(ecap, kv_mul, hd, V.page);
     if (V.kv_type == QR_KV_Q8_0)
-      hipLaunchKernelGGL(k_attn_sv_gqa<QR_KV_Q8_0>, g, dim3(1024), l, s, att, att_stride, V, st,
-                         ecap, kv_mul, hd, out);
-    else
-      hipLaunchKernelGGL(k_attn_sv_gqa<QR_KV_F32>, g, dim3(1024), l, s, att, att_stride, V, st,
-                         ecap, kv_mul, hd, out);
-    return hipGetLastError();
+      return gqa_launch_kv<QR_KV_Q8_0>(g, l, s, att, att_stride, V, st, ecap, kv_mul, hd, out);
+    return gqa_launch_kv<QR_KV_F32>(g, l, s, att, att_stride, V, st, ecap, kv_mul, hd, out);
   }
   const dim3 grid(n_heads, tokens);
   const int threads = ((hd + 63) / 64) * 64;
@@ -1079,8 +1103,6 @@ std::atomic<bool> g_sm_opt[64];
 std::atomic<bool> g_sm_opt2[64];
 std::atomic<bool> g_rows_opt[64];
 std::atomic<bool> g_rows_opt2[64];
-std::atomic<bool> g_gqa_opt[64];
-std::atomic<bool> g_gqa_opt2[64];
 
 #define DEC_HIP(call, what)                                                        \
   do {                                                                             \
@@ -1469,8 +1491,6 @@ int qr_decoder_create(qr_ctx* c, const qr_model* m, int kv_type, int order, int 
   DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_F32>, g_sm_opt2), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv_rows<QR_KV_Q8_0>, g_rows_opt), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv_rows<QR_KV_F32>, g_rows_opt2), "lds opt-in");
-  DEC_HIP(lds_opt_in((const void*)k_attn_sv_gqa<QR_KV_Q8_0>, g_gqa_opt), "lds opt-in");
-  DEC_HIP(lds_opt_in((const void*)k_attn_sv_gqa<QR_KV_F32>, g_gqa_opt2), "lds opt-in");
   qr_decoder* d = new (std::nothrow) qr_decoder();
   if (!d) return set_error(QR_ERR_NOMEM, "qr_decoder_create: host allocation");
   d->ctx = c;
