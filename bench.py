@@ -88,11 +88,28 @@ def cpu_model():
     return "unknown"
 
 
+# A buffer larger than the 256 MB Infinity Cache and the L2s together, read
+# (untimed) before every timed replay: a replay's first launches then find
+# none of the weights the previous replay's last launches left cached, however
+# the replay's length relates to the number of rotating copies.
+FLUSH_BYTES = 1 << 30
+_flush = {}
+
+
+def flush_caches(dev):
+    if "buf" not in _flush:
+        _flush["buf"], _flush["sink"] = dev.alloc(FLUSH_BYTES), dev.alloc(16)
+        dev.memset(_flush["buf"], 0, FLUSH_BYTES)
+    dev.read_kernel(_flush["buf"].ptr, FLUSH_BYTES, _flush["sink"].ptr)
+
+
 def timed_replays(dev, g, reps=5):
     """Median over `reps` timed replays of graph g (HIP events on the launch
-    stream, synchronized before and after each replay)."""
+    stream, synchronized before and after each replay; the caches flushed,
+    untimed, before each)."""
     t = []
     for _ in range(reps):
+        flush_caches(dev)
         dev.sync()
         dev.timer_start()
         dev.graph_launch(g)

@@ -62,11 +62,21 @@ class OModel(C.Structure):
         ("tok_row_bytes", C.c_size_t), ("rms_att", C.c_void_p), ("rms_ffn", C.c_void_p),
         ("wq", C.c_void_p), ("wk", C.c_void_p), ("wv", C.c_void_p), ("wo", C.c_void_p),
         ("wtype", C.c_void_p), ("moe", C.c_void_p), ("rms_final", C.c_void_p),
-        ("wcls", C.c_void_p), ("wcls_type", C.c_uint32),
+        ("wcls", C.c_void_p), ("wcls_type", C.c_uint32), ("threads", C.c_int),
     ]
 
 
 KV_F32, KV_Q8_0 = 0, 2
+
+
+def oracle_threads():
+    """OpenMP width for the oracle's model-sized loops: the CPUs this process
+    may run on, at most 16."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
 
 
 def _parr(keep, arrs):
@@ -368,6 +378,7 @@ class Oracle:
         wc = np.ascontiguousarray(m["wcls"])
         keep.extend([rf, wc])
         om.rms_final, om.wcls, om.wcls_type = rf.ctypes.data, wc.ctypes.data, m["wcls_type"]
+        om.threads = oracle_threads()
         return om
 
     def forward_seq(self, m, tokens, order, kv_type=KV_F32):

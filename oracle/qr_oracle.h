@@ -145,6 +145,9 @@ typedef struct {
     const float* rms_final;
     const void* wcls;            /* [vocab][dim] */
     uint32_t wcls_type;
+    int threads;                 /* OpenMP width of the quantized GEMVs and of the attention's
+                                    heads (rows and heads are independent: any width gives
+                                    the same bits) */
 } qro_model;
 
 void qro_rmsnorm(float* o, const float* x, const float* w, int n);
@@ -154,6 +157,9 @@ size_t qro_kv_row_bytes(int kv_type, int kv_dim);
 void qro_kv_store(void* row, const float* src, int kv_dim, int kv_type);
 void qro_attention(float* out, const float* q, const void* kc, const void* vc, size_t row_stride,
                    int kv_type, int pos, int n_heads, int n_kv_heads, int head_dim, float* att);
+void qro_attention_mt(float* out, const float* q, const void* kc, const void* vc,
+                      size_t row_stride, int kv_type, int pos, int n_heads, int n_kv_heads,
+                      int head_dim, float* att, int threads);
 void qro_forward(const qro_model* m, void* kc, void* vc, int token, int pos, int order, float* x,
                  float* logits);
 

@@ -96,45 +96,60 @@ void qro_kv_store(void* row, const float* src, int kv_dim, int kv_type) {
  * (src/kernels.c:162-168) times 1 / sqrtf(head_dim), softmax_ref, then each
  * output element accumulated over the positions in order.  att: scratch of
  * n_heads * (pos + 1) floats (optional: the normalised weights). */
+static void attention_head(float* out, const float* q, const uint8_t* K, const uint8_t* V,
+                           size_t row_stride, int kv_type, int pos, int h, int kv_mul,
+                           int head_dim, float* att, float* kb) {
+    int kvh = h / kv_mul, t, i;
+    float inv_sqrt = 1.0f / sqrtf((float)head_dim);
+    const float* qh = q + (size_t)h * head_dim;
+    float* a = att + (size_t)h * (pos + 1);
+    float* o = out + (size_t)h * head_dim;
+    for (t = 0; t <= pos; t++) {
+        const uint8_t* row = K + (size_t)t * row_stride;
+        float s = 0.0f;
+        for (i = 0; i < head_dim; i++) kb[i] = kv_elem(row, kv_type, kvh * head_dim + i);
+        for (i = 0; i < head_dim; i++) s += qh[i] * kb[i];
+        a[t] = s * inv_sqrt;
+    }
+    qro_softmax(a, pos + 1);
+    memset(o, 0, (size_t)head_dim * sizeof(float));
+    for (t = 0; t <= pos; t++) {
+        const uint8_t* row = V + (size_t)t * row_stride;
+        for (i = 0; i < head_dim; i++) o[i] += a[t] * kv_elem(row, kv_type, kvh * head_dim + i);
+    }
+}
+
+/* Each head's scores, softmax and value sums depend on that head alone (the
+ * reference's two head loops, src/runtime.c:136-193, share nothing between
+ * heads), so heads run in parallel with the same bits at any width. */
+void qro_attention_mt(float* out, const float* q, const void* kc, const void* vc,
+                      size_t row_stride, int kv_type, int pos, int n_heads, int n_kv_heads,
+                      int head_dim, float* att, int threads) {
+    int kv_mul = n_heads / (n_kv_heads > 0 ? n_kv_heads : 1), h;
+#pragma omp parallel num_threads(threads > 0 ? threads : 1)
+    {
+        float* kb = (float*)malloc((size_t)head_dim * sizeof(float));
+#pragma omp for schedule(static)
+        for (h = 0; h < n_heads; h++)
+            if (kb)
+                attention_head(out, q, (const uint8_t*)kc, (const uint8_t*)vc, row_stride,
+                               kv_type, pos, h, kv_mul, head_dim, att, kb);
+        free(kb);
+    }
+}
+
 void qro_attention(float* out, const float* q, const void* kc, const void* vc, size_t row_stride,
                    int kv_type, int pos, int n_heads, int n_kv_heads, int head_dim, float* att) {
-    int kv_mul = n_heads / (n_kv_heads > 0 ? n_kv_heads : 1), h, t, i;
-    float inv_sqrt = 1.0f / sqrtf((float)head_dim);
-    const uint8_t* K = (const uint8_t*)kc;
-    const uint8_t* V = (const uint8_t*)vc;
-    float* kb = (float*)malloc((size_t)head_dim * sizeof(float));
-    if (!kb) return;
-    for (h = 0; h < n_heads; h++) {
-        int kvh = h / kv_mul;
-        const float* qh = q + (size_t)h * head_dim;
-        float* a = att + (size_t)h * (pos + 1);
-        for (t = 0; t <= pos; t++) {
-            const uint8_t* row = K + (size_t)t * row_stride;
-            float s = 0.0f;
-            for (i = 0; i < head_dim; i++) kb[i] = kv_elem(row, kv_type, kvh * head_dim + i);
-            for (i = 0; i < head_dim; i++) s += qh[i] * kb[i];
-            a[t] = s * inv_sqrt;
-        }
-        qro_softmax(a, pos + 1);
-    }
-    for (h = 0; h < n_heads; h++) {
-        int kvh = h / kv_mul;
-        float* o = out + (size_t)h * head_dim;
-        const float* a = att + (size_t)h * (pos + 1);
-        memset(o, 0, (size_t)head_dim * sizeof(float));
-        for (t = 0; t <= pos; t++) {
-            const uint8_t* row = V + (size_t)t * row_stride;
-            for (i = 0; i < head_dim; i++) o[i] += a[t] * kv_elem(row, kv_type, kvh * head_dim + i);
-        }
-    }
-    free(kb);
+    qro_attention_mt(out, q, kc, vc, row_stride, kv_type, pos, n_heads, n_kv_heads, head_dim, att,
+                     1);
 }
 
 /* matmul_q (src/runtime.c:58-70). */
-static void mq(float* out, const float* x, const void* w, uint32_t type, int n, int d, int order) {
+static void mq(float* out, const float* x, const void* w, uint32_t type, int n, int d, int order,
+               int threads) {
     if (w == NULL) memset(out, 0, (size_t)n * sizeof(float));
     else if (type == QRO_TYPE_F32) qro_matmul_f32(out, x, (const float*)w, n, d, order);
-    else qro_matmul_q_fused(out, x, w, type, n, d, 1, order);
+    else qro_matmul_q_fused(out, x, w, type, n, d, threads, order);
 }
 
 /* forward_runtime (src/runtime.c:94-288) for one token at position pos.  kc / vc:
@@ -157,20 +172,21 @@ void qro_forward(const qro_model* m, void* kc, void* vc, int token, int pos, int
         uint8_t* kl = (uint8_t*)kc + (size_t)l * m->seq_len * rs;
         uint8_t* vl = (uint8_t*)vc + (size_t)l * m->seq_len * rs;
         qro_rmsnorm(xb, x, m->rms_att[l], dim);
-        mq(q, xb, m->wq[l], m->wtype[4 * l], qd, dim, order);
-        mq(k, xb, m->wk[l], m->wtype[4 * l + 1], kvd, dim, order);
-        mq(v, xb, m->wv[l], m->wtype[4 * l + 2], kvd, dim, order);
+        mq(q, xb, m->wq[l], m->wtype[4 * l], qd, dim, order, m->threads);
+        mq(k, xb, m->wk[l], m->wtype[4 * l + 1], kvd, dim, order, m->threads);
+        mq(v, xb, m->wv[l], m->wtype[4 * l + 2], kvd, dim, order, m->threads);
         qro_rope(q, k, qd, hd, m->n_kv_heads, pos, m->rope_base);
         qro_kv_store(kl + (size_t)pos * rs, k, kvd, m->kv_type);
         qro_kv_store(vl + (size_t)pos * rs, v, kvd, m->kv_type);
-        qro_attention(ao, q, kl, vl, rs, m->kv_type, pos, m->n_heads, m->n_kv_heads, hd, att);
-        mq(xb2, ao, m->wo[l], m->wtype[4 * l + 3], dim, qd, order);
+        qro_attention_mt(ao, q, kl, vl, rs, m->kv_type, pos, m->n_heads, m->n_kv_heads, hd, att,
+                         m->threads);
+        mq(xb2, ao, m->wo[l], m->wtype[4 * l + 3], dim, qd, order, m->threads);
         for (i = 0; i < dim; i++) x[i] += xb2[i];
         qro_rmsnorm(xb, x, m->rms_ffn[l], dim);
-        qro_moe_token(x, xb, &m->moe[l], order, order, 1, NULL, NULL);
+        qro_moe_token(x, xb, &m->moe[l], order, order, m->threads, NULL, NULL);
     }
     qro_rmsnorm(xb, x, m->rms_final, dim);
-    mq(logits, xb, m->wcls, m->wcls_type, m->vocab, dim, order);
+    mq(logits, xb, m->wcls, m->wcls_type, m->vocab, dim, order, m->threads);
 done:
     free(xb);
     free(xb2);

@@ -964,10 +964,13 @@ inline size_t sv_gqa_lds(int ecap, int kv_mul, int hd, int page) {
   return ((size_t)kv_mul * ((ecap + 3) & ~3) + 2 * (size_t)kSgGrp * hd) * 4 +
          (size_t)((ecap + page - 1) / page) * 4;
 }
+// k_attn_sv_gqa's static LDS (red[16] and inv_s[16]): the dynamic part may
+// take only what it leaves of the CU's 160 KiB.
+constexpr size_t kSvGqaStatic = 2 * 16 * sizeof(float);
 inline bool sv_gqa_ok(int ecap, int kv_mul, int hd, int page) {
   // kv_mul 1 and 2 (16 and 32 values per thread and group) would spill
-  return (kv_mul == 4 || kv_mul == 8) && hd % 64 == 0 &&
-         kv_mul * hd <= 1024 && ecap >= 1 && sv_gqa_lds(ecap, kv_mul, hd, page) <= 160 * 1024;
+  return (kv_mul == 4 || kv_mul == 8) && hd % 64 == 0 && kv_mul * hd <= 1024 && ecap >= 1 &&
+         sv_gqa_lds(ecap, kv_mul, hd, page) + kSvGqaStatic <= kDecLdsMax;
 }
 template <int KVT, int NPER>
 std::atomic<bool>* gqa_opt() {

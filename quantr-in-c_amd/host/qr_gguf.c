@@ -13,6 +13,8 @@
  */
 #define _POSIX_C_SOURCE 200809L
 #include <fcntl.h>
+#include <limits.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -322,23 +324,34 @@ int64_t qr_gguf_get_arr_len(const qr_gguf* g, const char* key) {
 
 /* ---- the decoder model (load_gguf_transformer, src/model.c:253-449) ------ */
 
+#define QR_GGUF_MAX_WIDTH (1 << 20) /* dim, ffn width, q and kv widths */
+#define QR_GGUF_MAX_COUNT 4096      /* layers, experts */
+#define QR_GGUF_MAX_VOCAB (1 << 24)
+
 static int known_wtype(uint32_t t) { return t == 0 || t == 8 || t == 12 || t == 13 || t == 14; }
 
 /* tensor i's bytes when it is [ne0][ne1] (ne2 = experts, or 1) of a type */
 static int check_tensor(const qr_gguf* g, int64_t i, uint64_t ne0, uint64_t ne1, uint64_t ne2,
                         int need_f32, size_t* bytes) {
     const tensor_t* t;
-    size_t rb;
+    size_t rb, off;
     if (i < 0) return 0;
     t = &g->t[i];
     if (!known_wtype(t->type) || (need_f32 && t->type != 0)) return 0;
     if (t->ne[0] != ne0 || (t->n_dims > 1 ? t->ne[1] : 1) != ne1 ||
         (t->n_dims > 2 ? t->ne[2] : 1) != ne2)
         return 0;
+    if (ne0 > (uint64_t)INT_MAX || ne1 > (uint64_t)SIZE_MAX || ne2 > (uint64_t)SIZE_MAX) return 0;
     rb = qr_row_bytes(t->type, (int)ne0);
     if (!rb && ne0) return 0;
-    *bytes = rb * (size_t)ne1 * (size_t)ne2;
-    if ((size_t)(t->data - g->base) + *bytes > g->size) return 0;
+    /* the product and the end offset are checked before they are formed: a
+     * crafted header must not wrap them past the bounds check */
+    if (ne1 && rb > SIZE_MAX / (size_t)ne1) return 0;
+    *bytes = rb * (size_t)ne1;
+    if (ne2 && *bytes > SIZE_MAX / (size_t)ne2) return 0;
+    *bytes *= (size_t)ne2;
+    off = (size_t)(t->data - g->base);
+    if (off > g->size || *bytes > g->size - off) return 0;
     return 1;
 }
 
@@ -374,12 +387,23 @@ int qr_gguf_model_host(const qr_gguf* g, int seq_len, qr_model* m, qr_layer* lay
     m->rope_base = qr_gguf_get_f32(g, key, 1000000.0f);
     if (dim <= 0 || L <= 0 || H <= 0 || KVH <= 0 || hd <= 0 || E <= 0 || K <= 0 || hid <= 0)
         return gg_fail(QR_ERR_UNSUPPORTED, "not a MoE GGUF this decoder serves");
+    /* sizes the later products (rows x row bytes x experts, in int and size_t)
+     * stay far from overflow with; every real model is well inside them */
+    if (dim > QR_GGUF_MAX_WIDTH || hid > QR_GGUF_MAX_WIDTH ||
+        (int64_t)H * hd > QR_GGUF_MAX_WIDTH || (int64_t)KVH * hd > QR_GGUF_MAX_WIDTH ||
+        L > QR_GGUF_MAX_COUNT || E > QR_GGUF_MAX_COUNT || K > E)
+        return gg_fail(QR_ERR_UNSUPPORTED, "model sizes beyond the loader's limits");
     it = qr_gguf_find(g, "token_embd.weight");
     if (it < 0) return gg_fail(QR_ERR_INVALID, "no token_embd.weight");
     /* vocab: the tokenizer's token count (src/model.c:306-312), else the
      * embedding's rows */
-    V = (int)qr_gguf_get_arr_len(g, "tokenizer.ggml.tokens");
-    if (V <= 0) V = (int)g->t[it].ne[1];
+    {
+        int64_t nv = qr_gguf_get_arr_len(g, "tokenizer.ggml.tokens");
+        if (nv <= 0) nv = (int64_t)g->t[it].ne[1];
+        if (nv <= 0 || nv > QR_GGUF_MAX_VOCAB)
+            return gg_fail(QR_ERR_UNSUPPORTED, "vocabulary size beyond the loader's limits");
+        V = (int)nv;
+    }
     if (!check_tensor(g, it, (uint64_t)dim, (uint64_t)V, 1, 0, &b))
         return gg_fail(QR_ERR_INVALID, "token_embd.weight shape or type");
     m->dim = dim;
@@ -503,10 +527,31 @@ int qr_gguf_expert_host(const qr_gguf* g, int layer, int e, const void** up, con
             if ((uint64_t)e >= (t->n_dims > 2 ? t->ne[2] : 1)) return QR_ERR_INVALID;
             if (outs[j]) *outs[j] = t->data + (size_t)e * slice;
         } else {
+            /* expert e's own tensor: the type and shape of expert 0's (which
+             * qr_gguf_model_host checked) and inside the file, as the
+             * gather reads expert 0's byte count from it */
+            int64_t i0;
+            const tensor_t *t, *t0;
+            size_t bytes;
+            snprintf(name, sizeof(name), "blk.%d.%s.0.weight", layer, kinds[j]);
+            i0 = qr_gguf_find(g, name);
             snprintf(name, sizeof(name), "blk.%d.%s.%d.weight", layer, kinds[j], e);
             i = qr_gguf_find(g, name);
-            if (i < 0) return QR_ERR_INVALID;
-            if (outs[j]) *outs[j] = g->t[i].data;
+            if (i < 0 || i0 < 0) return QR_ERR_INVALID;
+            t = &g->t[i];
+            t0 = &g->t[i0];
+            const uint64_t rows = t->n_dims > 1 ? t->ne[1] : 1;
+            if (t->type != t0->type || t->ne[0] != t0->ne[0] ||
+                rows != (t0->n_dims > 1 ? t0->ne[1] : 1) || t->n_dims > 2 ||
+                t->ne[0] > (uint64_t)INT_MAX || rows > (uint64_t)SIZE_MAX)
+                return QR_ERR_INVALID;
+            bytes = qr_row_bytes(t->type, (int)t->ne[0]);
+            if (rows && bytes > SIZE_MAX / (size_t)rows) return QR_ERR_INVALID;
+            bytes *= (size_t)rows;
+            if ((size_t)(t->data - g->base) > g->size ||
+                bytes > g->size - (size_t)(t->data - g->base))
+                return QR_ERR_INVALID;
+            if (outs[j]) *outs[j] = t->data;
         }
     }
     return QR_OK;

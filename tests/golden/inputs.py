@@ -227,3 +227,33 @@ def qwen3_small_model(seed=9500, n_layers=2, seq_len=640, n_kv_heads=2):
             down=blocks(s + 9, TYPE_Q6_K, E * dim * (hidden // 256))))
     m["layers"] = layers
     return m
+
+
+def qwen3_full_model(seed=9800, n_layers=2, seq_len=4352):
+    """The Qwen3-30B-A3B decode step at its full width: dim 2048, 32 query
+    heads over 4 kv heads of 128 (q_dim 4096), 128 experts top-8 with ffn 768
+    (gate / up Q4_K, down Q6_K), wq / wk / wo Q4_K and wv Q6_K, a Q4_K
+    embedding and a Q6_K lm_head of 151936 rows.  n_layers distinct layers
+    (about 400 MB of expert weights each)."""
+    dim, H, KVH, hd, E, K, hidden, vocab = 2048, 32, 4, 128, 128, 8, 768, 151936
+    wt = (TYPE_Q4_K, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q4_K)
+    m = dict(dim=dim, n_heads=H, n_kv_heads=KVH, head_dim=hd, n_layers=n_layers, E=E, K=K,
+             hidden=hidden, vocab=vocab, seq_len=seq_len, rope_base=1e6, wtype=list(wt),
+             tok_type=TYPE_Q4_K, wcls_type=TYPE_Q6_K, up_type=TYPE_Q4_K, down_type=TYPE_Q6_K)
+    m["tok_embd"] = _rows(seed, TYPE_Q4_K, vocab, dim)
+    m["wcls"] = _rows(seed + 1, TYPE_Q6_K, vocab, dim)
+    m["rms_final"] = (1.0 + activations(seed + 2, 1, dim, std=0.1)[0]).astype(np.float32)
+    layers = []
+    for l in range(n_layers):
+        s = seed + 10 + 20 * l
+        layers.append(dict(
+            rms_att=(1.0 + activations(s, 1, dim, std=0.1)[0]).astype(np.float32),
+            rms_ffn=(1.0 + activations(s + 1, 1, dim, std=0.1)[0]).astype(np.float32),
+            wq=_rows(s + 2, wt[0], H * hd, dim), wk=_rows(s + 3, wt[1], KVH * hd, dim),
+            wv=_rows(s + 4, wt[2], KVH * hd, dim), wo=_rows(s + 5, wt[3], dim, H * hd),
+            router=activations(s + 6, E, dim, std=0.05),
+            up=blocks(s + 7, TYPE_Q4_K, E * hidden * (dim // 256)),
+            gate=blocks(s + 8, TYPE_Q4_K, E * hidden * (dim // 256)),
+            down=blocks(s + 9, TYPE_Q6_K, E * dim * (hidden // 256))))
+    m["layers"] = layers
+    return m

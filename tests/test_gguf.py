@@ -214,3 +214,44 @@ def test_model_host_refuses_bad_shapes(case, match):
     data = G.decode_model_gguf(m, mutate=mut)[0]
     with pytest.raises(Q.QrError, match=match):
         Q.Gguf(data).model_host()
+
+
+@pytest.mark.parametrize("key,value", [("embedding_length", 1 << 21), ("expert_count", 5000),
+                                       ("expert_feed_forward_length", 1 << 21)])
+def test_model_host_refuses_sizes_beyond_limits(key, value):
+    """Widths and counts whose products (rows x row bytes x experts) could
+    approach size_t's range are refused before any size arithmetic."""
+    m = I.decode_model("a")
+    data, _ = G.decode_model_gguf(m)
+    kv = ("qwen3moe.%s" % key).encode()
+    i = data.index(kv) + len(kv) + 4  # the key's u32 value after its type
+    data = data[:i] + struct.pack("<I", value) + data[i + 4:]
+    with pytest.raises(Q.QrError, match="limits|shape|expert"):
+        Q.Gguf(data).model_host()
+
+
+@pytest.mark.parametrize("case", ["type", "rows", "past_end"])
+def test_expert_host_checks_each_expert(case):
+    """Per-expert tensors beyond expert 0 (which the mapping checks) are
+    checked when they are looked up for the gather: expert 1 of another type,
+    of other dimensions, or whose bytes run past the end of the file is
+    refused; expert 0 and the other experts still resolve."""
+    m = I.decode_model("a")
+    name = "blk.1.ffn_down_exps.1.weight"
+    if case == "type":
+        mut = _edit(name, lambda t: (t[0], 8, t[2], t[3]))
+    elif case == "rows":
+        mut = _edit(name, lambda t: (t[0], t[1], [t[2][0], t[2][1] * 2], t[3]))
+    else:
+        def mut(ts):
+            # expert 1's down tensor last, with no bytes: its data starts at the end
+            mine = [t for t in ts if t[0] == name][0]
+            return [t for t in ts if t[0] != name] + [(mine[0], mine[1], mine[2], b"")]
+    data, _ = G.decode_model_gguf(m, split_experts=True, mutate=mut)
+    g = Q.Gguf(data)
+    g.model_host()
+    g.expert_host(1, 0)
+    g.expert_host(1, 2)
+    with pytest.raises(Q.QrError, match="expert_host"):
+        g.expert_host(1, 1)
+    g.close()

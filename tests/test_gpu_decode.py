@@ -74,16 +74,18 @@ def prefilled(oracle, m, npre, seed):
 
 
 @pytest.mark.parametrize("graph", [0, Q.DEC_GRAPH], ids=["eager", "graph"])
-@pytest.mark.parametrize("order", [ORDER_SEQ, ORDER_AVX2])
-def test_decoder_q8_cache_head128(dev, oracle, order, graph):
+@pytest.mark.parametrize("order,kvh", [(ORDER_SEQ, 2), (ORDER_AVX2, 2), (ORDER_AVX2, 1)],
+                         ids=["seq_gqa4", "avx2_gqa4", "avx2_gqa8"])
+def test_decoder_q8_cache_head128(dev, oracle, order, kvh, graph):
     """Qwen3-like heads (head_dim 128, q_dim 1024 != dim 512, 8 heads over 2
-    kv heads) over a Q8_0 cache prefilled to 517 positions through a permuted
-    page table (pages of 64), then three decode steps at 517..519: logits,
-    residual and the cache rows the steps wrote, bit-exact with the oracle."""
-    m = I.qwen3_small_model(n_layers=2, seq_len=640)
+    kv heads, or over 1: GQA 8:1, the Qwen3-30B-A3B ratio) over a Q8_0 cache
+    prefilled to 517 positions through a permuted page table (pages of 64),
+    then three decode steps at 517..519: logits, residual and the cache rows
+    the steps wrote, bit-exact with the oracle."""
+    m = I.qwen3_small_model(n_layers=2, seq_len=640, n_kv_heads=kvh)
     npre = 517
     kv, kc, vc = prefilled(oracle, m, npre, seed=41)
-    print("decode head128 order %d graph %d" % (order, graph), flush=True)
+    print("decode head128 order %d kv heads %d graph %d" % (order, kvh, graph), flush=True)
     d = make_decoder(dev, m, Q.KV_Q8_0, order, page=64, flags=graph)
     ppl, page = d.pages()
     assert (ppl, page) == (10, 64)

@@ -56,8 +56,8 @@ def run(dev, qtype, W, X, n, d, nt):
 
 @pytest.mark.parametrize("nt", [1, 2, 3, 4, 8])
 @pytest.mark.parametrize("qtype", KT)
-@pytest.mark.parametrize("n,d", [(2048, 2048), (256, 2048), (2048, 5632), (1001, 2048),
-                                 (77, 256), (5, 16384)])
+@pytest.mark.parametrize("n,d", [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632),
+                                 (1001, 2048), (77, 256), (5, 16384)])
 def test_gemv_ggml_shapes(dev, oracle, qtype, n, d, nt):
     W = GB.random_rows(50 + n + d + qtype, qtype, n, d)
     X = synth.normal(60 + nt, (nt, d))
@@ -66,12 +66,15 @@ def test_gemv_ggml_shapes(dev, oracle, qtype, n, d, nt):
     assert_bits_equal(y, oracle.ggml_matmul(X, W, qtype, n, d), "ggml %d %dx%d nt=%d" % (qtype, n, d, nt))
 
 
+@pytest.mark.parametrize("nt", [1, 4])
 @pytest.mark.parametrize("qtype", KT)
-def test_gemv_ggml_lm_head(dev, oracle, qtype):
+def test_gemv_ggml_lm_head(dev, oracle, qtype, nt):
+    """The 32000 x 2048 lm_head at 1 token and at 4 (the width the benchmark
+    reports)."""
     W = GB.random_rows(70 + qtype, qtype, 32000, 2048)
-    X = synth.normal(71, (1, 2048))
-    y = run(dev, qtype, W, X, 32000, 2048, 1)
-    assert_bits_equal(y, oracle.ggml_matmul(X, W, qtype, 32000, 2048), "ggml lm_head")
+    X = synth.normal(71 + nt, (nt, 2048))
+    y = run(dev, qtype, W, X, 32000, 2048, nt)
+    assert_bits_equal(y, oracle.ggml_matmul(X, W, qtype, 32000, 2048), "ggml lm_head nt=%d" % nt)
 
 
 @pytest.mark.parametrize("qtype", KT)

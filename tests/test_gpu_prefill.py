@@ -7,10 +7,11 @@ loop of src/speculative.c:107-140 both call forward_runtime once per token).
   and its last residual, bit for bit, in every build.
 - A prefill followed by single-token steps continues exactly as the
   sequential decode does.
-- A Qwen3-like head shape over a Q8_0 cache in permuted pages of 64: 300
-  prompt tokens in chunks of 128 (the MFMA row products, three chunks) give the
-  logits, residual and cache rows of 300 sequential decode steps, bit for bit;
-  also with the projections stored tiled (GGUF load).
+- A Qwen3-like head shape (GQA 4:1 and 8:1) over a Q8_0 or fp32 cache in
+  permuted pages: 300 prompt tokens in chunks of 128 (the MFMA row products,
+  three chunks) give the oracle's logits at every position, its last residual
+  and its cache rows, bit for bit; also with the projections stored tiled
+  (GGUF load).
 """
 import numpy as np
 import pytest
@@ -96,27 +97,41 @@ def _kv_rows(dev, d, L, positions, rs):
     return np.stack(out)
 
 
+def oracle_prompt(oracle, m, toks, kv_type, order):
+    """The oracle over the whole prompt from an empty cache: every position's
+    logits, the residuals and the cache it wrote ([L][seq_len][row bytes])."""
+    rs = oracle.kv_row_bytes(kv_type, m["n_kv_heads"] * m["head_dim"])
+    kc = np.zeros((m["n_layers"], m["seq_len"], rs), np.uint8)
+    vc = np.zeros_like(kc)
+    lg, xs = oracle.forward_cached(m, kc.reshape(-1), vc.reshape(-1), [int(t) for t in toks], 0,
+                                   order, kv_type)
+    return lg, xs, kc, vc
+
+
+def _oracle_rows(kc, vc, L, positions):
+    out = []
+    for l in range(L):
+        for t in positions:
+            out.append(kc[l, t])
+            out.append(vc[l, t])
+    return np.stack(out)
+
+
 @pytest.mark.parametrize("source,page", [("pointers", 64), ("gguf_tiled", 64), ("pointers", 16)])
-def test_prefill_head128_chunks(dev, source, page):
+def test_prefill_head128_chunks(dev, oracle, source, page):
     """300 prompt tokens of a head_dim-128 model (q_dim 1024 != dim 512, GQA
     4:1) over a Q8_0 cache in permuted pages of 64 (16: pages smaller than
     the attention values' 32-position groups), prefilled in chunks of 128
-    (the projections as MFMA row products), against 300 sequential decode
-    steps: every token's logits, the last residual and the cache rows."""
+    (the projections as MFMA row products), against the oracle: every
+    token's logits, the last residual and the cache rows."""
     m = I.qwen3_small_model(n_layers=2, seq_len=320)
     rng = np.random.default_rng(9)
     toks = rng.integers(0, m["vocab"], size=300).astype(np.int32)
     order = ORDER_AVX2
-    ref = make_decoder(dev, m, Q.KV_Q8_0, order, page=page, flags=Q.DEC_GRAPH)
-    ppl, _ = ref.pages()
-    table = np.stack([rng.permutation(ppl) for _ in range(m["n_layers"])]).astype(np.int32)
-    ref.set_pages(table)
-    print("prefill head128 sequential reference", flush=True)
-    want_lg, want_x = sequential(dev, ref, m, toks)
-    rs = Q.load().qr_kv_row_bytes(Q.KV_Q8_0, m["n_kv_heads"] * m["head_dim"])
+    want_lg, want_xs, kc, vc = oracle_prompt(oracle, m, toks, Q.KV_Q8_0, order)
     probe = [0, 63, 64, 127, 128, 200, 299]
-    want_kv = _kv_rows(dev, ref, m["n_layers"], probe, rs)
-    ref.close()
+    want_kv = _oracle_rows(kc, vc, m["n_layers"], probe)
+    rs = kc.shape[2]
     if source == "gguf_tiled":
         gf = Q.Gguf(G.decode_model_gguf(m, head_dim_key=True)[0])
         gm = gf.load(dev, m["seq_len"])
@@ -124,32 +139,48 @@ def test_prefill_head128_chunks(dev, source, page):
         d = gm.decoder(kv_type=Q.KV_Q8_0, order=order, page=page)
     else:
         d = make_decoder(dev, m, Q.KV_Q8_0, order, page=page)
-    d.set_pages(table)
-    print("prefill head128 %s" % source, flush=True)
+    ppl, _ = d.pages()
+    d.set_pages(np.stack([rng.permutation(ppl) for _ in range(m["n_layers"])]).astype(np.int32))
+    print("prefill head128 %s page %d" % (source, page), flush=True)
     lg, x = prefill(dev, d, m, toks, chunk=128)
     kv = _kv_rows(dev, d, m["n_layers"], probe, rs)
     d.close()
     assert_bits_equal(lg, want_lg, "prefill logits")
-    assert_bits_equal(x, want_x, "prefill residual")
+    assert_bits_equal(x, want_xs[-1], "prefill residual")
     assert np.array_equal(kv, want_kv)
 
 
 @pytest.mark.parametrize("kv_type,page", [(Q.KV_Q8_0, 64), (Q.KV_F32, 16)],
                          ids=["q8_0_pages64", "f32_pages16"])
-def test_prefill_gqa8_chunks(dev, kv_type, page):
+def test_prefill_gqa8_chunks(dev, oracle, kv_type, page):
     """GQA 8:1 at head_dim 128, the shape whose prefill attention values run
     the query heads of a kv head in one workgroup (V staged once for the
-    eight): 300 prompt tokens in chunks of 128 against 300 sequential decode
-    steps, every token's logits and the last residual bit for bit."""
+    eight): 300 prompt tokens in chunks of 128 against the oracle, every
+    token's logits, the last residual and the cache rows bit for bit."""
     m = I.qwen3_small_model(n_layers=2, seq_len=320, n_kv_heads=1)
     rng = np.random.default_rng(19)
     toks = rng.integers(0, m["vocab"], size=300).astype(np.int32)
-    ref = make_decoder(dev, m, kv_type, ORDER_AVX2, page=page, flags=Q.DEC_GRAPH)
-    print("prefill gqa8 sequential reference", flush=True)
+    want_lg, want_xs, kc, vc = oracle_prompt(oracle, m, toks, kv_type, ORDER_AVX2)
+    probe = [0, 127, 128, 255, 256, 299]
+    d = make_decoder(dev, m, kv_type, ORDER_AVX2, page=page)
+    print("prefill gqa8 chunks kv %d page %d" % (kv_type, page), flush=True)
+    lg, x = prefill(dev, d, m, toks, chunk=128)
+    kv = _kv_rows(dev, d, m["n_layers"], probe, kc.shape[2])
+    d.close()
+    assert_bits_equal(lg, want_lg, "prefill logits")
+    assert_bits_equal(x, want_xs[-1], "prefill residual")
+    assert np.array_equal(kv, _oracle_rows(kc, vc, m["n_layers"], probe))
+
+
+def test_prefill_matches_sequential_decode(dev):
+    """Prefill in chunks of 128 against the same decoder's own single steps
+    (a consistency check beside the oracle comparisons above)."""
+    m = I.qwen3_small_model(n_layers=2, seq_len=320)
+    toks = np.random.default_rng(29).integers(0, m["vocab"], size=200).astype(np.int32)
+    ref = make_decoder(dev, m, Q.KV_Q8_0, ORDER_AVX2, page=64, flags=Q.DEC_GRAPH)
     want_lg, want_x = sequential(dev, ref, m, toks)
     ref.close()
-    d = make_decoder(dev, m, kv_type, ORDER_AVX2, page=page)
-    print("prefill gqa8 chunks", flush=True)
+    d = make_decoder(dev, m, Q.KV_Q8_0, ORDER_AVX2, page=64)
     lg, x = prefill(dev, d, m, toks, chunk=128)
     d.close()
     assert_bits_equal(lg, want_lg, "prefill logits")
