@@ -248,17 +248,21 @@ int qr_moe_forward_noalloc(qr_ctx* ctx, const qr_moe_layer* L, float* x, const f
 
 /* ---- single-token decode step (forward_runtime, src/runtime.c:94-288) ---- */
 
-/* KV cache row formats.  F32 is the reference's kv_cache_type 0
- * (src/runtime.c:74-92).  Q8_0 rows are quantize_row_q8_0 (src/quant.c:143-158)
- * of each position's kv_dim values, read back as qs * d like dequantize_row:
- * the reference's own type 2 is declared but unimplemented (kv_store_row
- * writes fp32 into a buffer sized at one byte per element, src/runtime.c:74-84
- * against src/model.c:82-88). */
+/* KV cache row formats.  F32 is the reference's kv_cache_type 0 and F16 its
+ * kv_cache_type 1 (src/runtime.c:74-92, selected by --kv-cache-quant fp16,
+ * src/main.c:140): each value stored with the truncating fp32_to_fp16 and read
+ * with fp16_to_fp32 (include/quant.h:53-77), half subnormals decoding as the
+ * reference decodes them.  Q8_0 rows are quantize_row_q8_0
+ * (src/quant.c:143-158) of each position's kv_dim values, read back as qs * d
+ * like dequantize_row: the reference's own type 2 is declared but
+ * unimplemented (kv_store_row writes fp32 into a buffer sized at one byte per
+ * element, src/runtime.c:74-84 against src/model.c:82-88). */
 #define QR_KV_F32 0
+#define QR_KV_F16 1
 #define QR_KV_Q8_0 2
 
-/* Bytes of one position's K (or V) row: kv_dim floats, or kv_dim / 32 Q8_0
- * blocks; 0 for a bad type or size. */
+/* Bytes of one position's K (or V) row: kv_dim floats, kv_dim halves, or
+ * kv_dim / 32 Q8_0 blocks; 0 for a bad type or size. */
 size_t qr_kv_row_bytes(int kv_type, int kv_dim);
 
 /* dequantize_row (src/quant.c:160-240) of `rows` rows of n elements each
@@ -284,10 +288,14 @@ int qr_attention(qr_ctx* ctx, const float* q, const void* kc, const void* vc,
                  const int32_t* ptab, int page, int kv_type, int npos, int n_heads,
                  int n_kv_heads, int head_dim, float* att, float* out);
 
-/* One transformer layer's device weights (src/model.c:358-434): attention
+/* One transformer layer's device weights (src/model.c:358-446): attention
  * projections [rows][cols] in GGUF row order (wq [n_heads * head_dim][dim],
  * wk / wv [n_kv_heads * head_dim][dim], wo [dim][n_heads * head_dim]) and the
- * MoE block (moe.dim == dim). */
+ * MoE block (moe.dim == dim).  moe.n_experts == 0 makes the layer dense, as
+ * expert_count == 0 does in the reference (src/runtime.c:270-284): moe.up,
+ * moe.gate and moe.down are then its ffn_up (w1, the SiLU slot), ffn_gate
+ * (w3) and ffn_down (w2) matrices of moe.hidden rows (columns for down), and
+ * the router and n_used are not read. */
 typedef struct {
     const float* rms_att;  /* [dim] */
     const float* rms_ffn;  /* [dim] */

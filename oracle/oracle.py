@@ -66,7 +66,7 @@ class OModel(C.Structure):
     ]
 
 
-KV_F32, KV_Q8_0 = 0, 2
+KV_F32, KV_F16, KV_Q8_0 = 0, 1, 2
 
 
 def oracle_threads():
@@ -620,7 +620,8 @@ class RefLib:
         token_embd_row_bytes) as refdrv_load_gguf lays them out."""
         cfg = np.zeros(9, np.int32)
         rope = np.zeros(1, np.float32)
-        off = np.zeros(3 + 7 * n_layers + 3 * n_layers * n_experts, np.int64)
+        # a dense model (no experts) reports its w1 / w2 / w3 in the experts' places
+        off = np.zeros(3 + 7 * n_layers + 3 * n_layers * max(n_experts, 1), np.int64)
         types = np.zeros(2 + 7 * n_layers, np.uint32)
         rb = np.zeros(1, np.uint64)
         n = self.lib.refdrv_load_gguf(path.encode(), _ptr(cfg), _ptr(rope), _ptr(off), _ptr(types),

@@ -553,6 +553,25 @@ void qro_moe_token(float* x, const float* xb, const qro_moe_layer* L, int router
     free(buf);
 }
 
+/* The dense FFN of forward_runtime (src/runtime.c:270-284), a layer with
+ * n_experts == 0: hb = up . xb (w1, the SiLU slot), hb2 = gate . xb (w3),
+ * hb = silu(hb) * hb2, xb = down . hb (w2), x += xb. */
+void qro_dense_ffn(float* x, const float* xb, const qro_moe_layer* L, int order, int threads) {
+    int dim = L->dim, H = L->hidden, i;
+    float* buf = (float*)malloc(((size_t)dim + (size_t)H * 2) * sizeof(float));
+    float *y, *hb, *hb2;
+    if (!buf) return;
+    y = buf;
+    hb = buf + dim;
+    hb2 = hb + H;
+    matmul_any(hb, xb, L->up, L->up_type, H, dim, threads, order, order);
+    matmul_any(hb2, xb, L->gate, L->gate_type, H, dim, threads, order, order);
+    for (i = 0; i < H; i++) hb[i] = qro_silu(hb[i]) * hb2[i];
+    matmul_any(y, hb, L->down, L->down_type, dim, H, threads, order, order);
+    for (i = 0; i < dim; i++) x[i] += y[i];
+    free(buf);
+}
+
 /* T independent tokens: the reference runs one forward_runtime per token
  * (src/runtime.c:294-304), so the batch is the per-token block in order. */
 void qro_moe_forward(float* x, const float* xb, int T, const qro_moe_layer* L, int router_order,

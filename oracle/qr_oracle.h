@@ -115,6 +115,7 @@ size_t qro_expert_slice_bytes(uint32_t type, int ne0, int ne1);
 
 /* router_order: the router's KernelOps.matmul order (and F32 experts');
  * dot_order: the Q8_0 fused-dot order of the build (K-quant dots have one). */
+void qro_dense_ffn(float* x, const float* xb, const qro_moe_layer* L, int order, int threads);
 void qro_moe_token(float* x, const float* xb, const qro_moe_layer* L, int router_order,
                    int dot_order, int threads, int32_t* idx_out, float* w_out);
 void qro_moe_forward(float* x, const float* xb, int T, const qro_moe_layer* L, int router_order,
@@ -125,12 +126,13 @@ int qro_moe_dispatch(const int32_t* idx, int T, int K, int E, int32_t* counts,
 
 /* ---- the single-token decode step (qr_oracle_decode.c) ------------------ */
 #define QRO_KV_F32 0
+#define QRO_KV_F16 1
 #define QRO_KV_Q8_0 2
 
 typedef struct {
     int dim, n_layers, n_heads, n_kv_heads, head_dim, vocab, seq_len;
     float rope_base;
-    int kv_type;                 /* QRO_KV_F32 or QRO_KV_Q8_0 */
+    int kv_type;                 /* QRO_KV_F32, QRO_KV_F16 or QRO_KV_Q8_0 */
     const void* tok_embd;        /* [vocab] rows of tok_row_bytes */
     uint32_t tok_type;
     size_t tok_row_bytes;

@@ -10,13 +10,15 @@
  *     src/runtime.c:102), q has n_heads * head_dim elements and RoPE is
  *     apply_rope over that whole vector (src/runtime.c:19-41, its `dim`
  *     argument being the q length, as in the reference where q_dim == dim);
- *   - the KV cache holds fp32 rows (the reference's type 0) or Q8_0 rows
- *     (quantize_row_q8_0 of each position's kv_dim values; an element reads
- *     as qs * d like dequantize_row, src/quant.c:169-176): the reference's own
- *     type 2 is unimplemented (src/runtime.c:74-84 writes fp32 into a buffer
- *     sized at one byte per element, src/model.c:82-88).
- * With head_dim = dim / n_heads and an fp32 cache, qro_forward is pinned bit
- * for bit to the reference's forward_runtime by golden logits
+ *   - the KV cache holds fp32 rows (the reference's type 0), fp16 rows (its
+ *     type 1: kv_store_row's truncating fp32_to_fp16 and kv_get_element's
+ *     fp16_to_fp32, src/runtime.c:74-92) or Q8_0 rows (quantize_row_q8_0 of
+ *     each position's kv_dim values; an element reads as qs * d like
+ *     dequantize_row, src/quant.c:169-176): the reference's own type 2 is
+ *     unimplemented (src/runtime.c:74-84 writes fp32 into a buffer sized at
+ *     one byte per element, src/model.c:82-88).
+ * With head_dim = dim / n_heads and an fp32 or fp16 cache, qro_forward is
+ * pinned bit for bit to the reference's forward_runtime by golden logits
  * (tests/golden/decode.npz).
  */
 #include <math.h>
@@ -77,17 +79,32 @@ static float kv_elem(const uint8_t* row, int kv_type, int i) {
         const uint8_t* b = row + (size_t)(i / QK8) * Q8_BYTES;
         return (float)(int8_t)b[2 + i % QK8] * qro_h2f((uint16_t)(b[0] | (b[1] << 8)));
     }
+    if (kv_type == QRO_KV_F16) /* kv_get_element, src/runtime.c:87-92 */
+        return qro_h2f((uint16_t)(row[2 * i] | (row[2 * i + 1] << 8)));
     return ((const float*)row)[i];
 }
 
 size_t qro_kv_row_bytes(int kv_type, int kv_dim) {
-    return kv_type == QRO_KV_Q8_0 ? (size_t)(kv_dim / QK8) * Q8_BYTES : (size_t)kv_dim * 4;
+    if (kv_type == QRO_KV_Q8_0) return (size_t)(kv_dim / QK8) * Q8_BYTES;
+    return (size_t)kv_dim * (kv_type == QRO_KV_F16 ? 2 : 4);
 }
 
-/* One position's K or V row into the cache: fp32 copy, or quantize_row_q8_0. */
+/* One position's K or V row into the cache: fp32 copy, truncated halves
+ * (kv_store_row, src/runtime.c:74-79), or quantize_row_q8_0. */
 void qro_kv_store(void* row, const float* src, int kv_dim, int kv_type) {
-    if (kv_type == QRO_KV_Q8_0) qro_quantize_row_q8_0(src, row, kv_dim);
-    else memcpy(row, src, (size_t)kv_dim * sizeof(float));
+    int i;
+    if (kv_type == QRO_KV_Q8_0) {
+        qro_quantize_row_q8_0(src, row, kv_dim);
+    } else if (kv_type == QRO_KV_F16) {
+        uint8_t* r = (uint8_t*)row;
+        for (i = 0; i < kv_dim; i++) {
+            uint16_t h = qro_f2h(src[i]);
+            r[2 * i] = (uint8_t)(h & 0xFF);
+            r[2 * i + 1] = (uint8_t)(h >> 8);
+        }
+    } else {
+        memcpy(row, src, (size_t)kv_dim * sizeof(float));
+    }
 }
 
 /* The attention of forward_runtime (src/runtime.c:136-193) at position pos:
@@ -183,7 +200,8 @@ void qro_forward(const qro_model* m, void* kc, void* vc, int token, int pos, int
         mq(xb2, ao, m->wo[l], m->wtype[4 * l + 3], dim, qd, order, m->threads);
         for (i = 0; i < dim; i++) x[i] += xb2[i];
         qro_rmsnorm(xb, x, m->rms_ffn[l], dim);
-        qro_moe_token(x, xb, &m->moe[l], order, order, m->threads, NULL, NULL);
+        if (m->moe[l].n_experts == 0) qro_dense_ffn(x, xb, &m->moe[l], order, m->threads);
+        else qro_moe_token(x, xb, &m->moe[l], order, order, m->threads, NULL, NULL);
     }
     qro_rmsnorm(xb, x, m->rms_final, dim);
     mq(logits, xb, m->wcls, m->wcls_type, m->vocab, dim, order, m->threads);

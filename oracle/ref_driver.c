@@ -336,7 +336,8 @@ int refdrv_gemv_bench(const float* x, const void* const* w_copies, int ncopies, 
  * tokens at positions 0 .. n_tokens-1 (the KV cache fills as it goes).
  * Per-layer tensors are arrays of L pointers (NULL allowed where the reference
  * allows it); wtype[l * 4 + {0,1,2,3}] are the types of wq, wk, wv, wo; MoE
- * experts are [E][rows][cols] tensors sliced as src/model.c:412-419 does.
+ * experts are [E][rows][cols] tensors sliced as src/model.c:412-419 does; with
+ * E = 0 up / gate / down are the dense FFN's w1 / w3 / w2 per layer.
  * kv_type: the reference's RunState.kv_cache_type (0 fp32, 1 fp16).
  * logits_out: [n_tokens][vocab]; x_out (optional): the residual after the
  * last layer, [n_tokens][dim].
@@ -436,6 +437,14 @@ int refdrv_forward(int dim, int hidden, int n_layers, int n_heads, int n_kv_head
     t.weights.exp_w1_type = t_up;
     t.weights.exp_w2_type = t_down;
     t.weights.exp_w3_type = t_gate;
+    if (E == 0) { /* a dense model: w1 = ffn_up, w3 = ffn_gate, w2 = ffn_down (src/model.c:434-446) */
+        t.weights.w1 = (float**)up;
+        t.weights.w3 = (float**)gate;
+        t.weights.w2 = (float**)down;
+        t.weights.w1_type = t_up;
+        t.weights.w3_type = t_gate;
+        t.weights.w2_type = t_down;
+    }
     if (kv_type == 0) malloc_run_state(&t.state, &t.config);
     else malloc_run_state_kv(&t.state, &t.config, kv_type);
     memset(&opt, 0, sizeof(opt));
@@ -516,10 +525,11 @@ int refdrv_gguf_vals(void* buf, size_t size, const char* key, uint32_t def_u32, 
  * expert_count, expert_used_count; rope the freq base.  off receives the file
  * offset of every weight pointer the loader set (-1 when NULL), in this order:
  * token_embedding_table, rms_final_weight, wcls, then per layer rms_att, rms_ffn,
- * wq, wk, wv, wo, ffn_gate_inp, then per layer and expert w1, w2, w3.
- * types: token_embd_type, wcls_type, then per layer wq, wk, wv, wo, exp_w1,
- * exp_w2, exp_w3 types; row_bytes: token_embd_row_bytes.  The file must be a
- * valid MoE GGUF (the reference exits otherwise). */
+ * wq, wk, wv, wo, ffn_gate_inp, then per layer and expert w1, w2, w3 (a dense
+ * model: per layer its w1, w2, w3).  types: token_embd_type, wcls_type, then
+ * per layer wq, wk, wv, wo, exp_w1, exp_w2, exp_w3 types (a dense model: w1,
+ * w2, w3); row_bytes: token_embd_row_bytes.  The file must be a valid GGUF
+ * model (the reference exits otherwise). */
 int refdrv_load_gguf(const char* path, int* cfg, float* rope, int64_t* off, uint32_t* types,
                      uint64_t* row_bytes) {
     Transformer t;
@@ -556,16 +566,28 @@ int refdrv_load_gguf(const char* path, int* cfg, float* rope, int64_t* off, uint
         types[m++] = t.weights.wk_type[l];
         types[m++] = t.weights.wv_type[l];
         types[m++] = t.weights.wo_type[l];
-        types[m++] = t.weights.exp_w1_type[l];
-        types[m++] = t.weights.exp_w2_type[l];
-        types[m++] = t.weights.exp_w3_type[l];
+        if (t.config.expert_count > 0) {
+            types[m++] = t.weights.exp_w1_type[l];
+            types[m++] = t.weights.exp_w2_type[l];
+            types[m++] = t.weights.exp_w3_type[l];
+        } else { /* a dense model: w1 / w2 / w3 in the experts' places */
+            types[m++] = t.weights.w1_type[l];
+            types[m++] = t.weights.w2_type[l];
+            types[m++] = t.weights.w3_type[l];
+        }
     }
-    for (l = 0; l < t.config.n_layers; l++)
+    for (l = 0; l < t.config.n_layers; l++) {
+        if (t.config.expert_count == 0) {
+            off[n++] = OFF(t.weights.w1[l]);
+            off[n++] = OFF(t.weights.w2[l]);
+            off[n++] = OFF(t.weights.w3[l]);
+        }
         for (e = 0; e < t.config.expert_count; e++) {
             off[n++] = OFF(t.weights.expert_w1[l][e]);
             off[n++] = OFF(t.weights.expert_w2[l][e]);
             off[n++] = OFF(t.weights.expert_w3[l][e]);
         }
+    }
 #undef OFF
     free_transformer(&t);
     return n;

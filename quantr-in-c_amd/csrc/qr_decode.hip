@@ -235,6 +235,36 @@ struct KvView {
   }
 };
 
+// One 32-element block of a position's row as kv_cache_type 1 stores it: each
+// value by the reference's truncating fp32_to_fp16 (src/runtime.c:74-79),
+// written as four 16-byte stores.
+__device__ inline void f16_block_store(const float* vals, uint8_t* dst) {
+  uint4* d4 = reinterpret_cast<uint4*>(dst);
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    uint4 w;
+    w.x = qr_f2h(vals[8 * j]) | (qr_f2h(vals[8 * j + 1]) << 16);
+    w.y = qr_f2h(vals[8 * j + 2]) | (qr_f2h(vals[8 * j + 3]) << 16);
+    w.z = qr_f2h(vals[8 * j + 4]) | (qr_f2h(vals[8 * j + 5]) << 16);
+    w.w = qr_f2h(vals[8 * j + 6]) | (qr_f2h(vals[8 * j + 7]) << 16);
+    d4[j] = w;
+  }
+}
+
+// Element col of a cache row as the attention reads it (kv_get_element,
+// src/runtime.c:87-92, for fp32 and fp16 rows; qs * d for Q8_0 rows).
+template <int KVT>
+__device__ inline float kv_value(const uint8_t* row, int col) {
+  if constexpr (KVT == QR_KV_Q8_0) {
+    const uint8_t* blk = row + (size_t)(col >> 5) * QR_Q8_BYTES;
+    return (float)(int8_t)blk[2 + (col & 31)] * qr_h2f(*reinterpret_cast<const uint16_t*>(blk));
+  } else if constexpr (KVT == QR_KV_F16) {
+    return qr_h2f(reinterpret_cast<const uint16_t*>(row)[col]);
+  } else {
+    return reinterpret_cast<const float*>(row)[col];
+  }
+}
+
 // npos = st[1] + 1 when the position comes from device state (a captured
 // decode step), else the argument.
 __device__ inline int npos_of(const int32_t* st, int npos) { return st ? st[1] + 1 : npos; }
@@ -295,6 +325,8 @@ __global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ q, const fl
   uint8_t* row = isv ? vbase + (size_t)(krow - K.base) : krow;
   if (K.kv_type == QR_KV_Q8_0) {
     q8_block_store(vals, row + (size_t)bi * QR_Q8_BYTES);
+  } else if (K.kv_type == QR_KV_F16) {
+    f16_block_store(vals, row + (size_t)bi * 64);
   } else {
     float4* dst = reinterpret_cast<float4*>(reinterpret_cast<float*>(row) + 32 * bi);
 #pragma unroll
@@ -304,8 +336,8 @@ __global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ q, const fl
 }
 
 // Rows [t0, t0 + n) of one layer's K and V caches from fp32 values
-// (src [n][kvd]): fp32 copies or quantize_row_q8_0 blocks.  One thread per
-// 32-element block.
+// (src [n][kvd]): fp32 copies, truncated halves or quantize_row_q8_0 blocks.
+// One thread per 32-element block.
 __global__ __launch_bounds__(256) void k_kv_write(const float* __restrict__ ksrc,
                                                   const float* __restrict__ vsrc, int t0, int n,
                                                   int kvd, KvView K, uint8_t* __restrict__ vbase) {
@@ -319,10 +351,11 @@ __global__ __launch_bounds__(256) void k_kv_write(const float* __restrict__ ksrc
     const float* src = (isv ? vsrc : ksrc) + (size_t)t * kvd + 32 * b;
     uint8_t* krow = const_cast<uint8_t*>(K.row(t0 + t));
     uint8_t* row = isv ? vbase + (size_t)(krow - K.base) : krow;
-    if (K.kv_type == QR_KV_Q8_0) {
+    if (K.kv_type == QR_KV_Q8_0 || K.kv_type == QR_KV_F16) {
       float vals[32];
       for (int j = 0; j < 32; j++) vals[j] = src[j];
-      q8_block_store(vals, row + (size_t)b * QR_Q8_BYTES);
+      if (K.kv_type == QR_KV_Q8_0) q8_block_store(vals, row + (size_t)b * QR_Q8_BYTES);
+      else f16_block_store(vals, row + (size_t)b * 64);
     } else {
       float* dst = reinterpret_cast<float*>(row) + 32 * b;
       for (int j = 0; j < 32; j++) dst[j] = src[j];
@@ -434,6 +467,12 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
 #pragma unroll
         for (int j = 0; j < 32; j++) dst[j] = (float)(int8_t)blk[2 + j] * d;
       }
+    } else if (K.kv_type == QR_KV_F16) {
+      f16_block_store(vals, row + (size_t)(kvh * nbh + b) * 64);
+      if (!isv) {
+#pragma unroll
+        for (int j = 0; j < 32; j++) dst[j] = qr_h2f(qr_f2h(vals[j]));
+      }
     } else {
       float* out = reinterpret_cast<float*>(row) + (size_t)kvh * hd + 32 * b;
 #pragma unroll
@@ -464,6 +503,19 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
         f.w = (float)(int8_t)(u[2 + 2 * w] >> 8) * d;
         *reinterpret_cast<float4*>(dst + 4 * w) = f;
       }
+    }
+  } else if (K.kv_type == QR_KV_F16) {
+    for (int j = threadIdx.x * 4; j < nt * hd; j += blockDim.x * 4) {
+      const int tt = j / hd, i = j - tt * hd;
+      if (ROPE && tt == cur) continue;  // staged above
+      const uint2 w = *reinterpret_cast<const uint2*>(
+          reinterpret_cast<const uint16_t*>(K.row(t0 + tt)) + (size_t)kvh * hd + i);
+      float4 f;
+      f.x = qr_h2f(w.x & 0xFFFFu);
+      f.y = qr_h2f(w.x >> 16);
+      f.z = qr_h2f(w.y & 0xFFFFu);
+      f.w = qr_h2f(w.y >> 16);
+      *reinterpret_cast<float4*>(kt + tt * ks + i) = f;
     }
   } else {
     for (int j = threadIdx.x * 4; j < nt * hd; j += blockDim.x * 4) {
@@ -543,7 +595,8 @@ constexpr int kAttnMaxPos = 22528;  // exponentials (LDS) beside the product buf
 constexpr int kSvProd = 256;
 constexpr int kSvPer = kValBlk / kSvProd;
 struct SvRegs {
-  uint32_t r[kSvPer][kValCols];  // Q8_0: [0] = d, [1..8] = the 32 qs bytes; fp32: the values
+  uint32_t r[kSvPer][kValCols];  // Q8_0: [0] = d, [1..8] = the 32 qs bytes; fp16: [0..15] =
+                                 // the 32 halves in pairs; fp32: the values
 };
 
 // V.row(t) with the page table read from LDS (pt), so that a row's address
@@ -568,6 +621,16 @@ __device__ inline void sv_load(SvRegs& R, const KvView& V, const int32_t* pt, in
       const uint8_t* blk = row + (size_t)(e0 >> 5) * QR_Q8_BYTES;
       R.r[u][0] = *reinterpret_cast<const uint16_t*>(blk);
       __builtin_memcpy(&R.r[u][1], blk + 2, 32);  // 2-byte aligned
+    } else if constexpr (KVT == QR_KV_F16) {
+      const uint4* f = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(row) + e0);
+#pragma unroll
+      for (int j = 0; j < kValCols / 8; j++) {
+        const uint4 w = f[j];
+        R.r[u][4 * j] = w.x;
+        R.r[u][4 * j + 1] = w.y;
+        R.r[u][4 * j + 2] = w.z;
+        R.r[u][4 * j + 3] = w.w;
+      }
     } else {
       const uint4* f = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(row) + e0);
 #pragma unroll
@@ -601,6 +664,10 @@ __device__ inline void sv_produce(const SvRegs& R, int b, int npos, int pid,
           pb[(4 * j + q) * kValPitch + tt] = at * v;
         }
       }
+    } else if constexpr (KVT == QR_KV_F16) {
+#pragma unroll
+      for (int c = 0; c < kValCols; c++)
+        pb[c * kValPitch + tt] = at * qr_h2f((R.r[u][c >> 1] >> (16 * (c & 1))) & 0xFFFFu);
     } else {
 #pragma unroll
       for (int c = 0; c < kValCols; c++) pb[c * kValPitch + tt] = at * __uint_as_float(R.r[u][c]);
@@ -800,14 +867,7 @@ __global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ 
       float v[U];
 #pragma unroll
       for (int u = 0; u < U; u++) {
-        const uint8_t* row = row0 + (size_t)u * V.row_bytes;
-        if constexpr (KVT == QR_KV_Q8_0) {
-          const uint8_t* blk = row + (size_t)(col >> 5) * QR_Q8_BYTES;
-          const float d = qr_h2f(*reinterpret_cast<const uint16_t*>(blk));
-          v[u] = (float)(int8_t)blk[2 + (col & 31)] * d;
-        } else {
-          v[u] = reinterpret_cast<const float*>(row)[col];
-        }
+        v[u] = kv_value<KVT>(row0 + (size_t)u * V.row_bytes, col);
       }
 #pragma unroll
       for (int u = 0; u < U; u++) acc += e[t + u] * v[u];
@@ -817,28 +877,14 @@ __global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ 
     float v[8];
 #pragma unroll
     for (int u = 0; u < 8; u++) {
-      const uint8_t* row = V.row(t + u);  // one address per wave: the page table by scalar loads
-      if constexpr (KVT == QR_KV_Q8_0) {
-        const uint8_t* blk = row + (size_t)(col >> 5) * QR_Q8_BYTES;
-        const float d = qr_h2f(*reinterpret_cast<const uint16_t*>(blk));
-        v[u] = (float)(int8_t)blk[2 + (col & 31)] * d;
-      } else {
-        v[u] = reinterpret_cast<const float*>(row)[col];
-      }
+      // one address per wave: the page table by scalar loads
+      v[u] = kv_value<KVT>(V.row(t + u), col);
     }
 #pragma unroll
     for (int u = 0; u < 8; u++) acc += e[t + u] * v[u];
   }
   for (; t < npos; t++) {
-    const uint8_t* row = V.row(t);
-    float v;
-    if constexpr (KVT == QR_KV_Q8_0) {
-      const uint8_t* blk = row + (size_t)(col >> 5) * QR_Q8_BYTES;
-      v = (float)(int8_t)blk[2 + (col & 31)] * qr_h2f(*reinterpret_cast<const uint16_t*>(blk));
-    } else {
-      v = reinterpret_cast<const float*>(row)[col];
-    }
-    acc += e[t] * v;
+    acc += e[t] * kv_value<KVT>(V.row(t), col);
   }
   out[tid] = acc;
 }
@@ -926,6 +972,8 @@ __global__ __launch_bounds__(1024) void k_attn_sv_gqa(const float* __restrict__ 
         const uint8_t* blk = row + ((col0 + cc) >> 5) * QR_Q8_BYTES;
         rd[k] = *reinterpret_cast<const uint16_t*>(blk);
         rq[k] = (uint32_t)blk[2 + ((col0 + cc) & 31)];
+      } else if constexpr (KVT == QR_KV_F16) {
+        rq[k] = reinterpret_cast<const uint16_t*>(row)[col0 + cc];
       } else {
         rq[k] = reinterpret_cast<const uint32_t*>(row)[col0 + cc];
       }
@@ -942,6 +990,7 @@ __global__ __launch_bounds__(1024) void k_attn_sv_gqa(const float* __restrict__ 
       const int idx = tid + nthr * k;
       float v;
       if constexpr (KVT == QR_KV_Q8_0) v = (float)(int8_t)(uint8_t)rq[k] * qr_h2f((uint16_t)rd[k]);
+      else if constexpr (KVT == QR_KV_F16) v = qr_h2f(rq[k]);
       else v = __uint_as_float(rq[k]);
       vb[idx] = v;  // [u][cc] = idx
     }
@@ -1008,6 +1057,8 @@ hipError_t sv_rows_launch(const float* att, int att_stride, const KvView& V, con
     const size_t l = sv_gqa_lds(ecap, kv_mul, hd, V.page);
     if (V.kv_type == QR_KV_Q8_0)
       return gqa_launch_kv<QR_KV_Q8_0>(g, l, s, att, att_stride, V, st, ecap, kv_mul, hd, out);
+    if (V.kv_type == QR_KV_F16)
+      return gqa_launch_kv<QR_KV_F16>(g, l, s, att, att_stride, V, st, ecap, kv_mul, hd, out);
     return gqa_launch_kv<QR_KV_F32>(g, l, s, att, att_stride, V, st, ecap, kv_mul, hd, out);
   }
   const dim3 grid(n_heads, tokens);
@@ -1015,6 +1066,9 @@ hipError_t sv_rows_launch(const float* att, int att_stride, const KvView& V, con
   const size_t lds = (size_t)lds_cap * 4;
   if (V.kv_type == QR_KV_Q8_0)
     hipLaunchKernelGGL(k_attn_sv_rows<QR_KV_Q8_0>, grid, dim3(threads), lds, s, att, att_stride, V,
+                       st, lds_cap, kv_mul, hd, out);
+  else if (V.kv_type == QR_KV_F16)
+    hipLaunchKernelGGL(k_attn_sv_rows<QR_KV_F16>, grid, dim3(threads), lds, s, att, att_stride, V,
                        st, lds_cap, kv_mul, hd, out);
   else
     hipLaunchKernelGGL(k_attn_sv_rows<QR_KV_F32>, grid, dim3(threads), lds, s, att, att_stride, V,
@@ -1034,6 +1088,9 @@ hipError_t sv_launch(const float* att, int att_stride, const KvView& V, const in
   const size_t lds = sv_lds_bytes(lds_cap, V.page);
   if (V.kv_type == QR_KV_Q8_0)
     hipLaunchKernelGGL(k_attn_sv<QR_KV_Q8_0>, grid, dim3(kSvThreads), lds, s, att, att_stride, V,
+                       st, npos, lds_cap, kv_mul, hd, out);
+  else if (V.kv_type == QR_KV_F16)
+    hipLaunchKernelGGL(k_attn_sv<QR_KV_F16>, grid, dim3(kSvThreads), lds, s, att, att_stride, V,
                        st, npos, lds_cap, kv_mul, hd, out);
   else
     hipLaunchKernelGGL(k_attn_sv<QR_KV_F32>, grid, dim3(kSvThreads), lds, s, att, att_stride, V,
@@ -1104,8 +1161,10 @@ std::atomic<bool> g_sc_opt[64];
 std::atomic<bool> g_sc_opt_r[64];
 std::atomic<bool> g_sm_opt[64];
 std::atomic<bool> g_sm_opt2[64];
+std::atomic<bool> g_sm_opt3[64];
 std::atomic<bool> g_rows_opt[64];
 std::atomic<bool> g_rows_opt2[64];
+std::atomic<bool> g_rows_opt3[64];
 
 #define DEC_HIP(call, what)                                                        \
   do {                                                                             \
@@ -1153,6 +1212,38 @@ static bool qk_stacked(const qr_decoder* d, const qr_layer& L) {
 
 // The decode step's kernels, in order, on stream s (the state holds the
 // token and the position).
+// The dense FFN's SwiGLU (src/runtime.c:278-280): g = silu(u) * g with u the
+// w1 (SiLU slot) rows and g the w3 rows.
+__global__ __launch_bounds__(256) void k_swiglu(const float* __restrict__ u, float* __restrict__ g,
+                                                long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
+    g[i] = qr_silu(u[i]) * g[i];
+}
+
+// x += y (the dense FFN's residual, src/runtime.c:282-284), n a multiple of 4.
+__global__ __launch_bounds__(256) void k_add4(float* __restrict__ x, const float* __restrict__ y,
+                                              long n4) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (long)gridDim.x * blockDim.x) {
+    float4 a = reinterpret_cast<float4*>(x)[i];
+    const float4 b = reinterpret_cast<const float4*>(y)[i];
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
+    reinterpret_cast<float4*>(x)[i] = a;
+  }
+}
+
+// A layer without experts (moe.n_experts == 0) has the dense SwiGLU FFN of
+// forward_runtime (src/runtime.c:270-284): w1 = moe.up (ffn_up, the SiLU
+// slot), w3 = moe.gate (ffn_gate), w2 = moe.down (ffn_down).
+inline bool is_dense(const qr_layer& L) { return L.moe.n_experts == 0; }
+
+// Its scratch for T tokens: the w1 rows, the w3 rows (then hb) and w2's output.
+inline size_t dense_scratch_bytes(const qr_moe_layer& M, int T) {
+  return (size_t)T * (2 * (size_t)M.hidden + (size_t)M.dim) * 4;
+}
+
 hipError_t enqueue_step(qr_decoder* d, float* logits, float* xout, hipStream_t s) {
   hipError_t e;
   const int dim = d->dim;
@@ -1161,9 +1252,11 @@ hipError_t enqueue_step(qr_decoder* d, float* logits, float* xout, hipStream_t s
                      d->st, dim, d->x);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const float inv_sqrt = 1.0f / sqrtf((float)d->hd);
+  const float* pend = nullptr;  // a dense FFN's output, added to x by the next norm
   for (int l = 0; l < d->nl; l++) {
     const qr_layer& L = d->layers[l];
-    if ((e = rmsnorm_launch(d->x, nullptr, L.rms_att, dim, d->xb, s))) return e;
+    if ((e = rmsnorm_launch(d->x, pend, L.rms_att, dim, d->xb, s))) return e;
+    pend = nullptr;
     if (qk_stacked(d, L)) {
       if ((e = matmul_q_dev(L.wq, L.wq_type, d->order, d->xb, d->q, d->qd + d->kvd, dim, s)))
         return e;
@@ -1183,11 +1276,25 @@ hipError_t enqueue_step(qr_decoder* d, float* logits, float* xout, hipStream_t s
       return e;
     if ((e = matmul_q_dev(L.wo, L.wo_type, d->order, d->ao, d->xb2, dim, d->qd, s))) return e;
     if ((e = rmsnorm_launch(d->x, d->xb2, L.rms_ffn, dim, d->xb, s))) return e;
+    if (is_dense(L)) {
+      const qr_moe_layer& M = L.moe;
+      float* u = reinterpret_cast<float*>(d->moe_base);
+      float* g = u + M.hidden;
+      float* y = g + M.hidden;
+      if ((e = matmul_q_dev(M.up, M.up_type, d->order, d->xb, u, M.hidden, dim, s))) return e;
+      if ((e = matmul_q_dev(M.gate, M.gate_type, d->order, d->xb, g, M.hidden, dim, s))) return e;
+      hipLaunchKernelGGL(k_swiglu, dim3((M.hidden + 255) / 256), dim3(256), 0, s, u, g,
+                         (long)M.hidden);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+      if ((e = matmul_q_dev(M.down, M.down_type, d->order, g, y, dim, M.hidden, s))) return e;
+      pend = y;
+      continue;
+    }
     MoeScratch ms;
     moe_scratch_carve(d->moe_base, &L.moe, 1, &ms);
     if ((e = moe_forward_launch(&L.moe, d->x, d->xb, 1, d->order, ms, s))) return e;
   }
-  if ((e = rmsnorm_launch(d->x, nullptr, d->rms_final, dim, d->xb, s))) return e;
+  if ((e = rmsnorm_launch(d->x, pend, d->rms_final, dim, d->xb, s))) return e;
   if ((e = matmul_q_dev(d->wcls, d->wcls_type, d->order, d->xb, logits, d->vocab, dim, s)))
     return e;
   if (xout) {
@@ -1296,6 +1403,26 @@ hipError_t enqueue_prefill_chunk(qr_decoder* d, int T, const int32_t* st, int pe
       return e;
     if ((e = matmul_rows_dev(d, L.wo, L.wo_type, d->pao, d->pxb2, dim, d->qd, T, s))) return e;
     if ((e = rmsnorm_launch(d->px, d->pxb2, L.rms_ffn, dim, d->pxb, s, T))) return e;
+    if (is_dense(L)) {
+      const qr_moe_layer& M = L.moe;
+      const size_t th = (size_t)T * M.hidden;
+      float* u = reinterpret_cast<float*>(d->pmoe);
+      float* g = u + th;
+      float* y = g + th;
+      d->prec_src = nullptr;  // pxb has new rows
+      if ((e = matmul_rows_dev(d, M.up, M.up_type, d->pxb, u, M.hidden, dim, T, s))) return e;
+      if ((e = matmul_rows_dev(d, M.gate, M.gate_type, d->pxb, g, M.hidden, dim, T, s, true)))
+        return e;
+      hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, u, g,
+                         (long)th);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+      d->prec_src = nullptr;
+      if ((e = matmul_rows_dev(d, M.down, M.down_type, g, y, dim, M.hidden, T, s))) return e;
+      const long n4 = (long)T * dim / 4;
+      hipLaunchKernelGGL(k_add4, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, d->px, y, n4);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+      continue;
+    }
     MoeScratch ms;
     moe_scratch_carve(d->pmoe, &L.moe, T, &ms);
     if ((e = moe_forward_launch(&L.moe, d->px, d->pxb, T, d->order, ms, s))) return e;
@@ -1327,7 +1454,22 @@ int check_layer_weights(const qr_model* m, int l, int order) {
   if ((rc = gemv_check(L.wk_type, order, L.wk, kvd, m->dim, "qr_decoder_create: wk"))) return rc;
   if ((rc = gemv_check(L.wv_type, order, L.wv, kvd, m->dim, "qr_decoder_create: wv"))) return rc;
   if ((rc = gemv_check(L.wo_type, order, L.wo, m->dim, qd, "qr_decoder_create: wo"))) return rc;
-  if ((rc = moe_check(&L.moe, "qr_decoder_create: moe"))) return rc;
+  if (is_dense(L)) {
+    const qr_moe_layer& M = L.moe;
+    if (!M.up || !M.gate || !M.down || M.hidden <= 0 || M.hidden % 4)
+      return set_error(QR_ERR_INVALID, "qr_decoder_create: layer %d dense FFN (hidden %d)", l,
+                       M.hidden);
+    if ((rc = gemv_check(M.up_type, order, M.up, M.hidden, m->dim, "qr_decoder_create: ffn_up")))
+      return rc;
+    if ((rc = gemv_check(M.gate_type, order, M.gate, M.hidden, m->dim,
+                         "qr_decoder_create: ffn_gate")))
+      return rc;
+    if ((rc = gemv_check(M.down_type, order, M.down, m->dim, M.hidden,
+                         "qr_decoder_create: ffn_down")))
+      return rc;
+  } else if ((rc = moe_check(&L.moe, "qr_decoder_create: moe"))) {
+    return rc;
+  }
   if (L.moe.dim != m->dim)
     return set_error(QR_ERR_INVALID, "qr_decoder_create: layer %d moe.dim %d != dim %d", l,
                      L.moe.dim, m->dim);
@@ -1349,6 +1491,7 @@ extern "C" {
 size_t qr_kv_row_bytes(int kv_type, int kv_dim) {
   if (kv_dim <= 0) return 0;
   if (kv_type == QR_KV_Q8_0) return kv_dim % 32 ? 0 : (size_t)(kv_dim / 32) * QR_Q8_BYTES;
+  if (kv_type == QR_KV_F16) return kv_dim % 32 ? 0 : (size_t)kv_dim * 2;
   if (kv_type == QR_KV_F32) return (size_t)kv_dim * 4;
   return 0;
 }
@@ -1418,6 +1561,7 @@ int qr_attention(qr_ctx* c, const float* q, const void* kc, const void* vc, cons
   DEC_HIP(lds_opt_in((const void*)k_attn_scores<false>, g_sc_opt), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_Q8_0>, g_sm_opt), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_F32>, g_sm_opt2), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_F16>, g_sm_opt3), "lds opt-in");
   KvView K;
   K.base = static_cast<const uint8_t*>(kc);
   K.ptab = ptab;
@@ -1492,8 +1636,10 @@ int qr_decoder_create(qr_ctx* c, const qr_model* m, int kv_type, int order, int 
   DEC_HIP(lds_opt_in((const void*)k_attn_scores<true>, g_sc_opt_r), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_Q8_0>, g_sm_opt), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_F32>, g_sm_opt2), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_sv<QR_KV_F16>, g_sm_opt3), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv_rows<QR_KV_Q8_0>, g_rows_opt), "lds opt-in");
   DEC_HIP(lds_opt_in((const void*)k_attn_sv_rows<QR_KV_F32>, g_rows_opt2), "lds opt-in");
+  DEC_HIP(lds_opt_in((const void*)k_attn_sv_rows<QR_KV_F16>, g_rows_opt3), "lds opt-in");
   qr_decoder* d = new (std::nothrow) qr_decoder();
   if (!d) return set_error(QR_ERR_NOMEM, "qr_decoder_create: host allocation");
   d->ctx = c;
@@ -1528,7 +1674,8 @@ int qr_decoder_create(qr_ctx* c, const qr_model* m, int kv_type, int order, int 
   // one allocation: activations, state, page table, RoPE table, MoE scratch
   size_t moe_bytes = 0;
   for (int l = 0; l < d->nl; l++) {
-    const size_t b = moe_scratch_bytes(&d->layers[l].moe, 1);
+    const qr_layer& L = d->layers[l];
+    const size_t b = is_dense(L) ? dense_scratch_bytes(L.moe, 1) : moe_scratch_bytes(&L.moe, 1);
     if (b > moe_bytes) moe_bytes = b;
   }
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
@@ -1677,10 +1824,16 @@ static int prefill_workspace(qr_decoder* d, int chunk) {
   const size_t T = (size_t)chunk;
   size_t moe_bytes = 0;
   for (int l = 0; l < d->nl; l++) {
-    const size_t b = moe_scratch_bytes(&d->layers[l].moe, chunk);
+    const qr_layer& L = d->layers[l];
+    const size_t b =
+        is_dense(L) ? dense_scratch_bytes(L.moe, chunk) : moe_scratch_bytes(&L.moe, chunk);
     if (b > moe_bytes) moe_bytes = b;
   }
-  const int wide = d->qd > d->dim ? d->qd : d->dim;
+  // the widest input a row product quantizes: q (wo's input), x, or a dense
+  // FFN's hidden rows (w2's input)
+  int wide = d->qd > d->dim ? d->qd : d->dim;
+  for (int l = 0; l < d->nl; l++)
+    if (is_dense(d->layers[l]) && d->layers[l].moe.hidden > wide) wide = d->layers[l].moe.hidden;
   const size_t o_x = 0, o_xb = o_x + up(T * d->dim * 4), o_xb2 = o_xb + up(T * d->dim * 4);
   const size_t o_q = o_xb2 + up(T * d->dim * 4), o_k = o_q + up(T * d->qd * 4);
   const size_t o_v = o_k + up(T * d->kvd * 4), o_ao = o_v + up(T * d->kvd * 4);

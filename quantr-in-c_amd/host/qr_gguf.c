@@ -385,8 +385,11 @@ int qr_gguf_model_host(const qr_gguf* g, int seq_len, qr_model* m, qr_layer* lay
 #undef U32
     snprintf(key, sizeof(key), "%s.rope.freq_base", arch);
     m->rope_base = qr_gguf_get_f32(g, key, 1000000.0f);
-    if (dim <= 0 || L <= 0 || H <= 0 || KVH <= 0 || hd <= 0 || E <= 0 || K <= 0 || hid <= 0)
-        return gg_fail(QR_ERR_UNSUPPORTED, "not a MoE GGUF this decoder serves");
+    /* expert_count 0 (or absent) is a dense model (src/runtime.c:270-284) */
+    if (E < 0 || (E > 0 && K <= 0)) return gg_fail(QR_ERR_UNSUPPORTED, "expert counts");
+    if (E == 0) K = 0;
+    if (dim <= 0 || L <= 0 || H <= 0 || KVH <= 0 || hd <= 0 || hid <= 0)
+        return gg_fail(QR_ERR_UNSUPPORTED, "not a model this decoder serves");
     /* sizes the later products (rows x row bytes x experts, in int and size_t)
      * stay far from overflow with; every real model is well inside them */
     if (dim > QR_GGUF_MAX_WIDTH || hid > QR_GGUF_MAX_WIDTH ||
@@ -460,13 +463,33 @@ int qr_gguf_model_host(const qr_gguf* g, int seq_len, qr_model* m, qr_layer* lay
             *wp[j] = g->t[it].data;
             *tp[j] = g->t[it].type;
         }
-        snprintf(name, sizeof(name), "blk.%d.ffn_gate_inp.weight", l);
-        it = qr_gguf_find(g, name);
-        if (!check_tensor(g, it, (uint64_t)dim, (uint64_t)E, 1, 1, &b)) return gg_fail(QR_ERR_INVALID, name);
         y->moe.dim = dim;
         y->moe.hidden = hid;
         y->moe.n_experts = E;
         y->moe.n_used = K;
+        if (E == 0) {
+            /* the dense FFN: w1 = ffn_up (the SiLU slot), w2 = ffn_down,
+             * w3 = ffn_gate (src/model.c:434-446), in the expert fields */
+            const char* kinds[3] = {"ffn_up", "ffn_down", "ffn_gate"};
+            const void** fp[3];
+            uint32_t* ft[3];
+            fp[0] = &y->moe.up; fp[1] = &y->moe.down; fp[2] = &y->moe.gate;
+            ft[0] = &y->moe.up_type; ft[1] = &y->moe.down_type; ft[2] = &y->moe.gate_type;
+            for (j = 0; j < 3; j++) {
+                const int down = j == 1;
+                snprintf(name, sizeof(name), "blk.%d.%s.weight", l, kinds[j]);
+                it = qr_gguf_find(g, name);
+                if (!check_tensor(g, it, (uint64_t)(down ? hid : dim), (uint64_t)(down ? dim : hid),
+                                  1, 0, &b))
+                    return gg_fail(QR_ERR_INVALID, name);
+                *fp[j] = g->t[it].data;
+                *ft[j] = g->t[it].type;
+            }
+            continue;
+        }
+        snprintf(name, sizeof(name), "blk.%d.ffn_gate_inp.weight", l);
+        it = qr_gguf_find(g, name);
+        if (!check_tensor(g, it, (uint64_t)dim, (uint64_t)E, 1, 1, &b)) return gg_fail(QR_ERR_INVALID, name);
         y->moe.router = (const float*)g->t[it].data;
         {
             /* expert_w1 = ffn_up_exps (the SiLU slot), expert_w3 = ffn_gate_exps,
@@ -664,6 +687,15 @@ static int plan_model(const qr_gguf* g, qr_gguf_model* gm, copy_plan* p) {
         plan_tile(p, &y->wv_type, kvd, m->dim);
         ADD(y->wo, qr_row_bytes(y->wo_type, qd) * (size_t)m->dim, &y->wo);
         plan_tile(p, &y->wo_type, m->dim, qd);
+        if (e->n_experts == 0) { /* a dense FFN: three matrices, tiled where they can be */
+            ADD(e->up, su, &e->up);
+            plan_tile(p, &e->up_type, e->hidden, m->dim);
+            ADD(e->gate, qr_row_bytes(e->gate_type, m->dim) * (size_t)e->hidden, &e->gate);
+            plan_tile(p, &e->gate_type, e->hidden, m->dim);
+            ADD(e->down, sd, &e->down);
+            plan_tile(p, &e->down_type, m->dim, e->hidden);
+            continue;
+        }
         ADD(e->router, (size_t)e->n_experts * (size_t)m->dim * 4, &e->router);
         if (e->n_experts > 1 && qr_gguf_expert_host(g, l, 1, &u1, &d1, &g1) != QR_OK)
             return QR_ERR_INVALID;

@@ -59,7 +59,7 @@ class Model(C.Structure):
     ]
 
 
-KV_F32, KV_Q8_0 = 0, 2
+KV_F32, KV_F16, KV_Q8_0 = 0, 1, 2
 MOE_PATH_AUTO, MOE_PATH_GEMV, MOE_PATH_MFMA = 0, 1, 2
 DEC_GRAPH = 1
 PREFILL_ALL_LOGITS = 1
@@ -554,11 +554,15 @@ def upload_decode_model(dev, m):
     wtype = (wq, wk, wv, wo), up_type (also gate), down_type) and the tensors
     (tok_embd, rms_final, wcls, and per layer rms_att, rms_ffn, wq, wk, wv,
     wo, router, up, gate, down).  A tensor is a numpy array (uploaded here) or
-    an int device address (used as is).  Returns (model, layers, keep); keep
+    an int device address (used as is).  E = 0 describes a dense model: up,
+    gate and down are then each layer's ffn_up (w1), ffn_gate (w3) and
+    ffn_down (w2), and router is empty.  Returns (model, layers, keep); keep
     holds the device buffers and must outlive the decoder."""
     keep = []
 
     def dptr(a):
+        if a is None or (isinstance(a, np.ndarray) and a.size == 0):
+            return 0  # e.g. the router of a dense layer (n_experts 0)
         if isinstance(a, (int, np.integer)):
             return int(a)
         if isinstance(a, DevBuf):

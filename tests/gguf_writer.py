@@ -57,10 +57,11 @@ def gguf_bytes(kvs, tensors, alignment=32, version=3, put_alignment_kv=False):
 
 def decode_model_gguf(m, arch="qwen3moe", alignment=32, split_experts=False, tokens=True,
                       head_dim_key=False, mutate=None):
-    """A MoE decode model dict (tests/golden/inputs.py decode_model /
+    """A decode model dict (tests/golden/inputs.py decode_model /
     qwen3_small_model) as GGUF tensors with the names load_gguf_transformer
     reads (src/model.c:253-449).  expert_w1 (the SiLU slot) is
-    ffn_up_exps, expert_w3 ffn_gate_exps, expert_w2 ffn_down_exps.  mutate
+    ffn_up_exps, expert_w3 ffn_gate_exps, expert_w2 ffn_down_exps; a dense
+    model (E = 0) has ffn_up (w1), ffn_gate (w3) and ffn_down (w2).  mutate
     (optional) edits the (name, type, ne, bytes) list before it is written."""
     dim, L, E, hid, V = m["dim"], m["n_layers"], m["E"], m["hidden"], m["vocab"]
     H, KVH, hd = m["n_heads"], m["n_kv_heads"], m["head_dim"]
@@ -68,11 +69,14 @@ def decode_model_gguf(m, arch="qwen3moe", alignment=32, split_experts=False, tok
            ("%s.embedding_length" % arch, U32, dim),
            ("%s.block_count" % arch, U32, L),
            ("%s.attention.head_count" % arch, U32, H),
-           ("%s.attention.head_count_kv" % arch, U32, KVH),
-           ("%s.expert_count" % arch, U32, E),
-           ("%s.expert_used_count" % arch, U32, m["K"]),
-           ("%s.expert_feed_forward_length" % arch, U32, hid),
-           ("%s.rope.freq_base" % arch, F32, float(m["rope_base"]))]
+           ("%s.attention.head_count_kv" % arch, U32, KVH)]
+    if E > 0:
+        kvs += [("%s.expert_count" % arch, U32, E),
+                ("%s.expert_used_count" % arch, U32, m["K"]),
+                ("%s.expert_feed_forward_length" % arch, U32, hid)]
+    else:  # a dense model: no expert keys, feed_forward_length (src/model.c:283-296)
+        kvs.append(("%s.feed_forward_length" % arch, U32, hid))
+    kvs.append(("%s.rope.freq_base" % arch, F32, float(m["rope_base"])))
     if head_dim_key:
         kvs.append(("%s.attention.key_length" % arch, U32, hd))
     if tokens:
@@ -89,10 +93,15 @@ def decode_model_gguf(m, arch="qwen3moe", alignment=32, split_experts=False, tok
               (p + "attn_q.weight", wt[0], [dim, H * hd], b(lw["wq"])),
               (p + "attn_k.weight", wt[1], [dim, KVH * hd], b(lw["wk"])),
               (p + "attn_v.weight", wt[2], [dim, KVH * hd], b(lw["wv"])),
-              (p + "attn_output.weight", wt[3], [H * hd, dim], b(lw["wo"])),
-              (p + "ffn_gate_inp.weight", 0, [dim, E], b(lw["router"]))]
+              (p + "attn_output.weight", wt[3], [H * hd, dim], b(lw["wo"]))]
         ut, dt = m["up_type"], m["down_type"]
         up, gate, down = b(lw["up"]), b(lw["gate"]), b(lw["down"])
+        if E == 0:  # the dense FFN's tensors (src/model.c:434-446)
+            t += [(p + "ffn_up.weight", ut, [dim, hid], up),
+                  (p + "ffn_down.weight", dt, [hid, dim], down),
+                  (p + "ffn_gate.weight", ut, [dim, hid], gate)]
+            continue
+        t.append((p + "ffn_gate_inp.weight", 0, [dim, E], b(lw["router"])))
         if split_experts:
             su, sd = len(up) // E, len(down) // E
             for e in range(E):

@@ -143,7 +143,9 @@ def gen_moe(rc, ra, r5):
 
 def gen_decode(rc, ra, r5):
     """forward_runtime of the small decode models, token by token from
-    position 0, in each build (fp32 KV cache: the reference's working type)."""
+    position 0, in each build, with the fp32 KV cache (kv_cache_type 0) and
+    with the fp16 one (kv_cache_type 1, malloc_run_state_kv: keys logits16_*,
+    x16_*)."""
     out = {}
     for name in I.DECODE_CASES:
         m = I.decode_model(name)
@@ -155,6 +157,9 @@ def gen_decode(rc, ra, r5):
             lg, xs = lib.forward(m, m["tokens"], backend, threads=2)
             out["logits_%s_%s" % (name, tag)] = lg
             out["x_%s_%s" % (name, tag)] = xs
+            lg, xs = lib.forward(m, m["tokens"], backend, threads=2, kv_type=1)
+            out["logits16_%s_%s" % (name, tag)] = lg
+            out["x16_%s_%s" % (name, tag)] = xs
     save("decode.npz", **out)
 
 

@@ -152,7 +152,16 @@ DECODE_CASES = {
           TYPE_Q6_K, [3, 17, 101, 42, 250, 7, 7, 199]),
     "b": (512, 8, 2, 2, 16, 4, 256, 200, (TYPE_Q6_K, TYPE_F32, TYPE_Q8_0, TYPE_Q5_K), TYPE_Q6_K,
           TYPE_Q8_0, [0, 199, 55, 55, 120]),
+    # dense models (no experts: the FFN of src/runtime.c:270-284), "c" with
+    # Q8_0 FFN weights as TinyLlama's GGUF stores them
+    "c": (256, 4, 2, 2, 0, 0, 512, 300, (TYPE_Q8_0, TYPE_Q6_K, TYPE_Q5_K, TYPE_Q8_0), TYPE_Q6_K,
+          TYPE_Q8_0, [5, 299, 17, 17, 120, 3]),
+    "d": (512, 8, 4, 2, 0, 0, 768, 256, (TYPE_Q5_K, TYPE_F32, TYPE_Q8_0, TYPE_Q6_K), TYPE_Q8_0,
+          TYPE_Q6_K, [1, 2, 255, 128, 64]),
 }
+# FFN weight types (up and gate, down) where they differ from the MoE cases'
+# Q5_K / Q6_K
+DECODE_FFN_TYPES = {"c": (TYPE_Q8_0, TYPE_Q8_0)}
 
 
 def _rows(seed, qtype, rows, cols):
@@ -167,10 +176,12 @@ def decode_model(name):
     dim, H, KVH, L, E, K, hidden, vocab, wt, tt, ct, tokens = DECODE_CASES[name]
     hd = dim // H
     seed = 9000 + 100 * (ord(name) - ord("a"))
+    ut, dt = DECODE_FFN_TYPES.get(name, (TYPE_Q5_K, TYPE_Q6_K))
     m = dict(dim=dim, n_heads=H, n_kv_heads=KVH, head_dim=hd, n_layers=L, E=E, K=K,
              hidden=hidden, vocab=vocab, seq_len=max(16, len(tokens)), rope_base=1e6,
              wtype=list(wt), tok_type=tt, wcls_type=ct, tokens=list(tokens),
-             up_type=TYPE_Q5_K, down_type=TYPE_Q6_K)
+             up_type=ut, down_type=dt)
+    ne = max(E, 1)  # a dense model (E = 0) has one up / gate / down per layer
     m["tok_embd"] = _rows(seed, tt, vocab, dim)
     m["wcls"] = _rows(seed + 1, ct, vocab, dim)
     m["rms_final"] = (1.0 + activations(seed + 2, 1, dim, std=0.1)[0]).astype(np.float32)
@@ -183,9 +194,9 @@ def decode_model(name):
             wq=_rows(s + 2, wt[0], H * hd, dim), wk=_rows(s + 3, wt[1], KVH * hd, dim),
             wv=_rows(s + 4, wt[2], KVH * hd, dim), wo=_rows(s + 5, wt[3], dim, H * hd),
             router=activations(s + 6, E, dim, std=0.05),
-            up=blocks(s + 7, TYPE_Q5_K, E * hidden * (dim // 256)),
-            gate=blocks(s + 8, TYPE_Q5_K, E * hidden * (dim // 256)),
-            down=blocks(s + 9, TYPE_Q6_K, E * dim * (hidden // 256)))
+            up=blocks(s + 7, ut, ne * hidden * (dim // BLOCK[ut][0])),
+            gate=blocks(s + 8, ut, ne * hidden * (dim // BLOCK[ut][0])),
+            down=blocks(s + 9, dt, ne * dim * (hidden // BLOCK[dt][0])))
         layers.append(lay)
     m["layers"] = layers
     return m
@@ -255,5 +266,35 @@ def qwen3_full_model(seed=9800, n_layers=2, seq_len=4352):
             up=blocks(s + 7, TYPE_Q4_K, E * hidden * (dim // 256)),
             gate=blocks(s + 8, TYPE_Q4_K, E * hidden * (dim // 256)),
             down=blocks(s + 9, TYPE_Q6_K, E * dim * (hidden // 256))))
+    m["layers"] = layers
+    return m
+
+
+def tinyllama_model(seed=9900, n_layers=2, seq_len=256, ffn_type=TYPE_Q8_0):
+    """TinyLlama-1.1B's layer shapes (dense: no experts): dim 2048, 32 heads
+    of 64 over 4 kv heads, FFN 5632, vocab 32000, every matrix Q8_0 (as its
+    Q8_0 GGUF stores them; ffn_type sets the FFN's type).  head_dim is
+    dim / n_heads, so the reference itself can run it."""
+    dim, H, KVH, hidden, vocab = 2048, 32, 4, 5632, 32000
+    hd = dim // H
+    wt = (TYPE_Q8_0, TYPE_Q8_0, TYPE_Q8_0, TYPE_Q8_0)
+    m = dict(dim=dim, n_heads=H, n_kv_heads=KVH, head_dim=hd, n_layers=n_layers, E=0, K=0,
+             hidden=hidden, vocab=vocab, seq_len=seq_len, rope_base=10000.0, wtype=list(wt),
+             tok_type=TYPE_Q8_0, wcls_type=TYPE_Q8_0, up_type=ffn_type, down_type=ffn_type)
+    m["tok_embd"] = _rows(seed, TYPE_Q8_0, vocab, dim)
+    m["wcls"] = _rows(seed + 1, TYPE_Q8_0, vocab, dim)
+    m["rms_final"] = (1.0 + activations(seed + 2, 1, dim, std=0.1)[0]).astype(np.float32)
+    layers = []
+    for l in range(n_layers):
+        s = seed + 10 + 20 * l
+        layers.append(dict(
+            rms_att=(1.0 + activations(s, 1, dim, std=0.1)[0]).astype(np.float32),
+            rms_ffn=(1.0 + activations(s + 1, 1, dim, std=0.1)[0]).astype(np.float32),
+            wq=_rows(s + 2, wt[0], H * hd, dim), wk=_rows(s + 3, wt[1], KVH * hd, dim),
+            wv=_rows(s + 4, wt[2], KVH * hd, dim), wo=_rows(s + 5, wt[3], dim, H * hd),
+            router=np.zeros((0, dim), np.float32),
+            up=_rows(s + 7, ffn_type, hidden, dim).reshape(-1),
+            gate=_rows(s + 8, ffn_type, hidden, dim).reshape(-1),
+            down=_rows(s + 9, ffn_type, dim, hidden).reshape(-1)))
     m["layers"] = layers
     return m

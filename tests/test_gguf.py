@@ -43,6 +43,8 @@ def _ours(data):
 def _files():
     a = I.decode_model("a")
     b = I.decode_model("b")
+    c = I.decode_model("c")
+    dd = I.decode_model("d")
     q3 = I.qwen3_small_model(n_layers=1, seq_len=64)
     at = dict(a)
     at["wcls"], at["wcls_type"] = a["tok_embd"], a["tok_type"]
@@ -53,6 +55,8 @@ def _files():
         "b_no_tokens": G.decode_model_gguf(b, tokens=False)[0],
         "q3_split_align64": G.decode_model_gguf(q3, split_experts=True, alignment=64,
                                                 head_dim_key=True)[0],
+        "c_dense": G.decode_model_gguf(c)[0],
+        "d_dense_align64": G.decode_model_gguf(dd, alignment=64)[0],
     }
 
 
@@ -140,7 +144,8 @@ def test_values_match_reference(ref):
     g.close()
 
 
-@pytest.mark.parametrize("name", ["a", "a_tied", "b_no_tokens", "q3_split_align64"])
+@pytest.mark.parametrize("name", ["a", "a_tied", "b_no_tokens", "q3_split_align64", "c_dense",
+                                  "d_dense_align64"])
 def test_model_mapping_matches_reference(ref, tmp_path, name):
     """load_transformer's configuration and every weight pointer (as a file
     offset) against qr_gguf_model_host / qr_gguf_expert_host."""
@@ -169,6 +174,9 @@ def test_model_mapping_matches_reference(ref, tmp_path, name):
         want_t += [y.wq_type, y.wk_type, y.wv_type, y.wo_type, y.moe.up_type, y.moe.down_type,
                    y.moe.gate_type]
     for l in range(L):
+        if E == 0:  # a dense layer: w1, w2, w3 in the expert fields
+            y = layers[l].moe
+            want += [y.up - b, y.down - b, y.gate - b]
         for e in range(E):
             up, down, gate = g.expert_host(l, e)
             want += [up - b, down - b, gate - b]

@@ -40,53 +40,60 @@ def run_tokens(dev, d, m, tokens, pos0=0):
     return lg, xs
 
 
+@pytest.mark.parametrize("kv", ["f32", "f16"])
 @pytest.mark.parametrize("graph", [0, Q.DEC_GRAPH], ids=["eager", "graph"])
 @pytest.mark.parametrize("build", list(BUILDS))
 @pytest.mark.parametrize("name", list(I.DECODE_CASES))
-def test_decoder_matches_reference_logits(dev, golden, name, build, graph):
+def test_decoder_matches_reference_logits(dev, golden, name, build, graph, kv):
+    """The reference's own logits and residuals, with its fp32 KV cache and
+    with its fp16 one (kv_cache_type 1, src/runtime.c:74-92)."""
     g = golden("decode.npz")
     m = I.decode_model(name)
     assert I.decode_digest(m) == str(g["sha_" + name])
-    key = "logits_%s_%s" % (name, build)
+    tag = "" if kv == "f32" else "16"
+    key = "logits%s_%s_%s" % (tag, name, build)
     if key not in g:
         pytest.skip("fixture written without an -mavx512f build")
-    print("decode case %s build %s graph %d" % (name, build, graph), flush=True)
-    d = make_decoder(dev, m, Q.KV_F32, BUILDS[build], flags=graph)
+    print("decode case %s build %s graph %d kv %s" % (name, build, graph, kv), flush=True)
+    d = make_decoder(dev, m, Q.KV_F16 if kv == "f16" else Q.KV_F32, BUILDS[build], flags=graph)
     lg, xs = run_tokens(dev, d, m, m["tokens"])
     d.close()
-    assert_bits_equal(xs, g["x_%s_%s" % (name, build)], "residual %s/%s" % (name, build))
+    assert_bits_equal(xs, g["x%s_%s_%s" % (tag, name, build)], "residual %s/%s" % (name, build))
     assert_bits_equal(lg, g[key], "logits %s/%s" % (name, build))
 
 
-def prefilled(oracle, m, npre, seed):
+def prefilled(oracle, m, npre, seed, kv_type=Q.KV_Q8_0):
     """Seeded N(0, 1) K / V values for positions 0 .. npre-1 of every layer
     and the oracle's contiguous cache holding them."""
     L, kvd = m["n_layers"], m["n_kv_heads"] * m["head_dim"]
     rng = np.random.default_rng(seed)
     kv = rng.standard_normal((L, 2, npre, kvd)).astype(np.float32)
-    rs = oracle.kv_row_bytes(Q.KV_Q8_0, kvd)
+    rs = oracle.kv_row_bytes(kv_type, kvd)
     kc = np.zeros((L, m["seq_len"], rs), np.uint8)
     vc = np.zeros_like(kc)
     for l in range(L):
-        kc[l, :npre] = oracle.kv_rows(kv[l, 0], Q.KV_Q8_0)
-        vc[l, :npre] = oracle.kv_rows(kv[l, 1], Q.KV_Q8_0)
+        kc[l, :npre] = oracle.kv_rows(kv[l, 0], kv_type)
+        vc[l, :npre] = oracle.kv_rows(kv[l, 1], kv_type)
     return kv, kc, vc
 
 
 @pytest.mark.parametrize("graph", [0, Q.DEC_GRAPH], ids=["eager", "graph"])
-@pytest.mark.parametrize("order,kvh", [(ORDER_SEQ, 2), (ORDER_AVX2, 2), (ORDER_AVX2, 1)],
-                         ids=["seq_gqa4", "avx2_gqa4", "avx2_gqa8"])
-def test_decoder_q8_cache_head128(dev, oracle, order, kvh, graph):
+@pytest.mark.parametrize("order,kvh,kv_type", [(ORDER_SEQ, 2, Q.KV_Q8_0), (ORDER_AVX2, 2, Q.KV_Q8_0),
+                                               (ORDER_AVX2, 1, Q.KV_Q8_0),
+                                               (ORDER_AVX2, 1, Q.KV_F16)],
+                         ids=["seq_gqa4", "avx2_gqa4", "avx2_gqa8", "avx2_gqa8_f16"])
+def test_decoder_q8_cache_head128(dev, oracle, order, kvh, kv_type, graph):
     """Qwen3-like heads (head_dim 128, q_dim 1024 != dim 512, 8 heads over 2
-    kv heads, or over 1: GQA 8:1, the Qwen3-30B-A3B ratio) over a Q8_0 cache
-    prefilled to 517 positions through a permuted page table (pages of 64),
-    then three decode steps at 517..519: logits, residual and the cache rows
-    the steps wrote, bit-exact with the oracle."""
+    kv heads, or over 1: GQA 8:1, the Qwen3-30B-A3B ratio) over a Q8_0 (or
+    fp16) cache prefilled to 517 positions through a permuted page table
+    (pages of 64), then three decode steps at 517..519: logits, residual and
+    the cache rows the steps wrote, bit-exact with the oracle."""
     m = I.qwen3_small_model(n_layers=2, seq_len=640, n_kv_heads=kvh)
     npre = 517
-    kv, kc, vc = prefilled(oracle, m, npre, seed=41)
-    print("decode head128 order %d kv heads %d graph %d" % (order, kvh, graph), flush=True)
-    d = make_decoder(dev, m, Q.KV_Q8_0, order, page=64, flags=graph)
+    kv, kc, vc = prefilled(oracle, m, npre, seed=41, kv_type=kv_type)
+    print("decode head128 order %d kv heads %d kv %d graph %d" % (order, kvh, kv_type, graph),
+          flush=True)
+    d = make_decoder(dev, m, kv_type, order, page=64, flags=graph)
     ppl, page = d.pages()
     assert (ppl, page) == (10, 64)
     rng = np.random.default_rng(5)
@@ -102,8 +109,7 @@ def test_decoder_q8_cache_head128(dev, oracle, order, kvh, graph):
         assert np.array_equal(dev.download(vr, rs, np.uint8), vc[l, t])
     toks = [11, 319, 200]
     lg, xs = run_tokens(dev, d, m, toks, pos0=npre)
-    wl, wx = oracle.forward_cached(m, kc.reshape(-1), vc.reshape(-1), toks, npre, order,
-                                   Q.KV_Q8_0)
+    wl, wx = oracle.forward_cached(m, kc.reshape(-1), vc.reshape(-1), toks, npre, order, kv_type)
     for l in range(m["n_layers"]):
         for t in range(npre, npre + len(toks)):
             kr, vr = d.kv_rows(l, t)
@@ -189,7 +195,7 @@ def test_rmsnorm(dev, oracle, n):
     assert_bits_equal(dev.download(od, n, np.float32), oracle.rmsnorm(xs, w), "rmsnorm(x + a)")
 
 
-@pytest.mark.parametrize("kv_type", [Q.KV_F32, Q.KV_Q8_0])
+@pytest.mark.parametrize("kv_type", [Q.KV_F32, Q.KV_F16, Q.KV_Q8_0])
 @pytest.mark.parametrize("npos,H,KVH,hd", [(1, 4, 4, 64), (130, 8, 2, 128), (4097, 32, 4, 128),
                                            (300, 4, 1, 512)])
 def test_attention(dev, oracle, kv_type, npos, H, KVH, hd):

@@ -51,21 +51,23 @@ def prefill(dev, d, m, tokens, pos0=0, chunk=0):
             dev.download(x_d, m["dim"], np.float32))
 
 
+@pytest.mark.parametrize("kv", ["f32", "f16"])
 @pytest.mark.parametrize("chunk", [0, 3, 1])
 @pytest.mark.parametrize("build", list(BUILDS))
 @pytest.mark.parametrize("name", list(I.DECODE_CASES))
-def test_prefill_matches_reference_logits(dev, golden, name, build, chunk):
+def test_prefill_matches_reference_logits(dev, golden, name, build, chunk, kv):
     g = golden("decode.npz")
     m = I.decode_model(name)
-    key = "logits_%s_%s" % (name, build)
+    tag = "" if kv == "f32" else "16"
+    key = "logits%s_%s_%s" % (tag, name, build)
     if key not in g:
         pytest.skip("fixture written without an -mavx512f build")
-    print("prefill case %s build %s chunk %d" % (name, build, chunk), flush=True)
-    d = make_decoder(dev, m, Q.KV_F32, BUILDS[build])
+    print("prefill case %s build %s chunk %d kv %s" % (name, build, chunk, kv), flush=True)
+    d = make_decoder(dev, m, Q.KV_F16 if kv == "f16" else Q.KV_F32, BUILDS[build])
     lg, x = prefill(dev, d, m, m["tokens"], chunk=chunk)
     d.close()
     assert_bits_equal(lg, g[key], "prefill logits %s/%s" % (name, build))
-    assert_bits_equal(x, g["x_%s_%s" % (name, build)][-1], "prefill residual")
+    assert_bits_equal(x, g["x%s_%s_%s" % (tag, name, build)][-1], "prefill residual")
 
 
 @pytest.mark.parametrize("name", list(I.DECODE_CASES))
@@ -150,8 +152,8 @@ def test_prefill_head128_chunks(dev, oracle, source, page):
     assert np.array_equal(kv, want_kv)
 
 
-@pytest.mark.parametrize("kv_type,page", [(Q.KV_Q8_0, 64), (Q.KV_F32, 16)],
-                         ids=["q8_0_pages64", "f32_pages16"])
+@pytest.mark.parametrize("kv_type,page", [(Q.KV_Q8_0, 64), (Q.KV_F32, 16), (Q.KV_F16, 32)],
+                         ids=["q8_0_pages64", "f32_pages16", "f16_pages32"])
 def test_prefill_gqa8_chunks(dev, oracle, kv_type, page):
     """GQA 8:1 at head_dim 128, the shape whose prefill attention values run
     the query heads of a kv head in one workgroup (V staged once for the

@@ -9,7 +9,7 @@ import pytest
 
 import inputs as I
 from conftest import assert_bits_equal, bits
-from oracle import ORDER_AVX2, ORDER_AVX512, ORDER_SEQ
+from oracle import KV_F16, KV_F32, ORDER_AVX2, ORDER_AVX512, ORDER_SEQ
 
 TYPES = (I.TYPE_Q8_0, I.TYPE_Q4_K, I.TYPE_Q5_K, I.TYPE_Q6_K)
 
@@ -128,23 +128,28 @@ def test_moe_block(oracle, golden, name, build):
 
 @pytest.mark.parametrize("name", sorted(I.DECODE_CASES))
 @pytest.mark.parametrize("build", ["c99", "avx2", "avx512"])
-def test_decode_step(oracle, golden, name, build):
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_decode_step(oracle, golden, name, build, kv):
     """The oracle's decode step (oracle/qr_oracle_decode.c) against the
     reference's own forward_runtime (src/runtime.c:94-288) on a two-layer MoE
-    model, token by token from position 0 (fp32 KV cache, head_dim =
-    dim / n_heads): embedding dequantization, RMSNorm, Q/K/V, RoPE, the
-    attention over the growing cache, Wo and the residual, the MoE block, the
-    final norm and the lm_head -- logits and residual bit-exact."""
+    model, token by token from position 0 (head_dim = dim / n_heads), with
+    the fp32 KV cache and with the fp16 one (kv_cache_type 1: truncating
+    stores, fp16_to_fp32 reads, src/runtime.c:74-92): embedding
+    dequantization, RMSNorm, Q/K/V, RoPE, the attention over the growing
+    cache, Wo and the residual, the MoE block, the final norm and the lm_head
+    -- logits and residual bit-exact."""
     g = golden("decode.npz")
     m = I.decode_model(name)
     assert I.decode_digest(m) == str(g["sha_" + name])
-    key = "logits_%s_%s" % (name, build)
+    tag = "" if kv == "f32" else "16"
+    key = "logits%s_%s_%s" % (tag, name, build)
     if key not in g:
         pytest.skip("fixture written without an -mavx512f build")
     order = {"c99": ORDER_SEQ, "avx2": ORDER_AVX2, "avx512": ORDER_AVX512}[build]
-    lg, xs = oracle.forward_seq(m, m["tokens"], order)
-    assert_bits_equal(lg, g[key], "logits %s/%s" % (name, build))
-    assert_bits_equal(xs, g["x_%s_%s" % (name, build)], "residual %s/%s" % (name, build))
+    lg, xs = oracle.forward_seq(m, m["tokens"], order, KV_F16 if kv == "f16" else KV_F32)
+    assert_bits_equal(lg, g[key], "logits %s/%s/%s" % (name, build, kv))
+    assert_bits_equal(xs, g["x%s_%s_%s" % (tag, name, build)], "residual %s/%s/%s" % (
+        name, build, kv))
 
 
 def test_rope_table_matches_rope(oracle):
