@@ -653,6 +653,60 @@ def cpu_baseline_moe(M, cpus, reps=24, copies=4):
                 by_threads={str(k): v for k, v in by.items()})
 
 
+def cpu_baseline_decode(M, cpus, reps=10, copies=2):
+    """The reference's forward_runtime per token at the nearest Qwen3-30B-A3B
+    shape it runs: head_dim = dim / n_heads (64, where the model has 128), its
+    fp32 KV cache, the same MoE layer, at position 4096.  One decoder layer
+    per timed call (a one-layer model rotating over `copies` weight copies,
+    attention weights Q8_0: the reference's Q4_K dot returns values that turn
+    into NaN router logits a layer later), so a token costs 48 such calls plus
+    the Q6_K lm_head, timed alone."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+    sh = M["shape"]
+    dim, hidden, E, K = sh["dim"], sh["hidden"], sh["E"], sh["K"]
+    c = QWEN3_DEC
+    H, KVH, V, P, L = c["n_heads"], c["n_kv_heads"], c["vocab"], c["prefill"], len(M["layers"])
+    hd = dim // H
+    kvd = KVH * hd
+    router, up, gate, down = M["parts"][:4]
+    ref = O.RefLib("avx2")
+    cps = []
+    for i in range(copies):
+        cps.append(dict(wq=synth.weights(7100 + i, H * hd, dim, Q.TYPE_Q8_0),
+                        wk=synth.weights(7110 + i, kvd, dim, Q.TYPE_Q8_0),
+                        wv=synth.weights(7120 + i, kvd, dim, Q.TYPE_Q8_0),
+                        wo=synth.weights(7130 + i, dim, H * hd, Q.TYPE_Q8_0),
+                        router=router if i == 0 else router.copy(),
+                        up=up if i == 0 else up.copy(), gate=gate if i == 0 else gate.copy(),
+                        down=down if i == 0 else down.copy()))
+    tok = synth.zipf_tokens(9001, 16, dim, M["u"])
+    rms = np.ones(dim, np.float32)
+    head = np.tile(synth.weights(7140, 8192, dim, Q.TYPE_Q6_K), (V // 8192 + 1, 1))[:V].copy()
+    x = synth.normal(7141, (dim,))
+    by = {}
+    for th in thread_counts(cpus):
+        tl = ref.decode_layer_bench(dim, H, KVH, hidden, E, K, P, tok, cps,
+                                    (Q.TYPE_Q8_0,) * 4, Q.TYPE_Q4_K, Q.TYPE_Q6_K, rms,
+                                    O.BACKEND_AVX2, th, 2, reps)
+        th_head = ref.gemv_bench(x, [head], Q.TYPE_Q6_K, V, dim, th, 1, 3)
+        lay, hm = float(np.median(tl)), float(np.median(th_head))
+        tok_s = 1.0 / (L * lay + hm)
+        by[th] = dict(tokens_per_s=round(tok_s, 3), layer_ms=round(lay * 1e3, 3),
+                      lm_head_ms=round(hm * 1e3, 2))
+        log("bench: CPU decode step (reference forward_runtime, %d layers at position %d), "
+            "%d threads: %.2f tokens/s (%.2f ms per layer, lm_head %.1f ms)"
+            % (L, P, th, tok_s, lay * 1e3, hm * 1e3))
+    return dict(value=by[cpus]["tokens_per_s"], unit="tokens/s", cores=cpus, kind="reference",
+                sample="forward_runtime (oracle/_ref, CI flags, OpenMP) of one decoder layer per "
+                       "call at position %d over its fp32 KV cache (head_dim %d = dim / n_heads, "
+                       "the reference's rule; 32 query / 4 kv heads; Q8_0 attention weights; the "
+                       "MoE layer of the GPU leg), %d weight copies, 2 warm-ups then the median "
+                       "of %d calls, times %d layers, plus the Q6_K 151936 x 2048 lm_head "
+                       "(matmul_q_fused, median of 3)" % (P, hd, copies, reps, L),
+                by_threads={str(k): v for k, v in by.items()})
+
+
 # ---------------------------------------------------------------------------
 def load_traffic():
     p = os.path.join(REPO, "profiles", "k_gemv_tiled_q4k_32000x2048_traffic.json")
@@ -780,6 +834,8 @@ def main():
         cpu = cpu_baseline_gemv(cpus)
         if M is not None:
             moe["cpu_baseline"] = cpu_baseline_moe(M, cpus)
+            if dec is not None:
+                dec["cpu_baseline"] = cpu_baseline_decode(M, cpus)
 
     h1 = h[("tiled", 1)] if h else None
 

@@ -473,6 +473,10 @@ class RefLib:
                                        C.c_int, C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p,
                                        C.c_uint32, C.c_void_p, C.c_uint32, C.c_int, C.c_int,
                                        C.c_int, C.c_int, C.c_void_p]
+        L.refdrv_decode_layer_bench.restype = C.c_int
+        L.refdrv_decode_layer_bench.argtypes = [C.c_int] * 8 + [C.c_void_p, C.c_int] + \
+            [C.c_void_p] * 6 + [C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_uint32,
+                                C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p]
         L.refdrv_gemv_bench.restype = C.c_int
         L.refdrv_gemv_bench.argtypes = [_f32p, C.c_void_p, C.c_int, C.c_uint32, C.c_int, C.c_int,
                                         C.c_int, C.c_int, C.c_int, _f32p, C.c_void_p]
@@ -567,6 +571,26 @@ class RefLib:
                                        times.ctypes.data_as(C.c_void_p))
         if rc != 0:
             raise RuntimeError("refdrv_moe_bench failed: %d" % rc)
+        return times
+
+    def decode_layer_bench(self, dim, n_heads, n_kv_heads, hidden, E, K, pos, tok_embd, copies,
+                           wtype, up_type, down_type, rms, backend, threads, warmup, reps):
+        """Seconds of each timed one-layer forward_runtime call at position pos
+        (refdrv_decode_layer_bench); copies: dicts of wq, wk, wv, wo, router,
+        up, gate, down arrays."""
+        n = len(copies)
+        arr = lambda k: (C.c_void_p * n)(*[c[k].ctypes.data for c in copies])  # noqa: E731
+        tok = np.ascontiguousarray(tok_embd, np.float32)
+        wt = np.array(wtype, np.uint32)
+        rms = np.ascontiguousarray(rms, np.float32)
+        times = np.zeros(reps, np.float64)
+        rc = self.lib.refdrv_decode_layer_bench(
+            dim, n_heads, n_kv_heads, hidden, E, K, pos, n, tok.ctypes.data, tok.shape[0],
+            arr("wq"), arr("wk"), arr("wv"), arr("wo"), wt.ctypes.data, arr("router"), arr("up"),
+            up_type, arr("gate"), arr("down"), down_type, rms.ctypes.data, backend, threads,
+            warmup, reps, times.ctypes.data_as(C.c_void_p))
+        if rc != 0:
+            raise RuntimeError("refdrv_decode_layer_bench failed: %d" % rc)
         return times
 
     def gemv_bench(self, x, copies, qtype, n, d, threads, warmup, reps):

@@ -313,6 +313,147 @@ int refdrv_moe_bench(const float* x_in, int T, int dim, int hidden, int E, int K
     return 0;
 }
 
+/*
+ * Timing of one decoder layer of forward_runtime at position `pos`, for the
+ * CPU baseline of the decode step: a one-layer model (RMSNorm, Q/K/V, RoPE,
+ * the attention over pos + 1 cached positions, Wo, RMSNorm, the MoE block)
+ * whose weights rotate over `ncopies` copies (copy c: wq[c] .. wo[c] of types
+ * wtype[0..3], router[c], up[c] / gate[c] / down[c] as [E][rows][cols]); the
+ * fp32 KV cache rows 0 .. pos-1 hold seeded values in [-0.5, 0.5); wcls is
+ * NULL, so the lm_head costs nothing here (the caller times it alone).
+ * head_dim is dim / n_heads, as the reference fixes it.  Call i embeds token
+ * i % n_tok of tok_embd (fp32 rows) at position pos.  times[r] receives
+ * call r's CLOCK_MONOTONIC seconds after `warmup` untimed calls.
+ */
+int refdrv_decode_layer_bench(int dim, int n_heads, int n_kv_heads, int hidden, int E, int K,
+                              int pos, int ncopies, const float* tok_embd, int n_tok,
+                              const void* const* wq, const void* const* wk,
+                              const void* const* wv, const void* const* wo,
+                              const uint32_t* wtype, const float* const* router,
+                              const void* const* up, uint32_t up_type, const void* const* gate,
+                              const void* const* down, uint32_t down_type, const float* rms,
+                              int backend, int threads, int warmup, int reps, double* times) {
+    Transformer t;
+    RuntimeContext rt;
+    RuntimeOptions opt;
+    float **rmsp, **qp, **kp, **vp, **op, **rp;
+    float ***ew1, ***ew2, ***ew3;
+    uint32_t *tq, *tk, *tv, *to, *t_up, *t_down, *t_gate;
+    size_t s_up, s_down, kv_dim, i, r;
+    int l, e, c;
+    struct timespec a, b;
+    uint64_t h = 0x9E3779B97F4A7C15ull;
+
+    if (E < 1 || E > 256 || K > 16 || K > E || ncopies < 1 || n_tok < 1 || pos < 0) return -1;
+    memset(&t, 0, sizeof(t));
+    t.config.dim = dim;
+    t.config.hidden_dim = hidden;
+    t.config.n_layers = 1;
+    t.config.n_heads = n_heads;
+    t.config.n_kv_heads = n_kv_heads;
+    t.config.vocab_size = 1;
+    t.config.seq_len = pos + 1;
+    t.config.rope_freq_base = 1000000.0f;
+    t.config.expert_count = E;
+    t.config.expert_used_count = K;
+    rmsp = (float**)malloc((size_t)ncopies * 6 * sizeof(float*));
+    ew1 = (float***)malloc((size_t)ncopies * 3 * sizeof(float**));
+    tq = (uint32_t*)malloc((size_t)ncopies * 7 * sizeof(uint32_t));
+    if (!rmsp || !ew1 || !tq) return -2;
+    qp = rmsp + ncopies;
+    kp = qp + ncopies;
+    vp = kp + ncopies;
+    op = vp + ncopies;
+    rp = op + ncopies;
+    ew2 = ew1 + ncopies;
+    ew3 = ew2 + ncopies;
+    tk = tq + ncopies;
+    tv = tk + ncopies;
+    to = tv + ncopies;
+    t_up = to + ncopies;
+    t_down = t_up + ncopies;
+    t_gate = t_down + ncopies;
+    s_up = (up_type == 8 ? (size_t)(dim / 32) * 34 : up_type == 12 ? (size_t)(dim / 256) * 144
+            : up_type == 13 ? (size_t)(dim / 256) * 176 : (size_t)(dim / 256) * 210) * (size_t)hidden;
+    s_down = (down_type == 8 ? (size_t)(hidden / 32) * 34 : down_type == 12 ? (size_t)(hidden / 256) * 144
+              : down_type == 13 ? (size_t)(hidden / 256) * 176 : (size_t)(hidden / 256) * 210) * (size_t)dim;
+    for (c = 0; c < ncopies; c++) {
+        rmsp[c] = (float*)rms;
+        qp[c] = (float*)wq[c];
+        kp[c] = (float*)wk[c];
+        vp[c] = (float*)wv[c];
+        op[c] = (float*)wo[c];
+        rp[c] = (float*)router[c];
+        tq[c] = wtype[0];
+        tk[c] = wtype[1];
+        tv[c] = wtype[2];
+        to[c] = wtype[3];
+        t_up[c] = t_gate[c] = up_type;
+        t_down[c] = down_type;
+        ew1[c] = (float**)malloc((size_t)E * 3 * sizeof(float*));
+        if (!ew1[c]) return -2;
+        ew2[c] = ew1[c] + E;
+        ew3[c] = ew2[c] + E;
+        for (e = 0; e < E; e++) {
+            ew1[c][e] = (float*)((const char*)up[c] + (size_t)e * s_up);
+            ew3[c][e] = (float*)((const char*)gate[c] + (size_t)e * s_up);
+            ew2[c][e] = (float*)((const char*)down[c] + (size_t)e * s_down);
+        }
+    }
+    t.weights.token_embedding_table = (float*)tok_embd;
+    t.weights.token_embd_type = 0;
+    t.weights.token_embd_row_bytes = (size_t)dim * sizeof(float);
+    t.weights.rms_final_weight = (float*)rms;
+    t.weights.wcls = NULL;
+    malloc_run_state(&t.state, &t.config);
+    /* the cache rows before pos (row t at t * dim floats; kv_dim of them read) */
+    kv_dim = (size_t)n_kv_heads * (size_t)(dim / n_heads);
+    for (r = 0; r < (size_t)pos; r++)
+        for (i = 0; i < kv_dim; i++) {
+            h = h * 6364136223846793005ull + 1442695040888963407ull;
+            ((float*)t.state.key_cache)[r * (size_t)dim + i] = (float)(h >> 40) * 0x1p-24f - 0.5f;
+            h = h * 6364136223846793005ull + 1442695040888963407ull;
+            ((float*)t.state.value_cache)[r * (size_t)dim + i] = (float)(h >> 40) * 0x1p-24f - 0.5f;
+        }
+    memset(&opt, 0, sizeof(opt));
+    opt.backend = (KernelBackend)backend;
+    opt.num_threads = threads;
+    runtime_init(&rt, opt);
+    for (i = 0; i < (size_t)(warmup + reps); i++) {
+        c = (int)(i % (size_t)ncopies);
+        t.weights.rms_att_weight = rmsp + c;
+        t.weights.rms_ffn_weight = rmsp + c;
+        t.weights.wq = qp + c;
+        t.weights.wk = kp + c;
+        t.weights.wv = vp + c;
+        t.weights.wo = op + c;
+        t.weights.wq_type = tq + c;
+        t.weights.wk_type = tk + c;
+        t.weights.wv_type = tv + c;
+        t.weights.wo_type = to + c;
+        t.weights.ffn_gate_inp = rp + c;
+        t.weights.expert_w1 = ew1 + c;
+        t.weights.expert_w2 = ew2 + c;
+        t.weights.expert_w3 = ew3 + c;
+        t.weights.exp_w1_type = t_up + c;
+        t.weights.exp_w2_type = t_down + c;
+        t.weights.exp_w3_type = t_gate + c;
+        clock_gettime(CLOCK_MONOTONIC, &a);
+        forward_runtime(&rt, &t, (int)(i % (size_t)n_tok), pos);
+        clock_gettime(CLOCK_MONOTONIC, &b);
+        if ((int)i >= warmup)
+            times[i - (size_t)warmup] =
+                (double)(b.tv_sec - a.tv_sec) + 1e-9 * (double)(b.tv_nsec - a.tv_nsec);
+    }
+    free_run_state(&t.state);
+    for (c = 0; c < ncopies; c++) free(ew1[c]);
+    free(rmsp);
+    free(ew1);
+    free(tq);
+    (void)l;
+    return 0;
+}
+
 /* CLOCK_MONOTONIC seconds of each of `reps` matmul_q_fused calls after
  * `warmup` untimed ones; call i uses weight copy i % ncopies. */
 int refdrv_gemv_bench(const float* x, const void* const* w_copies, int ncopies, uint32_t type,
