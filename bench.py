@@ -246,9 +246,10 @@ def bench_sweep(dev, types, warmup, pool_bytes=600 << 20, max_steps=2048, only=N
                         key, ms * 1e3, alg / (ms / 1e3) / 1e9, res[key]["frac"]))
                     xb.free()
                     yb.free()
-            if qtype in (Q.TYPE_Q4_K, Q.TYPE_Q5_K):
+            if qtype in (Q.TYPE_Q4_K, Q.TYPE_Q5_K, Q.TYPE_Q8_0) or (
+                    qtype == Q.TYPE_Q6_K and d % 2048 == 0):
                 # the same shapes in the tiled layout: a pool of tiled copies of the
-                # first n rows
+                # first n rows (Q6_K: rows of whole 2048-element multiples)
                 for n, _ in shapes:
                     wb = n * rb
                     copies_t = max(1, math.ceil(pool_bytes / wb))
@@ -256,7 +257,7 @@ def bench_sweep(dev, types, warmup, pool_bytes=600 << 20, max_steps=2048, only=N
                     dev.tile(qtype, pool.ptr, tpool.ptr, n, d)
                     for c in range(1, copies_t):
                         dev.copy(tpool.ptr + c * wb, tpool.ptr, wb)
-                    for nt in (1, 4):
+                    for nt in ((1,) if qtype == Q.TYPE_Q8_0 else (1, 4)):
                         steps = int(min(max(64, copies_t), max_steps))
                         xb = dev.upload(synth.normal(3 + nt, (nt, d)))
                         yb = dev.alloc(nt * n * 4)
@@ -487,7 +488,7 @@ def build_decoder(dev, M, cap):
     """The Qwen3-30B-A3B-shaped decoder: 48 layers of attention (wq / wk / wo
     Q4_K, wv Q6_K, 32 query heads over 4 kv heads of 128) on top of the MoE
     layers M, a Q4_K embedding and a Q6_K lm_head of 151936 rows (8192
-    distinct rows repeated), and a Q8_0 KV cache of `cap` positions."""
+    distinct rows repeated; tiled), and a Q8_0 KV cache of `cap` positions."""
     c = QWEN3_DEC
     dim, H, KVH, hd, V = c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["vocab"]
     qd, kvd = H * hd, KVH * hd
@@ -511,7 +512,12 @@ def build_decoder(dev, M, cap):
     for l in range(1, L):
         dev.copy(slab.ptr + l * per_layer, slab.ptr, per_layer)
     emb = _tiled(dev, synth.weights(5010, 8192, dim, Q.TYPE_Q4_K), V)
-    wcls = _tiled(dev, synth.weights(5011, 8192, dim, Q.TYPE_Q6_K), V)
+    # the Q6_K lm_head in the tiled layout, as qr_gguf_load stores it
+    wrows = _tiled(dev, synth.weights(5011, 8192, dim, Q.TYPE_Q6_K), V)
+    wcls = dev.alloc(V * synth.row_bytes(Q.TYPE_Q6_K, dim))
+    dev.tile(Q.TYPE_Q6_K, wrows.ptr, wcls.ptr, V, dim)
+    dev.sync()
+    wrows.free()
     rmsf = dev.upload((1.0 + synth.normal(5012, (dim,), 0.1)).astype(np.float32))
     log("bench: decoder weights built in %.1fs" % (time.time() - t0))
     layers = []
@@ -522,7 +528,7 @@ def build_decoder(dev, M, cap):
                            router=ml.router, up=ml.up, gate=ml.gate, down=ml.down))
     m = dict(dim=dim, n_heads=H, n_kv_heads=KVH, head_dim=hd, n_layers=L, vocab=V, seq_len=cap,
              rope_base=1e6, tok_embd=emb.ptr, tok_type=Q.TYPE_Q4_K, rms_final=rmsf.ptr,
-             wcls=wcls.ptr, wcls_type=Q.TYPE_Q6_K,
+             wcls=wcls.ptr, wcls_type=Q.TYPE_Q6_K | Q.TILED,
              wtype=(Q.TYPE_Q4_K | Q.TILED, Q.TYPE_Q4_K | Q.TILED, Q.TYPE_Q6_K,
                     Q.TYPE_Q4_K | Q.TILED),
              E=M["shape"]["E"], K=M["shape"]["K"], hidden=M["shape"]["hidden"],

@@ -1193,7 +1193,8 @@ hipError_t matmul_q_dev(const void* w, uint32_t type, int order, const float* x,
   if (type == QR_T_F32)
     return gemv_f32_launch(order, static_cast<const float*>(w), x, y, n, dd, 1, dd, n, s);
   if (type & QR_TILED)
-    return gemv_tiled_launch((int)(type & ~(uint32_t)QR_TILED), w, x, y, n, dd, 1, dd, n, s);
+    return gemv_tiled_launch((int)(type & ~(uint32_t)QR_TILED), w, x, y, n, dd, 1, dd, n, s,
+                             order);
   return gemv_launch((int)type, order, w, x, y, n, dd, 1, dd, n, nullptr, nullptr, s);
 }
 
@@ -1333,7 +1334,11 @@ hipError_t matmul_rows_dev(qr_decoder* d, const void* w, uint32_t type, const fl
   const bool tiled = (type & QR_TILED) != 0;
   const uint32_t base = type & ~(uint32_t)QR_TILED;
   const bool lanes = base == QR_T_Q8_0 && d->order != QR_ORDER_SEQ;
-  if (!lanes && T >= 2 && mfma_type_ok((int)base) && dd % 256 == 0 && (dd >> 8) <= 64) {
+  // the MFMA products read row-major or Q4_K / Q5_K tiles; Q6_K / Q8_0 tiles
+  // take the tiled GEMV four rows at a time
+  const bool sq_tiles = tiled && (base == QR_T_Q6_K || base == QR_T_Q8_0);
+  if (!lanes && !sq_tiles && T >= 2 && mfma_type_ok((int)base) && dd % 256 == 0 &&
+      (dd >> 8) <= 64) {
     // 16-pair work items: a dense matrix has one "expert", so the items are
     // what spreads it over the CUs (measured on a 128-token chunk of the
     // Qwen3-30B-A3B-shaped model: 71 ms for 512 prompt tokens against 75 ms
@@ -1354,7 +1359,7 @@ hipError_t matmul_rows_dev(qr_decoder* d, const void* w, uint32_t type, const fl
     const int nt = T - t0 < 4 ? T - t0 : 4;
     if (tiled)
       e = gemv_tiled_launch((int)base, w, x + (size_t)t0 * dd, y + (size_t)t0 * n, n, dd, nt, dd, n,
-                            s);
+                            s, d->order);
     else
       e = gemv_launch((int)base, d->order, w, x + (size_t)t0 * dd, y + (size_t)t0 * n, n, dd, nt,
                       dd, n, nullptr, nullptr, s);

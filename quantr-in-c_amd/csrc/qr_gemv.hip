@@ -19,6 +19,7 @@
 #include "qr_stream.h"
 #include "qr_blk.h"
 #include "qr_tiled.h"
+#include "qr_tiled_sq.h"
 #include "qr_ggml.h"
 
 namespace qr {
@@ -506,11 +507,66 @@ size_t tiled_lds_bytes(int type, int d, int nt, int nw) {
   return align16((size_t)nt * act_tok_bytes(d)) + (size_t)nw * nch * 1024;
 }
 
-bool gemv_tiled_ok(int type, int d, int nt) {
+static size_t sq_lds_bytes(int type, int d, int nt, int nw) {
+  return align16((size_t)nt * act_tok_bytes(d)) + (size_t)nw * sq_slot_kib(type) * 1024;
+}
+
+bool gemv_tiled_ok(int type, int d, int nt, int q8o) {
+  if (!(nt >= 1 && nt <= 4) && nt != 8) return false;
+  if (type == QR_T_Q6_K || type == QR_T_Q8_0) {
+    // the Q8_0 lane orders keep eight accumulators per row: streaming engine only
+    if (!sq_shape_ok(type, d) || (type == QR_T_Q8_0 && q8o != kQ8Seq)) return false;
+    return sq_lds_bytes(type, d, nt == 8 ? 4 : nt, 2) <= kLdsMax;
+  }
   if (type != QR_T_Q4_K && type != QR_T_Q5_K) return false;
   if (d <= 0 || (d & 255) || (d >> 8) > 64) return false;
-  if (!(nt >= 1 && nt <= 4) && nt != 8) return false;
   return tiled_lds_bytes(type, d, nt == 8 ? 4 : nt, 4) <= kLdsMax;
+}
+
+// Q6_K / Q8_0 (qr_tiled_sq.h): four waves per workgroup (a 14 / 17 KiB slot
+// each; two where four do not fit beside a long activation), as many
+// workgroups per CU as the LDS holds (up to 4), the waves then walking their
+// tiles.
+template <int TYPE, int NT, int NW>
+static hipError_t launch_sq_nw(const GemvArgs& a, hipStream_t st) {
+  static std::atomic<bool> opted[64];
+  const SqGeom g = sq_geom(TYPE, a.n, a.d);
+  if (g.ntiles <= 0) return hipSuccess;
+  const size_t lds = sq_lds_bytes(TYPE, a.d, NT, NW);
+  if (lds > 64 * 1024) {
+    hipError_t e = lds_opt_in((const void*)k_gemv_tiled_sq<TYPE, NT, NW>, opted);
+    if (e != hipSuccess) return e;
+  }
+  int per_cu = (int)(kLdsMax / lds);
+  per_cu = per_cu < 1 ? 1 : (per_cu > 4 ? 4 : per_cu);
+  const int want = (g.ntiles + NW - 1) / NW;
+  const int cap = device_cus() * per_cu;
+  const int grid = want < cap ? want : cap;
+  hipLaunchKernelGGL((k_gemv_tiled_sq<TYPE, NT, NW>), dim3(grid), dim3(64 * NW), lds, st, a);
+  return hipGetLastError();
+}
+template <int TYPE, int NT>
+static hipError_t launch_sq_t(const GemvArgs& a, hipStream_t st) {
+  if (sq_lds_bytes(TYPE, a.d, NT, 4) <= kLdsMax) return launch_sq_nw<TYPE, NT, 4>(a, st);
+  return launch_sq_nw<TYPE, NT, 2>(a, st);
+}
+
+template <int TYPE>
+static hipError_t launch_sq_type(GemvArgs a, int nt, hipStream_t st) {
+  switch (nt) {
+    case 1: return launch_sq_t<TYPE, 1>(a, st);
+    case 2: return launch_sq_t<TYPE, 2>(a, st);
+    case 3: return launch_sq_t<TYPE, 3>(a, st);
+    case 4: return launch_sq_t<TYPE, 4>(a, st);
+    case 8: {  // two launches of four tokens
+      hipError_t e = launch_sq_t<TYPE, 4>(a, st);
+      if (e != hipSuccess) return e;
+      a.X += (size_t)4 * a.xstride;
+      a.Y += (size_t)4 * a.ystride;
+      return launch_sq_t<TYPE, 4>(a, st);
+    }
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int TYPE, int NT, int NW, int PRO>
@@ -575,7 +631,7 @@ static hipError_t launch_tiled_type(GemvArgs a, int nt, hipStream_t st) {
 }
 
 hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, int n, int d,
-                             int nt, int xstride, int ystride, hipStream_t st) {
+                             int nt, int xstride, int ystride, hipStream_t st, int q8o) {
   GemvArgs a;
   a.W = static_cast<const uint8_t*>(W);
   a.X = X;
@@ -587,6 +643,16 @@ hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, 
   a.rows_per_wg = 0;
   a.acc = nullptr;
   a.accb = nullptr;
+  if (type == QR_T_Q6_K || type == QR_T_Q8_0) {
+    if (!gemv_tiled_ok(type, d, nt, q8o)) return hipErrorInvalidValue;
+    const SqGeom g = sq_geom(type, n, d);
+    a.t_nb = g.nb;
+    a.t_rb = g.RB;
+    a.t_ntiles = g.ntiles;
+    a.t_tile_bytes = g.tile_bytes;
+    if (type == QR_T_Q6_K) return launch_sq_type<QR_T_Q6_K>(a, nt, st);
+    return launch_sq_type<QR_T_Q8_0>(a, nt, st);
+  }
   const TiledGeom g = tiled_geom(type, n, d);
   a.t_nb = g.nb;
   a.t_rb = g.RB;
@@ -695,6 +761,22 @@ hipError_t ggml_dequant_launch(int type, const void* src, int rows, int n, float
 
 hipError_t tile_pack_launch(int type, const void* src, void* dst, int n, int d, bool reverse,
                             hipStream_t st) {
+  if (type == QR_T_Q6_K || type == QR_T_Q8_0) {
+    const long per = type == QR_T_Q6_K ? SqFmt<QR_T_Q6_K>::kChunks + 1 : SqFmt<QR_T_Q8_0>::kChunks;
+    const long total = (long)n * (d >> 8) * per;
+    if (total <= 0) return hipSuccess;
+    long grid = (total + 255) / 256;
+    if (grid > 65536) grid = 65536;
+    const uint8_t* s = static_cast<const uint8_t*>(src);
+    uint8_t* o = static_cast<uint8_t*>(dst);
+    if (type == QR_T_Q6_K)
+      hipLaunchKernelGGL(k_tile_pack_sq<QR_T_Q6_K>, dim3((unsigned)grid), dim3(256), 0, st, s, o,
+                         n, d, reverse ? 1 : 0);
+    else
+      hipLaunchKernelGGL(k_tile_pack_sq<QR_T_Q8_0>, dim3((unsigned)grid), dim3(256), 0, st, s, o,
+                         n, d, reverse ? 1 : 0);
+    return hipGetLastError();
+  }
   const long nch = type == QR_T_Q4_K ? TiledFmt<QR_T_Q4_K>::kChunks : TiledFmt<QR_T_Q5_K>::kChunks;
   const long total = (long)n * (d >> 8) * nch;
   if (total <= 0) return hipSuccess;

@@ -38,10 +38,13 @@ int gemv_rows_per_wg(int type, int q8o, int n, int d, int nt);
 hipError_t gemv_launch(int type, int q8o, const void* W, const float* X, float* Y, int n, int d,
                        int nt, int xstride, int ystride, int32_t* acc, int32_t* accb,
                        hipStream_t st);
-// Tiled layout (qr_tiled.h): type is the base type (QR_T_Q4_K / QR_T_Q5_K).
-bool gemv_tiled_ok(int type, int d, int nt);
+// Tiled layout (qr_tiled.h, qr_tiled_sq.h): type is the base type (QR_T_Q4_K /
+// QR_T_Q5_K / QR_T_Q6_K / QR_T_Q8_0).
+// Q6_K / Q8_0 tiles (qr_tiled_sq.h) too; Q8_0 in the sequential dot order
+// only (q8o, kQ8Seq = 0).
+bool gemv_tiled_ok(int type, int d, int nt, int q8o = 0);
 hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, int n, int d,
-                             int nt, int xstride, int ystride, hipStream_t st);
+                             int nt, int xstride, int ystride, hipStream_t st, int q8o = 0);
 hipError_t tile_pack_launch(int type, const void* src, void* dst, int n, int d, bool reverse,
                             hipStream_t st);
 // llama.cpp / ggml K-quants (qr_ggml.h): type is 12 / 13 / 14 (Q4_K / Q5_K / Q6_K).

@@ -479,11 +479,14 @@ size_t qr_row_bytes(uint32_t type, int d) {
 }
 
 static int tile_args(uint32_t type, const void* src, void* dst, int n, int d, const char* who) {
-  if (type != QR_T_Q4_K && type != QR_T_Q5_K)
-    return fail(QR_ERR_UNSUPPORTED, "%s: type %u has no tiled layout (Q4_K, Q5_K)", who, type);
+  if (type != QR_T_Q4_K && type != QR_T_Q5_K && type != QR_T_Q6_K && type != QR_T_Q8_0)
+    return fail(QR_ERR_UNSUPPORTED, "%s: type %u has no tiled layout (Q4_K, Q5_K, Q6_K, Q8_0)", who,
+                type);
   if (n < 0 || d <= 0 || (d & 255) || (d >> 8) > 64)
     return fail(QR_ERR_UNSUPPORTED, "%s: shape %d x %d (d a multiple of 256, at most 16384)", who,
                 n, d);
+  if (type == QR_T_Q6_K && d % 2048)
+    return fail(QR_ERR_UNSUPPORTED, "%s: tiled Q6_K needs d a multiple of 2048 (d=%d)", who, d);
   if (n > 0 && (!src || !dst)) return fail(QR_ERR_INVALID, "%s: null pointer", who);
   if (!aligned(src, 16) || !aligned(dst, 16))
     return fail(QR_ERR_INVALID, "%s: src and dst must be 16-byte aligned", who);
@@ -556,7 +559,7 @@ int qr_gemv_ord(qr_ctx* c, int order, uint32_t type, const void* w, const float*
     QR_HIP(hipGetLastError(), "k_zero_rows");
     return QR_OK;
   }
-  if (tiled && type != QR_T_Q4_K && type != QR_T_Q5_K)
+  if (tiled && type != QR_T_Q4_K && type != QR_T_Q5_K && type != QR_T_Q6_K && type != QR_T_Q8_0)
     return fail(QR_ERR_UNSUPPORTED, "qr_gemv: type %u has no tiled layout", type);
   if (type == QR_T_F32) {
     if (acc || accb) return fail(QR_ERR_INVALID, "qr_gemv: F32 has no integer sums");
@@ -577,9 +580,10 @@ int qr_gemv_ord(qr_ctx* c, int order, uint32_t type, const void* w, const float*
   }
   if (tiled) {
     if (acc || accb) return fail(QR_ERR_UNSUPPORTED, "qr_gemv: no integer sums on tiled weights");
-    if (!qr::gemv_tiled_ok((int)type, d, nt))
-      return fail(QR_ERR_UNSUPPORTED, "qr_gemv: tiled type %u at d=%d nt=%d", type, d, nt);
-    QR_HIP(qr::gemv_tiled_launch((int)type, w, x, y, n, d, nt, xstride, ystride, c->stream),
+    if (!qr::gemv_tiled_ok((int)type, d, nt, order))
+      return fail(QR_ERR_UNSUPPORTED, "qr_gemv: tiled type %u at d=%d nt=%d order %d", type, d, nt,
+                  order);
+    QR_HIP(qr::gemv_tiled_launch((int)type, w, x, y, n, d, nt, xstride, ystride, c->stream, order),
            "k_gemv_tiled");
     return QR_OK;
   }
@@ -688,8 +692,8 @@ int gemv_check(uint32_t type, int order, const void* w, int n, int d, const char
   if (type & QR_TILED) {
     type &= ~(uint32_t)QR_TILED;
     if (n <= 0 || d <= 0) return fail(QR_ERR_INVALID, "%s: weight shape %d x %d", who, n, d);
-    if (!gemv_tiled_ok((int)type, d, 1))
-      return fail(QR_ERR_UNSUPPORTED, "%s: tiled type %u at d=%d", who, type, d);
+    if (!gemv_tiled_ok((int)type, d, 1, order))
+      return fail(QR_ERR_UNSUPPORTED, "%s: tiled type %u at d=%d (order %d)", who, type, d, order);
     if (w && !aligned(w, 16)) return fail(QR_ERR_INVALID, "%s: weights must be 16-byte aligned", who);
     return QR_OK;
   }

@@ -312,7 +312,7 @@ class Device:
 
     def tile(self, qtype, src_ptr, dst_ptr, n, d, reverse=False):
         """qr_weights_tile (or qr_weights_untile): the tiled copy of an n x d
-        Q4_K / Q5_K matrix; pass qtype | TILED to gemv for it."""
+        Q4_K / Q5_K / Q6_K / Q8_0 matrix; pass qtype | TILED to gemv for it."""
         f = self.lib.qr_weights_untile if reverse else self.lib.qr_weights_tile
         self._check(f(self.ctx, qtype, _vp(src_ptr), _vp(dst_ptr), n, d),
                     "qr_weights_untile" if reverse else "qr_weights_tile")

@@ -298,3 +298,39 @@ def tinyllama_model(seed=9900, n_layers=2, seq_len=256, ffn_type=TYPE_Q8_0):
             down=_rows(s + 9, ffn_type, dim, hidden).reshape(-1)))
     m["layers"] = layers
     return m
+
+
+# ---- the tiled layouts of Q6_K and Q8_0 (qr_weights_tile) -------------------
+Q6_CHUNK_MAP = (12, 8, 0, 1, 9, 2, 3, 10, 4, 5, 11, 6, 7)
+
+
+def tile_sq(blob, qtype, n, d):
+    """Row-major Q6_K / Q8_0 rows [n][row bytes] -> the tiled layout, written
+    from its definition: 256 elements per lane (a Q6_K super-block, or 8
+    Q8_0 blocks), RB = 64 / (d / 256) rows per tile, chunk k of lane l at
+    16 (k L + l) of the tile; Q6_K chunks in the order Q6_CHUNK_MAP with the
+    L d fields (2 bytes) after them; Q8_0 chunk 0 = the 8 scales, chunk
+    1 + 2 j + h = bytes 16 h .. 16 h + 15 of block j's values."""
+    nb = d // 256
+    bb = 210 if qtype == TYPE_Q6_K else 272
+    src = np.ascontiguousarray(blob, np.uint8).reshape(n * nb, bb)
+    if qtype == TYPE_Q6_K:
+        chunks = [src[:, 16 * c:16 * c + 16] for c in Q6_CHUNK_MAP]
+        tail = src[:, 208:210]
+    else:
+        blk = src.reshape(n * nb, 8, 34)
+        chunks = [blk[:, :, 0:2].reshape(n * nb, 16)]
+        for j in range(8):
+            for h in range(2):
+                chunks.append(blk[:, j, 2 + 16 * h:18 + 16 * h])
+        tail = None
+    RB = 64 // nb
+    out = []
+    for t0 in range(0, n, RB):
+        rows = min(RB, n - t0)
+        lanes = slice(t0 * nb, (t0 + rows) * nb)
+        for c in chunks:
+            out.append(np.ascontiguousarray(c[lanes]).reshape(-1))
+        if tail is not None:
+            out.append(np.ascontiguousarray(tail[lanes]).reshape(-1))
+    return np.concatenate(out)

@@ -78,3 +78,28 @@ def test_tinyllama_prefill(dev, oracle, ffn):
     wl, wx = oracle.forward_seq(m, [int(t) for t in toks], ORDER_SEQ, Q.KV_F32)
     assert_bits_equal(x, wx[-1], "prefill residual")
     assert_bits_equal(lg, wl, "prefill logits")
+
+
+def test_tinyllama_gguf_tiled_q6k_head(dev, oracle):
+    """The dense model as a GGUF file with a Q6_K lm_head: qr_gguf_load stores
+    the lm_head in the tiled layout (rows of 2048), and the decoder reads it
+    with the tiled Q6_K GEMV; four decode steps bit-exact with the oracle."""
+    import gguf_writer as G
+    m = I.tinyllama_model(n_layers=1, seq_len=64)
+    m["wcls"] = I._rows(9950, Q.TYPE_Q6_K, m["vocab"], m["dim"])
+    m["wcls_type"] = Q.TYPE_Q6_K
+    gf = Q.Gguf(G.decode_model_gguf(m, arch="llama")[0])
+    gm = gf.load(dev, m["seq_len"])
+    assert gm.model.wcls_type == Q.TYPE_Q6_K | Q.TILED
+    d = gm.decoder(kv_type=Q.KV_F32, order=ORDER_SEQ, flags=Q.DEC_GRAPH)
+    toks = [2, 31000, 17, 17]
+    lg_d = dev.alloc(4 * m["vocab"])
+    lg = np.zeros((len(toks), m["vocab"]), np.float32)
+    for i, t in enumerate(toks):
+        d.forward(t, i, lg_d.ptr)
+        lg[i] = dev.download(lg_d, m["vocab"], np.float32)
+    d.close()
+    gm.close()
+    gf.close()
+    wl, _ = oracle.forward_seq(m, toks, ORDER_SEQ, Q.KV_F32)
+    assert_bits_equal(lg, wl, "logits")

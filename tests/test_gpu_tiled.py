@@ -1,4 +1,5 @@
-"""GPU parity of the tiled Q4_K / Q5_K layout (qr_weights_tile) and its GEMV.
+"""GPU parity of the tiled Q4_K / Q5_K / Q6_K / Q8_0 layouts (qr_weights_tile)
+and their GEMV.
 
 The tiled layout is this library's own permutation of the reference's
 row-major super-blocks (no reference counterpart): a tile of 64 / nb rows
@@ -117,10 +118,90 @@ def test_gemv_tiled_refusals(dev):
         dev.gemv(Q.TYPE_Q4_K | Q.TILED, wb.ptr, xb.ptr, yb.ptr, 64, 2048, 1, acc_ptr=acc.ptr,
                  accb_ptr=accb.ptr)
     with pytest.raises(Q.QrError, match="tiled layout"):
-        dev.gemv(Q.TYPE_Q6_K | Q.TILED, wb.ptr, xb.ptr, yb.ptr, 64, 2048, 1)
+        dev.gemv(Q.TYPE_F32 | Q.TILED, wb.ptr, xb.ptr, yb.ptr, 64, 2048, 1)
     with pytest.raises(Q.QrError, match="tiled"):
         dev.gemv(Q.TYPE_Q4_K | Q.TILED, wb.ptr, xb.ptr, yb.ptr, 64, 1408, 1)
+    with pytest.raises(Q.QrError, match="tiled"):  # Q6_K tiles need whole 2048-element rows
+        dev.gemv(Q.TYPE_Q6_K | Q.TILED, wb.ptr, xb.ptr, yb.ptr, 16, 768, 1)
+    with pytest.raises(Q.QrError, match="order"):  # Q8_0 tiles: the sequential order only
+        dev.gemv(Q.TYPE_Q8_0 | Q.TILED, wb.ptr, xb.ptr, yb.ptr, 64, 2048, 1, order=Q.ORDER_AVX2)
     with pytest.raises(Q.QrError, match="no tiled layout"):
-        dev.tile(Q.TYPE_Q8_0, wb.ptr, yb.ptr, 64, 2048)
+        dev.tile(Q.TYPE_F32, wb.ptr, yb.ptr, 64, 2048)
+    with pytest.raises(Q.QrError, match="2048"):
+        dev.tile(Q.TYPE_Q6_K, wb.ptr, yb.ptr, 16, 768)
     with pytest.raises(Q.QrError, match="overlap"):
         dev.tile(Q.TYPE_Q4_K, wb.ptr, wb.ptr, 64, 2048)
+
+
+# ---- Q6_K and Q8_0 (qr_tiled_sq.h) -------------------------------------------
+SQTYPES = (Q.TYPE_Q6_K, Q.TYPE_Q8_0)
+
+
+def sq_weights(seed, qtype, n, d):
+    if qtype == Q.TYPE_Q8_0:
+        return I.blocks(seed, qtype, n * (d // 32)).reshape(n, (d // 32) * 34)
+    return I.blocks(seed, qtype, n * (d // 256)).reshape(n, (d // 256) * 210)
+
+
+@pytest.mark.parametrize("qtype,n,d", [(Q.TYPE_Q6_K, 64, 2048), (Q.TYPE_Q6_K, 1001, 2048),
+                                       (Q.TYPE_Q6_K, 9, 4096), (Q.TYPE_Q6_K, 3, 16384),
+                                       (Q.TYPE_Q8_0, 64, 2048), (Q.TYPE_Q8_0, 1001, 2048),
+                                       (Q.TYPE_Q8_0, 77, 256), (Q.TYPE_Q8_0, 45, 5632),
+                                       (Q.TYPE_Q8_0, 7, 768)])
+def test_tile_layout_sq_and_inverse(dev, qtype, n, d):
+    """qr_weights_tile of Q6_K / Q8_0 against the layout written out from its
+    definition (inputs.tile_sq), and the reverse permutation back."""
+    W = sq_weights(600 + n + d + qtype, qtype, n, d)
+    wb, tb, ub = dev.upload(W), dev.alloc(W.nbytes), dev.alloc(W.nbytes)
+    dev.tile(qtype, wb.ptr, tb.ptr, n, d)
+    dev.tile(qtype, tb.ptr, ub.ptr, n, d, reverse=True)
+    got = dev.download(tb, W.nbytes, np.uint8)
+    assert np.array_equal(got, I.tile_sq(W, qtype, n, d))
+    assert np.array_equal(dev.download(ub, W.shape, np.uint8), W)
+
+
+@pytest.mark.parametrize("nt", [1, 2, 3, 4, 8])
+@pytest.mark.parametrize("qtype,n,d", [(Q.TYPE_Q6_K, 32000, 2048), (Q.TYPE_Q6_K, 2048, 2048),
+                                       (Q.TYPE_Q6_K, 256, 2048), (Q.TYPE_Q6_K, 5632, 2048),
+                                       (Q.TYPE_Q6_K, 512, 2048), (Q.TYPE_Q6_K, 1001, 2048),
+                                       (Q.TYPE_Q6_K, 13, 4096), (Q.TYPE_Q6_K, 7, 16384),
+                                       (Q.TYPE_Q8_0, 32000, 2048), (Q.TYPE_Q8_0, 2048, 2048),
+                                       (Q.TYPE_Q8_0, 256, 2048), (Q.TYPE_Q8_0, 5632, 2048),
+                                       (Q.TYPE_Q8_0, 2048, 5632), (Q.TYPE_Q8_0, 1001, 2048),
+                                       (Q.TYPE_Q8_0, 333, 256), (Q.TYPE_Q8_0, 5, 768),
+                                       (Q.TYPE_Q8_0, 40, 16384)])
+def test_gemv_tiled_sq_shapes(dev, oracle, qtype, n, d, nt):
+    """The Q6_K / Q8_0 tiled GEMV against the oracle's matmul_q_fused
+    (src/quant.c:441-523; Q8_0 in the -std=c99 build's order) bit for bit:
+    the sweep's shapes and lm_head, wv (512 rows), short last tiles, 64-row
+    and 1-row tiles, every batch width."""
+    W = synth.weights(3300 + n + d + qtype, n, d, qtype)
+    X = synth.normal(3400 + nt, (nt, d))
+    print("tiled sq type %d %dx%d nt %d" % (qtype, n, d, nt), flush=True)
+    y = run_tiled(dev, qtype, W, X, n, d, nt)
+    want = oracle.matmul_q_fused(X, W, qtype, n, d, threads=16).reshape(nt, n)
+    assert_bits_equal(y, want, "tiled type %d %dx%d nt=%d" % (qtype, n, d, nt))
+
+
+@pytest.mark.parametrize("qtype,d", [(Q.TYPE_Q6_K, 2048), (Q.TYPE_Q8_0, 2048),
+                                     (Q.TYPE_Q8_0, 768)])
+def test_gemv_tiled_sq_random_blocks(dev, oracle, qtype, d):
+    """Random block bytes plus a row of edge-case blocks (zero, subnormal,
+    largest and negative half scales; Q6_K's int8 scales over their whole
+    range), 1 and 3 tokens."""
+    W = I.dot_set(950 + qtype + d, qtype, 63, d)
+    for nt in (1, 3):
+        X = I.activations(951 + nt, nt, d)
+        y = run_tiled(dev, qtype, W, X, W.shape[0], d, nt)
+        want = oracle.matmul_q_fused(X, W, qtype, W.shape[0], d).reshape(nt, -1)
+        assert_bits_equal(y, want, "tiled random type %d d=%d nt=%d" % (qtype, d, nt))
+
+
+def test_gemv_tiled_sq_lm_head_151936(dev, oracle):
+    """The Qwen3-30B-A3B lm_head: 151936 x 2048 Q6_K, 1 token."""
+    n, d = 151936, 2048
+    W = np.tile(synth.weights(3500, 4096, d, Q.TYPE_Q6_K), (n // 4096 + 1, 1))[:n].copy()
+    X = synth.normal(3501, (1, d))
+    y = run_tiled(dev, Q.TYPE_Q6_K, W, X, n, d, 1)
+    want = oracle.matmul_q_fused(X, W, Q.TYPE_Q6_K, n, d, threads=16).reshape(1, n)
+    assert_bits_equal(y, want, "tiled Q6_K lm_head")
