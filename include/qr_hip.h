@@ -143,15 +143,19 @@ int qr_gemv_ord(qr_ctx* ctx, int order, uint32_t type, const void* w, const floa
                 int xstride, float* y, int ystride, int n, int d, int nt, int32_t* acc,
                 int32_t* accb);
 
-/* The tiled layout of a Q4_K / Q5_K matrix: the same bytes as the
- * reference's row-major super-blocks, permuted so that the GEMV streams each
+/* The tiled layout of a Q4_K / Q5_K / Q6_K / Q8_0 matrix: the same bytes as
+ * the reference's row-major blocks, permuted so that the GEMV streams each
  * wave's tile in the order it is consumed (no reference counterpart; the
- * results are the same bits).  A tile is 64 / (d / 256) rows; within it, the
- * k-th 16-byte chunk of every super-block is stored together (header chunk
- * first).  Pass `type | QR_TILED` to qr_gemv / qr_gemv_ex / qr_gemv_ord (no
- * integer sums) and in a decoder model's wq / wk / wv / wo / wcls types.
- * qr_weights_tile writes the tiled copy of an n x d matrix (d a multiple of
- * 256, at most 16384) into dst, qr_weights_untile the reverse; device
+ * results are the same bits).  A lane holds 256 elements of a row (a K-quant
+ * super-block, or 8 Q8_0 blocks) and a tile is 64 / (d / 256) rows; within
+ * it, the k-th 16-byte chunk of every lane is stored together (Q4_K / Q5_K:
+ * the header chunk first; Q6_K: its scales, then each unit pair's high bits
+ * and low nibbles, the lanes' fp16 d fields after the chunks; Q8_0: the 8
+ * scales, then the blocks' values).  Pass `type | QR_TILED` to qr_gemv /
+ * qr_gemv_ex / qr_gemv_ord (no integer sums; Q8_0 in QR_ORDER_SEQ only) and in
+ * a decoder model's wq / wk / wv / wo / wcls types.  qr_weights_tile writes
+ * the tiled copy of an n x d matrix (d a multiple of 256, at most 16384; Q6_K
+ * a multiple of 2048) into dst, qr_weights_untile the reverse; device
  * pointers, 16-byte aligned, not overlapping; enqueued on the context
  * stream.  qr_row_bytes(type | QR_TILED, d) is the plain row size. */
 #define QR_TILED 0x100u
