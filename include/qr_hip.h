@@ -450,6 +450,16 @@ int qr_gguf_expert_host(const qr_gguf* g, int layer, int e, const void** up, con
  * drained; no decoder built on it may be used afterwards). */
 typedef struct qr_gguf_model qr_gguf_model;
 int qr_gguf_load(qr_ctx* ctx, const qr_gguf* g, int seq_len, qr_gguf_model** out);
+/* qr_gguf_load with flags.  QR_GGUF_GGML_KQUANTS: the file's Q4_K / Q5_K /
+ * Q6_K tensors are in llama.cpp's own block layouts (a checkpoint quantized
+ * by llama.cpp; the reference reads the same bytes in its layouts,
+ * src/quant.c:180-238): their types carry QR_GGML, none is tiled, and the
+ * decoder computes them with ggml's Q8_K dots (a MoE layer's experts then all
+ * three ggml K-quants, and no shared expert).  No counterpart in the
+ * reference, which has no such option. */
+#define QR_GGUF_GGML_KQUANTS 1u
+int qr_gguf_load_ex(qr_ctx* ctx, const qr_gguf* g, int seq_len, uint32_t flags,
+                    qr_gguf_model** out);
 const qr_model* qr_gguf_model_get(const qr_gguf_model* m);
 int qr_gguf_model_free(qr_gguf_model* m);
 

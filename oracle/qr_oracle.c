@@ -62,7 +62,7 @@ static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); 
 /* src/quant.c:477-484 (and src/model.c:20-30): bytes per weight row.  Rows
  * keep only whole blocks; a tail shorter than one block is dropped. */
 size_t qro_row_bytes(uint32_t type, int d) {
-    switch (type) {
+    switch (type & ~QRO_GGML) {
         case QRO_TYPE_Q8_0: return (size_t)(d / QK8) * Q8_BYTES;
         case QRO_TYPE_Q4_K: return (size_t)(d / QKK) * Q4K_BYTES;
         case QRO_TYPE_Q5_K: return (size_t)(d / QKK) * Q5K_BYTES;
@@ -482,6 +482,8 @@ static void matmul_any(float* out, const float* x, const void* w, uint32_t type,
         memset(out, 0, (size_t)n * sizeof(float));
     } else if (type == QRO_TYPE_F32) {
         qro_matmul_f32(out, x, (const float*)w, n, d, router_order);
+    } else if (type & QRO_GGML) {
+        qro_ggml_matmul_mt(out, x, w, (int)(type & ~QRO_GGML), n, d, 1, threads);
     } else {
         qro_matmul_q_fused(out, x, w, type, n, d, threads, dot_order);
     }

@@ -49,6 +49,10 @@ extern "C" {
 #define QRO_TYPE_Q4_K 12
 #define QRO_TYPE_Q5_K 13
 #define QRO_TYPE_Q6_K 14
+/* llama.cpp / ggml's own K-quant layouts (qr_oracle_ggml.c) when set on a
+ * Q4_K / Q5_K / Q6_K type: the dot against Q8_K activations of ggml's
+ * generic ggml_vec_dot_q*_K_q8_K (same block sizes as the reference's). */
+#define QRO_GGML 0x200u
 
 /* fp32 accumulation orders of the reference builds.
  * SEQ:    the portable C99 loops (Makefile CFLAGS -O3 -std=c99, no FMA):
@@ -116,6 +120,11 @@ size_t qro_expert_slice_bytes(uint32_t type, int ne0, int ne1);
 /* router_order: the router's KernelOps.matmul order (and F32 experts');
  * dot_order: the Q8_0 fused-dot order of the build (K-quant dots have one). */
 void qro_dense_ffn(float* x, const float* xb, const qro_moe_layer* L, int order, int threads);
+/* qr_oracle_ggml.c: rows of a ggml-layout matrix against Q8_K(x) (rows in
+ * parallel, any width: the same bits), and one row's dequantization. */
+void qro_ggml_matmul_mt(float* out, const float* x, const void* w, int type, int n, int d, int nt,
+                        int threads);
+void qro_ggml_dequantize_row(int type, const void* src, float* y, int n);
 void qro_moe_token(float* x, const float* xb, const qro_moe_layer* L, int router_order,
                    int dot_order, int threads, int32_t* idx_out, float* w_out);
 void qro_moe_forward(float* x, const float* xb, int T, const qro_moe_layer* L, int router_order,

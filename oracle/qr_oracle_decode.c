@@ -19,7 +19,9 @@
  *     one byte per element, src/model.c:82-88).
  * With head_dim = dim / n_heads and an fp32 or fp16 cache, qro_forward is
  * pinned bit for bit to the reference's forward_runtime by golden logits
- * (tests/golden/decode.npz).
+ * (tests/golden/decode.npz).  Matrices of llama.cpp's K-quant layouts
+ * (QRO_GGML) take ggml's Q8_K dot (qr_oracle_ggml.c), the embedding row its
+ * dequantization: that composition has no reference counterpart.
  */
 #include <math.h>
 #include <stdlib.h>
@@ -166,6 +168,7 @@ static void mq(float* out, const float* x, const void* w, uint32_t type, int n, 
                int threads) {
     if (w == NULL) memset(out, 0, (size_t)n * sizeof(float));
     else if (type == QRO_TYPE_F32) qro_matmul_f32(out, x, (const float*)w, n, d, order);
+    else if (type & QRO_GGML) qro_ggml_matmul_mt(out, x, w, (int)(type & ~QRO_GGML), n, d, 1, threads);
     else qro_matmul_q_fused(out, x, w, type, n, d, threads, order);
 }
 
@@ -183,8 +186,13 @@ void qro_forward(const qro_model* m, void* kc, void* vc, int token, int pos, int
     float* att = (float*)calloc((size_t)m->n_heads * (size_t)(pos + 1), 4);
     int l, i;
     if (!xb || !xb2 || !q || !k || !v || !ao || !att) goto done;
-    qro_dequantize_row(x, (const uint8_t*)m->tok_embd + (size_t)token * m->tok_row_bytes,
-                       m->tok_type, dim);
+    if (m->tok_type & QRO_GGML)
+        qro_ggml_dequantize_row((int)(m->tok_type & ~QRO_GGML),
+                                (const uint8_t*)m->tok_embd + (size_t)token * m->tok_row_bytes, x,
+                                dim);
+    else
+        qro_dequantize_row(x, (const uint8_t*)m->tok_embd + (size_t)token * m->tok_row_bytes,
+                           m->tok_type, dim);
     for (l = 0; l < m->n_layers; l++) {
         uint8_t* kl = (uint8_t*)kc + (size_t)l * m->seq_len * rs;
         uint8_t* vl = (uint8_t*)vc + (size_t)l * m->seq_len * rs;

@@ -297,14 +297,21 @@ float qro_ggml_vec_dot(int type, const void* row, const void* q8k, int n) {
     return sumf;
 }
 
-/* out[t][r] = dot(row r, Q8_K(x[t])) for t < nt. */
-void qro_ggml_matmul(float* out, const float* x, const void* w, int type, int n, int d, int nt) {
+/* out[t][r] = dot(row r, Q8_K(x[t])) for t < nt; rows split over `threads`
+ * (each row's dot is independent: the same bits at any width). */
+void qro_ggml_matmul_mt(float* out, const float* x, const void* w, int type, int n, int d, int nt,
+                        int threads) {
     const size_t rb = qro_ggml_block_bytes(type) * (size_t)(d / QK);
     uint8_t yq[292 * 64];
     int t, r;
     for (t = 0; t < nt; t++) {
         qro_quantize_row_q8_K(x + (size_t)t * d, yq, d);
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
         for (r = 0; r < n; r++)
             out[(size_t)t * n + r] = qro_ggml_vec_dot(type, (const uint8_t*)w + (size_t)r * rb, yq, d);
     }
+}
+
+void qro_ggml_matmul(float* out, const float* x, const void* w, int type, int n, int d, int nt) {
+    qro_ggml_matmul_mt(out, x, w, type, n, d, nt, 1);
 }

@@ -26,14 +26,17 @@
 #include <vector>
 
 #include "qr_common.h"
+#include "qr_ggml_elem.h"
 #include "qr_internal.h"
 
 namespace qr {
 
 // ---------------------------------------------------------------------------
-// Element e of a row of `type` (dequantize_row, src/quant.c:160-240).
+// Element e of a row of `type` (dequantize_row, src/quant.c:160-240; a
+// llama.cpp-layout K-quant row through ggml's dequantize_row_q*_K).
 // ---------------------------------------------------------------------------
 __device__ inline float deq_elem(const uint8_t* __restrict__ row, int type, int e) {
+  if (type & QR_GGML) return ggml_deq_elem(row, type & ~(int)QR_GGML, e);
   if (type == QR_T_F32) return reinterpret_cast<const float*>(row)[e];
   if (type == QR_T_Q8_0) {
     const uint8_t* b = row + (size_t)(e >> 5) * QR_Q8_BYTES;
@@ -1187,11 +1190,14 @@ KvView kv_view(const qr_decoder* d, int layer, bool values) {
 
 // out[n] = W x for one token: matmul_q (src/runtime.c:58-70): fp32 weights
 // go through the build's KernelOps.matmul order, quantized ones through the
-// fused GEMV with the build's Q8_0 dot order.
+// fused GEMV with the build's Q8_0 dot order, llama.cpp-layout K-quants
+// through ggml's Q8_K dot.
 hipError_t matmul_q_dev(const void* w, uint32_t type, int order, const float* x, float* y, int n,
                         int dd, hipStream_t s) {
   if (type == QR_T_F32)
     return gemv_f32_launch(order, static_cast<const float*>(w), x, y, n, dd, 1, dd, n, s);
+  if (type & QR_GGML)
+    return gemv_ggml_launch((int)(type & ~(uint32_t)QR_GGML), w, x, y, n, dd, 1, dd, n, s);
   if (type & QR_TILED)
     return gemv_tiled_launch((int)(type & ~(uint32_t)QR_TILED), w, x, y, n, dd, 1, dd, n, s,
                              order);
@@ -1205,7 +1211,7 @@ hipError_t matmul_q_dev(const void* w, uint32_t type, int order, const float* x,
 static bool qk_stacked(const qr_decoder* d, const qr_layer& L) {
   if (L.wq_type != L.wk_type || L.wq_type == QR_T_F32 || !L.wq || !L.wk) return false;
   if (d->k != d->q + d->qd) return false;
-  const int base = (int)(L.wq_type & ~(uint32_t)QR_TILED);
+  const int base = (int)(L.wq_type & ~(uint32_t)(QR_TILED | QR_GGML));
   if ((L.wq_type & QR_TILED) && d->qd % (64 / (d->dim >> 8)) != 0) return false;
   const size_t qbytes = qr_wrow_bytes(base, d->dim) * (size_t)d->qd;
   return static_cast<const uint8_t*>(L.wk) == static_cast<const uint8_t*>(L.wq) + qbytes;
@@ -1322,7 +1328,8 @@ __global__ __launch_bounds__(256) void k_rows_dispatch(int T, int tile, int32_t*
 // order with all T rows at once; K-quant (row-major or tiled) and C99-order
 // Q8_0 weights as one grouped int8 MFMA product (qr_moe_mfma.hip, the rows
 // dispatched to a single "expert"), whose per-row terms and order are the
-// fused dot's; Q8_0 in a lane order through the GEMV, four rows per launch.
+// fused dot's; Q8_0 in a lane order and llama.cpp-layout K-quants through the
+// GEMV, four rows per launch.
 // The records of x are quantized unless `records` says the previous call
 // left those of the same x (and the same record order) in d->prec; the chunk's
 // single-expert dispatch lists are written once per chunk (prefill_rows_setup).
@@ -1331,6 +1338,16 @@ hipError_t matmul_rows_dev(qr_decoder* d, const void* w, uint32_t type, const fl
   hipError_t e;
   if (type == QR_T_F32)
     return gemv_f32_launch(d->order, static_cast<const float*>(w), x, y, n, dd, T, dd, n, s);
+  if (type & QR_GGML) {  // ggml's Q8_K dot, four rows per launch
+    d->prec_src = nullptr;  // d->prec keeps no records of x
+    for (int t0 = 0; t0 < T; t0 += 4) {
+      const int nt = T - t0 < 4 ? T - t0 : 4;
+      if ((e = gemv_ggml_launch((int)(type & ~(uint32_t)QR_GGML), w, x + (size_t)t0 * dd,
+                                y + (size_t)t0 * n, n, dd, nt, dd, n, s)))
+        return e;
+    }
+    return hipSuccess;
+  }
   const bool tiled = (type & QR_TILED) != 0;
   const uint32_t base = type & ~(uint32_t)QR_TILED;
   const bool lanes = base == QR_T_Q8_0 && d->order != QR_ORDER_SEQ;
@@ -1622,10 +1639,12 @@ int qr_decoder_create(qr_ctx* c, const qr_model* m, int kv_type, int order, int 
                      m->seq_len, page);
   if (!m->tok_embd || !m->rms_final || !m->wcls)
     return set_error(QR_ERR_INVALID, "qr_decoder_create: null embedding / final norm / wcls");
-  const bool tok_known = m->tok_type == QR_T_F32 || m->tok_type == QR_T_Q8_0 ||
-                         m->tok_type == QR_T_Q4_K || m->tok_type == QR_T_Q5_K ||
-                         m->tok_type == QR_T_Q6_K;
-  if (!tok_known || dim % qr_block_elems((int)m->tok_type))
+  const uint32_t tok_base = m->tok_type & ~(uint32_t)QR_GGML;
+  const bool tok_ggml = (m->tok_type & QR_GGML) != 0;
+  const bool tok_known = tok_base == QR_T_Q4_K || tok_base == QR_T_Q5_K ||
+                         tok_base == QR_T_Q6_K ||
+                         (!tok_ggml && (tok_base == QR_T_F32 || tok_base == QR_T_Q8_0));
+  if (!tok_known || dim % qr_block_elems((int)tok_base))
     return set_error(QR_ERR_INVALID, "qr_decoder_create: embedding type %u at dim %d", m->tok_type,
                      dim);
   int rc = gemv_check(m->wcls_type, order, m->wcls, m->vocab, dim, "qr_decoder_create: wcls");

@@ -512,6 +512,13 @@ struct GemvArgs {
   // tiles, bytes of a full tile -- set on the host
   int t_nb, t_rb, t_ntiles;
   size_t t_tile_bytes;
+  // pair mode of the ggml GEMV (expert products of llama.cpp-layout
+  // experts): workgroup row blockIdx.y = pair p multiplies expert eidx[p]'s
+  // matrix (W + eidx[p] * eslice) by activation row p / xk, into Y row p;
+  // eidx null: one matrix
+  const int32_t* eidx;
+  size_t eslice;
+  int xk, E;
 };
 
 }  // namespace qr

@@ -632,7 +632,7 @@ static hipError_t launch_tiled_type(GemvArgs a, int nt, hipStream_t st) {
 
 hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, int n, int d,
                              int nt, int xstride, int ystride, hipStream_t st, int q8o) {
-  GemvArgs a;
+  GemvArgs a{};
   a.W = static_cast<const uint8_t*>(W);
   a.X = X;
   a.Y = Y;
@@ -682,7 +682,7 @@ bool gemv_ggml_ok(int type, int d, int nt) {
 }
 
 template <int T, int NT, bool XS>
-static hipError_t launch_ggml_x(const GemvArgs& a, hipStream_t st) {
+static hipError_t launch_ggml_x(const GemvArgs& a, hipStream_t st, int pairs = 0) {
   static std::atomic<bool> opted[64];
   const int nb = a.d >> 8, RB = 64 / nb;
   const int ntiles = (a.n + RB - 1) / RB;
@@ -694,10 +694,13 @@ static hipError_t launch_ggml_x(const GemvArgs& a, hipStream_t st) {
   int per_cu = (int)(kLdsMax / lds);
   per_cu = per_cu < 1 ? 1 : (per_cu > 3 ? 3 : per_cu);
   const int want = (ntiles + 3) / 4;
-  const int cap = device_cus() * per_cu;
-  const int grid = want < cap ? want : cap;
-  if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((k_gemv_ggml<T, NT, XS>), dim3(grid), dim3(256), lds, st, a);
+  // pair mode: the pairs' matrices share the resident workgroups
+  const int cap = pairs > 0 ? (device_cus() * per_cu + pairs - 1) / pairs : device_cus() * per_cu;
+  int grid = want < cap ? want : cap;
+  if (grid < 1) grid = 1;
+  if (ntiles <= 0) return hipSuccess;
+  hipLaunchKernelGGL((k_gemv_ggml<T, NT, XS>), dim3(grid, pairs > 0 ? pairs : 1), dim3(256), lds,
+                     st, a);
   return hipGetLastError();
 }
 
@@ -737,6 +740,35 @@ hipError_t gemv_ggml_launch(int type, const void* W, const float* X, float* Y, i
   if (type == kGgmlQ4) return launch_ggml_type<kGgmlQ4>(a, nt, st);
   if (type == kGgmlQ5) return launch_ggml_type<kGgmlQ5>(a, nt, st);
   if (type == kGgmlQ6) return launch_ggml_type<kGgmlQ6>(a, nt, st);
+  return hipErrorInvalidValue;
+}
+
+// Expert products of llama.cpp-layout experts, one GEMV per (token, slot)
+// pair p: Y[p] = W_{eidx[p]} . X[p / xk] (n rows of d, one token each).
+hipError_t gemv_ggml_pairs_launch(int type, const void* W, size_t eslice, const int32_t* eidx,
+                                  int E, int xk, const float* X, int xstride, float* Y,
+                                  int ystride, int n, int d, int P, hipStream_t st) {
+  if (P <= 0) return hipSuccess;
+  if (!gemv_ggml_ok(type, d, 1) || xk < 1 || P > 65535) return hipErrorInvalidValue;
+  GemvArgs a{};
+  a.W = static_cast<const uint8_t*>(W);
+  a.X = X;
+  a.Y = Y;
+  a.n = n;
+  a.d = d;
+  a.xstride = xstride;
+  a.ystride = ystride;
+  a.eidx = eidx;
+  a.eslice = eslice;
+  a.xk = xk;
+  a.E = E;
+  const bool xs = ggml_xs(d, 1);
+  if (type == kGgmlQ4)
+    return xs ? launch_ggml_x<kGgmlQ4, 1, true>(a, st, P) : launch_ggml_x<kGgmlQ4, 1, false>(a, st, P);
+  if (type == kGgmlQ5)
+    return xs ? launch_ggml_x<kGgmlQ5, 1, true>(a, st, P) : launch_ggml_x<kGgmlQ5, 1, false>(a, st, P);
+  if (type == kGgmlQ6)
+    return xs ? launch_ggml_x<kGgmlQ6, 1, true>(a, st, P) : launch_ggml_x<kGgmlQ6, 1, false>(a, st, P);
   return hipErrorInvalidValue;
 }
 
@@ -798,7 +830,7 @@ hipError_t tile_pack_launch(int type, const void* src, void* dst, int n, int d, 
 hipError_t gemv_launch(int type, int q8o, const void* W, const float* X, float* Y, int n, int d,
                        int nt, int xstride, int ystride, int32_t* acc, int32_t* accb,
                        hipStream_t st) {
-  GemvArgs a;
+  GemvArgs a{};
   a.W = static_cast<const uint8_t*>(W);
   a.X = X;
   a.Y = Y;

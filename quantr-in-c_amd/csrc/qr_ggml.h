@@ -23,10 +23,9 @@
 #pragma once
 
 #include "qr_blk.h"
+#include "qr_ggml_elem.h"
 
 namespace qr {
-
-enum { kGgmlQ4 = 12, kGgmlQ5 = 13, kGgmlQ6 = 14 };
 
 template <int T>
 struct GgmlFmt {
@@ -39,11 +38,6 @@ struct GgmlFmt {
 // + 24), then d (fp32), then the 16 bsums as int32.
 constexpr int kQ8kBlk = 336;
 __host__ __device__ inline size_t q8k_tok_bytes(int d) { return (size_t)(d >> 8) * kQ8kBlk; }
-
-// IEEE half -> float (exact; v_cvt_f32_f16).
-__device__ inline float ggml_h2f(uint32_t h) {
-  return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xFFFFu));
-}
 
 // quantize_row_q8_K_ref (ggml-quants.c) of nt rows of d values into the LDS
 // layout above.  One wave per (token, block): lane l takes elements l + 64 k.
@@ -261,6 +255,14 @@ namespace qr {
 template <int T, int NT, bool XS>
 __global__ __launch_bounds__(256) void k_gemv_ggml(GemvArgs g) {
   extern __shared__ __align__(16) uint8_t smem[];
+  if (g.eidx) {  // pair mode: this workgroup row's expert, activation row and output row
+    const int p = blockIdx.y;
+    const int e = g.eidx[p];
+    if (e < 0 || e >= g.E) return;  // uniform, before any barrier
+    g.W += (size_t)e * g.eslice;
+    g.X += (size_t)(p / g.xk) * g.xstride;
+    g.Y += (size_t)p * g.ystride;
+  }
   constexpr int BB = GgmlFmt<T>::kBytes, NDMA = GgmlFmt<T>::kDma;
   constexpr size_t SB = (size_t)NDMA * 1024;
   const int nb = g.d >> 8, RB = 64 / nb;
@@ -376,40 +378,6 @@ __global__ __launch_bounds__(256) void k_quantize_q8k(const float* __restrict__ 
     const uint32_t dbits = __builtin_bit_cast(uint32_t, *reinterpret_cast<const float*>(b + 256));
     for (int i = 0; i < 4; i++) out[i] = (uint8_t)(dbits >> (8 * i));
   }
-}
-
-// dequantize_row_q{4,5,6}_K (ggml-quants.c) of element e of a row.
-__device__ inline float ggml_deq_elem(const uint8_t* row, int type, int e) {
-  const int i = e >> 8, r = e & 255;
-  if (type == kGgmlQ4 || type == kGgmlQ5) {
-    const uint8_t* blk = row + (size_t)i * (type == kGgmlQ4 ? 144 : 176);
-    const float d = ggml_h2f(blk[0] | (blk[1] << 8)), mn = ggml_h2f(blk[2] | (blk[3] << 8));
-    const uint8_t* s = blk + 4;
-    const int g = r >> 6, half = (r >> 5) & 1, k = r & 31, j = 2 * g + half;
-    int sc, m;
-    if (j < 4) {
-      sc = s[j] & 63;
-      m = s[j + 4] & 63;
-    } else {
-      sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
-      m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
-    }
-    const uint8_t* qs = blk + (type == kGgmlQ4 ? 16 : 48);
-    int q = half ? (qs[32 * g + k] >> 4) : (qs[32 * g + k] & 0xF);
-    if (type == kGgmlQ5) q += (blk[16 + k] >> j) & 1 ? 16 : 0;
-    const float d1 = d * (float)sc, m1 = mn * (float)m;
-    return d1 * (float)q - m1;
-  }
-  const uint8_t* blk = row + (size_t)i * 210;
-  const float d = ggml_h2f(blk[208] | (blk[209] << 8));
-  const int n = r >> 7, rr = r & 127, s = rr >> 5, l = rr & 31;
-  const uint8_t* ql = blk + 64 * n;
-  const uint8_t* qh = blk + 128 + 32 * n;
-  const int lo = (s & 1) ? ql[l + 32] : ql[l];
-  const int nib = (s & 2) ? (lo >> 4) : (lo & 0xF);
-  const int q = (int)(int8_t)(nib | (((qh[l] >> (2 * s)) & 3) << 4)) - 32;
-  const int8_t sc = (int8_t)blk[192 + 8 * n + (l >> 4) + 2 * s];
-  return d * (float)sc * (float)q;
 }
 
 __global__ __launch_bounds__(256) void k_ggml_dequant_rows(const uint8_t* __restrict__ src,

@@ -52,6 +52,9 @@ bool gemv_ggml_ok(int type, int d, int nt);
 hipError_t gemv_ggml_launch(int type, const void* W, const float* X, float* Y, int n, int d, int nt,
                             int xstride, int ystride, hipStream_t st);
 hipError_t quantize_q8k_launch(const float* x, void* y, long nblocks, hipStream_t st);
+hipError_t gemv_ggml_pairs_launch(int type, const void* W, size_t eslice, const int32_t* eidx,
+                                  int E, int xk, const float* X, int xstride, float* Y,
+                                  int ystride, int n, int d, int P, hipStream_t st);
 hipError_t ggml_dequant_launch(int type, const void* src, int rows, int n, float* out,
                                hipStream_t st);
 hipError_t gemv_f32_launch(int order, const float* W, const float* X, float* Y, int n, int d,
@@ -83,6 +86,7 @@ struct MoeScratch {
   int32_t* shoff;     // [2]   single-"expert" dispatch of the T tokens
   int32_t* shtiles;   // [2]
   int32_t* shperm;    // [T]
+  float* hu;          // [T*K][hidden]  up rows of llama.cpp-layout experts (else null)
 };
 size_t moe_scratch_bytes(const qr_moe_layer* L, int T);
 void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s);

@@ -24,6 +24,10 @@
 //   k_down_combine1  T == 1: all K down projections of the token plus the
 //                    slot-order combine (and the shared expert) in one pass.
 //   k_combine        T > 1: slot-order gather-combine.
+// llama.cpp-layout experts (ggml K-quants) take ggml's Q8_K dot instead: the
+// routing, then the ggml GEMV in pair mode (qr_ggml.h; one matrix-vector
+// product per (token, slot) pair, the pair's expert chosen on the device) for
+// up, gate and down, k_silu_mul between them, and k_combine.
 #include <cstdlib>
 
 #include "qr_gemv.h"
@@ -60,6 +64,7 @@ size_t moe_scratch_bytes(const qr_moe_layer* L, int T) {
     b += a256((size_t)T * (sh / 32) * 48);          // hqs
     b += a256(2 * 4) * 2 + a256((size_t)T * 4);     // shoff, shtiles, shperm
   }
+  if (L->up_type & QR_GGML) b += a256(P * (size_t)L->hidden * 4);  // hu
   return b;
 }
 
@@ -98,6 +103,8 @@ void moe_scratch_carve(void* base, const qr_moe_layer* L, int T, MoeScratch* s) 
     s->shtiles = reinterpret_cast<int32_t*>(take(2 * 4));
     s->shperm = reinterpret_cast<int32_t*>(take((size_t)T * 4));
   }
+  s->hu = nullptr;
+  if (L->up_type & QR_GGML) s->hu = reinterpret_cast<float*>(take(P * (size_t)L->hidden * 4));
 }
 
 // ---------------------------------------------------------------------------
@@ -744,8 +751,39 @@ static hipError_t shared_expert(const qr_moe_layer* L, const float* xb, int T, c
   return gemv_f32_launch(QR_ORDER_SEQ, L->sh_gate_inp, xb, s.sgl, 1, dim, T, dim, 1, st);
 }
 
+// llama.cpp-layout experts (ggml K-quants, Q8_K activations): the routing,
+// then one GEMV per (token, slot) pair in pair mode -- up and gate of token
+// p / K through expert idx[p], the SwiGLU, down of hb row p -- and the
+// weighted sum in slot order (qro_moe_token's loop: each pair's output row
+// p, the identity as the combine's pair -> row map).
+static hipError_t moe_forward_ggml(const qr_moe_layer* L, float* x, const float* xb, int T,
+                                   int order, const MoeScratch& s, hipStream_t st) {
+  const int E = L->n_experts, K = L->n_used, P = T * K;
+  const int ut = (int)(L->up_type & ~(uint32_t)QR_GGML), dt = (int)(L->down_type & ~(uint32_t)QR_GGML);
+  const size_t su = qr_wrow_bytes(ut, L->dim) * (size_t)L->hidden;
+  const size_t sd = qr_wrow_bytes(dt, L->hidden) * (size_t)L->dim;
+  hipError_t e = moe_route_launch(L, xb, T, order, s.logits, nullptr, s.idx, s.wts, st);
+  if (e != hipSuccess) return e;
+  e = gemv_ggml_pairs_launch(ut, L->up, su, s.idx, E, K, xb, L->dim, s.hu, L->hidden, L->hidden,
+                             L->dim, P, st);
+  if (e != hipSuccess) return e;
+  e = gemv_ggml_pairs_launch(ut, L->gate, su, s.idx, E, K, xb, L->dim, s.hb, L->hidden, L->hidden,
+                             L->dim, P, st);
+  if (e != hipSuccess) return e;
+  const long n = (long)P * L->hidden;
+  hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s.hu, s.hb,
+                     n);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  e = gemv_ggml_pairs_launch(dt, L->down, sd, s.idx, E, 1, s.hb, L->hidden, s.y, L->dim, L->dim,
+                             L->hidden, P, st);
+  if (e != hipSuccess) return e;
+  if ((e = rows_dispatch_launch(P, 1, s.offsets, s.inv, s.tiles, st)) != hipSuccess) return e;
+  return combine_launch(x, s.y, s.inv, s.wts, T, K, L->dim, nullptr, nullptr, st);
+}
+
 hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, int T, int order,
                               const MoeScratch& s, hipStream_t st, int path) {
+  if (L->up_type & QR_GGML) return moe_forward_ggml(L, x, xb, T, order, s, st);
   const int E = L->n_experts, K = L->n_used, P = T * K;
   const bool sh = L->sh_hidden > 0;
   const size_t su = qr_wrow_bytes((int)L->up_type, L->dim) * (size_t)L->hidden;

@@ -654,6 +654,28 @@ static int check_layer(const qr_moe_layer* L, const char* who) {
 static int check_experts(const qr_moe_layer* L, const char* who) {
   const uint32_t ts[3] = {L->up_type, L->gate_type, L->down_type};
   const void* ps[3] = {L->up, L->gate, L->down};
+  const int ng = ((ts[0] & QR_GGML) != 0) + ((ts[1] & QR_GGML) != 0) + ((ts[2] & QR_GGML) != 0);
+  if (ng) {  // llama.cpp-layout experts: all three, on ggml's Q8_K dot
+    if (ng != 3 || L->up_type != L->gate_type)
+      return fail(QR_ERR_UNSUPPORTED, "%s: ggml experts need ggml up, gate and down (up = gate)",
+                  who);
+    if (!qr::gemv_ggml_ok((int)(L->up_type & ~(uint32_t)QR_GGML), L->dim, 1) ||
+        !qr::gemv_ggml_ok((int)(L->down_type & ~(uint32_t)QR_GGML), L->hidden, 1))
+      return fail(QR_ERR_UNSUPPORTED, "%s: ggml expert types %u / %u at dim %d, hidden %d", who,
+                  L->up_type, L->down_type, L->dim, L->hidden);
+    for (int i = 0; i < 3; i++) {
+      if (!ps[i]) return fail(QR_ERR_INVALID, "%s: null expert tensor", who);
+      if (!aligned(ps[i], 16))
+        return fail(QR_ERR_INVALID, "%s: expert tensors must be 16-byte aligned", who);
+    }
+    const size_t su = qr_row_bytes(L->up_type, L->dim) * (size_t)L->hidden;
+    const size_t sd = qr_row_bytes(L->down_type, L->hidden) * (size_t)L->dim;
+    if ((su & 15) || (sd & 15))
+      return fail(QR_ERR_UNSUPPORTED, "%s: expert slice not 16-byte aligned", who);
+    if (L->sh_hidden > 0)
+      return fail(QR_ERR_UNSUPPORTED, "%s: no shared expert beside ggml experts", who);
+    return QR_OK;
+  }
   for (int i = 0; i < 3; i++) {
     if (ts[i] == QR_T_F32 || !known_type(ts[i]))
       return fail(QR_ERR_UNSUPPORTED, "%s: expert type %u (quantized types only)", who, ts[i]);
@@ -689,6 +711,15 @@ int moe_check(const qr_moe_layer* L, const char* who) {
 }
 
 int gemv_check(uint32_t type, int order, const void* w, int n, int d, const char* who) {
+  if (type & QR_GGML) {
+    type &= ~(uint32_t)QR_GGML;
+    if (n <= 0 || d <= 0) return fail(QR_ERR_INVALID, "%s: weight shape %d x %d", who, n, d);
+    if (!gemv_ggml_ok((int)type, d, 1))
+      return fail(QR_ERR_UNSUPPORTED, "%s: ggml type %u at d=%d (Q4_K, Q5_K, Q6_K; not tiled)",
+                  who, type, d);
+    if (w && !aligned(w, 16)) return fail(QR_ERR_INVALID, "%s: weights must be 16-byte aligned", who);
+    return QR_OK;
+  }
   if (type & QR_TILED) {
     type &= ~(uint32_t)QR_TILED;
     if (n <= 0 || d <= 0) return fail(QR_ERR_INVALID, "%s: weight shape %d x %d", who, n, d);

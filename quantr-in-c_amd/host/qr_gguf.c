@@ -738,7 +738,38 @@ static int plan_model(const qr_gguf* g, qr_gguf_model* gm, copy_plan* p) {
     return QR_OK;
 }
 
+/* The file's K-quant tensors read in llama.cpp's layouts: their types carry
+ * QR_GGML (which no tiling plan accepts). */
+static void mark_ggml(uint32_t* type) {
+    if (*type == QR_TYPE_Q4_K || *type == QR_TYPE_Q5_K || *type == QR_TYPE_Q6_K) *type |= QR_GGML;
+}
+
+static void mark_ggml_model(qr_gguf_model* gm) {
+    qr_model* m = &gm->model;
+    int l;
+    mark_ggml(&m->tok_type);
+    mark_ggml(&m->wcls_type);
+    for (l = 0; l < m->n_layers; l++) {
+        qr_layer* y = &gm->layers[l];
+        mark_ggml(&y->wq_type);
+        mark_ggml(&y->wk_type);
+        mark_ggml(&y->wv_type);
+        mark_ggml(&y->wo_type);
+        mark_ggml(&y->moe.up_type);
+        mark_ggml(&y->moe.gate_type);
+        mark_ggml(&y->moe.down_type);
+        mark_ggml(&y->moe.sh_up_type);
+        mark_ggml(&y->moe.sh_gate_type);
+        mark_ggml(&y->moe.sh_down_type);
+    }
+}
+
 int qr_gguf_load(qr_ctx* ctx, const qr_gguf* g, int seq_len, qr_gguf_model** out) {
+    return qr_gguf_load_ex(ctx, g, seq_len, 0, out);
+}
+
+int qr_gguf_load_ex(qr_ctx* ctx, const qr_gguf* g, int seq_len, uint32_t flags,
+                    qr_gguf_model** out) {
     qr_gguf_model* gm;
     copy_plan plan = {NULL, 0, 0, 0};
     int L, i, rc, tied;
@@ -747,6 +778,7 @@ int qr_gguf_load(qr_ctx* ctx, const qr_gguf* g, int seq_len, qr_gguf_model** out
     if (!out) return QR_ERR_INVALID;
     *out = NULL;
     if (!ctx || !g) return QR_ERR_INVALID;
+    if (flags & ~QR_GGUF_GGML_KQUANTS) return gg_fail(QR_ERR_INVALID, "qr_gguf_load: unknown flags");
     gm = (qr_gguf_model*)calloc(1, sizeof(*gm));
     if (!gm) return QR_ERR_NOMEM;
     gm->ctx = ctx;
@@ -762,6 +794,7 @@ int qr_gguf_load(qr_ctx* ctx, const qr_gguf* g, int seq_len, qr_gguf_model** out
     }
     rc = qr_gguf_model_host(g, seq_len, &gm->model, gm->layers, L);
     if (rc != L) goto fail;
+    if (flags & QR_GGUF_GGML_KQUANTS) mark_ggml_model(gm);
     tied = gm->model.wcls == gm->model.tok_embd;
     rc = plan_model(g, gm, &plan);
     if (rc != QR_OK) {

@@ -17,8 +17,9 @@ HEADERS = [os.path.join(REPO_DIR, "include", "qr_hip.h"),
            os.path.join(REPO_DIR, "include", "qr_dropin.h")]
 
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 0, 8, 12, 13, 14
-TILED = 0x100  # OR'ed into a Q4_K / Q5_K type: the weights are in the tiled layout
+TILED = 0x100  # OR'ed into a Q4_K / Q5_K / Q6_K / Q8_0 type: the weights are in the tiled layout
 GGML = 0x200   # OR'ed into a Q4_K / Q5_K / Q6_K type: llama.cpp's block layout, Q8_K activations
+GGUF_GGML_KQUANTS = 1  # qr_gguf_load_ex: the file's K-quant tensors in llama.cpp's layouts
 ORDER_SEQ, ORDER_AVX2, ORDER_AVX512 = 0, 1, 2
 
 _vp = C.c_void_p
@@ -143,6 +144,7 @@ _SIGS = {
     "qr_gguf_expert_host": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(_vp), C.POINTER(_vp),
                                       C.POINTER(_vp)]),
     "qr_gguf_load": (C.c_int, [_vp, _vp, C.c_int, C.POINTER(_vp)]),
+    "qr_gguf_load_ex": (C.c_int, [_vp, _vp, C.c_int, C.c_uint32, C.POINTER(_vp)]),
     "qr_gguf_model_get": (C.POINTER(Model), [_vp]),
     "qr_gguf_model_free": (C.c_int, [_vp]),
     # drop-ins (include/qr_dropin.h)
@@ -501,9 +503,10 @@ class Gguf:
             raise QrError("qr_gguf_expert_host failed")
         return up.value, down.value, gate.value
 
-    def load(self, dev, seq_len):
-        """A GgufModel: the model uploaded to dev's GPU."""
-        return GgufModel(dev, self, seq_len)
+    def load(self, dev, seq_len, ggml_kquants=False):
+        """A GgufModel: the model uploaded to dev's GPU (ggml_kquants: its
+        K-quant tensors in llama.cpp's layouts, QR_GGUF_GGML_KQUANTS)."""
+        return GgufModel(dev, self, seq_len, GGUF_GGML_KQUANTS if ggml_kquants else 0)
 
     def close(self):
         if self.h is not None:
@@ -521,10 +524,11 @@ class GgufModel:
     """qr_gguf_load: a qr_model of device pointers in one device allocation
     this object owns (the Gguf may be closed after loading)."""
 
-    def __init__(self, dev, g, seq_len):
+    def __init__(self, dev, g, seq_len, flags=0):
         self.dev, self.g = dev, g
         h = _vp()
-        dev._check(dev.lib.qr_gguf_load(dev.ctx, _vp(g.h), seq_len, C.byref(h)), "qr_gguf_load")
+        dev._check(dev.lib.qr_gguf_load_ex(dev.ctx, _vp(g.h), seq_len, flags, C.byref(h)),
+                   "qr_gguf_load")
         self.h = h.value
         mp = dev.lib.qr_gguf_model_get(_vp(self.h))
         self.model = mp.contents
