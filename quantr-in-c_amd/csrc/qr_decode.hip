@@ -28,6 +28,7 @@
 #include "qr_common.h"
 #include "qr_ggml_elem.h"
 #include "qr_internal.h"
+#include "qr_norm.h"
 
 namespace qr {
 
@@ -151,11 +152,7 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ x,
       }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-      float ss = seq_sum_lds_long(sq, n);
-      ss = ss / (float)n + 1e-5f;
-      scale_s = 1.0f / sqrtf(ss);
-    }
+    if (threadIdx.x == 0) scale_s = rms_scale(seq_sum_lds_long(sq, n), n);
     __syncthreads();
     const float scale = scale_s;
 #pragma unroll
@@ -180,11 +177,7 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ x,
       sq[i] = xi * xi;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-      float ss = seq_sum_lds_long(sq, n);
-      ss = ss / (float)n + 1e-5f;
-      scale_s = 1.0f / sqrtf(ss);
-    }
+    if (threadIdx.x == 0) scale_s = rms_scale(seq_sum_lds_long(sq, n), n);
     __syncthreads();
     const float scale = scale_s;
     for (int i = threadIdx.x; i < n; i += blockDim.x) o[i] = w[i] * (x[i] * scale);
@@ -1156,6 +1149,12 @@ struct qr_decoder {
   uint8_t* pmoe = nullptr;
   const float* prec_src = nullptr;  // the rows prec holds records of (nullptr: none)
   int prec_perm = 0;
+  // per layer: the v matrix in the Q6_K / Q8_0 tiled layout when the decode
+  // step runs q / k and v in one normalising launch (k_gemv_norm2), else
+  // null; row-major v matrices are tiled into wvt (owned) at creation
+  std::vector<const void*> wv_tiled;
+  std::vector<int> wv_tiled_type;
+  uint8_t* wvt = nullptr;
 };
 
 namespace {
@@ -1192,16 +1191,35 @@ KvView kv_view(const qr_decoder* d, int layer, bool values) {
 // go through the build's KernelOps.matmul order, quantized ones through the
 // fused GEMV with the build's Q8_0 dot order, llama.cpp-layout K-quants
 // through ggml's Q8_K dot.
+// R (quantized weights only): y = R + W x, the residual add in the GEMV's
+// store (y may be R).
 hipError_t matmul_q_dev(const void* w, uint32_t type, int order, const float* x, float* y, int n,
-                        int dd, hipStream_t s) {
-  if (type == QR_T_F32)
+                        int dd, hipStream_t s, const float* R = nullptr) {
+  if (type == QR_T_F32) {
+    if (R) return hipErrorInvalidValue;
     return gemv_f32_launch(order, static_cast<const float*>(w), x, y, n, dd, 1, dd, n, s);
+  }
   if (type & QR_GGML)
-    return gemv_ggml_launch((int)(type & ~(uint32_t)QR_GGML), w, x, y, n, dd, 1, dd, n, s);
+    return gemv_ggml_launch((int)(type & ~(uint32_t)QR_GGML), w, x, y, n, dd, 1, dd, n, s, R);
   if (type & QR_TILED)
     return gemv_tiled_launch((int)(type & ~(uint32_t)QR_TILED), w, x, y, n, dd, 1, dd, n, s,
-                             order);
-  return gemv_launch((int)type, order, w, x, y, n, dd, 1, dd, n, nullptr, nullptr, s);
+                             order, R);
+  return gemv_launch((int)type, order, w, x, y, n, dd, 1, dd, n, nullptr, nullptr, s, R);
+}
+
+// x += W v in the GEMV's store where the type allows it (every quantized
+// layout): true; else the caller adds W v to x itself.
+inline bool residual_gemv(uint32_t type) { return type != QR_T_F32; }
+
+// The attention RMSNorm formed inside the q (and k) GEMV's launch
+// (qr_norm.h): a tiled Q4_K / Q5_K wq, aligned norm weights and residual.
+inline bool norm_in_q(const qr_decoder* d, const qr_layer& L) {
+  if (!(L.wq_type & QR_TILED) || (L.wq_type & QR_GGML)) return false;
+  const int base = (int)(L.wq_type & ~(uint32_t)QR_TILED);
+  return gemv_tiled_norm_ok(base, d->dim) &&
+         (reinterpret_cast<uintptr_t>(L.rms_att) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(d->x) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(d->xb) & 15) == 0;
 }
 
 // wq and wk as one matrix of qd + kvd rows: the same type and width, wk's
@@ -1259,19 +1277,42 @@ hipError_t enqueue_step(qr_decoder* d, float* logits, float* xout, hipStream_t s
                      d->st, dim, d->x);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const float inv_sqrt = 1.0f / sqrtf((float)d->hd);
-  const float* pend = nullptr;  // a dense FFN's output, added to x by the next norm
+  // a layer output not yet added to x (an fp32 down or wo matrix, whose
+  // GEMV has no residual store): the next norm adds it
+  const float* pend = nullptr;
   for (int l = 0; l < d->nl; l++) {
     const qr_layer& L = d->layers[l];
-    if ((e = rmsnorm_launch(d->x, pend, L.rms_att, dim, d->xb, s))) return e;
-    pend = nullptr;
-    if (qk_stacked(d, L)) {
-      if ((e = matmul_q_dev(L.wq, L.wq_type, d->order, d->xb, d->q, d->qd + d->kvd, dim, s)))
+    const bool stacked = qk_stacked(d, L);
+    const bool vdone = !pend && stacked && d->wv_tiled[l] && norm_in_q(d, L);
+    if (vdone) {
+      // the norm, q / k and v in one launch, xb stored for the rest
+      const int base = (int)(L.wq_type & ~(uint32_t)QR_TILED);
+      if ((e = gemv_norm2_launch(base, L.wq, d->q, d->qd + d->kvd, d->wv_tiled_type[l],
+                                 d->wv_tiled[l], d->v, d->kvd, d->x, L.rms_att, d->xb, dim, s)))
+        return e;
+    } else if (!pend && norm_in_q(d, L)) {
+      // the norm inside the q (and stacked k) launch, xb stored for the rest
+      const int base = (int)(L.wq_type & ~(uint32_t)QR_TILED);
+      if ((e = gemv_tiled_norm_launch(base, L.wq, d->x, L.rms_att, d->xb, d->q,
+                                      stacked ? d->qd + d->kvd : d->qd, dim, s)))
+        return e;
+      if (!stacked &&
+          (e = matmul_q_dev(L.wk, L.wk_type, d->order, d->xb, d->k, d->kvd, dim, s)))
         return e;
     } else {
-      if ((e = matmul_q_dev(L.wq, L.wq_type, d->order, d->xb, d->q, d->qd, dim, s))) return e;
-      if ((e = matmul_q_dev(L.wk, L.wk_type, d->order, d->xb, d->k, d->kvd, dim, s))) return e;
+      if ((e = rmsnorm_launch(d->x, pend, L.rms_att, dim, d->xb, s))) return e;
+      pend = nullptr;
+      if (stacked) {
+        if ((e = matmul_q_dev(L.wq, L.wq_type, d->order, d->xb, d->q, d->qd + d->kvd, dim, s)))
+          return e;
+      } else {
+        if ((e = matmul_q_dev(L.wq, L.wq_type, d->order, d->xb, d->q, d->qd, dim, s))) return e;
+        if ((e = matmul_q_dev(L.wk, L.wk_type, d->order, d->xb, d->k, d->kvd, dim, s))) return e;
+      }
     }
-    if ((e = matmul_q_dev(L.wv, L.wv_type, d->order, d->xb, d->v, d->kvd, dim, s))) return e;
+    if (!vdone &&
+        (e = matmul_q_dev(L.wv, L.wv_type, d->order, d->xb, d->v, d->kvd, dim, s)))
+      return e;
     const KvView K = kv_view(d, l, false), V = kv_view(d, l, true);
     // RoPE, the position's K / V rows and the scores in one launch
     const RopeArgs R{d->rope, d->k, d->v, const_cast<uint8_t*>(V.base), d->qd};
@@ -1281,25 +1322,46 @@ hipError_t enqueue_step(qr_decoder* d, float* logits, float* xout, hipStream_t s
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = sv_launch(d->att, d->cap, V, d->st, 0, d->cap, d->nh, d->kv_mul, d->hd, d->ao, s)))
       return e;
-    if ((e = matmul_q_dev(L.wo, L.wo_type, d->order, d->ao, d->xb2, dim, d->qd, s))) return e;
-    if ((e = rmsnorm_launch(d->x, d->xb2, L.rms_ffn, dim, d->xb, s))) return e;
+    // x += wo . ao (src/runtime.c:196-198), in the GEMV's store where it can
+    const float* fadd = nullptr;
+    if (residual_gemv(L.wo_type)) {
+      if ((e = matmul_q_dev(L.wo, L.wo_type, d->order, d->ao, d->x, dim, d->qd, s, d->x)))
+        return e;
+    } else {
+      if ((e = matmul_q_dev(L.wo, L.wo_type, d->order, d->ao, d->xb2, dim, d->qd, s))) return e;
+      fadd = d->xb2;
+    }
     if (is_dense(L)) {
       const qr_moe_layer& M = L.moe;
       float* u = reinterpret_cast<float*>(d->moe_base);
       float* g = u + M.hidden;
       float* y = g + M.hidden;
+      if ((e = rmsnorm_launch(d->x, fadd, L.rms_ffn, dim, d->xb, s))) return e;
       if ((e = matmul_q_dev(M.up, M.up_type, d->order, d->xb, u, M.hidden, dim, s))) return e;
       if ((e = matmul_q_dev(M.gate, M.gate_type, d->order, d->xb, g, M.hidden, dim, s))) return e;
       hipLaunchKernelGGL(k_swiglu, dim3((M.hidden + 255) / 256), dim3(256), 0, s, u, g,
                          (long)M.hidden);
       if ((e = hipGetLastError()) != hipSuccess) return e;
-      if ((e = matmul_q_dev(M.down, M.down_type, d->order, g, y, dim, M.hidden, s))) return e;
-      pend = y;
+      if (residual_gemv(M.down_type)) {  // x += w2 . hb (src/runtime.c:282-284)
+        if ((e = matmul_q_dev(M.down, M.down_type, d->order, g, d->x, dim, M.hidden, s, d->x)))
+          return e;
+      } else {
+        if ((e = matmul_q_dev(M.down, M.down_type, d->order, g, y, dim, M.hidden, s))) return e;
+        pend = y;
+      }
       continue;
     }
     MoeScratch ms;
     moe_scratch_carve(d->moe_base, &L.moe, 1, &ms);
-    if ((e = moe_forward_launch(&L.moe, d->x, d->xb, 1, d->order, ms, s))) return e;
+    if (!fadd && moe_t1_norm_ok(&L.moe, d->x, d->xb, L.rms_ffn, d->order)) {
+      // the FFN norm inside the router's launch
+      if ((e = moe_forward_launch(&L.moe, d->x, d->xb, 1, d->order, ms, s, QR_MOE_PATH_AUTO,
+                                  L.rms_ffn)))
+        return e;
+    } else {
+      if ((e = rmsnorm_launch(d->x, fadd, L.rms_ffn, dim, d->xb, s))) return e;
+      if ((e = moe_forward_launch(&L.moe, d->x, d->xb, 1, d->order, ms, s))) return e;
+    }
   }
   if ((e = rmsnorm_launch(d->x, pend, d->rms_final, dim, d->xb, s))) return e;
   if ((e = matmul_q_dev(d->wcls, d->wcls_type, d->order, d->xb, logits, d->vocab, dim, s)))
@@ -1464,6 +1526,45 @@ void drop_graph(qr_decoder* d) {
   if (d->graph) (void)hipGraphDestroy(d->graph);
   d->exec = nullptr;
   d->graph = nullptr;
+}
+
+// Which layers run q / k and v in one normalising launch (k_gemv_norm2), and
+// their v matrices in the Q6_K / Q8_0 tiled layout: the caller's when it
+// passes them tiled, else a copy tiled here (the decode step reads it; the
+// prompt's row products keep reading the caller's row-major matrix).
+hipError_t plan_wv_tiled(qr_decoder* d, hipStream_t s) {
+  d->wv_tiled.assign(d->nl, nullptr);
+  d->wv_tiled_type.assign(d->nl, 0);
+  std::vector<size_t> off(d->nl, (size_t)-1);
+  size_t total = 0;
+  for (int l = 0; l < d->nl; l++) {
+    const qr_layer& L = d->layers[l];
+    if (!qk_stacked(d, L) || !norm_in_q(d, L)) continue;
+    const int qb = (int)(L.wq_type & ~(uint32_t)QR_TILED);
+    const uint32_t vt = L.wv_type;
+    const int vb = (int)(vt & ~(uint32_t)QR_TILED);
+    if ((vt & QR_GGML) || (vb != QR_T_Q6_K && vb != QR_T_Q8_0)) continue;
+    if (vb == QR_T_Q8_0 && d->order != QR_ORDER_SEQ) continue;  // tiles take the C99 order
+    if (!gemv_norm2_ok(qb, vb, d->dim)) continue;
+    d->wv_tiled_type[l] = vb;
+    if (vt & QR_TILED) {
+      d->wv_tiled[l] = L.wv;
+    } else {
+      off[l] = total;
+      total += (qr_wrow_bytes(vb, d->dim) * (size_t)d->kvd + 255) & ~(size_t)255;
+    }
+  }
+  if (!total) return hipSuccess;
+  hipError_t e = hipMalloc((void**)&d->wvt, total);
+  if (e != hipSuccess) return e;
+  for (int l = 0; l < d->nl; l++) {
+    if (off[l] == (size_t)-1) continue;
+    uint8_t* dst = d->wvt + off[l];
+    e = tile_pack_launch(d->wv_tiled_type[l], d->layers[l].wv, dst, d->kvd, d->dim, false, s);
+    if (e != hipSuccess) return e;
+    d->wv_tiled[l] = dst;
+  }
+  return hipSuccess;
 }
 
 int check_layer_weights(const qr_model* m, int l, int order) {
@@ -1750,6 +1851,7 @@ int qr_decoder_create(qr_ctx* c, const qr_model* m, int kv_type, int order, int 
   e = hipMemcpyAsync(d->ptab, pt.data(), pt.size() * 4, hipMemcpyHostToDevice, s);
   if (e == hipSuccess)
     e = hipMemcpyAsync(d->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = plan_wv_tiled(d, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) {
     qr_decoder_destroy(d);
@@ -1768,6 +1870,7 @@ int qr_decoder_destroy(qr_decoder* d) {
   if (d->vc) (void)hipFree(d->vc);
   if (d->mem) (void)hipFree(d->mem);
   if (d->pmem) (void)hipFree(d->pmem);
+  if (d->wvt) (void)hipFree(d->wvt);
   delete d;
   return QR_OK;
 }

@@ -519,6 +519,13 @@ struct GemvArgs {
   const int32_t* eidx;
   size_t eslice;
   int xk, E;
+  // residual: Y = R + W X (one token; R may be Y itself); null: Y = W X
+  const float* R;
+  // normalising start-up of the tiled GEMV (qr_norm.h, one token): X is
+  // the residual stream, nw the norm's weights, and workgroup 0 also stores
+  // the normalised vector at nxb when given
+  const float* nw;
+  float* nxb;
 };
 
 }  // namespace qr

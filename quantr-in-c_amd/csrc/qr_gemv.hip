@@ -101,8 +101,9 @@ __global__ __launch_bounds__(kWg) void k_gemv(GemvArgs g) {
 
   for (int i = threadIdx.x; i < R * NT; i += blockDim.x) {
     const int t = i / R, row = i - t * R;
-    g.Y[(size_t)t * g.ystride + r0 + row] = row_value<TYPE, Q8O>(
-        terms + ((size_t)t * g.rows_per_wg + row) * SL * tstride, tstride, U);
+    const float v = row_value<TYPE, Q8O>(terms + ((size_t)t * g.rows_per_wg + row) * SL * tstride,
+                                         tstride, U);
+    g.Y[(size_t)t * g.ystride + r0 + row] = g.R ? g.R[r0 + row] + v : v;
   }
 }
 
@@ -168,14 +169,14 @@ __global__ __launch_bounds__(64 * kStreamWaves) void k_gemv_stream(GemvArgs g) {
           float sum = 0.0f;
 #pragma unroll
           for (int j = 0; j < 8; j++) sum += v[j];
-          g.Y[(size_t)t * g.ystride + r0 + row] = sum;
+          g.Y[(size_t)t * g.ystride + r0 + row] = g.R ? g.R[r0 + row] + sum : sum;
         }
       }
     } else {
       for (int i = lane; i < RWt * NT; i += 64) {
         const int t = i / RWt, row = i - t * RWt;
-        g.Y[(size_t)t * g.ystride + r0 + row] =
-            row_sum_seq(terms + (t * sh.RW + row) * sh.TS, sh.U);
+        const float v = row_sum_seq(terms + (t * sh.RW + row) * sh.TS, sh.U);
+        g.Y[(size_t)t * g.ystride + r0 + row] = g.R ? g.R[r0 + row] + v : v;
       }
     }
     if (next >= ntiles) break;
@@ -304,7 +305,7 @@ __global__ __launch_bounds__(64 * kBlkWaves) void k_gemv_blk(GemvArgs g) {
     blk_chain<NT>(terms, b, nb, y);
     if (live && b == nb - 1) {
 #pragma unroll
-      for (int t = 0; t < NT; t++) g.Y[(size_t)t * g.ystride + row] = y[t];
+      for (int t = 0; t < NT; t++) g.Y[(size_t)t * g.ystride + row] = g.R ? g.R[row] + y[t] : y[t];
     }
     if (tile >= ntiles) break;
   }
@@ -631,8 +632,11 @@ static hipError_t launch_tiled_type(GemvArgs a, int nt, hipStream_t st) {
 }
 
 hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, int n, int d,
-                             int nt, int xstride, int ystride, hipStream_t st, int q8o) {
+                             int nt, int xstride, int ystride, hipStream_t st, int q8o,
+                             const float* R) {
+  if (R && nt != 1) return hipErrorInvalidValue;
   GemvArgs a{};
+  a.R = R;
   a.W = static_cast<const uint8_t*>(W);
   a.X = X;
   a.Y = Y;
@@ -661,6 +665,129 @@ hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, 
   if (type == QR_T_Q4_K) return launch_tiled_type<QR_T_Q4_K>(a, nt, st);
   if (type == QR_T_Q5_K) return launch_tiled_type<QR_T_Q5_K>(a, nt, st);
   return hipErrorInvalidValue;
+}
+
+// The normalising start-up (kProNorm): LDS of the one-token kernel plus the
+// normalised vector and its scale.
+static size_t tiled_norm_lds(int type, int d, int nw) {
+  return tiled_lds_bytes(type, d, 1, nw) + (size_t)d * 4 + 16;
+}
+
+bool gemv_tiled_norm_ok(int type, int d) {
+  return (type == QR_T_Q4_K || type == QR_T_Q5_K) && d % 256 == 0 && (d >> 8) <= 64 &&
+         d <= kNormFuseMax && tiled_norm_lds(type, d, 4) <= kLdsMax;
+}
+
+template <int TYPE>
+static hipError_t launch_tiled_norm(const GemvArgs& a, hipStream_t st) {
+  const TiledGeom g = tiled_geom(TYPE, a.n, a.d);
+  if (g.ntiles <= 0) return hipSuccess;
+  const int cus = device_cus();
+  const size_t lds8 = tiled_norm_lds(TYPE, a.d, 8);
+  const int nw = (2 * lds8 <= kLdsMax && (g.ntiles + 7) / 8 >= cus) ? 8 : 4;
+  const size_t lds = tiled_norm_lds(TYPE, a.d, nw);
+  int per_cu = (int)(kLdsMax / lds);
+  per_cu = per_cu < 1 ? 1 : (per_cu > 4 ? 4 : per_cu);
+  // every workgroup is resident at once (each forms the same chain; a second
+  // wave of workgroups would form it again after the first)
+  const int want = (g.ntiles + nw - 1) / nw;
+  const int grid = want < cus * per_cu ? want : cus * per_cu;
+  if (nw == 8) return launch_tiled_k<TYPE, 1, 8, kProNorm>(a, grid, lds, st);
+  return launch_tiled_k<TYPE, 1, 4, kProNorm>(a, grid, lds, st);
+}
+
+// Two matrices after one normalisation (k_gemv_norm2): a tiled Q4_K / Q5_K
+// matrix A and a tiled Q6_K / Q8_0 matrix B, four waves per workgroup.
+static size_t norm2_lds(int ta, int tb, int d) {
+  const size_t la = tiled_norm_lds(ta, d, 4);
+  const size_t lb = sq_lds_bytes(tb, d, 1, 4) + (size_t)d * 4 + 16;
+  return la > lb ? la : lb;
+}
+
+bool gemv_norm2_ok(int ta, int tb, int d) {
+  return gemv_tiled_norm_ok(ta, d) && (tb == QR_T_Q6_K || tb == QR_T_Q8_0) && sq_shape_ok(tb, d) &&
+         norm2_lds(ta, tb, d) <= kLdsMax;
+}
+
+template <int TA, int TB>
+static hipError_t launch_norm2(const GemvArgs& a, const GemvArgs& b, hipStream_t st) {
+  static std::atomic<bool> opted[64];
+  const size_t lds = norm2_lds(TA, TB, a.d);
+  if (lds > 64 * 1024) {
+    hipError_t e = lds_opt_in((const void*)k_gemv_norm2<TA, TB, 4>, opted);
+    if (e != hipSuccess) return e;
+  }
+  // every workgroup resident at once (each forms the chain): the two roles
+  // share the CUs in proportion to their tiles
+  int per_cu = (int)(kLdsMax / lds);
+  per_cu = per_cu < 1 ? 1 : (per_cu > 4 ? 4 : per_cu);
+  const int cap = device_cus() * per_cu;
+  int ga = (a.t_ntiles + 3) / 4, gb = (b.t_ntiles + 3) / 4;
+  if (ga + gb > cap) {
+    const int ga2 = (int)((long)cap * ga / (ga + gb));
+    gb = cap - (ga2 < 1 ? 1 : ga2);
+    ga = ga2 < 1 ? 1 : ga2;
+    if (gb < 1) return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL((k_gemv_norm2<TA, TB, 4>), dim3(ga + gb), dim3(256), lds, st, a, b, ga);
+  return hipGetLastError();
+}
+
+hipError_t gemv_norm2_launch(int ta, const void* Wa, float* Ya, int na, int tb, const void* Wb,
+                             float* Yb, int nb_rows, const float* x, const float* nw, float* xb,
+                             int d, hipStream_t st) {
+  if (!gemv_norm2_ok(ta, tb, d) || na <= 0 || nb_rows <= 0) return hipErrorInvalidValue;
+  GemvArgs a{}, b{};
+  a.W = static_cast<const uint8_t*>(Wa);
+  b.W = static_cast<const uint8_t*>(Wb);
+  a.X = b.X = x;
+  a.nw = b.nw = nw;
+  a.nxb = xb;  // the q / k role's workgroup 0 stores the normalised vector
+  a.Y = Ya;
+  b.Y = Yb;
+  a.n = na;
+  b.n = nb_rows;
+  a.d = b.d = d;
+  a.xstride = b.xstride = d;
+  a.ystride = na;
+  b.ystride = nb_rows;
+  const TiledGeom g = tiled_geom(ta, na, d);
+  a.t_nb = g.nb;
+  a.t_rb = g.RB;
+  a.t_ntiles = g.ntiles;
+  a.t_tile_bytes = g.tile_bytes;
+  const SqGeom h = sq_geom(tb, nb_rows, d);
+  b.t_nb = h.nb;
+  b.t_rb = h.RB;
+  b.t_ntiles = h.ntiles;
+  b.t_tile_bytes = h.tile_bytes;
+  if (ta == QR_T_Q4_K)
+    return tb == QR_T_Q6_K ? launch_norm2<QR_T_Q4_K, QR_T_Q6_K>(a, b, st)
+                           : launch_norm2<QR_T_Q4_K, QR_T_Q8_0>(a, b, st);
+  return tb == QR_T_Q6_K ? launch_norm2<QR_T_Q5_K, QR_T_Q6_K>(a, b, st)
+                         : launch_norm2<QR_T_Q5_K, QR_T_Q8_0>(a, b, st);
+}
+
+hipError_t gemv_tiled_norm_launch(int type, const void* W, const float* x, const float* nw,
+                                  float* xb, float* Y, int n, int d, hipStream_t st) {
+  if (!gemv_tiled_norm_ok(type, d)) return hipErrorInvalidValue;
+  GemvArgs a{};
+  a.W = static_cast<const uint8_t*>(W);
+  a.X = x;
+  a.Y = Y;
+  a.n = n;
+  a.d = d;
+  a.xstride = d;
+  a.ystride = n;
+  a.nw = nw;
+  a.nxb = xb;
+  const TiledGeom g = tiled_geom(type, n, d);
+  a.t_nb = g.nb;
+  a.t_rb = g.RB;
+  a.t_ntiles = g.ntiles;
+  a.t_tile_bytes = g.tile_bytes;
+  if (type == QR_T_Q4_K) return launch_tiled_norm<QR_T_Q4_K>(a, st);
+  return launch_tiled_norm<QR_T_Q5_K>(a, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -728,8 +855,10 @@ static hipError_t launch_ggml_type(GemvArgs a, int nt, hipStream_t st) {
 }
 
 hipError_t gemv_ggml_launch(int type, const void* W, const float* X, float* Y, int n, int d, int nt,
-                            int xstride, int ystride, hipStream_t st) {
+                            int xstride, int ystride, hipStream_t st, const float* R) {
+  if (R && nt != 1) return hipErrorInvalidValue;
   GemvArgs a{};
+  a.R = R;
   a.W = static_cast<const uint8_t*>(W);
   a.X = X;
   a.Y = Y;
@@ -829,8 +958,10 @@ hipError_t tile_pack_launch(int type, const void* src, void* dst, int n, int d, 
 
 hipError_t gemv_launch(int type, int q8o, const void* W, const float* X, float* Y, int n, int d,
                        int nt, int xstride, int ystride, int32_t* acc, int32_t* accb,
-                       hipStream_t st) {
+                       hipStream_t st, const float* R) {
+  if (R && nt != 1) return hipErrorInvalidValue;
   GemvArgs a{};
+  a.R = R;
   a.W = static_cast<const uint8_t*>(W);
   a.X = X;
   a.Y = Y;

@@ -345,7 +345,7 @@ __global__ __launch_bounds__(256) void k_gemv_ggml(GemvArgs g) {
         float y = F[t];
 #pragma unroll
         for (int l = 0; l < 8; l++) y += S[t][l];
-        g.Y[(size_t)t * g.ystride + row] = y;
+        g.Y[(size_t)t * g.ystride + row] = g.R ? g.R[row] + y : y;
       }
     }
     if (tile >= ntiles) break;

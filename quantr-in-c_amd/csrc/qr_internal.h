@@ -35,22 +35,38 @@ int device_cus();
 // per device; done[] is the caller's per-device flag array of 64 entries).
 hipError_t lds_opt_in(const void* fn, std::atomic<bool>* done);
 int gemv_rows_per_wg(int type, int q8o, int n, int d, int nt);
+// R (one token only): Y = R + W X, the residual add of src/runtime.c:196-198
+// and 282-284 in the GEMV's store (R may be Y).
 hipError_t gemv_launch(int type, int q8o, const void* W, const float* X, float* Y, int n, int d,
                        int nt, int xstride, int ystride, int32_t* acc, int32_t* accb,
-                       hipStream_t st);
+                       hipStream_t st, const float* R = nullptr);
 // Tiled layout (qr_tiled.h, qr_tiled_sq.h): type is the base type (QR_T_Q4_K /
 // QR_T_Q5_K / QR_T_Q6_K / QR_T_Q8_0).
 // Q6_K / Q8_0 tiles (qr_tiled_sq.h) too; Q8_0 in the sequential dot order
 // only (q8o, kQ8Seq = 0).
 bool gemv_tiled_ok(int type, int d, int nt, int q8o = 0);
 hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, int n, int d,
-                             int nt, int xstride, int ystride, hipStream_t st, int q8o = 0);
+                             int nt, int xstride, int ystride, hipStream_t st, int q8o = 0,
+                             const float* R = nullptr);
+// One token of a tiled Q4_K / Q5_K matrix against rmsnorm_ref(x, nw) formed
+// inside the launch (qr_norm.h); xb (optional) receives the normalised
+// vector.  d <= kNormFuseMax.
+bool gemv_tiled_norm_ok(int type, int d);
+hipError_t gemv_tiled_norm_launch(int type, const void* W, const float* x, const float* nw,
+                                  float* xb, float* Y, int n, int d, hipStream_t st);
+// The same normalisation feeding two matrices in one launch: tiled Q4_K /
+// Q5_K A (na rows into Ya; xb from its workgroup 0) and tiled Q6_K / Q8_0 B
+// (nb rows into Yb; Q8_0 in the sequential dot order).
+bool gemv_norm2_ok(int ta, int tb, int d);
+hipError_t gemv_norm2_launch(int ta, const void* Wa, float* Ya, int na, int tb, const void* Wb,
+                             float* Yb, int nb, const float* x, const float* nw, float* xb, int d,
+                             hipStream_t st);
 hipError_t tile_pack_launch(int type, const void* src, void* dst, int n, int d, bool reverse,
                             hipStream_t st);
 // llama.cpp / ggml K-quants (qr_ggml.h): type is 12 / 13 / 14 (Q4_K / Q5_K / Q6_K).
 bool gemv_ggml_ok(int type, int d, int nt);
 hipError_t gemv_ggml_launch(int type, const void* W, const float* X, float* Y, int n, int d, int nt,
-                            int xstride, int ystride, hipStream_t st);
+                            int xstride, int ystride, hipStream_t st, const float* R = nullptr);
 hipError_t quantize_q8k_launch(const float* x, void* y, long nblocks, hipStream_t st);
 hipError_t gemv_ggml_pairs_launch(int type, const void* W, size_t eslice, const int32_t* eidx,
                                   int E, int xk, const float* X, int xstride, float* Y,
@@ -97,8 +113,14 @@ hipError_t moe_dispatch_launch(const int32_t* idx, int T, int K, int E, int tile
                                int32_t* offsets, int32_t* tiles, int32_t* perm, int32_t* inv,
                                hipStream_t st);
 // path: QR_MOE_PATH_* (include/qr_hip.h); AUTO picks by the pairs per expert.
+// norm_w (one token, where moe_t1_norm_ok): xb is written, not read -- the
+// router's launch forms xb = rmsnorm_ref(x, norm_w) (src/kernels.c:170-180)
+// before the layer uses it.
+bool moe_t1_norm_ok(const qr_moe_layer* L, const float* x, const float* xb, const float* nw,
+                    int order);
 hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, int T, int order,
-                              const MoeScratch& s, hipStream_t st, int path = QR_MOE_PATH_AUTO);
+                              const MoeScratch& s, hipStream_t st, int path = QR_MOE_PATH_AUTO,
+                              const float* norm_w = nullptr);
 hipError_t softmax_launch(float* x, int rows, int n, hipStream_t st);
 // qr_decode.hip: a single-"expert" dispatch of T rows for the grouped MFMA
 // product (offsets {0, T}, the identity permutation, tiles {0, ceil(T / tile)}).
@@ -107,11 +129,15 @@ hipError_t rows_dispatch_launch(int T, int tile, int32_t* off, int32_t* perm, in
 
 // qr_moe_t1.hip
 bool router1_ok(int dim);
+bool router1_norm_ok(int dim);
 // Router logits of T tokens (grid E x T), and with W2 the sequential-order dot
 // of the one row W2 with each token into out2[t] (E = 0: that dot alone).
+// With nw (one token): xb is the residual x, normalised inside the launch
+// (rmsnorm_ref with weights nw), the normalised vector stored at xb_out.
 hipError_t router1_launch(int order, const float* W, const float* xb, int E, int d, float* logits,
                           hipStream_t st, int T = 1, const float* W2 = nullptr,
-                          float* out2 = nullptr);
+                          float* out2 = nullptr, const float* nw = nullptr,
+                          float* xb_out = nullptr);
 bool gateup1_ok(int type, int dim, int E, int K);
 // With sh_up / sh_gate (the shared expert's rows, of the routed up type and
 // width), its hb = silu(sh_up . xb) * (sh_gate . xb) into hbs as well.

@@ -781,8 +781,25 @@ static hipError_t moe_forward_ggml(const qr_moe_layer* L, float* x, const float*
   return combine_launch(x, s.y, s.inv, s.wts, T, K, L->dim, nullptr, nullptr, st);
 }
 
+// The one-token path of three launches (router, gate/up, down + combine).
+static bool t1_path(const qr_moe_layer* L, const float* xb, int order) {
+  const bool q8_lanes = order != QR_ORDER_SEQ &&
+                        (L->up_type == QR_T_Q8_0 || L->down_type == QR_T_Q8_0);
+  return !q8_lanes && !(L->up_type & QR_GGML) && router1_ok(L->dim) &&
+         gateup1_ok((int)L->up_type, L->dim, L->n_experts, L->n_used) &&
+         L->up_type == L->gate_type &&
+         down1v2_ok((int)L->down_type, L->n_used, L->dim, L->hidden) && al16(L->router) &&
+         al16(xb);
+}
+
+bool moe_t1_norm_ok(const qr_moe_layer* L, const float* x, const float* xb, const float* nw,
+                    int order) {
+  return t1_path(L, xb, order) && router1_norm_ok(L->dim) && al16(x) && al16(nw);
+}
+
 hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, int T, int order,
-                              const MoeScratch& s, hipStream_t st, int path) {
+                              const MoeScratch& s, hipStream_t st, int path, const float* norm_w) {
+  if (norm_w && !(T == 1 && moe_t1_norm_ok(L, x, xb, norm_w, order))) return hipErrorInvalidValue;
   if (L->up_type & QR_GGML) return moe_forward_ggml(L, x, xb, T, order, s, st);
   const int E = L->n_experts, K = L->n_used, P = T * K;
   const bool sh = L->sh_hidden > 0;
@@ -798,15 +815,14 @@ hipError_t moe_forward_launch(const qr_moe_layer* L, float* x, const float* xb, 
                         (L->up_type == QR_T_Q8_0 || L->down_type == QR_T_Q8_0);
 
   // One token: logits, then gate/up with the routing done in every wave, then
-  // down + combine (qr_moe_t1.hip): three launches, no routing kernel.
-  if (!q8_lanes && T == 1 && router1_ok(L->dim) && gateup1_ok((int)L->up_type, L->dim, E, K) &&
-      L->up_type == L->gate_type && down1v2_ok((int)L->down_type, K, L->dim, L->hidden) &&
-      (reinterpret_cast<uintptr_t>(L->router) & 15) == 0 &&
-      (reinterpret_cast<uintptr_t>(xb) & 15) == 0) {
+  // down + combine (qr_moe_t1.hip): three launches, no routing kernel.  With
+  // norm_w the router's workgroups also form xb = rmsnorm_ref(x, norm_w).
+  if (T == 1 && t1_path(L, xb, order)) {
     // the shared expert's gate logit beside the router's (one more workgroup)
     const bool sg = sh && (reinterpret_cast<uintptr_t>(L->sh_gate_inp) & 15) == 0;
-    e = router1_launch(order, L->router, xb, E, L->dim, s.logits, st, 1,
-                       sg ? static_cast<const float*>(L->sh_gate_inp) : nullptr, s.sgl);
+    e = router1_launch(order, L->router, norm_w ? x : xb, E, L->dim, s.logits, st, 1,
+                       sg ? static_cast<const float*>(L->sh_gate_inp) : nullptr, s.sgl, norm_w,
+                       norm_w ? const_cast<float*>(xb) : nullptr);
     if (e != hipSuccess) return e;
     // the shared expert's up/gate rows as more tiles of the same launch when
     // they share the routed up type (its down product then on the GEMV)

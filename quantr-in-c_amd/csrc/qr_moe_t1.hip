@@ -21,6 +21,7 @@
 //               shared expert) for the tile's rows.
 #include "qr_blk.h"
 #include "qr_internal.h"
+#include "qr_norm.h"
 #include "qr_route.h"
 #include "qr_stream.h"
 
@@ -52,12 +53,18 @@ __device__ inline float router_seq(float* sw, const float* sx, int d, int lane) 
 // workgroups e = E compute, in matmul_ref's order whatever LANES is, the dot
 // of the one row W2 with each token into out2[t] (the shared expert's gate
 // logit, computed beside the router's).
-template <int LANES>
+// NORM (one token): xb is the residual stream x, and every workgroup forms
+// rmsnorm_ref(x, nw) itself (qr_norm.h) while its row lands; workgroup 0
+// stores the normalised vector at xb_out for the launches after it.
+constexpr int kRouterNormNP = kNormFuseMax / 4 / 64;
+template <int LANES, bool NORM>
 __global__ __launch_bounds__(64) void k_router1(const float* __restrict__ W,
                                                 const float* __restrict__ xb, int d, int E,
                                                 float* __restrict__ logits,
                                                 const float* __restrict__ W2,
-                                                float* __restrict__ out2) {
+                                                float* __restrict__ out2,
+                                                const float* __restrict__ nw,
+                                                float* __restrict__ xb_out) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int e = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
   const size_t rbytes = kib_round((size_t)d * 4);
@@ -66,7 +73,14 @@ __global__ __launch_bounds__(64) void k_router1(const float* __restrict__ W,
   const bool extra = e >= E;  // uniform
   const float* row = extra ? W2 : W + (size_t)e * d;
   dma_bytes<true>(reinterpret_cast<const uint8_t*>(row), smem, d * 4, lane);
-  dma_bytes(reinterpret_cast<const uint8_t*>(xb + (size_t)t * d), smem + rbytes, d * 4, lane);
+  if constexpr (NORM) {
+    NormRegs<kRouterNormNP> r;
+    norm_load<kRouterNormNP>(xb, nw, d, lane, 64, r);
+    norm_finish<kRouterNormNP>(r, d, sx, reinterpret_cast<float*>(smem + 2 * rbytes), lane, 64,
+                               e == 0 ? xb_out : nullptr);
+  } else {
+    dma_bytes(reinterpret_cast<const uint8_t*>(xb + (size_t)t * d), smem + rbytes, d * 4, lane);
+  }
   wait_vmcnt<0>();
   if (LANES == 1 || extra) {
     const float s = router_seq(sw, sx, d, lane);
@@ -105,24 +119,44 @@ __global__ __launch_bounds__(64) void k_router1(const float* __restrict__ W,
 }
 
 bool router1_ok(int dim) { return dim > 0 && (dim & 3) == 0 && 2 * kib_round((size_t)dim * 4) <= 64 * 1024; }
+bool router1_norm_ok(int dim) { return router1_ok(dim) && dim <= kNormFuseMax; }
+
+template <bool NORM>
+static void router1_k(int order, dim3 grid, size_t lds, hipStream_t st, const float* W,
+                      const float* xb, int d, int E, float* logits, const float* W2, float* out2,
+                      const float* nw, float* xb_out) {
+  switch (order) {
+    case QR_ORDER_SEQ:
+      hipLaunchKernelGGL((k_router1<1, NORM>), grid, dim3(64), lds, st, W, xb, d, E, logits, W2,
+                         out2, nw, xb_out);
+      break;
+    case QR_ORDER_AVX2:
+      hipLaunchKernelGGL((k_router1<8, NORM>), grid, dim3(64), lds, st, W, xb, d, E, logits, W2,
+                         out2, nw, xb_out);
+      break;
+    default:
+      hipLaunchKernelGGL((k_router1<16, NORM>), grid, dim3(64), lds, st, W, xb, d, E, logits, W2,
+                         out2, nw, xb_out);
+      break;
+  }
+}
 
 hipError_t router1_launch(int order, const float* W, const float* xb, int E, int d, float* logits,
-                          hipStream_t st, int T, const float* W2, float* out2) {
+                          hipStream_t st, int T, const float* W2, float* out2, const float* nw,
+                          float* xb_out) {
   if ((E > 0 && (reinterpret_cast<uintptr_t>(W) & 15)) || (reinterpret_cast<uintptr_t>(xb) & 15) ||
       (W2 && (reinterpret_cast<uintptr_t>(W2) & 15)) || T < 1)
     return hipErrorInvalidValue;
-  const size_t lds = 2 * kib_round((size_t)d * 4);
   const dim3 grid(E + (W2 ? 1 : 0), T);
-  switch (order) {
-    case QR_ORDER_SEQ:
-      hipLaunchKernelGGL(k_router1<1>, grid, dim3(64), lds, st, W, xb, d, E, logits, W2, out2);
-      break;
-    case QR_ORDER_AVX2:
-      hipLaunchKernelGGL(k_router1<8>, grid, dim3(64), lds, st, W, xb, d, E, logits, W2, out2);
-      break;
-    default:
-      hipLaunchKernelGGL(k_router1<16>, grid, dim3(64), lds, st, W, xb, d, E, logits, W2, out2);
-      break;
+  if (nw) {
+    if (T != 1 || !router1_norm_ok(d) || (reinterpret_cast<uintptr_t>(nw) & 15) ||
+        (xb_out && (reinterpret_cast<uintptr_t>(xb_out) & 15)))
+      return hipErrorInvalidValue;
+    router1_k<true>(order, grid, 2 * kib_round((size_t)d * 4) + 16, st, W, xb, d, E, logits, W2,
+                    out2, nw, xb_out);
+  } else {
+    router1_k<false>(order, grid, 2 * kib_round((size_t)d * 4), st, W, xb, d, E, logits, W2,
+                     out2, nullptr, nullptr);
   }
   return hipGetLastError();
 }

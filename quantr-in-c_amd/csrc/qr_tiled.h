@@ -22,6 +22,7 @@
 #pragma once
 
 #include "qr_blk.h"
+#include "qr_norm.h"
 
 namespace qr {
 
@@ -85,6 +86,12 @@ __global__ __launch_bounds__(256) void k_tile_pack(const uint8_t* __restrict__ s
 //   kProLate (larger activations): the quantizing waves load the activation
 //            with ordinary loads and quantize it first, and issue their first
 //            tile's DMA after the barrier; the other waves issue theirs at once.
+//   kProNorm (one token): X is the residual stream and the activation is its
+//            rmsnorm_ref with weights nw (qr_norm.h).  Every wave issues its
+//            first tile's DMA, the workgroup loads x and nw, thread 0 forms
+//            the sum of squares while the tiles land, and the normalised
+//            vector goes to LDS (after the slots, d floats and the scale)
+//            for the quantizer; workgroup 0 also stores it at nxb.
 // Then, tile after tile, the wave takes chunk k once it has landed (the
 // wave's DMA operations complete in issue order), and right after reading it
 // refills chunk k of its slot with chunk k of its next tile: a ring of NCH
@@ -92,7 +99,7 @@ __global__ __launch_bounds__(256) void k_tile_pack(const uint8_t* __restrict__ s
 // on the last tile the count runs down.  The Y stores between tiles only make
 // those waits stricter.  The row sums are the sequential chain of qr_blk.h.
 // ---------------------------------------------------------------------------
-enum { kProAsm1 = 0, kProAsm2 = 1, kProLate = 2 };
+enum { kProAsm1 = 0, kProAsm2 = 1, kProLate = 2, kProNorm = 3 };
 
 // One global_load_lds_dwordx4 per chunk: chunk k's 16 bytes for this lane at
 // src[k], into LDS sbase + 1024 k (+ 16 lane by the hardware).
@@ -287,16 +294,17 @@ __device__ inline void tiled_tile(const uint8_t* slot, uint32_t sbase, int lane,
   tiled_unit<TYPE, NT, 7, RING>(slot, sbase, lane, nsrc, hdr, dd, dm, qh, act, tokb, b, terms);
 }
 
+// The GEMV's work as workgroup `bid` of `nbid` (a kernel of its own, or one
+// role of a kernel that runs two matrices).
 template <int TYPE, int NT, int NW, int PRO>
-__global__ __launch_bounds__(64 * NW) void k_gemv_tiled(GemvArgs g) {
-  extern __shared__ __align__(16) uint8_t smem[];
+__device__ inline void tiled_body(const GemvArgs& g, uint8_t* smem, int bid, int nbid) {
   constexpr int NCH = TiledFmt<TYPE>::kChunks;
   constexpr int QW = NW < 4 ? NW : 4;  // quantizing waves
   constexpr bool NIB = BlkFmt<TYPE>::kNib;
   const int nb = g.t_nb, ntiles = g.t_ntiles;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int tstep = gridDim.x * NW;
-  int tile = blockIdx.x * NW + wave;
+  const int tstep = nbid * NW;
+  int tile = bid * NW + wave;
   const bool has = tile < ntiles;
   const size_t tokb = act_tok_bytes(g.d);
   uint8_t* act = smem;
@@ -335,6 +343,18 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tiled(GemvArgs g) {
     } else if (has) {
       tiled_dma<NCH>(src, sbase);
     }
+  } else if constexpr (PRO == kProNorm) {
+    static_assert(NT == 1, "the normalising start-up takes one token");
+    constexpr int NP = (kNormFuseMax / 4 + 64 * NW - 1) / (64 * NW);
+    float* xs = reinterpret_cast<float*>(smem + align16(tokb) + (size_t)NW * NCH * 1024);
+    if (has) tiled_dma<NCH>(src, sbase);
+    NormRegs<NP> r;
+    norm_load<NP>(g.X, g.nw, g.d, (int)threadIdx.x, 64 * NW, r);
+    norm_finish<NP>(r, g.d, xs, xs + g.d, (int)threadIdx.x, 64 * NW, bid == 0 ? g.nxb : nullptr);
+    if (wave < QW) {
+      ActPre pre;
+      quantize_act_blk<NIB, kActLds>(g.X, (size_t)g.d, 1, g.d, act, pre, xs, qtid, 64 * QW);
+    }
   } else {
     if (wave < QW) {
       ActPre pre;
@@ -352,6 +372,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tiled(GemvArgs g) {
   if constexpr (PRO == kProLate) {
     if (wave < QW) tiled_dma<NCH>(src, sbase);
   }
+  // after the normalisation the first tile has long landed; the wait also
+  // covers workgroup 0's stores, which would otherwise count in the ring's
+  // "in flight" figures
+  if constexpr (PRO == kProNorm) wait_vmcnt<0>();
   const int rl = lane / nb, b = lane - rl * nb;
   for (;;) {
     const int next = tile + tstep;
@@ -368,11 +392,17 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tiled(GemvArgs g) {
     if (lane < L && b == nb - 1) {
       const int row = tile * g.t_rb + rl;
 #pragma unroll
-      for (int t = 0; t < NT; t++) g.Y[(size_t)t * g.ystride + row] = y[t];
+      for (int t = 0; t < NT; t++) g.Y[(size_t)t * g.ystride + row] = g.R ? g.R[row] + y[t] : y[t];
     }
     if (next >= ntiles) break;
     tile = next;
   }
+}
+
+template <int TYPE, int NT, int NW, int PRO>
+__global__ __launch_bounds__(64 * NW) void k_gemv_tiled(GemvArgs g) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  tiled_body<TYPE, NT, NW, PRO>(g, smem, (int)blockIdx.x, (int)gridDim.x);
 }
 
 }  // namespace qr

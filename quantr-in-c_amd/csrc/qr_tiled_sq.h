@@ -32,6 +32,8 @@
 #pragma once
 
 #include "qr_blk.h"
+#include "qr_norm.h"
+#include "qr_tiled.h"
 
 namespace qr {
 
@@ -311,19 +313,21 @@ __device__ inline void sq_tile_q8(const uint8_t* slot, uint32_t sbase, int lane,
 }
 
 // The GEMV: NW waves per workgroup, wave w of workgroup g takes tiles
-// g NW + w, then + gridDim.x NW, ...; its LDS slot holds one tile (kOps KiB).
-// Every wave issues its first tile's DMA at once; the first QW = min(NW, 4)
-// waves then quantize the activation (NAT layout) into LDS.
-template <int TYPE, int NT, int NW>
-__global__ __launch_bounds__(64 * NW) void k_gemv_tiled_sq(GemvArgs g) {
-  extern __shared__ __align__(16) uint8_t smem[];
+// g NW + w, then + (workgroups) NW, ...; its LDS slot holds one tile (kOps
+// KiB).  Every wave issues its first tile's DMA at once; the first QW =
+// min(NW, 4) waves then quantize the activation (NAT layout) into LDS.
+// NORM (one token): the activation is rmsnorm_ref(X, nw) formed in the
+// workgroup (qr_norm.h; the normalised vector after the slots), as the tiled
+// Q4_K / Q5_K GEMV's kProNorm start-up does.  Workgroup `bid` of `nbid`.
+template <int TYPE, int NT, int NW, bool NORM>
+__device__ inline void sq_body(const GemvArgs& g, uint8_t* smem, int bid, int nbid) {
   constexpr int NSLOT = SqFmt<TYPE>::kOps;
   constexpr int NCH = SqFmt<TYPE>::kChunks;
   constexpr int QW = NW < 4 ? NW : 4;
   const int nb = g.t_nb, ntiles = g.t_ntiles;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int tstep = gridDim.x * NW;
-  int tile = blockIdx.x * NW + wave;
+  const int tstep = nbid * NW;
+  int tile = bid * NW + wave;
   const bool has = tile < ntiles;
   const size_t tokb = act_tok_bytes(g.d);
   uint8_t* act = smem;
@@ -337,7 +341,19 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tiled_sq(GemvArgs g) {
   // later in the same in-order stream, also covers the DMA: their quantizer
   // starts when both have landed, which is when the tile is needed anyway)
   if (has) sq_dma<TYPE>(src, dsrc, sbase);
-  if (wave < QW) {
+  if constexpr (NORM) {
+    static_assert(NT == 1, "the normalising start-up takes one token");
+    constexpr int NP = (kNormFuseMax / 4 + 64 * NW - 1) / (64 * NW);
+    float* xs = reinterpret_cast<float*>(smem + align16(tokb) + (size_t)NW * NSLOT * 1024);
+    NormRegs<NP> r;
+    norm_load<NP>(g.X, g.nw, g.d, (int)threadIdx.x, 64 * NW, r);
+    norm_finish<NP>(r, g.d, xs, xs + g.d, (int)threadIdx.x, 64 * NW, bid == 0 ? g.nxb : nullptr);
+    if (wave < QW) {
+      ActPre pre;
+      quantize_act_blk<false, kActLds>(g.X, (size_t)g.d, 1, g.d, act, pre, xs, (int)threadIdx.x,
+                                       64 * QW);
+    }
+  } else if (wave < QW) {
     ActPre pre;
     act_load8(g.X, (size_t)g.xstride, NT, g.d, (int)threadIdx.x, pre.v);
     quantize_act_blk<false, kActGlobal>(g.X, (size_t)g.xstride, NT, g.d, act, pre, nullptr,
@@ -347,6 +363,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tiled_sq(GemvArgs g) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   if (!has) return;  // no barriers below
+  // after a normalisation: the first tile has landed, and the wait covers the
+  // workgroup's stores, which would otherwise count in the ring's figures
+  if constexpr (NORM) wait_vmcnt<0>();
   const int rl = lane / nb, b = lane - rl * nb;
   for (;;) {
     const int next = tile + tstep;
@@ -369,11 +388,30 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tiled_sq(GemvArgs g) {
     if (lane < L && b == nb - 1) {
       const int row = tile * g.t_rb + rl;
 #pragma unroll
-      for (int t = 0; t < NT; t++) g.Y[(size_t)t * g.ystride + row] = y[t];
+      for (int t = 0; t < NT; t++) g.Y[(size_t)t * g.ystride + row] = g.R ? g.R[row] + y[t] : y[t];
     }
     if (next >= ntiles) break;
     tile = next;
   }
+}
+
+template <int TYPE, int NT, int NW>
+__global__ __launch_bounds__(64 * NW) void k_gemv_tiled_sq(GemvArgs g) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  sq_body<TYPE, NT, NW, false>(g, smem, (int)blockIdx.x, (int)gridDim.x);
+}
+
+// One token through two matrices after one normalisation: workgroups
+// [0, ga) run a tiled Q4_K / Q5_K matrix (a, kProNorm), the rest a tiled
+// Q6_K / Q8_0 matrix (b), every workgroup forming the same rmsnorm_ref of the
+// residual (the decode step's q / k and v projections in one launch).
+template <int TA, int TB, int NW>
+__global__ __launch_bounds__(64 * NW) void k_gemv_norm2(GemvArgs a, GemvArgs b, int ga) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  if ((int)blockIdx.x < ga)  // uniform per workgroup
+    tiled_body<TA, 1, NW, kProNorm>(a, smem, (int)blockIdx.x, ga);
+  else
+    sq_body<TB, 1, NW, true>(b, smem, (int)blockIdx.x - ga, (int)gridDim.x - ga);
 }
 
 }  // namespace qr

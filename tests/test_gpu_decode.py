@@ -243,3 +243,61 @@ def test_decoder_rejects_bad_arguments(dev):
     with pytest.raises(Q.QrError, match="permutation"):
         d.set_pages(np.zeros((1, 4), np.int32))
     d.close()
+
+
+@pytest.mark.parametrize("wv_tiled", [False, True], ids=["wv_rows", "wv_tiled"])
+@pytest.mark.parametrize("order", [ORDER_SEQ, ORDER_AVX2], ids=["c99", "avx2"])
+def test_decode_stacked_qk_q8_v(dev, oracle, order, wv_tiled):
+    """wq and wk back to back in the tiled Q4_K layout and a Q8_0 wv: in the
+    C99 build the attention norm, q / k and v run in one launch (the v matrix
+    tiled by the caller, or a tiled copy the decoder makes); in the AVX2
+    build v keeps its own GEMV (the tiled Q8_0 dot is the C99 order, so a
+    tiled Q8_0 v is refused there).  Four decode steps from position 0,
+    graph-replayed, bit-exact with the oracle."""
+    m = I.qwen3_small_model(n_layers=2, seq_len=64)
+    H, KVH, hd, dim = m["n_heads"], m["n_kv_heads"], m["head_dim"], m["dim"]
+    qd, kvd = H * hd, KVH * hd
+    m["wtype"] = [Q.TYPE_Q4_K, Q.TYPE_Q4_K, Q.TYPE_Q8_0, Q.TYPE_Q5_K]
+    for l, lw in enumerate(m["layers"]):
+        lw["wk"] = I._rows(9600 + l, Q.TYPE_Q4_K, kvd, dim)
+        lw["wv"] = I._rows(9610 + l, Q.TYPE_Q8_0, kvd, dim)
+    mdev = dict(m)
+    mdev["layers"] = [dict(lw) for lw in m["layers"]]
+    keep = []
+    for lw in mdev["layers"]:
+        qk = np.concatenate([lw["wq"].reshape(-1), lw["wk"].reshape(-1)])
+        src = dev.upload(qk)
+        both = dev.alloc(qk.nbytes)
+        dev.tile(Q.TYPE_Q4_K, src.ptr, both.ptr, qd + kvd, dim)
+        keep += [src, both]
+        lw["wq"], lw["wk"] = both.ptr, both.ptr + lw["wq"].nbytes
+        if wv_tiled:
+            vs = dev.upload(lw["wv"])
+            vt = dev.alloc(lw["wv"].nbytes)
+            dev.tile(Q.TYPE_Q8_0, vs.ptr, vt.ptr, kvd, dim)
+            keep += [vs, vt]
+            lw["wv"] = vt.ptr
+    dev.sync()
+    mdev["wtype"] = [Q.TYPE_Q4_K | Q.TILED, Q.TYPE_Q4_K | Q.TILED,
+                     Q.TYPE_Q8_0 | (Q.TILED if wv_tiled else 0), Q.TYPE_Q5_K]
+    model, layers, k2 = Q.upload_decode_model(dev, mdev)
+    print("stacked qk, Q8_0 v (tiled %d) order %d" % (wv_tiled, order), flush=True)
+    if wv_tiled and order != ORDER_SEQ:  # tiled Q8_0 holds only the C99 dot order
+        with pytest.raises(Q.QrError, match="tiled type 8"):
+            Q.Decoder(dev, model, layers, kv_type=Q.KV_Q8_0, order=order, page=16)
+        return
+    d = Q.Decoder(dev, model, layers, kv_type=Q.KV_Q8_0, order=order, page=16,
+                  flags=Q.DEC_GRAPH)
+    toks = [5, 300, 5, 17]
+    lg_d, x_d = dev.alloc(4 * m["vocab"]), dev.alloc(4 * m["dim"])
+    lg = np.zeros((len(toks), m["vocab"]), np.float32)
+    xs = np.zeros((len(toks), m["dim"]), np.float32)
+    for i, t in enumerate(toks):
+        d.forward(t, i, lg_d.ptr, x_d.ptr)
+        lg[i] = dev.download(lg_d, m["vocab"], np.float32)
+        xs[i] = dev.download(x_d, m["dim"], np.float32)
+    d.close()
+    del k2, keep
+    wl, wx = oracle.forward_seq(m, toks, order, Q.KV_Q8_0)
+    assert_bits_equal(xs, wx, "residual")
+    assert_bits_equal(lg, wl, "logits")

@@ -174,6 +174,37 @@ def test_prefill_gqa8_chunks(dev, oracle, kv_type, page):
     assert np.array_equal(kv, _oracle_rows(kc, vc, m["n_layers"], probe))
 
 
+def test_prefill_gqa8_lds_boundary(dev, oracle):
+    """GQA 8:1 at head_dim 128 in pages of 256 near 4096 positions, where the
+    per-kv-head values kernel's LDS (eight score rows of the chunk's extent
+    plus the value tiles and page table) reaches the CU's 160 KiB: a chunk
+    ending at extent 4088 still fits it, one ending at 4092 runs the per-head
+    kernel instead.  The prefix is prefilled on the device; the oracle then
+    runs the two chunks' tokens over that cache: every logit bit-exact."""
+    m = I.qwen3_small_model(n_layers=1, seq_len=4096, n_kv_heads=1)
+    rng = np.random.default_rng(41)
+    toks = rng.integers(0, m["vocab"], size=4092).astype(np.int32)
+    d = make_decoder(dev, m, Q.KV_Q8_0, ORDER_SEQ, page=256)
+    print("prefill gqa8 lds boundary", flush=True)
+    d.prefill(toks[:4080], 0, chunk=512)
+    rs = oracle.kv_row_bytes(Q.KV_Q8_0, m["n_kv_heads"] * m["head_dim"])
+    kc = np.zeros((1, m["seq_len"], rs), np.uint8)
+    vc = np.zeros_like(kc)
+    for t in range(4080):
+        kr, vr = d.kv_rows(0, t)
+        kc[0, t] = dev.download(kr, rs, np.uint8)
+        vc[0, t] = dev.download(vr, rs, np.uint8)
+    lg1, _ = prefill(dev, d, m, toks[4080:4088], pos0=4080, chunk=8)   # extent 4088
+    lg2, x2 = prefill(dev, d, m, toks[4088:4092], pos0=4088, chunk=4)  # extent 4092
+    d.close()
+    want_lg, want_xs = oracle.forward_cached(m, kc.reshape(-1), vc.reshape(-1),
+                                             [int(t) for t in toks[4080:]], 4080, ORDER_SEQ,
+                                             Q.KV_Q8_0)
+    assert_bits_equal(lg1, want_lg[:8], "logits, chunk ending at extent 4088")
+    assert_bits_equal(lg2, want_lg[8:], "logits, chunk ending at extent 4092")
+    assert_bits_equal(x2, want_xs[-1], "last residual")
+
+
 def test_prefill_matches_sequential_decode(dev):
     """Prefill in chunks of 128 against the same decoder's own single steps
     (a consistency check beside the oracle comparisons above)."""
