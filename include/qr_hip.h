@@ -346,7 +346,11 @@ typedef struct qr_decoder qr_decoder;
  * apply_rope calls them (src/runtime.c:19-41; its frequency index runs over
  * the whole q vector, as there).  `order` is the reference build
  * (QR_ORDER_*): the order of the fp32 matmuls and the router, and of the
- * Q8_0 dot. */
+ * Q8_0 dot.  Where a layer's wq and wk are one tiled Q4_K / Q5_K matrix
+ * (wk's bytes right after wq's) and wv is Q6_K (rows a multiple of 2048) or
+ * C99-order Q8_0, the decoder keeps a tiled copy of a row-major wv (about
+ * rows x row bytes per layer) so that the norm, q / k and v run as one
+ * launch. */
 int qr_decoder_create(qr_ctx* ctx, const qr_model* model, int kv_type, int order, int page,
                       int flags, qr_decoder** out);
 int qr_decoder_destroy(qr_decoder* dec);
@@ -418,7 +422,7 @@ float qr_gguf_get_f32(const qr_gguf* g, const char* key, float def);
 const char* qr_gguf_get_str(const qr_gguf* g, const char* key);
 int64_t qr_gguf_get_arr_len(const qr_gguf* g, const char* key); /* -1 if absent */
 
-/* The decoder model of a MoE GGUF as HOST pointers into the buffer, mapped as
+/* The decoder model of a MoE or dense GGUF as HOST pointers into the buffer, mapped as
  * load_gguf_transformer does (src/model.c:253-449): {arch}.embedding_length,
  * block_count, attention.head_count(_kv), expert_count, expert_used_count,
  * expert_feed_forward_length, rope.freq_base (default 1e6); token_embd,
@@ -426,7 +430,9 @@ int64_t qr_gguf_get_arr_len(const qr_gguf* g, const char* key); /* -1 if absent 
  * attn_q / attn_k / attn_v / attn_output / ffn_gate_inp, and the experts with
  * expert_w1 = ffn_up_exps (the SiLU slot), expert_w3 = ffn_gate_exps,
  * expert_w2 = ffn_down_exps as one 3-D tensor each or per-expert tensors
- * (then the pointers are expert 0's; see qr_gguf_expert_host).  Beyond the
+ * (then the pointers are expert 0's; see qr_gguf_expert_host); a file
+ * without expert_count is dense: ffn_up (w1), ffn_gate (w3) and ffn_down (w2)
+ * of feed_forward_length rows, in a layer with n_experts = 0.  Beyond the
  * reference: head_dim is attention.key_length when the file states it
  * (else dim / n_heads, as there); vocab is the tokenizer's token count, else
  * the embedding's rows; every tensor's shape and type is checked, all
@@ -442,8 +448,9 @@ int qr_gguf_expert_host(const qr_gguf* g, int layer, int e, const void** up, con
  * allocation (each tensor 256-byte aligned; per-expert tensors gathered
  * into one range per kind, expert e at e * slice, as a 3-D tensor is laid
  * out; a tied output shares the embedding's copy; Q4_K / Q5_K attention
- * projections and output matrices with at most 64 super-blocks per row are
- * stored tiled and their types carry QR_TILED).  Returns a qr_model of
+ * projections, dense FFN matrices and output matrices with at most 64
+ * super-blocks per row, and a Q6_K output matrix with rows a multiple of
+ * 2048, are stored tiled and their types carry QR_TILED).  Returns a qr_model of
  * device pointers for qr_decoder_create.  The copy owns its memory: the
  * qr_gguf may be closed after loading, two loads are two copies, and
  * qr_gguf_model_free releases one of them (after the context stream has
