@@ -356,7 +356,7 @@ class Oracle:
         for l in range(L):
             ml = Oracle.make_layer(keep, m["dim"], m["hidden"], m["E"], m["K"], lay[l]["router"],
                                    lay[l]["up"], m["up_type"], lay[l]["gate"], m["up_type"],
-                                   lay[l]["down"], m["down_type"])
+                                   lay[l]["down"], m["down_type"], shared=lay[l].get("shared"))
             moes[l] = ml
         keep.append(moes)
         wtype = np.array([t for l in range(L) for t in m["wtype"]], np.uint32)

@@ -557,7 +557,8 @@ def upload_decode_model(dev, m):
     seq_len, rope_base, E, K, hidden), the types (tok_type, wcls_type,
     wtype = (wq, wk, wv, wo), up_type (also gate), down_type) and the tensors
     (tok_embd, rms_final, wcls, and per layer rms_att, rms_ffn, wq, wk, wv,
-    wo, router, up, gate, down).  A tensor is a numpy array (uploaded here) or
+    wo, router, up, gate, down, and optionally shared: a shared expert as
+    {hidden, gate_inp, up, gate, down, up_type, down_type}).  A tensor is a numpy array (uploaded here) or
     an int device address (used as is).  E = 0 describes a dense model: up,
     gate and down are then each layer's ffn_up (w1), ffn_gate (w3) and
     ffn_down (w2), and router is empty.  Returns (model, layers, keep); keep
@@ -591,6 +592,13 @@ def upload_decode_model(dev, m):
         e.up, e.gate, e.down = dptr(lw["up"]), dptr(lw["gate"]), dptr(lw["down"])
         e.up_type = e.gate_type = m["up_type"]
         e.down_type = m["down_type"]
+        sh = lw.get("shared")
+        if sh is not None:  # a shared expert with its sigmoid gate
+            e.sh_hidden = sh["hidden"]
+            e.sh_gate_inp, e.sh_up = dptr(sh["gate_inp"]), dptr(sh["up"])
+            e.sh_gate, e.sh_down = dptr(sh["gate"]), dptr(sh["down"])
+            e.sh_up_type = e.sh_gate_type = sh["up_type"]
+            e.sh_down_type = sh["down_type"]
     mo = Model()
     mo.dim, mo.n_heads, mo.n_kv_heads = m["dim"], m["n_heads"], m["n_kv_heads"]
     mo.head_dim, mo.n_layers, mo.vocab = m["head_dim"], L, m["vocab"]

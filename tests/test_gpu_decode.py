@@ -245,10 +245,11 @@ def test_decoder_rejects_bad_arguments(dev):
     d.close()
 
 
+@pytest.mark.parametrize("qk_type", [Q.TYPE_Q4_K, Q.TYPE_Q5_K], ids=["qk_q4k", "qk_q5k"])
 @pytest.mark.parametrize("wv_tiled", [False, True], ids=["wv_rows", "wv_tiled"])
 @pytest.mark.parametrize("order", [ORDER_SEQ, ORDER_AVX2], ids=["c99", "avx2"])
-def test_decode_stacked_qk_q8_v(dev, oracle, order, wv_tiled):
-    """wq and wk back to back in the tiled Q4_K layout and a Q8_0 wv: in the
+def test_decode_stacked_qk_q8_v(dev, oracle, order, wv_tiled, qk_type):
+    """wq and wk back to back in the tiled Q4_K / Q5_K layout and a Q8_0 wv: in the
     C99 build the attention norm, q / k and v run in one launch (the v matrix
     tiled by the caller, or a tiled copy the decoder makes); in the AVX2
     build v keeps its own GEMV (the tiled Q8_0 dot is the C99 order, so a
@@ -257,9 +258,10 @@ def test_decode_stacked_qk_q8_v(dev, oracle, order, wv_tiled):
     m = I.qwen3_small_model(n_layers=2, seq_len=64)
     H, KVH, hd, dim = m["n_heads"], m["n_kv_heads"], m["head_dim"], m["dim"]
     qd, kvd = H * hd, KVH * hd
-    m["wtype"] = [Q.TYPE_Q4_K, Q.TYPE_Q4_K, Q.TYPE_Q8_0, Q.TYPE_Q5_K]
+    m["wtype"] = [qk_type, qk_type, Q.TYPE_Q8_0, Q.TYPE_Q5_K]
     for l, lw in enumerate(m["layers"]):
-        lw["wk"] = I._rows(9600 + l, Q.TYPE_Q4_K, kvd, dim)
+        lw["wq"] = I._rows(9590 + l, qk_type, qd, dim)
+        lw["wk"] = I._rows(9600 + l, qk_type, kvd, dim)
         lw["wv"] = I._rows(9610 + l, Q.TYPE_Q8_0, kvd, dim)
     mdev = dict(m)
     mdev["layers"] = [dict(lw) for lw in m["layers"]]
@@ -268,7 +270,7 @@ def test_decode_stacked_qk_q8_v(dev, oracle, order, wv_tiled):
         qk = np.concatenate([lw["wq"].reshape(-1), lw["wk"].reshape(-1)])
         src = dev.upload(qk)
         both = dev.alloc(qk.nbytes)
-        dev.tile(Q.TYPE_Q4_K, src.ptr, both.ptr, qd + kvd, dim)
+        dev.tile(qk_type, src.ptr, both.ptr, qd + kvd, dim)
         keep += [src, both]
         lw["wq"], lw["wk"] = both.ptr, both.ptr + lw["wq"].nbytes
         if wv_tiled:
@@ -278,7 +280,7 @@ def test_decode_stacked_qk_q8_v(dev, oracle, order, wv_tiled):
             keep += [vs, vt]
             lw["wv"] = vt.ptr
     dev.sync()
-    mdev["wtype"] = [Q.TYPE_Q4_K | Q.TILED, Q.TYPE_Q4_K | Q.TILED,
+    mdev["wtype"] = [qk_type | Q.TILED, qk_type | Q.TILED,
                      Q.TYPE_Q8_0 | (Q.TILED if wv_tiled else 0), Q.TYPE_Q5_K]
     model, layers, k2 = Q.upload_decode_model(dev, mdev)
     print("stacked qk, Q8_0 v (tiled %d) order %d" % (wv_tiled, order), flush=True)
@@ -298,6 +300,41 @@ def test_decode_stacked_qk_q8_v(dev, oracle, order, wv_tiled):
         xs[i] = dev.download(x_d, m["dim"], np.float32)
     d.close()
     del k2, keep
+    wl, wx = oracle.forward_seq(m, toks, order, Q.KV_Q8_0)
+    assert_bits_equal(xs, wx, "residual")
+    assert_bits_equal(lg, wl, "logits")
+
+
+@pytest.mark.parametrize("order,graph", [(ORDER_SEQ, Q.DEC_GRAPH), (ORDER_AVX2, 0)],
+                         ids=["c99_graph", "avx2_eager"])
+def test_decode_shared_expert(dev, oracle, order, graph):
+    """A MoE decoder whose layers also have a shared expert with a sigmoid gate
+    (Qwen1.5-MoE's layer form): the router's launch forms the FFN norm and the
+    shared gate logit beside the router logits, the shared gate / up rows run
+    in the gate / up launch and its down on the GEMV.  Four decode steps
+    bit-exact with the oracle."""
+    m = I.qwen3_small_model(n_layers=2, seq_len=64)
+    dim, sh = m["dim"], 512
+    for l, lw in enumerate(m["layers"]):
+        s = 9660 + 10 * l
+        lw["shared"] = dict(hidden=sh, gate_inp=I.activations(s, 1, dim, std=0.05)[0],
+                            up=I._rows(s + 1, Q.TYPE_Q4_K, sh, dim).reshape(-1),
+                            gate=I._rows(s + 2, Q.TYPE_Q4_K, sh, dim).reshape(-1),
+                            down=I._rows(s + 3, Q.TYPE_Q6_K, dim, sh).reshape(-1),
+                            up_type=Q.TYPE_Q4_K, down_type=Q.TYPE_Q6_K)
+    toks = [5, 300, 5, 17]
+    print("decode shared expert order %d graph %d" % (order, graph), flush=True)
+    model, layers, keep = Q.upload_decode_model(dev, m)
+    d = Q.Decoder(dev, model, layers, kv_type=Q.KV_Q8_0, order=order, page=16, flags=graph)
+    lg_d, x_d = dev.alloc(4 * m["vocab"]), dev.alloc(4 * m["dim"])
+    lg = np.zeros((len(toks), m["vocab"]), np.float32)
+    xs = np.zeros((len(toks), m["dim"]), np.float32)
+    for i, t in enumerate(toks):
+        d.forward(t, i, lg_d.ptr, x_d.ptr)
+        lg[i] = dev.download(lg_d, m["vocab"], np.float32)
+        xs[i] = dev.download(x_d, m["dim"], np.float32)
+    d.close()
+    del keep
     wl, wx = oracle.forward_seq(m, toks, order, Q.KV_Q8_0)
     assert_bits_equal(xs, wx, "residual")
     assert_bits_equal(lg, wl, "logits")
