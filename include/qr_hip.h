@@ -143,6 +143,18 @@ int qr_gemv_ord(qr_ctx* ctx, int order, uint32_t type, const void* w, const floa
                 int xstride, float* y, int ystride, int n, int d, int nt, int32_t* acc,
                 int32_t* accb);
 
+/* T tokens through one quantized matrix as a grouped int8 MFMA product (the
+ * kernel of qr_decoder_prefill's projections): y[t * ystride + r] = W[r] .
+ * x[t * xstride ...] for r < n, t < T, the same bits as qr_gemv_ord gives
+ * token by token (every 32-element unit's fp32 term added in unit order).
+ * Q4_K / Q5_K (row-major or QR_TILED), Q6_K and Q8_0 (QR_ORDER_SEQ only),
+ * d a multiple of 256 and at most 16384; any T.  Uses the context scratch
+ * (48 bytes per 32 activation values, plus 4 T + 32).  No counterpart in the
+ * reference, which runs one matmul_q_fused per token (speculative
+ * verification, src/speculative.c:107-140; prompts, src/runtime.c:294-304). */
+int qr_gemv_rows(qr_ctx* ctx, int order, uint32_t type, const void* w, const float* x,
+                 int xstride, float* y, int ystride, int n, int d, int T);
+
 /* The tiled layout of a Q4_K / Q5_K / Q6_K / Q8_0 matrix: the same bytes as
  * the reference's row-major blocks, permuted so that the GEMV streams each
  * wave's tile in the order it is consumed (no reference counterpart; the

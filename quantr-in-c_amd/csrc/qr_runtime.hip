@@ -13,6 +13,7 @@
 
 #include "qr_common.h"
 #include "qr_internal.h"
+#include "qr_tokens.h"
 
 // A registered weight tensor: its device copy, its size, and a 64-bit digest
 // of what it was uploaded from (the first and last up to 64 bytes of each
@@ -605,6 +606,49 @@ int qr_gemv_ex(qr_ctx* c, uint32_t type, const void* w, const float* x, int xstr
 int qr_gemv(qr_ctx* c, uint32_t type, const void* w, const float* x, float* y, int n, int d,
             int nt) {
   return qr_gemv_ex(c, type, w, x, d, y, n, n, d, nt, nullptr, nullptr);
+}
+
+int qr_gemv_rows(qr_ctx* c, int order, uint32_t type, const void* w, const float* x, int xstride,
+                 float* y, int ystride, int n, int d, int T) {
+  if (!c) return fail(QR_ERR_INVALID, "qr_gemv_rows: null ctx");
+  if (order < QR_ORDER_SEQ || order > QR_ORDER_AVX512)
+    return fail(QR_ERR_INVALID, "qr_gemv_rows: order %d", order);
+  const bool tiled = (type & QR_TILED) != 0;
+  const uint32_t base = type & ~(uint32_t)QR_TILED;
+  if (n < 0 || d <= 0 || T < 0) return fail(QR_ERR_INVALID, "qr_gemv_rows: bad size");
+  if (n == 0 || T == 0) return QR_OK;
+  if (!w || !x || !y) return fail(QR_ERR_INVALID, "qr_gemv_rows: null pointer");
+  if (xstride < d || ystride < n || (xstride & 3))
+    return fail(QR_ERR_INVALID, "qr_gemv_rows: strides (xstride >= d, a multiple of 4; ystride >= n)");
+  if ((type & QR_GGML) || !qr::mfma_type_ok((int)base) || d % 256 || (d >> 8) > 64 ||
+      (tiled && base != QR_T_Q4_K && base != QR_T_Q5_K))
+    return fail(QR_ERR_UNSUPPORTED,
+                "qr_gemv_rows: type %u at d=%d (Q4_K / Q5_K row-major or tiled, Q6_K, Q8_0; d a "
+                "multiple of 256, at most 16384)", type, d);
+  if (base == QR_T_Q8_0 && order != QR_ORDER_SEQ)
+    return fail(QR_ERR_UNSUPPORTED, "qr_gemv_rows: Q8_0 in a lane order (use qr_gemv_ord)");
+  if (!aligned(w, 16) || !aligned(x, 16))
+    return fail(QR_ERR_INVALID, "qr_gemv_rows: w and x must be 16-byte aligned");
+  const size_t slice = qr_wrow_bytes((int)base, d) * (size_t)n;
+  if (slice >= ((size_t)1 << 32)) return fail(QR_ERR_UNSUPPORTED, "qr_gemv_rows: matrix of 4 GiB or more");
+  // scratch: the rows' activation records, then the single-"expert" dispatch
+  const size_t rec = (((size_t)T * (d / 32) * qr::kXQ) + 255) & ~(size_t)255;
+  void* base_p = nullptr;
+  int rc = ctx_scratch(c, rec + 16 + 4 * (size_t)T + 16, "qr_gemv_rows", &base_p);
+  if (rc) return rc;
+  uint8_t* recp = static_cast<uint8_t*>(base_p);
+  int32_t* off = reinterpret_cast<int32_t*>(recp + rec);
+  int32_t* tiles = off + 4;
+  int32_t* perm = tiles + 4;
+  const int tile = 16;
+  QR_HIP(qr::rows_dispatch_launch(T, tile, off, perm, tiles, c->stream), "k_rows_dispatch");
+  QR_HIP(qr::quant_rows_launch(x, xstride, T, d, base != QR_T_Q8_0, recp, c->stream),
+         "k_quant_rows");
+  QR_HIP(qr::expert_mfma_launch((int)base, false, static_cast<const uint8_t*>(w), nullptr, slice,
+                                1, 1, n, d, recp, 1, off, perm, tiles, y, ystride,
+                                (T + tile - 1) / tile + 1, tile, nullptr, false, c->stream, tiled),
+         "k_expert_mfma");
+  return QR_OK;
 }
 
 int qr_matmul_f32(qr_ctx* c, int order, const float* w, const float* x, float* y, int n, int d,

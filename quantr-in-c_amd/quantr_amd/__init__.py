@@ -96,6 +96,8 @@ _SIGS = {
     "qr_gemv": (C.c_int, [_vp, C.c_uint32, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
     "qr_gemv_ord": (C.c_int, [_vp, C.c_int, C.c_uint32, _vp, _vp, C.c_int, _vp, C.c_int, C.c_int,
                               C.c_int, C.c_int, _vp, _vp]),
+    "qr_gemv_rows": (C.c_int, [_vp, C.c_int, C.c_uint32, _vp, _vp, C.c_int, _vp, C.c_int, C.c_int,
+                               C.c_int, C.c_int]),
     "qr_matmul_f32": (C.c_int, [_vp, C.c_int, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
     "qr_softmax": (C.c_int, [_vp, _vp, C.c_int, C.c_int]),
     "qr_row_bytes": (C.c_size_t, [C.c_uint32, C.c_int]),
@@ -311,6 +313,14 @@ class Device:
         self._check(self.lib.qr_gemv_ord(self.ctx, order, qtype, _vp(w_ptr), _vp(x_ptr),
                                           xstride or d, _vp(y_ptr), ystride or n, n, d, nt,
                                           _vp(acc_ptr), _vp(accb_ptr)), "qr_gemv_ord")
+
+    def gemv_rows(self, qtype, w_ptr, x_ptr, y_ptr, n, d, T, xstride=None, ystride=None,
+                  order=ORDER_SEQ):
+        """qr_gemv_rows: T tokens through one matrix as an int8 MFMA product
+        (the same bits as gemv token by token)."""
+        self._check(self.lib.qr_gemv_rows(self.ctx, order, qtype, _vp(w_ptr), _vp(x_ptr),
+                                           xstride or d, _vp(y_ptr), ystride or n, n, d, T),
+                    "qr_gemv_rows")
 
     def tile(self, qtype, src_ptr, dst_ptr, n, d, reverse=False):
         """qr_weights_tile (or qr_weights_untile): the tiled copy of an n x d

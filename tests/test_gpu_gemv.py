@@ -384,3 +384,54 @@ def test_registry_parts_regather(dev):
         got = dev.download(out.value, 1024, np.uint8)
         assert (got == np.concatenate(parts)).all()
     lib.qr_weights_release(dev.ctx, _fp(key))
+
+
+@pytest.mark.parametrize("layout", ["rows", "tiled"])
+@pytest.mark.parametrize("T", [1, 2, 4, 5, 16, 37])
+@pytest.mark.parametrize("qtype", TYPES)
+def test_gemv_rows_mfma(dev, oracle, qtype, T, layout):
+    """qr_gemv_rows (T tokens on int8 MFMA, the prefill projections' kernel):
+    every token's output bit-exact with matmul_q_fused, at 1..37 tokens, on
+    the TinyLlama 5632 x 2048 shape (Q6_K / Q8_0 tiles take the GEMV, so
+    their tiled layout is refused here)."""
+    n, d = 5632, 2048
+    W = synth.weights(2000 + qtype, n, d, qtype)
+    X = synth.normal(60 + T, (T, d))
+    ty = qtype
+    wb = dev.upload(W)
+    if layout == "tiled":
+        if qtype not in (Q.TYPE_Q4_K, Q.TYPE_Q5_K):
+            xb, yb = dev.upload(X), dev.alloc(4 * n * T)
+            with pytest.raises(Q.QrError, match="qr_gemv_rows"):
+                dev.gemv_rows(qtype | Q.TILED, wb.ptr, xb.ptr, yb.ptr, n, d, T)
+            return
+        tb = dev.alloc(W.nbytes)
+        dev.tile(qtype, wb.ptr, tb.ptr, n, d)
+        wb, ty = tb, qtype | Q.TILED
+    xb, yb = dev.upload(X), dev.alloc(4 * n * T)
+    print("gemv_rows type %d T %d %s" % (qtype, T, layout), flush=True)
+    dev.gemv_rows(ty, wb.ptr, xb.ptr, yb.ptr, n, d, T)
+    got = dev.download(yb, (T, n), np.float32)
+    want = oracle.matmul_q_fused(X, W, qtype, n, d, threads=16).reshape(T, n)
+    assert_bits_equal(got, want, "gemv_rows type %d T=%d %s" % (qtype, T, layout))
+
+
+def test_gemv_rows_lm_head_and_refusals(dev, oracle):
+    """The 32000 x 2048 Q6_K lm_head at 4 tokens with strided rows; Q8_0 in a
+    lane order and ggml layouts are refused."""
+    n, d, T = 32000, 2048, 4
+    W = synth.weights(77, n, d, Q.TYPE_Q6_K)
+    X = synth.normal(78, (T, d + 64))
+    wb, xb, yb = dev.upload(W), dev.upload(X), dev.alloc(4 * (n + 8) * T)
+    dev.gemv_rows(Q.TYPE_Q6_K, wb.ptr, xb.ptr, yb.ptr, n, d, T, xstride=d + 64, ystride=n + 8)
+    got = dev.download(yb, (T, n + 8), np.float32)[:, :n]
+    want = oracle.matmul_q_fused(np.ascontiguousarray(X[:, :d]), W, Q.TYPE_Q6_K, n, d,
+                                 threads=16).reshape(T, n)
+    assert_bits_equal(got, want, "gemv_rows lm_head")
+    W8 = synth.weights(79, 256, d, Q.TYPE_Q8_0)
+    w8 = dev.upload(W8)
+    with pytest.raises(Q.QrError, match="lane order"):
+        dev.gemv_rows(Q.TYPE_Q8_0, w8.ptr, xb.ptr, yb.ptr, 256, d, T, xstride=d + 64,
+                      order=ORDER_AVX2)
+    with pytest.raises(Q.QrError, match="qr_gemv_rows"):
+        dev.gemv_rows(Q.TYPE_Q4_K | Q.GGML, wb.ptr, xb.ptr, yb.ptr, 256, d, T, xstride=d + 64)
