@@ -794,46 +794,62 @@ hipError_t gemv_tiled_norm_launch(int type, const void* W, const float* x, const
 // llama.cpp / ggml K-quants against Q8_K (qr_ggml.h).
 // ---------------------------------------------------------------------------
 static bool ggml_xs(int d, int nt) { return blk_xs_bytes(d, nt) <= kXsMax; }
-static size_t ggml_lds_bytes(int type, int d, int nt) {
+// The register start-up: one token, Q4_K / Q5_K, G = d / 2048 groups of 8
+// per thread (G <= 2)
+static int ggml_regs_g(int type, int d, int nt) {
+  if (nt != 1 || (type != kGgmlQ4 && type != kGgmlQ5)) return 0;
+  return d <= 2048 ? 1 : d <= 4096 ? 2 : 0;
+}
+static size_t ggml_lds_bytes(int type, int d, int nt, int xm) {
   const int ndma = type == kGgmlQ4 ? GgmlFmt<kGgmlQ4>::kDma
                    : type == kGgmlQ5 ? GgmlFmt<kGgmlQ5>::kDma : GgmlFmt<kGgmlQ6>::kDma;
-  return (ggml_xs(d, nt) ? blk_xs_bytes(d, nt) : 0) + align16((size_t)nt * q8k_tok_bytes(d)) +
+  return (xm == kXmLds ? blk_xs_bytes(d, nt) : 0) + align16((size_t)nt * q8k_tok_bytes(d)) +
          (size_t)4 * ndma * 1024;
+}
+static int ggml_xm(int type, int d, int nt) {
+  return ggml_regs_g(type, d, nt) ? kXmRegs : ggml_xs(d, nt) ? kXmLds : kXmLate;
 }
 
 bool gemv_ggml_ok(int type, int d, int nt) {
   if (type != kGgmlQ4 && type != kGgmlQ5 && type != kGgmlQ6) return false;
   if (d <= 0 || (d & 255) || (d >> 8) > 64) return false;
   if (!(nt >= 1 && nt <= 4) && nt != 8) return false;
-  return ggml_lds_bytes(type, d, nt == 8 ? 4 : nt) <= kLdsMax;
+  const int n4 = nt == 8 ? 4 : nt;
+  return ggml_lds_bytes(type, d, n4, ggml_xm(type, d, n4)) <= kLdsMax;
 }
 
-template <int T, int NT, bool XS>
+template <int T, int NT, int XM, int G = 1>
 static hipError_t launch_ggml_x(const GemvArgs& a, hipStream_t st, int pairs = 0) {
   static std::atomic<bool> opted[64];
   const int nb = a.d >> 8, RB = 64 / nb;
   const int ntiles = (a.n + RB - 1) / RB;
-  const size_t lds = ggml_lds_bytes(T, a.d, NT);
+  const size_t lds = ggml_lds_bytes(T, a.d, NT, XM);
   if (lds > 64 * 1024) {
-    hipError_t e = lds_opt_in((const void*)k_gemv_ggml<T, NT, XS>, opted);
+    hipError_t e = lds_opt_in((const void*)k_gemv_ggml<T, NT, XM, G>, opted);
     if (e != hipSuccess) return e;
   }
   int per_cu = (int)(kLdsMax / lds);
-  per_cu = per_cu < 1 ? 1 : (per_cu > 3 ? 3 : per_cu);
+  per_cu = per_cu < 1 ? 1 : (per_cu > 4 ? 4 : per_cu);
   const int want = (ntiles + 3) / 4;
   // pair mode: the pairs' matrices share the resident workgroups
   const int cap = pairs > 0 ? (device_cus() * per_cu + pairs - 1) / pairs : device_cus() * per_cu;
   int grid = want < cap ? want : cap;
   if (grid < 1) grid = 1;
   if (ntiles <= 0) return hipSuccess;
-  hipLaunchKernelGGL((k_gemv_ggml<T, NT, XS>), dim3(grid, pairs > 0 ? pairs : 1), dim3(256), lds,
-                     st, a);
+  hipLaunchKernelGGL((k_gemv_ggml<T, NT, XM, G>), dim3(grid, pairs > 0 ? pairs : 1), dim3(256),
+                     lds, st, a);
   return hipGetLastError();
 }
 
 template <int T, int NT>
-static hipError_t launch_ggml_t(const GemvArgs& a, hipStream_t st) {
-  return ggml_xs(a.d, NT) ? launch_ggml_x<T, NT, true>(a, st) : launch_ggml_x<T, NT, false>(a, st);
+static hipError_t launch_ggml_t(const GemvArgs& a, hipStream_t st, int pairs = 0) {
+  if constexpr (NT == 1 && (T == kGgmlQ4 || T == kGgmlQ5)) {
+    const int G = ggml_regs_g(T, a.d, NT);
+    if (G == 1) return launch_ggml_x<T, 1, kXmRegs, 1>(a, st, pairs);
+    if (G == 2) return launch_ggml_x<T, 1, kXmRegs, 2>(a, st, pairs);
+  }
+  return ggml_xs(a.d, NT) ? launch_ggml_x<T, NT, kXmLds>(a, st, pairs)
+                          : launch_ggml_x<T, NT, kXmLate>(a, st, pairs);
 }
 
 template <int T>
@@ -891,13 +907,9 @@ hipError_t gemv_ggml_pairs_launch(int type, const void* W, size_t eslice, const 
   a.eslice = eslice;
   a.xk = xk;
   a.E = E;
-  const bool xs = ggml_xs(d, 1);
-  if (type == kGgmlQ4)
-    return xs ? launch_ggml_x<kGgmlQ4, 1, true>(a, st, P) : launch_ggml_x<kGgmlQ4, 1, false>(a, st, P);
-  if (type == kGgmlQ5)
-    return xs ? launch_ggml_x<kGgmlQ5, 1, true>(a, st, P) : launch_ggml_x<kGgmlQ5, 1, false>(a, st, P);
-  if (type == kGgmlQ6)
-    return xs ? launch_ggml_x<kGgmlQ6, 1, true>(a, st, P) : launch_ggml_x<kGgmlQ6, 1, false>(a, st, P);
+  if (type == kGgmlQ4) return launch_ggml_t<kGgmlQ4, 1>(a, st, P);
+  if (type == kGgmlQ5) return launch_ggml_t<kGgmlQ5, 1>(a, st, P);
+  if (type == kGgmlQ6) return launch_ggml_t<kGgmlQ6, 1>(a, st, P);
   return hipErrorInvalidValue;
 }
 

@@ -24,6 +24,7 @@
 
 #include "qr_blk.h"
 #include "qr_ggml_elem.h"
+#include "qr_tiled.h"
 
 namespace qr {
 
@@ -109,6 +110,74 @@ __device__ inline void quantize_q8k_lds(const float* __restrict__ x, size_t xstr
   }
 }
 
+// The same quantization from registers: thread tid of the workgroup holds the
+// 8 values of group tid + 256 k in v[2 k], v[2 k + 1] (elements 8 (tid + 256 k)
+// onward), so a 256-element block is the 32 groups of one half-wave.  d is a
+// multiple of 256, so a half-wave's groups are all inside the activation or
+// all past it.  Every thread of the workgroup calls it.
+template <int G>
+__device__ inline void quantize_q8k_regs(const float4 (&v)[2 * G], int d, uint8_t* act, int tid) {
+  const int ngr = d >> 3;
+#pragma unroll
+  for (int k = 0; k < G; k++) {
+    const int gi = tid + 256 * k;
+    const bool live = gi < ngr;
+    float x[8] = {v[2 * k].x, v[2 * k].y, v[2 * k].z, v[2 * k].w,
+                  v[2 * k + 1].x, v[2 * k + 1].y, v[2 * k + 1].z, v[2 * k + 1].w};
+    const int tq = gi & 31;  // the group's place in its block
+    float best = 0.0f, vmax = 0.0f;
+    int bi = 1 << 30;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float ax = __builtin_fabsf(x[i]);
+      if (ax > best) {
+        best = ax;
+        vmax = x[i];
+        bi = 8 * tq + i;
+      }
+    }
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) {
+      const float ob = __shfl_xor(best, o);
+      const float ov = __shfl_xor(vmax, o);
+      const int oi = __shfl_xor(bi, o);
+      if (ob > best || (ob == best && oi < bi)) {
+        best = ob;
+        vmax = ov;
+        bi = oi;
+      }
+    }
+    int q[8];
+    float dd;
+    if (best == 0.0f) {  // an all-zero block (or only NaNs): d = 0, zero quants
+#pragma unroll
+      for (int i = 0; i < 8; i++) q[i] = 0;
+      dd = 0.0f;
+    } else {
+      const float iscale = -127.f / vmax;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int r = (int)__builtin_rintf(iscale * x[i]);
+        q[i] = r < 127 ? r : 127;
+      }
+      dd = 1.0f / iscale;
+    }
+    // bsum of the 16 elements of groups tq and tq ^ 1
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) s += q[i];
+    s += __shfl_xor(s, 1);
+    if (live) {
+      uint8_t* blk = act + (size_t)(gi >> 5) * kQ8kBlk;
+      const int m = tq >> 2, tb = tq & 3;  // element 8 tq + i: dword 8 m + i, byte tb
+#pragma unroll
+      for (int i = 0; i < 8; i++) blk[(m * 8 + i) * 4 + tb] = (uint8_t)(int8_t)q[i];
+      if ((tq & 1) == 0) reinterpret_cast<int*>(blk + 260)[tq >> 1] = s;
+      if (tq == 0) *reinterpret_cast<float*>(blk + 256) = dd;
+    }
+  }
+}
+
 // Dword i of the lane's block in LDS (its 144 / 176 / 210 bytes at `o`;
 // 210-byte blocks of odd lanes start 2 bytes past a dword).
 template <int T>
@@ -117,12 +186,23 @@ __device__ inline uint32_t gblk_u32(const uint32_t* lds, int o, int i) {
   else return lds[(o >> 2) + i];
 }
 
-// Transpose of 8 dwords D (32 bytes): result l holds bytes l, 8 + l, 16 + l,
+// Transpose of 8 dwords D (32 bytes): o[l] holds bytes l, 8 + l, 16 + l,
 // 24 + l -- byte (l & 3) of D[l >> 2], D[2 + (l >> 2)], D[4 + ...], D[6 + ...].
-__device__ inline uint32_t gtr(const uint32_t (&D)[8], int l) {
-  const int s = 8 * (l & 3), h = l >> 2;
-  return ((D[h] >> s) & 0xFFu) | (((D[2 + h] >> s) & 0xFFu) << 8) |
-         (((D[4 + h] >> s) & 0xFFu) << 16) | (((D[6 + h] >> s) & 0xFFu) << 24);
+// Byte selects (v_perm: selector bytes 0-3 pick the second operand's bytes,
+// 4-7 the first's), two per result: first the byte pairs of D[h], D[2 + h]
+// and of D[4 + h], D[6 + h], then the pairs side by side.
+__device__ inline void gtr8(const uint32_t (&D)[8], uint32_t (&o)[8]) {
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const uint32_t p01 = __builtin_amdgcn_perm(D[2 + h], D[h], 0x05010400u);
+    const uint32_t p23 = __builtin_amdgcn_perm(D[2 + h], D[h], 0x07030602u);
+    const uint32_t q01 = __builtin_amdgcn_perm(D[6 + h], D[4 + h], 0x05010400u);
+    const uint32_t q23 = __builtin_amdgcn_perm(D[6 + h], D[4 + h], 0x07030602u);
+    o[4 * h + 0] = __builtin_amdgcn_perm(q01, p01, 0x05040100u);
+    o[4 * h + 1] = __builtin_amdgcn_perm(q01, p01, 0x07060302u);
+    o[4 * h + 2] = __builtin_amdgcn_perm(q23, p23, 0x05040100u);
+    o[4 * h + 3] = __builtin_amdgcn_perm(q23, p23, 0x07060302u);
+  }
 }
 
 // a - 32 for four bytes a in 0..63, as signed bytes (no borrow across bytes).
@@ -165,27 +245,31 @@ __device__ inline void ggml_block_ints(const uint32_t* lds, int o, const uint8_t
     for (int t = 0; t < NT; t++) {
       const int* bs = reinterpret_cast<const int*>(act + (size_t)t * tokb + 260);
       int s = 0;
+      // |bs[2 j] + bs[2 j + 1]| < 2^12, mn < 64: 24-bit products
 #pragma unroll
-      for (int j = 0; j < 16; j++) s += __mul24(bs[j], mn[j >> 1]);  // |bs| < 2^11, mn < 64
+      for (int j = 0; j < 8; j++) s += __mul24(bs[2 * j] + bs[2 * j + 1], mn[j]);
       sumi[t] = s;
     }
-    uint32_t H[8];
+    uint32_t HT[8];
     if constexpr (T == kGgmlQ5) {
+      uint32_t H[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) H[i] = gblk_u32<T>(lds, o, 4 + i);
+      gtr8(H, HT);
     }
     constexpr int QS = T == kGgmlQ4 ? 4 : 12;  // dword of qs[0]
 #pragma unroll
     for (int g = 0; g < 4; g++) {  // 64-element groups: sub-blocks 2 g (low), 2 g + 1 (high)
-      uint32_t D[8];
+      uint32_t D[8], WT[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) D[i] = gblk_u32<T>(lds, o, QS + 8 * g + i);
+      gtr8(D, WT);
 #pragma unroll
       for (int l = 0; l < 8; l++) {
-        const uint32_t w = gtr(D, l);
+        const uint32_t w = WT[l];
         uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
         if constexpr (T == kGgmlQ5) {
-          const uint32_t h = gtr(H, l);
+          const uint32_t h = HT[l];
           lo |= ((h >> (2 * g)) & 0x01010101u) << 4;
           hi |= ((h >> (2 * g + 1)) & 0x01010101u) << 4;
         }
@@ -211,16 +295,19 @@ __device__ inline void ggml_block_ints(const uint32_t* lds, int o, const uint8_t
     }
 #pragma unroll
     for (int n = 0; n < 2; n++) {  // 128-element halves
-      uint32_t L0[8], L1[8], H[8];
+      uint32_t L0[8], L1[8], H[8], T0[8], T1[8], TH[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         L0[i] = gblk_u32<T>(lds, o, 16 * n + i);
         L1[i] = gblk_u32<T>(lds, o, 16 * n + 8 + i);
         H[i] = gblk_u32<T>(lds, o, 32 + 8 * n + i);
       }
+      gtr8(L0, T0);
+      gtr8(L1, T1);
+      gtr8(H, TH);
 #pragma unroll
       for (int l = 0; l < 8; l++) {
-        const uint32_t t0 = gtr(L0, l), t1 = gtr(L1, l), th = gtr(H, l);
+        const uint32_t t0 = T0[l], t1 = T1[l], th = TH[l];
         uint32_t A[4];
         A[0] = minus32((t0 & 0x0F0F0F0Fu) | ((th & 0x03030303u) << 4));
         A[1] = minus32((t1 & 0x0F0F0F0Fu) | (((th >> 2) & 0x03030303u) << 4));
@@ -247,13 +334,24 @@ __device__ inline void ggml_block_ints(const uint32_t* lds, int o, const uint8_t
 
 namespace qr {
 
-// The GEMV: persistent waves, one tile in flight per wave, NT tokens.  XS:
-// the fp32 activation is first moved into LDS by DMA, then each wave's first
-// tile DMA is issued, and the quantizer waits only for the activation (the
-// wave's operations complete in issue order); without XS (activations beyond
-// kXsMax) it is read and quantized before the first tile is requested.
-template <int T, int NT, bool XS>
+// The GEMV: persistent waves, one tile in flight per wave, NT tokens.  The
+// start-up, three forms (XM):
+//   kXmRegs (one token, d <= 256 G, Q4_K / Q5_K): one asm block per thread
+//            loads its G groups of 8 activation values and issues the wave's
+//            first tile DMA behind them, then waits for the values only; the
+//            workgroup quantizes from registers while the tiles land, and
+//            the workgroup needs no LDS for the fp32 activation.
+//   kXmLds   (activations up to kXsMax): the fp32 activation is first moved
+//            into LDS by DMA, then each wave's first tile DMA is issued, and
+//            the quantizer waits only for the activation (the wave's
+//            operations complete in issue order).
+//   kXmLate  (larger activations): it is read and quantized before the first
+//            tile is requested.
+enum { kXmRegs = 0, kXmLds = 1, kXmLate = 2 };
+
+template <int T, int NT, int XM, int G = 1>
 __global__ __launch_bounds__(256) void k_gemv_ggml(GemvArgs g) {
+  constexpr bool XS = XM == kXmLds;
   extern __shared__ __align__(16) uint8_t smem[];
   if (g.eidx) {  // pair mode: this workgroup row's expert, activation row and output row
     const int p = blockIdx.y;
@@ -284,7 +382,37 @@ __global__ __launch_bounds__(256) void k_gemv_ggml(GemvArgs g) {
     const int rows = min(RB, g.n - t * RB);
     tile_dma<NDMA>(g.W + (size_t)t * RB * rb, slot, rows * (int)rb, lane);
   };
-  if constexpr (XS) {
+  if constexpr (XM == kXmRegs) {
+    static_assert(NT == 1 && (T == kGgmlQ4 || T == kGgmlQ5), "register start-up");
+    const int tid = threadIdx.x;
+    const float* xp[G];
+#pragma unroll
+    for (int k = 0; k < G; k++) {
+      const int gi = tid + 256 * k;
+      xp[k] = g.X + 8 * (size_t)(gi < (g.d >> 3) ? gi : 0);
+    }
+    float4 v[2 * G];
+    const bool has = tile < ntiles;
+    if (has) {
+      const int rows = min(RB, g.n - tile * RB);
+      const int valid = rows * (int)rb;
+      const uint8_t* tb = g.W + (size_t)tile * RB * rb;
+      const uint8_t* src[NDMA];
+#pragma unroll
+      for (int k = 0; k < NDMA; k++) {
+        const int off = k * 1024 + lane * 16;
+        src[k] = tb + (off < valid ? off : 0);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      tiled_pro_asm<NDMA, G>(xp, src, lds_u32addr(slot), v);
+    } else {
+      tiled_x_asm<G>(xp, v);
+    }
+    quantize_q8k_regs<G>(v, g.d, act, tid);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (!has) return;  // no barriers below
+  } else if constexpr (XS) {
     stage_act_dma(g.X, (size_t)g.xstride, NT, g.d, smem, wave, lane);
     const bool has = tile < ntiles;
     dma(tile);

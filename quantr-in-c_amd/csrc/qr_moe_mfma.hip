@@ -60,6 +60,10 @@ struct MF {
   static constexpr bool kMin = TYPE == QR_T_Q4_K || TYPE == QR_T_Q5_K;
 };
 
+// The bits of the float 1.5 * 2^23: adding an integer |S| < 2^22 to them
+// gives the bits of the float 1.5 * 2^23 + S.
+constexpr int kQ6Magic = 0x4B400000;
+
 // Four bits (bits 0..3 of x) to bit 4 of 4 bytes.
 __device__ inline uint32_t bits4_to_b4(uint32_t x) { return spread4(x) << 4; }
 
@@ -502,20 +506,38 @@ __global__ __launch_bounds__(64 * NW) void k_expert_mfma(MfmaArgs a) {
             const float bd = *reinterpret_cast<const float*>(rec + 32);
             const float bsf = *reinterpret_cast<const float*>(rec + 36);
             const int bs = *reinterpret_cast<const int*>(rec + 40);
+            // Q6_K: the accumulator starts at the bits of 1.5 * 2^23, so each
+            // exact sum S (|S| <= 32 * 63 * 127 < 2^22) comes out as the bits
+            // of the float 1.5 * 2^23 + S; less 1.5 * 2^23 + 32 bs (exact
+            // too) that is (float)(S - 32 bs) in one exact subtraction, the
+            // value the reference's (float)isum holds
+            const float q6m = __builtin_bit_cast(float, kQ6Magic + 32 * bs);
 #pragma unroll
             for (int m = 0; m < NMAT; m++)
 #pragma unroll
               for (int r = 0; r < RA; r++) {
-                const v4i zero = {0, 0, 0, 0};
-                const v4i Dv = __builtin_amdgcn_mfma_i32_16x16x32_i8(Wq[m][r], B, zero, 0, 0, 0);
+                const v4i c0 = TYPE == QR_T_Q6_K ? v4i{kQ6Magic, kQ6Magic, kQ6Magic, kQ6Magic}
+                                                 : v4i{0, 0, 0, 0};
+                const v4i Dv = __builtin_amdgcn_mfma_i32_16x16x32_i8(Wq[m][r], B, c0, 0, 0, 0);
                 const int si = (m * 8 + s) * WR + 16 * r + 4 * kg;
                 const float4 sc4 = *reinterpret_cast<const float4*>(scl + si);
                 const float4 mn4 = *reinterpret_cast<const float4*>(mnl + si);
                 const float scv[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
                 const float mnv[4] = {mn4.x, mn4.y, mn4.z, mn4.w};
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                  acc[m][r][j][i] += term_of(scv[i], mnv[i], Dv[i], bd, bsf, bs);
+                for (int i = 0; i < 4; i++) {
+                  if constexpr (TYPE == QR_T_Q6_K) {
+                    // each element passes through an empty asm before its
+                    // float view: without it this compiler (ROCm 7.2 clang)
+                    // folds the four subtractions of the float views of an
+                    // MFMA result's elements into one, on element 0
+                    int di = Dv[i];
+                    asm("" : "+v"(di));
+                    acc[m][r][j][i] += scv[i] * (__builtin_bit_cast(float, di) - q6m) * bd;
+                  } else {
+                    acc[m][r][j][i] += term_of(scv[i], mnv[i], Dv[i], bd, bsf, bs);
+                  }
+                }
               }
           }
         }
