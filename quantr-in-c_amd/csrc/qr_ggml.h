@@ -258,7 +258,10 @@ __device__ inline void ggml_block_ints(const uint32_t* lds, int o, const uint8_t
       gtr8(H, HT);
     }
     constexpr int QS = T == kGgmlQ4 ? 4 : 12;  // dword of qs[0]
-#pragma unroll
+    // one token: the four groups unrolled together; more tokens: one group
+    // after the other (unrolled, their values would hold too many registers)
+    constexpr int GU = NT == 1 ? 4 : 1;
+#pragma unroll GU
     for (int g = 0; g < 4; g++) {  // 64-element groups: sub-blocks 2 g (low), 2 g + 1 (high)
       uint32_t D[8], WT[8];
 #pragma unroll
@@ -293,8 +296,13 @@ __device__ inline void ggml_block_ints(const uint32_t* lds, int o, const uint8_t
 #pragma unroll
       for (int k = 0; k < 4; k++) sc[4 * i + k] = (int)(int8_t)((w >> (8 * k)) & 0xFFu);
     }
-#pragma unroll
+    // the halves likewise; a half's scales are picked without indexing
+    constexpr int HU = NT == 1 ? 2 : 1;
+#pragma unroll HU
     for (int n = 0; n < 2; n++) {  // 128-element halves
+      int scn[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) scn[i] = n ? sc[8 + i] : sc[i];
       uint32_t L0[8], L1[8], H[8], T0[8], T1[8], TH[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) {
@@ -322,7 +330,7 @@ __device__ inline void ggml_block_ints(const uint32_t* lds, int o, const uint8_t
             const int xv = (int)xt[m * 8 + l];
             const int s0 = __builtin_amdgcn_sdot4((int)(A[s] & 0x0000FFFFu), xv, 0, false);
             const int s1 = __builtin_amdgcn_sdot4((int)(A[s] & 0xFFFF0000u), xv, 0, false);
-            aux[t][l] += __mul24(sc[2 * m], s0) + __mul24(sc[2 * m + 1], s1);  // |s| < 2^14
+            aux[t][l] += __mul24(scn[2 * s], s0) + __mul24(scn[2 * s + 1], s1);  // |s| < 2^14
           }
         }
       }
@@ -349,8 +357,12 @@ namespace qr {
 //            tile is requested.
 enum { kXmRegs = 0, kXmLds = 1, kXmLate = 2 };
 
+// Q4_K with the register start-up fits four workgroups to a CU by LDS; at
+// most 128 registers a lane keep four waves on each SIMD.
 template <int T, int NT, int XM, int G = 1>
-__global__ __launch_bounds__(256) void k_gemv_ggml(GemvArgs g) {
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(T == kGgmlQ4 && XM == kXmRegs ? 4 : 1)))
+void k_gemv_ggml(GemvArgs g) {
   constexpr bool XS = XM == kXmLds;
   extern __shared__ __align__(16) uint8_t smem[];
   if (g.eidx) {  // pair mode: this workgroup row's expert, activation row and output row
