@@ -100,6 +100,12 @@ __device__ inline void quant_rows_group(const float* __restrict__ x, int xstride
 // one expert keep their order): perm[offsets[e] + i] = the i-th pair of e,
 // inv[p] = its position (-1 for an index outside 0..E-1).  `idx` may point
 // to global or LDS memory.
+//
+// Wave w owns the pairs of one contiguous range (ranges in wave order), so a
+// pair's position is offsets[e] + (pairs of e in the ranges of waves before
+// w) + (pairs of e before it in w's range): the first term and the second
+// come from per-wave counts, the third from a running per-wave count and the
+// wave's ballots over each 64 pairs.
 // ---------------------------------------------------------------------------
 constexpr int kDispThreads = 1024;
 constexpr int kDispWaves = kDispThreads / 64;
@@ -109,23 +115,36 @@ __device__ inline void dispatch_wg(const int32_t* idx, int P, int E, int tile,
                                    int32_t* __restrict__ tiles, int32_t* __restrict__ perm,
                                    int32_t* __restrict__ inv) {
   __shared__ int cnt[256];
-  __shared__ int off[257];
-  __shared__ int run[256];
-  __shared__ int wtab[kDispWaves][256];
+  __shared__ int wcnt[kDispWaves][256];  // the wave's counts, then its running position
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  for (int e = tid; e < E; e += kDispThreads) {
-    cnt[e] = 0;
-    run[e] = 0;
+  const int per = ((P + kDispWaves - 1) / kDispWaves + 63) & ~63;  // whole rounds of 64
+  const int p0 = wave * per, p1 = min(P, p0 + per);
+  for (int i = tid; i < kDispWaves * 256; i += kDispThreads) (&wcnt[0][0])[i] = 0;
+  __syncthreads();
+  // the indices are read four rounds at a time, so their loads overlap
+  for (int b = p0; b < p1; b += 4 * 64) {  // wave-uniform
+    int ev[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int p = b + 64 * k + lane;
+      ev[k] = p < p1 ? idx[p] : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if (ev[k] >= 0 && ev[k] < E) atomicAdd(&wcnt[wave][ev[k]], 1);  // a count: order-free
   }
   __syncthreads();
-  for (int p = tid; p < P; p += kDispThreads) {
-    const int e = idx[p];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);  // a count: order-free
+  for (int e = tid; e < E; e += kDispThreads) {
+    int c = 0;
+#pragma unroll
+    for (int w = 0; w < kDispWaves; w++) c += wcnt[w][e];
+    cnt[e] = c;
   }
   __syncthreads();
   if (wave == 0) {
     // exclusive scans of the counts and of the tiles per expert: lane l owns
-    // experts 4l .. 4l+3, then an inclusive scan across the wave
+    // experts 4l .. 4l+3, then an inclusive scan across the wave; the first
+    // position of expert e goes back to cnt[e]
     int c[4], tl[4], cs = 0, ts = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -149,7 +168,7 @@ __device__ inline void dispatch_wg(const int32_t* idx, int P, int E, int tile,
     for (int i = 0; i < 4; i++) {
       const int e = 4 * lane + i;
       if (e < E) {
-        off[e] = acc;
+        cnt[e] = acc;
         counts[e] = c[i];
         offsets[e] = acc;
         if (tiles) tiles[e] = tacc;
@@ -158,46 +177,55 @@ __device__ inline void dispatch_wg(const int32_t* idx, int P, int E, int tile,
       tacc += tl[i];
     }
     if (lane == 63) {
-      off[E] = ci;
       offsets[E] = ci;
       if (tiles) tiles[E] = ti;
     }
   }
   __syncthreads();
-  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int c0 = 0; c0 < P; c0 += kDispThreads) {
-    for (int i = tid; i < kDispWaves * 256; i += kDispThreads) (&wtab[0][0])[i] = 0;
-    __syncthreads();
-    const int p = c0 + tid;
-    int e = p < P ? idx[p] : -1;
-    if (e >= E) e = -1;
-    const bool valid = e >= 0;
-    // lanes of this wave holding the same expert: match the 8 expert bits
-    uint64_t peers = __ballot(valid);
+  // each wave's first position per expert
+  for (int e = tid; e < E; e += kDispThreads) {
+    int run = cnt[e];
 #pragma unroll
-    for (int b = 0; b < 8; b++) {
-      const bool bit = valid && ((e >> b) & 1);
-      const uint64_t m = __ballot(bit);
-      peers &= bit ? m : ~m;
+    for (int w = 0; w < kDispWaves; w++) {
+      const int c = wcnt[w][e];
+      wcnt[w][e] = run;
+      run += c;
     }
-    const int rank = __popcll(peers & lt);
-    if (valid && rank == 0) wtab[wave][e] = __popcll(peers);
-    __syncthreads();
-    if (valid) {
-      int base = off[e] + run[e] + rank;
-      for (int w = 0; w < wave; w++) base += wtab[w][e];
-      perm[base] = p;
-      inv[p] = base;
-    } else if (p < P) {
-      inv[p] = -1;
+  }
+  __syncthreads();
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int b = p0; b < p1; b += 4 * 64) {  // wave-uniform
+    int ev[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int p = b + 64 * r + lane;
+      ev[r] = p < p1 ? idx[p] : -1;
     }
-    __syncthreads();
-    for (int ee = tid; ee < E; ee += kDispThreads) {
-      int s = 0;
-      for (int w = 0; w < kDispWaves; w++) s += wtab[w][ee];
-      run[ee] += s;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {  // rounds of 64 pairs, in order
+      const int p = b + 64 * r + lane;
+      const int e = ev[r] < E ? ev[r] : -1;
+      const bool valid = e >= 0;
+      // lanes of this round holding the same expert: match the 8 expert bits
+      uint64_t peers = __ballot(valid);
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const bool bit = valid && ((e >> k) & 1);
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+      }
+      const int rank = __popcll(peers & lt);
+      if (valid) {
+        const int pos = wcnt[wave][e] + rank;
+        perm[pos] = p;
+        inv[p] = pos;
+      } else if (p < p1) {
+        inv[p] = -1;
+      }
+      // the wave's LDS operations complete in order: every lane's read above
+      // precedes the first lane's update, which the next round's reads see
+      if (valid && rank == 0) wcnt[wave][e] += __popcll(peers);
     }
-    __syncthreads();
   }
 }
 
