@@ -246,11 +246,12 @@ def bench_sweep(dev, types, warmup, pool_bytes=600 << 20, max_steps=2048, only=N
                         key, ms * 1e3, alg / (ms / 1e3) / 1e9, res[key]["frac"]))
                     xb.free()
                     yb.free()
-            if qtype in (Q.TYPE_Q4_K, Q.TYPE_Q5_K, Q.TYPE_Q8_0) or (
-                    qtype == Q.TYPE_Q6_K and d % 2048 == 0):
+            if qtype in (Q.TYPE_Q4_K, Q.TYPE_Q5_K, Q.TYPE_Q6_K, Q.TYPE_Q8_0):
                 # the same shapes in the tiled layout: a pool of tiled copies of the
-                # first n rows (Q6_K: rows of whole 2048-element multiples)
+                # first n rows (Q6_K: n * (d / 256) a multiple of 8)
                 for n, _ in shapes:
+                    if qtype == Q.TYPE_Q6_K and (n * (d // 256)) % 8:
+                        continue
                     wb = n * rb
                     copies_t = max(1, math.ceil(pool_bytes / wb))
                     tpool = dev.alloc(wb * copies_t)

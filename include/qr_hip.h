@@ -162,14 +162,14 @@ int qr_gemv_rows(qr_ctx* ctx, int order, uint32_t type, const void* w, const flo
  * super-block, or 8 Q8_0 blocks) and a tile is 64 / (d / 256) rows; within
  * it, the k-th 16-byte chunk of every lane is stored together (Q4_K / Q5_K:
  * the header chunk first; Q6_K: its scales, then each unit pair's high bits
- * and low nibbles, the lanes' fp16 d fields after the chunks; Q8_0: the 8
- * scales, then the blocks' values).  Pass `type | QR_TILED` to qr_gemv /
- * qr_gemv_ex / qr_gemv_ord (no integer sums; Q8_0 in QR_ORDER_SEQ only) and in
- * a decoder model's wq / wk / wv / wo / wcls types.  qr_weights_tile writes
- * the tiled copy of an n x d matrix (d a multiple of 256, at most 16384; Q6_K
- * a multiple of 2048) into dst, qr_weights_untile the reverse; device
- * pointers, 16-byte aligned, not overlapping; enqueued on the context
- * stream.  qr_row_bytes(type | QR_TILED, d) is the plain row size. */
+ * and low nibbles, and the fp16 d fields of all super-blocks after all the
+ * tiles, in row-major order; Q8_0: the 8 scales, then the blocks' values).
+ * Pass `type | QR_TILED` to qr_gemv / qr_gemv_ex / qr_gemv_ord (no integer
+ * sums; Q8_0 in QR_ORDER_SEQ only) and in a decoder model's wq / wk / wv / wo
+ * / wcls types.  qr_weights_tile writes the tiled copy of an n x d matrix (d
+ * a multiple of 256, at most 16384; Q6_K with n * (d / 256) a multiple of 8)
+ * into dst, qr_weights_untile the reverse; device pointers, 16-byte aligned,
+ * not overlapping; enqueued on the context stream.  qr_row_bytes(type | QR_TILED, d) is the plain row size. */
 #define QR_TILED 0x100u
 
 /* llama.cpp / ggml's own K-quant layouts (ggml-common.h: block_q4_K with its
@@ -359,10 +359,10 @@ typedef struct qr_decoder qr_decoder;
  * the whole q vector, as there).  `order` is the reference build
  * (QR_ORDER_*): the order of the fp32 matmuls and the router, and of the
  * Q8_0 dot.  Where a layer's wq and wk are one tiled Q4_K / Q5_K matrix
- * (wk's bytes right after wq's) and wv is Q6_K (rows a multiple of 2048) or
- * C99-order Q8_0, the decoder keeps a tiled copy of a row-major wv (about
- * rows x row bytes per layer) so that the norm, q / k and v run as one
- * launch. */
+ * (wk's bytes right after wq's) and wv is Q6_K (kv_dim * dim / 256 a
+ * multiple of 8) or C99-order Q8_0, the decoder keeps a tiled copy of a
+ * row-major wv (about rows x row bytes per layer) so that the norm, q / k and
+ * v run as one launch. */
 int qr_decoder_create(qr_ctx* ctx, const qr_model* model, int kv_type, int order, int page,
                       int flags, qr_decoder** out);
 int qr_decoder_destroy(qr_decoder* dec);

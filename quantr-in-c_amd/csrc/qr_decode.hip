@@ -1545,7 +1545,7 @@ hipError_t plan_wv_tiled(qr_decoder* d, hipStream_t s) {
     const int vb = (int)(vt & ~(uint32_t)QR_TILED);
     if ((vt & QR_GGML) || (vb != QR_T_Q6_K && vb != QR_T_Q8_0)) continue;
     if (vb == QR_T_Q8_0 && d->order != QR_ORDER_SEQ) continue;  // tiles take the C99 order
-    if (!gemv_norm2_ok(qb, vb, d->dim)) continue;
+    if (!gemv_norm2_ok(qb, vb, d->kvd, d->dim)) continue;
     d->wv_tiled_type[l] = vb;
     if (vt & QR_TILED) {
       d->wv_tiled[l] = L.wv;

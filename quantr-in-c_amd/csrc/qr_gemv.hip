@@ -512,11 +512,11 @@ static size_t sq_lds_bytes(int type, int d, int nt, int nw) {
   return align16((size_t)nt * act_tok_bytes(d)) + (size_t)nw * sq_slot_kib(type) * 1024;
 }
 
-bool gemv_tiled_ok(int type, int d, int nt, int q8o) {
+bool gemv_tiled_ok(int type, int n, int d, int nt, int q8o) {
   if (!(nt >= 1 && nt <= 4) && nt != 8) return false;
   if (type == QR_T_Q6_K || type == QR_T_Q8_0) {
     // the Q8_0 lane orders keep eight accumulators per row: streaming engine only
-    if (!sq_shape_ok(type, d) || (type == QR_T_Q8_0 && q8o != kQ8Seq)) return false;
+    if (!sq_shape_ok(type, n, d) || (type == QR_T_Q8_0 && q8o != kQ8Seq)) return false;
     return sq_lds_bytes(type, d, nt == 8 ? 4 : nt, 2) <= kLdsMax;
   }
   if (type != QR_T_Q4_K && type != QR_T_Q5_K) return false;
@@ -648,7 +648,7 @@ hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, 
   a.acc = nullptr;
   a.accb = nullptr;
   if (type == QR_T_Q6_K || type == QR_T_Q8_0) {
-    if (!gemv_tiled_ok(type, d, nt, q8o)) return hipErrorInvalidValue;
+    if (!gemv_tiled_ok(type, n, d, nt, q8o)) return hipErrorInvalidValue;
     const SqGeom g = sq_geom(type, n, d);
     a.t_nb = g.nb;
     a.t_rb = g.RB;
@@ -704,8 +704,9 @@ static size_t norm2_lds(int ta, int tb, int d) {
   return la > lb ? la : lb;
 }
 
-bool gemv_norm2_ok(int ta, int tb, int d) {
-  return gemv_tiled_norm_ok(ta, d) && (tb == QR_T_Q6_K || tb == QR_T_Q8_0) && sq_shape_ok(tb, d) &&
+bool gemv_norm2_ok(int ta, int tb, int nb_rows, int d) {
+  return gemv_tiled_norm_ok(ta, d) && (tb == QR_T_Q6_K || tb == QR_T_Q8_0) &&
+         sq_shape_ok(tb, nb_rows, d) &&
          norm2_lds(ta, tb, d) <= kLdsMax;
 }
 
@@ -736,7 +737,7 @@ static hipError_t launch_norm2(const GemvArgs& a, const GemvArgs& b, hipStream_t
 hipError_t gemv_norm2_launch(int ta, const void* Wa, float* Ya, int na, int tb, const void* Wb,
                              float* Yb, int nb_rows, const float* x, const float* nw, float* xb,
                              int d, hipStream_t st) {
-  if (!gemv_norm2_ok(ta, tb, d) || na <= 0 || nb_rows <= 0) return hipErrorInvalidValue;
+  if (!gemv_norm2_ok(ta, tb, nb_rows, d) || na <= 0 || nb_rows <= 0) return hipErrorInvalidValue;
   GemvArgs a{}, b{};
   a.W = static_cast<const uint8_t*>(Wa);
   b.W = static_cast<const uint8_t*>(Wb);

@@ -44,7 +44,7 @@ hipError_t gemv_launch(int type, int q8o, const void* W, const float* X, float* 
 // QR_T_Q5_K / QR_T_Q6_K / QR_T_Q8_0).
 // Q6_K / Q8_0 tiles (qr_tiled_sq.h) too; Q8_0 in the sequential dot order
 // only (q8o, kQ8Seq = 0).
-bool gemv_tiled_ok(int type, int d, int nt, int q8o = 0);
+bool gemv_tiled_ok(int type, int n, int d, int nt, int q8o = 0);
 hipError_t gemv_tiled_launch(int type, const void* W, const float* X, float* Y, int n, int d,
                              int nt, int xstride, int ystride, hipStream_t st, int q8o = 0,
                              const float* R = nullptr);
@@ -57,7 +57,7 @@ hipError_t gemv_tiled_norm_launch(int type, const void* W, const float* x, const
 // The same normalisation feeding two matrices in one launch: tiled Q4_K /
 // Q5_K A (na rows into Ya; xb from its workgroup 0) and tiled Q6_K / Q8_0 B
 // (nb rows into Yb; Q8_0 in the sequential dot order).
-bool gemv_norm2_ok(int ta, int tb, int d);
+bool gemv_norm2_ok(int ta, int tb, int nb_rows, int d);
 hipError_t gemv_norm2_launch(int ta, const void* Wa, float* Ya, int na, int tb, const void* Wb,
                              float* Yb, int nb, const float* x, const float* nw, float* xb, int d,
                              hipStream_t st);

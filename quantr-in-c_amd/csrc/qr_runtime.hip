@@ -486,8 +486,9 @@ static int tile_args(uint32_t type, const void* src, void* dst, int n, int d, co
   if (n < 0 || d <= 0 || (d & 255) || (d >> 8) > 64)
     return fail(QR_ERR_UNSUPPORTED, "%s: shape %d x %d (d a multiple of 256, at most 16384)", who,
                 n, d);
-  if (type == QR_T_Q6_K && d % 2048)
-    return fail(QR_ERR_UNSUPPORTED, "%s: tiled Q6_K needs d a multiple of 2048 (d=%d)", who, d);
+  if (type == QR_T_Q6_K && ((long)n * (d >> 8)) % 8)
+    return fail(QR_ERR_UNSUPPORTED,
+                "%s: tiled Q6_K needs n * (d / 256) a multiple of 8 (%d x %d)", who, n, d);
   if (n > 0 && (!src || !dst)) return fail(QR_ERR_INVALID, "%s: null pointer", who);
   if (!aligned(src, 16) || !aligned(dst, 16))
     return fail(QR_ERR_INVALID, "%s: src and dst must be 16-byte aligned", who);
@@ -581,7 +582,7 @@ int qr_gemv_ord(qr_ctx* c, int order, uint32_t type, const void* w, const float*
   }
   if (tiled) {
     if (acc || accb) return fail(QR_ERR_UNSUPPORTED, "qr_gemv: no integer sums on tiled weights");
-    if (!qr::gemv_tiled_ok((int)type, d, nt, order))
+    if (!qr::gemv_tiled_ok((int)type, n, d, nt, order))
       return fail(QR_ERR_UNSUPPORTED, "qr_gemv: tiled type %u at d=%d nt=%d order %d", type, d, nt,
                   order);
     QR_HIP(qr::gemv_tiled_launch((int)type, w, x, y, n, d, nt, xstride, ystride, c->stream, order),
@@ -767,8 +768,9 @@ int gemv_check(uint32_t type, int order, const void* w, int n, int d, const char
   if (type & QR_TILED) {
     type &= ~(uint32_t)QR_TILED;
     if (n <= 0 || d <= 0) return fail(QR_ERR_INVALID, "%s: weight shape %d x %d", who, n, d);
-    if (!gemv_tiled_ok((int)type, d, 1, order))
-      return fail(QR_ERR_UNSUPPORTED, "%s: tiled type %u at d=%d (order %d)", who, type, d, order);
+    if (!gemv_tiled_ok((int)type, n, d, 1, order))
+      return fail(QR_ERR_UNSUPPORTED, "%s: tiled type %u at %d x %d (order %d)", who, type, n, d,
+                  order);
     if (w && !aligned(w, 16)) return fail(QR_ERR_INVALID, "%s: weights must be 16-byte aligned", who);
     return QR_OK;
   }

@@ -13,11 +13,12 @@
 //   Q6_K (a 210-byte super-block per lane, src/quant.c:220-226: ql[128],
 //   qh[64], int8 scales[16], fp16 d): 13 chunks in consumption order --
 //   the scales, then for each pair of 32-element units the 16 qh bytes of the
-//   pair and the 16 ql bytes of each unit -- and after the 13 L chunks the L
-//   d fields, 2 bytes each (byte 208 L + 2 l of the tile), which the wave
-//   moves with one more DMA instruction (its first L / 8 lanes, 16 bytes
-//   each), so rows must be whole multiples of 2048 elements (L a multiple of
-//   8 in every tile).
+//   pair and the 16 ql bytes of each unit -- so a tile is 208 L bytes; the d
+//   fields of all super-units follow all the tiles, 2 bytes each in row-major
+//   order (super-unit u's at byte 208 n nb + 2 u).  A tile's L fields are one
+//   2 L-byte run, which the wave moves with one more DMA instruction from the
+//   16-byte unit that holds its start; the matrix needs n nb a multiple of 8
+//   so that no such unit passes the end of the fields.
 //   Source chunk of tiled chunk k: 12, 8, 0, 1, 9, 2, 3, 10, 4, 5, 11, 6, 7.
 //
 //   Q8_0 (8 consecutive 34-byte blocks per lane, 272 bytes): 17 chunks --
@@ -43,7 +44,7 @@ template <>
 struct SqFmt<QR_T_Q6_K> {
   static constexpr int kBytes = QR_Q6K_BYTES;  // 210
   static constexpr int kChunks = 13;
-  static constexpr bool kTailD = true;  // the d fields after the chunks
+  static constexpr bool kTailD = true;  // the d fields after all the tiles
   static constexpr int kOps = 14;       // DMA instructions per tile: d fields, then chunks
 };
 template <>
@@ -57,15 +58,19 @@ struct SqFmt<QR_T_Q8_0> {
 __host__ __device__ inline int sq_bytes(int type) {
   return type == QR_T_Q6_K ? SqFmt<QR_T_Q6_K>::kBytes : SqFmt<QR_T_Q8_0>::kBytes;
 }
+// Tile bytes per lane: the chunks (Q6_K's d fields sit after all the tiles).
+__host__ __device__ inline int sq_lane_bytes(int type) {
+  return type == QR_T_Q6_K ? 16 * SqFmt<QR_T_Q6_K>::kChunks : SqFmt<QR_T_Q8_0>::kBytes;
+}
 // LDS slot KiB per wave (one per DMA instruction of a tile)
 __host__ __device__ inline int sq_slot_kib(int type) {
   return type == QR_T_Q6_K ? SqFmt<QR_T_Q6_K>::kOps : SqFmt<QR_T_Q8_0>::kOps;
 }
-// Rows of d elements the layout takes: whole super-units (and, for Q6_K,
-// whole multiples of 2048 so every tile's d fields are whole 16-byte units).
-__host__ __device__ inline bool sq_shape_ok(int type, int d) {
-  if (d <= 0 || (d & 255) || (d >> 8) > 64) return false;
-  return type == QR_T_Q8_0 || (type == QR_T_Q6_K && (d % 2048) == 0);
+// n rows of d elements the layout takes: whole super-units (and, for Q6_K,
+// n (d / 256) a multiple of 8: the d fields end on a 16-byte unit).
+__host__ __device__ inline bool sq_shape_ok(int type, int n, int d) {
+  if (n < 0 || d <= 0 || (d & 255) || (d >> 8) > 64) return false;
+  return type == QR_T_Q8_0 || (type == QR_T_Q6_K && ((long)n * (d >> 8)) % 8 == 0);
 }
 
 struct SqGeom {
@@ -79,7 +84,7 @@ __host__ __device__ inline SqGeom sq_geom(int type, int n, int d) {
   g.nb = d >> 8;
   g.RB = g.nb > 0 ? 64 / g.nb : 0;
   g.ntiles = g.RB > 0 ? (n + g.RB - 1) / g.RB : 0;
-  g.tile_bytes = (size_t)g.RB * g.nb * sq_bytes(type);
+  g.tile_bytes = (size_t)g.RB * g.nb * sq_lane_bytes(type);
   return g;
 }
 
@@ -117,10 +122,10 @@ __global__ __launch_bounds__(256) void k_tile_pack_sq(const uint8_t* __restrict_
     const int L = min(g.RB, n - t * g.RB) * g.nb;
     const size_t tbase = (size_t)t * g.tile_bytes;
     const size_t pbase = (size_t)su * BB;
-    if (k == NCH) {  // Q6_K's d
+    if (k == NCH) {  // Q6_K's d, after all the tiles in row-major order
 #pragma unroll
       for (int b = 0; b < 2; b++) {
-        const size_t tp = tbase + (size_t)208 * L + 2 * (size_t)l + b;
+        const size_t tp = (size_t)208 * n * g.nb + 2 * (size_t)su + b;
         const size_t pp = pbase + 208 + b;
         dst[reverse ? pp : tp] = src[reverse ? tp : pp];
       }
@@ -137,8 +142,12 @@ __global__ __launch_bounds__(256) void k_tile_pack_sq(const uint8_t* __restrict_
 
 // This lane's DMA sources in tile t: chunk k at src[k] (lanes past the tile
 // reload its first 16 bytes into slot bytes nobody reads) and, Q6_K, 16
-// bytes of the d fields at dsrc (lanes l < L / 8; the others the tile's first
-// 16 bytes again).
+// bytes of the d fields at dsrc: the tile's run of 2 L bytes starts sq_doff
+// bytes into a 16-byte unit, lane j takes unit j of the run (the lanes past
+// it the first unit again).
+__device__ inline int sq_doff(const GemvArgs& g, int t) {
+  return (int)(((size_t)2 * t * g.t_rb * g.t_nb) & 15);  // the fields start on a 16-byte unit
+}
 template <int TYPE>
 __device__ inline void sq_src(const GemvArgs& g, int t, int lane,
                               const uint8_t* (&src)[SqFmt<TYPE>::kChunks], const uint8_t*& dsrc) {
@@ -148,7 +157,14 @@ __device__ inline void sq_src(const GemvArgs& g, int t, int lane,
   const bool on = lane < L;
 #pragma unroll
   for (int k = 0; k < NCH; k++) src[k] = on ? base + (size_t)k * 16 * L + 16 * lane : base;
-  dsrc = lane < (L >> 3) ? base + (size_t)208 * L + 16 * lane : base;
+  if constexpr (SqFmt<TYPE>::kTailD) {
+    const size_t run = (size_t)208 * g.n * g.t_nb + (size_t)2 * t * g.t_rb * g.t_nb;
+    const uint8_t* unit0 = g.W + (run & ~(size_t)15);
+    const int units = (sq_doff(g, t) + 2 * L + 15) >> 4;
+    dsrc = lane < units ? unit0 + 16 * lane : unit0;
+  } else {
+    dsrc = base;
+  }
 }
 
 // The slot's KiB of the d fields (Q6_K): after the chunks.
@@ -174,7 +190,7 @@ __device__ inline void sq_dma(const uint8_t* const (&src)[SqFmt<TYPE>::kChunks],
 template <int TYPE, int K, bool RING>
 __device__ inline uint4 sq_chunk(const uint8_t* slot, uint32_t sbase, int lane,
                                  const uint8_t* const (&nsrc)[SqFmt<TYPE>::kChunks],
-                                 const uint8_t* ndsrc, float* dval) {
+                                 const uint8_t* ndsrc, float* dval, int doff = 0) {
   constexpr int NCH = SqFmt<TYPE>::kChunks;
   constexpr bool TD = SqFmt<TYPE>::kTailD;
   constexpr int AFTER_RING = NCH - 1 + ((TD && K >= 1) ? 1 : 0);
@@ -183,7 +199,7 @@ __device__ inline uint4 sq_chunk(const uint8_t* slot, uint32_t sbase, int lane,
   else wait_vmcnt<AFTER_LAST>();
   const uint4 v = *reinterpret_cast<const uint4*>(slot + K * 1024 + 16 * lane);
   if constexpr (TD && K == 0)  // the d fields landed before chunk 0 (issued first)
-    *dval = qr_h2f(*reinterpret_cast<const uint16_t*>(slot + kSqDSlot * 1024 + 2 * lane));
+    *dval = qr_h2f(*reinterpret_cast<const uint16_t*>(slot + kSqDSlot * 1024 + doff + 2 * lane));
   if constexpr (RING) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the reads are done before the refill
     if constexpr (TD && K == 0) lds_dma16_nt(ndsrc, sbase + (uint32_t)(kSqDSlot * 1024));
@@ -206,9 +222,10 @@ __device__ inline void sq_act(const uint8_t* act, int u, uint32_t (&xv)[8], floa
 template <int NT, bool RING>
 __device__ inline void sq_tile_q6(const uint8_t* slot, uint32_t sbase, int lane,
                                   const uint8_t* const (&nsrc)[13], const uint8_t* ndsrc,
-                                  const uint8_t* act, size_t tokb, int b, float (&terms)[NT][8]) {
+                                  const uint8_t* act, size_t tokb, int b, float (&terms)[NT][8],
+                                  int doff) {
   float d;
-  const uint4 sv = sq_chunk<QR_T_Q6_K, 0, RING>(slot, sbase, lane, nsrc, ndsrc, &d);
+  const uint4 sv = sq_chunk<QR_T_Q6_K, 0, RING>(slot, sbase, lane, nsrc, ndsrc, &d, doff);
   const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
   for (int p = 0; p < 4; p++) {
@@ -370,15 +387,16 @@ __device__ inline void sq_body(const GemvArgs& g, uint8_t* smem, int bid, int nb
   for (;;) {
     const int next = tile + tstep;
     float terms[NT][8];
+    const int doff = TYPE == QR_T_Q6_K ? sq_doff(g, tile) : 0;
     if (next < ntiles) {
       sq_src<TYPE>(g, next, lane, src, dsrc);
       if constexpr (TYPE == QR_T_Q6_K)
-        sq_tile_q6<NT, true>(slot, sbase, lane, src, dsrc, act, tokb, b, terms);
+        sq_tile_q6<NT, true>(slot, sbase, lane, src, dsrc, act, tokb, b, terms, doff);
       else
         sq_tile_q8<NT, true>(slot, sbase, lane, src, dsrc, act, tokb, b, terms);
     } else {
       if constexpr (TYPE == QR_T_Q6_K)
-        sq_tile_q6<NT, false>(slot, sbase, lane, src, dsrc, act, tokb, b, terms);
+        sq_tile_q6<NT, false>(slot, sbase, lane, src, dsrc, act, tokb, b, terms, doff);
       else
         sq_tile_q8<NT, false>(slot, sbase, lane, src, dsrc, act, tokb, b, terms);
     }

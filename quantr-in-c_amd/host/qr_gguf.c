@@ -647,13 +647,14 @@ static int tileable(uint32_t type, int cols) {
            cols / 256 <= 64;
 }
 
-/* The lm_head also in Q6_K, when its rows are whole multiples of 2048 (the
+/* The lm_head also in Q6_K, when rows x (cols / 256) is a multiple of 8 (the
  * Q6_K tiled layout's condition): the decode step reads it with the tiled
  * GEMV (the projections stay row-major in Q6_K, which the prompt's row
  * products read with int8 MFMA). */
-static int tileable_out(uint32_t type, int cols) {
-    return tileable(type, cols) || (type == QR_TYPE_Q6_K && cols > 0 && cols % 2048 == 0 &&
-                                    cols / 256 <= 64);
+static int tileable_out(uint32_t type, int rows, int cols) {
+    return tileable(type, cols) ||
+           (type == QR_TYPE_Q6_K && rows > 0 && cols > 0 && cols % 256 == 0 && cols / 256 <= 64 &&
+            ((long)rows * (cols / 256)) % 8 == 0);
 }
 
 static void plan_tile_if(copy_plan* p, uint32_t* type, int rows, int cols, int ok) {
@@ -681,7 +682,7 @@ static int plan_model(const qr_gguf* g, qr_gguf_model* gm, copy_plan* p) {
     ADD(m->rms_final, (size_t)m->dim * 4, &m->rms_final);
     if (!tied) {
         ADD(m->wcls, qr_row_bytes(m->wcls_type, m->dim) * (size_t)m->vocab, &m->wcls);
-        plan_tile_if(p, &m->wcls_type, m->vocab, m->dim, tileable_out(m->wcls_type, m->dim));
+        plan_tile_if(p, &m->wcls_type, m->vocab, m->dim, tileable_out(m->wcls_type, m->vocab, m->dim));
     }
     for (l = 0; l < m->n_layers; l++) {
         qr_layer* y = &gm->layers[l];

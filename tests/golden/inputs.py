@@ -308,9 +308,10 @@ def tile_sq(blob, qtype, n, d):
     """Row-major Q6_K / Q8_0 rows [n][row bytes] -> the tiled layout, written
     from its definition: 256 elements per lane (a Q6_K super-block, or 8
     Q8_0 blocks), RB = 64 / (d / 256) rows per tile, chunk k of lane l at
-    16 (k L + l) of the tile; Q6_K chunks in the order Q6_CHUNK_MAP with the
-    L d fields (2 bytes) after them; Q8_0 chunk 0 = the 8 scales, chunk
-    1 + 2 j + h = bytes 16 h .. 16 h + 15 of block j's values."""
+    16 (k L + l) of the tile; Q6_K chunks in the order Q6_CHUNK_MAP, and the
+    d fields (2 bytes) of every super-block after all the tiles, in row-major
+    order; Q8_0 chunk 0 = the 8 scales, chunk 1 + 2 j + h = bytes
+    16 h .. 16 h + 15 of block j's values."""
     nb = d // 256
     bb = 210 if qtype == TYPE_Q6_K else 272
     src = np.ascontiguousarray(blob, np.uint8).reshape(n * nb, bb)
@@ -331,6 +332,6 @@ def tile_sq(blob, qtype, n, d):
         lanes = slice(t0 * nb, (t0 + rows) * nb)
         for c in chunks:
             out.append(np.ascontiguousarray(c[lanes]).reshape(-1))
-        if tail is not None:
-            out.append(np.ascontiguousarray(tail[lanes]).reshape(-1))
+    if tail is not None:
+        out.append(np.ascontiguousarray(tail).reshape(-1))
     return np.concatenate(out)

@@ -121,14 +121,14 @@ def test_gemv_tiled_refusals(dev):
         dev.gemv(Q.TYPE_F32 | Q.TILED, wb.ptr, xb.ptr, yb.ptr, 64, 2048, 1)
     with pytest.raises(Q.QrError, match="tiled"):
         dev.gemv(Q.TYPE_Q4_K | Q.TILED, wb.ptr, xb.ptr, yb.ptr, 64, 1408, 1)
-    with pytest.raises(Q.QrError, match="tiled"):  # Q6_K tiles need whole 2048-element rows
-        dev.gemv(Q.TYPE_Q6_K | Q.TILED, wb.ptr, xb.ptr, yb.ptr, 16, 768, 1)
+    with pytest.raises(Q.QrError, match="tiled"):  # Q6_K tiles: n (d / 256) a multiple of 8
+        dev.gemv(Q.TYPE_Q6_K | Q.TILED, wb.ptr, xb.ptr, yb.ptr, 15, 768, 1)
     with pytest.raises(Q.QrError, match="order"):  # Q8_0 tiles: the sequential order only
         dev.gemv(Q.TYPE_Q8_0 | Q.TILED, wb.ptr, xb.ptr, yb.ptr, 64, 2048, 1, order=Q.ORDER_AVX2)
     with pytest.raises(Q.QrError, match="no tiled layout"):
         dev.tile(Q.TYPE_F32, wb.ptr, yb.ptr, 64, 2048)
-    with pytest.raises(Q.QrError, match="2048"):
-        dev.tile(Q.TYPE_Q6_K, wb.ptr, yb.ptr, 16, 768)
+    with pytest.raises(Q.QrError, match="multiple of 8"):
+        dev.tile(Q.TYPE_Q6_K, wb.ptr, yb.ptr, 15, 768)
     with pytest.raises(Q.QrError, match="overlap"):
         dev.tile(Q.TYPE_Q4_K, wb.ptr, wb.ptr, 64, 2048)
 
@@ -145,6 +145,8 @@ def sq_weights(seed, qtype, n, d):
 
 @pytest.mark.parametrize("qtype,n,d", [(Q.TYPE_Q6_K, 64, 2048), (Q.TYPE_Q6_K, 1001, 2048),
                                        (Q.TYPE_Q6_K, 9, 4096), (Q.TYPE_Q6_K, 3, 16384),
+                                       (Q.TYPE_Q6_K, 2048, 5632), (Q.TYPE_Q6_K, 40, 768),
+                                       (Q.TYPE_Q6_K, 336, 256), (Q.TYPE_Q6_K, 12, 5632),
                                        (Q.TYPE_Q8_0, 64, 2048), (Q.TYPE_Q8_0, 1001, 2048),
                                        (Q.TYPE_Q8_0, 77, 256), (Q.TYPE_Q8_0, 45, 5632),
                                        (Q.TYPE_Q8_0, 7, 768)])
@@ -165,6 +167,9 @@ def test_tile_layout_sq_and_inverse(dev, qtype, n, d):
                                        (Q.TYPE_Q6_K, 256, 2048), (Q.TYPE_Q6_K, 5632, 2048),
                                        (Q.TYPE_Q6_K, 512, 2048), (Q.TYPE_Q6_K, 1001, 2048),
                                        (Q.TYPE_Q6_K, 13, 4096), (Q.TYPE_Q6_K, 7, 16384),
+                                       (Q.TYPE_Q6_K, 2048, 5632), (Q.TYPE_Q6_K, 12, 5632),
+                                       (Q.TYPE_Q6_K, 40, 768), (Q.TYPE_Q6_K, 336, 256),
+                                       (Q.TYPE_Q6_K, 4, 1536),
                                        (Q.TYPE_Q8_0, 32000, 2048), (Q.TYPE_Q8_0, 2048, 2048),
                                        (Q.TYPE_Q8_0, 256, 2048), (Q.TYPE_Q8_0, 5632, 2048),
                                        (Q.TYPE_Q8_0, 2048, 5632), (Q.TYPE_Q8_0, 1001, 2048),
@@ -174,7 +179,8 @@ def test_gemv_tiled_sq_shapes(dev, oracle, qtype, n, d, nt):
     """The Q6_K / Q8_0 tiled GEMV against the oracle's matmul_q_fused
     (src/quant.c:441-523; Q8_0 in the -std=c99 build's order) bit for bit:
     the sweep's shapes and lm_head, wv (512 rows), short last tiles, 64-row
-    and 1-row tiles, every batch width."""
+    and 1-row tiles, every batch width; Q6_K tiles whose d fields start
+    inside a 16-byte unit (22, 3, 1 and 6 super-blocks per row)."""
     W = synth.weights(3300 + n + d + qtype, n, d, qtype)
     X = synth.normal(3400 + nt, (nt, d))
     print("tiled sq type %d %dx%d nt %d" % (qtype, n, d, nt), flush=True)
