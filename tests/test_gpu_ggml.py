@@ -57,8 +57,13 @@ def run(dev, qtype, W, X, n, d, nt):
 @pytest.mark.parametrize("nt", [1, 2, 3, 4, 8])
 @pytest.mark.parametrize("qtype", KT)
 @pytest.mark.parametrize("n,d", [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632),
-                                 (1001, 2048), (77, 256), (5, 16384)])
+                                 (1001, 2048), (77, 256), (5, 16384), (300, 4096), (64, 3072),
+                                 (40, 1024), (13, 512)])
 def test_gemv_ggml_shapes(dev, oracle, qtype, n, d, nt):
+    """Every start-up: one token's activation loaded into registers (d up to
+    2048: one group of 8 per thread, some threads idle below 2048; up to 4096:
+    two), staged in LDS, or quantized first (d = 5632, 16384, several
+    tokens)."""
     W = GB.random_rows(50 + n + d + qtype, qtype, n, d)
     X = synth.normal(60 + nt, (nt, d))
     print("ggml gemv type %d %dx%d nt %d" % (qtype, n, d, nt), flush=True)
