@@ -257,6 +257,35 @@ def test_dispatch(dev, oracle, T, K, E):
         assert (flat[seg] == e).all() and (np.diff(seg) > 0).all()
 
 
+@pytest.mark.parametrize("T,K,E", [(600, 8, 128), (5, 3, 7)])
+def test_dispatch_invalid_indices(dev, T, K, E):
+    """Indices outside 0 .. E-1 (-1, E, large) are left out: inv = -1, not
+    counted, not in perm; the valid pairs keep the stable expert order, which
+    a brute-force stable sort fixes."""
+    rng = np.random.default_rng(T + E)
+    idx = rng.integers(0, E, size=(T, K)).astype(np.int32)
+    bad = rng.random((T, K)) < 0.05
+    idx[bad] = rng.choice(np.array([-1, E, E + 1000, -77], np.int32), size=int(bad.sum()))
+    ib = dev.upload(idx)
+    cb, ob, pb, vb = dev.alloc(E * 4), dev.alloc((E + 1) * 4), dev.alloc(T * K * 4), dev.alloc(T * K * 4)
+    dev.moe_dispatch(ib.ptr, T, K, E, cb.ptr, ob.ptr, pb.ptr, vb.ptr)
+    flat = idx.ravel()
+    valid = (flat >= 0) & (flat < E)
+    nv = int(valid.sum())
+    counts = dev.download(cb, E, np.int32)
+    offsets = dev.download(ob, E + 1, np.int32)
+    perm = dev.download(pb, T * K, np.int32)[:nv]
+    inv = dev.download(vb, T * K, np.int32)
+    want_counts = np.bincount(flat[valid], minlength=E)
+    assert (counts == want_counts).all()
+    assert (offsets == np.concatenate([[0], np.cumsum(want_counts)])).all()
+    order = sorted(np.nonzero(valid)[0].tolist(), key=lambda q: (flat[q], q))  # stable by expert
+    assert perm.tolist() == order
+    want_inv = np.full(T * K, -1, np.int64)
+    want_inv[np.array(order, np.int64)] = np.arange(nv)
+    assert (inv == want_inv).all()
+
+
 def test_dropin_moe_block(dev, oracle):
     """qr_moe_block: the MoE block with the reference's host pointers (per
     expert pointer arrays as TransformerWeights holds them)."""
