@@ -12,6 +12,7 @@
 // of W).  Its waves sweep the rows' units 64 at a time (lane = unit), compute
 // each unit's int32 sum with v_dot4_i32_i8 and its fp32 term, and park the
 // term in LDS; then R*NT threads add their row's terms in unit order.
+#include <algorithm>
 #include <cstdlib>
 
 #include "qr_gemv.h"
@@ -438,6 +439,19 @@ hipError_t lds_opt_in(const void* fn, std::atomic<bool>* done) {
   return hipSuccess;
 }
 
+int resident_by_regs(const void* fn, int threads, std::atomic<int>& cache) {
+  int v = cache.load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int nb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, threads, 0) != hipSuccess) {
+    (void)hipGetLastError();  // not this launch's error; leave the grid unbounded by it
+    nb = 64;
+  }
+  v = nb < 1 ? 1 : nb;
+  cache.store(v, std::memory_order_relaxed);
+  return v;
+}
+
 template <int TYPE, int NT, bool XS, bool ACC>
 static hipError_t launch_blk_k(const GemvArgs& a, int grid, size_t lds, hipStream_t st) {
   static std::atomic<bool> opted[64];
@@ -829,12 +843,20 @@ static hipError_t launch_ggml_x(const GemvArgs& a, hipStream_t st, int pairs = 0
     hipError_t e = lds_opt_in((const void*)k_gemv_ggml<T, NT, XM, G>, opted);
     if (e != hipSuccess) return e;
   }
+  static std::atomic<int> by_regs{0};
   int per_cu = (int)(kLdsMax / lds);
   per_cu = per_cu < 1 ? 1 : (per_cu > 4 ? 4 : per_cu);
+  // a grid beyond what stays resident would leave its last workgroups a round
+  // of their own after the others (Q4_K at 4 tokens holds 209 registers: two
+  // workgroups per CU, not the four its LDS allows)
+  per_cu = std::min(per_cu, resident_by_regs((const void*)k_gemv_ggml<T, NT, XM, G>, 256, by_regs));
   const int want = (ntiles + 3) / 4;
   // pair mode: the pairs' matrices share the resident workgroups
   const int cap = pairs > 0 ? (device_cus() * per_cu + pairs - 1) / pairs : device_cus() * per_cu;
-  int grid = want < cap ? want : cap;
+  // as few rounds of the resident grid as the tiles need, the tiles spread
+  // evenly over them (every wave the same number of tiles, give or take one)
+  const int rounds = (want + cap - 1) / cap;
+  int grid = (want + rounds - 1) / rounds;
   if (grid < 1) grid = 1;
   if (ntiles <= 0) return hipSuccess;
   hipLaunchKernelGGL((k_gemv_ggml<T, NT, XM, G>), dim3(grid, pairs > 0 ? pairs : 1), dim3(256),

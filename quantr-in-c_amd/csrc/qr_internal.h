@@ -34,6 +34,10 @@ int device_cus();
 // Let kernel fn use up to 160 KiB of dynamic LDS on the current device (once
 // per device; done[] is the caller's per-device flag array of 64 entries).
 hipError_t lds_opt_in(const void* fn, std::atomic<bool>* done);
+// Workgroups of `threads` threads that one CU holds at once by the kernel's
+// registers and wave slots alone (the caller counts its dynamic LDS); asked of
+// the runtime once per kernel and kept in `cache` (0 = not asked yet).
+int resident_by_regs(const void* fn, int threads, std::atomic<int>& cache);
 int gemv_rows_per_wg(int type, int q8o, int n, int d, int nt);
 // R (one token only): Y = R + W X, the residual add of src/runtime.c:196-198
 // and 282-284 in the GEMV's store (R may be Y).
