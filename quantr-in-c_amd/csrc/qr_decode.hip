@@ -152,7 +152,10 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ x,
       }
     }
     __syncthreads();
-    if (threadIdx.x == 0) scale_s = rms_scale(seq_sum_lds_long(sq, n), n);
+    if (threadIdx.x < 64) {  // wave 0
+      const float ss = seq_sum_wave<64>(sq, n, (int)threadIdx.x);
+      if (threadIdx.x == 0) scale_s = rms_scale(ss, n);
+    }
     __syncthreads();
     const float scale = scale_s;
 #pragma unroll
@@ -177,7 +180,10 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ x,
       sq[i] = xi * xi;
     }
     __syncthreads();
-    if (threadIdx.x == 0) scale_s = rms_scale(seq_sum_lds_long(sq, n), n);
+    if (threadIdx.x < 64) {  // wave 0
+      const float ss = seq_sum_wave<64>(sq, n, (int)threadIdx.x);
+      if (threadIdx.x == 0) scale_s = rms_scale(ss, n);
+    }
     __syncthreads();
     const float scale = scale_s;
     for (int i = threadIdx.x; i < n; i += blockDim.x) o[i] = w[i] * (x[i] * scale);
@@ -748,8 +754,9 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_sv(const float* __restrict_
   if (producer) {
     sv_load<KVT>(A, V, pt, 0, npos, pid, kvh, hd, c0);
     sv_load<KVT>(B, V, pt, 1, npos, pid, kvh, hd, c0);
-  } else if (wave == 0 && lane == 0) {
-    inv_s = 1.0f / seq_sum_lds_long(e, npos);
+  } else if (wave == 0) {
+    const float den = seq_sum_wave<64>(e, npos, lane);
+    if (lane == 0) inv_s = 1.0f / den;
   }
   __syncthreads();
   const float inv = inv_s;

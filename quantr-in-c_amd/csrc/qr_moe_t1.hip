@@ -32,7 +32,7 @@ namespace qr {
 // ---------------------------------------------------------------------------
 // matmul_ref (src/kernels.c:18-28) of one staged row: every product w[j] * x[j]
 // rounded, then added in order -- the products formed by the whole wave in
-// place (w becomes the products), the chain of adds by lane 0.
+// place (w becomes the products), the chain of adds by the wave (seq_sum_wave).
 __device__ inline float router_seq(float* sw, const float* sx, int d, int lane) {
   const int d4 = d >> 2;  // d % 4 == 0 (router1_ok)
 #pragma unroll 4
@@ -46,7 +46,7 @@ __device__ inline float router_seq(float* sw, const float* sx, int d, int lane) 
     reinterpret_cast<float4*>(sw)[j] = w;
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  return seq_sum_lds_long(sw, d);  // lane 0's value is used
+  return seq_sum_wave<64>(sw, d, lane);
 }
 
 // Workgroup (e, t): logit e of token t (xb + t d, logits + t E).  With `W2`, the

@@ -53,7 +53,7 @@ __device__ inline void lds_barrier() {
 }
 
 // The workgroup's normalisation of the loaded values: squares into xs (d
-// floats of LDS), the chain by thread 0, then xs = o (and out = o where out
+// floats of LDS), the chain by wave 0, then xs = o (and out = o where out
 // is given).  slot: one float of LDS.  Every thread of the workgroup calls
 // it; it ends with xs complete for all of them.
 template <int NP>
@@ -74,7 +74,10 @@ __device__ inline void norm_finish(const NormRegs<NP>& r, int d, float* xs, floa
     }
   }
   lds_barrier();
-  if (tid == 0) *slot = rms_scale(seq_sum_lds_long(xs, d), d);
+  if (tid < 64) {  // wave 0
+    const float ss = seq_sum_wave<64>(xs, d, tid);
+    if (tid == 0) *slot = rms_scale(ss, d);
+  }
   lds_barrier();
   const float scale = *slot;
 #pragma unroll
