@@ -212,20 +212,6 @@ __device__ inline float seq_sum_lds_short(const float* __restrict__ p, int n) {
   for (; i < n; i++) s += p[i];
   return s;
 }
-// Long sums: blocks of 256 (a single loop carrying one buffer across the
-// whole row measured slower: 13.1 against 12.1 us for 4097 terms).
-__device__ inline float seq_sum_lds_long(const float* __restrict__ p, int n) {
-  float s = 0.0f;
-  int i = 0;
-  for (; i + 256 <= n; i += 256) add256_lds(p + i, s);
-  for (; i + 32 <= n; i += 32) {
-    float4 A[8];
-    read32(p + i, A);
-    add32(A, s);
-  }
-  for (; i < n; i++) s += p[i];
-  return s;
-}
 
 
 // The same sequential sum ((0 + p[0]) + p[1]) + ... + p[n - 1] by one whole

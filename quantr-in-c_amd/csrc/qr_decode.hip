@@ -94,14 +94,16 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ tab, 
 
 // ---------------------------------------------------------------------------
 // Sequential sums.  The reference adds n terms one at a time (rmsnorm's sum
-// of squares, softmax's denominator, each attention value); one lane does the
-// same here (seq_sum_lds_long, qr_common.h), the terms produced in parallel
-// beforehand and read from LDS 32 adds ahead of their use.
+// of squares, softmax's denominator, each attention value); the decode step
+// does the same, the terms produced in parallel beforehand: one whole wave
+// for a single sum (seq_sum_wave, qr_common.h: the terms in registers, the
+// running sum passed lane to lane), one lane per attention element for the
+// value sums (read from LDS 32 adds ahead of their use).
 
 // ---------------------------------------------------------------------------
 // rmsnorm_ref (src/kernels.c:170-180), optionally after x += add (the
 // residual of src/runtime.c:196-198).  Every thread loads its share of x (and
-// add, w) at once, the squares go to LDS, lane 0 adds them in order, the
+// add, w) at once, the squares go to LDS, wave 0 adds them in order, the
 // workgroup scales from registers.  n <= kNormMax; VEC: n % 4 == 0.
 // Workgroup r normalizes row r of a batch (x, add, o advanced by r n).
 // ---------------------------------------------------------------------------
