@@ -360,6 +360,13 @@ static hipError_t launch_stream_t(const GemvArgs& a, hipStream_t st) {
   constexpr int kDefault = NT > 2 ? 2 : 3;
   int per_cu = lds > 0 ? (int)((160 * 1024) / lds) : kDefault;
   per_cu = per_cu < 1 ? 1 : (per_cu > kDefault ? kDefault : per_cu);
+  // no more than stay resident by registers (Q8_0 at two tokens in the AVX2 /
+  // AVX-512 orders holds 190: two per CU)
+  static std::atomic<int> by_regs[2];  // the two kernel forms below
+  const bool one = 64 % sh.U == 0;
+  const void* fn = one ? (const void*)k_gemv_stream<TYPE, NT, 1, Q8O>
+                       : (const void*)k_gemv_stream<TYPE, 1, kUPL, Q8O>;
+  per_cu = std::min(per_cu, resident_by_regs(fn, 64 * kStreamWaves, by_regs[one ? 0 : 1]));
   const int cap = device_cus() * per_cu;
   const int grid = want < cap ? want : cap;
   if (grid <= 0) return hipSuccess;
