@@ -218,7 +218,7 @@ __device__ inline float seq_sum_lds_short(const float* __restrict__ p, int n) {
 // wave: all 64 lanes call it and every lane gets the sum.  Lane L holds the
 // SEG terms from SEG L on in registers; the running sum goes through lane L's
 // terms and then moves one lane up (DPP wave shift), so the chain of adds
-// reads registers only: about 5.4 cycles per add at SEG = 64, against 7.1
+// reads registers only: 5.6-5.7 cycles per add at SEG = 64, against 7.1
 // with the terms read from LDS in batches.  The last n % SEG terms go one per
 // lane, the running sum moving a lane up with each add.  p: 16-byte aligned.
 __device__ inline float wave_up1(float v) {
