@@ -569,11 +569,12 @@ def bench_decode(dev, M, steps, warmup, order):
         d.forward(int(toks[i]), P + i, lg.ptr)
     ms = dev.timer_stop() / steps
     logits = dev.download(lg, c["vocab"], np.float32)
-    # prompt prefill: 512 prompt tokens at positions 0 .. 511 in chunks of 128
-    # (qr_decoder_prefill; the workspace is allocated by an untimed first call)
+    # prompt prefill: 512 prompt tokens at positions 0 .. 511 in the default
+    # chunk (qr_decoder_prefill with chunk 0; the workspace is allocated by an
+    # untimed first call of the same size)
     pn = c["prefill_prompt"]
     ptoks = np.random.default_rng(5031).integers(0, c["vocab"], size=pn)
-    d.prefill(ptoks[:128], 0, lg.ptr)
+    d.prefill(ptoks, 0, lg.ptr)
     dev.sync()
     dev.timer_start()
     d.prefill(ptoks, 0, lg.ptr)
@@ -593,7 +594,7 @@ def bench_decode(dev, M, steps, warmup, order):
                   c["vocab"] * synth.row_bytes(Q.TYPE_Q6_K, dim) + 4 * dim)
     s = ms / 1e3
     return dict(ms_per_step=ms, tokens_per_s=1.0 / s, layers=L, positions=npos,
-                prefill=dict(tokens=int(pn), chunk=128, ms=round(pms, 3),
+                prefill=dict(tokens=int(pn), chunk=min(int(pn), Q.PREFILL_CHUNK), ms=round(pms, 3),
                              tokens_per_s=round(pn / (pms / 1e3), 1),
                              speedup_vs_decode=round((pn / (pms / 1e3)) * s, 2)),
                 alg_bytes=int(step_bytes), achieved_gbps=step_bytes / s / 1e9,

@@ -1404,6 +1404,12 @@ __global__ __launch_bounds__(256) void k_rows_dispatch(int T, int tile, int32_t*
 // The records of x are quantized unless `records` says the previous call
 // left those of the same x (and the same record order) in d->prec; the chunk's
 // single-expert dispatch lists are written once per chunk (prefill_rows_setup).
+// Pairs per work item of the T-row products: a dense matrix has one
+// "expert", so the items are what spreads it over the CUs.  16 for chunks
+// below 256 rows (128-token chunks: 71 ms for 512 prompt tokens against 75
+// ms with 32-pair items), 32 from 256 on.
+static int rows_tile(int T) { return T >= 256 ? 32 : 16; }
+
 hipError_t matmul_rows_dev(qr_decoder* d, const void* w, uint32_t type, const float* x, float* y,
                            int n, int dd, int T, hipStream_t s, bool records = false) {
   hipError_t e;
@@ -1427,11 +1433,7 @@ hipError_t matmul_rows_dev(qr_decoder* d, const void* w, uint32_t type, const fl
   const bool sq_tiles = tiled && (base == QR_T_Q6_K || base == QR_T_Q8_0);
   if (!lanes && !sq_tiles && T >= 2 && mfma_type_ok((int)base) && dd % 256 == 0 &&
       (dd >> 8) <= 64) {
-    // 16-pair work items: a dense matrix has one "expert", so the items are
-    // what spreads it over the CUs (measured on a 128-token chunk of the
-    // Qwen3-30B-A3B-shaped model: 71 ms for 512 prompt tokens against 75 ms
-    // with 32-pair items)
-    const int tile = 16;
+    const int tile = rows_tile(T);
     const int perm = base != QR_T_Q8_0;
     if (!records || d->prec_src != x || d->prec_perm != perm) {
       if ((e = quant_rows_launch(x, dd, T, dd, perm != 0, d->prec, s))) return e;
@@ -1464,9 +1466,9 @@ hipError_t enqueue_prefill_chunk(qr_decoder* d, int T, const int32_t* st, int pe
                                  hipStream_t s) {
   hipError_t e;
   const int dim = d->dim;
-  // the chunk's single-expert dispatch of its T rows (16-pair items, as
-  // matmul_rows_dev launches them)
-  hipLaunchKernelGGL(k_rows_dispatch, dim3(1), dim3(256), 0, s, T, 16, d->poff,
+  // the chunk's single-expert dispatch of its T rows (in the items
+  // matmul_rows_dev launches)
+  hipLaunchKernelGGL(k_rows_dispatch, dim3(1), dim3(256), 0, s, T, rows_tile(T), d->poff,
                      d->pperm, d->ptiles);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   d->prec_src = nullptr;

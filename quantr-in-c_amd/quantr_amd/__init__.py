@@ -64,6 +64,7 @@ KV_F32, KV_F16, KV_Q8_0 = 0, 1, 2
 MOE_PATH_AUTO, MOE_PATH_GEMV, MOE_PATH_MFMA = 0, 1, 2
 DEC_GRAPH = 1
 PREFILL_ALL_LOGITS = 1
+PREFILL_CHUNK = 512  # QR_PREFILL_CHUNK: the chunk of qr_decoder_prefill(..., chunk=0)
 
 _SIGS = {
     "qr_last_error": (C.c_char_p, []),

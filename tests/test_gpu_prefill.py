@@ -220,6 +220,24 @@ def test_prefill_matches_sequential_decode(dev):
     assert_bits_equal(x, want_x, "prefill residual")
 
 
+@pytest.mark.parametrize("chunk", [0, 256, 1024])
+def test_prefill_large_chunks(dev, chunk):
+    """The default chunk (0: QR_PREFILL_CHUNK) and chunks up to the maximum
+    against the same decoder's single steps: a 300-token prompt in one chunk
+    (0, 1024) or two (256)."""
+    m = I.qwen3_small_model(n_layers=2, seq_len=320)
+    toks = np.random.default_rng(31).integers(0, m["vocab"], size=300).astype(np.int32)
+    print("prefill chunk %d" % chunk, flush=True)
+    ref = make_decoder(dev, m, Q.KV_Q8_0, ORDER_AVX2, page=64, flags=Q.DEC_GRAPH)
+    want_lg, want_x = sequential(dev, ref, m, toks)
+    ref.close()
+    d = make_decoder(dev, m, Q.KV_Q8_0, ORDER_AVX2, page=64)
+    lg, x = prefill(dev, d, m, toks, chunk=chunk)
+    d.close()
+    assert_bits_equal(lg, want_lg, "prefill logits, chunk %d" % chunk)
+    assert_bits_equal(x, want_x, "prefill residual, chunk %d" % chunk)
+
+
 def test_prefill_bad_args(dev):
     m = I.decode_model("a")
     d = make_decoder(dev, m, Q.KV_F32, ORDER_SEQ)
