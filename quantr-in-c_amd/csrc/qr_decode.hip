@@ -1489,7 +1489,13 @@ hipError_t enqueue_prefill_chunk(qr_decoder* d, int T, const int32_t* st, int pe
                        0, s, d->pq, d->pk, d->pv, d->rope, st, d->qd, d->kvd, K,
                        const_cast<uint8_t*>(V.base));
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_scores<false>, dim3((d->cap + kScTile - 1) / kScTile, d->nkv, T),
+    // position tiles up to the chunk's last position (not the cache's
+    // capacity: tiles past a token's positions are dispatched only to
+    // return), an odd count of them: workgroups go to the XCDs in turn, and an
+    // even count would send every token's tile x to the same XCD -- the early
+    // tiles, which every token has, to a few XCDs, the late ones, which few
+    // tokens have, to the others
+    hipLaunchKernelGGL(k_attn_scores<false>, dim3(((pend + kScTile - 1) / kScTile) | 1, d->nkv, T),
                        dim3(256), d->sc_lds, s, d->pq, K, st, 0, d->kv_mul, d->hd, inv_sqrt, d->cap,
                        d->patt, RopeArgs{});
     if ((e = hipGetLastError()) != hipSuccess) return e;
