@@ -823,7 +823,9 @@ __global__ __launch_bounds__(512) void k_attn_sv_rows(const float* __restrict__ 
   extern __shared__ __align__(16) float e[];
   __shared__ float red[8];
   __shared__ float inv_s;
-  const int nh = gridDim.x, h = blockIdx.x, z = blockIdx.y;
+  // the chunk's last token first: its chain is the longest (causal), so the
+  // longest workgroups are dispatched first and the short ones fill in
+  const int nh = gridDim.x, h = blockIdx.x, z = gridDim.y - 1 - blockIdx.y;
   att += ((size_t)z * nh + h) * att_stride;
   out += ((size_t)z * nh + h) * hd;
   const int npos = st[2 * z + 1] + 1;
@@ -920,7 +922,9 @@ __global__ __launch_bounds__(1024) void k_attn_sv_gqa(const float* __restrict__ 
   __shared__ float inv_s[16];
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int kvh = blockIdx.x, z = blockIdx.y;
+  // the chunk's last token first: its chains are the longest (causal), so
+  // the longest workgroups are dispatched first and the short ones fill in
+  const int kvh = blockIdx.x, z = gridDim.y - 1 - blockIdx.y;
   const int nh = gridDim.x * kv_mul;
   const int j = tid / hd, c = tid - j * hd;
   const int h = kvh * kv_mul + j;
