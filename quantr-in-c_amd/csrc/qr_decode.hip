@@ -1386,15 +1386,22 @@ hipError_t enqueue_step(qr_decoder* d, float* logits, float* xout, hipStream_t s
 }
 
 // A single-"expert" dispatch of T rows for the grouped MFMA product:
-// offsets {0, T}, the identity permutation, tiles {0, ceil(T / tile)}.
+// offsets {0, T}, the identity permutation, tiles {0, ceil(T / tile)}; with
+// tiles2, also {0, ceil(T / 32)} there (a chunk's products take 16- or
+// 32-pair items by their row count).
 __global__ __launch_bounds__(256) void k_rows_dispatch(int T, int tile, int32_t* off,
-                                                       int32_t* perm, int32_t* tiles) {
+                                                       int32_t* perm, int32_t* tiles,
+                                                       int32_t* tiles2) {
   for (int i = threadIdx.x; i < T; i += blockDim.x) perm[i] = i;
   if (threadIdx.x == 0) {
     off[0] = 0;
     off[1] = T;
     tiles[0] = 0;
     tiles[1] = (T + tile - 1) / tile;
+    if (tiles2) {
+      tiles2[0] = 0;
+      tiles2[1] = (T + 31) / 32;
+    }
   }
 }
 
@@ -1411,8 +1418,10 @@ __global__ __launch_bounds__(256) void k_rows_dispatch(int T, int tile, int32_t*
 // Pairs per work item of the T-row products: a dense matrix has one
 // "expert", so the items are what spreads it over the CUs.  16 for chunks
 // below 256 rows (128-token chunks: 71 ms for 512 prompt tokens against 75
-// ms with 32-pair items), 32 from 256 on.
-static int rows_tile(int T) { return T >= 256 ? 32 : 16; }
+// ms with 32-pair items) and for matrices of fewer than 2048 rows (wk / wv
+// at a 512-token chunk: 15-17 against 19-21 us, their few row blocks need
+// the items), 32 otherwise (wq / wo: 74-78 -> 42-46 us).
+static int rows_tile(int T, int n) { return T >= 256 && n >= 2048 ? 32 : 16; }
 
 hipError_t matmul_rows_dev(qr_decoder* d, const void* w, uint32_t type, const float* x, float* y,
                            int n, int dd, int T, hipStream_t s, bool records = false) {
@@ -1437,7 +1446,7 @@ hipError_t matmul_rows_dev(qr_decoder* d, const void* w, uint32_t type, const fl
   const bool sq_tiles = tiled && (base == QR_T_Q6_K || base == QR_T_Q8_0);
   if (!lanes && !sq_tiles && T >= 2 && mfma_type_ok((int)base) && dd % 256 == 0 &&
       (dd >> 8) <= 64) {
-    const int tile = rows_tile(T);
+    const int tile = rows_tile(T, n);
     const int perm = base != QR_T_Q8_0;
     if (!records || d->prec_src != x || d->prec_perm != perm) {
       if ((e = quant_rows_launch(x, dd, T, dd, perm != 0, d->prec, s))) return e;
@@ -1446,7 +1455,8 @@ hipError_t matmul_rows_dev(qr_decoder* d, const void* w, uint32_t type, const fl
     }
     const size_t slice = qr_wrow_bytes((int)base, dd) * (size_t)n;
     return expert_mfma_launch((int)base, false, static_cast<const uint8_t*>(w), nullptr, slice, 1,
-                              1, n, dd, d->prec, 1, d->poff, d->pperm, d->ptiles, y, n,
+                              1, n, dd, d->prec, 1, d->poff, d->pperm,
+                              tile == 16 ? d->ptiles : d->ptiles + 2, y, n,
                               (T + tile - 1) / tile + 1, tile, nullptr, false, s, tiled);
   }
   for (int t0 = 0; t0 < T; t0 += 4) {
@@ -1472,8 +1482,8 @@ hipError_t enqueue_prefill_chunk(qr_decoder* d, int T, const int32_t* st, int pe
   const int dim = d->dim;
   // the chunk's single-expert dispatch of its T rows (in the items
   // matmul_rows_dev launches)
-  hipLaunchKernelGGL(k_rows_dispatch, dim3(1), dim3(256), 0, s, T, rows_tile(T), d->poff,
-                     d->pperm, d->ptiles);
+  hipLaunchKernelGGL(k_rows_dispatch, dim3(1), dim3(256), 0, s, T, 16, d->poff, d->pperm,
+                     d->ptiles, d->ptiles + 2);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   d->prec_src = nullptr;
   hipLaunchKernelGGL(k_embed, dim3(T), dim3(256), 0, s, static_cast<const uint8_t*>(d->tok_embd),
@@ -1625,7 +1635,8 @@ int check_layer_weights(const qr_model* m, int l, int order) {
 namespace qr {
 hipError_t rows_dispatch_launch(int T, int tile, int32_t* off, int32_t* perm, int32_t* tiles,
                                 hipStream_t st) {
-  hipLaunchKernelGGL(k_rows_dispatch, dim3(1), dim3(256), 0, st, T, tile, off, perm, tiles);
+  hipLaunchKernelGGL(k_rows_dispatch, dim3(1), dim3(256), 0, st, T, tile, off, perm, tiles,
+                     (int32_t*)nullptr);
   return hipGetLastError();
 }
 }  // namespace qr
